@@ -1,0 +1,655 @@
+// C-ABI host layer: validation, positional-encoding tables, scratch memory,
+// dispatch onto the HIP kernels, and the reference-compatible drop-in entry
+// points (synchronous, exit on error).
+//
+// Validation runs before any HIP call, so every argument error is reported
+// (and testable) without a GPU.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdint>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <tuple>
+#include <vector>
+
+#include "../kernels/launch.hpp"
+#include "attn_mi355x.h"
+
+namespace {
+
+thread_local int g_last_hip_error = 0;
+
+int hip_fail(hipError_t e) {
+    g_last_hip_error = (int)e;
+    return ATN_ERR_HIP;
+}
+
+#define ATN_HIP(call)                                  \
+    do {                                               \
+        hipError_t e_ = (call);                        \
+        if (e_ != hipSuccess) return hip_fail(e_);     \
+    } while (0)
+
+// ---------------------------------------------------------------- validation
+bool mul_ok(int64_t a, int64_t b, int64_t* out) {
+    if (a < 0 || b < 0) return false;
+    if (a != 0 && b > INT64_MAX / a) return false;
+    *out = a * b;
+    return true;
+}
+
+struct Shape {
+    int B, H, Lq, Lk, D;
+    int64_t BH, nq, nk;  // element counts of Q/out and of K/V
+};
+
+int check_shape(int B, int H, int Lq, int Lk, int D, Shape* s) {
+    if (B < 1 || H < 1 || Lq < 1 || Lk < 1 || D < 1) return ATN_ERR_BAD_DIMENSION;
+    int64_t bh, t;
+    if (!mul_ok(B, H, &bh)) return ATN_ERR_SIZE_OVERFLOW;
+    if (!mul_ok(bh, Lq, &t) || !mul_ok(t, D, &s->nq)) return ATN_ERR_SIZE_OVERFLOW;
+    if (!mul_ok(bh, Lk, &t) || !mul_ok(t, D, &s->nk)) return ATN_ERR_SIZE_OVERFLOW;
+    if (s->nq > (INT64_MAX / 8) || s->nk > (INT64_MAX / 8)) return ATN_ERR_SIZE_OVERFLOW;
+    // The kernels index rows of one head with 32-bit ints.
+    if ((int64_t)Lq * D > INT32_MAX || (int64_t)Lk * D > INT32_MAX) return ATN_ERR_SIZE_OVERFLOW;
+    s->B = B; s->H = H; s->Lq = Lq; s->Lk = Lk; s->D = D; s->BH = bh;
+    return ATN_OK;
+}
+
+bool overlaps(const void* a, int64_t abytes, const void* b, int64_t bbytes) {
+    const uintptr_t x = (uintptr_t)a, y = (uintptr_t)b;
+    return x < y + (uintptr_t)bbytes && y < x + (uintptr_t)abytes;
+}
+
+size_t elem_size(int dtype) { return dtype == ATN_DTYPE_F32 ? 4 : 2; }
+
+bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
+
+// ---------------------------------------------------------------- resolved encoding
+struct PePlan {
+    int pek = atn::kPeNone;   // kernel template selector
+    atn::PeSide q{}, k{};
+    int rotary = 0;
+    float base = 10000.0f;
+    int pairing = ATN_ROPE_INTERLEAVED;
+    bool caller_tables = false;
+};
+
+int check_pe(const atn_pe_desc* pe, int D, PePlan* plan) {
+    *plan = PePlan{};
+    if (pe == nullptr || pe->kind == ATN_PE_NONE) return ATN_OK;
+    if (pe->kind == ATN_PE_ROPE) {
+        const int r = pe->rotary_dim == 0 ? D : pe->rotary_dim;
+        if (r < 2 || r > D || (r & 1)) return ATN_ERR_BAD_ROTARY;
+        if (pe->pairing != ATN_ROPE_INTERLEAVED && pe->pairing != ATN_ROPE_HALF)
+            return ATN_ERR_BAD_ARGUMENT;
+        if ((pe->table_a == nullptr) != (pe->table_b == nullptr)) return ATN_ERR_NULL_POINTER;
+        const float base = pe->base == 0.0f ? 10000.0f : pe->base;
+        if (!(base > 0.0f) || !std::isfinite(base)) return ATN_ERR_BAD_ARGUMENT;
+        plan->pek = pe->pairing == ATN_ROPE_HALF ? atn::kPeRopeHalf : atn::kPeRopeInterleaved;
+        plan->rotary = r;
+        plan->base = base;
+        plan->pairing = pe->pairing;
+    } else if (pe->kind == ATN_PE_SINUSOIDAL) {
+        if ((pe->table_a == nullptr) != (pe->table_b == nullptr)) return ATN_ERR_NULL_POINTER;
+        plan->pek = atn::kPeSinusoidal;
+        plan->rotary = D;
+    } else {
+        return ATN_ERR_BAD_ARGUMENT;
+    }
+    plan->caller_tables = pe->table_a != nullptr;
+    plan->q.on = pe->apply_q ? 1 : 0;
+    plan->k.on = pe->apply_k ? 1 : 0;
+    plan->q.rotary = plan->k.rotary = plan->rotary;
+    return ATN_OK;
+}
+
+// ---------------------------------------------------------------- per-device state
+struct Table {
+    float* a = nullptr;
+    float* b = nullptr;
+    int npos = 0;
+    int nfreq = 0;
+};
+
+struct DeviceState {
+    void* ws = nullptr;
+    size_t ws_bytes = 0;
+    std::map<std::tuple<int, int, uint32_t>, Table> tables;  // (kind, dim, base bits)
+};
+
+std::mutex g_mu;
+std::map<int, DeviceState> g_dev;
+
+int current_device(int* dev) {
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess || n <= 0) {
+        g_last_hip_error = (int)e;
+        return ATN_ERR_NO_DEVICE;
+    }
+    ATN_HIP(hipGetDevice(dev));
+    return ATN_OK;
+}
+
+// Host-side angle tables with the reference CPU path's float expressions
+// (final/rope.cu:27-33, final/sinusoidal.cu:846-851), compact layout
+// [pos][nfreq]: RoPE a = cos, b = sin; sinusoidal a = sin, b = cos.
+void build_rope_table(std::vector<float>& a, std::vector<float>& b, int npos, int r, float base) {
+    const int nf = r / 2;
+    std::vector<float> freq(nf);
+    for (int i = 0; i < nf; i++) freq[i] = 1.0f / powf(base, (2.0f * i) / r);
+    a.resize((size_t)npos * nf);
+    b.resize((size_t)npos * nf);
+    for (int pos = 0; pos < npos; pos++)
+        for (int i = 0; i < nf; i++) {
+            const float theta = pos * freq[i];
+            a[(size_t)pos * nf + i] = cosf(theta);
+            b[(size_t)pos * nf + i] = sinf(theta);
+        }
+}
+
+void build_sin_table(std::vector<float>& a, std::vector<float>& b, int npos, int D) {
+    const int nf = (D + 1) / 2;
+    std::vector<float> freq(nf);
+    for (int f = 0; f < nf; f++) freq[f] = 1.0f / powf(10000.0f, (2.0f * f) / (float)D);
+    a.resize((size_t)npos * nf);
+    b.resize((size_t)npos * nf);
+    for (int pos = 0; pos < npos; pos++)
+        for (int f = 0; f < nf; f++) {
+            const float angle = pos * freq[f];
+            a[(size_t)pos * nf + f] = sinf(angle);
+            b[(size_t)pos * nf + f] = cosf(angle);
+        }
+}
+
+// Returns the device tables for this encoding, building or growing them
+// (synchronously) when needed.  Caller holds g_mu.
+int get_table(DeviceState& ds, const PePlan& plan, int D, int npos, Table** out) {
+    const bool rope = plan.pek != atn::kPeSinusoidal;
+    uint32_t base_bits;
+    std::memcpy(&base_bits, &plan.base, 4);
+    const auto key = std::make_tuple(rope ? 1 : 2, rope ? plan.rotary : D, rope ? base_bits : 0u);
+    Table& t = ds.tables[key];
+    if (t.a == nullptr || t.npos < npos) {
+        const int want = npos < 64 ? 64 : npos;
+        std::vector<float> a, b;
+        int nf;
+        if (rope) {
+            build_rope_table(a, b, want, plan.rotary, plan.base);
+            nf = plan.rotary / 2;
+        } else {
+            build_sin_table(a, b, want, D);
+            nf = (D + 1) / 2;
+        }
+        if (t.a) {
+            ATN_HIP(hipFree(t.a));  // hipFree waits for in-flight work
+            ATN_HIP(hipFree(t.b));
+            t.a = t.b = nullptr;
+        }
+        const size_t bytes = a.size() * sizeof(float);
+        ATN_HIP(hipMalloc(&t.a, bytes));
+        ATN_HIP(hipMalloc(&t.b, bytes));
+        ATN_HIP(hipMemcpy(t.a, a.data(), bytes, hipMemcpyHostToDevice));
+        ATN_HIP(hipMemcpy(t.b, b.data(), bytes, hipMemcpyHostToDevice));
+        t.npos = want;
+        t.nfreq = nf;
+    }
+    *out = &t;
+    return ATN_OK;
+}
+
+// Fills the PeSide table pointers (library tables or the caller's).
+int bind_tables(const atn_pe_desc* pe, PePlan& plan, int D, int npos) {
+    if (plan.pek == atn::kPeNone) return ATN_OK;
+    if (plan.caller_tables) {
+        const bool rope = plan.pek != atn::kPeSinusoidal;
+        for (atn::PeSide* s : {&plan.q, &plan.k}) {
+            s->a = pe->table_a;
+            s->b = pe->table_b;
+            s->ld = rope ? plan.rotary : D;
+            s->dup = 1;
+        }
+        return ATN_OK;
+    }
+    int dev;
+    int st = current_device(&dev);
+    if (st != ATN_OK) return st;
+    std::lock_guard<std::mutex> lk(g_mu);
+    Table* t = nullptr;
+    st = get_table(g_dev[dev], plan, D, npos, &t);
+    if (st != ATN_OK) return st;
+    for (atn::PeSide* s : {&plan.q, &plan.k}) {
+        s->a = t->a;
+        s->b = t->b;
+        s->ld = t->nfreq;
+        s->dup = 0;
+    }
+    return ATN_OK;
+}
+
+// ---------------------------------------------------------------- streaming plan
+struct StreamPlan {
+    int nsplit, dchunk;
+    size_t s_elems, p_elems;  // partial scores, probabilities (floats)
+    size_t bytes;
+};
+
+StreamPlan stream_plan(const Shape& s) {
+    StreamPlan p{};
+    const int64_t tiles = s.BH * ((s.Lq + 63) / 64) * ((s.Lk + 63) / 64);
+    int nsplit = 1;
+    if (tiles < 256) {
+        const int64_t want = (512 + tiles - 1) / tiles;
+        const int64_t maxs = s.D / 64 > 1 ? s.D / 64 : 1;
+        nsplit = (int)(want < maxs ? want : maxs);
+    }
+    int dchunk = (s.D + nsplit - 1) / nsplit;
+    dchunk = (dchunk + 15) / 16 * 16;
+    nsplit = (s.D + dchunk - 1) / dchunk;
+    p.nsplit = nsplit;
+    p.dchunk = dchunk;
+    const size_t per = (size_t)s.BH * s.Lq * s.Lk;
+    p.s_elems = per * nsplit;
+    p.p_elems = nsplit > 1 ? per : 0;  // P aliases S when there is one split
+    p.bytes = (p.s_elems + p.p_elems) * sizeof(float) + 256;
+    return p;
+}
+
+int ensure_workspace(size_t bytes, void** ws) {
+    int dev;
+    int st = current_device(&dev);
+    if (st != ATN_OK) return st;
+    std::lock_guard<std::mutex> lk(g_mu);
+    DeviceState& ds = g_dev[dev];
+    if (ds.ws_bytes < bytes) {
+        if (ds.ws) {
+            ATN_HIP(hipFree(ds.ws));  // waits for in-flight work using it
+            ds.ws = nullptr;
+            ds.ws_bytes = 0;
+        }
+        ATN_HIP(hipMalloc(&ds.ws, bytes));
+        ds.ws_bytes = bytes;
+    }
+    *ws = ds.ws;
+    return ATN_OK;
+}
+
+// ---------------------------------------------------------------- core
+int attention_core(int dtype, const void* Q, const void* K, const void* V, void* out, int B,
+                   int H, int Lq, int Lk, int D, const atn_pe_desc* pe, void* workspace,
+                   size_t workspace_bytes, hipStream_t stream) {
+    if (dtype != ATN_DTYPE_F32 && dtype != ATN_DTYPE_BF16) return ATN_ERR_BAD_ARGUMENT;
+    if (!Q || !K || !V || !out) return ATN_ERR_NULL_POINTER;
+    Shape s;
+    int st = check_shape(B, H, Lq, Lk, D, &s);
+    if (st != ATN_OK) return st;
+    const size_t es = elem_size(dtype);
+    for (const void* p : {Q, K, V, (const void*)out})
+        if (!aligned(p, es)) return ATN_ERR_MISALIGNED;
+    const int64_t qb = s.nq * (int64_t)es, kb = s.nk * (int64_t)es;
+    if (overlaps(out, qb, Q, qb) || overlaps(out, qb, K, kb) || overlaps(out, qb, V, kb))
+        return ATN_ERR_ALIASING;
+    PePlan plan;
+    st = check_pe(pe, D, &plan);
+    if (st != ATN_OK) return st;
+    const StreamPlan sp = stream_plan(s);
+    if (workspace != nullptr && workspace_bytes < sp.bytes) return ATN_ERR_WORKSPACE;
+    const int64_t tiles = s.BH * ((Lq + 63) / 64) * ((Lk + 63) / 64) * sp.nsplit;
+    const int64_t pv_tiles = s.BH * ((Lq + 63) / 64) * ((D + 63) / 64);
+    if (tiles > (1LL << 24) || pv_tiles > (1LL << 24)) return ATN_ERR_SIZE_OVERFLOW;
+
+    int dev;
+    st = current_device(&dev);
+    if (st != ATN_OK) return st;
+    st = bind_tables(pe, plan, D, Lq > Lk ? Lq : Lk);
+    if (st != ATN_OK) return st;
+    void* ws = workspace;
+    if (ws == nullptr) {
+        st = ensure_workspace(sp.bytes, &ws);
+        if (st != ATN_OK) return st;
+    }
+    float* S = reinterpret_cast<float*>(((uintptr_t)ws + 255) & ~(uintptr_t)255);
+    float* P = sp.nsplit > 1 ? S + sp.s_elems : S;
+
+    const size_t va = dtype == ATN_DTYPE_F32 ? 16 : 8;
+    const int vec_qk = (D % 4 == 0) && aligned(Q, va) && aligned(K, va);
+    const int vec_vo = (D % 4 == 0) && aligned(V, va) && aligned(out, va);
+    const float scale = 1.0f / sqrtf((float)D);  // final/attention.cu:206
+
+    ATN_HIP(atn::launch_qk_partial(dtype, plan.pek, Q, K, S, (int)s.BH, Lq, Lk, D, sp.dchunk,
+                                   sp.nsplit, plan.q, plan.k, vec_qk, stream));
+    ATN_HIP(atn::launch_softmax(S, P, s.BH * Lq, Lk, sp.nsplit, (size_t)s.BH * Lq * Lk, scale,
+                                stream));
+    ATN_HIP(atn::launch_pv(dtype, P, V, out, (int)s.BH, Lq, Lk, D, vec_vo, stream));
+    return ATN_OK;
+}
+
+int pe_apply_core(int dtype, const void* in, void* out, long n_rows, int seq_len, int D,
+                  const atn_pe_desc* pe, hipStream_t stream) {
+    if (dtype != ATN_DTYPE_F32 && dtype != ATN_DTYPE_BF16) return ATN_ERR_BAD_ARGUMENT;
+    if (!in || !out || !pe) return ATN_ERR_NULL_POINTER;
+    if (n_rows < 1 || seq_len < 1 || D < 1) return ATN_ERR_BAD_DIMENSION;
+    int64_t n;
+    if (!mul_ok(n_rows, D, &n) || n > INT64_MAX / 8) return ATN_ERR_SIZE_OVERFLOW;
+    const size_t es = elem_size(dtype);
+    if (!aligned(in, es) || !aligned(out, es)) return ATN_ERR_MISALIGNED;
+    if (in != out && overlaps(in, n * (int64_t)es, out, n * (int64_t)es))
+        return ATN_ERR_ALIASING;
+    atn_pe_desc d = *pe;
+    d.apply_q = d.apply_k = 1;
+    PePlan plan;
+    int st = check_pe(&d, D, &plan);
+    if (st != ATN_OK) return st;
+    if (plan.pek == atn::kPeNone) return ATN_ERR_BAD_ARGUMENT;
+    int dev;
+    st = current_device(&dev);
+    if (st != ATN_OK) return st;
+    st = bind_tables(&d, plan, D, seq_len);
+    if (st != ATN_OK) return st;
+    const size_t va = dtype == ATN_DTYPE_F32 ? 16 : 8;
+    const int vec = (D % 4 == 0) && aligned(in, va) && aligned(out, va);
+    ATN_HIP(atn::launch_pe_apply(dtype, plan.pek, in, out, n_rows, seq_len, D, plan.q, vec,
+                                 stream));
+    return ATN_OK;
+}
+
+// ---------------------------------------------------------------- drop-in helpers
+[[noreturn]] void die(int status, const char* where) {
+    std::fprintf(stderr, "attn_mi355x error %d (%s) at %s", status, atn_status_string(status),
+                 where);
+    if (status == ATN_ERR_HIP || status == ATN_ERR_NO_DEVICE)
+        std::fprintf(stderr, " [hip %d: %s]", g_last_hip_error,
+                     hipGetErrorString((hipError_t)g_last_hip_error));
+    std::fprintf(stderr, "\n");
+    std::exit(EXIT_FAILURE);
+}
+
+void sync_or_die(int status, const char* where) {
+    if (status != ATN_OK) die(status, where);
+    hipError_t e = hipGetLastError();
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e != hipSuccess) {
+        g_last_hip_error = (int)e;
+        die(ATN_ERR_HIP, where);
+    }
+}
+
+atn_pe_desc rope_desc(int rotary, int pairing, bool q, bool k, const float* c, const float* s) {
+    atn_pe_desc d{};
+    d.kind = ATN_PE_ROPE;
+    d.pairing = pairing;
+    d.rotary_dim = rotary;
+    d.apply_q = q;
+    d.apply_k = k;
+    d.base = 10000.0f;
+    d.table_a = c;
+    d.table_b = s;
+    return d;
+}
+
+atn_pe_desc sin_desc(bool q, bool k, const float* sin_t, const float* cos_t) {
+    atn_pe_desc d{};
+    d.kind = ATN_PE_SINUSOIDAL;
+    d.apply_q = q;
+    d.apply_k = k;
+    d.table_a = sin_t;
+    d.table_b = cos_t;
+    return d;
+}
+
+}  // namespace
+
+// ====================================================================== C ABI
+extern "C" {
+
+const char* atn_status_string(int status) {
+    switch (status) {
+        case ATN_OK: return "ok";
+        case ATN_ERR_NULL_POINTER: return "null pointer";
+        case ATN_ERR_BAD_DIMENSION: return "dimension < 1";
+        case ATN_ERR_BAD_ROTARY: return "rotary_dim must be even and in [2, head_d]";
+        case ATN_ERR_SIZE_OVERFLOW: return "size overflow";
+        case ATN_ERR_ALIASING: return "output overlaps an input";
+        case ATN_ERR_NO_DEVICE: return "no HIP device";
+        case ATN_ERR_HIP: return "HIP runtime error";
+        case ATN_ERR_WORKSPACE: return "workspace too small";
+        case ATN_ERR_BAD_ARGUMENT: return "bad argument";
+        case ATN_ERR_MISALIGNED: return "pointer not aligned to its element size";
+        default: return "unknown status";
+    }
+}
+
+int atn_last_hip_error(void) { return g_last_hip_error; }
+
+int atn_device_count(void) {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) return 0;
+    return n;
+}
+
+int atn_attention_fwd_ex(int dtype, const void* Q, const void* K, const void* V, void* out,
+                         int batch, int heads, int len_q, int len_k, int head_d,
+                         const atn_pe_desc* pe, void* workspace, size_t workspace_bytes,
+                         void* stream) {
+    return attention_core(dtype, Q, K, V, out, batch, heads, len_q, len_k, head_d, pe, workspace,
+                          workspace_bytes, (hipStream_t)stream);
+}
+
+size_t atn_attention_workspace_bytes(int dtype, int batch, int heads, int len_q, int len_k,
+                                     int head_d, const atn_pe_desc* pe) {
+    if (dtype != ATN_DTYPE_F32 && dtype != ATN_DTYPE_BF16) return 0;
+    Shape s;
+    if (check_shape(batch, heads, len_q, len_k, head_d, &s) != ATN_OK) return 0;
+    PePlan plan;
+    if (check_pe(pe, head_d, &plan) != ATN_OK) return 0;
+    return stream_plan(s).bytes;
+}
+
+int atn_pe_apply_ex(int dtype, const void* in, void* out, long n_rows, int seq_len, int head_d,
+                    const atn_pe_desc* pe, void* stream) {
+    return pe_apply_core(dtype, in, out, n_rows, seq_len, head_d, pe, (hipStream_t)stream);
+}
+
+int atn_prepare_pe_ex(const atn_pe_desc* pe, int head_d, int max_positions) {
+    if (!pe) return ATN_ERR_NULL_POINTER;
+    if (head_d < 1 || max_positions < 1) return ATN_ERR_BAD_DIMENSION;
+    PePlan plan;
+    int st = check_pe(pe, head_d, &plan);
+    if (st != ATN_OK) return st;
+    if (plan.pek == atn::kPeNone || plan.caller_tables) return ATN_OK;
+    return bind_tables(pe, plan, head_d, max_positions);
+}
+
+// ---- drop-ins ----
+void attention_forward_optimized(const float* Q, const float* K, const float* V, float* out,
+                                 int batch_sz, int num_heads, int len_q, int len_k, int head_d) {
+    sync_or_die(attention_core(ATN_DTYPE_F32, Q, K, V, out, batch_sz, num_heads, len_q, len_k,
+                               head_d, nullptr, nullptr, 0, nullptr),
+                "attention_forward_optimized");
+}
+
+void attention_forward(const float* Q, const float* K, const float* V, float* out, int batch_sz,
+                       int num_heads, int len_q, int len_k, int head_d) {
+    sync_or_die(attention_core(ATN_DTYPE_F32, Q, K, V, out, batch_sz, num_heads, len_q, len_k,
+                               head_d, nullptr, nullptr, 0, nullptr),
+                "attention_forward");
+}
+
+void attention_forward_rope_fused(const float* Q, const float* K, const float* V, float* out,
+                                  const float* cos_cache, const float* sin_cache, int batch_sz,
+                                  int num_heads, int len_q, int len_k, int head_d) {
+    if (!cos_cache || !sin_cache) die(ATN_ERR_NULL_POINTER, "attention_forward_rope_fused");
+    const atn_pe_desc d = rope_desc(head_d, ATN_ROPE_INTERLEAVED, true, true, cos_cache, sin_cache);
+    sync_or_die(attention_core(ATN_DTYPE_F32, Q, K, V, out, batch_sz, num_heads, len_q, len_k,
+                               head_d, &d, nullptr, 0, nullptr),
+                "attention_forward_rope_fused");
+}
+
+void attention_forward_rope_fused_v7_hybrid(const float* Q, const float* K_rotated,
+                                            const float* V, float* out, int batch_sz,
+                                            int num_heads, int len_q, int len_k, int head_d,
+                                            int rotary_dim) {
+    const atn_pe_desc d = rope_desc(rotary_dim, ATN_ROPE_INTERLEAVED, true, false, nullptr, nullptr);
+    if (rotary_dim == 0) die(ATN_ERR_BAD_ROTARY, "attention_forward_rope_fused_v7_hybrid");
+    sync_or_die(attention_core(ATN_DTYPE_F32, Q, K_rotated, V, out, batch_sz, num_heads, len_q,
+                               len_k, head_d, &d, nullptr, 0, nullptr),
+                "attention_forward_rope_fused_v7_hybrid");
+}
+
+void attention_forward_separate_rope(const float* Q, const float* K, const float* V,
+                                     float* Q_rope, float* K_rope, float* out,
+                                     const float* cos_cache, const float* sin_cache, int batch_sz,
+                                     int num_heads, int len_q, int len_k, int head_d,
+                                     int rotary_dim) {
+    const char* w = "attention_forward_separate_rope";
+    if (!cos_cache || !sin_cache || !Q_rope || !K_rope) die(ATN_ERR_NULL_POINTER, w);
+    if (rotary_dim == 0) die(ATN_ERR_BAD_ROTARY, w);
+    const atn_pe_desc d = rope_desc(rotary_dim, ATN_ROPE_INTERLEAVED, true, true, cos_cache, sin_cache);
+    Shape s;
+    int st = check_shape(batch_sz, num_heads, len_q, len_k, head_d, &s);
+    if (st != ATN_OK) die(st, w);
+    st = pe_apply_core(ATN_DTYPE_F32, Q, Q_rope, (long)(s.BH * len_q), len_q, head_d, &d, nullptr);
+    if (st != ATN_OK) die(st, w);
+    st = pe_apply_core(ATN_DTYPE_F32, K, K_rope, (long)(s.BH * len_k), len_k, head_d, &d, nullptr);
+    if (st != ATN_OK) die(st, w);
+    sync_or_die(attention_core(ATN_DTYPE_F32, Q_rope, K_rope, V, out, batch_sz, num_heads, len_q,
+                               len_k, head_d, nullptr, nullptr, 0, nullptr),
+                w);
+}
+
+void rope_forward(const float* input, float* output, const float* cos_cache,
+                  const float* sin_cache, int total_tokens, int hdim, int rotary_dim,
+                  int seq_len) {
+    if (!cos_cache || !sin_cache) die(ATN_ERR_NULL_POINTER, "rope_forward");
+    if (rotary_dim == 0) die(ATN_ERR_BAD_ROTARY, "rope_forward");
+    const atn_pe_desc d = rope_desc(rotary_dim, ATN_ROPE_INTERLEAVED, true, true, cos_cache, sin_cache);
+    sync_or_die(pe_apply_core(ATN_DTYPE_F32, input, output, total_tokens, seq_len, hdim, &d,
+                              nullptr),
+                "rope_forward");
+}
+
+void apply_sinusoidal_embeddings(const float* input, const float* sin_table,
+                                 const float* cos_table, float* output, int total_tokens,
+                                 int hdim, int seqlen) {
+    if (!sin_table || !cos_table) die(ATN_ERR_NULL_POINTER, "apply_sinusoidal_embeddings");
+    const atn_pe_desc d = sin_desc(true, true, sin_table, cos_table);
+    sync_or_die(pe_apply_core(ATN_DTYPE_F32, input, output, total_tokens, seqlen, hdim, &d,
+                              nullptr),
+                "apply_sinusoidal_embeddings");
+}
+
+void attention_forward_sinusoidal_fused(const float* Q, const float* K, const float* V,
+                                        float* out, int batch_sz, int num_heads, int len_q,
+                                        int len_k, int head_d) {
+    const atn_pe_desc d = sin_desc(true, true, nullptr, nullptr);
+    sync_or_die(attention_core(ATN_DTYPE_F32, Q, K, V, out, batch_sz, num_heads, len_q, len_k,
+                               head_d, &d, nullptr, 0, nullptr),
+                "attention_forward_sinusoidal_fused");
+}
+
+void attention_forward_sinusoidal_hybrid(const float* Q, const float* K, const float* V,
+                                         const float* sin_table, const float* cos_table,
+                                         float* K_emb, float* out, int batch_sz, int num_heads,
+                                         int len_q, int len_k, int head_d) {
+    const char* w = "attention_forward_sinusoidal_hybrid";
+    if (!sin_table || !cos_table || !K_emb) die(ATN_ERR_NULL_POINTER, w);
+    Shape s;
+    int st = check_shape(batch_sz, num_heads, len_q, len_k, head_d, &s);
+    if (st != ATN_OK) die(st, w);
+    const atn_pe_desc dk = sin_desc(true, true, sin_table, cos_table);
+    st = pe_apply_core(ATN_DTYPE_F32, K, K_emb, (long)(s.BH * len_k), len_k, head_d, &dk, nullptr);
+    if (st != ATN_OK) die(st, w);
+    const atn_pe_desc dq = sin_desc(true, false, sin_table, cos_table);
+    sync_or_die(attention_core(ATN_DTYPE_F32, Q, K_emb, V, out, batch_sz, num_heads, len_q, len_k,
+                               head_d, &dq, nullptr, 0, nullptr),
+                w);
+}
+
+void attention_forward_sinusoidal_separate(const float* Q, const float* K, const float* V,
+                                           const float* sin_table, const float* cos_table,
+                                           float* Q_emb, float* K_emb, float* out, int batch_sz,
+                                           int num_heads, int len_q, int len_k, int head_d) {
+    const char* w = "attention_forward_sinusoidal_separate";
+    if (!sin_table || !cos_table || !Q_emb || !K_emb) die(ATN_ERR_NULL_POINTER, w);
+    Shape s;
+    int st = check_shape(batch_sz, num_heads, len_q, len_k, head_d, &s);
+    if (st != ATN_OK) die(st, w);
+    const atn_pe_desc d = sin_desc(true, true, sin_table, cos_table);
+    st = pe_apply_core(ATN_DTYPE_F32, Q, Q_emb, (long)(s.BH * len_q), len_q, head_d, &d, nullptr);
+    if (st != ATN_OK) die(st, w);
+    st = pe_apply_core(ATN_DTYPE_F32, K, K_emb, (long)(s.BH * len_k), len_k, head_d, &d, nullptr);
+    if (st != ATN_OK) die(st, w);
+    sync_or_die(attention_core(ATN_DTYPE_F32, Q_emb, K_emb, V, out, batch_sz, num_heads, len_q,
+                               len_k, head_d, nullptr, nullptr, 0, nullptr),
+                w);
+}
+
+void attention_forward_bf16(const atn_bf16* Q, const atn_bf16* K, const atn_bf16* V,
+                            atn_bf16* out, int bs, int nh, int len_q, int len_k, int head_d) {
+    sync_or_die(attention_core(ATN_DTYPE_BF16, Q, K, V, out, bs, nh, len_q, len_k, head_d,
+                               nullptr, nullptr, 0, nullptr),
+                "attention_forward_bf16");
+}
+
+void attention_forward_rope_bf16(const atn_bf16* Q, const atn_bf16* K_rotated,
+                                 const atn_bf16* V, atn_bf16* out, int bs, int nh, int len_q,
+                                 int len_k, int head_d, int rotary_dim) {
+    if (rotary_dim == 0) die(ATN_ERR_BAD_ROTARY, "attention_forward_rope_bf16");
+    const atn_pe_desc d = rope_desc(rotary_dim, ATN_ROPE_INTERLEAVED, true, false, nullptr, nullptr);
+    sync_or_die(attention_core(ATN_DTYPE_BF16, Q, K_rotated, V, out, bs, nh, len_q, len_k, head_d,
+                               &d, nullptr, 0, nullptr),
+                "attention_forward_rope_bf16");
+}
+
+void attention_forward_rope_fused_bf16(const atn_bf16* Q, const atn_bf16* K, const atn_bf16* V,
+                                       atn_bf16* out, int bs, int nh, int len_q, int len_k,
+                                       int head_d) {
+    const atn_pe_desc d = rope_desc(head_d, ATN_ROPE_INTERLEAVED, true, true, nullptr, nullptr);
+    sync_or_die(attention_core(ATN_DTYPE_BF16, Q, K, V, out, bs, nh, len_q, len_k, head_d, &d,
+                               nullptr, 0, nullptr),
+                "attention_forward_rope_fused_bf16");
+}
+
+void attention_forward_sinusoidal_bf16(const atn_bf16* Q, const atn_bf16* K, const atn_bf16* V,
+                                       atn_bf16* out, int bs, int nh, int len_q, int len_k,
+                                       int head_d) {
+    const atn_pe_desc d = sin_desc(true, true, nullptr, nullptr);
+    sync_or_die(attention_core(ATN_DTYPE_BF16, Q, K, V, out, bs, nh, len_q, len_k, head_d, &d,
+                               nullptr, 0, nullptr),
+                "attention_forward_sinusoidal_bf16");
+}
+
+void precompute_rope_cache(float* cos_cache, float* sin_cache, int max_seq_len, int rotary_dim,
+                           float base) {
+    // final/rope.cu:20-40
+    for (int pos = 0; pos < max_seq_len; pos++) {
+        for (int i = 0; i < rotary_dim / 2; i++) {
+            const float freq = 1.0f / powf(base, (2.0f * i) / rotary_dim);
+            const float theta = pos * freq;
+            const float c = cosf(theta), s = sinf(theta);
+            cos_cache[(size_t)pos * rotary_dim + 2 * i] = c;
+            cos_cache[(size_t)pos * rotary_dim + 2 * i + 1] = c;
+            sin_cache[(size_t)pos * rotary_dim + 2 * i] = s;
+            sin_cache[(size_t)pos * rotary_dim + 2 * i + 1] = s;
+        }
+    }
+}
+
+void precompute_sinusoidal_table(float* sin_table, float* cos_table, int seqlen, int hdim) {
+    // final/sinusoidal.cu:838-855
+    for (int pos = 0; pos < seqlen; pos++) {
+        for (int d = 0; d < hdim; d++) {
+            const float freq = 1.0f / powf(10000.0f, (2.0f * (d / 2)) / (float)hdim);
+            const float angle = pos * freq;
+            sin_table[(size_t)pos * hdim + d] = sinf(angle);
+            cos_table[(size_t)pos * hdim + d] = cosf(angle);
+        }
+    }
+}
+
+}  // extern "C"

@@ -1,0 +1,156 @@
+// Device-side building blocks shared by the attention kernels (gfx950 only).
+//
+// Storage types: float (fp32) and uint16_t holding raw bfloat16 bits.  All
+// arithmetic is fp32.  Reductions are wave64: DPP quad/row permutes, one
+// ds_swizzle for the 16-lane hop and two v_readlane for the 32-lane hop, so
+// no LDS crossbar (ds_bpermute) is used inside a wave.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace atn {
+
+constexpr int kWave = 64;
+
+// ---------------------------------------------------------------- bf16 <-> fp32
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
+
+// Round-to-nearest-even fp32 -> bf16, NaN kept quiet.
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+// Element access for the two storage types.
+template <typename T>
+struct Elem;
+
+template <>
+struct Elem<float> {
+    static __device__ __forceinline__ float ld(const float* p, size_t i) { return p[i]; }
+    static __device__ __forceinline__ void st(float* p, size_t i, float v) { p[i] = v; }
+    // 4 consecutive elements; p + i must be 16-byte aligned.
+    static __device__ __forceinline__ float4 ld4(const float* p, size_t i) {
+        return *reinterpret_cast<const float4*>(p + i);
+    }
+    static __device__ __forceinline__ void st4(float* p, size_t i, float4 v) {
+        *reinterpret_cast<float4*>(p + i) = v;
+    }
+    static constexpr int kVecAlign = 16;
+};
+
+template <>
+struct Elem<uint16_t> {
+    static __device__ __forceinline__ float ld(const uint16_t* p, size_t i) {
+        return bf16_bits_to_f32(p[i]);
+    }
+    static __device__ __forceinline__ void st(uint16_t* p, size_t i, float v) {
+        p[i] = f32_to_bf16_bits(v);
+    }
+    // 4 consecutive bf16 (8 bytes); p + i must be 8-byte aligned.
+    static __device__ __forceinline__ float4 ld4(const uint16_t* p, size_t i) {
+        uint2 w = *reinterpret_cast<const uint2*>(p + i);
+        return make_float4(__uint_as_float(w.x << 16), __uint_as_float(w.x & 0xffff0000u),
+                           __uint_as_float(w.y << 16), __uint_as_float(w.y & 0xffff0000u));
+    }
+    static __device__ __forceinline__ void st4(uint16_t* p, size_t i, float4 v) {
+        uint2 w;
+        w.x = (uint32_t)f32_to_bf16_bits(v.x) | ((uint32_t)f32_to_bf16_bits(v.y) << 16);
+        w.y = (uint32_t)f32_to_bf16_bits(v.z) | ((uint32_t)f32_to_bf16_bits(v.w) << 16);
+        *reinterpret_cast<uint2*>(p + i) = w;
+    }
+    static constexpr int kVecAlign = 8;
+};
+
+// ---------------------------------------------------------------- wave64 reductions
+// DPP controls (GFX9 encoding).
+constexpr int kDppQuadXor1 = 0xB1;     // quad_perm [1,0,3,2]
+constexpr int kDppQuadXor2 = 0x4E;     // quad_perm [2,3,0,1]
+constexpr int kDppRowHalfMirror = 0x141;
+constexpr int kDppRowMirror = 0x140;
+// ds_swizzle bitmask mode: and 0x1f, or 0, xor 0x10 -> lane ^ 16 within 32.
+constexpr int kSwizzleXor16 = 0x401F;
+
+template <int Ctrl>
+__device__ __forceinline__ float dpp(float v) {
+    return __int_as_float(
+        __builtin_amdgcn_update_dpp(0, __float_as_int(v), Ctrl, 0xF, 0xF, false));
+}
+
+__device__ __forceinline__ float swz_xor16(float v) {
+    return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), kSwizzleXor16));
+}
+
+__device__ __forceinline__ float lane_read(float v, int lane) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
+// Full-wave max; result is wave-uniform.
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, dpp<kDppQuadXor1>(v));
+    v = fmaxf(v, dpp<kDppQuadXor2>(v));
+    v = fmaxf(v, dpp<kDppRowHalfMirror>(v));
+    v = fmaxf(v, dpp<kDppRowMirror>(v));
+    v = fmaxf(v, swz_xor16(v));
+    return fmaxf(lane_read(v, 0), lane_read(v, 32));
+}
+
+// Full-wave sum; result is wave-uniform.
+__device__ __forceinline__ float wave_sum(float v) {
+    v += dpp<kDppQuadXor1>(v);
+    v += dpp<kDppQuadXor2>(v);
+    v += dpp<kDppRowHalfMirror>(v);
+    v += dpp<kDppRowMirror>(v);
+    v += swz_xor16(v);
+    return lane_read(v, 0) + lane_read(v, 32);
+}
+
+// ---------------------------------------------------------------- positional encodings
+enum PeKind : int { kPeNone = 0, kPeRopeInterleaved = 1, kPeRopeHalf = 2, kPeSinusoidal = 3 };
+
+// Angle tables for one side (Q or K).  Two layouts:
+//   compact (dup = 0): a[pos*ld + f], b[pos*ld + f] indexed by frequency f
+//     (the library's own tables: RoPE a = cos, b = sin, f = pair index;
+//      sinusoidal a = sin, b = cos, f = d / 2);
+//   caller (dup = 1): the reference's host formats -- RoPE caches
+//     [pos][rotary_dim] with each value duplicated at 2i and 2i+1
+//     (final/rope.cu:20-40), sinusoidal tables [pos][D] indexed by d
+//     (final/sinusoidal.cu:838-855).
+struct PeSide {
+    const float* a;
+    const float* b;
+    int ld;
+    int dup;
+    int rotary;  // RoPE: rotated width (even); sinusoidal: unused
+    int on;      // 0: this side is not encoded
+};
+
+// fp32 rotation written as separate multiply and subtract/add so the result
+// equals the reference CPU path's x_e*c - x_o*s bit for bit.
+__device__ __forceinline__ float rot_first(float x0, float x1, float c, float s) {
+#pragma clang fp contract(off)
+    return x0 * c - x1 * s;
+}
+__device__ __forceinline__ float rot_second(float x0, float x1, float c, float s) {
+#pragma clang fp contract(off)
+    return x0 * s + x1 * c;
+}
+
+// cos/sin for RoPE frequency f at position pos.
+__device__ __forceinline__ void rope_cs(const PeSide& t, int pos, int f, float& c, float& s) {
+    const size_t idx = (size_t)pos * t.ld + (t.dup ? 2 * f : f);
+    c = t.a[idx];
+    s = t.b[idx];
+}
+
+// Sinusoidal PE value for dim d at position pos (even d: sin, odd d: cos).
+__device__ __forceinline__ float sin_pe(const PeSide& t, int pos, int d) {
+    const size_t idx = (size_t)pos * t.ld + (t.dup ? d : (d >> 1));
+    return (d & 1) ? t.b[idx] : t.a[idx];
+}
+
+}  // namespace atn

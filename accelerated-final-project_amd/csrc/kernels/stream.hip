@@ -1,0 +1,418 @@
+// Split-D streaming attention for any shape (gfx950).
+//
+// Attention with head_dim D much larger than the sequence lengths is a
+// bandwidth problem: per (b,h) the score matrix is only Lq x Lk while Q, K
+// and V are Lq x D / Lk x D.  One workgroup per query row (the reference's
+// launch, final/attention.cu:209-215) re-streams all of K and V per query and
+// keeps <= 64 of 256 threads busy; here the work is cut along D instead:
+//
+//   stage 1  k_qk_partial  S_part[split][bh][i][j] = sum_{d in chunk} q~_id k~_jd
+//            (q~, k~ = Q/K with the positional encoding applied at load), one
+//            workgroup per (bh, 64x64 score tile, D-chunk) -- every Q/K element
+//            is read once when the tile covers Lq x Lk;
+//   stage 2  k_softmax     P = softmax(scale * sum_split S_part) per row, exact
+//            (max, exp, sum, divide -- final/attention.cu:262-270 order);
+//   stage 3  k_pv          O[bh][i][d] = sum_j P_ij V_jd, one workgroup per
+//            (bh, 64 rows, 64 dims) -- every V element is read once per
+//            64-row query block.
+//
+// All math is fp32; bf16 storage is widened at load and rounded (RNE) once
+// at the final store.  Workgroups are 256 threads (4 waves) computing 64x64
+// tiles with 4x4 register blocks from LDS-staged 16-deep slices.
+#include "common.hpp"
+#include "launch.hpp"
+
+namespace atn {
+
+namespace {
+
+constexpr int kTile = 64;   // rows x cols of an output tile
+constexpr int kDepth = 16;  // contraction slice staged in LDS per step
+constexpr int kPad = 4;     // LDS row padding (floats), keeps float4 alignment
+
+// Loads x[d..d+3] of one row (row pointer xr, position pos), applies the
+// positional encoding of this side, and returns fp32.  Elements at or past
+// dend read as 0.  d is a multiple of 4.
+template <typename T, int PEK>
+__device__ __forceinline__ float4 load_row4_pe(const T* __restrict__ xr, int pos, int d, int dend,
+                                              const PeSide& pe, bool vec_ok) {
+    float v[4] = {0.f, 0.f, 0.f, 0.f};
+    if (vec_ok && d + 3 < dend) {
+        float4 t = Elem<T>::ld4(xr, d);
+        v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
+    } else {
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+            if (d + c < dend) v[c] = Elem<T>::ld(xr, d + c);
+    }
+    if constexpr (PEK == kPeRopeInterleaved) {
+        if (pe.on) {
+#pragma unroll
+            for (int c = 0; c < 4; c += 2) {
+                const int e = d + c;  // even
+                if (e < pe.rotary) {
+                    float cs, sn;
+                    rope_cs(pe, pos, e >> 1, cs, sn);
+                    const float x0 = v[c], x1 = v[c + 1];
+                    v[c] = rot_first(x0, x1, cs, sn);
+                    v[c + 1] = rot_second(x0, x1, cs, sn);
+                }
+            }
+        }
+    } else if constexpr (PEK == kPeRopeHalf) {
+        if (pe.on) {
+            const int h = pe.rotary >> 1;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const int e = d + c;
+                if (e < pe.rotary) {
+                    const bool lo = e < h;
+                    const int f = lo ? e : e - h;
+                    const float xp = Elem<T>::ld(xr, lo ? e + h : e - h);
+                    float cs, sn;
+                    rope_cs(pe, pos, f, cs, sn);
+                    v[c] = lo ? rot_first(v[c], xp, cs, sn) : rot_second(xp, v[c], cs, sn);
+                }
+            }
+        }
+    } else if constexpr (PEK == kPeSinusoidal) {
+        if (pe.on) {
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+                if (d + c < dend) v[c] = v[c] + sin_pe(pe, pos, d + c);
+        }
+    }
+    return make_float4(v[0], v[1], v[2], v[3]);
+}
+
+template <typename T, int PEK>
+__global__ __launch_bounds__(256) void k_qk_partial(const T* __restrict__ Q,
+                                                     const T* __restrict__ K,
+                                                     float* __restrict__ S, int BH, int Lq, int Lk,
+                                                     int D, int dchunk, int nsplit, int tiles_q,
+                                                     int tiles_k, PeSide pq, PeSide pk,
+                                                     int vec_ok) {
+    __shared__ float Qs[kDepth][kTile + kPad];
+    __shared__ float Ks[kDepth][kTile + kPad];
+
+    const int tid = threadIdx.x;
+    long wg = blockIdx.x;
+    const int split = (int)(wg % nsplit);
+    wg /= nsplit;
+    const int tk = (int)(wg % tiles_k);
+    wg /= tiles_k;
+    const int tq = (int)(wg % tiles_q);
+    const int bh = (int)(wg / tiles_q);
+
+    const int q0 = tq * kTile, k0 = tk * kTile;
+    const int dbeg = split * dchunk;
+    const int dend = min(D, dbeg + dchunk);
+
+    const int lrow = tid >> 2;       // loader: row within tile
+    const int lcol = (tid & 3) * 4;  // loader: first of 4 depth slots
+    const int ty = tid >> 4, tx = tid & 15;
+
+    const int qi = q0 + lrow, kj = k0 + lrow;
+    const T* qrow = Q + ((size_t)bh * Lq + (qi < Lq ? qi : 0)) * D;
+    const T* krow = K + ((size_t)bh * Lk + (kj < Lk ? kj : 0)) * D;
+    const bool vec = vec_ok != 0;
+
+    float acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = 0.f;
+
+    for (int d0 = dbeg; d0 < dend; d0 += kDepth) {
+        float4 qv = make_float4(0.f, 0.f, 0.f, 0.f), kv = qv;
+        if (qi < Lq) qv = load_row4_pe<T, PEK>(qrow, qi, d0 + lcol, dend, pq, vec);
+        if (kj < Lk) kv = load_row4_pe<T, PEK>(krow, kj, d0 + lcol, dend, pk, vec);
+        __syncthreads();
+        Qs[lcol + 0][lrow] = qv.x; Qs[lcol + 1][lrow] = qv.y;
+        Qs[lcol + 2][lrow] = qv.z; Qs[lcol + 3][lrow] = qv.w;
+        Ks[lcol + 0][lrow] = kv.x; Ks[lcol + 1][lrow] = kv.y;
+        Ks[lcol + 2][lrow] = kv.z; Ks[lcol + 3][lrow] = kv.w;
+        __syncthreads();
+#pragma unroll
+        for (int dd = 0; dd < kDepth; ++dd) {
+            const float4 a = *reinterpret_cast<const float4*>(&Qs[dd][ty * 4]);
+            const float4 b = *reinterpret_cast<const float4*>(&Ks[dd][tx * 4]);
+            const float av[4] = {a.x, a.y, a.z, a.w};
+            const float bv[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(av[i], bv[j], acc[i][j]);
+        }
+    }
+
+    float* Sp = S + ((size_t)split * BH + bh) * (size_t)Lq * Lk;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int r = q0 + ty * 4 + i;
+        if (r >= Lq) continue;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int c = k0 + tx * 4 + j;
+            if (c < Lk) Sp[(size_t)r * Lk + c] = acc[i][j];
+        }
+    }
+}
+
+// One workgroup per score row.  Separate LDS slots for the max and the sum
+// reductions, so the second reduction never overwrites a slot the first may
+// still be reading.
+__global__ __launch_bounds__(256) void k_softmax(const float* __restrict__ S, float* P, long rows,
+                                                  int Lk, int nsplit, size_t split_stride,
+                                                  float scale) {
+    __shared__ float red_max[4];
+    __shared__ float red_sum[4];
+    const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63;
+
+    for (long r = blockIdx.x; r < rows; r += gridDim.x) {
+        const float* s = S + (size_t)r * Lk;
+        float* p = P + (size_t)r * Lk;
+        float m = -INFINITY;
+        for (int j = tid; j < Lk; j += 256) {
+            float acc = s[j];
+            for (int sp = 1; sp < nsplit; ++sp) acc += s[(size_t)sp * split_stride + j];
+            acc *= scale;
+            p[j] = acc;
+            m = fmaxf(m, acc);
+        }
+        m = wave_max(m);
+        if (lane == 0) red_max[wid] = m;
+        __syncthreads();
+        m = fmaxf(fmaxf(red_max[0], red_max[1]), fmaxf(red_max[2], red_max[3]));
+
+        float l = 0.f;
+        for (int j = tid; j < Lk; j += 256) {
+            const float e = expf(p[j] - m);
+            p[j] = e;
+            l += e;
+        }
+        l = wave_sum(l);
+        if (lane == 0) red_sum[wid] = l;
+        __syncthreads();
+        l = (red_sum[0] + red_sum[1]) + (red_sum[2] + red_sum[3]);
+        for (int j = tid; j < Lk; j += 256) p[j] = p[j] / l;
+        __syncthreads();  // red_* reused by the next row
+    }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void k_pv(const float* __restrict__ P, const T* __restrict__ V,
+                                             T* __restrict__ O, int Lq, int Lk, int D,
+                                             int tiles_q, int tiles_d, int vec_ok) {
+    __shared__ float Ps[kDepth][kTile + kPad];  // [key][row]
+    __shared__ float Vs[kDepth][kTile + kPad];  // [key][dim]
+
+    const int tid = threadIdx.x;
+    long wg = blockIdx.x;
+    const int td = (int)(wg % tiles_d);
+    wg /= tiles_d;
+    const int tq = (int)(wg % tiles_q);
+    const int bh = (int)(wg / tiles_q);
+    const int q0 = tq * kTile, d0 = td * kTile;
+    const int ty = tid >> 4, tx = tid & 15;
+
+    // P loader: 64 rows x 16 keys, 4 keys per thread
+    const int prow = tid >> 2, pk = (tid & 3) * 4;
+    // V loader: 16 keys x 64 dims, 4 dims per thread
+    const int vkey = tid >> 4, vd = (tid & 15) * 4;
+    const bool vec = vec_ok != 0;
+    const bool p_vec = (Lk & 3) == 0;
+
+    const float* prow_ptr = P + ((size_t)bh * Lq + (q0 + prow < Lq ? q0 + prow : 0)) * Lk;
+    const T* Vh = V + (size_t)bh * Lk * D;
+
+    float acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = 0.f;
+
+    for (int k0 = 0; k0 < Lk; k0 += kDepth) {
+        float pv[4] = {0.f, 0.f, 0.f, 0.f};
+        if (q0 + prow < Lq) {
+            const int kk = k0 + pk;
+            if (p_vec && kk + 3 < Lk) {
+                const float4 t = *reinterpret_cast<const float4*>(prow_ptr + kk);
+                pv[0] = t.x; pv[1] = t.y; pv[2] = t.z; pv[3] = t.w;
+            } else {
+#pragma unroll
+                for (int c = 0; c < 4; ++c)
+                    if (kk + c < Lk) pv[c] = prow_ptr[kk + c];
+            }
+        }
+        float vv[4] = {0.f, 0.f, 0.f, 0.f};
+        const int key = k0 + vkey;
+        if (key < Lk) {
+            const T* vr = Vh + (size_t)key * D;
+            const int dd = d0 + vd;
+            if (vec && dd + 3 < D) {
+                const float4 t = Elem<T>::ld4(vr, dd);
+                vv[0] = t.x; vv[1] = t.y; vv[2] = t.z; vv[3] = t.w;
+            } else {
+#pragma unroll
+                for (int c = 0; c < 4; ++c)
+                    if (dd + c < D) vv[c] = Elem<T>::ld(vr, dd + c);
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int c = 0; c < 4; ++c) Ps[pk + c][prow] = pv[c];
+        *reinterpret_cast<float4*>(&Vs[vkey][vd]) = make_float4(vv[0], vv[1], vv[2], vv[3]);
+        __syncthreads();
+#pragma unroll
+        for (int kk = 0; kk < kDepth; ++kk) {
+            const float4 a = *reinterpret_cast<const float4*>(&Ps[kk][ty * 4]);
+            const float4 b = *reinterpret_cast<const float4*>(&Vs[kk][tx * 4]);
+            const float av[4] = {a.x, a.y, a.z, a.w};
+            const float bv[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(av[i], bv[j], acc[i][j]);
+        }
+    }
+
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int r = q0 + ty * 4 + i;
+        if (r >= Lq) continue;
+        T* orow = O + ((size_t)bh * Lq + r) * D;
+        const int dd = d0 + tx * 4;
+        if (vec && dd + 3 < D) {
+            Elem<T>::st4(orow, dd, make_float4(acc[i][0], acc[i][1], acc[i][2], acc[i][3]));
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                if (dd + j < D) Elem<T>::st(orow, dd + j, acc[i][j]);
+        }
+    }
+}
+
+// Positional-encoding pre-pass: out[row] = PE(in[row]) with position
+// row % seq_len (the "separate"/"hybrid" pipelines' pre-pass).
+template <typename T, int PEK>
+__global__ __launch_bounds__(256) void k_pe_apply(const T* __restrict__ in, T* __restrict__ out,
+                                                   long n_rows, int seq_len, int D, PeSide pe,
+                                                   int vec_ok) {
+    const bool vec = vec_ok != 0;
+    for (long row = blockIdx.x; row < n_rows; row += gridDim.x) {
+        const int pos = (int)(row % seq_len);
+        const T* xr = in + (size_t)row * D;
+        T* yr = out + (size_t)row * D;
+        for (int d = threadIdx.x * 4; d < D; d += 256 * 4) {
+            const float4 v = load_row4_pe<T, PEK>(xr, pos, d, D, pe, vec);
+            if (vec && d + 3 < D) {
+                Elem<T>::st4(yr, d, v);
+            } else {
+                const float vv[4] = {v.x, v.y, v.z, v.w};
+                for (int c = 0; c < 4 && d + c < D; ++c) Elem<T>::st(yr, d + c, vv[c]);
+            }
+        }
+    }
+}
+
+template <typename T>
+hipError_t qk_partial_t(int pek, const void* Q, const void* K, float* S, int BH, int Lq, int Lk,
+                        int D, int dchunk, int nsplit, const PeSide& pq, const PeSide& pk,
+                        int vec_ok, hipStream_t st) {
+    const int tiles_q = (Lq + kTile - 1) / kTile, tiles_k = (Lk + kTile - 1) / kTile;
+    const long nwg = (long)BH * tiles_q * tiles_k * nsplit;
+    const T* q = static_cast<const T*>(Q);
+    const T* k = static_cast<const T*>(K);
+    const dim3 grid((unsigned)nwg), block(256);
+    switch (pek) {
+        case kPeNone:
+            hipLaunchKernelGGL((k_qk_partial<T, kPeNone>), grid, block, 0, st, q, k, S, BH, Lq, Lk,
+                               D, dchunk, nsplit, tiles_q, tiles_k, pq, pk, vec_ok);
+            break;
+        case kPeRopeInterleaved:
+            hipLaunchKernelGGL((k_qk_partial<T, kPeRopeInterleaved>), grid, block, 0, st, q, k, S,
+                               BH, Lq, Lk, D, dchunk, nsplit, tiles_q, tiles_k, pq, pk, vec_ok);
+            break;
+        case kPeRopeHalf:
+            hipLaunchKernelGGL((k_qk_partial<T, kPeRopeHalf>), grid, block, 0, st, q, k, S, BH, Lq,
+                               Lk, D, dchunk, nsplit, tiles_q, tiles_k, pq, pk, vec_ok);
+            break;
+        case kPeSinusoidal:
+            hipLaunchKernelGGL((k_qk_partial<T, kPeSinusoidal>), grid, block, 0, st, q, k, S, BH,
+                               Lq, Lk, D, dchunk, nsplit, tiles_q, tiles_k, pq, pk, vec_ok);
+            break;
+        default:
+            return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+template <typename T>
+hipError_t pe_apply_t(int pek, const void* in, void* out, long n_rows, int seq_len, int D,
+                      const PeSide& pe, int vec_ok, hipStream_t st) {
+    const long nwg = n_rows < 65536 ? n_rows : 65536;
+    const T* x = static_cast<const T*>(in);
+    T* y = static_cast<T*>(out);
+    const dim3 grid((unsigned)nwg), block(256);
+    switch (pek) {
+        case kPeRopeInterleaved:
+            hipLaunchKernelGGL((k_pe_apply<T, kPeRopeInterleaved>), grid, block, 0, st, x, y,
+                               n_rows, seq_len, D, pe, vec_ok);
+            break;
+        case kPeRopeHalf:
+            hipLaunchKernelGGL((k_pe_apply<T, kPeRopeHalf>), grid, block, 0, st, x, y, n_rows,
+                               seq_len, D, pe, vec_ok);
+            break;
+        case kPeSinusoidal:
+            hipLaunchKernelGGL((k_pe_apply<T, kPeSinusoidal>), grid, block, 0, st, x, y, n_rows,
+                               seq_len, D, pe, vec_ok);
+            break;
+        default:
+            return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_qk_partial(int dtype, int pek, const void* Q, const void* K, float* S, int BH,
+                             int Lq, int Lk, int D, int dchunk, int nsplit, const PeSide& pq,
+                             const PeSide& pk, int vec_ok, hipStream_t st) {
+    if (dtype == kDtypeF32)
+        return qk_partial_t<float>(pek, Q, K, S, BH, Lq, Lk, D, dchunk, nsplit, pq, pk, vec_ok,
+                                   st);
+    return qk_partial_t<uint16_t>(pek, Q, K, S, BH, Lq, Lk, D, dchunk, nsplit, pq, pk, vec_ok, st);
+}
+
+hipError_t launch_softmax(const float* S, float* P, long rows, int Lk, int nsplit,
+                          size_t split_stride, float scale, hipStream_t st) {
+    const long nwg = rows < 65536 ? rows : 65536;
+    hipLaunchKernelGGL(k_softmax, dim3((unsigned)nwg), dim3(256), 0, st, S, P, rows, Lk, nsplit,
+                       split_stride, scale);
+    return hipGetLastError();
+}
+
+hipError_t launch_pv(int dtype, const float* P, const void* V, void* O, int BH, int Lq, int Lk,
+                     int D, int vec_ok, hipStream_t st) {
+    const int tiles_q = (Lq + kTile - 1) / kTile, tiles_d = (D + kTile - 1) / kTile;
+    const dim3 grid((unsigned)((long)BH * tiles_q * tiles_d)), block(256);
+    if (dtype == kDtypeF32) {
+        hipLaunchKernelGGL((k_pv<float>), grid, block, 0, st, P, static_cast<const float*>(V),
+                           static_cast<float*>(O), Lq, Lk, D, tiles_q, tiles_d, vec_ok);
+    } else {
+        hipLaunchKernelGGL((k_pv<uint16_t>), grid, block, 0, st, P,
+                           static_cast<const uint16_t*>(V), static_cast<uint16_t*>(O), Lq, Lk, D,
+                           tiles_q, tiles_d, vec_ok);
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_pe_apply(int dtype, int pek, const void* in, void* out, long n_rows,
+                           int seq_len, int D, const PeSide& pe, int vec_ok, hipStream_t st) {
+    if (dtype == kDtypeF32)
+        return pe_apply_t<float>(pek, in, out, n_rows, seq_len, D, pe, vec_ok, st);
+    return pe_apply_t<uint16_t>(pek, in, out, n_rows, seq_len, D, pe, vec_ok, st);
+}
+
+}  // namespace atn

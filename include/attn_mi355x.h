@@ -1,0 +1,232 @@
+/*
+ * attn_mi355x.h -- C ABI of the MI355X (gfx950) large-head-dim attention library.
+ *
+ * Drop-in entry points keep the reference project's names, argument order and
+ * semantics (agoel2005/accelerated-final-project, cited as file:line):
+ *   - all tensors are device pointers, contiguous [batch][heads][len][head_d];
+ *   - scale = 1/sqrtf(head_d) (also for RoPE, final/rope.cu:234); no mask;
+ *   - positions run 0..len-1 independently for Q and for K;
+ *   - RoPE and sinusoidal bases are 10000;
+ *   - the call is synchronous (the reference ends every launcher with
+ *     cudaDeviceSynchronize, final/attention.cu:219-220) and, on any error,
+ *     prints "attn_mi355x error <code> (<text>) at <entry point>" to stderr
+ *     and calls exit(EXIT_FAILURE) like the reference's CUDA_CHECK
+ *     (final/attention.cu:12-21).
+ * The atn_*_ex entry points are the asynchronous, non-exiting forms: they
+ * validate every argument before any HIP call, return an ATN_* status and
+ * enqueue on the given stream (a hipStream_t passed as void*; NULL = the
+ * null stream).
+ *
+ * bf16 tensors are raw bfloat16 bits (uint16_t), the upper half of an IEEE
+ * float32; conversions round to nearest even.  Arithmetic is fp32 throughout
+ * (accumulation, softmax), bf16 outputs are rounded once at the end.
+ *
+ * Buffers are owned by the caller.  `out` must not alias an input.  Pointers
+ * need only element alignment; 16-byte (fp32) / 8-byte (bf16) alignment with
+ * head_d % 4 == 0 selects the vector-load path.
+ */
+#ifndef ATTN_MI355X_H
+#define ATTN_MI355X_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef uint16_t atn_bf16;
+
+/* ---- status codes (returned by every atn_*_ex function) ---- */
+#define ATN_OK 0
+#define ATN_ERR_NULL_POINTER (-1)   /* a required pointer is NULL */
+#define ATN_ERR_BAD_DIMENSION (-2)  /* a size is < 1 */
+#define ATN_ERR_BAD_ROTARY (-3)     /* rotary_dim odd, < 2 or > head_d */
+#define ATN_ERR_SIZE_OVERFLOW (-4)  /* an element count overflows 63 bits */
+#define ATN_ERR_ALIASING (-5)       /* out overlaps an input */
+#define ATN_ERR_NO_DEVICE (-6)      /* no HIP device is visible */
+#define ATN_ERR_HIP (-7)            /* a HIP runtime call failed */
+#define ATN_ERR_WORKSPACE (-8)      /* caller workspace too small */
+#define ATN_ERR_BAD_ARGUMENT (-9)   /* enum out of range, bad table size ... */
+#define ATN_ERR_MISALIGNED (-10)    /* pointer not aligned to its element size */
+
+/* Text for a status code (static storage). */
+const char *atn_status_string(int status);
+/* hipError_t of the last failing HIP call in this thread (0 if none). */
+int atn_last_hip_error(void);
+
+/* ---- enums of the _ex interface ---- */
+#define ATN_DTYPE_F32 0
+#define ATN_DTYPE_BF16 1
+
+#define ATN_PE_NONE 0
+#define ATN_PE_ROPE 1
+#define ATN_PE_SINUSOIDAL 2
+
+#define ATN_ROPE_INTERLEAVED 0 /* pairs (2i, 2i+1): every reference RoPE kernel */
+#define ATN_ROPE_HALF 1        /* pairs (i, i + rotary_dim/2) */
+
+/* Positional encoding applied to Q and/or K inside the attention call.
+ * Angles: RoPE theta(pos, i) = pos * (1/powf(base, (2i)/rotary_dim));
+ * sinusoidal angle(pos, d) = pos * (1/powf(10000, 2*(d/2)/head_d)), even d
+ * adds sin, odd d adds cos (final/sinusoidal.cu:838-855).
+ * Tables: NULL = the library builds its own (host libm, uploaded once per
+ * device and shape, then cached); or the caller's device tables in the
+ * reference formats -- RoPE cos/sin caches [pos][rotary_dim] with values
+ * duplicated at 2i and 2i+1 (final/rope.cu:20-40), sinusoidal sin/cos
+ * tables [pos][head_d] (final/sinusoidal.cu:838-855); they need at least
+ * max(len_q, len_k) rows. */
+typedef struct atn_pe_desc {
+    int kind;          /* ATN_PE_* */
+    int pairing;       /* RoPE: ATN_ROPE_* */
+    int rotary_dim;    /* RoPE: rotated width (even, <= head_d); 0 = head_d */
+    int apply_q;       /* nonzero: encode Q */
+    int apply_k;       /* nonzero: encode K */
+    float base;        /* RoPE base; 0 = 10000 (sinusoidal is always 10000) */
+    const float *table_a; /* RoPE cos cache / sinusoidal sin table, or NULL */
+    const float *table_b; /* RoPE sin cache / sinusoidal cos table, or NULL */
+} atn_pe_desc;
+
+/* ==================== drop-in entry points (synchronous) ==================== */
+
+/* fp32 fused SDPA.  Replaces attention_forward_optimized,
+ * final/attention.cu:195-221 (kernel :84-191); the dispatcher copy in
+ * kernels/attention_kernel.cu:304-336 has the same contract. */
+void attention_forward_optimized(const float *Q, const float *K, const float *V, float *out,
+                                 int batch_sz, int num_heads, int len_q, int len_k, int head_d);
+
+/* Small-head-dim path of the reference dispatcher: attention_forward,
+ * kernels/attention_kernel.cu:339-365.  Same results as above. */
+void attention_forward(const float *Q, const float *K, const float *V, float *out, int batch_sz,
+                       int num_heads, int len_q, int len_k, int head_d);
+
+/* fp32 RoPE, full fusion with caller caches [pos][head_d] (interleaved,
+ * rotary = head_d): attention_forward_rope_fused, final/rope.cu:1209-1238
+ * (kernel :1058-1207). */
+void attention_forward_rope_fused(const float *Q, const float *K, const float *V, float *out,
+                                  const float *cos_cache, const float *sin_cache, int batch_sz,
+                                  int num_heads, int len_q, int len_k, int head_d);
+
+/* fp32 RoPE v7 hybrid: Q rotated in-kernel (interleaved, partial
+ * rotary_dim, base 10000), K already rotated by the caller:
+ * attention_forward_rope_fused_v7_hybrid, final/rope.cu:230-247
+ * (kernel :102-228). */
+void attention_forward_rope_fused_v7_hybrid(const float *Q, const float *K_rotated,
+                                            const float *V, float *out, int batch_sz,
+                                            int num_heads, int len_q, int len_k, int head_d,
+                                            int rotary_dim);
+
+/* fp32 RoPE "separate" pipeline: pre-pass Q->Q_rope, K->K_rope with caller
+ * caches [pos][rotary_dim], then plain attention:
+ * attention_forward_separate_rope, final/rope.cu:1379-1416.  Position of a
+ * token is its row index within its sequence (the reference's rope_kernel
+ * uses token % 64, final/rope.cu:1257, correct only for len = 64). */
+void attention_forward_separate_rope(const float *Q, const float *K, const float *V,
+                                     float *Q_rope, float *K_rope, float *out,
+                                     const float *cos_cache, const float *sin_cache, int batch_sz,
+                                     int num_heads, int len_q, int len_k, int head_d,
+                                     int rotary_dim);
+
+/* RoPE pre-pass over total_tokens rows of head_d (interleaved, dims >=
+ * rotary_dim copied), position = token % seq_len: replaces the rope_kernel
+ * launch of final/rope.cu:1240-1280 (whose position is token % 64). */
+void rope_forward(const float *input, float *output, const float *cos_cache,
+                  const float *sin_cache, int total_tokens, int hdim, int rotary_dim,
+                  int seq_len);
+
+/* Sinusoidal PE pre-pass: output = input + PE(token % seqlen) with caller
+ * tables [pos][hdim]: replaces the apply_sinusoidal_embeddings launch,
+ * final/sinusoidal.cu:714-744 (same argument order). */
+void apply_sinusoidal_embeddings(const float *input, const float *sin_table,
+                                 const float *cos_table, float *output, int total_tokens,
+                                 int hdim, int seqlen);
+
+/* fp32 sinusoidal V5 full fusion (PE computed for q and k inside the call):
+ * the reference launches attention_fwd_kernel_sinusoidal_fused_v5 directly
+ * (final/sinusoidal.cu:82-234, launch :1135-1137); this is its host form. */
+void attention_forward_sinusoidal_fused(const float *Q, const float *K, const float *V,
+                                        float *out, int batch_sz, int num_heads, int len_q,
+                                        int len_k, int head_d);
+
+/* fp32 sinusoidal hybrid: K_emb = K + PE (pre-pass), Q + PE fused, caller
+ * tables [pos][head_d]: attention_forward_sinusoidal_hybrid,
+ * kernels/attention_kernel_sinusoidal_hybrid.cu:282-315. */
+void attention_forward_sinusoidal_hybrid(const float *Q, const float *K, const float *V,
+                                         const float *sin_table, const float *cos_table,
+                                         float *K_emb, float *out, int batch_sz, int num_heads,
+                                         int len_q, int len_k, int head_d);
+
+/* fp32 sinusoidal separate: Q_emb, K_emb pre-passes then plain attention:
+ * attention_forward_sinusoidal_separate,
+ * kernels/attention_kernel_sinusoidal_hybrid.cu:465-502. */
+void attention_forward_sinusoidal_separate(const float *Q, const float *K, const float *V,
+                                           const float *sin_table, const float *cos_table,
+                                           float *Q_emb, float *K_emb, float *out, int batch_sz,
+                                           int num_heads, int len_q, int len_k, int head_d);
+
+/* bf16 SDPA (fp32 math): attention_forward_bf16,
+ * kernels/attention_bf16_optimized_fused.cu:493-505 (kernel :80-180). */
+void attention_forward_bf16(const atn_bf16 *Q, const atn_bf16 *K, const atn_bf16 *V,
+                            atn_bf16 *out, int bs, int nh, int len_q, int len_k, int head_d);
+
+/* bf16 RoPE v7 form (K pre-rotated, Q rotated in-kernel, partial
+ * rotary_dim): attention_forward_rope_bf16,
+ * kernels/attention_bf16_optimized_fused.cu:507-519 (kernel :186-321). */
+void attention_forward_rope_bf16(const atn_bf16 *Q, const atn_bf16 *K_rotated,
+                                 const atn_bf16 *V, atn_bf16 *out, int bs, int nh, int len_q,
+                                 int len_k, int head_d, int rotary_dim);
+
+/* bf16 RoPE full fusion (Q and K rotated in-kernel, interleaved, rotary =
+ * head_d, base 10000).  The reference exports this form under the same name
+ * as the v7 one (kernels/attention_bf16_all_kernels.cu:451-466, kernel
+ * :211-323); it is exported here under a distinct name. */
+void attention_forward_rope_fused_bf16(const atn_bf16 *Q, const atn_bf16 *K, const atn_bf16 *V,
+                                       atn_bf16 *out, int bs, int nh, int len_q, int len_k,
+                                       int head_d);
+
+/* bf16 sinusoidal V5: attention_forward_sinusoidal_bf16,
+ * kernels/attention_bf16_optimized_fused.cu:521-533 (kernel :327-487). */
+void attention_forward_sinusoidal_bf16(const atn_bf16 *Q, const atn_bf16 *K, const atn_bf16 *V,
+                                       atn_bf16 *out, int bs, int nh, int len_q, int len_k,
+                                       int head_d);
+
+/* Host-side table builders in the reference's formats (host memory):
+ * precompute_rope_cache, final/rope.cu:20-40; the sinusoidal table of
+ * generate_sinusoidal_embeddings_cpu, final/sinusoidal.cu:838-855
+ * (= precompute_sinusoidal_table, kernels/attention_kernel_sinusoidal_hybrid.cu:75-87). */
+void precompute_rope_cache(float *cos_cache, float *sin_cache, int max_seq_len, int rotary_dim,
+                           float base);
+void precompute_sinusoidal_table(float *sin_table, float *cos_table, int seqlen, int hdim);
+
+/* ==================== asynchronous, status-returning forms ==================== */
+
+/* General fused attention: dtype ATN_DTYPE_*, optional positional encoding
+ * (pe == NULL: plain SDPA), workspace == NULL: library-managed scratch
+ * (allocated on first use per device, grown as needed), else caller scratch
+ * of at least atn_attention_workspace_bytes(...) bytes.  Enqueued on stream. */
+int atn_attention_fwd_ex(int dtype, const void *Q, const void *K, const void *V, void *out,
+                         int batch, int heads, int len_q, int len_k, int head_d,
+                         const atn_pe_desc *pe, void *workspace, size_t workspace_bytes,
+                         void *stream);
+
+/* Scratch bytes atn_attention_fwd_ex needs for this shape (0 on bad input). */
+size_t atn_attention_workspace_bytes(int dtype, int batch, int heads, int len_q, int len_k,
+                                     int head_d, const atn_pe_desc *pe);
+
+/* Positional-encoding pre-pass over n_rows rows of head_d, position =
+ * row % seq_len (pe->apply_q/apply_k are ignored; the encoding is applied). */
+int atn_pe_apply_ex(int dtype, const void *in, void *out, long n_rows, int seq_len, int head_d,
+                    const atn_pe_desc *pe, void *stream);
+
+/* Prepares the library's angle tables for this encoding and shape on the
+ * current device (otherwise built on first use, which synchronizes). */
+int atn_prepare_pe_ex(const atn_pe_desc *pe, int head_d, int max_positions);
+
+/* Number of visible HIP devices (0 when none); never aborts. */
+int atn_device_count(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ATTN_MI355X_H */

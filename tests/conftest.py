@@ -1,0 +1,32 @@
+import os
+import sys
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+for sub in ("accelerated-final-project_amd", "oracle", "tests"):
+    p = os.path.join(ROOT, sub)
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs a HIP device (runs on the MI355X box)")
+
+
+@pytest.fixture(scope="session")
+def am():
+    """The product binding; fails loudly if the HIP library is not built."""
+    import attn_mi355x
+    attn_mi355x.lib()
+    return attn_mi355x
+
+
+@pytest.fixture(scope="session")
+def dev(am):
+    """Device 0 through the library's own HIP runtime (no PyTorch)."""
+    import hip_rt
+    if hip_rt.device_count() < 1:
+        pytest.fail("GPU test collected on a host without a HIP device")
+    print(f"[gpu] device: {hip_rt.device_name(0)}", flush=True)
+    return 0

@@ -1,0 +1,89 @@
+"""Shared test helpers: seeded inputs, tolerance checks, golden fixtures."""
+import json
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+GOLDEN = os.path.join(HERE, "golden")
+REF_DATA = "/root/reference/pytorch_reference_data"
+
+# fp32 bar of the north star: an element fails iff abs > 1e-4 AND rel > 1e-4
+# (the conjunction of final/attention.cu:310 with tighter tolerances).
+F32_ABS, F32_REL = 1e-4, 1e-4
+# bf16 bar: within rel 2e-2 of the fp32 oracle run on the bf16-rounded inputs.
+BF16_REL = 2e-2
+
+
+def manifest():
+    with open(os.path.join(GOLDEN, "manifest.json")) as f:
+        return json.load(f)
+
+
+def load_fixture(name):
+    """Committed golden fixture -> dict of Q, K, V, output (float32 [B,H,L,D])."""
+    m = manifest()["sets"][name]
+    fx = m["fixture"]
+    shape = tuple(fx["shape"])
+    pat = fx["file"]
+    return {t: np.fromfile(os.path.join(GOLDEN, pat.replace("<T>", t)), dtype="<f4").reshape(shape)
+            for t in ("Q", "K", "V", "output")}
+
+
+def check_f32(got, ref, abs_tol=F32_ABS, rel_tol=F32_REL):
+    """Returns (n_fail, max_abs, max_rel) with the reference's conjunction."""
+    g = np.asarray(got, dtype=np.float64).ravel()
+    r = np.asarray(ref, dtype=np.float64).ravel()
+    a = np.abs(g - r)
+    rel = a / (np.abs(r) + 1e-8)
+    fail = ((a > abs_tol) & (rel > rel_tol)) | ~np.isfinite(g)
+    return int(fail.sum()), float(a.max()), float(rel.max())
+
+
+def check_bf16(got, ref, rel_tol=BF16_REL):
+    """bf16 output vs fp32 oracle: an element fails iff its error exceeds
+    rel_tol * |ref| AND rel_tol * rms(ref); the norm-wise relative error must
+    also be <= rel_tol.  Returns (n_fail, normwise_rel, max_abs)."""
+    g = np.asarray(got, dtype=np.float64).ravel()
+    r = np.asarray(ref, dtype=np.float64).ravel()
+    a = np.abs(g - r)
+    rms = float(np.sqrt(np.mean(r * r))) if r.size else 0.0
+    fail = ((a > rel_tol * np.abs(r)) & (a > rel_tol * rms)) | ~np.isfinite(g)
+    nrel = float(np.linalg.norm(g - r) / max(np.linalg.norm(r), 1e-30))
+    return int(fail.sum()) + (0 if nrel <= rel_tol else 1), nrel, float(a.max()) if a.size else 0.0
+
+
+def rng_inputs(shape_q, shape_kv, seed, sigma=1.0):
+    """Host N(0, sigma) float32 inputs from numpy's PCG64 (seeded)."""
+    rng = np.random.default_rng(seed)
+    Q = (rng.standard_normal(shape_q, dtype=np.float32) * np.float32(sigma))
+    K = (rng.standard_normal(shape_kv, dtype=np.float32) * np.float32(sigma))
+    V = (rng.standard_normal(shape_kv, dtype=np.float32) * np.float32(sigma))
+    return Q, K, V
+
+
+def device_inputs(shape_q, shape_kv, seed, dtype="f32", sigma=1.0):
+    """Seeded N(0, sigma) inputs uploaded to the device as dtype ('f32' or
+    'bf16', RNE-rounded on the host); returns (device arrays, host float32
+    copies of exactly the values the kernel sees)."""
+    import hip_rt
+    Q, K, V = rng_inputs(shape_q, shape_kv, seed, sigma)
+    devs, host = [], []
+    for x in (Q, K, V):
+        d = hip_rt.DeviceArray.from_numpy(x, dtype)
+        devs.append(d)
+        host.append(x if dtype == "f32" else hip_rt.bf16_bits_to_f32(hip_rt.f32_to_bf16_bits(x)))
+    return devs, host
+
+
+def upload(x, dtype="f32"):
+    import hip_rt
+    return hip_rt.DeviceArray.from_numpy(np.ascontiguousarray(x), dtype)
+
+
+def empty(shape, dtype="f32"):
+    """Device array pre-filled with NaN bits, so unwritten outputs fail."""
+    import hip_rt
+    d = hip_rt.DeviceArray(shape, dtype)
+    d.fill_nan()
+    return d

@@ -1,0 +1,261 @@
+"""GPU parity: every drop-in entry point vs the CPU oracle on identical inputs.
+
+fp32: element fails iff abs > 1e-4 AND rel > 1e-4.
+bf16: within rel 2e-2 of the fp32 oracle run on the bf16-rounded inputs.
+Shapes follow the reference's own test lists (final/attention.cu:490-522,
+final/rope.cu:1911-1923, final/sinusoidal.cu's test list) plus tile-boundary,
+odd-size and misalignment edges.  Every output buffer starts as NaN, so an
+element the kernels fail to write fails the check.
+"""
+import numpy as np
+import pytest
+
+import helpers as H
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+
+def _f32_call(fn, Q, K, V):
+    import hip_rt
+    q, k, v = H.upload(Q), H.upload(K), H.upload(V)
+    out = H.empty(Q.shape)
+    fn(q, k, v, out)
+    hip_rt.synchronize()
+    return out.numpy()
+
+
+@pytest.mark.parametrize("name", ["tiny", "small", "hdim512"])
+def test_golden_fixtures(am, dev, name):
+    """BASELINE config 1 is the 'tiny' golden set exactly."""
+    fx = H.load_fixture(name)
+    print(f"[case] golden {name} shape={fx['Q'].shape}", flush=True)
+    got = _f32_call(am.attention_forward_optimized, fx["Q"], fx["K"], fx["V"])
+    n, mabs, _ = H.check_f32(got, fx["output"])
+    assert n == 0, f"{n} mismatches vs PyTorch golden, max abs {mabs}"
+    ref = oracle.attention(fx["Q"], fx["K"], fx["V"], nthreads=8)
+    n, mabs, _ = H.check_f32(got, ref)
+    assert n == 0, f"{n} mismatches vs oracle, max abs {mabs}"
+
+
+SDPA_SHAPES = [  # (B, H, Lq, Lk, D)
+    (1, 1, 4, 4, 8), (1, 2, 8, 8, 16), (2, 4, 32, 32, 32), (2, 8, 64, 64, 64),
+    (1, 2, 16, 32, 32), (1, 4, 16, 16, 64), (2, 8, 64, 64, 128),
+    (1, 4, 64, 64, 512), (1, 4, 64, 64, 2048), (1, 2, 32, 32, 4096), (1, 1, 16, 16, 8192),
+    (1, 4, 64, 64, 4096), (1, 4, 64, 64, 8192),
+    # tile edges and odd sizes
+    (1, 1, 1, 1, 8), (1, 2, 65, 63, 96), (1, 1, 3, 129, 36), (2, 3, 17, 200, 7), (1, 1, 130, 5, 33),
+]
+
+
+@pytest.mark.parametrize("shape", SDPA_SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_sdpa_f32(am, dev, shape):
+    B, Hh, Lq, Lk, D = shape
+    print(f"[case] sdpa f32 {shape}", flush=True)
+    Q, K, V = H.rng_inputs((B, Hh, Lq, D), (B, Hh, Lk, D), seed=100 + sum(shape))
+    got = _f32_call(am.attention_forward_optimized, Q, K, V)
+    ref = oracle.attention(Q, K, V, nthreads=8)
+    n, mabs, mrel = H.check_f32(got, ref)
+    assert n == 0, f"{n} mismatches, max abs {mabs}, max rel {mrel}"
+    got2 = _f32_call(am.attention_forward, Q, K, V)
+    assert np.array_equal(got, got2)
+
+
+def test_sdpa_llama_shape(am, dev):
+    B, Hh, L, D = 4, 32, 512, 128  # final/attention.cu:522
+    print("[case] sdpa f32 llama (4,32,512,128)", flush=True)
+    Q, K, V = H.rng_inputs((B, Hh, L, D), (B, Hh, L, D), seed=7)
+    got = _f32_call(am.attention_forward_optimized, Q, K, V)
+    ref = oracle.attention(Q, K, V, nthreads=16)
+    n, mabs, _ = H.check_f32(got, ref)
+    assert n == 0, f"{n} mismatches, max abs {mabs}"
+
+
+def test_sdpa_misaligned_views(am, dev):
+    """Pointers offset by one element take the scalar-load path."""
+    import hip_rt
+    B, Hh, L, D = 1, 2, 40, 64
+    print("[case] sdpa f32 misaligned", flush=True)
+    Q, K, V = H.rng_inputs((B, Hh, L, D), (B, Hh, L, D), seed=3)
+    views = []
+    for x in (Q, K, V, None):
+        base = hip_rt.DeviceArray((Q.size + 1,), "f32")
+        v = hip_rt.DeviceArray.view(base, 1, (B, Hh, L, D))
+        if x is not None:
+            v.upload(x)
+        views.append(v)
+    am.attention_forward_optimized(*views)
+    hip_rt.synchronize()
+    ref = oracle.attention(Q, K, V)
+    nf, mabs, _ = H.check_f32(views[3].numpy(), ref)
+    assert nf == 0, mabs
+
+
+BF16_SHAPES = [(1, 4, 32, 128, 8192), (1, 2, 8, 8, 16), (2, 4, 64, 64, 512), (1, 3, 33, 70, 260)]
+
+
+@pytest.mark.parametrize("shape", BF16_SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_sdpa_bf16(am, dev, shape):
+    """BASELINE config 3 is the first shape."""
+    import hip_rt
+    B, Hh, Lq, Lk, D = shape
+    print(f"[case] sdpa bf16 {shape}", flush=True)
+    (q, k, v), (Q, K, V) = H.device_inputs((B, Hh, Lq, D), (B, Hh, Lk, D), 11, "bf16")
+    out = H.empty(Q.shape, "bf16")
+    am.attention_forward_bf16(q, k, v, out)
+    hip_rt.synchronize()
+    ref = oracle.attention(Q, K, V, nthreads=16)
+    n, nrel, mabs = H.check_bf16(out.numpy(), ref)
+    assert n == 0, f"normwise rel {nrel}, max abs {mabs}"
+
+
+# ---------------------------------------------------------------- RoPE
+ROPE_SHAPES = [(1, 1, 4, 8), (1, 2, 8, 16), (2, 4, 32, 32), (1, 4, 16, 64), (1, 4, 64, 128),
+               (1, 4, 64, 512), (1, 4, 64, 2048)]  # final/rope.cu:1911-1923
+
+
+@pytest.mark.parametrize("shape", ROPE_SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_rope_fused_cache(am, dev, shape):
+    B, Hh, L, D = shape
+    print(f"[case] rope fused cache {shape}", flush=True)
+    Q, K, V = H.rng_inputs((B, Hh, L, D), (B, Hh, L, D), seed=21 + D)
+    c, s = oracle.rope_cache(L, D)
+    tc, ts = H.upload(c), H.upload(s)
+    got = _f32_call(lambda q, k, v, o: am.attention_forward_rope_fused(q, k, v, o, tc, ts), Q, K, V)
+    ref = oracle.attention_rope(Q, K, V, c, s, nthreads=8)
+    n, mabs, _ = H.check_f32(got, ref)
+    assert n == 0, f"{n} mismatches, max abs {mabs}"
+
+
+@pytest.mark.parametrize("shape,rot", [((1, 4, 64, 64, 128), 64), ((1, 4, 64, 64, 512), 128),
+                                       ((1, 4, 64, 64, 2048), 128), ((1, 2, 24, 40, 96), 96),
+                                       ((1, 2, 24, 40, 98), 50)],
+                         ids=lambda s: str(s))
+def test_rope_v7_hybrid_and_separate(am, dev, shape, rot):
+    """K pre-rotated by the pre-pass (bit-exact vs the oracle), Q rotated in
+    the attention call; and the separate pipeline (final/rope.cu:1800-1906)."""
+    import hip_rt
+    B, Hh, Lq, Lk, D = shape
+    print(f"[case] rope v7/separate {shape} rot={rot}", flush=True)
+    Q, K, V = H.rng_inputs((B, Hh, Lq, D), (B, Hh, Lk, D), seed=31 + D)
+    c, s = oracle.rope_cache(max(Lq, Lk), rot)
+    tc, ts = H.upload(c), H.upload(s)
+    q, k, v = H.upload(Q), H.upload(K), H.upload(V)
+    k_rot = H.empty(K.shape)
+    am.rope_forward(k, k_rot, tc, ts, rot, Lk)
+    hip_rt.synchronize()
+    k_rot_ref = oracle.apply_rope(K, c, s, rotary_dim=rot)
+    assert np.array_equal(k_rot.numpy(), k_rot_ref), "pre-pass not bit-exact"
+    out = H.empty(Q.shape)
+    am.attention_forward_rope_fused_v7_hybrid(q, k_rot, v, out, rot)
+    hip_rt.synchronize()
+    ref = oracle.attention_rope(Q, k_rot_ref, V, c, s, rotary_dim=rot, rotate_k=False, nthreads=8)
+    n, mabs, _ = H.check_f32(out.numpy(), ref)
+    assert n == 0, f"v7: {n} mismatches, max abs {mabs}"
+    q_rope, k_rope, out2 = H.empty(Q.shape), H.empty(K.shape), H.empty(Q.shape)
+    am.attention_forward_separate_rope(q, k, v, q_rope, k_rope, out2, tc, ts, rot)
+    hip_rt.synchronize()
+    ref2 = oracle.attention_rope(Q, K, V, c, s, rotary_dim=rot, nthreads=8)
+    n, mabs, _ = H.check_f32(out2.numpy(), ref2)
+    assert n == 0, f"separate: {n} mismatches, max abs {mabs}"
+    assert np.array_equal(q_rope.numpy(), oracle.apply_rope(Q, c, s, rotary_dim=rot))
+
+
+@pytest.mark.parametrize("shape", [(1, 2, 8, 8, 16), (1, 4, 64, 64, 512), (2, 2, 40, 72, 96),
+                                   (1, 4, 64, 64, 2048)], ids=str)
+def test_rope_bf16_full_fusion_and_v7(am, dev, shape):
+    import hip_rt
+    B, Hh, Lq, Lk, D = shape
+    print(f"[case] rope bf16 {shape}", flush=True)
+    (q, k, v), (Q, K, V) = H.device_inputs((B, Hh, Lq, D), (B, Hh, Lk, D), 41, "bf16")
+    out = H.empty(Q.shape, "bf16")
+    am.attention_forward_rope_fused_bf16(q, k, v, out)
+    hip_rt.synchronize()
+    c, s = oracle.rope_cache(max(Lq, Lk), D)
+    ref = oracle.attention_rope(Q, K, V, c, s, nthreads=16)
+    n, nrel, mabs = H.check_bf16(out.numpy(), ref)
+    assert n == 0, f"full fusion: normwise rel {nrel}, max abs {mabs}"
+    # v7 form: K pre-rotated by the caller and stored in bf16
+    rot = D // 2 if (D // 2) % 2 == 0 else D
+    cr, sr = oracle.rope_cache(max(Lq, Lk), rot)
+    k_rot = H.upload(oracle.apply_rope(K, cr, sr, rotary_dim=rot), "bf16")
+    out.fill_nan()
+    am.attention_forward_rope_bf16(q, k_rot, v, out, rot)
+    hip_rt.synchronize()
+    ref = oracle.attention_rope(Q, k_rot.numpy(), V, cr, sr, rotary_dim=rot, rotate_k=False,
+                                nthreads=16)
+    n, nrel, mabs = H.check_bf16(out.numpy(), ref)
+    assert n == 0, f"v7: normwise rel {nrel}, max abs {mabs}"
+
+
+@pytest.mark.parametrize("shape", [(1, 2, 16, 16, 64), (1, 2, 64, 96, 512), (2, 2, 33, 65, 256)],
+                         ids=str)
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_rope_half_ex(am, dev, shape, dtype):
+    import hip_rt
+    B, Hh, Lq, Lk, D = shape
+    print(f"[case] rope half ex {shape} {dtype}", flush=True)
+    (q, k, v), (Q, K, V) = H.device_inputs((B, Hh, Lq, D), (B, Hh, Lk, D), 51, dtype)
+    out = H.empty(Q.shape, dtype)
+    am.attention_ex(q, k, v, out, pe=am.make_pe("rope", pairing="half"))
+    hip_rt.synchronize()
+    c, s = oracle.rope_cache(max(Lq, Lk), D)
+    ref = oracle.attention_rope(Q, K, V, c, s, pairing="half", nthreads=16)
+    if dtype == "f32":
+        n, mabs, _ = H.check_f32(out.numpy(), ref)
+        assert n == 0, f"{n} mismatches, max abs {mabs}"
+    else:
+        n, nrel, mabs = H.check_bf16(out.numpy(), ref)
+        assert n == 0, f"normwise rel {nrel}"
+
+
+# ---------------------------------------------------------------- sinusoidal
+SIN_SHAPES = [(1, 1, 4, 4, 8), (1, 2, 8, 8, 16), (2, 4, 32, 32, 32), (1, 4, 64, 64, 512),
+              (1, 4, 64, 64, 2048), (1, 2, 32, 32, 4096), (1, 2, 20, 50, 100), (1, 1, 9, 13, 7)]
+
+
+@pytest.mark.parametrize("shape", SIN_SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_sinusoidal_f32(am, dev, shape):
+    import hip_rt
+    B, Hh, Lq, Lk, D = shape
+    print(f"[case] sinusoidal f32 {shape}", flush=True)
+    Q, K, V = H.rng_inputs((B, Hh, Lq, D), (B, Hh, Lk, D), seed=61 + D)
+    st, ct = oracle.sinusoidal_table(max(Lq, Lk), D)
+    ref = oracle.attention_sinusoidal(Q, K, V, st, ct, nthreads=8)
+    got = _f32_call(am.attention_forward_sinusoidal_fused, Q, K, V)
+    n, mabs, _ = H.check_f32(got, ref)
+    assert n == 0, f"fused: {n} mismatches, max abs {mabs}"
+    tst, tct = H.upload(st), H.upload(ct)
+    q, k, v = H.upload(Q), H.upload(K), H.upload(V)
+    k_emb, q_emb, out = H.empty(K.shape), H.empty(Q.shape), H.empty(Q.shape)
+    am.attention_forward_sinusoidal_hybrid(q, k, v, tst, tct, k_emb, out)
+    hip_rt.synchronize()
+    n, mabs, _ = H.check_f32(out.numpy(), ref)
+    assert n == 0, f"hybrid: {n} mismatches, max abs {mabs}"
+    assert np.array_equal(k_emb.numpy(), oracle.add_sinusoidal(K, st, ct))
+    out.fill_nan()
+    am.attention_forward_sinusoidal_separate(q, k, v, tst, tct, q_emb, k_emb, out)
+    hip_rt.synchronize()
+    n, mabs, _ = H.check_f32(out.numpy(), ref)
+    assert n == 0, f"separate: {n} mismatches, max abs {mabs}"
+    assert np.array_equal(q_emb.numpy(), oracle.add_sinusoidal(Q, st, ct))
+    pe_out = H.empty(Q.shape)
+    am.apply_sinusoidal_embeddings(q, tst, tct, pe_out, Lq)
+    hip_rt.synchronize()
+    assert np.array_equal(pe_out.numpy(), oracle.add_sinusoidal(Q, st, ct))
+
+
+@pytest.mark.parametrize("shape", [(1, 2, 8, 8, 16), (1, 4, 64, 64, 512), (1, 2, 48, 200, 1024)],
+                         ids=str)
+def test_sinusoidal_bf16(am, dev, shape):
+    import hip_rt
+    B, Hh, Lq, Lk, D = shape
+    print(f"[case] sinusoidal bf16 {shape}", flush=True)
+    (q, k, v), (Q, K, V) = H.device_inputs((B, Hh, Lq, D), (B, Hh, Lk, D), 71, "bf16", sigma=0.5)
+    out = H.empty(Q.shape, "bf16")
+    am.attention_forward_sinusoidal_bf16(q, k, v, out)
+    hip_rt.synchronize()
+    st, ct = oracle.sinusoidal_table(max(Lq, Lk), D)
+    ref = oracle.attention_sinusoidal(Q, K, V, st, ct, nthreads=16)
+    n, nrel, mabs = H.check_bf16(out.numpy(), ref)
+    assert n == 0, f"normwise rel {nrel}, max abs {mabs}"
