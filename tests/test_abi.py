@@ -1,0 +1,182 @@
+"""C-ABI boundary tests that need no GPU.
+
+* libattn_mi355x.so loads and exports every function include/attn_mi355x.h
+  declares;
+* every argument error of the _ex entry points is reported with its status
+  code before any HIP call (fake, never dereferenced device addresses are
+  passed: validation rejects them first);
+* on a host without a HIP device a valid call reports ATN_ERR_NO_DEVICE;
+* the drop-in entry points keep the reference's error convention (print,
+  then exit(EXIT_FAILURE); final/attention.cu:12-21) -- checked in a child
+  process;
+* the host-side table builders (precompute_rope_cache,
+  precompute_sinusoidal_table) give the oracle's bits.
+"""
+import ctypes
+import os
+import subprocess
+import sys
+
+import numpy as np
+import pytest
+
+import oracle
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+# Fake device addresses: 256-byte aligned, far apart, never dereferenced
+# (every call below is rejected by validation before any HIP call).
+QA, KA, VA, OA, WA = (0x7F0000000000 + i * 0x100000000 for i in range(5))
+
+
+@pytest.fixture(scope="module")
+def L(am):
+    return am.lib()
+
+
+def test_exports_every_header_function(am, L):
+    names = am.header_functions()
+    assert "attention_forward_optimized" in names and len(names) >= 20
+    for n in names:
+        assert hasattr(L, n), f"{n} declared in include/attn_mi355x.h but not exported"
+
+
+def test_reference_dropin_names_present(am):
+    """The drop-in names of the reference's host launchers."""
+    names = set(am.header_functions())
+    for n in ["attention_forward_optimized", "attention_forward", "attention_forward_rope_fused",
+              "attention_forward_rope_fused_v7_hybrid", "attention_forward_separate_rope",
+              "attention_forward_sinusoidal_hybrid", "attention_forward_sinusoidal_separate",
+              "attention_forward_bf16", "attention_forward_rope_bf16",
+              "attention_forward_sinusoidal_bf16", "precompute_rope_cache"]:
+        assert n in names
+
+
+def test_status_strings(am, L):
+    for code in range(0, -11, -1):
+        s = am.status_string(code)
+        assert s and s != "unknown status"
+    assert am.status_string(-99) == "unknown status"
+
+
+def fwd(am, L, dtype=0, q=QA, k=KA, v=VA, o=OA, B=1, H=4, Lq=64, Lk=64, D=2048, pe=None,
+        ws=None, wsb=0):
+    return L.atn_attention_fwd_ex(dtype, q, k, v, o, B, H, Lq, Lk, D,
+                                  ctypes.byref(pe) if pe is not None else None, ws, wsb, None)
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(dtype=7), -9),
+    (dict(q=None), -1), (dict(k=None), -1), (dict(v=None), -1), (dict(o=None), -1),
+    (dict(B=0), -2), (dict(H=-1), -2), (dict(Lq=0), -2), (dict(Lk=0), -2), (dict(D=0), -2),
+    (dict(B=1 << 20, H=1 << 20, Lq=1 << 20, D=1 << 20), -4),
+    (dict(Lq=1 << 20, D=1 << 12), -4),  # one head's Lq*D beyond 32-bit row indexing
+    (dict(q=QA + 2), -10), (dict(o=OA + 1), -10),
+    (dict(dtype=1, v=VA + 1), -10),
+    (dict(o=QA + 64), -5),  # out overlaps Q
+    (dict(o=VA), -5),
+    (dict(ws=WA, wsb=16), -8),
+])
+def test_fwd_ex_validation(am, L, kw, code):
+    assert fwd(am, L, **kw) == code
+
+
+@pytest.mark.parametrize("pe_kw,code", [
+    (dict(kind="rope", rotary_dim=7), -3),
+    (dict(kind="rope", rotary_dim=4096), -3),
+    (dict(kind="rope", rotary_dim=-2), -3),
+])
+def test_fwd_ex_rope_validation(am, L, pe_kw, code):
+    pe = am.make_pe(**pe_kw)
+    assert fwd(am, L, pe=pe) == code
+
+
+def test_fwd_ex_pe_descriptor_errors(am, L):
+    pe = am.make_pe("rope")
+    pe.pairing = 5
+    assert fwd(am, L, pe=pe) == -9
+    pe = am.make_pe("rope")
+    pe.table_a = 0x1000
+    assert fwd(am, L, pe=pe) == -1  # one table without the other
+    pe = am.make_pe("sinusoidal")
+    pe.kind = 9
+    assert fwd(am, L, pe=pe) == -9
+    pe = am.make_pe("rope")
+    pe.base = -1.0
+    assert fwd(am, L, pe=pe) == -9
+    pe = am.make_pe("rope", rotary_dim=0)
+    assert fwd(am, L, pe=pe, D=9) == -3  # rotary = head_d must be even
+
+
+def test_pe_apply_ex_validation(am, L):
+    pe = am.make_pe("rope")
+    f = L.atn_pe_apply_ex
+    assert f(0, None, OA, 10, 10, 64, ctypes.byref(pe), None) == -1
+    assert f(0, QA, OA, 0, 10, 64, ctypes.byref(pe), None) == -2
+    assert f(0, QA, OA, 10, 0, 64, ctypes.byref(pe), None) == -2
+    assert f(0, QA, QA + 8, 10, 10, 64, ctypes.byref(pe), None) == -5
+    assert f(3, QA, OA, 10, 10, 64, ctypes.byref(pe), None) == -9
+    assert f(0, QA, OA, 10, 10, 64, None, None) == -1
+    none = am.PeDesc()
+    assert f(0, QA, OA, 10, 10, 64, ctypes.byref(none), None) == -9  # kind NONE
+
+
+def test_workspace_bytes(am):
+    n = am.workspace_bytes(0, 1, 4, 64, 64, 2048)
+    assert n > 0 and n % 4 == 0
+    assert am.workspace_bytes(0, 0, 4, 64, 64, 2048) == 0
+    assert am.workspace_bytes(9, 1, 4, 64, 64, 2048) == 0
+    assert am.workspace_bytes(0, 1, 4, 64, 64, 2048, am.make_pe("rope", rotary_dim=3)) == 0
+
+
+def test_no_device_path(am, L):
+    if am.device_count() > 0:
+        pytest.skip("a HIP device is visible; the no-device path is exercised on the CPU host")
+    assert fwd(am, L) == -6
+    assert L.atn_prepare_pe_ex(ctypes.byref(am.make_pe("rope")), 64, 64) == -6
+
+
+def _child(code: str):
+    env = dict(os.environ)
+    env["PYTHONPATH"] = os.pathsep.join(
+        [os.path.join(ROOT, "accelerated-final-project_amd"), env.get("PYTHONPATH", "")])
+    return subprocess.run([sys.executable, "-c", code], capture_output=True, text=True,
+                          timeout=120, env=env)
+
+
+def test_dropin_exits_on_bad_argument():
+    """Reference convention: print the error and exit(EXIT_FAILURE)."""
+    r = _child("import attn_mi355x as a; a.lib().attention_forward_optimized("
+               f"{QA}, {KA}, {VA}, {OA}, 0, 4, 64, 64, 2048)")
+    assert r.returncode == 1
+    assert "attn_mi355x error -2" in r.stderr and "attention_forward_optimized" in r.stderr
+
+
+def test_dropin_exits_on_aliasing():
+    r = _child("import attn_mi355x as a; a.lib().attention_forward_bf16("
+               f"{QA}, {KA}, {VA}, {QA}, 1, 4, 64, 64, 2048)")
+    assert r.returncode == 1 and "attn_mi355x error -5" in r.stderr
+
+
+def test_host_rope_cache_matches_oracle(am):
+    for npos, r in [(16, 8), (1024, 128), (64, 2048)]:
+        c, s = am.precompute_rope_cache(npos, r)
+        oc, os_ = oracle.rope_cache(npos, r)
+        assert np.array_equal(c, oc) and np.array_equal(s, os_)
+
+
+def test_host_sinusoidal_table_matches_oracle(am):
+    for npos, d in [(16, 8), (2048, 1024), (33, 7)]:
+        s, c = am.precompute_sinusoidal_table(npos, d)
+        os_, oc = oracle.sinusoidal_table(npos, d)
+        assert np.array_equal(s, os_) and np.array_equal(c, oc)
+
+
+def test_python_binding_checks_shapes(am):
+    import hip_rt
+
+    class Fake:
+        pass
+    with pytest.raises(ValueError):
+        am._check(Fake(), "f32", (1,), "Q")
+    assert hip_rt.bf16_bits_to_f32(hip_rt.f32_to_bf16_bits(np.float32([1.5])))[0] == 1.5
