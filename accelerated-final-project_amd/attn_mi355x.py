@@ -37,6 +37,7 @@ ATN_ERR_HIP = -7
 ATN_ERR_WORKSPACE = -8
 ATN_ERR_BAD_ARGUMENT = -9
 ATN_ERR_MISALIGNED = -10
+ATN_ERR_DEVICE_TIMEOUT = -11
 
 ATN_DTYPE_F32 = 0
 ATN_DTYPE_BF16 = 1
@@ -45,6 +46,8 @@ ATN_PE_ROPE = 1
 ATN_PE_SINUSOIDAL = 2
 ATN_ROPE_INTERLEAVED = 0
 ATN_ROPE_HALF = 1
+ATN_PATH_FUSED_SMALL = 1
+ATN_PATH_SPLIT_D = 2
 
 
 class PeDesc(ctypes.Structure):
@@ -91,6 +94,8 @@ _SIGS = {
                                       ctypes.c_size_t),
     "atn_pe_apply_ex": ([_i, _vp, _vp, ctypes.c_long, _i, _i, ctypes.POINTER(PeDesc), _vp], _i),
     "atn_prepare_pe_ex": ([ctypes.POINTER(PeDesc), _i, _i], _i),
+    "atn_sync_status_ex": ([_vp, _i, _i, _vp], _i),
+    "atn_attention_path_ex": ([_i] * 6 + [ctypes.POINTER(PeDesc)], _i),
     "attention_forward_optimized": ([_vp] * 4 + [_i] * 5, None),
     "attention_forward": ([_vp] * 4 + [_i] * 5, None),
     "attention_forward_rope_fused": ([_vp] * 6 + [_i] * 5, None),
@@ -210,6 +215,18 @@ def attention_ex(Q, K, V, out=None, pe: PeDesc | None = None, workspace=None, st
     if st != ATN_OK:
         raise AtnError(st, "atn_attention_fwd_ex")
     return out
+
+
+def path(dtype_code: int, B, H, Lq, Lk, D, pe: PeDesc | None = None) -> int:
+    """ATN_PATH_* that atn_attention_fwd_ex takes for this shape."""
+    return lib().atn_attention_path_ex(dtype_code, B, H, Lq, Lk, D,
+                                       ctypes.byref(pe) if pe is not None else None)
+
+
+def sync_status(workspace=None, B: int = 1, H: int = 1, stream=None) -> int:
+    """atn_sync_status_ex: ATN_OK or ATN_ERR_DEVICE_TIMEOUT."""
+    return lib().atn_sync_status_ex(None if workspace is None else workspace.ptr, B, H,
+                                    _stream_handle(stream))
 
 
 def workspace_bytes(dtype_code: int, B, H, Lq, Lk, D, pe: PeDesc | None = None) -> int:

@@ -11,6 +11,9 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <ctime>
+#include <unistd.h>
+#include <algorithm>
 #include <map>
 #include <mutex>
 #include <tuple>
@@ -116,10 +119,20 @@ struct Table {
     int nfreq = 0;
 };
 
+// Library-managed scratch, one per (device, stream) so that calls on
+// different streams never share partial results or barrier counters.  It is
+// zero-filled when allocated; every call leaves its synchronization words at
+// zero again.
+struct Workspace {
+    void* ptr = nullptr;
+    size_t bytes = 0;
+};
+
 struct DeviceState {
-    void* ws = nullptr;
-    size_t ws_bytes = 0;
+    std::map<hipStream_t, Workspace> ws;
     std::map<std::tuple<int, int, uint32_t>, Table> tables;  // (kind, dim, base bits)
+    int cus = 0;
+    std::map<std::pair<int, int>, int> fused_cap;  // (dtype, LDS bytes) -> resident workgroups
 };
 
 std::mutex g_mu;
@@ -260,23 +273,101 @@ StreamPlan stream_plan(const Shape& s) {
     return p;
 }
 
-int ensure_workspace(size_t bytes, void** ws) {
+int ensure_workspace(size_t bytes, hipStream_t stream, void** ws) {
     int dev;
     int st = current_device(&dev);
     if (st != ATN_OK) return st;
     std::lock_guard<std::mutex> lk(g_mu);
-    DeviceState& ds = g_dev[dev];
-    if (ds.ws_bytes < bytes) {
-        if (ds.ws) {
-            ATN_HIP(hipFree(ds.ws));  // waits for in-flight work using it
-            ds.ws = nullptr;
-            ds.ws_bytes = 0;
+    Workspace& w = g_dev[dev].ws[stream];
+    if (w.bytes < bytes) {
+        if (w.ptr) {
+            ATN_HIP(hipFree(w.ptr));  // waits for in-flight work using it
+            w.ptr = nullptr;
+            w.bytes = 0;
         }
-        ATN_HIP(hipMalloc(&ds.ws, bytes));
-        ds.ws_bytes = bytes;
+        ATN_HIP(hipMalloc(&w.ptr, bytes));
+        ATN_HIP(hipMemset(w.ptr, 0, bytes));
+        w.bytes = bytes;
     }
-    *ws = ds.ws;
+    *ws = w.ptr;
     return ATN_OK;
+}
+
+// ---------------------------------------------------------------- fused plan
+// Workspace layout (every path): a fixed 32 KiB sync region -- [0, 4) the
+// status word, [256, 8448) one epoch word per head, [8448, 24832) one 64-bit
+// barrier flag per workgroup of the single-launch kernel -- then float
+// scratch.  Fixed offsets keep the barrier words of one call from landing
+// on another call's words when shapes change between calls.
+constexpr size_t kSyncEpochOff = 256;
+constexpr size_t kSyncFlagOff = 8448;
+constexpr int kSyncMaxWorkgroups = 2048;
+constexpr size_t kSyncBytes = 32768;
+
+size_t round256(size_t b) { return (b + 255) / 256 * 256; }
+
+struct FusedPlan {
+    bool ok = false;
+    int dc = 0, nchunk = 0, lds = 0;
+    size_t part_elems = 0, red_elems = 0, bytes = 0;
+};
+
+constexpr int kFusedMaxLq = 64, kFusedMaxLk = 128;
+constexpr int kLdsLimit = 160 * 1024 - 256;
+
+// Cut each head's D into slices so that about one workgroup per CU runs and
+// the whole grid is resident at once (the kernel's barriers need that).
+// Capacity is the device's CU count x resident workgroups per CU for the
+// chosen LDS size.
+FusedPlan fused_plan(int dtype, int pek, const Shape& s, bool query_device) {
+    FusedPlan p;
+    if (s.Lq > kFusedMaxLq || s.Lk > kFusedMaxLk || s.D % 4 != 0) return p;
+    int cus = 256;
+    int dev = 0;
+    if (query_device) {
+        if (hipGetDevice(&dev) != hipSuccess) return p;
+        std::lock_guard<std::mutex> lk(g_mu);
+        DeviceState& ds = g_dev[dev];
+        if (ds.cus == 0 &&
+            hipDeviceGetAttribute(&ds.cus, hipDeviceAttributeMultiprocessorCount, dev) !=
+                hipSuccess)
+            return p;
+        cus = ds.cus;
+    }
+    auto capacity = [&](int lds) {
+        std::lock_guard<std::mutex> lk(g_mu);
+        int& c = g_dev[dev].fused_cap[std::make_pair(dtype, lds)];
+        if (c == 0) c = atn::fused_small_capacity(dtype, pek, lds);
+        return c;
+    };
+    if (s.BH > cus) return p;
+    const int64_t per_head = cus / s.BH;
+    int64_t dc = (s.D + per_head - 1) / per_head;
+    dc = (dc + 31) / 32 * 32;
+    for (;; dc += 32) {
+        if (dc > 1024) return p;  // one 4-element column group per thread at most
+        const int lds = atn::fused_small_lds_bytes(dtype, pek, s.Lq, s.Lk, (int)dc);
+        if (lds > kLdsLimit) return p;
+        const int64_t n = (s.D + dc - 1) / dc;
+        int cap = (int)cus;  // one workgroup per CU is always resident
+        if (query_device && n > 1) {
+            cap = capacity(lds);
+            if (cap <= 0) return p;
+        }
+        if (s.BH * n > kSyncMaxWorkgroups) return p;
+        if (n == 1 || s.BH * n <= cap) {
+            p.ok = true;
+            p.dc = (int)dc;
+            p.nchunk = (int)n;
+            p.lds = lds;
+            break;
+        }
+    }
+    const size_t E = (size_t)((s.Lq + 15) / 16 * 16) * ((s.Lk + 31) / 32 * 32);
+    p.part_elems = p.nchunk > 1 ? (size_t)s.BH * p.nchunk * E : 0;
+    p.red_elems = p.nchunk > 1 ? (size_t)s.BH * E : 0;
+    p.bytes = kSyncBytes + (p.part_elems + p.red_elems) * 4;
+    return p;
 }
 
 // ---------------------------------------------------------------- core
@@ -297,8 +388,11 @@ int attention_core(int dtype, const void* Q, const void* K, const void* V, void*
     PePlan plan;
     st = check_pe(pe, D, &plan);
     if (st != ATN_OK) return st;
+    const FusedPlan fp = fused_plan(dtype, plan.pek, s, false);
     const StreamPlan sp = stream_plan(s);
-    if (workspace != nullptr && workspace_bytes < sp.bytes) return ATN_ERR_WORKSPACE;
+    const size_t need_upper =
+        std::max(fp.ok ? fp.bytes : (size_t)0, kSyncBytes + sp.bytes);
+    if (workspace != nullptr && workspace_bytes < need_upper) return ATN_ERR_WORKSPACE;
     const int64_t tiles = s.BH * ((Lq + 63) / 64) * ((Lk + 63) / 64) * sp.nsplit;
     const int64_t pv_tiles = s.BH * ((Lq + 63) / 64) * ((D + 63) / 64);
     if (tiles > (1LL << 24) || pv_tiles > (1LL << 24)) return ATN_ERR_SIZE_OVERFLOW;
@@ -308,19 +402,36 @@ int attention_core(int dtype, const void* Q, const void* K, const void* V, void*
     if (st != ATN_OK) return st;
     st = bind_tables(pe, plan, D, Lq > Lk ? Lq : Lk);
     if (st != ATN_OK) return st;
+    // the device's own capacity decides between the single-launch kernel
+    // and the three-kernel pipeline
+    const FusedPlan fd = fused_plan(dtype, plan.pek, s, true);
+    const size_t need = fd.ok ? fd.bytes : kSyncBytes + sp.bytes;
     void* ws = workspace;
     if (ws == nullptr) {
-        st = ensure_workspace(sp.bytes, &ws);
+        st = ensure_workspace(need_upper > need ? need_upper : need, stream, &ws);
         if (st != ATN_OK) return st;
+    } else if (workspace_bytes < need) {
+        return ATN_ERR_WORKSPACE;
     }
-    float* S = reinterpret_cast<float*>(((uintptr_t)ws + 255) & ~(uintptr_t)255);
-    float* P = sp.nsplit > 1 ? S + sp.s_elems : S;
+    int* status = reinterpret_cast<int*>(ws);
 
     const size_t va = dtype == ATN_DTYPE_F32 ? 16 : 8;
     const int vec_qk = (D % 4 == 0) && aligned(Q, va) && aligned(K, va);
     const int vec_vo = (D % 4 == 0) && aligned(V, va) && aligned(out, va);
     const float scale = 1.0f / sqrtf((float)D);  // final/attention.cu:206
 
+    float* scratch = reinterpret_cast<float*>((char*)ws + kSyncBytes);
+    if (fd.ok && vec_qk && vec_vo) {
+        unsigned* epochs = reinterpret_cast<unsigned*>((char*)ws + kSyncEpochOff);
+        auto* flags = reinterpret_cast<unsigned long long*>((char*)ws + kSyncFlagOff);
+        ATN_HIP(atn::launch_fused_small(dtype, plan.pek, Q, K, V, out, scratch,
+                                        scratch + fd.part_elems, epochs, flags, status,
+                                        (int)s.BH, Lq, Lk, D, fd.dc, fd.nchunk, scale, plan.q,
+                                        plan.k, vec_qk && vec_vo, stream));
+        return ATN_OK;
+    }
+    float* S = scratch;
+    float* P = sp.nsplit > 1 ? S + sp.s_elems : S;
     ATN_HIP(atn::launch_qk_partial(dtype, plan.pek, Q, K, S, (int)s.BH, Lq, Lk, D, sp.dchunk,
                                    sp.nsplit, plan.q, plan.k, vec_qk, stream));
     ATN_HIP(atn::launch_softmax(S, P, s.BH * Lq, Lk, sp.nsplit, (size_t)s.BH * Lq * Lk, scale,
@@ -369,6 +480,28 @@ int pe_apply_core(int dtype, const void* in, void* out, long n_rows, int seq_len
     std::exit(EXIT_FAILURE);
 }
 
+// After the stream has drained: reads the status word of a workspace (the
+// library's own for `stream` when ws == NULL).  A barrier timeout is
+// reported once and the whole sync region is cleared (status, epochs and
+// flags back to zero), which re-enables the single-launch kernel.
+int workspace_status(void* ws, hipStream_t stream) {
+    if (ws == nullptr) {
+        int dev;
+        int st = current_device(&dev);
+        if (st != ATN_OK) return st;
+        std::lock_guard<std::mutex> lk(g_mu);
+        auto& m = g_dev[dev].ws;
+        auto it = m.find(stream);
+        if (it == m.end() || it->second.ptr == nullptr) return ATN_OK;
+        ws = it->second.ptr;
+    }
+    int word = 0;
+    ATN_HIP(hipMemcpy(&word, ws, sizeof(int), hipMemcpyDeviceToHost));
+    if (word == 0) return ATN_OK;
+    ATN_HIP(hipMemset(ws, 0, kSyncBytes));
+    return ATN_ERR_DEVICE_TIMEOUT;
+}
+
 void sync_or_die(int status, const char* where) {
     if (status != ATN_OK) die(status, where);
     hipError_t e = hipGetLastError();
@@ -377,6 +510,8 @@ void sync_or_die(int status, const char* where) {
         g_last_hip_error = (int)e;
         die(ATN_ERR_HIP, where);
     }
+    const int ws = workspace_status(nullptr, nullptr);
+    if (ws != ATN_OK) die(ws, where);
 }
 
 atn_pe_desc rope_desc(int rotary, int pairing, bool q, bool k, const float* c, const float* s) {
@@ -420,6 +555,7 @@ const char* atn_status_string(int status) {
         case ATN_ERR_WORKSPACE: return "workspace too small";
         case ATN_ERR_BAD_ARGUMENT: return "bad argument";
         case ATN_ERR_MISALIGNED: return "pointer not aligned to its element size";
+        case ATN_ERR_DEVICE_TIMEOUT: return "device-side wait timed out (outputs are NaN)";
         default: return "unknown status";
     }
 }
@@ -447,12 +583,38 @@ size_t atn_attention_workspace_bytes(int dtype, int batch, int heads, int len_q,
     if (check_shape(batch, heads, len_q, len_k, head_d, &s) != ATN_OK) return 0;
     PePlan plan;
     if (check_pe(pe, head_d, &plan) != ATN_OK) return 0;
-    return stream_plan(s).bytes;
+    const FusedPlan fp = fused_plan(dtype, plan.pek, s, false);
+    return std::max(fp.ok ? fp.bytes : (size_t)0, kSyncBytes + stream_plan(s).bytes);
 }
 
 int atn_pe_apply_ex(int dtype, const void* in, void* out, long n_rows, int seq_len, int head_d,
                     const atn_pe_desc* pe, void* stream) {
     return pe_apply_core(dtype, in, out, n_rows, seq_len, head_d, pe, (hipStream_t)stream);
+}
+
+int atn_attention_path_ex(int dtype, int batch, int heads, int len_q, int len_k, int head_d,
+                          const atn_pe_desc* pe) {
+    if (dtype != ATN_DTYPE_F32 && dtype != ATN_DTYPE_BF16) return ATN_ERR_BAD_ARGUMENT;
+    Shape s;
+    int st = check_shape(batch, heads, len_q, len_k, head_d, &s);
+    if (st != ATN_OK) return st;
+    PePlan plan;
+    st = check_pe(pe, head_d, &plan);
+    if (st != ATN_OK) return st;
+    int n = 0;
+    const bool dev = hipGetDeviceCount(&n) == hipSuccess && n > 0;
+    return fused_plan(dtype, plan.pek, s, dev).ok ? ATN_PATH_FUSED_SMALL : ATN_PATH_SPLIT_D;
+}
+
+int atn_sync_status_ex(void* workspace, int batch, int heads, void* stream) {
+    hipStream_t st = (hipStream_t)stream;
+    int dev;
+    int s = current_device(&dev);
+    if (s != ATN_OK) return s;
+    (void)batch;
+    (void)heads;
+    ATN_HIP(hipStreamSynchronize(st));
+    return workspace_status(workspace, st);
 }
 
 int atn_prepare_pe_ex(const atn_pe_desc* pe, int head_d, int max_positions) {

@@ -21,6 +21,14 @@ hipError_t launch_softmax(const float* S, float* P, long rows, int Lk, int nspli
                           size_t split_stride, float scale, hipStream_t st);
 hipError_t launch_pv(int dtype, const float* P, const void* V, void* O, int BH, int Lq, int Lk,
                      int D, int vec_ok, hipStream_t st);
+// Single-launch split-D kernel for len_q <= 64, len_k <= 128 (fused_small.hip).
+int fused_small_lds_bytes(int dtype, int pek, int Lq, int Lk, int dc);
+int fused_small_capacity(int dtype, int pek, int lds);
+hipError_t launch_fused_small(int dtype, int pek, const void* Q, const void* K, const void* V,
+                              void* O, float* part, float* red, unsigned* epochs,
+                              unsigned long long* flags, int* status, int BH, int Lq, int Lk,
+                              int D, int dc, int nchunk, float scale, const PeSide& pq,
+                              const PeSide& pk, int vec_ok, hipStream_t st);
 hipError_t launch_pe_apply(int dtype, int pek, const void* in, void* out, long n_rows,
                            int seq_len, int D, const PeSide& pe, int vec_ok, hipStream_t st);
 

@@ -52,6 +52,12 @@ def hip():
         H.hipEventSynchronize.argtypes = [_vp]
         H.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), _vp, _vp]
         H.hipGetLastError.argtypes = []
+        H.hipStreamBeginCapture.argtypes = [_vp, ctypes.c_int]
+        H.hipStreamEndCapture.argtypes = [_vp, ctypes.POINTER(_vp)]
+        H.hipGraphInstantiate.argtypes = [ctypes.POINTER(_vp), _vp, _vp, _vp, ctypes.c_size_t]
+        H.hipGraphLaunch.argtypes = [_vp, _vp]
+        H.hipGraphExecDestroy.argtypes = [_vp]
+        H.hipGraphDestroy.argtypes = [_vp]
     return _hip
 
 
@@ -213,3 +219,35 @@ class Event:
         if self.handle:
             hip().hipEventDestroy(_vp(self.handle))
             self.handle = None
+
+
+class Graph:
+    """A HIP graph captured from the work `fn()` enqueues on `stream`
+    (relaxed capture mode), instantiated for replay with launch()."""
+
+    def __init__(self, stream: Stream, fn):
+        H = hip()
+        check(H.hipStreamBeginCapture(_vp(stream.handle), 2), "hipStreamBeginCapture")
+        try:
+            fn()
+        finally:
+            g = _vp()
+            err = H.hipStreamEndCapture(_vp(stream.handle), ctypes.byref(g))
+        check(err, "hipStreamEndCapture")
+        self.graph = g.value
+        e = _vp()
+        check(H.hipGraphInstantiate(ctypes.byref(e), _vp(self.graph), None, None, 0),
+              "hipGraphInstantiate")
+        self.exec = e.value
+        self.stream = stream
+
+    def launch(self) -> None:
+        check(hip().hipGraphLaunch(_vp(self.exec), _vp(self.stream.handle)), "hipGraphLaunch")
+
+    def destroy(self) -> None:
+        if self.exec:
+            hip().hipGraphExecDestroy(_vp(self.exec))
+            self.exec = None
+        if self.graph:
+            hip().hipGraphDestroy(_vp(self.graph))
+            self.graph = None

@@ -154,8 +154,9 @@ def main():
     out = hip_rt.DeviceArray((B, H, Lq, D), dtype)
     desc = pe_desc(am, pe)
     dcode = am.ATN_DTYPE_F32 if dtype == "f32" else am.ATN_DTYPE_BF16
+    # a caller workspace is zero-filled once before its first use
     ws = hip_rt.DeviceArray((max(am.workspace_bytes(dcode, B, H, Lq, Lk, D, desc), 4) // 4,),
-                            "f32")
+                            "f32", fill=0)
     stream = hip_rt.Stream()
     if desc is not None:
         st = am.lib().atn_prepare_pe_ex(desc, D, max(Lq, Lk))
@@ -169,16 +170,34 @@ def main():
         step()
     hip_rt.synchronize()
 
+    # eager: one Python-driven call per step (host-bound for small shapes)
     e0, e1 = hip_rt.Event(), hip_rt.Event()
-    t0 = time.perf_counter()
     e0.record(stream)
     for _ in range(a.steps):
         step()
     e1.record(stream)
     e1.synchronize()
+    eager_ms = e0.elapsed_ms(e1) / a.steps
+
+    # timed region: the K steps captured once as a HIP graph and replayed,
+    # so the GPU runs them back to back with no host work in between
+    graph = hip_rt.Graph(stream, lambda: [step() for _ in range(a.steps)])
+    graph.launch()  # warm replay
+    stream.synchronize()
+    hip_rt.synchronize()
+    t0 = time.perf_counter()
+    e0.record(stream)
+    graph.launch()
+    e1.record(stream)
+    e1.synchronize()
     hip_rt.synchronize()
     wall = time.perf_counter() - t0
     ev_ms = e0.elapsed_ms(e1)
+    graph.destroy()
+    st = am.lib().atn_sync_status_ex(ws.ptr, B, H, stream.handle)
+    if st != 0:
+        raise am.AtnError(st, "device status after the timed region")
+    path = am.path(dcode, B, H, Lq, Lk, D, desc)
 
     es = 4 if dtype == "f32" else 2
     alg_bytes = (2 * B * H * Lq * D + 2 * B * H * Lk * D) * es
@@ -210,7 +229,9 @@ def main():
         peak = BF16_PEAK_TFLOPS if dtype == "bf16" else FP32_PEAK_TFLOPS
         roof = {"bound": "mfma", "achieved": round(tflops, 2), "peak": peak, "unit": "TFLOP/s",
                 "frac": round(tflops / peak, 4), "traffic": None}
-    roof["kernel"] = "attention pipeline (atn_attention_fwd_ex, all launches of one call)"
+    roof["kernel"] = ("k_fused_small (one launch per step)" if path == am.ATN_PATH_FUSED_SMALL
+                      else "split-D pipeline (k_qk_partial + k_softmax + k_pv per step)")
+    roof["timing"] = "HIP events around one graph replay of all timed steps, on its stream"
 
     cpu = None
     if a.cpu_seconds > 0:
@@ -226,6 +247,7 @@ def main():
         "steps": a.steps,
         "warmup": a.warmup,
         "ms_per_step": round(ms, 6),
+        "ms_per_step_eager_python": round(eager_ms, 6),
         "tflops": round(tflops, 4),
         "pct_hbm_roofline": round(100 * gbs / HBM_PEAK_GBS, 2),
         "wall_s": round(wall, 4),

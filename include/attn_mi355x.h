@@ -49,6 +49,7 @@ typedef uint16_t atn_bf16;
 #define ATN_ERR_WORKSPACE (-8)      /* caller workspace too small */
 #define ATN_ERR_BAD_ARGUMENT (-9)   /* enum out of range, bad table size ... */
 #define ATN_ERR_MISALIGNED (-10)    /* pointer not aligned to its element size */
+#define ATN_ERR_DEVICE_TIMEOUT (-11) /* a kernel's bounded cross-workgroup wait expired */
 
 /* Text for a status code (static storage). */
 const char *atn_status_string(int status);
@@ -201,9 +202,19 @@ void precompute_sinusoidal_table(float *sin_table, float *cos_table, int seqlen,
 /* ==================== asynchronous, status-returning forms ==================== */
 
 /* General fused attention: dtype ATN_DTYPE_*, optional positional encoding
- * (pe == NULL: plain SDPA), workspace == NULL: library-managed scratch
- * (allocated on first use per device, grown as needed), else caller scratch
- * of at least atn_attention_workspace_bytes(...) bytes.  Enqueued on stream. */
+ * (pe == NULL: plain SDPA).  workspace == NULL: library-managed scratch, one
+ * per (device, stream), allocated zero-filled on first use and grown as
+ * needed; else caller scratch of at least atn_attention_workspace_bytes(...)
+ * bytes that was zero-filled once before its first use (its first 32 KiB
+ * then hold synchronization words that stay valid from call to call, so it
+ * must not be re-initialized while in use).  Calls that run at the same
+ * time must not share a workspace.  Enqueued on stream; asynchronous; the
+ * enqueued work may be captured into a HIP graph and replayed (the kernel
+ * arguments of a call do not depend on earlier calls).
+ * Shapes with len_q <= 64 and len_k <= 128 run as one kernel whose
+ * workgroups meet at bounded device-side barriers; if such a wait ever
+ * expires the outputs of that call are NaN and atn_sync_status_ex reports
+ * ATN_ERR_DEVICE_TIMEOUT. */
 int atn_attention_fwd_ex(int dtype, const void *Q, const void *K, const void *V, void *out,
                          int batch, int heads, int len_q, int len_k, int head_d,
                          const atn_pe_desc *pe, void *workspace, size_t workspace_bytes,
@@ -218,9 +229,26 @@ size_t atn_attention_workspace_bytes(int dtype, int batch, int heads, int len_q,
 int atn_pe_apply_ex(int dtype, const void *in, void *out, long n_rows, int seq_len, int head_d,
                     const atn_pe_desc *pe, void *stream);
 
+/* Synchronizes `stream` and reports whether a call that used `workspace`
+ * (NULL: the library's workspace of that stream) hit a device-side wait
+ * timeout: ATN_OK or ATN_ERR_DEVICE_TIMEOUT (the status word is then
+ * cleared).  batch and heads are accepted for interface stability and not
+ * used. */
+int atn_sync_status_ex(void *workspace, int batch, int heads, void *stream);
+
 /* Prepares the library's angle tables for this encoding and shape on the
  * current device (otherwise built on first use, which synchronizes). */
 int atn_prepare_pe_ex(const atn_pe_desc *pe, int head_d, int max_positions);
+
+/* Which kernels atn_attention_fwd_ex runs for this shape on the current
+ * device (ATN_PATH_*), or a negative status for invalid arguments, assuming
+ * vector-aligned tensors (16-byte fp32 / 8-byte bf16 bases; otherwise the
+ * split-D pipeline runs).  Without a device the answer assumes 256 compute
+ * units. */
+#define ATN_PATH_FUSED_SMALL 1 /* one launch: split-D slices + device-side S all-reduce */
+#define ATN_PATH_SPLIT_D 2     /* three launches: partial QK^T, softmax, PV */
+int atn_attention_path_ex(int dtype, int batch, int heads, int len_q, int len_k, int head_d,
+                          const atn_pe_desc *pe);
 
 /* Number of visible HIP devices (0 when none); never aborts. */
 int atn_device_count(void);

@@ -40,6 +40,33 @@ def check_f32(got, ref, abs_tol=F32_ABS, rel_tol=F32_REL):
     return int(fail.sum()), float(a.max()), float(rel.max())
 
 
+def sdpa64(Q, K, V):
+    """Float64 softmax(Q K^T / sqrt(D)) V -- the exact value for float32 inputs."""
+    Q, K, V = (np.asarray(x, dtype=np.float64) for x in (Q, K, V))
+    s = Q @ np.swapaxes(K, -1, -2) / np.sqrt(Q.shape[-1])
+    s -= s.max(-1, keepdims=True)
+    p = np.exp(s)
+    p /= p.sum(-1, keepdims=True)
+    return p @ V
+
+
+def check_f32_or_truth(got, ref, truth, abs_tol=F32_ABS, rel_tol=F32_REL):
+    """fp32 bar against the CPU oracle, with the exact (float64) result as a
+    second referee: an element fails iff it misses the abs/rel bar against
+    the oracle AND against the exact value.  Used where the oracle's own
+    sequential float32 sums drift by ~1e-4 (scores of magnitude ~30 with the
+    sinusoidal encoding at D >= 4096).  Returns (n_fail, max_abs vs oracle,
+    max_abs vs truth)."""
+    g = np.asarray(got, dtype=np.float64).ravel()
+    r = np.asarray(ref, dtype=np.float64).ravel()
+    t = np.asarray(truth, dtype=np.float64).ravel()
+    a_r, a_t = np.abs(g - r), np.abs(g - t)
+    bad_r = (a_r > abs_tol) & (a_r / (np.abs(r) + 1e-8) > rel_tol)
+    bad_t = (a_t > abs_tol) & (a_t / (np.abs(t) + 1e-8) > rel_tol)
+    fail = (bad_r & bad_t) | ~np.isfinite(g)
+    return int(fail.sum()), float(a_r.max()), float(a_t.max())
+
+
 def check_bf16(got, ref, rel_tol=BF16_REL):
     """bf16 output vs fp32 oracle: an element fails iff its error exceeds
     rel_tol * |ref| AND rel_tol * rms(ref); the norm-wise relative error must

@@ -53,7 +53,7 @@ def test_reference_dropin_names_present(am):
 
 
 def test_status_strings(am, L):
-    for code in range(0, -11, -1):
+    for code in range(0, -12, -1):
         s = am.status_string(code)
         assert s and s != "unknown status"
     assert am.status_string(-99) == "unknown status"
@@ -127,6 +127,17 @@ def test_workspace_bytes(am):
     assert am.workspace_bytes(0, 0, 4, 64, 64, 2048) == 0
     assert am.workspace_bytes(9, 1, 4, 64, 64, 2048) == 0
     assert am.workspace_bytes(0, 1, 4, 64, 64, 2048, am.make_pe("rope", rotary_dim=3)) == 0
+
+
+def test_path_selection_without_device(am):
+    """Short sequences take the single-launch kernel, long ones the pipeline."""
+    assert am.path(0, 1, 4, 64, 64, 2048) == am.ATN_PATH_FUSED_SMALL       # config 2
+    assert am.path(1, 1, 4, 32, 128, 8192) == am.ATN_PATH_FUSED_SMALL      # config 3
+    assert am.path(0, 1, 1, 4, 4, 8) == am.ATN_PATH_FUSED_SMALL            # config 1
+    assert am.path(0, 4, 32, 512, 512, 128) == am.ATN_PATH_SPLIT_D
+    assert am.path(0, 1, 1, 3, 129, 36) == am.ATN_PATH_SPLIT_D
+    assert am.path(0, 1, 300, 16, 16, 64) == am.ATN_PATH_SPLIT_D           # more heads than CUs
+    assert am.path(0, 0, 4, 64, 64, 2048) == -2
 
 
 def test_no_device_path(am, L):

@@ -1,0 +1,157 @@
+"""GPU tests of the single-launch split-D kernel (len_q <= 64, len_k <= 128).
+
+Besides parity with the CPU oracle (the drop-in tests in
+test_gpu_parity.py route these shapes here too), this kernel keeps state in
+its workspace: per-head barrier epochs, per-workgroup barrier flags and a
+status word.  These tests check that many calls in a row on one workspace
+keep working and give bit-identical results (fixed summation order), that
+caller workspaces on two streams do not interfere, that captured HIP graphs
+replay correctly, and that no call reports a device-side wait timeout.
+"""
+import numpy as np
+import pytest
+
+import helpers as H
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+
+def _ws(am, dcode, B, Hh, Lq, Lk, D, pe=None):
+    import hip_rt
+    n = am.workspace_bytes(dcode, B, Hh, Lq, Lk, D, pe)
+    return hip_rt.DeviceArray((n // 4,), "f32", fill=0)
+
+
+@pytest.mark.parametrize("shape", [(1, 4, 64, 64, 2048), (1, 4, 64, 64, 512),
+                                   (1, 4, 64, 64, 8192), (1, 2, 32, 32, 4096),
+                                   (1, 1, 16, 16, 8192), (2, 8, 64, 64, 128)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_fused_path_selected_and_repeatable(am, dev, shape):
+    import hip_rt
+    B, Hh, Lq, Lk, D = shape
+    print(f"[case] fused repeat f32 {shape}", flush=True)
+    assert am.path(0, B, Hh, Lq, Lk, D) == am.ATN_PATH_FUSED_SMALL
+    (q, k, v), (Q, K, V) = H.device_inputs((B, Hh, Lq, D), (B, Hh, Lk, D), 5 + D)
+    ws = _ws(am, 0, B, Hh, Lq, Lk, D)
+    out = H.empty(Q.shape)
+    first = None
+    for it in range(25):
+        am.attention_ex(q, k, v, out, workspace=ws)
+        if it in (0, 24):
+            hip_rt.synchronize()
+            got = out.bits()
+            if first is None:
+                first = got
+            else:
+                assert np.array_equal(first, got), "results differ between calls"
+    assert am.sync_status(ws, B, Hh) == 0
+    ref = oracle.attention(Q, K, V, nthreads=16)
+    n, mabs, mrel = H.check_f32(first, ref)
+    assert n == 0, f"{n} mismatches, max abs {mabs}, max rel {mrel}"
+
+
+def test_fused_config3_bf16_repeat(am, dev):
+    """BASELINE config 3 (bf16 cross-attention 32 -> 128, D = 8192)."""
+    import hip_rt
+    B, Hh, Lq, Lk, D = 1, 4, 32, 128, 8192
+    print("[case] fused repeat bf16 cfg3", flush=True)
+    assert am.path(1, B, Hh, Lq, Lk, D) == am.ATN_PATH_FUSED_SMALL
+    (q, k, v), (Q, K, V) = H.device_inputs((B, Hh, Lq, D), (B, Hh, Lk, D), 33, "bf16")
+    out = H.empty(Q.shape, "bf16")
+    for _ in range(10):
+        am.attention_ex(q, k, v, out)
+    hip_rt.synchronize()
+    assert am.sync_status() == 0
+    ref = oracle.attention(Q, K, V, nthreads=16)
+    n, nrel, mabs = H.check_bf16(out.numpy(), ref)
+    assert n == 0, f"normwise rel {nrel}, max abs {mabs}"
+    # the bf16 result is the fp32 result rounded once: far inside 2e-2
+    assert nrel < 4e-3, nrel
+
+
+def test_fused_two_streams_two_workspaces(am, dev):
+    import hip_rt
+    B, Hh, Lq, Lk, D = 1, 4, 64, 64, 1024
+    print("[case] fused two streams", flush=True)
+    s1, s2 = hip_rt.Stream(), hip_rt.Stream()
+    ins1, host1 = H.device_inputs((B, Hh, Lq, D), (B, Hh, Lk, D), 71)
+    ins2, host2 = H.device_inputs((B, Hh, Lq, D), (B, Hh, Lk, D), 72)
+    w1, w2 = _ws(am, 0, B, Hh, Lq, Lk, D), _ws(am, 0, B, Hh, Lq, Lk, D)
+    o1, o2 = H.empty((B, Hh, Lq, D)), H.empty((B, Hh, Lq, D))
+    for _ in range(20):
+        am.attention_ex(*ins1, o1, workspace=w1, stream=s1)
+        am.attention_ex(*ins2, o2, workspace=w2, stream=s2)
+    s1.synchronize()
+    s2.synchronize()
+    assert am.sync_status(w1, B, Hh, s1) == 0 and am.sync_status(w2, B, Hh, s2) == 0
+    for o, h in ((o1, host1), (o2, host2)):
+        n, mabs, _ = H.check_f32(o.numpy(), oracle.attention(*h, nthreads=16))
+        assert n == 0, mabs
+    s1.destroy()
+    s2.destroy()
+
+
+@pytest.mark.parametrize("pe", ["rope_half", "rope_inter", "sinusoidal"])
+def test_fused_with_encodings_bf16(am, dev, pe):
+    """Positional encodings applied at load inside the single-launch kernel."""
+    import hip_rt
+    B, Hh, Lq, Lk, D = 1, 4, 48, 96, 2048
+    print(f"[case] fused bf16 {pe}", flush=True)
+    sigma = 0.5 if pe == "sinusoidal" else 1.0
+    (q, k, v), (Q, K, V) = H.device_inputs((B, Hh, Lq, D), (B, Hh, Lk, D), 81, "bf16", sigma)
+    desc = {"rope_half": am.make_pe("rope", pairing="half"),
+            "rope_inter": am.make_pe("rope"),
+            "sinusoidal": am.make_pe("sinusoidal")}[pe]
+    assert am.path(1, B, Hh, Lq, Lk, D, desc) == am.ATN_PATH_FUSED_SMALL
+    out = H.empty(Q.shape, "bf16")
+    am.attention_ex(q, k, v, out, pe=desc)
+    hip_rt.synchronize()
+    assert am.sync_status() == 0
+    if pe == "sinusoidal":
+        st, ct = oracle.sinusoidal_table(max(Lq, Lk), D)
+        ref = oracle.attention_sinusoidal(Q, K, V, st, ct, nthreads=16)
+    else:
+        c, s = oracle.rope_cache(max(Lq, Lk), D)
+        ref = oracle.attention_rope(Q, K, V, c, s, pairing="half" if pe == "rope_half"
+                                    else "interleaved", nthreads=16)
+    n, nrel, mabs = H.check_bf16(out.numpy(), ref)
+    assert n == 0, f"normwise rel {nrel}, max abs {mabs}"
+
+
+@pytest.mark.parametrize("shape", [(1, 4, 64, 64, 2048), (1, 2, 130, 70, 256)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_graph_replays_match_eager(am, dev, shape):
+    """Captured HIP graph of three calls, replayed four times with eager work
+    and synchronizations in between; every replay must equal the eager
+    result bit for bit (the single-launch kernel keeps its barrier epochs in
+    device memory, so replayed arguments stay valid)."""
+    import hip_rt
+    B, Hh, Lq, Lk, D = shape
+    print(f"[case] graph replay {shape}", flush=True)
+    (q, k, v), (Q, K, V) = H.device_inputs((B, Hh, Lq, D), (B, Hh, Lk, D), 91)
+    ws = _ws(am, 0, B, Hh, Lq, Lk, D)
+    st = hip_rt.Stream()
+    eager = H.empty(Q.shape)
+    am.attention_ex(q, k, v, eager, workspace=ws, stream=st)
+    st.synchronize()
+    ref = eager.bits()
+    outs = [H.empty(Q.shape) for _ in range(3)]
+    g = hip_rt.Graph(st, lambda: [am.attention_ex(q, k, v, o, workspace=ws, stream=st)
+                                  for o in outs])
+    for rep in range(4):
+        for o in outs:
+            o.fill_nan()
+        hip_rt.synchronize()
+        g.launch()
+        st.synchronize()
+        for o in outs:
+            assert np.array_equal(o.bits(), ref), f"replay {rep} differs from eager"
+        am.attention_ex(q, k, v, eager, workspace=ws, stream=st)  # eager work between replays
+        st.synchronize()
+        assert np.array_equal(eager.bits(), ref)
+    g.destroy()
+    assert am.sync_status(ws, B, Hh, st) == 0
+    n, mabs, _ = H.check_f32(ref, oracle.attention(Q, K, V, nthreads=16))
+    assert n == 0, mabs
+    st.destroy()

@@ -222,22 +222,25 @@ def test_sinusoidal_f32(am, dev, shape):
     Q, K, V = H.rng_inputs((B, Hh, Lq, D), (B, Hh, Lk, D), seed=61 + D)
     st, ct = oracle.sinusoidal_table(max(Lq, Lk), D)
     ref = oracle.attention_sinusoidal(Q, K, V, st, ct, nthreads=8)
+    # exact SDPA of the float32-encoded inputs (the oracle's own float32 sums
+    # drift by ~1e-4 here at D = 4096, where scores reach ~30)
+    truth = H.sdpa64(oracle.add_sinusoidal(Q, st, ct), oracle.add_sinusoidal(K, st, ct), V)
     got = _f32_call(am.attention_forward_sinusoidal_fused, Q, K, V)
-    n, mabs, _ = H.check_f32(got, ref)
-    assert n == 0, f"fused: {n} mismatches, max abs {mabs}"
+    n, mabs, mtruth = H.check_f32_or_truth(got, ref, truth)
+    assert n == 0, f"fused: {n} mismatches, max abs {mabs} (vs exact {mtruth})"
     tst, tct = H.upload(st), H.upload(ct)
     q, k, v = H.upload(Q), H.upload(K), H.upload(V)
     k_emb, q_emb, out = H.empty(K.shape), H.empty(Q.shape), H.empty(Q.shape)
     am.attention_forward_sinusoidal_hybrid(q, k, v, tst, tct, k_emb, out)
     hip_rt.synchronize()
-    n, mabs, _ = H.check_f32(out.numpy(), ref)
-    assert n == 0, f"hybrid: {n} mismatches, max abs {mabs}"
+    n, mabs, mtruth = H.check_f32_or_truth(out.numpy(), ref, truth)
+    assert n == 0, f"hybrid: {n} mismatches, max abs {mabs} (vs exact {mtruth})"
     assert np.array_equal(k_emb.numpy(), oracle.add_sinusoidal(K, st, ct))
     out.fill_nan()
     am.attention_forward_sinusoidal_separate(q, k, v, tst, tct, q_emb, k_emb, out)
     hip_rt.synchronize()
-    n, mabs, _ = H.check_f32(out.numpy(), ref)
-    assert n == 0, f"separate: {n} mismatches, max abs {mabs}"
+    n, mabs, mtruth = H.check_f32_or_truth(out.numpy(), ref, truth)
+    assert n == 0, f"separate: {n} mismatches, max abs {mabs} (vs exact {mtruth})"
     assert np.array_equal(q_emb.numpy(), oracle.add_sinusoidal(Q, st, ct))
     pe_out = H.empty(Q.shape)
     am.apply_sinusoidal_embeddings(q, tst, tct, pe_out, Lq)
