@@ -48,6 +48,7 @@ ATN_ROPE_INTERLEAVED = 0
 ATN_ROPE_HALF = 1
 ATN_PATH_FUSED_SMALL = 1
 ATN_PATH_SPLIT_D = 2
+ATN_PATH_GEMM = 3
 
 
 class PeDesc(ctypes.Structure):

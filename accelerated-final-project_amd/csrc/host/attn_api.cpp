@@ -370,6 +370,39 @@ FusedPlan fused_plan(int dtype, int pek, const Shape& s, bool query_device) {
     return p;
 }
 
+// ---------------------------------------------------------------- gemm plan
+// Long-sequence bf16 shapes: two MFMA GEMMs around an exact row softmax.
+// Workspace after the sync region: encoded Q and K (bf16, only for the sides
+// a positional encoding applies to), S (fp32), P (bf16).
+constexpr int kGemmMinL = 128;
+
+struct GemmPlan {
+    bool ok = false, encoded = false;
+    size_t q_off = 0, k_off = 0, qs_off = 0, ks_off = 0, s_off = 0, p_off = 0, bytes = 0;
+};
+
+GemmPlan gemm_plan(int dtype, const Shape& s, const PePlan& plan) {
+    GemmPlan p;
+    if (dtype != ATN_DTYPE_BF16 || s.Lq < kGemmMinL || s.Lk < kGemmMinL || s.D % 8 != 0 ||
+        s.Lk % 8 != 0)
+        return p;
+    size_t off = kSyncBytes;
+    auto take = [&](size_t b) { size_t o = off; off += round256(b); return o; };
+    // with a positional encoding both sides are re-encoded as scaled fp16
+    p.encoded = plan.pek != atn::kPeNone;
+    if (p.encoded) {
+        p.q_off = take((size_t)s.BH * s.Lq * s.D * 2);
+        p.k_off = take((size_t)s.BH * s.Lk * s.D * 2);
+        p.qs_off = take((size_t)s.BH * s.Lq * 4);
+        p.ks_off = take((size_t)s.BH * s.Lk * 4);
+    }
+    p.s_off = take((size_t)s.BH * s.Lq * s.Lk * 4);
+    p.p_off = take((size_t)s.BH * s.Lq * s.Lk * 2);
+    p.bytes = off;
+    p.ok = true;
+    return p;
+}
+
 // ---------------------------------------------------------------- core
 int attention_core(int dtype, const void* Q, const void* K, const void* V, void* out, int B,
                    int H, int Lq, int Lk, int D, const atn_pe_desc* pe, void* workspace,
@@ -389,9 +422,10 @@ int attention_core(int dtype, const void* Q, const void* K, const void* V, void*
     st = check_pe(pe, D, &plan);
     if (st != ATN_OK) return st;
     const FusedPlan fp = fused_plan(dtype, plan.pek, s, false);
+    const GemmPlan gp = gemm_plan(dtype, s, plan);
     const StreamPlan sp = stream_plan(s);
-    const size_t need_upper =
-        std::max(fp.ok ? fp.bytes : (size_t)0, kSyncBytes + sp.bytes);
+    const size_t need_upper = std::max({fp.ok ? fp.bytes : (size_t)0,
+                                        gp.ok ? gp.bytes : (size_t)0, kSyncBytes + sp.bytes});
     if (workspace != nullptr && workspace_bytes < need_upper) return ATN_ERR_WORKSPACE;
     const int64_t tiles = s.BH * ((Lq + 63) / 64) * ((Lk + 63) / 64) * sp.nsplit;
     const int64_t pv_tiles = s.BH * ((Lq + 63) / 64) * ((D + 63) / 64);
@@ -405,7 +439,14 @@ int attention_core(int dtype, const void* Q, const void* K, const void* V, void*
     // the device's own capacity decides between the single-launch kernel
     // and the three-kernel pipeline
     const FusedPlan fd = fused_plan(dtype, plan.pek, s, true);
-    const size_t need = fd.ok ? fd.bytes : kSyncBytes + sp.bytes;
+    const size_t va = dtype == ATN_DTYPE_F32 ? 16 : 8;
+    const int vec_qk = (D % 4 == 0) && aligned(Q, va) && aligned(K, va);
+    const int vec_vo = (D % 4 == 0) && aligned(V, va) && aligned(out, va);
+    const bool use_fused = fd.ok && vec_qk && vec_vo;
+    const bool use_gemm = !use_fused && gp.ok && aligned(Q, 16) && aligned(K, 16) &&
+                          aligned(V, 16) && aligned(out, 16);
+    const size_t need =
+        use_fused ? fd.bytes : (use_gemm ? gp.bytes : kSyncBytes + sp.bytes);
     void* ws = workspace;
     if (ws == nullptr) {
         st = ensure_workspace(need_upper > need ? need_upper : need, stream, &ws);
@@ -414,14 +455,39 @@ int attention_core(int dtype, const void* Q, const void* K, const void* V, void*
         return ATN_ERR_WORKSPACE;
     }
     int* status = reinterpret_cast<int*>(ws);
-
-    const size_t va = dtype == ATN_DTYPE_F32 ? 16 : 8;
-    const int vec_qk = (D % 4 == 0) && aligned(Q, va) && aligned(K, va);
-    const int vec_vo = (D % 4 == 0) && aligned(V, va) && aligned(out, va);
     const float scale = 1.0f / sqrtf((float)D);  // final/attention.cu:206
 
     float* scratch = reinterpret_cast<float*>((char*)ws + kSyncBytes);
-    if (fd.ok && vec_qk && vec_vo) {
+    if (use_gemm) {
+        char* w = static_cast<char*>(ws);
+        const uint16_t* qe = static_cast<const uint16_t*>(Q);
+        const uint16_t* ke = static_cast<const uint16_t*>(K);
+        const float* qinv = nullptr;
+        const float* kinv = nullptr;
+        if (gp.encoded) {
+            uint16_t* qd = reinterpret_cast<uint16_t*>(w + gp.q_off);
+            uint16_t* kd = reinterpret_cast<uint16_t*>(w + gp.k_off);
+            float* qs = reinterpret_cast<float*>(w + gp.qs_off);
+            float* ks = reinterpret_cast<float*>(w + gp.ks_off);
+            ATN_HIP(atn::launch_encode_f16(plan.q.on ? plan.pek : atn::kPeNone, qe, qd, qs,
+                                           (long)(s.BH * Lq), Lq, D, plan.q, stream));
+            ATN_HIP(atn::launch_encode_f16(plan.k.on ? plan.pek : atn::kPeNone, ke, kd, ks,
+                                           (long)(s.BH * Lk), Lk, D, plan.k, stream));
+            qe = qd;
+            ke = kd;
+            qinv = qs;
+            kinv = ks;
+        }
+        float* S = reinterpret_cast<float*>(w + gp.s_off);
+        uint16_t* P = reinterpret_cast<uint16_t*>(w + gp.p_off);
+        ATN_HIP(atn::launch_gemm_qk(gp.encoded ? 1 : 0, qe, ke, qinv, kinv, S, (int)s.BH, Lq, Lk, D,
+                                    scale, stream));
+        ATN_HIP(atn::launch_softmax_bf16(S, P, s.BH * Lq, Lk, stream));
+        ATN_HIP(atn::launch_gemm_pv(P, static_cast<const uint16_t*>(V),
+                                    static_cast<uint16_t*>(out), (int)s.BH, Lq, Lk, D, stream));
+        return ATN_OK;
+    }
+    if (use_fused) {
         unsigned* epochs = reinterpret_cast<unsigned*>((char*)ws + kSyncEpochOff);
         auto* flags = reinterpret_cast<unsigned long long*>((char*)ws + kSyncFlagOff);
         ATN_HIP(atn::launch_fused_small(dtype, plan.pek, Q, K, V, out, scratch,
@@ -584,7 +650,9 @@ size_t atn_attention_workspace_bytes(int dtype, int batch, int heads, int len_q,
     PePlan plan;
     if (check_pe(pe, head_d, &plan) != ATN_OK) return 0;
     const FusedPlan fp = fused_plan(dtype, plan.pek, s, false);
-    return std::max(fp.ok ? fp.bytes : (size_t)0, kSyncBytes + stream_plan(s).bytes);
+    const GemmPlan gp = gemm_plan(dtype, s, plan);
+    return std::max({fp.ok ? fp.bytes : (size_t)0, gp.ok ? gp.bytes : (size_t)0,
+                     kSyncBytes + stream_plan(s).bytes});
 }
 
 int atn_pe_apply_ex(int dtype, const void* in, void* out, long n_rows, int seq_len, int head_d,
@@ -603,7 +671,9 @@ int atn_attention_path_ex(int dtype, int batch, int heads, int len_q, int len_k,
     if (st != ATN_OK) return st;
     int n = 0;
     const bool dev = hipGetDeviceCount(&n) == hipSuccess && n > 0;
-    return fused_plan(dtype, plan.pek, s, dev).ok ? ATN_PATH_FUSED_SMALL : ATN_PATH_SPLIT_D;
+    if (fused_plan(dtype, plan.pek, s, dev).ok) return ATN_PATH_FUSED_SMALL;
+    if (gemm_plan(dtype, s, plan).ok) return ATN_PATH_GEMM;
+    return ATN_PATH_SPLIT_D;
 }
 
 int atn_sync_status_ex(void* workspace, int batch, int heads, void* stream) {

@@ -153,4 +153,59 @@ __device__ __forceinline__ float sin_pe(const PeSide& t, int pos, int d) {
     return (d & 1) ? t.b[idx] : t.a[idx];
 }
 
+// Loads x[d..d+3] of one row (row pointer xr, position pos), applies the
+// positional encoding of this side, and returns fp32.  Elements at or past
+// dend read as 0.  d is a multiple of 4.
+template <typename T, int PEK>
+__device__ __forceinline__ float4 load_row4_pe(const T* __restrict__ xr, int pos, int d, int dend,
+                                              const PeSide& pe, bool vec_ok) {
+    float v[4] = {0.f, 0.f, 0.f, 0.f};
+    if (vec_ok && d + 3 < dend) {
+        float4 t = Elem<T>::ld4(xr, d);
+        v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
+    } else {
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+            if (d + c < dend) v[c] = Elem<T>::ld(xr, d + c);
+    }
+    if constexpr (PEK == kPeRopeInterleaved) {
+        if (pe.on) {
+#pragma unroll
+            for (int c = 0; c < 4; c += 2) {
+                const int e = d + c;  // even
+                if (e < pe.rotary) {
+                    float cs, sn;
+                    rope_cs(pe, pos, e >> 1, cs, sn);
+                    const float x0 = v[c], x1 = v[c + 1];
+                    v[c] = rot_first(x0, x1, cs, sn);
+                    v[c + 1] = rot_second(x0, x1, cs, sn);
+                }
+            }
+        }
+    } else if constexpr (PEK == kPeRopeHalf) {
+        if (pe.on) {
+            const int h = pe.rotary >> 1;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const int e = d + c;
+                if (e < pe.rotary) {
+                    const bool lo = e < h;
+                    const int f = lo ? e : e - h;
+                    const float xp = Elem<T>::ld(xr, lo ? e + h : e - h);
+                    float cs, sn;
+                    rope_cs(pe, pos, f, cs, sn);
+                    v[c] = lo ? rot_first(v[c], xp, cs, sn) : rot_second(xp, v[c], cs, sn);
+                }
+            }
+        }
+    } else if constexpr (PEK == kPeSinusoidal) {
+        if (pe.on) {
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+                if (d + c < dend) v[c] = v[c] + sin_pe(pe, pos, d + c);
+        }
+    }
+    return make_float4(v[0], v[1], v[2], v[3]);
+}
+
 }  // namespace atn

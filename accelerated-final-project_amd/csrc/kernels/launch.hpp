@@ -29,6 +29,18 @@ hipError_t launch_fused_small(int dtype, int pek, const void* Q, const void* K, 
                               unsigned long long* flags, int* status, int BH, int Lq, int Lk,
                               int D, int dc, int nchunk, float scale, const PeSide& pq,
                               const PeSide& pk, int vec_ok, hipStream_t st);
+// Long-sequence bf16 path (gemm_path.hip): S = scale Q K^T (fp32),
+// P = bf16(softmax(S)), O = P V.  Needs D % 8 == 0, Lk % 8 == 0 and 16-byte
+// aligned bases.
+hipError_t launch_encode_f16(int pek, const uint16_t* in, uint16_t* out, float* inv, long n_rows,
+                             int seq_len, int D, const PeSide& pe, hipStream_t st);
+hipError_t launch_gemm_qk(int f16, const uint16_t* Q, const uint16_t* K, const float* qinv,
+                          const float* kinv, float* S, int BH, int Lq, int Lk, int D, float scale,
+                          hipStream_t st);
+hipError_t launch_softmax_bf16(const float* S, uint16_t* P, long rows, int Lk, hipStream_t st);
+hipError_t launch_gemm_pv(const uint16_t* P, const uint16_t* V, uint16_t* O, int BH, int Lq, int Lk,
+                          int D, hipStream_t st);
+
 hipError_t launch_pe_apply(int dtype, int pek, const void* in, void* out, long n_rows,
                            int seq_len, int D, const PeSide& pe, int vec_ok, hipStream_t st);
 
