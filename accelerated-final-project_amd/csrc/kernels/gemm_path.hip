@@ -22,10 +22,11 @@
 // GEMM epilogue multiplies the row and column scales back (exactly).
 //
 // Both GEMMs use 256 x 256 output tiles per workgroup of 512 threads (8
-// waves, each 64 rows x 128 columns = 2 x 4 tiles of
-// v_mfma_f32_32x32x16_bf16), a K step of 32 with the next step's global
-// loads in flight during the current step's MFMAs (double-buffered LDS),
-// and an XCD-aware tile order: consecutive tile indices run on the same XCD
+// waves, each 64 x 128 = 2 x 4 tiles of
+// v_mfma_f32_32x32x16_{f16,bf16}), a K step of 64 with the global loads of
+// step k + 1 in flight while step k runs its MFMAs (double-buffered LDS,
+// 144 KiB), and an
+// XCD-aware tile order: consecutive tile indices run on the same XCD
 // (workgroups are dealt round-robin to the 8 XCDs), so concurrent
 // workgroups of one head share their Q/K/V panels in that XCD's L2.
 //
@@ -43,10 +44,15 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
-constexpr int kBM = 256, kBN = 256, kBK = 32;
-constexpr int kGemmThreads = 512;
-constexpr int kLdsRow = kBK + 8;  // bf16 elements per LDS row (16-byte aligned, padded)
+constexpr int kBM = 256, kBN = 256, kBK = 64;
+constexpr int kGemmThreads = 512;            // 8 waves
+constexpr int kWavesN = 2;                   // wave grid: (8 / kWavesN) x kWavesN
+constexpr int kTI = kBM / (kGemmThreads / 64 / kWavesN) / 32;  // 32x32 tiles per wave (rows)
+constexpr int kTJ = kBN / kWavesN / 32;                        // (columns)
+constexpr int kDepth = 1;                    // register stages of global prefetch (1 or 2)
+constexpr int kLdsRow = kBK + 8;  // 16-bit elements per LDS row (16-byte aligned, padded)
 constexpr int kTileElems = kBM * kLdsRow;
+constexpr int kChunkPerRow = kBK / 8;
 
 // 8 x 8-element MFMA step on raw 16-bit operands (bf16 or fp16 bits).
 template <bool F16>
@@ -90,8 +96,11 @@ struct GemmArgs {
 
 template <bool F16, bool B_NN, int OUT>
 __global__ __launch_bounds__(kGemmThreads) void k_gemm(GemmArgs g) {
-    __shared__ __align__(16) uint16_t As[2][kTileElems];
-    __shared__ __align__(16) uint16_t Bs[2][kTileElems];  // [n][k] (B^T rows)
+    // one LDS block: A stages 0/1, then B^T stages 0/1 ([n][k] rows); the
+    // bf16 epilogue reuses it whole as an output staging tile
+    __shared__ __align__(16) uint16_t lds[4 * kTileElems];
+    uint16_t(*As)[kTileElems] = reinterpret_cast<uint16_t(*)[kTileElems]>(lds);
+    uint16_t(*Bs)[kTileElems] = reinterpret_cast<uint16_t(*)[kTileElems]>(lds + 2 * kTileElems);
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -101,8 +110,17 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm(GemmArgs g) {
     if (t >= total) return;
     const int bh = (int)(t / per_head);
     const int rem = (int)(t - (long)bh * per_head);
-    // within a head: row panels outer, so neighbours share the A panel
-    const int tm = rem / g.tiles_n, tn = rem - tm * g.tiles_n;
+    // within a head: NT runs row panels outer (neighbours share the Q
+    // panel); NN runs row panels fastest, so the few workgroups of one V
+    // panel run together and share it in L2
+    int tm, tn;
+    if constexpr (B_NN) {
+        tn = rem / g.tiles_m;
+        tm = rem - tn * g.tiles_m;
+    } else {
+        tm = rem / g.tiles_n;
+        tn = rem - tm * g.tiles_n;
+    }
     const int m0 = tm * kBM, n0 = tn * kBN;
 
     const uint16_t* A = g.A + bh * g.sa;
@@ -111,119 +129,191 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm(GemmArgs g) {
     // ---- global -> register staging: each thread moves two 16-byte chunks
     // of A (rows m0.., 4 chunks of 8 per row) and, for B^T rows (NT), two
     // chunks of B; for NN, an 8-key x 2-column block of B (8 dwords), which
-    // it transposes with v_perm_b32 into two 16-byte LDS rows.
+    // it transposes with v_perm_b32 into two 16-byte LDS rows.  Two register
+    // stages rotate with the two LDS buffers, so a step's global loads are
+    // issued two MFMA phases before their data is needed.
     // A chunk c (0..1023): row = c / 4, k8 = (c % 4) * 8.
-    uint4 ra[2], rb[2];
-    uint32_t rv[8];
-    const int vkg = tid >> 7, vdp = tid & 127;  // NN: keys 8 vkg.., columns 2 vdp, 2 vdp + 1
-    auto load_stage = [&](int k0) {
+    constexpr int kChunks = kBM * kBK / 8 / kGemmThreads;  // 16-byte chunks per thread per operand
+    constexpr int kVBlocks = kBK / 8 * (kBN / 2) / kGemmThreads;  // NN: 8x2 blocks per thread
+    static_assert(kChunks >= 1 && kVBlocks >= 1, "tile too small for the thread count");
+    struct Stage {
+        uint4 a[kChunks], b[kChunks];
+        uint32_t v[kVBlocks][8];
+    };
+    Stage st0, st1;
+    // NN block b = tid + u * threads: keys 8 * (b / 128).., columns 2 * (b % 128), +1
+    auto load_stage = [&](Stage& r, int k0) {
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
+        for (int u = 0; u < kChunks; ++u) {
             const int cidx = tid + u * kGemmThreads;
-            const int row = cidx >> 2, k8 = (cidx & 3) * 8;
+            const int row = cidx / kChunkPerRow, k8 = (cidx % kChunkPerRow) * 8;
             const int gm = m0 + row, gk = k0 + k8;
-            ra[u] = make_uint4(0, 0, 0, 0);
+            r.a[u] = make_uint4(0, 0, 0, 0);
             if (gm < g.M && gk < g.K)
-                ra[u] = *reinterpret_cast<const uint4*>(A + (long)gm * g.lda + gk);
+                r.a[u] = *reinterpret_cast<const uint4*>(A + (long)gm * g.lda + gk);
         }
         if constexpr (!B_NN) {
 #pragma unroll
-            for (int u = 0; u < 2; ++u) {
+            for (int u = 0; u < kChunks; ++u) {
                 const int cidx = tid + u * kGemmThreads;
-                const int row = cidx >> 2, k8 = (cidx & 3) * 8;
+                const int row = cidx / kChunkPerRow, k8 = (cidx % kChunkPerRow) * 8;
                 const int gn = n0 + row, gk = k0 + k8;
-                rb[u] = make_uint4(0, 0, 0, 0);
+                r.b[u] = make_uint4(0, 0, 0, 0);
                 if (gn < g.N && gk < g.K)
-                    rb[u] = *reinterpret_cast<const uint4*>(B + (long)gn * g.ldb + gk);
+                    r.b[u] = *reinterpret_cast<const uint4*>(B + (long)gn * g.ldb + gk);
             }
         } else {
-            // B is [K x N]: 8 consecutive keys x 2 consecutive columns
-            const int gn = n0 + 2 * vdp;
+            // B is [K x N]: blocks of 8 consecutive keys x 2 consecutive columns
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const int gk = k0 + vkg * 8 + e;
-                rv[e] = 0u;
-                if (gk < g.K && gn < g.N)
-                    rv[e] = *reinterpret_cast<const uint32_t*>(B + (long)gk * g.ldb + gn);
+            for (int u = 0; u < kVBlocks; ++u) {
+                const int blk = tid + u * kGemmThreads;
+                const int vkg = blk / (kBN / 2), vdp = blk % (kBN / 2);
+                const int gn = n0 + 2 * vdp;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const int gk = k0 + vkg * 8 + e;
+                    r.v[u][e] = 0u;
+                    if (gk < g.K && gn < g.N)
+                        r.v[u][e] = *reinterpret_cast<const uint32_t*>(B + (long)gk * g.ldb + gn);
+                }
             }
         }
     };
-    auto store_stage = [&](int s) {
+    auto store_stage = [&](const Stage& r, int s) {
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
+        for (int u = 0; u < kChunks; ++u) {
             const int cidx = tid + u * kGemmThreads;
-            const int row = cidx >> 2, k8 = (cidx & 3) * 8;
-            *reinterpret_cast<uint4*>(&As[s][row * kLdsRow + k8]) = ra[u];
+            const int row = cidx / kChunkPerRow, k8 = (cidx % kChunkPerRow) * 8;
+            *reinterpret_cast<uint4*>(&As[s][row * kLdsRow + k8]) = r.a[u];
         }
         if constexpr (!B_NN) {
 #pragma unroll
-            for (int u = 0; u < 2; ++u) {
+            for (int u = 0; u < kChunks; ++u) {
                 const int cidx = tid + u * kGemmThreads;
-                const int row = cidx >> 2, k8 = (cidx & 3) * 8;
-                *reinterpret_cast<uint4*>(&Bs[s][row * kLdsRow + k8]) = rb[u];
+                const int row = cidx / kChunkPerRow, k8 = (cidx % kChunkPerRow) * 8;
+                *reinterpret_cast<uint4*>(&Bs[s][row * kLdsRow + k8]) = r.b[u];
             }
         } else {
-            // rv[e] = (B[k_e][n] | B[k_e][n + 1] << 16): gather the low halves
+            // v[e] = (B[k_e][n] | B[k_e][n + 1] << 16): gather the low halves
             // into row n and the high halves into row n + 1 of Bs[n][k]
-            uint4 lo, hi;
-            lo.x = __builtin_amdgcn_perm(rv[1], rv[0], 0x05040100u);
-            lo.y = __builtin_amdgcn_perm(rv[3], rv[2], 0x05040100u);
-            lo.z = __builtin_amdgcn_perm(rv[5], rv[4], 0x05040100u);
-            lo.w = __builtin_amdgcn_perm(rv[7], rv[6], 0x05040100u);
-            hi.x = __builtin_amdgcn_perm(rv[1], rv[0], 0x07060302u);
-            hi.y = __builtin_amdgcn_perm(rv[3], rv[2], 0x07060302u);
-            hi.z = __builtin_amdgcn_perm(rv[5], rv[4], 0x07060302u);
-            hi.w = __builtin_amdgcn_perm(rv[7], rv[6], 0x07060302u);
-            *reinterpret_cast<uint4*>(&Bs[s][(2 * vdp) * kLdsRow + vkg * 8]) = lo;
-            *reinterpret_cast<uint4*>(&Bs[s][(2 * vdp + 1) * kLdsRow + vkg * 8]) = hi;
+#pragma unroll
+            for (int u = 0; u < kVBlocks; ++u) {
+                const int blk = tid + u * kGemmThreads;
+                const int vkg = blk / (kBN / 2), vdp = blk % (kBN / 2);
+                const uint32_t* v = r.v[u];
+                uint4 lo, hi;
+                lo.x = __builtin_amdgcn_perm(v[1], v[0], 0x05040100u);
+                lo.y = __builtin_amdgcn_perm(v[3], v[2], 0x05040100u);
+                lo.z = __builtin_amdgcn_perm(v[5], v[4], 0x05040100u);
+                lo.w = __builtin_amdgcn_perm(v[7], v[6], 0x05040100u);
+                hi.x = __builtin_amdgcn_perm(v[1], v[0], 0x07060302u);
+                hi.y = __builtin_amdgcn_perm(v[3], v[2], 0x07060302u);
+                hi.z = __builtin_amdgcn_perm(v[5], v[4], 0x07060302u);
+                hi.w = __builtin_amdgcn_perm(v[7], v[6], 0x07060302u);
+                *reinterpret_cast<uint4*>(&Bs[s][(2 * vdp) * kLdsRow + vkg * 8]) = lo;
+                *reinterpret_cast<uint4*>(&Bs[s][(2 * vdp + 1) * kLdsRow + vkg * 8]) = hi;
+            }
         }
     };
 
-    // ---- wave tile: 64 rows x 128 columns = 2 x 4 MFMA tiles of 32 x 32
-    const int wm = (wave >> 1) * 64, wn = (wave & 1) * 128;
-    v16f acc[2][4];
+    // ---- wave tile: 128 x 128 = 4 x 4 MFMA tiles of 32 x 32
+    constexpr int TI = kTI, TJ = kTJ;
+    const int wm = (wave / kWavesN) * (TI * 32), wn = (wave % kWavesN) * (TJ * 32);
+    v16f acc[TI][TJ];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < TI; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < TJ; ++j)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
     const int lrow = lane & 31, lkh = (lane >> 5) * 8;
     const int nk = (g.K + kBK - 1) / kBK;
-
-    load_stage(0);
-    store_stage(0);
-    __syncthreads();
-    for (int kt = 0; kt < nk; ++kt) {
-        const int s = kt & 1;
-        if (kt + 1 < nk) load_stage((kt + 1) * kBK);
+    auto compute = [&](int s) {
 #pragma unroll
         for (int ks = 0; ks < kBK; ks += 16) {
-            uint4 af[2], bfr[4];
+            uint4 af[TI], bfr[TJ];
 #pragma unroll
-            for (int i = 0; i < 2; ++i)
+            for (int i = 0; i < TI; ++i)
                 af[i] = *reinterpret_cast<const uint4*>(
                     &As[s][(wm + i * 32 + lrow) * kLdsRow + ks + lkh]);
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
+            for (int j = 0; j < TJ; ++j)
                 bfr[j] = *reinterpret_cast<const uint4*>(
                     &Bs[s][(wn + j * 32 + lrow) * kLdsRow + ks + lkh]);
 #pragma unroll
-            for (int i = 0; i < 2; ++i)
+            for (int i = 0; i < TI; ++i)
 #pragma unroll
-                for (int j = 0; j < 4; ++j) acc[i][j] = mfma_32x32x16<F16>(af[i], bfr[j], acc[i][j]);
+                for (int j = 0; j < TJ; ++j) acc[i][j] = mfma_32x32x16<F16>(af[i], bfr[j], acc[i][j]);
         }
-        if (kt + 1 < nk) store_stage(s ^ 1);
+    };
+
+    if constexpr (kDepth == 1) {
+        // one register stage: step kt + 1's loads fly during step kt's MFMAs
+        load_stage(st0, 0);
+        store_stage(st0, 0);
         __syncthreads();
+        for (int kt = 0; kt < nk; ++kt) {
+            const int sb = kt & 1;
+            if (kt + 1 < nk) load_stage(st0, (kt + 1) * kBK);
+            compute(sb);
+            if (kt + 1 < nk) store_stage(st0, sb ^ 1);
+            __syncthreads();
+        }
+    } else {
+        // two register stages: step kt reads LDS buffer kt % 2 while register
+        // stage (kt % 2) carries step kt + 2
+        load_stage(st0, 0);
+        if (nk > 1) load_stage(st1, kBK);
+        store_stage(st0, 0);
+        __syncthreads();
+        for (int kt = 0; kt < nk; kt += 2) {
+            if (kt + 2 < nk) load_stage(st0, (kt + 2) * kBK);
+            compute(0);
+            if (kt + 1 < nk) store_stage(st1, 1);
+            __syncthreads();
+            if (kt + 1 >= nk) break;
+            if (kt + 3 < nk) load_stage(st1, (kt + 3) * kBK);
+            compute(1);
+            if (kt + 2 < nk) store_stage(st0, 0);
+            __syncthreads();
+        }
     }
 
     // ---- epilogue: lane holds column (lane % 32) and rows
-    // 8 * (r / 4) + 4 * (lane / 32) + r % 4 of each 32 x 32 tile
+    // 8 * (r / 4) + 4 * (lane / 32) + r % 4 of each 32 x 32 tile.
+    // bf16 output goes through LDS (the operand buffers are free now) and
+    // leaves as 16-byte row chunks.
+    if constexpr (OUT == kOutBf16) {
+        uint16_t* Ct = lds;  // 256 x (256 + 8) bf16 staging tile
+        constexpr int kCRow = kBN + 8;
+        static_assert(kBM * kCRow <= 4 * kTileElems, "output staging does not fit");
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < TI; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+            for (int j = 0; j < TJ; ++j) {
+                const int col = wn + j * 32 + (lane & 31);
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int row = wm + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                    Ct[row * kCRow + col] = f32_to_bf16_bits(acc[i][j][r]);
+                }
+            }
+        __syncthreads();
+        uint16_t* C = static_cast<uint16_t*>(g.C) + bh * g.sc;
+        for (int cidx = tid; cidx < kBM * kBN / 8; cidx += kGemmThreads) {
+            const int row = cidx / (kBN / 8), c8 = (cidx % (kBN / 8)) * 8;
+            const int grow = m0 + row, gcol = n0 + c8;
+            if (grow < g.M && gcol < g.N)
+                *reinterpret_cast<uint4*>(C + (long)grow * g.ldc + gcol) =
+                    *reinterpret_cast<const uint4*>(&Ct[row * kCRow + c8]);
+        }
+        return;
+    }
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) {
             const int col = n0 + wn + j * 32 + (lane & 31);
             if (col >= g.N) continue;
             const float csc = g.cs ? g.cs[(long)bh * g.N + col] * g.scale : g.scale;
