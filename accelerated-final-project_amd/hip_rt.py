@@ -83,6 +83,12 @@ def device_name(dev: int = 0) -> str:
     return buf.value.decode()
 
 
+def copy_d2d(dst: "DeviceArray", src: "DeviceArray", nbytes: int) -> None:
+    """Device-to-device copy of nbytes (runs as the HIP runtime's copy kernel)."""
+    assert nbytes <= min(dst.nbytes, src.nbytes)
+    check(hip().hipMemcpy(_vp(dst.ptr), _vp(src.ptr), nbytes, D2D), "hipMemcpy D2D")
+
+
 def synchronize() -> None:
     check(hip().hipDeviceSynchronize(), "hipDeviceSynchronize")
 

@@ -34,6 +34,13 @@ for sub in ("accelerated-final-project_amd", "oracle"):
 import numpy as np  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
+
+# HBM traffic per launch of the dominant kernel, measured with rocprofv3
+# FETCH_SIZE / WRITE_SIZE and scaled by a known-size device copy
+# (profiles/fused_small_cfg2_traffic.md).  Keyed by (config, head_dim).
+MEASURED_TRAFFIC_BYTES = {
+    (2, 2048): (11316 + 6224) * 1024,
+}
 BF16_PEAK_TFLOPS = 2500.0
 FP32_PEAK_TFLOPS = 157.3
 
@@ -59,6 +66,9 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="target CPU-oracle sample time (0 = skip)")
     ap.add_argument("--seed", type=int, default=2)
+    ap.add_argument("--calib-copy", type=int, default=0, metavar="MIB",
+                    help="also run 5 device-to-device copies of MIB MiB (the HIP runtime's "
+                         "copy kernel), a known-size reference for rocprofv3 traffic counters")
     return ap.parse_args()
 
 
@@ -198,6 +208,13 @@ def main():
     if st != 0:
         raise am.AtnError(st, "device status after the timed region")
     path = am.path(dcode, B, H, Lq, Lk, D, desc)
+    if a.calib_copy > 0:
+        n = a.calib_copy << 20
+        src, dst = hip_rt.DeviceArray((n // 4,), "f32", fill=0), hip_rt.DeviceArray((n // 4,), "f32")
+        for _ in range(5):
+            hip_rt.copy_d2d(dst, src, n)
+        hip_rt.synchronize()
+        print(f"[bench] calibration: 5 device copies of {a.calib_copy} MiB", file=sys.stderr)
 
     es = 4 if dtype == "f32" else 2
     alg_bytes = (2 * B * H * Lq * D + 2 * B * H * Lk * D) * es
@@ -222,16 +239,21 @@ def main():
     err = float(np.max(np.abs(got - ref)))
 
     bound = "hbm" if flops / alg_bytes < (312 if dtype == "bf16" else 19.7) else "mfma"
+    traffic = MEASURED_TRAFFIC_BYTES.get((a.config, D))
     if bound == "hbm":
         roof = {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None}
+                "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic}
     else:
         peak = BF16_PEAK_TFLOPS if dtype == "bf16" else FP32_PEAK_TFLOPS
         roof = {"bound": "mfma", "achieved": round(tflops, 2), "peak": peak, "unit": "TFLOP/s",
-                "frac": round(tflops / peak, 4), "traffic": None}
+                "frac": round(tflops / peak, 4), "traffic": traffic}
     roof["kernel"] = ("k_fused_small (one launch per step)" if path == am.ATN_PATH_FUSED_SMALL
                       else "split-D pipeline (k_qk_partial + k_softmax + k_pv per step)")
     roof["timing"] = "HIP events around one graph replay of all timed steps, on its stream"
+    if traffic is not None:
+        roof["traffic_note"] = ("bytes per launch from rocprofv3 FETCH_SIZE + WRITE_SIZE scaled by "
+                                "a known-size device copy (profiles/fused_small_cfg2_traffic.md); "
+                                "measured for this build's kernel")
 
     cpu = None
     if a.cpu_seconds > 0:
