@@ -231,29 +231,27 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
 // NT independent 16x16 fp32 MFMA accumulations sharing one A operand:
 // acc[u] += sum_k A[k] B_u[k] over k in [0, kdim) step 4, where lane
 // (lr, lk) reads A at a[kk * ak] and tile u's B at b[u * bstep + kk * bk]
-// (a, b already offset to the lane's row and k = lk).  The operands of
-// step k + 1 are read (from a clamped index, so without a branch) before
-// the MFMAs of step k issue, hiding the LDS latency; no other control flow
-// inside the loop, so the accumulators stay in place.
+// (a, b already offset to the lane's row and k = lk).  kdim is a multiple
+// of 32: the operands of 8 k-steps are read from LDS first, then the 8 x NT
+// MFMAs issue back to back (no control flow inside, so the accumulators
+// stay in place).
 template <int NT>
 __device__ __forceinline__ void mma_f32(const float* a, int ak, const float* b, int bstep,
                                         int bk, int kdim, v4f (&acc)[NT]) {
-    float av = a[0];
-    float bv[NT];
+    for (int kb = 0; kb < kdim; kb += 32) {
+        float av[8], bv[8][NT];
 #pragma unroll
-    for (int u = 0; u < NT; ++u) bv[u] = b[u * bstep];
-    for (int kk = 0; kk < kdim; kk += 4) {
-        const int kn = min(kk + 4, kdim - 4);
-        const float an = a[kn * ak];
-        float bn[NT];
+        for (int st = 0; st < 8; ++st) {
+            const int kk = kb + 4 * st;
+            av[st] = a[kk * ak];
 #pragma unroll
-        for (int u = 0; u < NT; ++u) bn[u] = b[u * bstep + kn * bk];
+            for (int u = 0; u < NT; ++u) bv[st][u] = b[u * bstep + kk * bk];
+        }
 #pragma unroll
-        for (int u = 0; u < NT; ++u)
-            acc[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv[u], acc[u], 0, 0, 0);
-        av = an;
+        for (int st = 0; st < 8; ++st)
 #pragma unroll
-        for (int u = 0; u < NT; ++u) bv[u] = bn[u];
+            for (int u = 0; u < NT; ++u)
+                acc[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[st], bv[st][u], acc[u], 0, 0, 0);
     }
 }
 
