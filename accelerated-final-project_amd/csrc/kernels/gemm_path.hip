@@ -31,8 +31,9 @@
 // workgroups of one head share their Q/K/V panels in that XCD's L2.
 //
 // V enters the second GEMM as the B operand, which MFMA wants contiguous
-// along K (= keys); V rows are contiguous along D, so the V tile is
-// transposed on its way into LDS.
+// along K (= keys); V rows are contiguous along D, so the V tile is stored
+// in LDS as it lies in memory and the MFMA operand is gathered across keys
+// by gfx950's transposing LDS read (ds_read_b64_tr_b16).
 #include "common.hpp"
 #include "launch.hpp"
 
@@ -72,6 +73,23 @@ __device__ __forceinline__ long xcd_tile(long w, long total) {
     const long per = (total + 7) / 8;
     const long t = (w % 8) * per + w / 8;
     return t;  // may be >= total for the last XCD: caller checks
+}
+
+// NN B tile in LDS: [kBK keys][kBN columns], rows unpadded, with the 16-column
+// (32-byte) chunks of key row k permuted by XOR with kNNSwz[k % 4].  The
+// transposing read takes, per 16 lanes, one 32-byte chunk from each of 4
+// consecutive keys (and the next chunk for the next 16 lanes); {0, 2, 5, 7}
+// puts those chunks in distinct banks for 32 or 64 four-byte banks, and the
+// 16-byte row writes stay whole 128 / 256-byte runs.
+__device__ __forceinline__ int nn_lds_off(int k, int n) {
+    const int swz = (0x7520 >> (4 * (k & 3))) & 0xf;  // {0, 2, 5, 7}[k % 4]
+    return k * kBN + ((((n >> 4) ^ swz)) << 4) + (n & 15);
+}
+
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ v4i16 ds_read_tr16(const uint16_t* p) {
+    return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) v4i16*)(p));
 }
 
 // Epilogue selectors
@@ -126,22 +144,21 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm(GemmArgs g) {
     const uint16_t* A = g.A + bh * g.sa;
     const uint16_t* B = g.B + bh * g.sb;
 
-    // ---- global -> register staging: each thread moves two 16-byte chunks
-    // of A (rows m0.., 4 chunks of 8 per row) and, for B^T rows (NT), two
-    // chunks of B; for NN, an 8-key x 2-column block of B (8 dwords), which
-    // it transposes with v_perm_b32 into two 16-byte LDS rows.  Two register
-    // stages rotate with the two LDS buffers, so a step's global loads are
-    // issued two MFMA phases before their data is needed.
-    // A chunk c (0..1023): row = c / 4, k8 = (c % 4) * 8.
+    // ---- global -> register staging: each thread moves 16-byte chunks of A
+    // (rows m0.., kChunkPerRow chunks of 8 per row) and of B: for NT, chunks
+    // of B^T rows, the same way; for NN, chunks of the B rows (keys k0..,
+    // 32 chunks of 8 columns per row), which stay N-contiguous in LDS and are
+    // transposed by the LDS read (ds_read_b64_tr_b16).  A register stage
+    // carries step k + 1 while step k runs its MFMAs.
     constexpr int kChunks = kBM * kBK / 8 / kGemmThreads;  // 16-byte chunks per thread per operand
-    constexpr int kVBlocks = kBK / 8 * (kBN / 2) / kGemmThreads;  // NN: 8x2 blocks per thread
-    static_assert(kChunks >= 1 && kVBlocks >= 1, "tile too small for the thread count");
+    constexpr int kNNChunkPerRow = kBN / 8;
+    static_assert(kChunks >= 1 && kBK * kBN / 8 / kGemmThreads == kChunks,
+                  "tile too small for the thread count");
+    static_assert(kBK * kBN <= kTileElems, "NN B tile does not fit its LDS stage");
     struct Stage {
         uint4 a[kChunks], b[kChunks];
-        uint32_t v[kVBlocks][8];
     };
     Stage st0, st1;
-    // NN block b = tid + u * threads: keys 8 * (b / 128).., columns 2 * (b % 128), +1
     auto load_stage = [&](Stage& r, int k0) {
 #pragma unroll
         for (int u = 0; u < kChunks; ++u) {
@@ -163,19 +180,15 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm(GemmArgs g) {
                     r.b[u] = *reinterpret_cast<const uint4*>(B + (long)gn * g.ldb + gk);
             }
         } else {
-            // B is [K x N]: blocks of 8 consecutive keys x 2 consecutive columns
+            // B is [K x N]: chunk c covers key c / 32, columns (c % 32) * 8 ..
 #pragma unroll
-            for (int u = 0; u < kVBlocks; ++u) {
-                const int blk = tid + u * kGemmThreads;
-                const int vkg = blk / (kBN / 2), vdp = blk % (kBN / 2);
-                const int gn = n0 + 2 * vdp;
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const int gk = k0 + vkg * 8 + e;
-                    r.v[u][e] = 0u;
-                    if (gk < g.K && gn < g.N)
-                        r.v[u][e] = *reinterpret_cast<const uint32_t*>(B + (long)gk * g.ldb + gn);
-                }
+            for (int u = 0; u < kChunks; ++u) {
+                const int cidx = tid + u * kGemmThreads;
+                const int kr = cidx / kNNChunkPerRow, n8 = (cidx % kNNChunkPerRow) * 8;
+                const int gk = k0 + kr, gn = n0 + n8;
+                r.b[u] = make_uint4(0, 0, 0, 0);
+                if (gk < g.K && gn < g.N)
+                    r.b[u] = *reinterpret_cast<const uint4*>(B + (long)gk * g.ldb + gn);
             }
         }
     };
@@ -194,24 +207,11 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm(GemmArgs g) {
                 *reinterpret_cast<uint4*>(&Bs[s][row * kLdsRow + k8]) = r.b[u];
             }
         } else {
-            // v[e] = (B[k_e][n] | B[k_e][n + 1] << 16): gather the low halves
-            // into row n and the high halves into row n + 1 of Bs[n][k]
 #pragma unroll
-            for (int u = 0; u < kVBlocks; ++u) {
-                const int blk = tid + u * kGemmThreads;
-                const int vkg = blk / (kBN / 2), vdp = blk % (kBN / 2);
-                const uint32_t* v = r.v[u];
-                uint4 lo, hi;
-                lo.x = __builtin_amdgcn_perm(v[1], v[0], 0x05040100u);
-                lo.y = __builtin_amdgcn_perm(v[3], v[2], 0x05040100u);
-                lo.z = __builtin_amdgcn_perm(v[5], v[4], 0x05040100u);
-                lo.w = __builtin_amdgcn_perm(v[7], v[6], 0x05040100u);
-                hi.x = __builtin_amdgcn_perm(v[1], v[0], 0x07060302u);
-                hi.y = __builtin_amdgcn_perm(v[3], v[2], 0x07060302u);
-                hi.z = __builtin_amdgcn_perm(v[5], v[4], 0x07060302u);
-                hi.w = __builtin_amdgcn_perm(v[7], v[6], 0x07060302u);
-                *reinterpret_cast<uint4*>(&Bs[s][(2 * vdp) * kLdsRow + vkg * 8]) = lo;
-                *reinterpret_cast<uint4*>(&Bs[s][(2 * vdp + 1) * kLdsRow + vkg * 8]) = hi;
+            for (int u = 0; u < kChunks; ++u) {
+                const int cidx = tid + u * kGemmThreads;
+                const int kr = cidx / kNNChunkPerRow, n8 = (cidx % kNNChunkPerRow) * 8;
+                *reinterpret_cast<uint4*>(&Bs[s][nn_lds_off(kr, n8)]) = r.b[u];
             }
         }
     };
@@ -238,9 +238,26 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm(GemmArgs g) {
                 af[i] = *reinterpret_cast<const uint4*>(
                     &As[s][(wm + i * 32 + lrow) * kLdsRow + ks + lkh]);
 #pragma unroll
-            for (int j = 0; j < TJ; ++j)
-                bfr[j] = *reinterpret_cast<const uint4*>(
-                    &Bs[s][(wn + j * 32 + lrow) * kLdsRow + ks + lkh]);
+            for (int j = 0; j < TJ; ++j) {
+                if constexpr (!B_NN) {
+                    bfr[j] = *reinterpret_cast<const uint4*>(
+                        &Bs[s][(wn + j * 32 + lrow) * kLdsRow + ks + lkh]);
+                } else {
+                    // lane L supplies the address of keys ks + 8 (L / 32) + 4 h +
+                    // (L % 16) / 4, columns wn + 32 j + 16 ((L / 16) % 2) + 4 (L % 4);
+                    // the transposing read hands lane l keys ks + 8 (l / 32) + 4 h
+                    // + 0..3 of column wn + 32 j + l % 32: half h of its operand
+                    const int kr = ks + 8 * (lane >> 5) + ((lane & 15) >> 2);
+                    const int nc = wn + j * 32 + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+                    const v4i16 lo = ds_read_tr16(&Bs[s][nn_lds_off(kr, nc)]);
+                    const v4i16 hi = ds_read_tr16(&Bs[s][nn_lds_off(kr + 4, nc)]);
+                    bfr[j] = make_uint4(
+                        (uint32_t)(uint16_t)lo[0] | ((uint32_t)(uint16_t)lo[1] << 16),
+                        (uint32_t)(uint16_t)lo[2] | ((uint32_t)(uint16_t)lo[3] << 16),
+                        (uint32_t)(uint16_t)hi[0] | ((uint32_t)(uint16_t)hi[1] << 16),
+                        (uint32_t)(uint16_t)hi[2] | ((uint32_t)(uint16_t)hi[3] << 16));
+                }
+            }
 #pragma unroll
             for (int i = 0; i < TI; ++i)
 #pragma unroll
@@ -377,7 +394,8 @@ __global__ __launch_bounds__(256) void k_encode_f16(const uint16_t* __restrict__
     }
 }
 
-// P[row] = bf16(softmax(S[row])) for rows of length Lk; one wave per row.
+// P[row] = bf16(softmax(S[row])) for rows of length Lk; one wave per row,
+// three passes over the row (any Lk).
 __global__ __launch_bounds__(256) void k_softmax_bf(const float* __restrict__ S,
                                                     uint16_t* __restrict__ P, long rows, int Lk) {
     const int lane = threadIdx.x & 63;
@@ -395,14 +413,71 @@ __global__ __launch_bounds__(256) void k_softmax_bf(const float* __restrict__ S,
     for (int j = lane; j < Lk; j += 64) p[j] = f32_to_bf16_bits(__expf(s[j] - m) * inv);
 }
 
-// Register-resident encoder: the row is split into 8-element units (for
+// The same for Lk % 4 == 0 and Lk <= 256 * NV4: the row is read once, with
+// 16-byte loads, and kept in registers (NV4 float4 per lane); P leaves as
+// 8-byte groups of four bf16.
+template <int NV4>
+__global__ __launch_bounds__(256) void k_softmax_bf_regs(const float* __restrict__ S,
+                                                         uint16_t* __restrict__ P, long rows,
+                                                         int Lk) {
+    const int lane = threadIdx.x & 63;
+    const long row = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const float* s = S + row * Lk;
+    float4 x[NV4];
+    float m = -INFINITY;
+#pragma unroll
+    for (int u = 0; u < NV4; ++u) {
+        const int j = (lane + 64 * u) * 4;
+        x[u] = make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+        if (j < Lk) x[u] = *reinterpret_cast<const float4*>(s + j);
+        m = fmaxf(m, fmaxf(fmaxf(x[u].x, x[u].y), fmaxf(x[u].z, x[u].w)));
+    }
+    m = wave_max(m);
+    float l = 0.f;
+#pragma unroll
+    for (int u = 0; u < NV4; ++u) {
+        x[u].x = __expf(x[u].x - m);
+        x[u].y = __expf(x[u].y - m);
+        x[u].z = __expf(x[u].z - m);
+        x[u].w = __expf(x[u].w - m);
+        l += (x[u].x + x[u].y) + (x[u].z + x[u].w);
+    }
+    l = wave_sum(l);
+    const float inv = 1.0f / l;
+    uint16_t* p = P + row * Lk;
+#pragma unroll
+    for (int u = 0; u < NV4; ++u) {
+        const int j = (lane + 64 * u) * 4;
+        if (j < Lk) {
+            uint2 w;
+            w.x = (uint32_t)f32_to_bf16_bits(x[u].x * inv) |
+                  ((uint32_t)f32_to_bf16_bits(x[u].y * inv) << 16);
+            w.y = (uint32_t)f32_to_bf16_bits(x[u].z * inv) |
+                  ((uint32_t)f32_to_bf16_bits(x[u].w * inv) << 16);
+            *reinterpret_cast<uint2*>(p + j) = w;
+        }
+    }
+}
+
+// Register-resident encoder.  The row is split into 8-element units (for
 // rotate-half, unit u < r/16 is paired with its partner unit u + r/16 so both
-// halves of every rotation are in one thread); each thread keeps its units
-// in registers, so the row is read once: 16-byte loads of x, 32-byte loads
-// of the compact cos/sin (or sin/cos) table rows, one block-wide max, then
-// scaled fp16 16-byte stores.
+// halves of every rotation are in one thread) and each thread keeps its units
+// in registers, so a row is read once: 16-byte loads of x, one block-wide
+// max, then scaled fp16 16-byte stores.
+//
+// Rows at the same position (row % seq_len) share their compact table row, so
+// a workgroup takes one position and up to kEncGroup rows at that position
+// (stride seq_len, i.e. the same token of consecutive heads): each thread
+// loads the cos/sin (or sin/cos) values of its units once and applies them to
+// every row of the group, which divides the table traffic (as large as the
+// data itself at fp32) by the group size.  kEncRows rows are in flight at a
+// time.  Workgroup b takes position b % seq_len of group b / seq_len, so
+// concurrently running workgroups stream neighbouring rows of one head.
 constexpr int kEncThreads = 256;
 constexpr int kEncMaxUnits = 4;  // units per thread: D <= 4 * 256 * 8 = 8192
+constexpr int kEncGroup = 8;     // rows (heads) per workgroup sharing one position
+constexpr int kEncRows = 2;      // rows in flight per thread
 
 __device__ __forceinline__ void unpack_bf16x8(const uint4& w, float* v) {
     const uint32_t x[4] = {w.x, w.y, w.z, w.w};
@@ -434,95 +509,134 @@ __device__ __forceinline__ void ld4f(const float* p, float* v) {
     v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
 }
 
-template <int PEK>
+template <int PEK, int U>
 __global__ __launch_bounds__(kEncThreads) void k_encode_f16_regs(const uint16_t* __restrict__ in,
                                                                  uint16_t* __restrict__ out,
                                                                  float* __restrict__ inv,
                                                                  long n_rows, int seq_len, int D,
                                                                  PeSide pe) {
-    __shared__ float red[kEncThreads / 64];
-    const int tid = threadIdx.x;
+    __shared__ float red[2][kEncRows][kEncThreads / 64];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int pos = (int)(blockIdx.x % (unsigned)seq_len);
+    const long h0 = (long)(blockIdx.x / (unsigned)seq_len) * kEncGroup;  // first row group member
+    const long nh = n_rows / seq_len;
+    const int nrow = (int)(nh - h0 < kEncGroup ? nh - h0 : kEncGroup);
     const bool half_pairs = PEK == kPeRopeHalf && pe.on;
-    const int hu = half_pairs ? pe.rotary / 16 : 0;        // paired units (rotate-half)
-    const int nunits = D / 8 - hu;                        // units handled as the "first" of a job
-    for (long row = blockIdx.x; row < n_rows; row += gridDim.x) {
-        const int pos = (int)(row % seq_len);
-        const uint16_t* xr = in + row * D;
-        float v[kEncMaxUnits][2][8];
-        int du[kEncMaxUnits][2];
-        float m = 0.f;
+    const int hu = half_pairs ? pe.rotary / 16 : 0;  // paired units (rotate-half)
+    const int nunits = D / 8 - hu;                    // units handled as the "first" of a job
+
+    // this thread's units and their table values (loaded once per workgroup)
+    int d0[U], d1[U];
+    bool enc[U];
+    float ta[U][8], tb[U][8];
 #pragma unroll
-        for (int k = 0; k < kEncMaxUnits; ++k) {
-            const int job = tid + k * kEncThreads;
-            du[k][0] = du[k][1] = -1;
-            if (job >= nunits) continue;
-            // job -> first unit; rotate-half pairs jobs < hu with unit job + hu
-            const int u0 = (half_pairs && job >= hu) ? job + hu : job;
-            const int d0 = u0 * 8;
-            du[k][0] = d0;
-            unpack_bf16x8(*reinterpret_cast<const uint4*>(xr + d0), v[k][0]);
-            if constexpr (PEK == kPeRopeHalf) {
-                if (half_pairs && job < hu) {
-                    const int d1 = d0 + pe.rotary / 2;
-                    du[k][1] = d1;
-                    unpack_bf16x8(*reinterpret_cast<const uint4*>(xr + d1), v[k][1]);
-                    float c[8], sn[8];
-                    ld8f(pe.a + (size_t)pos * pe.ld + d0, c);
-                    ld8f(pe.b + (size_t)pos * pe.ld + d0, sn);
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) {
-                        const float x0 = v[k][0][e], x1 = v[k][1][e];
-                        v[k][0][e] = rot_first(x0, x1, c[e], sn[e]);
-                        v[k][1][e] = rot_second(x0, x1, c[e], sn[e]);
-                    }
-                }
-            } else if constexpr (PEK == kPeRopeInterleaved) {
-                if (pe.on && d0 < pe.rotary) {
-                    float c[4], sn[4];
-                    ld4f(pe.a + (size_t)pos * pe.ld + d0 / 2, c);
-                    ld4f(pe.b + (size_t)pos * pe.ld + d0 / 2, sn);
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const float x0 = v[k][0][2 * e], x1 = v[k][0][2 * e + 1];
-                        v[k][0][2 * e] = rot_first(x0, x1, c[e], sn[e]);
-                        v[k][0][2 * e + 1] = rot_second(x0, x1, c[e], sn[e]);
-                    }
-                }
-            } else if constexpr (PEK == kPeSinusoidal) {
-                if (pe.on) {
-                    float sv[4], cv[4];
-                    ld4f(pe.a + (size_t)pos * pe.ld + d0 / 2, sv);
-                    ld4f(pe.b + (size_t)pos * pe.ld + d0 / 2, cv);
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        v[k][0][2 * e] = v[k][0][2 * e] + sv[e];
-                        v[k][0][2 * e + 1] = v[k][0][2 * e + 1] + cv[e];
-                    }
-                }
+    for (int k = 0; k < U; ++k) {
+        const int job = tid + k * kEncThreads;
+        d0[k] = d1[k] = -1;
+        enc[k] = false;
+        if (job >= nunits) continue;
+        // job -> first unit; rotate-half pairs jobs < hu with unit job + hu
+        const int u0 = (half_pairs && job >= hu) ? job + hu : job;
+        d0[k] = u0 * 8;
+        if constexpr (PEK == kPeRopeHalf) {
+            if (half_pairs && job < hu) {
+                d1[k] = d0[k] + pe.rotary / 2;
+                enc[k] = true;
+                ld8f(pe.a + (size_t)pos * pe.ld + d0[k], ta[k]);
+                ld8f(pe.b + (size_t)pos * pe.ld + d0[k], tb[k]);
             }
-#pragma unroll
-            for (int h = 0; h < 2; ++h)
-                if (du[k][h] >= 0)
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) m = fmaxf(m, fabsf(v[k][h][e]));
+        } else if constexpr (PEK == kPeRopeInterleaved) {
+            if (pe.on && d0[k] < pe.rotary) {
+                enc[k] = true;
+                ld4f(pe.a + (size_t)pos * pe.ld + d0[k] / 2, ta[k]);
+                ld4f(pe.b + (size_t)pos * pe.ld + d0[k] / 2, tb[k]);
+            }
+        } else if constexpr (PEK == kPeSinusoidal) {
+            if (pe.on) {
+                enc[k] = true;
+                ld4f(pe.a + (size_t)pos * pe.ld + d0[k] / 2, ta[k]);
+                ld4f(pe.b + (size_t)pos * pe.ld + d0[k] / 2, tb[k]);
+            }
         }
-        m = wave_max(m);
-        if ((tid & 63) == 0) red[tid >> 6] = m;
+    }
+
+    for (int i = 0; i < nrow; i += kEncRows) {
+        const int par = (i / kEncRows) & 1;  // red[] parity: one barrier per batch of rows
+        float v[kEncRows][U][2][8];
+        // all loads of the batch first
+#pragma unroll
+        for (int rr = 0; rr < kEncRows; ++rr) {
+            if (i + rr >= nrow) continue;
+            const uint16_t* xr = in + ((h0 + i + rr) * seq_len + pos) * D;
+#pragma unroll
+            for (int k = 0; k < U; ++k) {
+                if (d0[k] >= 0) unpack_bf16x8(*reinterpret_cast<const uint4*>(xr + d0[k]), v[rr][k][0]);
+                if (d1[k] >= 0) unpack_bf16x8(*reinterpret_cast<const uint4*>(xr + d1[k]), v[rr][k][1]);
+            }
+        }
+        float m[kEncRows];
+#pragma unroll
+        for (int rr = 0; rr < kEncRows; ++rr) {
+            m[rr] = 0.f;
+            if (i + rr >= nrow) continue;
+#pragma unroll
+            for (int k = 0; k < U; ++k) {
+                if (d0[k] < 0) continue;
+                float(&x)[2][8] = v[rr][k];
+                if (enc[k]) {
+                    if constexpr (PEK == kPeRopeHalf) {
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) {
+                            const float x0 = x[0][e], x1 = x[1][e];
+                            x[0][e] = rot_first(x0, x1, ta[k][e], tb[k][e]);
+                            x[1][e] = rot_second(x0, x1, ta[k][e], tb[k][e]);
+                        }
+                    } else if constexpr (PEK == kPeRopeInterleaved) {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const float x0 = x[0][2 * e], x1 = x[0][2 * e + 1];
+                            x[0][2 * e] = rot_first(x0, x1, ta[k][e], tb[k][e]);
+                            x[0][2 * e + 1] = rot_second(x0, x1, ta[k][e], tb[k][e]);
+                        }
+                    } else if constexpr (PEK == kPeSinusoidal) {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            x[0][2 * e] = x[0][2 * e] + ta[k][e];
+                            x[0][2 * e + 1] = x[0][2 * e + 1] + tb[k][e];
+                        }
+                    }
+                }
+#pragma unroll
+                for (int e = 0; e < 8; ++e) m[rr] = fmaxf(m[rr], fabsf(x[0][e]));
+                if (d1[k] >= 0)
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) m[rr] = fmaxf(m[rr], fabsf(x[1][e]));
+            }
+        }
+#pragma unroll
+        for (int rr = 0; rr < kEncRows; ++rr) {
+            m[rr] = wave_max(m[rr]);
+            if (lane == 0) red[par][rr][wave] = m[rr];
+        }
         __syncthreads();
-        m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-        __syncthreads();  // red is reused by the next row
-        int kexp = 0;
-        if (m > 0.f && m <= 3.0e38f) kexp = 14 - ilogbf(m);
-        kexp = max(-100, min(100, kexp));
-        const float up = ldexpf(1.0f, kexp);
-        if (tid == 0) inv[row] = ldexpf(1.0f, -kexp);
-        uint16_t* yr = out + row * D;
 #pragma unroll
-        for (int k = 0; k < kEncMaxUnits; ++k)
+        for (int rr = 0; rr < kEncRows; ++rr) {
+            if (i + rr >= nrow) continue;
+            const float mr = fmaxf(fmaxf(red[par][rr][0], red[par][rr][1]),
+                                   fmaxf(red[par][rr][2], red[par][rr][3]));
+            int kexp = 0;
+            if (mr > 0.f && mr <= 3.0e38f) kexp = 14 - ilogbf(mr);
+            kexp = max(-100, min(100, kexp));
+            const float up = ldexpf(1.0f, kexp);
+            const long row = (h0 + i + rr) * seq_len + pos;
+            if (tid == 0) inv[row] = ldexpf(1.0f, -kexp);
+            uint16_t* yr = out + row * D;
 #pragma unroll
-            for (int h = 0; h < 2; ++h)
-                if (du[k][h] >= 0)
-                    *reinterpret_cast<uint4*>(yr + du[k][h]) = pack_f16x8(v[k][h], up);
+            for (int k = 0; k < U; ++k) {
+                if (d0[k] >= 0) *reinterpret_cast<uint4*>(yr + d0[k]) = pack_f16x8(v[rr][k][0], up);
+                if (d1[k] >= 0) *reinterpret_cast<uint4*>(yr + d1[k]) = pack_f16x8(v[rr][k][1], up);
+            }
+        }
     }
 }
 
@@ -561,32 +675,50 @@ hipError_t launch_gemm_qk(int f16, const uint16_t* Q, const uint16_t* K, const f
     return hipGetLastError();
 }
 
+template <int PEK>
+static void launch_encode_regs(int units, const uint16_t* in, uint16_t* out, float* inv,
+                               long n_rows, int seq_len, int D, const PeSide& pe, hipStream_t st) {
+    const long groups = (n_rows / seq_len + kEncGroup - 1) / kEncGroup;
+    const dim3 grid((unsigned)(groups * seq_len)), block(kEncThreads);
+    if (units <= 1)
+        hipLaunchKernelGGL((k_encode_f16_regs<PEK, 1>), grid, block, 0, st, in, out, inv, n_rows,
+                           seq_len, D, pe);
+    else if (units == 2)
+        hipLaunchKernelGGL((k_encode_f16_regs<PEK, 2>), grid, block, 0, st, in, out, inv, n_rows,
+                           seq_len, D, pe);
+    else
+        hipLaunchKernelGGL((k_encode_f16_regs<PEK, 4>), grid, block, 0, st, in, out, inv, n_rows,
+                           seq_len, D, pe);
+}
+
 hipError_t launch_encode_f16(int pek, const uint16_t* in, uint16_t* out, float* inv, long n_rows,
                              int seq_len, int D, const PeSide& pe, hipStream_t st) {
     const long grid = n_rows < 65536 ? n_rows : 65536;
     // register-resident form: D % 8 == 0, D <= 8192, the library's compact
-    // tables, and a rotary width that keeps 8-element units whole
+    // tables, a rotary width that keeps 8-element units whole, and rows that
+    // are whole sequences (n_rows a multiple of seq_len)
     const bool rope = pek == kPeRopeInterleaved || pek == kPeRopeHalf;
-    const bool fast = D % 8 == 0 && D <= kEncMaxUnits * kEncThreads * 8 &&
+    const bool fast = D % 8 == 0 && D <= kEncMaxUnits * kEncThreads * 8 && seq_len > 0 &&
+                      n_rows % seq_len == 0 &&
                       (pek == kPeNone || !pe.on || (pe.dup == 0 && pe.ld % 4 == 0)) &&
                       (!rope || !pe.on || pe.rotary % (pek == kPeRopeHalf ? 16 : 8) == 0);
     if (fast) {
+        const int hu = (pek == kPeRopeHalf && pe.on) ? pe.rotary / 16 : 0;
+        const int jobs = D / 8 - hu;
+        const int units = (jobs + kEncThreads - 1) / kEncThreads;
         switch (pek) {
             case kPeNone:
-                hipLaunchKernelGGL((k_encode_f16_regs<kPeNone>), dim3((unsigned)grid),
-                                   dim3(kEncThreads), 0, st, in, out, inv, n_rows, seq_len, D, pe);
+                launch_encode_regs<kPeNone>(units, in, out, inv, n_rows, seq_len, D, pe, st);
                 break;
             case kPeRopeInterleaved:
-                hipLaunchKernelGGL((k_encode_f16_regs<kPeRopeInterleaved>), dim3((unsigned)grid),
-                                   dim3(kEncThreads), 0, st, in, out, inv, n_rows, seq_len, D, pe);
+                launch_encode_regs<kPeRopeInterleaved>(units, in, out, inv, n_rows, seq_len, D, pe,
+                                                       st);
                 break;
             case kPeRopeHalf:
-                hipLaunchKernelGGL((k_encode_f16_regs<kPeRopeHalf>), dim3((unsigned)grid),
-                                   dim3(kEncThreads), 0, st, in, out, inv, n_rows, seq_len, D, pe);
+                launch_encode_regs<kPeRopeHalf>(units, in, out, inv, n_rows, seq_len, D, pe, st);
                 break;
             case kPeSinusoidal:
-                hipLaunchKernelGGL((k_encode_f16_regs<kPeSinusoidal>), dim3((unsigned)grid),
-                                   dim3(kEncThreads), 0, st, in, out, inv, n_rows, seq_len, D, pe);
+                launch_encode_regs<kPeSinusoidal>(units, in, out, inv, n_rows, seq_len, D, pe, st);
                 break;
             default:
                 return hipErrorInvalidValue;
@@ -617,8 +749,19 @@ hipError_t launch_encode_f16(int pek, const uint16_t* in, uint16_t* out, float* 
 }
 
 hipError_t launch_softmax_bf16(const float* S, uint16_t* P, long rows, int Lk, hipStream_t st) {
-    const long grid = (rows + 3) / 4;
-    hipLaunchKernelGGL(k_softmax_bf, dim3((unsigned)grid), dim3(256), 0, st, S, P, rows, Lk);
+    const dim3 grid((unsigned)((rows + 3) / 4)), block(256);
+    if (Lk % 4 != 0 || Lk > 256 * 16)
+        hipLaunchKernelGGL(k_softmax_bf, grid, block, 0, st, S, P, rows, Lk);
+    else if (Lk <= 256)
+        hipLaunchKernelGGL(k_softmax_bf_regs<1>, grid, block, 0, st, S, P, rows, Lk);
+    else if (Lk <= 512)
+        hipLaunchKernelGGL(k_softmax_bf_regs<2>, grid, block, 0, st, S, P, rows, Lk);
+    else if (Lk <= 1024)
+        hipLaunchKernelGGL(k_softmax_bf_regs<4>, grid, block, 0, st, S, P, rows, Lk);
+    else if (Lk <= 2048)
+        hipLaunchKernelGGL(k_softmax_bf_regs<8>, grid, block, 0, st, S, P, rows, Lk);
+    else
+        hipLaunchKernelGGL(k_softmax_bf_regs<16>, grid, block, 0, st, S, P, rows, Lk);
     return hipGetLastError();
 }
 
