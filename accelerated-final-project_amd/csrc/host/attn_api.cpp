@@ -386,6 +386,10 @@ GemmPlan gemm_plan(int dtype, const Shape& s, const PePlan& plan) {
     if (dtype != ATN_DTYPE_BF16 || s.Lq < kGemmMinL || s.Lk < kGemmMinL || s.D % 8 != 0 ||
         s.Lk % 8 != 0)
         return p;
+    // the GEMM kernels address one head's matrix with 32-bit element offsets
+    const int64_t lim = (int64_t)1 << 31;
+    if ((int64_t)s.Lq * s.D >= lim || (int64_t)s.Lk * s.D >= lim || (int64_t)s.Lq * s.Lk >= lim)
+        return p;
     size_t off = kSyncBytes;
     auto take = [&](size_t b) { size_t o = off; off += round256(b); return o; };
     // with a positional encoding both sides are re-encoded as scaled fp16

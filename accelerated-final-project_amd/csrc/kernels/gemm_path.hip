@@ -22,10 +22,11 @@
 // GEMM epilogue multiplies the row and column scales back (exactly).
 //
 // Both GEMMs use 256 x 256 output tiles per workgroup of 512 threads (8
-// waves, each 64 x 128 = 2 x 4 tiles of
-// v_mfma_f32_32x32x16_{f16,bf16}), a K step of 64 with the global loads of
-// step k + 1 in flight while step k runs its MFMAs (double-buffered LDS,
-// 144 KiB), and an
+// waves, each 64 x 128 (NT) or 128 x 64 (NN) = 8 tiles of
+// v_mfma_f32_32x32x16_{f16,bf16}), a K step of 64 in double-buffered LDS
+// (144 KiB) fed from a register stage two steps ahead, a software-pipelined
+// step (fragment reads, LDS writes and global loads interleaved with the
+// MFMAs, one barrier per step), and an
 // XCD-aware tile order: consecutive tile indices run on the same XCD
 // (workgroups are dealt round-robin to the 8 XCDs), so concurrent
 // workgroups of one head share their Q/K/V panels in that XCD's L2.
@@ -47,10 +48,10 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
 constexpr int kBM = 256, kBN = 256, kBK = 64;
 constexpr int kGemmThreads = 512;            // 8 waves
-constexpr int kWavesN = 2;                   // wave grid: (8 / kWavesN) x kWavesN
-constexpr int kTI = kBM / (kGemmThreads / 64 / kWavesN) / 32;  // 32x32 tiles per wave (rows)
-constexpr int kTJ = kBN / kWavesN / 32;                        // (columns)
-constexpr int kDepth = 1;                    // register stages of global prefetch (1 or 2)
+// wave grid (8 / waves_n) x waves_n: NT 4 x 2 (waves of 64 x 128), NN 2 x 4
+// (128 x 64: four P fragments and two transposed V fragments per sub-step)
+template <bool B_NN>
+constexpr int waves_n() { return B_NN ? 4 : 2; }
 constexpr int kLdsRow = kBK + 8;  // 16-bit elements per LDS row (16-byte aligned, padded)
 constexpr int kTileElems = kBM * kLdsRow;
 constexpr int kChunkPerRow = kBK / 8;
@@ -90,6 +91,25 @@ typedef short v4i16 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ v4i16 ds_read_tr16(const uint16_t* p) {
     return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
         (__attribute__((address_space(3))) v4i16*)(p));
+}
+
+// Scheduling pattern for one sub-step: MFMA, then fragment reads, six times;
+// the R reads are spread as evenly as possible (mask 0x008 = MFMA,
+// 0x100 = LDS read).
+template <int R>
+__device__ __forceinline__ void sched_mfma_reads() {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, R / 6 + (0 < R % 6 ? 1 : 0), 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, R / 6 + (1 < R % 6 ? 1 : 0), 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, R / 6 + (2 < R % 6 ? 1 : 0), 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, R / 6 + (3 < R % 6 ? 1 : 0), 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, R / 6 + (4 < R % 6 ? 1 : 0), 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, R / 6 + (5 < R % 6 ? 1 : 0), 0);
 }
 
 // Epilogue selectors
@@ -148,8 +168,7 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm(GemmArgs g) {
     // (rows m0.., kChunkPerRow chunks of 8 per row) and of B: for NT, chunks
     // of B^T rows, the same way; for NN, chunks of the B rows (keys k0..,
     // 32 chunks of 8 columns per row), which stay N-contiguous in LDS and are
-    // transposed by the LDS read (ds_read_b64_tr_b16).  A register stage
-    // carries step k + 1 while step k runs its MFMAs.
+    // transposed by the LDS read (ds_read_b64_tr_b16).
     constexpr int kChunks = kBM * kBK / 8 / kGemmThreads;  // 16-byte chunks per thread per operand
     constexpr int kNNChunkPerRow = kBN / 8;
     static_assert(kChunks >= 1 && kBK * kBN / 8 / kGemmThreads == kChunks,
@@ -158,37 +177,37 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm(GemmArgs g) {
     struct Stage {
         uint4 a[kChunks], b[kChunks];
     };
-    Stage st0, st1;
-    auto load_stage = [&](Stage& r, int k0) {
+    // A tile that lies inside the matrices (EDGE false) loads without bounds
+    // checks: straight-line code that the scheduler can spread among the
+    // MFMAs.  Edge tiles zero-fill what lies outside.
+    // Offsets within one head's matrix are 32-bit (the host keeps every
+    // per-head matrix below 2^31 elements): a uniform base plus a per-lane
+    // 32-bit offset is the global_load form with the base in SGPRs.
+    auto load_chunk = [&](const uint16_t* base, long ld, int r, int c, int rmax, int cmax,
+                          auto edge) -> uint4 {
+        if constexpr (decltype(edge)::value) {
+            if (r >= rmax || c >= cmax) return make_uint4(0, 0, 0, 0);
+        }
+        const uint32_t off = (uint32_t)r * (uint32_t)ld + (uint32_t)c;
+        return *reinterpret_cast<const uint4*>(base + off);
+    };
+    auto load_stage = [&](Stage& r, int k0, auto edge) {
 #pragma unroll
         for (int u = 0; u < kChunks; ++u) {
             const int cidx = tid + u * kGemmThreads;
             const int row = cidx / kChunkPerRow, k8 = (cidx % kChunkPerRow) * 8;
-            const int gm = m0 + row, gk = k0 + k8;
-            r.a[u] = make_uint4(0, 0, 0, 0);
-            if (gm < g.M && gk < g.K)
-                r.a[u] = *reinterpret_cast<const uint4*>(A + (long)gm * g.lda + gk);
+            r.a[u] = load_chunk(A, g.lda, m0 + row, k0 + k8, g.M, g.K, edge);
         }
-        if constexpr (!B_NN) {
 #pragma unroll
-            for (int u = 0; u < kChunks; ++u) {
-                const int cidx = tid + u * kGemmThreads;
+        for (int u = 0; u < kChunks; ++u) {
+            const int cidx = tid + u * kGemmThreads;
+            if constexpr (!B_NN) {
                 const int row = cidx / kChunkPerRow, k8 = (cidx % kChunkPerRow) * 8;
-                const int gn = n0 + row, gk = k0 + k8;
-                r.b[u] = make_uint4(0, 0, 0, 0);
-                if (gn < g.N && gk < g.K)
-                    r.b[u] = *reinterpret_cast<const uint4*>(B + (long)gn * g.ldb + gk);
-            }
-        } else {
-            // B is [K x N]: chunk c covers key c / 32, columns (c % 32) * 8 ..
-#pragma unroll
-            for (int u = 0; u < kChunks; ++u) {
-                const int cidx = tid + u * kGemmThreads;
+                r.b[u] = load_chunk(B, g.ldb, n0 + row, k0 + k8, g.N, g.K, edge);
+            } else {
+                // B is [K x N]: chunk c covers key c / 32, columns (c % 32) * 8 ..
                 const int kr = cidx / kNNChunkPerRow, n8 = (cidx % kNNChunkPerRow) * 8;
-                const int gk = k0 + kr, gn = n0 + n8;
-                r.b[u] = make_uint4(0, 0, 0, 0);
-                if (gk < g.K && gn < g.N)
-                    r.b[u] = *reinterpret_cast<const uint4*>(B + (long)gk * g.ldb + gn);
+                r.b[u] = load_chunk(B, g.ldb, k0 + kr, n0 + n8, g.K, g.N, edge);
             }
         }
     };
@@ -199,26 +218,23 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm(GemmArgs g) {
             const int row = cidx / kChunkPerRow, k8 = (cidx % kChunkPerRow) * 8;
             *reinterpret_cast<uint4*>(&As[s][row * kLdsRow + k8]) = r.a[u];
         }
-        if constexpr (!B_NN) {
 #pragma unroll
-            for (int u = 0; u < kChunks; ++u) {
-                const int cidx = tid + u * kGemmThreads;
+        for (int u = 0; u < kChunks; ++u) {
+            const int cidx = tid + u * kGemmThreads;
+            if constexpr (!B_NN) {
                 const int row = cidx / kChunkPerRow, k8 = (cidx % kChunkPerRow) * 8;
                 *reinterpret_cast<uint4*>(&Bs[s][row * kLdsRow + k8]) = r.b[u];
-            }
-        } else {
-#pragma unroll
-            for (int u = 0; u < kChunks; ++u) {
-                const int cidx = tid + u * kGemmThreads;
+            } else {
                 const int kr = cidx / kNNChunkPerRow, n8 = (cidx % kNNChunkPerRow) * 8;
                 *reinterpret_cast<uint4*>(&Bs[s][nn_lds_off(kr, n8)]) = r.b[u];
             }
         }
     };
 
-    // ---- wave tile: 128 x 128 = 4 x 4 MFMA tiles of 32 x 32
-    constexpr int TI = kTI, TJ = kTJ;
-    const int wm = (wave / kWavesN) * (TI * 32), wn = (wave % kWavesN) * (TJ * 32);
+    // ---- wave tile: TI x TJ MFMA tiles of 32 x 32
+    constexpr int WN = waves_n<B_NN>();
+    constexpr int TI = kBM / (kGemmThreads / 64 / WN) / 32, TJ = kBN / WN / 32;
+    const int wm = (wave / WN) * (TI * 32), wn = (wave % WN) * (TJ * 32);
     v16f acc[TI][TJ];
 #pragma unroll
     for (int i = 0; i < TI; ++i)
@@ -227,103 +243,153 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm(GemmArgs g) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
+    // MFMA operands of one 16-wide sub-step
+    struct Frag {
+        uint4 a[TI], b[TJ];
+    };
     const int lrow = lane & 31, lkh = (lane >> 5) * 8;
-    const int nk = (g.K + kBK - 1) / kBK;
-    auto compute = [&](int s) {
+    auto read_frag = [&](Frag& f, int s, int ks) {
 #pragma unroll
-        for (int ks = 0; ks < kBK; ks += 16) {
-            uint4 af[TI], bfr[TJ];
+        for (int i = 0; i < TI; ++i)
+            f.a[i] = *reinterpret_cast<const uint4*>(&As[s][(wm + i * 32 + lrow) * kLdsRow + ks + lkh]);
 #pragma unroll
-            for (int i = 0; i < TI; ++i)
-                af[i] = *reinterpret_cast<const uint4*>(
-                    &As[s][(wm + i * 32 + lrow) * kLdsRow + ks + lkh]);
-#pragma unroll
-            for (int j = 0; j < TJ; ++j) {
-                if constexpr (!B_NN) {
-                    bfr[j] = *reinterpret_cast<const uint4*>(
-                        &Bs[s][(wn + j * 32 + lrow) * kLdsRow + ks + lkh]);
-                } else {
-                    // lane L supplies the address of keys ks + 8 (L / 32) + 4 h +
-                    // (L % 16) / 4, columns wn + 32 j + 16 ((L / 16) % 2) + 4 (L % 4);
-                    // the transposing read hands lane l keys ks + 8 (l / 32) + 4 h
-                    // + 0..3 of column wn + 32 j + l % 32: half h of its operand
-                    const int kr = ks + 8 * (lane >> 5) + ((lane & 15) >> 2);
-                    const int nc = wn + j * 32 + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
-                    const v4i16 lo = ds_read_tr16(&Bs[s][nn_lds_off(kr, nc)]);
-                    const v4i16 hi = ds_read_tr16(&Bs[s][nn_lds_off(kr + 4, nc)]);
-                    bfr[j] = make_uint4(
-                        (uint32_t)(uint16_t)lo[0] | ((uint32_t)(uint16_t)lo[1] << 16),
-                        (uint32_t)(uint16_t)lo[2] | ((uint32_t)(uint16_t)lo[3] << 16),
-                        (uint32_t)(uint16_t)hi[0] | ((uint32_t)(uint16_t)hi[1] << 16),
-                        (uint32_t)(uint16_t)hi[2] | ((uint32_t)(uint16_t)hi[3] << 16));
-                }
+        for (int j = 0; j < TJ; ++j) {
+            if constexpr (!B_NN) {
+                f.b[j] = *reinterpret_cast<const uint4*>(
+                    &Bs[s][(wn + j * 32 + lrow) * kLdsRow + ks + lkh]);
+            } else {
+                // lane L supplies the address of keys ks + 8 (L / 32) + 4 h +
+                // (L % 16) / 4, columns wn + 32 j + 16 ((L / 16) % 2) + 4 (L % 4);
+                // the transposing read hands lane l keys ks + 8 (l / 32) + 4 h
+                // + 0..3 of column wn + 32 j + l % 32: half h of its operand
+                const int kr = ks + 8 * (lane >> 5) + ((lane & 15) >> 2);
+                const int nc = wn + j * 32 + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+                const v4i16 lo = ds_read_tr16(&Bs[s][nn_lds_off(kr, nc)]);
+                const v4i16 hi = ds_read_tr16(&Bs[s][nn_lds_off(kr + 4, nc)]);
+                const uint2 l2 = __builtin_bit_cast(uint2, lo), h2 = __builtin_bit_cast(uint2, hi);
+                f.b[j] = make_uint4(l2.x, l2.y, h2.x, h2.y);
             }
-#pragma unroll
-            for (int i = 0; i < TI; ++i)
-#pragma unroll
-                for (int j = 0; j < TJ; ++j) acc[i][j] = mfma_32x32x16<F16>(af[i], bfr[j], acc[i][j]);
         }
     };
-
-    if constexpr (kDepth == 1) {
-        // one register stage: step kt + 1's loads fly during step kt's MFMAs
-        load_stage(st0, 0);
-        store_stage(st0, 0);
-        __syncthreads();
-        for (int kt = 0; kt < nk; ++kt) {
-            const int sb = kt & 1;
-            if (kt + 1 < nk) load_stage(st0, (kt + 1) * kBK);
-            compute(sb);
-            if (kt + 1 < nk) store_stage(st0, sb ^ 1);
-            __syncthreads();
-        }
-    } else {
-        // two register stages: step kt reads LDS buffer kt % 2 while register
-        // stage (kt % 2) carries step kt + 2
-        load_stage(st0, 0);
-        if (nk > 1) load_stage(st1, kBK);
-        store_stage(st0, 0);
-        __syncthreads();
-        for (int kt = 0; kt < nk; kt += 2) {
-            if (kt + 2 < nk) load_stage(st0, (kt + 2) * kBK);
-            compute(0);
-            if (kt + 1 < nk) store_stage(st1, 1);
-            __syncthreads();
-            if (kt + 1 >= nk) break;
-            if (kt + 3 < nk) load_stage(st1, (kt + 3) * kBK);
-            compute(1);
-            if (kt + 2 < nk) store_stage(st0, 0);
-            __syncthreads();
-        }
-    }
-
-    // ---- epilogue: lane holds column (lane % 32) and rows
-    // 8 * (r / 4) + 4 * (lane / 32) + r % 4 of each 32 x 32 tile.
-    // bf16 output goes through LDS (the operand buffers are free now) and
-    // leaves as 16-byte row chunks.
-    if constexpr (OUT == kOutBf16) {
-        uint16_t* Ct = lds;  // 256 x (256 + 8) bf16 staging tile
-        constexpr int kCRow = kBN + 8;
-        static_assert(kBM * kCRow <= 4 * kTileElems, "output staging does not fit");
+    // NN runs the product transposed, acc[i][j] = (B^T A^T) tile: its
+    // accumulator rows are output columns, so each lane ends up with four
+    // consecutive output columns of one output row (see the epilogue)
+    auto mma = [&](const Frag& f) {
 #pragma unroll
         for (int i = 0; i < TI; ++i)
 #pragma unroll
             for (int j = 0; j < TJ; ++j) {
-                const int col = wn + j * 32 + (lane & 31);
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int row = wm + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                    Ct[row * kCRow + col] = f32_to_bf16_bits(acc[i][j][r]);
-                }
+                if constexpr (B_NN)
+                    acc[i][j] = mfma_32x32x16<F16>(f.b[j], f.a[i], acc[i][j]);
+                else
+                    acc[i][j] = mfma_32x32x16<F16>(f.a[i], f.b[j], acc[i][j]);
             }
+    };
+
+    // ---- K loop, software-pipelined over the four 16-wide sub-steps of a
+    // step: sub-step q + 1's fragments are read while sub-step q's MFMAs run;
+    // step kt + 1's tile (in registers since step kt - 1) goes to the other
+    // LDS buffer during sub-step 0, and step kt + 2's global loads are issued
+    // during sub-step 1, a whole step ahead of their use; the one barrier per
+    // step sits before sub-step 3's MFMAs, so the first fragments of step
+    // kt + 1 are read while those run.  Buffer kt % 2 is rewritten only in
+    // step kt + 1, after every wave passed the barrier that ends its reads.
+    // The last two steps are peeled (no store / no load), so the steady-state
+    // step is one basic block, and sched_group_barrier interleaves its LDS
+    // and global memory instructions one or two at a time between the MFMAs.
+    const int nk = (g.K + kBK - 1) / kBK;
+    constexpr int kReads = TI + (B_NN ? 2 : 1) * TJ;  // LDS reads per fragment set
+    constexpr int kMfma = TI * TJ;                    // MFMAs per sub-step
+    static_assert(kMfma >= 8 && kReads <= 12, "interleave pattern assumes 8 MFMAs per sub-step");
+    auto sched_reads = [&]() { sched_mfma_reads<kReads>(); };
+    Stage st;
+    Frag f0, f1;
+    auto step = [&](int kt, auto next, auto next2, auto edge) {
+        constexpr bool N1 = decltype(next)::value, N2 = decltype(next2)::value;
+        const int s = kt & 1;
+        // sub-step 0: MFMAs on f0, read f1, write step kt + 1's tile
+        read_frag(f1, s, 16);
+        mma(f0);
+        if constexpr (N1) store_stage(st, s ^ 1);
+        sched_reads();
+        if constexpr (N1) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x200, kChunks, 0);  // DS write
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x200, kChunks, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        // sub-step 1: MFMAs on f1, read f0, global loads of step kt + 2
+        if constexpr (N2) load_stage(st, (kt + 2) * kBK, edge);
+        read_frag(f0, s, 32);
+        mma(f1);
+        sched_reads();
+        if constexpr (N2) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x020, kChunks, 0);  // VMEM read
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x020, kChunks, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        // sub-step 2: MFMAs on f0, read f1
+        read_frag(f1, s, 48);
+        mma(f0);
+        sched_reads();
+        __builtin_amdgcn_sched_barrier(0);
         __syncthreads();
+        // sub-step 3: MFMAs on f1, read step kt + 1's first fragments
+        if constexpr (N1) read_frag(f0, s ^ 1, 0);
+        mma(f1);
+        if constexpr (N1) sched_reads();
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    auto kloop = [&](auto edge) {
+        using T = std::integral_constant<bool, true>;
+        using F = std::integral_constant<bool, false>;
+        load_stage(st, 0, edge);
+        store_stage(st, 0);
+        if (nk > 1) load_stage(st, kBK, edge);
+        __syncthreads();
+        read_frag(f0, 0, 0);
+        int kt = 0;
+        for (; kt + 2 < nk; ++kt) step(kt, T{}, T{}, edge);
+        if (kt + 1 < nk) {
+            step(kt, T{}, F{}, edge);
+            ++kt;
+        }
+        step(kt, F{}, F{}, edge);
+    };
+    if (m0 + kBM <= g.M && n0 + kBN <= g.N && g.K % kBK == 0)
+        kloop(std::integral_constant<bool, false>{});
+    else
+        kloop(std::integral_constant<bool, true>{});
+
+    // ---- epilogue.  NT: lane holds column (lane % 32) and rows
+    // 8 * (r / 4) + 4 * (lane / 32) + r % 4 of each 32 x 32 tile.
+    // NN (transposed product): lane holds output row m0 + wm + 32 i + lane % 32
+    // and columns n0 + wn + 32 j + 8 * (r / 4) + 4 * (lane / 32) + r % 4, i.e.
+    // four consecutive bf16 per group of four r, stored as one 8-byte word
+    // (N is a multiple of 4, so a group is wholly inside or outside).
+    if constexpr (OUT == kOutBf16) {
+        static_assert(B_NN, "bf16 output comes from the NN product");
         uint16_t* C = static_cast<uint16_t*>(g.C) + bh * g.sc;
-        for (int cidx = tid; cidx < kBM * kBN / 8; cidx += kGemmThreads) {
-            const int row = cidx / (kBN / 8), c8 = (cidx % (kBN / 8)) * 8;
-            const int grow = m0 + row, gcol = n0 + c8;
-            if (grow < g.M && gcol < g.N)
-                *reinterpret_cast<uint4*>(C + (long)grow * g.ldc + gcol) =
-                    *reinterpret_cast<const uint4*>(&Ct[row * kCRow + c8]);
+#pragma unroll
+        for (int i = 0; i < TI; ++i) {
+            const int row = m0 + wm + i * 32 + (lane & 31);
+            if (row >= g.M) continue;
+#pragma unroll
+            for (int j = 0; j < TJ; ++j)
+#pragma unroll
+                for (int rg = 0; rg < 4; ++rg) {
+                    const int col = n0 + wn + j * 32 + 8 * rg + 4 * (lane >> 5);
+                    if (col >= g.N) continue;
+                    uint2 w;
+                    w.x = (uint32_t)f32_to_bf16_bits(acc[i][j][4 * rg]) |
+                          ((uint32_t)f32_to_bf16_bits(acc[i][j][4 * rg + 1]) << 16);
+                    w.y = (uint32_t)f32_to_bf16_bits(acc[i][j][4 * rg + 2]) |
+                          ((uint32_t)f32_to_bf16_bits(acc[i][j][4 * rg + 3]) << 16);
+                    *reinterpret_cast<uint2*>(C + (long)row * g.ldc + col) = w;
+                }
         }
         return;
     }
