@@ -120,9 +120,8 @@ struct Table {
 };
 
 // Library-managed scratch, one per (device, stream) so that calls on
-// different streams never share partial results or barrier counters.  It is
-// zero-filled when allocated; every call leaves its synchronization words at
-// zero again.
+// different streams never share partial results or epoch words.  It is
+// zero-filled when allocated.
 struct Workspace {
     void* ptr = nullptr;
     size_t bytes = 0;
@@ -295,12 +294,12 @@ int ensure_workspace(size_t bytes, hipStream_t stream, void** ws) {
 
 // ---------------------------------------------------------------- fused plan
 // Workspace layout (every path): a fixed 32 KiB sync region -- [0, 4) the
-// status word, [256, 8448) one epoch word per head, [8448, 24832) one 64-bit
-// barrier flag per workgroup of the single-launch kernel -- then float
-// scratch.  Fixed offsets keep the barrier words of one call from landing
-// on another call's words when shapes change between calls.
+// status word, [256, 8448) one epoch word per row group of the
+// single-launch kernel, [8448, 24832) two sets of 2048 per-workgroup done
+// words -- then scratch.  Fixed offsets keep the epoch words of one call
+// from landing elsewhere when shapes change between calls.
 constexpr size_t kSyncEpochOff = 256;
-constexpr size_t kSyncFlagOff = 8448;
+constexpr size_t kSyncDoneOff = 8448;
 constexpr int kSyncMaxWorkgroups = 2048;
 constexpr size_t kSyncBytes = 32768;
 
@@ -308,30 +307,55 @@ size_t round256(size_t b) { return (b + 255) / 256 * 256; }
 
 struct FusedPlan {
     bool ok = false;
-    int dc = 0, nchunk = 0, lds = 0;
-    size_t part_elems = 0, red_elems = 0, bytes = 0;
+    int MB = 0, dc = 0, nchunk = 0, lds = 0, gather1 = 0, workgroups = 0;
+    size_t part_words = 0, red_words = 0, bytes = 0;
 };
 
 constexpr int kFusedMaxLq = 64, kFusedMaxLk = 128;
 constexpr int kLdsLimit = 160 * 1024 - 256;
+constexpr int kFusedThreads = 256, kFusedMaxWords = 64;
 
-// Cut each head's D into slices so that about one workgroup per CU runs and
-// the whole grid is resident at once (the kernel's barriers need that).
-// Capacity is the device's CU count x resident workgroups per CU for the
-// chosen LDS size.
+// Words one thread of the kernel reads in each exchange step, for E scores
+// per row group over n slices: the one gather (16-byte words, four entries
+// of every fourth 256-entry block per thread), and the larger of the
+// reduce-scatter and all-gather steps (4-byte words; their 16-byte forms
+// read a quarter as many).
+int gather1_words(int E, int n) { return 4 * ((E + 1023) / 1024) * n; }
+int rsag_words(int E, int n) {
+    const int per = (E + n - 1) / n;
+    const int rs = per <= kFusedThreads ? (n + kFusedThreads / per - 1) / (kFusedThreads / per)
+                                        : (per + kFusedThreads - 1) / kFusedThreads * n;
+    return std::max(rs, E / kFusedThreads);
+}
+
+// Tuning overrides (environment): ATN_FUSED_ROWS = query rows per row group
+// (16, 32 or 64), ATN_FUSED_EXCHANGE = "gather" or "rsag".  A plan the
+// override makes impossible falls back to the default choice.
+int env_int(const char* name) {
+    const char* v = std::getenv(name);
+    return v ? std::atoi(v) : 0;
+}
+
+// Cuts each head's query rows into row groups of MB rows and D into slices
+// so that about one workgroup per CU runs and the whole grid is resident at
+// once (the kernel's exchange waits need that).  Capacity is the device's
+// CU count x resident workgroups per CU for the chosen LDS size.  Preferred:
+// the one-gather exchange (one memory round trip) with at least half the
+// CUs busy, largest row group first (fewest K/V re-reads); otherwise the
+// whole head as one row group with reduce-scatter + all-gather.
 FusedPlan fused_plan(int dtype, int pek, const Shape& s, bool query_device) {
-    FusedPlan p;
-    if (s.Lq > kFusedMaxLq || s.Lk > kFusedMaxLk || s.D % 4 != 0) return p;
+    FusedPlan none;
+    if (s.Lq > kFusedMaxLq || s.Lk > kFusedMaxLk || s.D % 4 != 0) return none;
     int cus = 256;
     int dev = 0;
     if (query_device) {
-        if (hipGetDevice(&dev) != hipSuccess) return p;
+        if (hipGetDevice(&dev) != hipSuccess) return none;
         std::lock_guard<std::mutex> lk(g_mu);
         DeviceState& ds = g_dev[dev];
         if (ds.cus == 0 &&
             hipDeviceGetAttribute(&ds.cus, hipDeviceAttributeMultiprocessorCount, dev) !=
                 hipSuccess)
-            return p;
+            return none;
         cus = ds.cus;
     }
     auto capacity = [&](int lds) {
@@ -340,34 +364,75 @@ FusedPlan fused_plan(int dtype, int pek, const Shape& s, bool query_device) {
         if (c == 0) c = atn::fused_small_capacity(dtype, pek, lds);
         return c;
     };
-    if (s.BH > cus) return p;
-    const int64_t per_head = cus / s.BH;
-    int64_t dc = (s.D + per_head - 1) / per_head;
-    dc = (dc + 31) / 32 * 32;
-    for (;; dc += 32) {
-        if (dc > 1024) return p;  // one 4-element column group per thread at most
-        const int lds = atn::fused_small_lds_bytes(dtype, pek, s.Lq, s.Lk, (int)dc);
-        if (lds > kLdsLimit) return p;
-        const int64_t n = (s.D + dc - 1) / dc;
-        int cap = (int)cus;  // one workgroup per CU is always resident
-        if (query_device && n > 1) {
-            cap = capacity(lds);
-            if (cap <= 0) return p;
+    const int MQ = (int)(s.Lq + 15) / 16 * 16, NK = (int)(s.Lk + 31) / 32 * 32;
+    // the smallest slice width that fits LDS and the device for row groups of MB rows
+    auto plan_rows = [&](int MB) {
+        FusedPlan p;
+        const int64_t groups = s.BH * ((s.Lq + MB - 1) / MB);
+        if (groups > cus) return p;
+        const int64_t per_group = cus / groups;
+        int64_t dc = (s.D + per_group - 1) / per_group;
+        dc = (dc + 31) / 32 * 32;
+        for (;; dc += 32) {
+            if (dc > 1024) return p;  // one 4-element column group per thread at most
+            const int lds = atn::fused_small_lds_bytes(dtype, pek, MB, (int)s.Lk, (int)dc);
+            if (lds > kLdsLimit) return p;
+            const int64_t n = (s.D + dc - 1) / dc;
+            int cap = (int)cus;  // one workgroup per CU is always resident
+            if (query_device && n > 1) {
+                cap = capacity(lds);
+                if (cap <= 0) return p;
+            }
+            if (groups * n > kSyncMaxWorkgroups) return p;
+            if (n == 1 || groups * n <= cap) {
+                p.MB = MB;
+                p.dc = (int)dc;
+                p.nchunk = (int)n;
+                p.lds = lds;
+                p.workgroups = (int)(groups * n);
+                break;
+            }
         }
-        if (s.BH * n > kSyncMaxWorkgroups) return p;
-        if (n == 1 || s.BH * n <= cap) {
-            p.ok = true;
-            p.dc = (int)dc;
-            p.nchunk = (int)n;
-            p.lds = lds;
-            break;
+        const int E = MB * NK;
+        if (p.nchunk > 1) {
+            p.gather1 = gather1_words(E, p.nchunk) <= kFusedMaxWords ? 1 : 0;
+            if (!p.gather1 && rsag_words(E, p.nchunk) > kFusedMaxWords) return FusedPlan{};
+            p.part_words = (size_t)groups * p.nchunk * E;
+            p.red_words = p.gather1 ? 0 : (size_t)groups * E;
+        }
+        p.bytes = kSyncBytes + round256(p.part_words * 4) + p.red_words * 4;
+        p.ok = true;
+        return p;
+    };
+    const int force_rows = env_int("ATN_FUSED_ROWS");
+    const char* xe = std::getenv("ATN_FUSED_EXCHANGE");
+    const int force_x = xe == nullptr ? -1 : (std::strcmp(xe, "gather") == 0 ? 1 : 0);
+    auto pick = [&](const FusedPlan& p) {
+        return p.ok && (force_x < 0 || p.nchunk == 1 || p.gather1 == force_x) &&
+               (force_rows == 0 || p.MB == force_rows);
+    };
+    if (force_rows > 0 || force_x >= 0) {
+        for (int MB : {64, 32, 16}) {
+            if (MB > MQ && MB != 16) continue;
+            FusedPlan p = plan_rows(MB);
+            if (force_x == 0 && p.ok && p.gather1) {  // rebuild as reduce-scatter + all-gather
+                const int E = MB * NK;
+                if (rsag_words(E, p.nchunk) <= kFusedMaxWords) {
+                    p.gather1 = 0;
+                    p.red_words = (size_t)s.BH * ((s.Lq + MB - 1) / MB) * E;
+                    p.bytes = kSyncBytes + round256(p.part_words * 4) + p.red_words * 4;
+                }
+            }
+            if (pick(p)) return p;
         }
     }
-    const size_t E = (size_t)((s.Lq + 15) / 16 * 16) * ((s.Lk + 31) / 32 * 32);
-    p.part_elems = p.nchunk > 1 ? (size_t)s.BH * p.nchunk * E : 0;
-    p.red_elems = p.nchunk > 1 ? (size_t)s.BH * E : 0;
-    p.bytes = kSyncBytes + (p.part_elems + p.red_elems) * 4;
-    return p;
+    for (int MB : {64, 32, 16}) {
+        if (MB > MQ) continue;
+        const FusedPlan p = plan_rows(MB);
+        if (p.ok && (p.nchunk == 1 || p.gather1) && 2 * p.workgroups >= std::min(cus, 2048))
+            return p;
+    }
+    return plan_rows(MQ);
 }
 
 // ---------------------------------------------------------------- gemm plan
@@ -493,11 +558,12 @@ int attention_core(int dtype, const void* Q, const void* K, const void* V, void*
     }
     if (use_fused) {
         unsigned* epochs = reinterpret_cast<unsigned*>((char*)ws + kSyncEpochOff);
-        auto* flags = reinterpret_cast<unsigned long long*>((char*)ws + kSyncFlagOff);
-        ATN_HIP(atn::launch_fused_small(dtype, plan.pek, Q, K, V, out, scratch,
-                                        scratch + fd.part_elems, epochs, flags, status,
-                                        (int)s.BH, Lq, Lk, D, fd.dc, fd.nchunk, scale, plan.q,
-                                        plan.k, vec_qk && vec_vo, stream));
+        float* part = reinterpret_cast<float*>((char*)ws + kSyncBytes);
+        float* red = reinterpret_cast<float*>((char*)ws + kSyncBytes + round256(fd.part_words * 4));
+        unsigned* done = reinterpret_cast<unsigned*>((char*)ws + kSyncDoneOff);
+        ATN_HIP(atn::launch_fused_small(dtype, plan.pek, Q, K, V, out, part, red, epochs, done,
+                                        status, (int)s.BH, Lq, Lk, D, fd.MB, fd.dc, fd.nchunk,
+                                        fd.gather1, scale, plan.q, plan.k, stream));
         return ATN_OK;
     }
     float* S = scratch;
@@ -551,9 +617,10 @@ int pe_apply_core(int dtype, const void* in, void* out, long n_rows, int seq_len
 }
 
 // After the stream has drained: reads the status word of a workspace (the
-// library's own for `stream` when ws == NULL).  A barrier timeout is
-// reported once and the whole sync region is cleared (status, epochs and
-// flags back to zero), which re-enables the single-launch kernel.
+// library's own for `stream` when ws == NULL).  An exchange timeout is
+// reported once; the status word is cleared and every epoch word moves one
+// step on, past the epoch whose exchange words the failed call may have
+// left behind, which re-enables the single-launch kernel.
 int workspace_status(void* ws, hipStream_t stream) {
     if (ws == nullptr) {
         int dev;
@@ -568,7 +635,12 @@ int workspace_status(void* ws, hipStream_t stream) {
     int word = 0;
     ATN_HIP(hipMemcpy(&word, ws, sizeof(int), hipMemcpyDeviceToHost));
     if (word == 0) return ATN_OK;
-    ATN_HIP(hipMemset(ws, 0, kSyncBytes));
+    std::vector<unsigned> epochs(kSyncMaxWorkgroups);
+    char* e_dev = static_cast<char*>(ws) + kSyncEpochOff;
+    ATN_HIP(hipMemcpy(epochs.data(), e_dev, epochs.size() * 4, hipMemcpyDeviceToHost));
+    for (unsigned& e : epochs) e += 1u;
+    ATN_HIP(hipMemcpy(e_dev, epochs.data(), epochs.size() * 4, hipMemcpyHostToDevice));
+    ATN_HIP(hipMemset(ws, 0, sizeof(int)));
     return ATN_ERR_DEVICE_TIMEOUT;
 }
 

@@ -3,47 +3,53 @@
 //
 // The reference's headline shapes (e.g. B=1, H=4, L=64, D=2048) move a few
 // MiB and hold a 64x64 score matrix per head, so one query row per
-// workgroup (final/attention.cu:209-215) leaves the chip idle.  Here head bh
-// is cut along D into `nchunk` slices of `dc` dims and workgroup (bh, c):
+// workgroup (final/attention.cu:209-215) leaves the chip idle.  Here the
+// query rows of head bh are cut into `QB` row groups of `MB` rows, D into
+// `nchunk` slices of `dc` dims, and workgroup (group g = (bh, qb), c):
 //
-//   1. loads its Q/K/V slices once (16-byte loads, 8 in flight per thread;
-//      the positional encoding is applied to Q and K at load) into LDS;
-//   2. computes the partial scores S_c = Q[:, c] K[:, c]^T on MFMA
+//   1. loads its Q rows' slice and the head's K/V slices once (16-byte
+//      loads, all in flight before the first LDS store; the positional
+//      encoding is applied to Q and K at load) into LDS;
+//   2. computes the partial scores S_c = Q[rows, c] K[:, c]^T on MFMA
 //      (fp32: v_mfma_f32_16x16x4_f32; bf16: v_mfma_f32_16x16x32_bf16, with
 //      encoded Q/K split into hi + lo bf16 parts so nothing is lost to
-//      re-rounding), four independent 16x16 tiles per wave;
-//   3. all-reduces S over the head's slices through global memory: every
-//      workgroup publishes S_c, meets the others at barrier A, reduces
-//      1/nchunk of the entries over all slices (reduce-scatter), meets them
-//      at barrier B and reads the whole reduced S (all-gather) -- a fixed
-//      summation order, so results are bit-reproducible;
+//      re-rounding), up to eight independent 16x16 tiles per wave;
+//   3. all-reduces S over the group's slices through global memory, either
+//      in one gather (every workgroup reads every slice's partial of its
+//      group: one memory round trip) or, when that volume is too large, as
+//      a reduce-scatter then an all-gather (two round trips).  Partials are
+//      always summed in slice order, so results are bit-reproducible;
 //   4. exact softmax of scale * S per row (max, exp, sum, divide;
 //      final/attention.cu:262-270), four threads per row;
-//   5. O[:, slice] = P V[:, slice] on MFMA (bf16: P split into hi + lo bf16
-//      parts), one store per output element.
+//   5. O[rows, slice] = P V[:, slice] on MFMA (bf16: P split into hi + lo
+//      bf16 parts), one store per output element.
 //
-// Every Q, K, V element is read from HBM once and O is written once.
+// Q and O are touched once; K and V once per row group, and the QB
+// workgroups that share a K/V slice get workgroup ids QB apart by a
+// multiple of the (head, slice) count, which the dispatcher's round-robin
+// over the 8 XCDs puts on one XCD whenever that count is a multiple of 8,
+// so the repeats hit that XCD's L2.
 //
-// Cross-workgroup exchange.  The partial and reduced scores and the barrier
-// words are accessed only with device-scope (agent) atomic loads and stores,
-// which gfx950 performs at the device's coherence point, so no L2 write-back
-// or invalidate is needed; a workgroup waits for its own exchange stores to
-// complete (s_waitcnt) before it publishes its flag.
-//
-// Barriers without counters.  Each head has an epoch word and each
-// workgroup one 64-bit flag word, both at fixed places in the workspace's
-// sync region.  A call reads its head's epoch e at start, publishes
-// (e, head, 1) at barrier A and (e, head, 2) at barrier B; a waiter accepts
-// phase 1 or 2 resp. exactly phase 2 of (e, head).  After barrier B every
-// workgroup of the head has read e, so workgroup 0 of the head then stores
-// e + 1.  Nothing needs resetting between calls, no two workgroups write the
-// same word, kernel arguments do not change from call to call (a captured
-// HIP graph replays correctly), and a word left by another head, another
-// layout or an earlier epoch never matches.  Waits are bounded: on a
-// timeout the workgroup sets the status word, writes NaN to its output
-// slice and exits, so every wave ends; while the status word is set, later
-// calls fail closed the same way until the host clears the sync region.
-// The host launches at most as many workgroups as the device holds at once.
+// Exchange.  Partial and reduced scores are stored and loaded with
+// device-scope (agent) atomic operations, which gfx950 performs at the
+// device's coherence point, so no L2 write-back or invalidate is needed.  A
+// writer waits for its exchange stores to complete (s_waitcnt), then
+// publishes one done word per workgroup and step; wave 0 of each reader
+// polls the n done words of its group (one small word per writer keeps the
+// polling traffic low) and the exchange words are then read once.  Done
+// words carry a tag made of the row group g (< 2048) and the group's epoch
+// word in the workspace's sync region, read at start (exchange_tag below):
+// a call that has seen every slice's done word of its group knows that
+// every workgroup of the group has read the epoch, so slice 0 of the group
+// then stores epoch + 1.  A done word left by an earlier call, another
+// group or another layout never carries the expected tag; nothing is reset
+// between calls and kernel arguments never change from call to call (a
+// captured HIP graph replays correctly).  Waits are bounded: on a timeout
+// the workgroup sets the status word, writes NaN to its output slice and
+// exits, so every wave ends; while the status word is set, later calls
+// fail closed the same way until the host clears the status word (and
+// moves every epoch past the failed call's).  The host launches at most as
+// many workgroups as the device holds at once.
 #include <atomic>
 #include <type_traits>
 
@@ -144,7 +150,7 @@ __host__ __device__ inline Geo make_geo(bool bf16, bool split, int Lq, int Lk, i
     g.v_off = take((bf16 ? dc * g.vstr : g.NK * g.vstr) * es);
     g.s_off = take(g.MQ * g.sstr * 4);
     g.p_off = take(bf16 ? 2 * g.MQ * g.pstr * 2 : g.MQ * g.pstr * 4);
-    g.red_off = take(kThreads * 4);
+    g.red_off = take(kThreads * 16);
     g.bytes = off;
     return g;
 }
@@ -154,15 +160,21 @@ struct FusedArgs {
     const void* K;
     const void* V;
     void* O;
-    float* part;                // [BH][nchunk][E] partial scores
-    float* red;                 // [BH][E] reduced scores
-    unsigned* epochs;           // [BH] per-head epoch words (sync region)
-    unsigned long long* flags;  // [BH][nchunk] barrier flags (sync region)
-    int* status;                // nonzero after a barrier timeout
+    float* part;       // [G][E / 256][nchunk][256] partial scores
+    float* red;        // [G][E] reduced scores (two-phase exchange)
+    unsigned* epochs;  // [G] per-group epoch words (sync region)
+    unsigned* done;    // [2][2048] per-workgroup done words, one set per exchange step
+    int* status;       // nonzero after an exchange timeout
     int Lq, Lk, D, dc, nchunk;
+    int MB, QB;        // query rows per row group, row groups per head
+    int gather1;       // 1: one-gather exchange, 0: reduce-scatter + all-gather
     float scale;
     PeSide pq, pk;
 };
+
+// Most words one thread reads in one exchange step (the host keeps every
+// plan within it).
+constexpr int kMaxWords = 64;
 
 __device__ __forceinline__ void st_dev(float* p, float v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -171,30 +183,49 @@ __device__ __forceinline__ float ld_dev(const float* p) {
     return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-__device__ __forceinline__ unsigned long long flag_word(unsigned epoch, int bh, int phase) {
-    return ((unsigned long long)epoch << 32) | ((unsigned long long)(unsigned)bh << 2) |
-           (unsigned long long)phase;
+// Tag of the done words of row group rg (< 2048) at `epoch`: the top bit is
+// always set, so zero-filled memory never carries a valid tag; the epoch
+// field repeats after 2^20 calls of one group.
+__device__ __forceinline__ unsigned exchange_tag(unsigned epoch, int rg) {
+    return 0x80000000u | ((epoch << 11) & 0x7ffff800u) | (unsigned)rg;
 }
 
-// Publishes `val` in this workgroup's flag, then waits until every flag of
-// the head equals `want` or `want_alt`.  Returns false (for the whole
-// workgroup) on timeout.
-__device__ bool head_sync(unsigned long long* flags, int c, int n, unsigned long long val,
-                          unsigned long long want, unsigned long long want_alt, int* status,
-                          int* flag_lds) {
-    __builtin_amdgcn_s_waitcnt(0);  // this wave's exchange stores have completed
-    __syncthreads();
+// Buffer resource over `bytes` bytes at `base` (uniform), raw (unformatted)
+// 32-bit elements; loads past the end return zero.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
+}
+
+// 16 bytes at byte offset `off`, with the device-scope cache policy (sc1)
+// that agent-scope atomic loads use, so it reads the coherence point; each
+// 4-byte element is single-copy atomic, which is all the exchange needs.
+__device__ __forceinline__ float4 ld_dev4(__amdgpu_buffer_rsrc_t r, int off) {
+    constexpr int kSc1 = 16;
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kSc1);
+    return make_float4(__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]),
+                       __uint_as_float(v[3]));
+}
+
+// Reads the words base[u * stride], u < cnt, all in flight at once.
+template <int NW>
+__device__ __forceinline__ void ld_words(const float* base, int stride, int cnt, float (&w)[NW]) {
+#pragma unroll
+    for (int u = 0; u < NW; ++u) w[u] = u < cnt ? ld_dev(base + u * stride) : 0.f;
+}
+
+// Wave 0 polls the done words done[0..n) until each carries `tag`, while
+// the other waves wait at the barrier.  A writer stores its done word only
+// after its exchange words have completed (s_waitcnt), so they can be read
+// once every done word is seen.  Returns false for the whole workgroup on
+// timeout.
+__device__ bool wait_done(const unsigned* done, int n, unsigned tag, int* flag_lds) {
     if (threadIdx.x < 64) {
-        if (threadIdx.x == 0)
-            __hip_atomic_store(flags + c, val, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         bool ok = true;
         for (int it = 0;; ++it) {
-            int mine = 1;
-            for (int i = threadIdx.x; i < n; i += 64) {
-                const unsigned long long f =
-                    __hip_atomic_load(flags + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                mine &= (f == want) | (f == want_alt);
-            }
+            bool mine = true;
+            for (int i = threadIdx.x; i < n; i += 64)
+                mine &= __hip_atomic_load(const_cast<unsigned*>(done + i), __ATOMIC_RELAXED,
+                                          __HIP_MEMORY_SCOPE_AGENT) == tag;
             if (__all(mine)) break;
             if (it > kSpinLimit) {
                 ok = false;
@@ -202,23 +233,52 @@ __device__ bool head_sync(unsigned long long* flags, int c, int n, unsigned long
             }
             __builtin_amdgcn_s_sleep(1);
         }
-        if (threadIdx.x == 0) {
-            if (!ok) __hip_atomic_store(status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            *flag_lds = ok ? 1 : 0;
-        }
+        if (threadIdx.x == 0 && !ok) *flag_lds = 0;
     }
     __syncthreads();
     return *flag_lds != 0;
 }
 
+__device__ __forceinline__ void st_done(unsigned* p, unsigned tag) {
+    __hip_atomic_store(p, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// NaN into rows [0, lq) of the row group starting at output row `row0`,
+// dims [d0, d0 + dc).
 template <typename T>
-__device__ void poison_slice(T* O, int bh, int Lq, int D, int d0, int dc) {
+__device__ void poison_slice(T* O, size_t row0, int lq, int D, int d0, int dc) {
     const float nan = __int_as_float(0x7fc00000);
-    for (int f = threadIdx.x; f < Lq * dc; f += kThreads) {
+    for (int f = threadIdx.x; f < lq * dc; f += kThreads) {
         const int r = f / dc, d = d0 + f % dc;
-        if (d < D) Elem<T>::st(O, ((size_t)bh * Lq + r) * D + d, nan);
+        if (d < D) Elem<T>::st(O, (row0 + r) * D + d, nan);
     }
 }
+
+// 4 consecutive elements as loaded (fp32: 16 bytes; bf16: 8 bytes of raw
+// bits), widened to fp32 on demand.
+template <typename T>
+struct Raw4;
+template <>
+struct Raw4<float> {
+    typedef float4 type;
+    static __device__ __forceinline__ float4 zero() { return make_float4(0.f, 0.f, 0.f, 0.f); }
+    static __device__ __forceinline__ float4 ld(const float* p) {
+        return *reinterpret_cast<const float4*>(p);
+    }
+    static __device__ __forceinline__ float4 f4(float4 v) { return v; }
+};
+template <>
+struct Raw4<uint16_t> {
+    typedef uint2 type;
+    static __device__ __forceinline__ uint2 zero() { return make_uint2(0u, 0u); }
+    static __device__ __forceinline__ uint2 ld(const uint16_t* p) {
+        return *reinterpret_cast<const uint2*>(p);
+    }
+    static __device__ __forceinline__ float4 f4(uint2 w) {
+        return make_float4(__uint_as_float(w.x << 16), __uint_as_float(w.x & 0xffff0000u),
+                           __uint_as_float(w.y << 16), __uint_as_float(w.y & 0xffff0000u));
+    }
+};
 
 __device__ __forceinline__ bf16x8 lds8(const uint16_t* p) {
     return __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(p));
@@ -323,106 +383,155 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar)
     const int lr = lane & 15, lk = lane >> 4;
-    const int bh = blockIdx.x / a.nchunk, c = blockIdx.x % a.nchunk;
-    const int Lq = a.Lq, Lk = a.Lk, D = a.D, dc = a.dc, n = a.nchunk;
+    // workgroup id -> (row group qb, head bh, slice c): id = qb * W + bh * n + c
+    const int n = a.nchunk;
+    const int W = (int)gridDim.x / a.QB;  // (head, slice) pairs
+    const int qb = (int)blockIdx.x / W, hc = (int)blockIdx.x - qb * W;
+    const int bh = hc / n, c = hc - bh * n;
+    const int rg = bh * a.QB + qb;  // row group (epoch word, exchange region, tag)
+    const int q0 = qb * a.MB;       // first query row of the group
+    const int Lq = min(a.MB, a.Lq - q0), Lk = a.Lk, D = a.D, dc = a.dc;
     const int d0 = c * dc;
-    const Geo g = make_geo(kBf16, kSplit, Lq, Lk, dc);
+    const Geo g = make_geo(kBf16, kSplit, a.MB, Lk, dc);
     const int MQ = g.MQ, NK = g.NK, E = MQ * NK, nrb = MQ / 16;
+    const size_t orow0 = (size_t)bh * a.Lq + q0;  // output row of the group's row 0
 
-    const T* __restrict__ Q = static_cast<const T*>(a.Q) + (size_t)bh * Lq * D;
+    const T* __restrict__ Q = static_cast<const T*>(a.Q) + orow0 * D;
     const T* __restrict__ K = static_cast<const T*>(a.K) + (size_t)bh * Lk * D;
     const T* __restrict__ V = static_cast<const T*>(a.V) + (size_t)bh * Lk * D;
     T* __restrict__ O = static_cast<T*>(a.O);
 
-    // the head's epoch and the status word, read while the slices load
-    unsigned epoch = 0;
-    int failed = 0;
-    if (n > 1) {
-        epoch = __hip_atomic_load(a.epochs + bh, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        failed = __hip_atomic_load(a.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // the group's epoch and the status word, read once (thread 0) while the
+    // slices load, and handed to every thread through LDS
+    __shared__ unsigned sh_epoch;
+    __shared__ int sh_failed;
+    if (tid == 0) {
+        flag = 1;
+        sh_epoch = 0;
+        sh_failed = 0;
+        if (n > 1) {
+            sh_epoch = __hip_atomic_load(a.epochs + rg, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            sh_failed = __hip_atomic_load(a.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
     }
 
     // ---- 1. Q, K, V slices -> LDS.  Thread t owns 4-element column group
-    // t % vpr of rows t / vpr, t / vpr + rstep, ... of the stacked row space
-    // [Q: MQ rows | K: NK rows | V: NK rows]; 8 predicated vector loads are
-    // issued before their LDS stores.  (The host sends this kernel only
-    // shapes with D % 4 == 0 and aligned bases, so a vector is in or out.)
+    // t % vpr of rows t / vpr + k * rstep of each tensor, so the addresses of
+    // its loads step by a uniform stride.  Each round issues up to kQ row
+    // loads of Q and kKV of K and of V before the first is encoded and
+    // stored.  Rows past the sequence (up to MQ / NK) and columns past D are
+    // stored as zeros.  (The host sends this kernel only shapes with
+    // D % 4 == 0 and aligned bases, so a vector is in or out.)
     {
+        typedef typename Raw4<T>::type Raw;
+        constexpr int kQ = 8, kKV = 16;
         const int vpr = dc >> 2;
         const int rstep = kThreads / vpr;
         const int cg = tid % vpr, r0 = tid / vpr;
-        const int d = d0 + cg * 4;
+        const int col = cg * 4, d = d0 + col;
         const bool lane_ok = r0 < rstep && d < D;
-        const int R = MQ + 2 * NK;
-        for (int rb0 = r0; rb0 < R; rb0 += 8 * rstep) {
-            float4 buf[8];
+        const int cq = r0 < rstep ? (MQ - r0 + rstep - 1) / rstep : 0;
+        const int ckv = r0 < rstep ? (NK - r0 + rstep - 1) / rstep : 0;
+        const size_t gstep = (size_t)rstep * D;
+        const T* qp = Q + (size_t)r0 * D + d;
+        const T* kp = K + (size_t)r0 * D + d;
+        const T* vp = V + (size_t)r0 * D + d;
+        // one encoded row vector of Q (isq) or K into its LDS rows
+        auto store_qk = [&](bool isq, int row, float4 f) {
+            const float e4[4] = {f.x, f.y, f.z, f.w};
+            if constexpr (kBf16) {
+                const int off = row * (isq ? g.qstr : g.kstr) + col;
+                uint16_t* hi = reinterpret_cast<uint16_t*>(smem + (isq ? g.q_off : g.k_off));
+                uint2 w;
+                w.x = pack_bf16x2(e4[0], e4[1]);
+                w.y = pack_bf16x2(e4[2], e4[3]);
+                *reinterpret_cast<uint2*>(hi + off) = w;
+                if constexpr (kSplit) {
+                    uint16_t* lo = reinterpret_cast<uint16_t*>(smem + (isq ? g.ql_off : g.kl_off));
+                    float r4[4];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                const int row = rb0 + u * rstep;
-                const bool isq = row < MQ, isk = !isq && row < MQ + NK;
-                const int lrow = isq ? row : (isk ? row - MQ : row - MQ - NK);
-                const T* xr = (isq ? Q : (isk ? K : V)) + (size_t)lrow * D;
-                buf[u] = make_float4(0.f, 0.f, 0.f, 0.f);
-                if (lane_ok && row < R && lrow < (isq ? Lq : Lk)) {
-                    buf[u] = Elem<T>::ld4(xr, d);
-                    if constexpr (PEK != kPeNone) {
-                        if (isq) buf[u] = encode4<T, PEK>(buf[u], xr, lrow, d, a.pq);
-                        else if (isk) buf[u] = encode4<T, PEK>(buf[u], xr, lrow, d, a.pk);
-                    }
+                    for (int e = 0; e < 4; ++e)
+                        r4[e] = e4[e] - bf16_bits_to_f32(f32_to_bf16_bits(e4[e]));
+                    uint2 wl;
+                    wl.x = pack_bf16x2(r4[0], r4[1]);
+                    wl.y = pack_bf16x2(r4[2], r4[3]);
+                    *reinterpret_cast<uint2*>(lo + off) = wl;
+                }
+            } else {
+                float* dst = reinterpret_cast<float*>(smem + (isq ? g.q_off : g.k_off)) +
+                             row * (isq ? g.qstr : g.kstr) + col;
+                *reinterpret_cast<float2*>(dst) = make_float2(e4[0], e4[1]);
+                *reinterpret_cast<float2*>(dst + 2) = make_float2(e4[2], e4[3]);
+            }
+        };
+        auto store_v = [&](int row, Raw raw) {
+            if constexpr (kBf16) {
+                // transposed [dim][key]: the raw bf16 bits go straight in
+                uint16_t* vt = reinterpret_cast<uint16_t*>(smem + g.v_off) + col * g.vstr + row;
+                vt[0] = (uint16_t)raw.x;
+                vt[g.vstr] = (uint16_t)(raw.x >> 16);
+                vt[2 * g.vstr] = (uint16_t)raw.y;
+                vt[3 * g.vstr] = (uint16_t)(raw.y >> 16);
+            } else {
+                float* dst = reinterpret_cast<float*>(smem + g.v_off) + row * g.vstr + col;
+                *reinterpret_cast<float2*>(dst) = make_float2(raw.x, raw.y);
+                *reinterpret_cast<float2*>(dst + 2) = make_float2(raw.z, raw.w);
+            }
+        };
+        for (int j = 0; j * kQ < cq || j * kKV < ckv; ++j) {
+            Raw bq[kQ], bk[kKV], bv[kKV];
+#pragma unroll
+            for (int u = 0; u < kQ; ++u) {
+                const int k = j * kQ + u, row = r0 + k * rstep;
+                bq[u] = Raw4<T>::zero();
+                if (lane_ok && k < cq && row < Lq) bq[u] = Raw4<T>::ld(qp + k * gstep);
+            }
+#pragma unroll
+            for (int u = 0; u < kKV; ++u) {
+                const int k = j * kKV + u, row = r0 + k * rstep;
+                bk[u] = Raw4<T>::zero();
+                bv[u] = Raw4<T>::zero();
+                if (lane_ok && k < ckv && row < Lk) {
+                    bk[u] = Raw4<T>::ld(kp + k * gstep);
+                    bv[u] = Raw4<T>::ld(vp + k * gstep);
                 }
             }
 #pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                const int row = rb0 + u * rstep;
-                if (!(r0 < rstep) || row >= R) continue;
-                const bool isq = row < MQ, isk = !isq && row < MQ + NK;
-                const int lrow = isq ? row : (isk ? row - MQ : row - MQ - NK);
-                const int col = cg * 4;
-                const float e4[4] = {buf[u].x, buf[u].y, buf[u].z, buf[u].w};
-                if constexpr (kBf16) {
-                    if (isq || isk) {
-                        const int off = lrow * (isq ? g.qstr : g.kstr) + col;
-                        uint16_t* hi =
-                            reinterpret_cast<uint16_t*>(smem + (isq ? g.q_off : g.k_off));
-                        uint2 w;
-                        w.x = pack_bf16x2(e4[0], e4[1]);
-                        w.y = pack_bf16x2(e4[2], e4[3]);
-                        *reinterpret_cast<uint2*>(hi + off) = w;
-                        if constexpr (kSplit) {
-                            uint16_t* lo =
-                                reinterpret_cast<uint16_t*>(smem + (isq ? g.ql_off : g.kl_off));
-                            float r4[4];
+            for (int u = 0; u < kQ; ++u) {
+                const int k = j * kQ + u, row = r0 + k * rstep;
+                if (k >= cq) break;
+                float4 f = Raw4<T>::f4(bq[u]);
+                if constexpr (PEK != kPeNone)
+                    if (lane_ok && row < Lq)
+                        f = encode4<T, PEK>(f, Q + (size_t)row * D, q0 + row, d, a.pq);
+                store_qk(true, row, f);
+            }
 #pragma unroll
-                            for (int e = 0; e < 4; ++e)
-                                r4[e] = e4[e] - bf16_bits_to_f32(f32_to_bf16_bits(e4[e]));
-                            uint2 wl;
-                            wl.x = pack_bf16x2(r4[0], r4[1]);
-                            wl.y = pack_bf16x2(r4[2], r4[3]);
-                            *reinterpret_cast<uint2*>(lo + off) = wl;
-                        }
-                    } else {
-                        uint16_t* vt = reinterpret_cast<uint16_t*>(smem + g.v_off);
-#pragma unroll
-                        for (int e = 0; e < 4; ++e)
-                            vt[(col + e) * g.vstr + lrow] = f32_to_bf16_bits(e4[e]);
-                    }
-                } else {
-                    const int base = isq ? g.q_off : (isk ? g.k_off : g.v_off);
-                    const int str = isq ? g.qstr : (isk ? g.kstr : g.vstr);
-                    float* dst = reinterpret_cast<float*>(smem + base) + lrow * str + col;
-                    *reinterpret_cast<float2*>(dst) = make_float2(e4[0], e4[1]);
-                    *reinterpret_cast<float2*>(dst + 2) = make_float2(e4[2], e4[3]);
-                }
+            for (int u = 0; u < kKV; ++u) {
+                const int k = j * kKV + u, row = r0 + k * rstep;
+                if (k >= ckv) break;
+                float4 f = Raw4<T>::f4(bk[u]);
+                if constexpr (PEK != kPeNone)
+                    if (lane_ok && row < Lk) f = encode4<T, PEK>(f, K + (size_t)row * D, row, d, a.pk);
+                store_qk(false, row, f);
+                store_v(row, bv[u]);
             }
         }
     }
     __syncthreads();
 
+    const unsigned epoch = sh_epoch;
+    const unsigned tag = exchange_tag(epoch, rg);
+
     // ---- 2. partial scores S_c on MFMA.  Each wave owns one 16-row block
     // and up to 8 column tiles; the row block's A operand is read once per
-    // k-step and shared by the tiles' independent accumulators.
+    // k-step and shared by the tiles' independent accumulators.  With more
+    // than one slice the partials go out as tagged words.
+    // Partials of the group live in [E / 256][slice][256] order (E is a
+    // multiple of 512), so that every read pattern of step 3 is one base
+    // address plus a uniform stride per word.
     float* S = reinterpret_cast<float*>(smem + g.s_off);
-    float* part = a.part + ((size_t)bh * n + c) * E;
+    float* part = a.part + (size_t)rg * n * E + (size_t)c * 256;
     {
         int rb, c0, cs;
         const int cnt = wave_tiles(wave, nrb, NK / 16, &rb, &c0, &cs);
@@ -431,7 +540,8 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int i = rb * 16 + lk * 4 + r;
-                if (n > 1) st_dev(part + i * NK + j, acc[r]);
+                const int e = i * NK + j;
+                if (n > 1) st_dev(part + (e >> 8) * (n * 256) + (e & 255), acc[r]);
                 else S[i * g.sstr + j] = acc[r];
             }
         };
@@ -467,89 +577,191 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
         else if (cnt > 4) run(std::integral_constant<int, 8>{});
     }
 
-    // ---- 3. all-reduce of S over the head's slices
+    // ---- 3. all-reduce of S over the group's slices (tagged words)
     if (n > 1) {
-        unsigned long long* fl = a.flags + (size_t)bh * n;
-        const unsigned long long fa = flag_word(epoch, bh, 1), fb = flag_word(epoch, bh, 2);
-        if (failed) {  // an earlier call timed out: fail closed
-            poison_slice<T>(O, bh, Lq, D, d0, dc);
+        unsigned* done1 = a.done + rg * n;
+        unsigned* done2 = a.done + 2048 + rg * n;
+        __builtin_amdgcn_s_waitcnt(0);  // this wave's partials have completed
+        __syncthreads();
+        if (tid == 0) st_done(done1 + c, tag);
+        if (sh_failed) {  // an earlier call timed out: fail closed
+            poison_slice<T>(O, orow0, Lq, D, d0, dc);
             return;
         }
-        if (!head_sync(fl, c, n, fa, fa, fb, a.status, &flag)) {
-            poison_slice<T>(O, bh, Lq, D, d0, dc);
-            return;
-        }
-        // reduce-scatter: this workgroup owns entries [e0, e1)
-        const int per = (E + n - 1) / n;
-        const int e0 = c * per, e1 = min(E, e0 + per);
-        const int cnt_e = max(0, e1 - e0);
-        float* redl = reinterpret_cast<float*>(smem + g.red_off);
-        const float* pb = a.part + (size_t)bh * n * E;
-        if (cnt_e > 0 && cnt_e <= kThreads) {
-            const int G = kThreads / cnt_e;  // partial groups summed in parallel
-            const int el = tid % cnt_e, grp = tid / cnt_e;
-            float acc = 0.f;
-            if (grp < G) {
-                const float* src = pb + e0 + el;
-                int p = grp;
-                for (; p + 7 * G < n; p += 8 * G) {
-                    float x[8];
+        const float* pg = a.part + (size_t)rg * n * E;
+        float* rd = a.red + (size_t)rg * E;
+        auto put_s = [&](int e, float v) {
+            const int i = e / NK, j = e - i * NK;
+            S[i * g.sstr + j] = v;
+        };
+        // returns false (for the whole workgroup) on a timeout
+        auto exchange = [&]() -> bool {
+            float w[kMaxWords];
+            if (!wait_done(done1, n, tag, &flag)) return false;
+            if (a.gather1) {
+                // one gather, 16-byte words: thread t sums entries 4 (t % 64)
+                // .. + 3 of 256-entry blocks t / 64 + 4 i, every slice's
+                // partial of each in slice order; vector u = i * n + slice
+                const int nblk = E >> 8, b0 = tid >> 6;  // 256-entry blocks
+                const int cnt = (b0 < nblk ? (nblk - b0 + 3) / 4 : 0) * n;
+                const __amdgpu_buffer_rsrc_t rs = make_rsrc(pg, n * E * 4);
+                const int voff = ((tid >> 6) * n * 256 + (tid & 63) * 4) * 4;
+                float4 w4[kMaxWords / 4];
 #pragma unroll
-                    for (int u = 0; u < 8; ++u) x[u] = ld_dev(src + (size_t)(p + u * G) * E);
-#pragma unroll
-                    for (int u = 0; u < 8; ++u) acc += x[u];
+                for (int u = 0; u < kMaxWords / 4; ++u) {
+                    const int i = u / n, p = u - i * n;  // n is uniform: scalar math
+                    w4[u] = u < cnt ? ld_dev4(rs, voff + (4 * i * n + p) * 1024)
+                                    : make_float4(0.f, 0.f, 0.f, 0.f);
                 }
-                for (; p < n; p += G) acc += ld_dev(src + (size_t)p * E);
+                float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+                int p = 0, i = 0;
+#pragma unroll
+                for (int u = 0; u < kMaxWords / 4; ++u) {
+                    if (u < cnt) {
+                        acc.x += w4[u].x;
+                        acc.y += w4[u].y;
+                        acc.z += w4[u].z;
+                        acc.w += w4[u].w;
+                        if (++p == n) {
+                            const int e = (tid >> 6) * 256 + i * 1024 + (tid & 63) * 4;
+                            put_s(e, acc.x);
+                            put_s(e + 1, acc.y);
+                            put_s(e + 2, acc.z);
+                            put_s(e + 3, acc.w);
+                            acc = make_float4(0.f, 0.f, 0.f, 0.f);
+                            p = 0;
+                            ++i;
+                        }
+                    }
+                }
+                return true;
             }
-            redl[tid] = acc;
-            __syncthreads();
-            if (tid < cnt_e) {
-                float s = 0.f;
-                for (int q = 0; q < G; ++q) s += redl[q * cnt_e + tid];
-                st_dev(a.red + (size_t)bh * E + e0 + tid, s);
-            }
-        } else {
-            for (int e = e0 + tid; e < e1; e += kThreads) {
-                const float* src = pb + e;
+            // reduce-scatter: this workgroup owns entries [e0, e1)
+            const int per = (E + n - 1) / n;
+            const int e0 = c * per, e1 = min(E, e0 + per);
+            const int cnt_e = max(0, e1 - e0);
+            float* redl = reinterpret_cast<float*>(smem + g.red_off);
+            const __amdgpu_buffer_rsrc_t rs = make_rsrc(pg, n * E * 4);
+            if (E % (16 * n) == 0 && cnt_e <= 4 * kThreads &&
+                (n + kThreads / (cnt_e >> 2) - 1) / (kThreads / (cnt_e >> 2)) <= kMaxWords / 4) {
+                // 16-byte words: G groups of cnt_e / 4 threads, each thread 4
+                // consecutive entries (a 4-aligned run never crosses a
+                // 256-entry block); group q sums slices q, q + G, ...
+                const int c4 = cnt_e >> 2;
+                const int G = kThreads / c4;
+                const int el4 = tid % c4, grp = tid / c4;
+                const int cnt = grp < G ? (n - grp + G - 1) / G : 0;
+                const int e = e0 + 4 * el4;
+                const int voff = (((e >> 8) * n + grp) * 256 + (e & 255)) * 4;
+                float4 w4[kMaxWords / 4];
+#pragma unroll
+                for (int u = 0; u < kMaxWords / 4; ++u)
+                    w4[u] = u < cnt ? ld_dev4(rs, voff + u * G * 1024)
+                                    : make_float4(0.f, 0.f, 0.f, 0.f);
+                float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+                for (int u = 0; u < kMaxWords / 4; ++u) {
+                    if (u < cnt) {
+                        acc.x += w4[u].x;
+                        acc.y += w4[u].y;
+                        acc.z += w4[u].z;
+                        acc.w += w4[u].w;
+                    }
+                }
+                reinterpret_cast<float4*>(redl)[tid] = acc;
+                __syncthreads();
+                if (tid < c4) {
+                    float4 sum = make_float4(0.f, 0.f, 0.f, 0.f);
+                    for (int q = 0; q < G; ++q) {
+                        const float4 v = reinterpret_cast<const float4*>(redl)[q * c4 + tid];
+                        sum.x += v.x;
+                        sum.y += v.y;
+                        sum.z += v.z;
+                        sum.w += v.w;
+                    }
+                    float* dst = rd + e0 + 4 * tid;
+                    st_dev(dst, sum.x);
+                    st_dev(dst + 1, sum.y);
+                    st_dev(dst + 2, sum.z);
+                    st_dev(dst + 3, sum.w);
+                }
+            } else if (cnt_e <= kThreads) {
+                // G groups of cnt_e threads; group q sums slices q, q + G, ...
+                const int G = cnt_e > 0 ? kThreads / cnt_e : 1;
+                const int el = cnt_e > 0 ? tid % cnt_e : 0;
+                const int grp = cnt_e > 0 ? tid / cnt_e : G;
+                const int cnt = grp < G ? (n - grp + G - 1) / G : 0;
+                const int e = e0 + el;
+                ld_words<kMaxWords>(pg + ((e >> 8) * n + grp) * 256 + (e & 255), G * 256, cnt, w);
                 float acc = 0.f;
-                int p = 0;
-                for (; p + 7 < n; p += 8) {
-                    float x[8];
 #pragma unroll
-                    for (int u = 0; u < 8; ++u) x[u] = ld_dev(src + (size_t)(p + u) * E);
-#pragma unroll
-                    for (int u = 0; u < 8; ++u) acc += x[u];
+                for (int u = 0; u < kMaxWords; ++u)
+                    if (u < cnt) acc += w[u];
+                redl[tid] = acc;
+                __syncthreads();
+                if (tid < cnt_e) {
+                    float sum = 0.f;
+                    for (int q = 0; q < G; ++q) sum += redl[q * cnt_e + tid];
+                    st_dev(rd + e0 + tid, sum);
                 }
-                for (; p < n; ++p) acc += ld_dev(src + (size_t)p * E);
-                st_dev(a.red + (size_t)bh * E + e, acc);
+            } else {
+                // entries e0 + tid + 256 k, every slice of each; word
+                // u = k * n + slice
+                const int ne = tid < cnt_e ? (cnt_e - tid + kThreads - 1) / kThreads : 0;
+                const int cnt = ne * n;
+                const int e = e0 + tid;
+                ld_words<kMaxWords>(pg + (e >> 8) * n * 256 + (e & 255), 256, cnt, w);
+                float acc = 0.f;
+                int p = 0, k = 0;
+#pragma unroll
+                for (int u = 0; u < kMaxWords; ++u) {
+                    if (u < cnt) {
+                        acc += w[u];
+                        if (++p == n) {
+                            st_dev(rd + e + k * kThreads, acc);
+                            acc = 0.f;
+                            p = 0;
+                            ++k;
+                        }
+                    }
+                }
             }
-        }
-        if (!head_sync(fl, c, n, fb, fb, fb, a.status, &flag)) {
-            poison_slice<T>(O, bh, Lq, D, d0, dc);
+            __builtin_amdgcn_s_waitcnt(0);  // this wave's reduced words have completed
+            __syncthreads();
+            if (tid == 0) st_done(done2 + c, tag);
+            // all-gather: the reduced S into LDS, 16-byte words (E is a
+            // multiple of 512): vectors tid + 256 u
+            if (!wait_done(done2, n, tag, &flag)) return false;
+            const __amdgpu_buffer_rsrc_t rr = make_rsrc(rd, E * 4);
+            const int cnt = tid < (E >> 2) ? ((E >> 2) - tid + kThreads - 1) / kThreads : 0;
+            float4 w4[kMaxWords / 4];
+#pragma unroll
+            for (int u = 0; u < kMaxWords / 4; ++u)
+                w4[u] = u < cnt ? ld_dev4(rr, (tid + u * kThreads) * 16)
+                                : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+            for (int u = 0; u < kMaxWords / 4; ++u) {
+                if (u < cnt) {
+                    const int e = 4 * (tid + u * kThreads);
+                    put_s(e, w4[u].x);
+                    put_s(e + 1, w4[u].y);
+                    put_s(e + 2, w4[u].z);
+                    put_s(e + 3, w4[u].w);
+                }
+            }
+            return true;
+        };
+        if (!exchange()) {
+            if (tid == 0)
+                __hip_atomic_store(a.status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            poison_slice<T>(O, orow0, Lq, D, d0, dc);
             return;
         }
-        // every workgroup of the head has read `epoch`: advance it
+        // this workgroup has seen words of every slice of the group, so every
+        // workgroup of the group has read `epoch`: advance it
         if (c == 0 && tid == 0)
-            __hip_atomic_store(a.epochs + bh, epoch + 1u, __ATOMIC_RELAXED,
+            __hip_atomic_store(a.epochs + rg, epoch + 1u, __ATOMIC_RELAXED,
                                __HIP_MEMORY_SCOPE_AGENT);
-        // all-gather: the reduced S into LDS (16 loads in flight per thread)
-        const float* rs = a.red + (size_t)bh * E;
-        for (int base = 0; base < E; base += kThreads * 16) {
-            float x[16];
-#pragma unroll
-            for (int u = 0; u < 16; ++u) {
-                const int e = base + u * kThreads + tid;
-                x[u] = e < E ? ld_dev(rs + e) : 0.f;
-            }
-#pragma unroll
-            for (int u = 0; u < 16; ++u) {
-                const int e = base + u * kThreads + tid;
-                if (e < E) {
-                    const int i = e / NK, j = e - i * NK;
-                    S[i * g.sstr + j] = x[u];
-                }
-            }
-        }
     }
     __syncthreads();
 
@@ -640,7 +852,7 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
                         const int i = rb * 16 + lk * 4 + r;
-                        if (i < Lq) Elem<T>::st(O, ((size_t)bh * Lq + i) * D + dd, acc[u][r]);
+                        if (i < Lq) Elem<T>::st(O, (orow0 + i) * D + dd, acc[u][r]);
                     }
                 }
             };
@@ -669,8 +881,8 @@ template <typename T, int PEK>
 hipError_t launch_t(const FusedArgs& a, int BH, int lds, hipStream_t st) {
     hipError_t e = ensure_lds_limit<T, PEK>(lds);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((k_fused_small<T, PEK>), dim3((unsigned)(BH * a.nchunk)), dim3(kThreads),
-                       lds, st, a);
+    hipLaunchKernelGGL((k_fused_small<T, PEK>), dim3((unsigned)(BH * a.QB * a.nchunk)),
+                       dim3(kThreads), lds, st, a);
     return hipGetLastError();
 }
 
@@ -689,9 +901,9 @@ int capacity_t(int lds) {
 
 }  // namespace
 
-int fused_small_lds_bytes(int dtype, int pek, int Lq, int Lk, int dc) {
+int fused_small_lds_bytes(int dtype, int pek, int MB, int Lk, int dc) {
     const bool bf16 = dtype == kDtypeBF16;
-    return make_geo(bf16, bf16 && pek != kPeNone, Lq, Lk, dc).bytes;
+    return make_geo(bf16, bf16 && pek != kPeNone, MB, Lk, dc).bytes;
 }
 
 int fused_small_capacity(int dtype, int pek, int lds) {
@@ -703,14 +915,13 @@ int fused_small_capacity(int dtype, int pek, int lds) {
 }
 
 hipError_t launch_fused_small(int dtype, int pek, const void* Q, const void* K, const void* V,
-                              void* O, float* part, float* red, unsigned* epochs,
-                              unsigned long long* flags, int* status, int BH, int Lq, int Lk,
-                              int D, int dc, int nchunk, float scale, const PeSide& pq,
-                              const PeSide& pk, int vec_ok, hipStream_t st) {
-    (void)vec_ok;  // the host sends only vector-aligned shapes here
-    FusedArgs a{Q, K, V, O, part, red, epochs, flags, status, Lq, Lk, D, dc, nchunk, scale,
-                pq, pk};
-    const int lds = fused_small_lds_bytes(dtype, pek, Lq, Lk, dc);
+                              void* O, float* part, float* red,
+                              unsigned* epochs, unsigned* done, int* status, int BH, int Lq,
+                              int Lk, int D, int MB, int dc, int nchunk, int gather1, float scale,
+                              const PeSide& pq, const PeSide& pk, hipStream_t st) {
+    FusedArgs a{Q, K, V, O, part, red, epochs, done, status, Lq, Lk, D, dc, nchunk,
+                MB, (Lq + MB - 1) / MB, gather1, scale, pq, pk};
+    const int lds = fused_small_lds_bytes(dtype, pek, MB, Lk, dc);
 #define ATN_FUSED_CASE(T)                                                                \
     switch (pek) {                                                                       \
         case kPeNone: return launch_t<T, kPeNone>(a, BH, lds, st);                       \

@@ -21,14 +21,17 @@ hipError_t launch_softmax(const float* S, float* P, long rows, int Lk, int nspli
                           size_t split_stride, float scale, hipStream_t st);
 hipError_t launch_pv(int dtype, const float* P, const void* V, void* O, int BH, int Lq, int Lk,
                      int D, int vec_ok, hipStream_t st);
-// Single-launch split-D kernel for len_q <= 64, len_k <= 128 (fused_small.hip).
-int fused_small_lds_bytes(int dtype, int pek, int Lq, int Lk, int dc);
+// Single-launch split-D kernel for len_q <= 64, len_k <= 128 (fused_small.hip):
+// row groups of MB query rows, D slices of dc dims; gather1 selects the
+// one-gather exchange (each thread polls (MB*NK/256) * nchunk <= 64 words)
+// over reduce-scatter + all-gather.
+int fused_small_lds_bytes(int dtype, int pek, int MB, int Lk, int dc);
 int fused_small_capacity(int dtype, int pek, int lds);
 hipError_t launch_fused_small(int dtype, int pek, const void* Q, const void* K, const void* V,
-                              void* O, float* part, float* red, unsigned* epochs,
-                              unsigned long long* flags, int* status, int BH, int Lq, int Lk,
-                              int D, int dc, int nchunk, float scale, const PeSide& pq,
-                              const PeSide& pk, int vec_ok, hipStream_t st);
+                              void* O, float* part, float* red,
+                              unsigned* epochs, unsigned* done, int* status, int BH, int Lq,
+                              int Lk, int D, int MB, int dc, int nchunk, int gather1, float scale,
+                              const PeSide& pq, const PeSide& pk, hipStream_t st);
 // Long-sequence bf16 path (gemm_path.hip): S = scale Q K^T (fp32),
 // P = bf16(softmax(S)), O = P V.  Needs D % 8 == 0, Lk % 8 == 0 and 16-byte
 // aligned bases.

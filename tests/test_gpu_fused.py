@@ -2,9 +2,10 @@
 
 Besides parity with the CPU oracle (the drop-in tests in
 test_gpu_parity.py route these shapes here too), this kernel keeps state in
-its workspace: per-head barrier epochs, per-workgroup barrier flags and a
-status word.  These tests check that many calls in a row on one workspace
+its workspace: per-row-group epoch words that tag the exchanged scores, and
+a status word.  These tests check that many calls in a row on one workspace
 keep working and give bit-identical results (fixed summation order), that
+every row-group size and both exchange forms agree with the oracle, that
 caller workspaces on two streams do not interfere, that captured HIP graphs
 replay correctly, and that no call reports a device-side wait timeout.
 """
@@ -155,3 +156,48 @@ def test_graph_replays_match_eager(am, dev, shape):
     n, mabs, _ = H.check_f32(ref, oracle.attention(Q, K, V, nthreads=16))
     assert n == 0, mabs
     st.destroy()
+
+
+@pytest.mark.parametrize("rows,exchange", [("16", "gather"), ("16", "rsag"), ("32", "rsag"),
+                                           ("64", "rsag"), ("", "")],
+                         ids=lambda v: v or "default")
+@pytest.mark.parametrize("shape,dtype,pe", [((1, 4, 64, 64, 2048), "f32", None),
+                                            ((1, 3, 40, 72, 1024), "f32", None),
+                                            ((1, 2, 48, 96, 1024), "bf16", "rope_half")],
+                         ids=["cfg2", "ragged", "bf16rope"])
+def test_fused_row_groups_and_exchanges(am, dev, monkeypatch, rows, exchange, shape, dtype, pe):
+    """Every row-group size and both exchange forms (one gather; reduce-scatter
+    + all-gather), forced through the planner's tuning overrides, give the
+    oracle's result, and repeated calls on one workspace are bit-identical."""
+    import hip_rt
+    if rows:
+        monkeypatch.setenv("ATN_FUSED_ROWS", rows)
+        monkeypatch.setenv("ATN_FUSED_EXCHANGE", exchange)
+    B, Hh, Lq, Lk, D = shape
+    print(f"[case] fused rows={rows or 'default'} exchange={exchange or 'default'} "
+          f"{dtype} {shape} pe={pe}", flush=True)
+    dcode = 0 if dtype == "f32" else 1
+    desc = am.make_pe("rope", pairing="half") if pe else None
+    assert am.path(dcode, B, Hh, Lq, Lk, D, desc) == am.ATN_PATH_FUSED_SMALL
+    (q, k, v), (Q, K, V) = H.device_inputs((B, Hh, Lq, D), (B, Hh, Lk, D), 101 + D, dtype)
+    ws = _ws(am, dcode, B, Hh, Lq, Lk, D, desc)
+    out = H.empty(Q.shape, dtype)
+    first = None
+    for it in range(6):
+        am.attention_ex(q, k, v, out, pe=desc, workspace=ws)
+        if it in (0, 5):
+            hip_rt.synchronize()
+            got = out.bits()
+            if first is None:
+                first = got
+            else:
+                assert np.array_equal(first, got), "results differ between calls"
+    assert am.sync_status(ws, B, Hh) == 0
+    if pe:
+        c, s = oracle.rope_cache(max(Lq, Lk), D)
+        ref = oracle.attention_rope(Q, K, V, c, s, pairing="half", nthreads=16)
+        n, nrel, mabs = H.check_bf16(out.numpy(), ref)
+        assert n == 0, f"normwise rel {nrel}, max abs {mabs}"
+    else:
+        n, mabs, mrel = H.check_f32(out.numpy(), oracle.attention(Q, K, V, nthreads=16))
+        assert n == 0, f"{n} mismatches, max abs {mabs}, max rel {mrel}"
