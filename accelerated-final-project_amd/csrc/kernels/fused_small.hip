@@ -115,8 +115,11 @@ __device__ __forceinline__ float4 encode4(float4 v4, const T* __restrict__ xr, i
 // MFMA operand reads are free of bank conflicts: fp32 A operands (Q, P)
 // read 16 rows x 2 columns per half-wave -> row stride = 2 (mod 32); fp32 V
 // (B operand of PV) reads 2 rows x 16 columns -> stride = 16 (mod 32); the
-// softmax reads 8 rows x 4 columns of S -> stride = 4 (mod 32).  bf16 rows
-// are padded by 8 elements (16-byte aligned 8-element reads).
+// softmax reads 8 rows x 4 columns of S -> stride = 4 (mod 32).  bf16 Q, K
+// and P rows are padded by 8 elements (16-byte aligned 8-element reads);
+// bf16 V is kept [key][dim] with a row stride of dc + 16 elements, i.e. 32
+// or 96 bytes (mod 128), so the 4 rows x 32 bytes that each 16-lane group of
+// a transposing read (ds_read_b64_tr_b16) touches fall in distinct banks.
 struct Geo {
     int MQ, NK, dc;
     int qstr, kstr, vstr, sstr, pstr;
@@ -133,7 +136,7 @@ __host__ __device__ inline Geo make_geo(bool bf16, bool split, int Lq, int Lk, i
     const int es = bf16 ? 2 : 4;
     if (bf16) {
         g.qstr = g.kstr = dc + 8;
-        g.vstr = g.NK + 8;  // V stored transposed: [dim][key]
+        g.vstr = dc + 16;   // V stored [key][dim], read transposed
         g.pstr = g.NK + 8;  // P hi and lo, [row][key]
     } else {
         g.qstr = g.kstr = dc + 2;
@@ -147,7 +150,7 @@ __host__ __device__ inline Geo make_geo(bool bf16, bool split, int Lq, int Lk, i
     g.k_off = take(g.NK * g.kstr * es);
     g.ql_off = (bf16 && split) ? take(g.MQ * g.qstr * es) : g.q_off;
     g.kl_off = (bf16 && split) ? take(g.NK * g.kstr * es) : g.k_off;
-    g.v_off = take((bf16 ? dc * g.vstr : g.NK * g.vstr) * es);
+    g.v_off = take(g.NK * g.vstr * es);
     g.s_off = take(g.MQ * g.sstr * 4);
     g.p_off = take(bf16 ? 2 * g.MQ * g.pstr * 2 : g.MQ * g.pstr * 4);
     g.red_off = take(kThreads * 16);
@@ -254,6 +257,10 @@ __device__ void poison_slice(T* O, size_t row0, int lq, int D, int d0, int dc) {
     }
 }
 
+// Buffer-load cache-policy operand bit that marks the access volatile for
+// the compiler (kept in program order, never sunk or merged).
+constexpr int kAuxVolatile = (int)(1u << 31);
+
 // 4 consecutive elements as loaded (fp32: 16 bytes; bf16: 8 bytes of raw
 // bits), widened to fp32 on demand.
 template <typename T>
@@ -266,6 +273,12 @@ struct Raw4<float> {
         return *reinterpret_cast<const float4*>(p);
     }
     static __device__ __forceinline__ float4 f4(float4 v) { return v; }
+    template <int Aux = 0>
+    static __device__ __forceinline__ float4 ld_buf(__amdgpu_buffer_rsrc_t r, int off) {
+        const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, Aux);
+        return make_float4(__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]),
+                           __uint_as_float(v[3]));
+    }
 };
 template <>
 struct Raw4<uint16_t> {
@@ -277,6 +290,11 @@ struct Raw4<uint16_t> {
     static __device__ __forceinline__ float4 f4(uint2 w) {
         return make_float4(__uint_as_float(w.x << 16), __uint_as_float(w.x & 0xffff0000u),
                            __uint_as_float(w.y << 16), __uint_as_float(w.y & 0xffff0000u));
+    }
+    template <int Aux = 0>
+    static __device__ __forceinline__ uint2 ld_buf(__amdgpu_buffer_rsrc_t r, int off) {
+        const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, Aux);
+        return make_uint2(v[0], v[1]);
     }
 };
 
@@ -359,6 +377,42 @@ __device__ __forceinline__ void mma_bf16(const uint16_t* a, const uint16_t* a_lo
     }
 }
 
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ v4i16 ds_read_tr16(const uint16_t* p) {
+    return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4i16*)(p));
+}
+
+// PV form of mma_bf16 (A = P as hi + lo parts): the B operand comes from V
+// kept [key][dim] in LDS (row stride vstr; vb points at tile 0's first
+// column, tile u's columns start nstep later).  Lane (lr, lk) needs keys
+// kk + 8 lk + 0..7 of column lr: in each 16-lane group lane L supplies the
+// address of key kk + 8 lk + 4 h + (L % 16) / 4, columns 4 (L % 4) .. + 3,
+// and the transposing read (ds_read_b64_tr_b16) hands lane L keys 4 h +
+// 0..3 of column L % 16 -- half h of its operand.
+template <int NT>
+__device__ __forceinline__ void mma_bf16_vt(const uint16_t* a, const uint16_t* a_lo,
+                                            const uint16_t* vb, int vstr, int nstep, int kdim,
+                                            v4f (&acc)[NT]) {
+    const int lane = threadIdx.x & 63;
+    const uint16_t* vl = vb + (8 * (lane >> 4) + ((lane & 15) >> 2)) * vstr + 4 * (lane & 3);
+    for (int kk = 0; kk < kdim; kk += 32) {
+        const bf16x8 ah = lds8(a + kk), al = lds8(a_lo + kk);
+        bf16x8 bv[NT];
+#pragma unroll
+        for (int u = 0; u < NT; ++u) {
+            const uint16_t* p = vl + kk * vstr + u * nstep;
+            const uint2 lo = __builtin_bit_cast(uint2, ds_read_tr16(p));
+            const uint2 hi = __builtin_bit_cast(uint2, ds_read_tr16(p + 4 * vstr));
+            bv[u] = __builtin_bit_cast(bf16x8, make_uint4(lo.x, lo.y, hi.x, hi.y));
+        }
+#pragma unroll
+        for (int u = 0; u < NT; ++u) {
+            acc[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bv[u], acc[u], 0, 0, 0);
+            acc[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bv[u], acc[u], 0, 0, 0);
+        }
+    }
+}
+
 // Wave -> (16-row block, set of 16-column tiles) for an output of nrb row
 // blocks and `tiles` column tiles: waves w and w + nrb share a row block and
 // take every (4 / nrb)-th column tile.  Returns the number of tiles (0 for
@@ -416,26 +470,44 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
     }
 
     // ---- 1. Q, K, V slices -> LDS.  Thread t owns 4-element column group
-    // t % vpr of rows t / vpr + k * rstep of each tensor, so the addresses of
-    // its loads step by a uniform stride.  Each round issues up to kQ row
-    // loads of Q and kKV of K and of V before the first is encoded and
-    // stored.  Rows past the sequence (up to MQ / NK) and columns past D are
-    // stored as zeros.  (The host sends this kernel only shapes with
-    // D % 4 == 0 and aligned bases, so a vector is in or out.)
+    // t % vpr of rows t / vpr + k * rstep of each tensor.  Loads are raw
+    // buffer loads over each tensor's rows of this group or head, so rows
+    // past the sequence read as zeros without a branch (a column past D
+    // gets an offset past the buffer); branch-free loads let the compiler
+    // count them, so a round issues up to kQ row loads of Q and kKV of K and
+    // of V before the first is encoded and stored, and when everything fits
+    // one round, V is only written to LDS after the exchange (its latency
+    // hides behind the exchange's).  (The host sends this kernel only shapes
+    // with D % 4 == 0 and aligned bases.)
+    typedef typename Raw4<T>::type Raw;
+    constexpr int kQ = 8, kKV = 16;
+    const int vpr = dc >> 2;
+    const int rstep = kThreads / vpr;
+    const int cg = tid % vpr, r0 = tid / vpr;
+    const int col = cg * 4, d = d0 + col;
+    const bool lane_ok = r0 < rstep && d < D;
+    const int cq = r0 < rstep ? (MQ - r0 + rstep - 1) / rstep : 0;
+    const int ckv = r0 < rstep ? (NK - r0 + rstep - 1) / rstep : 0;
+    const bool defer_v = (MQ + rstep - 1) / rstep <= kQ && (NK + rstep - 1) / rstep <= kKV;
+    Raw bv[kKV];
+    auto store_v = [&](int row, Raw raw) {
+        if constexpr (kBf16) {
+            // the raw bf16 bits, [key][dim]
+            *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(smem + g.v_off) +
+                                      row * g.vstr + col) = raw;
+        } else {
+            float* dst = reinterpret_cast<float*>(smem + g.v_off) + row * g.vstr + col;
+            *reinterpret_cast<float2*>(dst) = make_float2(raw.x, raw.y);
+            *reinterpret_cast<float2*>(dst + 2) = make_float2(raw.z, raw.w);
+        }
+    };
     {
-        typedef typename Raw4<T>::type Raw;
-        constexpr int kQ = 8, kKV = 16;
-        const int vpr = dc >> 2;
-        const int rstep = kThreads / vpr;
-        const int cg = tid % vpr, r0 = tid / vpr;
-        const int col = cg * 4, d = d0 + col;
-        const bool lane_ok = r0 < rstep && d < D;
-        const int cq = r0 < rstep ? (MQ - r0 + rstep - 1) / rstep : 0;
-        const int ckv = r0 < rstep ? (NK - r0 + rstep - 1) / rstep : 0;
-        const size_t gstep = (size_t)rstep * D;
-        const T* qp = Q + (size_t)r0 * D + d;
-        const T* kp = K + (size_t)r0 * D + d;
-        const T* vp = V + (size_t)r0 * D + d;
+        constexpr int es = (int)sizeof(T);
+        constexpr int kOob = 0x7ffffff0;  // past every buffer
+        const __amdgpu_buffer_rsrc_t rq = make_rsrc(Q, Lq * D * es);
+        const __amdgpu_buffer_rsrc_t rk = make_rsrc(K, Lk * D * es);
+        const __amdgpu_buffer_rsrc_t rv = make_rsrc(V, Lk * D * es);
+        const int off0 = (r0 * D + d) * es, ostep = rstep * D * es;
         // one encoded row vector of Q (isq) or K into its LDS rows
         auto store_qk = [&](bool isq, int row, float4 f) {
             const float e4[4] = {f.x, f.y, f.z, f.w};
@@ -464,57 +536,52 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
                 *reinterpret_cast<float2*>(dst + 2) = make_float2(e4[2], e4[3]);
             }
         };
-        auto store_v = [&](int row, Raw raw) {
-            if constexpr (kBf16) {
-                // transposed [dim][key]: the raw bf16 bits go straight in
-                uint16_t* vt = reinterpret_cast<uint16_t*>(smem + g.v_off) + col * g.vstr + row;
-                vt[0] = (uint16_t)raw.x;
-                vt[g.vstr] = (uint16_t)(raw.x >> 16);
-                vt[2 * g.vstr] = (uint16_t)raw.y;
-                vt[3 * g.vstr] = (uint16_t)(raw.y >> 16);
-            } else {
-                float* dst = reinterpret_cast<float*>(smem + g.v_off) + row * g.vstr + col;
-                *reinterpret_cast<float2*>(dst) = make_float2(raw.x, raw.y);
-                *reinterpret_cast<float2*>(dst + 2) = make_float2(raw.z, raw.w);
-            }
-        };
-        for (int j = 0; j * kQ < cq || j * kKV < ckv; ++j) {
-            Raw bq[kQ], bk[kKV], bv[kKV];
+        // round j: loads of Q rows j*kQ.. and K/V rows j*kKV.. (all in
+        // flight), then Q and K (and, unless deferred, V) into LDS
+        auto round = [&](int j, Raw (&vr)[kKV], bool store_v_now) {
+            Raw bq[kQ], bk[kKV];
+#pragma unroll
+            for (int u = 0; u < kQ; ++u)
+                bq[u] = Raw4<T>::ld_buf(rq, lane_ok ? off0 + (j * kQ + u) * ostep : kOob);
+            // all K loads, then all V loads: the K stores below wait only for
+            // the loads issued before the last K load
+#pragma unroll
+            for (int u = 0; u < kKV; ++u)
+                bk[u] = Raw4<T>::ld_buf(rk, lane_ok ? off0 + (j * kKV + u) * ostep : kOob);
+#pragma unroll
+            for (int u = 0; u < kKV; ++u)  // volatile: issued here, not sunk to the use
+                vr[u] = Raw4<T>::template ld_buf<kAuxVolatile>(
+                    rv, lane_ok ? off0 + (j * kKV + u) * ostep : kOob);
 #pragma unroll
             for (int u = 0; u < kQ; ++u) {
                 const int k = j * kQ + u, row = r0 + k * rstep;
-                bq[u] = Raw4<T>::zero();
-                if (lane_ok && k < cq && row < Lq) bq[u] = Raw4<T>::ld(qp + k * gstep);
-            }
-#pragma unroll
-            for (int u = 0; u < kKV; ++u) {
-                const int k = j * kKV + u, row = r0 + k * rstep;
-                bk[u] = Raw4<T>::zero();
-                bv[u] = Raw4<T>::zero();
-                if (lane_ok && k < ckv && row < Lk) {
-                    bk[u] = Raw4<T>::ld(kp + k * gstep);
-                    bv[u] = Raw4<T>::ld(vp + k * gstep);
+                if (k < cq) {
+                    float4 f = Raw4<T>::f4(bq[u]);
+                    if constexpr (PEK != kPeNone)
+                        if (lane_ok && row < Lq)
+                            f = encode4<T, PEK>(f, Q + (size_t)row * D, q0 + row, d, a.pq);
+                    store_qk(true, row, f);
                 }
             }
 #pragma unroll
-            for (int u = 0; u < kQ; ++u) {
-                const int k = j * kQ + u, row = r0 + k * rstep;
-                if (k >= cq) break;
-                float4 f = Raw4<T>::f4(bq[u]);
-                if constexpr (PEK != kPeNone)
-                    if (lane_ok && row < Lq)
-                        f = encode4<T, PEK>(f, Q + (size_t)row * D, q0 + row, d, a.pq);
-                store_qk(true, row, f);
-            }
-#pragma unroll
             for (int u = 0; u < kKV; ++u) {
                 const int k = j * kKV + u, row = r0 + k * rstep;
-                if (k >= ckv) break;
-                float4 f = Raw4<T>::f4(bk[u]);
-                if constexpr (PEK != kPeNone)
-                    if (lane_ok && row < Lk) f = encode4<T, PEK>(f, K + (size_t)row * D, row, d, a.pk);
-                store_qk(false, row, f);
-                store_v(row, bv[u]);
+                if (k < ckv) {
+                    float4 f = Raw4<T>::f4(bk[u]);
+                    if constexpr (PEK != kPeNone)
+                        if (lane_ok && row < Lk)
+                            f = encode4<T, PEK>(f, K + (size_t)row * D, row, d, a.pk);
+                    store_qk(false, row, f);
+                    if (store_v_now) store_v(row, vr[u]);
+                }
+            }
+        };
+        if (defer_v) {
+            round(0, bv, false);
+        } else {
+            for (int j = 0; j * kQ < cq || j * kKV < ckv; ++j) {
+                Raw vr[kKV];
+                round(j, vr, true);
             }
         }
     }
@@ -763,55 +830,85 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
             __hip_atomic_store(a.epochs + rg, epoch + 1u, __ATOMIC_RELAXED,
                                __HIP_MEMORY_SCOPE_AGENT);
     }
+    if (defer_v) {
+#pragma unroll
+        for (int u = 0; u < kKV; ++u)
+            if (u < ckv) store_v(r0 + u * rstep, bv[u]);
+    }
     __syncthreads();
 
-    // ---- 4. softmax of scale * S: one quad of threads per row, each thread
-    // every fourth column; quad DPP reductions; P to its own LDS region
+    // ---- 4. softmax of scale * S: T = 16, 8 or 4 consecutive threads per
+    // row (as many as 256 threads allow for MQ rows), each a run of NK / T
+    // columns; DPP reductions within the T lanes; P to its own LDS region
     {
-        const int i = tid >> 2, q4 = tid & 3;
-        const bool row_ok = i < Lq;
-        auto run = [&](auto cnt_tag) {
-            constexpr int C4 = decltype(cnt_tag)::value;  // NK / 4
-            float v[C4];
+        auto run = [&](auto t_tag, auto w_tag) {
+            constexpr int TT = decltype(t_tag)::value, W = decltype(w_tag)::value;
+            const int i = tid / TT, j0 = (tid % TT) * W;
+            if (i >= MQ) return;  // whole waves (MQ * TT is a multiple of 64)
+            const bool row_ok = i < Lq;
+            float v[W];
             float m = -INFINITY;
 #pragma unroll
-            for (int u = 0; u < C4; ++u) {
-                const int j = q4 + 4 * u;
-                v[u] = (row_ok && j < Lk) ? S[i * g.sstr + j] * a.scale : -INFINITY;
-                m = fmaxf(m, v[u]);
+            for (int u = 0; u < W; u += 2) {
+                const float2 x = *reinterpret_cast<const float2*>(&S[i * g.sstr + j0 + u]);
+                v[u] = (row_ok && j0 + u < Lk) ? x.x * a.scale : -INFINITY;
+                v[u + 1] = (row_ok && j0 + u + 1 < Lk) ? x.y * a.scale : -INFINITY;
+                m = fmaxf(m, fmaxf(v[u], v[u + 1]));
             }
             m = fmaxf(m, dpp<kDppQuadXor1>(m));
             m = fmaxf(m, dpp<kDppQuadXor2>(m));
+            if constexpr (TT >= 8) m = fmaxf(m, dpp<kDppRowHalfMirror>(m));
+            if constexpr (TT >= 16) m = fmaxf(m, dpp<kDppRowMirror>(m));
             float l = 0.f;
 #pragma unroll
-            for (int u = 0; u < C4; ++u) {
+            for (int u = 0; u < W; ++u) {
                 v[u] = row_ok ? __expf(v[u] - m) : 0.f;
                 l += v[u];
             }
             l += dpp<kDppQuadXor1>(l);
             l += dpp<kDppQuadXor2>(l);
+            if constexpr (TT >= 8) l += dpp<kDppRowHalfMirror>(l);
+            if constexpr (TT >= 16) l += dpp<kDppRowMirror>(l);
             const float inv = row_ok ? 1.0f / l : 0.f;
-            if (i < MQ) {
 #pragma unroll
-                for (int u = 0; u < C4; ++u) {
-                    const int j = q4 + 4 * u;
-                    const float p = v[u] * inv;
-                    if constexpr (kBf16) {
-                        uint16_t* ph = reinterpret_cast<uint16_t*>(smem + g.p_off);
-                        const uint16_t hi = f32_to_bf16_bits(p);
-                        ph[i * g.pstr + j] = hi;
-                        ph[(MQ + i) * g.pstr + j] = f32_to_bf16_bits(p - bf16_bits_to_f32(hi));
-                    } else {
-                        reinterpret_cast<float*>(smem + g.p_off)[i * g.pstr + j] = p;
-                    }
+            for (int u = 0; u < W; u += 2) {
+                const float p0 = v[u] * inv, p1 = v[u + 1] * inv;
+                if constexpr (kBf16) {
+                    uint16_t* ph = reinterpret_cast<uint16_t*>(smem + g.p_off);
+                    const uint16_t h0 = f32_to_bf16_bits(p0), h1 = f32_to_bf16_bits(p1);
+                    *reinterpret_cast<uint32_t*>(&ph[i * g.pstr + j0 + u]) =
+                        (uint32_t)h0 | ((uint32_t)h1 << 16);
+                    *reinterpret_cast<uint32_t*>(&ph[(MQ + i) * g.pstr + j0 + u]) =
+                        pack_bf16x2(p0 - bf16_bits_to_f32(h0), p1 - bf16_bits_to_f32(h1));
+                } else {
+                    *reinterpret_cast<float2*>(
+                        &reinterpret_cast<float*>(smem + g.p_off)[i * g.pstr + j0 + u]) =
+                        make_float2(p0, p1);
                 }
             }
         };
-        switch (NK) {
-            case 32: run(std::integral_constant<int, 8>{}); break;
-            case 64: run(std::integral_constant<int, 16>{}); break;
-            case 96: run(std::integral_constant<int, 24>{}); break;
-            default: run(std::integral_constant<int, 32>{}); break;
+        using std::integral_constant;
+        if (MQ <= 16) {
+            switch (NK) {
+                case 32: run(integral_constant<int, 16>{}, integral_constant<int, 2>{}); break;
+                case 64: run(integral_constant<int, 16>{}, integral_constant<int, 4>{}); break;
+                case 96: run(integral_constant<int, 16>{}, integral_constant<int, 6>{}); break;
+                default: run(integral_constant<int, 16>{}, integral_constant<int, 8>{}); break;
+            }
+        } else if (MQ <= 32) {
+            switch (NK) {
+                case 32: run(integral_constant<int, 8>{}, integral_constant<int, 4>{}); break;
+                case 64: run(integral_constant<int, 8>{}, integral_constant<int, 8>{}); break;
+                case 96: run(integral_constant<int, 8>{}, integral_constant<int, 12>{}); break;
+                default: run(integral_constant<int, 8>{}, integral_constant<int, 16>{}); break;
+            }
+        } else {
+            switch (NK) {
+                case 32: run(integral_constant<int, 4>{}, integral_constant<int, 8>{}); break;
+                case 64: run(integral_constant<int, 4>{}, integral_constant<int, 16>{}); break;
+                case 96: run(integral_constant<int, 4>{}, integral_constant<int, 24>{}); break;
+                default: run(integral_constant<int, 4>{}, integral_constant<int, 32>{}); break;
+            }
         }
     }
     __syncthreads();
@@ -833,10 +930,9 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
                 if constexpr (kBf16) {
                     const uint16_t* ph = reinterpret_cast<const uint16_t*>(smem + g.p_off) +
                                          (rb * 16 + lr) * g.pstr + lk * 8;
-                    const uint16_t* vt = reinterpret_cast<const uint16_t*>(smem + g.v_off) +
-                                         (tc * 16 + lr) * g.vstr + lk * 8;
-                    mma_bf16<NT, true, false>(ph, ph + MQ * g.pstr, vt, vt, step * g.vstr, NK,
-                                              acc);
+                    const uint16_t* vb = reinterpret_cast<const uint16_t*>(smem + g.v_off) +
+                                         tc * 16;
+                    mma_bf16_vt<NT>(ph, ph + MQ * g.pstr, vb, g.vstr, step, NK, acc);
                 } else {
                     const float* pp = reinterpret_cast<const float*>(smem + g.p_off) +
                                       (rb * 16 + lr) * g.pstr + lk;
