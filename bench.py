@@ -39,7 +39,7 @@ HBM_PEAK_GBS = 8000.0
 # FETCH_SIZE / WRITE_SIZE and scaled by a known-size device copy
 # (profiles/fused_small_cfg2_traffic.md).  Keyed by (config, head_dim).
 MEASURED_TRAFFIC_BYTES = {
-    (2, 2048): (11316 + 6224) * 1024,
+    (2, 2048): (14845 + 3081) * 1024,
 }
 BF16_PEAK_TFLOPS = 2500.0
 FP32_PEAK_TFLOPS = 157.3
