@@ -1,0 +1,179 @@
+"""Context numbers: this library next to PyTorch-ROCm on the same MI355X.
+
+    python accelerated-final-project_amd/torch_compare.py [--iters 100] [--json out.json]
+
+The reference's PyTorch harness (final/benchmark_pytorch_wrapper.cu:25-130)
+times F.scaled_dot_product_attention ("optimized") and matmul -> softmax ->
+matmul ("naive") on its four head-dim shapes, 10 warm-up and 100 timed
+calls between CUDA events.  This does the same on the MI355X for those four
+shapes and the BASELINE configurations, and puts this library's
+atn_attention_fwd_ex beside them: all three run on the same device tensors
+and on torch's current stream, timed by the same events.  For the RoPE
+(rotate-half) and sinusoidal configurations the torch side encodes Q and K
+with elementwise ops from tables built the way the reference builds its
+caches (final/rope.cu:20-40, final/sinusoidal.cu:838-855), then attends.
+
+The printed max |difference| against torch SDPA is context only; parity is
+established against the CPU oracle by the test suite.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+if HERE not in sys.path:
+    sys.path.insert(0, HERE)
+
+# (name, dtype, B, H, Lq, Lk, D, pe); the first four are the reference
+# harness's shapes (fp32, no encoding), then BASELINE configs 1-5
+SHAPES = [
+    ("ref hdim=512", "f32", 1, 4, 64, 64, 512, "none"),
+    ("ref hdim=2048", "f32", 1, 4, 64, 64, 2048, "none"),
+    ("ref hdim=4096", "f32", 1, 2, 32, 32, 4096, "none"),
+    ("ref hdim=8192", "f32", 1, 1, 16, 16, 8192, "none"),
+    ("cfg1", "f32", 1, 1, 4, 4, 8, "none"),
+    ("cfg2", "f32", 1, 4, 64, 64, 2048, "none"),
+    ("cfg3", "bf16", 1, 4, 32, 128, 8192, "none"),
+    ("cfg4 rope-half", "bf16", 8, 8, 1024, 1024, 4096, "rope_half"),
+    ("cfg5 sinusoidal", "bf16", 4, 16, 256, 2048, 1024, "sinusoidal"),
+]
+
+
+def tables(torch, pe, npos, D, dev):
+    """fp32 encoding tables [npos][D/2] with the reference's expressions."""
+    pos = torch.arange(npos, dtype=torch.float32, device=dev)[:, None]
+    i = torch.arange(D // 2, dtype=torch.float32, device=dev)[None, :]
+    freq = 1.0 / torch.pow(torch.tensor(10000.0, device=dev), (2.0 * i) / D)
+    ang = pos * freq
+    return torch.cos(ang), torch.sin(ang)
+
+
+def torch_encode(torch, x, pe, cos, sin):
+    """Encoded copy of x [B,H,L,D] (fp32 math, cast back to x's dtype)."""
+    L, D = x.shape[2], x.shape[3]
+    xf = x.float()
+    if pe == "rope_half":
+        c, s = cos[:L], sin[:L]
+        x1, x2 = xf[..., : D // 2], xf[..., D // 2:]
+        y = torch.cat([x1 * c - x2 * s, x2 * c + x1 * s], dim=-1)
+    else:  # sinusoidal: even dims + sin, odd dims + cos
+        pe_t = torch.stack([sin[:L], cos[:L]], dim=-1).reshape(L, D)
+        y = xf + pe_t
+    return y.to(x.dtype)
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--iters", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--json", default="")
+    a = ap.parse_args()
+
+    import torch
+    import torch.nn.functional as F
+
+    import attn_mi355x as am
+
+    if not torch.cuda.is_available():
+        print("torch_compare.py: no GPU visible to torch", file=sys.stderr)
+        sys.exit(1)
+    dev = torch.device("cuda:0")
+    lib = am.lib()
+    print(f"GPU: {torch.cuda.get_device_name(0)}  torch {torch.__version__}  "
+          f"HIP {torch.version.hip}", flush=True)
+
+    def timed(fn):
+        for _ in range(a.warmup):
+            fn()
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(a.iters):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / a.iters
+
+    rows = []
+    g = torch.Generator(device=dev).manual_seed(0)
+    for name, dt, B, H, Lq, Lk, D, pe in SHAPES:
+        tdt = torch.float32 if dt == "f32" else torch.bfloat16
+        sigma = 0.5 if pe == "sinusoidal" else 1.0
+        Q = (torch.randn(B, H, Lq, D, device=dev, generator=g) * sigma).to(tdt)
+        K = (torch.randn(B, H, Lk, D, device=dev, generator=g) * sigma).to(tdt)
+        V = (torch.randn(B, H, Lk, D, device=dev, generator=g) * sigma).to(tdt)
+        out = torch.empty_like(Q)
+        desc = None
+        if pe == "rope_half":
+            desc = am.make_pe("rope", pairing="half")
+        elif pe == "sinusoidal":
+            desc = am.make_pe("sinusoidal")
+        dcode = am.ATN_DTYPE_F32 if dt == "f32" else am.ATN_DTYPE_BF16
+        nbytes = lib.atn_attention_workspace_bytes(dcode, B, H, Lq, Lk, D,
+                                                   ctypes.byref(desc) if desc else None)
+        ws = torch.zeros(max(nbytes, 4) // 4 + 1, dtype=torch.float32, device=dev)
+        if desc is not None:
+            st = lib.atn_prepare_pe_ex(ctypes.byref(desc), D, max(Lq, Lk))
+            if st != am.ATN_OK:
+                raise am.AtnError(st, "atn_prepare_pe_ex")
+
+        def ours():
+            st = lib.atn_attention_fwd_ex(
+                dcode, ctypes.c_void_p(Q.data_ptr()), ctypes.c_void_p(K.data_ptr()),
+                ctypes.c_void_p(V.data_ptr()), ctypes.c_void_p(out.data_ptr()), B, H, Lq, Lk, D,
+                ctypes.byref(desc) if desc else None, ctypes.c_void_p(ws.data_ptr()),
+                ws.numel() * 4, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+            if st != am.ATN_OK:
+                raise am.AtnError(st, "atn_attention_fwd_ex")
+
+        if pe == "none":
+            def enc():
+                return Q, K
+        else:
+            cos, sin = tables(torch, pe, max(Lq, Lk), D, dev)
+
+            def enc():
+                return torch_encode(torch, Q, pe, cos, sin), torch_encode(torch, K, pe, cos, sin)
+
+        def sdpa():
+            q, k = enc()
+            return F.scaled_dot_product_attention(q, k, V)
+
+        scale = 1.0 / (D ** 0.5)
+
+        def naive():
+            q, k = enc()
+            s = torch.matmul(q, k.transpose(-2, -1).contiguous()) * scale
+            return torch.matmul(F.softmax(s, dim=-1), V)
+
+        t_ours = timed(ours)
+        t_sdpa = timed(sdpa)
+        t_naive = timed(naive)
+        ours()
+        ref = sdpa()
+        torch.cuda.synchronize()
+        diff = float((out.float() - ref.float()).abs().max())
+        flops = 4 * B * H * Lq * Lk * D
+        alg_bytes = (2 * B * H * Lq * D + 2 * B * H * Lk * D) * (4 if dt == "f32" else 2)
+        row = {"shape": name, "dtype": dt, "B": B, "H": H, "Lq": Lq, "Lk": Lk, "D": D, "pe": pe,
+               "ours_ms": t_ours, "torch_sdpa_ms": t_sdpa, "torch_naive_ms": t_naive,
+               "ours_tflops": flops / t_ours / 1e9, "ours_gbs": alg_bytes / t_ours / 1e6,
+               "speedup_vs_sdpa": t_sdpa / t_ours, "max_abs_diff_vs_sdpa": diff}
+        rows.append(row)
+        print(f"{name:16s} {dt:4s} ours {t_ours:9.4f} ms  sdpa {t_sdpa:9.4f} ms  "
+              f"naive {t_naive:9.4f} ms  x{t_sdpa / t_ours:6.2f} vs sdpa  "
+              f"{row['ours_tflops']:8.2f} TFLOP/s  max|d| {diff:.2e}", flush=True)
+        del Q, K, V, out, ws
+        torch.cuda.empty_cache()
+    if a.json:
+        with open(a.json, "w") as f:
+            json.dump(rows, f, indent=1)
+
+
+if __name__ == "__main__":
+    main()
