@@ -437,13 +437,16 @@ FusedPlan fused_plan(int dtype, int pek, const Shape& s, bool query_device) {
 
 // ---------------------------------------------------------------- gemm plan
 // Long-sequence bf16 shapes: two MFMA GEMMs around an exact row softmax.
-// Workspace after the sync region: encoded Q and K (bf16, only for the sides
-// a positional encoding applies to), S (fp32), P (bf16).
+// Workspace after the sync region: encoded Q and K (fp16 with per-row
+// scales, when a positional encoding is on), E = exp(S - tile row max)
+// (fp16), per-(row, 256-key tile) max, sum and softmax factor (fp32).
 constexpr int kGemmMinL = 128;
 
 struct GemmPlan {
     bool ok = false, encoded = false;
-    size_t q_off = 0, k_off = 0, qs_off = 0, ks_off = 0, s_off = 0, p_off = 0, bytes = 0;
+    int tiles_k = 0;  // 256-key tiles per score row
+    size_t q_off = 0, k_off = 0, qs_off = 0, ks_off = 0, e_off = 0, m_off = 0, l_off = 0,
+           g_off = 0, bytes = 0;
 };
 
 GemmPlan gemm_plan(int dtype, const Shape& s, const PePlan& plan) {
@@ -465,8 +468,12 @@ GemmPlan gemm_plan(int dtype, const Shape& s, const PePlan& plan) {
         p.qs_off = take((size_t)s.BH * s.Lq * 4);
         p.ks_off = take((size_t)s.BH * s.Lk * 4);
     }
-    p.s_off = take((size_t)s.BH * s.Lq * s.Lk * 4);
-    p.p_off = take((size_t)s.BH * s.Lq * s.Lk * 2);
+    p.tiles_k = (int)((s.Lk + 255) / 256);
+    const size_t stats = (size_t)s.BH * s.Lq * p.tiles_k * 4;
+    p.e_off = take((size_t)s.BH * s.Lq * s.Lk * 2);
+    p.m_off = take(stats);
+    p.l_off = take(stats);
+    p.g_off = take(stats);
     p.bytes = off;
     p.ok = true;
     return p;
@@ -547,12 +554,14 @@ int attention_core(int dtype, const void* Q, const void* K, const void* V, void*
             qinv = qs;
             kinv = ks;
         }
-        float* S = reinterpret_cast<float*>(w + gp.s_off);
-        uint16_t* P = reinterpret_cast<uint16_t*>(w + gp.p_off);
-        ATN_HIP(atn::launch_gemm_qk(gp.encoded ? 1 : 0, qe, ke, qinv, kinv, S, (int)s.BH, Lq, Lk, D,
-                                    scale, stream));
-        ATN_HIP(atn::launch_softmax_bf16(S, P, s.BH * Lq, Lk, stream));
-        ATN_HIP(atn::launch_gemm_pv(P, static_cast<const uint16_t*>(V),
+        uint16_t* E = reinterpret_cast<uint16_t*>(w + gp.e_off);
+        float* st_m = reinterpret_cast<float*>(w + gp.m_off);
+        float* st_l = reinterpret_cast<float*>(w + gp.l_off);
+        float* ga = reinterpret_cast<float*>(w + gp.g_off);
+        ATN_HIP(atn::launch_gemm_qk(gp.encoded ? 1 : 0, qe, ke, qinv, kinv, E, st_m, st_l,
+                                    (int)s.BH, Lq, Lk, D, scale, stream));
+        ATN_HIP(atn::launch_rowscale(st_m, st_l, ga, s.BH * Lq, gp.tiles_k, stream));
+        ATN_HIP(atn::launch_gemm_pv(E, ga, static_cast<const uint16_t*>(V),
                                     static_cast<uint16_t*>(out), (int)s.BH, Lq, Lk, D, stream));
         return ATN_OK;
     }

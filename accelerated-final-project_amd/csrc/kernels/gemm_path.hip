@@ -9,10 +9,17 @@
 //
 //   k_encode_f16  (with a positional encoding) Q~, K~ = encoded Q, K as
 //                 fp16 rows with a power-of-two scale per row
-//   k_gemm  (NT)  S = scale * Q K^T            (fp32 S to the workspace)
-//   k_softmax_bf  P = softmax(S) per row       (exact: max, exp, sum, divide;
-//                                               bf16 P)
-//   k_gemm  (NN)  O = P V                      (bf16 O)
+//   k_gemm  (NT)  S = scale * Q K^T, kept on chip; per row of its 256-key
+//                 tile t the epilogue writes E = exp(S - m_t) (fp16, in
+//                 (0, 1]) and the tile's max m_t and sum l_t of E
+//   k_rowscale    per row: m = max_t m_t, l = sum_t l_t exp(m_t - m), and
+//                 g_t = exp(m_t - m) / l
+//   k_gemm  (NN)  O = P V with P = E g_t, applied to each A chunk on its
+//                 way to LDS (bf16 P, bf16 O)
+//
+// so the row softmax is exact (max, exp, sum, divide as in the reference,
+// final/attention.cu:262-270) without an S round trip through HBM; every
+// stored value is in (0, 1], for any input range.
 //
 // Plain bf16 inputs are exact MFMA operands.  Encoded rows are not bf16
 // values any more; rounding them back to bf16 (8-bit mantissa) costs up to
@@ -113,8 +120,51 @@ __device__ __forceinline__ void sched_mfma_reads() {
 }
 
 // Epilogue selectors
-constexpr int kOutScoresF32 = 0;  // C = scale * acc, fp32, row stride ldc
+constexpr int kOutExpF16 = 0;     // C = fp16 exp(S - tile row max), S = scale * acc; stats
 constexpr int kOutBf16 = 1;       // C = bf16(acc), row stride ldc
+
+// fp16 bits of the 8 elements of w, times f, as 8 bf16.  Each product is
+// one v_fma_mix_f32 (an fp16 half of a register widened and multiplied in
+// fp32, with a zero addend: the rounding of the product itself), and each
+// pair is rounded to bf16 (nearest even) by gfx950's v_cvt_pk_bf16_f32.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ float f16lo_mul(uint32_t x, float f) {
+    float r;
+    asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(x), "v"(f));
+    return r;
+}
+__device__ __forceinline__ float f16hi_mul(uint32_t x, float f) {
+    float r;
+    asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(x), "v"(f));
+    return r;
+}
+__device__ __forceinline__ uint4 scale_f16x8_to_bf16(const uint4& w, float f) {
+    const uint32_t x[4] = {w.x, w.y, w.z, w.w};
+    uint32_t y[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const bf16x2_t b = {(__bf16)f16lo_mul(x[i], f), (__bf16)f16hi_mul(x[i], f)};
+        y[i] = __builtin_bit_cast(uint32_t, b);
+    }
+    return make_uint4(y[0], y[1], y[2], y[3]);
+}
+
+// Max / sum over each half-wave (lanes with the same lane / 32): DPP within
+// quads, 8 and 16 lanes, then the 16-lane hop by ds_swizzle.
+__device__ __forceinline__ float half_max(float v) {
+    v = fmaxf(v, dpp<kDppQuadXor1>(v));
+    v = fmaxf(v, dpp<kDppQuadXor2>(v));
+    v = fmaxf(v, dpp<kDppRowHalfMirror>(v));
+    v = fmaxf(v, dpp<kDppRowMirror>(v));
+    return fmaxf(v, swz_xor16(v));
+}
+__device__ __forceinline__ float half_sum(float v) {
+    v += dpp<kDppQuadXor1>(v);
+    v += dpp<kDppQuadXor2>(v);
+    v += dpp<kDppRowHalfMirror>(v);
+    v += dpp<kDppRowMirror>(v);
+    return v + swz_xor16(v);
+}
 
 // C[M x N] = A[M x K] * B^T where B is [N x K] (NT, both K-contiguous) when
 // B_NN == false, or A[M x K] * B with B [K x N] N-contiguous when B_NN.
@@ -125,6 +175,10 @@ struct GemmArgs {
     void* C;
     const float* rs;              // optional per-row scales [heads][M] (or NULL)
     const float* cs;              // optional per-column scales [heads][N] (or NULL)
+    float* st_m;                  // NT exp epilogue: tile row maxima [heads][M][tiles_n]
+    float* st_l;                  // NT exp epilogue: tile row sums of E [heads][M][tiles_n]
+    const float* ga;              // NN: factors of A's rows per 256-column tile [heads][M][gt]
+    int gt;                       // NN: 256-column tiles per row of A
     int M, N, K;
     long lda, ldb, ldc;           // row strides (elements)
     long sa, sb, sc;              // head strides (elements)
@@ -132,11 +186,17 @@ struct GemmArgs {
     float scale;
 };
 
-template <bool F16, bool B_NN, int OUT>
+// NN softmax factors of A's rows: kept in LDS ([256 rows][gt], read when a
+// chunk is stored) when a row has at most kFacTiles 256-key tiles, else
+// loaded with each chunk into the register stage.
+constexpr int kFacTiles = 8;
+
+template <bool F16, bool B_NN, int OUT, bool FAC_LDS = false>
 __global__ __launch_bounds__(kGemmThreads) void k_gemm(GemmArgs g) {
     // one LDS block: A stages 0/1, then B^T stages 0/1 ([n][k] rows); the
     // bf16 epilogue reuses it whole as an output staging tile
     __shared__ __align__(16) uint16_t lds[4 * kTileElems];
+    __shared__ float fac[FAC_LDS ? kBM * kFacTiles : 1];
     uint16_t(*As)[kTileElems] = reinterpret_cast<uint16_t(*)[kTileElems]>(lds);
     uint16_t(*Bs)[kTileElems] = reinterpret_cast<uint16_t(*)[kTileElems]>(lds + 2 * kTileElems);
 
@@ -176,6 +236,7 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm(GemmArgs g) {
     static_assert(kBK * kBN <= kTileElems, "NN B tile does not fit its LDS stage");
     struct Stage {
         uint4 a[kChunks], b[kChunks];
+        float ga[(B_NN && !FAC_LDS) ? kChunks : 1];  // NN: factor of each A chunk
     };
     // A tile that lies inside the matrices (EDGE false) loads without bounds
     // checks: straight-line code that the scheduler can spread among the
@@ -191,12 +252,20 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm(GemmArgs g) {
         const uint32_t off = (uint32_t)r * (uint32_t)ld + (uint32_t)c;
         return *reinterpret_cast<const uint4*>(base + off);
     };
+    const float* ga = B_NN ? g.ga + (long)bh * g.M * g.gt : nullptr;
     auto load_stage = [&](Stage& r, int k0, auto edge) {
 #pragma unroll
         for (int u = 0; u < kChunks; ++u) {
             const int cidx = tid + u * kGemmThreads;
             const int row = cidx / kChunkPerRow, k8 = (cidx % kChunkPerRow) * 8;
             r.a[u] = load_chunk(A, g.lda, m0 + row, k0 + k8, g.M, g.K, edge);
+            if constexpr (B_NN && !FAC_LDS) {
+                // a chunk's 8 keys lie in one 256-key tile of the scores
+                const int gr = m0 + row;
+                r.ga[u] = 0.f;
+                if (!decltype(edge)::value || gr < g.M)
+                    r.ga[u] = ga[(uint32_t)gr * (uint32_t)g.gt + (uint32_t)((k0 + k8) >> 8)];
+            }
         }
 #pragma unroll
         for (int u = 0; u < kChunks; ++u) {
@@ -211,12 +280,23 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm(GemmArgs g) {
             }
         }
     };
-    auto store_stage = [&](const Stage& r, int s) {
+    auto store_stage = [&](const Stage& r, int s, int k0) {
 #pragma unroll
         for (int u = 0; u < kChunks; ++u) {
             const int cidx = tid + u * kGemmThreads;
             const int row = cidx / kChunkPerRow, k8 = (cidx % kChunkPerRow) * 8;
-            *reinterpret_cast<uint4*>(&As[s][row * kLdsRow + k8]) = r.a[u];
+            if constexpr (B_NN) {  // P = E * g: fp16 E scaled, rounded to bf16
+                float f;
+                if constexpr (FAC_LDS)
+                    f = fac[row * kFacTiles + ((k0 + k8) >> 8)];
+                else
+                    f = r.ga[u];
+                *reinterpret_cast<uint4*>(&As[s][row * kLdsRow + k8]) =
+                    scale_f16x8_to_bf16(r.a[u], f);
+            } else {
+                (void)k0;
+                *reinterpret_cast<uint4*>(&As[s][row * kLdsRow + k8]) = r.a[u];
+            }
         }
 #pragma unroll
         for (int u = 0; u < kChunks; ++u) {
@@ -310,7 +390,7 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm(GemmArgs g) {
         // sub-step 0: MFMAs on f0, read f1, write step kt + 1's tile
         read_frag(f1, s, 16);
         mma(f0);
-        if constexpr (N1) store_stage(st, s ^ 1);
+        if constexpr (N1) store_stage(st, s ^ 1, (kt + 1) * kBK);
         sched_reads();
         if constexpr (N1) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
@@ -346,8 +426,16 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm(GemmArgs g) {
     auto kloop = [&](auto edge) {
         using T = std::integral_constant<bool, true>;
         using F = std::integral_constant<bool, false>;
+        if constexpr (FAC_LDS) {
+            // this tile's rows' factors: [row][tile], kFacTiles >= gt
+            for (int e = tid; e < kBM * kFacTiles; e += kGemmThreads) {
+                const int r = e / kFacTiles, t = e - r * kFacTiles;
+                fac[e] = (m0 + r < g.M && t < g.gt) ? ga[(long)(m0 + r) * g.gt + t] : 0.f;
+            }
+        }
         load_stage(st, 0, edge);
-        store_stage(st, 0);
+        if constexpr (FAC_LDS) __syncthreads();
+        store_stage(st, 0, 0);
         if (nk > 1) load_stage(st, kBK, edge);
         __syncthreads();
         read_frag(f0, 0, 0);
@@ -393,27 +481,96 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm(GemmArgs g) {
         }
         return;
     }
+    // NT: scores S = scale * acc * (row scale) * (column scale) of this
+    // 256-key tile; per row its maximum m_t over the tile's valid columns and
+    // the sum l_t of E = exp(S - m_t).  A row's 256 columns are 32 lanes x TJ
+    // tiles in each of the two column waves (wave % 2), combined through LDS.
+    if constexpr (OUT == kOutExpF16) {
+    static_assert(!B_NN && WN == 2, "the exp epilogue is the NT product's");
+    __syncthreads();  // every wave is done with the LDS stages
+    float* red = reinterpret_cast<float*>(lds);  // [max | sum][column wave][256 rows]
+    const int half = lane >> 5, lc = lane & 31, cw = wave & 1;
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) {
+        const int col = n0 + wn + j * 32 + lc;
+        const float csc =
+            col < g.N ? (g.cs ? g.cs[(long)bh * g.N + col] * g.scale : g.scale) : 0.f;
+#pragma unroll
+        for (int i = 0; i < TI; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int row = m0 + wm + i * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+                float v = acc[i][j][r] * csc;
+                if (g.rs && row < g.M) v *= g.rs[(long)bh * g.M + row];
+                acc[i][j][r] = col < g.N ? v : -INFINITY;
+            }
+    }
+    float rm[TI][16], rl[TI][16];
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            float m = acc[i][0][r];
+#pragma unroll
+            for (int j = 1; j < TJ; ++j) m = fmaxf(m, acc[i][j][r]);
+            rm[i][r] = half_max(m);
+        }
+    auto rloc = [&](int i, int r) { return wm + i * 32 + 8 * (r >> 2) + 4 * half + (r & 3); };
+    if (lc == 0)
+#pragma unroll
+        for (int i = 0; i < TI; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) red[cw * kBM + rloc(i, r)] = rm[i][r];
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const float m = fmaxf(rm[i][r], red[(cw ^ 1) * kBM + rloc(i, r)]);
+            rm[i][r] = m;
+            float l = 0.f;
+#pragma unroll
+            for (int j = 0; j < TJ; ++j) {
+                // a row with no valid column keeps m = -inf: its E are 0
+                const float e = m == -INFINITY ? 0.f : __expf(acc[i][j][r] - m);
+                acc[i][j][r] = e;
+                l += e;
+            }
+            rl[i][r] = half_sum(l);
+        }
+    if (lc == 0)
+#pragma unroll
+        for (int i = 0; i < TI; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) red[(2 + cw) * kBM + rloc(i, r)] = rl[i][r];
+    __syncthreads();
+    if (cw == 0 && lc == 0)
+#pragma unroll
+        for (int i = 0; i < TI; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int row = m0 + rloc(i, r);
+                if (row >= g.M) continue;
+                const long si = ((long)bh * g.M + row) * g.tiles_n + tn;
+                g.st_m[si] = rm[i][r];
+                g.st_l[si] = rl[i][r] + red[3 * kBM + rloc(i, r)];
+            }
+    uint16_t* C = static_cast<uint16_t*>(g.C) + bh * g.sc;
 #pragma unroll
     for (int i = 0; i < TI; ++i)
 #pragma unroll
         for (int j = 0; j < TJ; ++j) {
-            const int col = n0 + wn + j * 32 + (lane & 31);
+            const int col = n0 + wn + j * 32 + lc;
             if (col >= g.N) continue;
-            const float csc = g.cs ? g.cs[(long)bh * g.N + col] * g.scale : g.scale;
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const int row = m0 + wm + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                if (row >= g.M) continue;
-                const long off = bh * g.sc + (long)row * g.ldc + col;
-                if constexpr (OUT == kOutScoresF32) {
-                    float v = acc[i][j][r] * csc;
-                    if (g.rs) v *= g.rs[(long)bh * g.M + row];
-                    static_cast<float*>(g.C)[off] = v;
-                } else {
-                    static_cast<uint16_t*>(g.C)[off] = f32_to_bf16_bits(acc[i][j][r]);
-                }
+                const int row = m0 + rloc(i, r);
+                if (row < g.M)
+                    C[(long)row * g.ldc + col] =
+                        __builtin_bit_cast(uint16_t, (_Float16)acc[i][j][r]);
             }
         }
+    }
 }
 
 // Encoded rows as fp16 with a power-of-two row scale: pass 1 finds the
@@ -460,70 +617,28 @@ __global__ __launch_bounds__(256) void k_encode_f16(const uint16_t* __restrict__
     }
 }
 
-// P[row] = bf16(softmax(S[row])) for rows of length Lk; one wave per row,
-// three passes over the row (any Lk).
-__global__ __launch_bounds__(256) void k_softmax_bf(const float* __restrict__ S,
-                                                    uint16_t* __restrict__ P, long rows, int Lk) {
-    const int lane = threadIdx.x & 63;
-    const long row = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+// Per row of the scores: m = max_t m_t over its 256-key tiles, l = sum_t
+// l_t exp(m_t - m) (the tiles' E sums brought to the common maximum), and
+// the factor g_t = exp(m_t - m) / l that turns tile t's E into the softmax
+// probabilities.  A row with no valid key (m = -inf) gets g = 0.
+__global__ __launch_bounds__(256) void k_rowscale(const float* __restrict__ st_m,
+                                                  const float* __restrict__ st_l,
+                                                  float* __restrict__ ga, long rows, int T) {
+    const long row = (long)blockIdx.x * 256 + threadIdx.x;
     if (row >= rows) return;
-    const float* s = S + row * Lk;
-    uint16_t* p = P + row * Lk;
+    const float* mr = st_m + row * T;
+    const float* lr = st_l + row * T;
+    float* gr = ga + row * T;
     float m = -INFINITY;
-    for (int j = lane; j < Lk; j += 64) m = fmaxf(m, s[j]);
-    m = wave_max(m);
+    for (int t = 0; t < T; ++t) m = fmaxf(m, mr[t]);
+    if (m == -INFINITY) {
+        for (int t = 0; t < T; ++t) gr[t] = 0.f;
+        return;
+    }
     float l = 0.f;
-    for (int j = lane; j < Lk; j += 64) l += __expf(s[j] - m);
-    l = wave_sum(l);
+    for (int t = 0; t < T; ++t) l += lr[t] * __expf(mr[t] - m);
     const float inv = 1.0f / l;
-    for (int j = lane; j < Lk; j += 64) p[j] = f32_to_bf16_bits(__expf(s[j] - m) * inv);
-}
-
-// The same for Lk % 4 == 0 and Lk <= 256 * NV4: the row is read once, with
-// 16-byte loads, and kept in registers (NV4 float4 per lane); P leaves as
-// 8-byte groups of four bf16.
-template <int NV4>
-__global__ __launch_bounds__(256) void k_softmax_bf_regs(const float* __restrict__ S,
-                                                         uint16_t* __restrict__ P, long rows,
-                                                         int Lk) {
-    const int lane = threadIdx.x & 63;
-    const long row = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (row >= rows) return;
-    const float* s = S + row * Lk;
-    float4 x[NV4];
-    float m = -INFINITY;
-#pragma unroll
-    for (int u = 0; u < NV4; ++u) {
-        const int j = (lane + 64 * u) * 4;
-        x[u] = make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
-        if (j < Lk) x[u] = *reinterpret_cast<const float4*>(s + j);
-        m = fmaxf(m, fmaxf(fmaxf(x[u].x, x[u].y), fmaxf(x[u].z, x[u].w)));
-    }
-    m = wave_max(m);
-    float l = 0.f;
-#pragma unroll
-    for (int u = 0; u < NV4; ++u) {
-        x[u].x = __expf(x[u].x - m);
-        x[u].y = __expf(x[u].y - m);
-        x[u].z = __expf(x[u].z - m);
-        x[u].w = __expf(x[u].w - m);
-        l += (x[u].x + x[u].y) + (x[u].z + x[u].w);
-    }
-    l = wave_sum(l);
-    const float inv = 1.0f / l;
-    uint16_t* p = P + row * Lk;
-#pragma unroll
-    for (int u = 0; u < NV4; ++u) {
-        const int j = (lane + 64 * u) * 4;
-        if (j < Lk) {
-            uint2 w;
-            w.x = (uint32_t)f32_to_bf16_bits(x[u].x * inv) |
-                  ((uint32_t)f32_to_bf16_bits(x[u].y * inv) << 16);
-            w.y = (uint32_t)f32_to_bf16_bits(x[u].z * inv) |
-                  ((uint32_t)f32_to_bf16_bits(x[u].w * inv) << 16);
-            *reinterpret_cast<uint2*>(p + j) = w;
-        }
-    }
+    for (int t = 0; t < T; ++t) gr[t] = __expf(mr[t] - m) * inv;
 }
 
 // Register-resident encoder.  The row is split into 8-element units (for
@@ -709,12 +824,14 @@ __global__ __launch_bounds__(kEncThreads) void k_encode_f16_regs(const uint16_t*
 }  // namespace
 
 hipError_t launch_gemm_qk(int f16, const uint16_t* Q, const uint16_t* K, const float* qinv,
-                          const float* kinv, float* S, int BH, int Lq, int Lk, int D, float scale,
-                          hipStream_t st) {
+                          const float* kinv, uint16_t* E, float* st_m, float* st_l, int BH, int Lq,
+                          int Lk, int D, float scale, hipStream_t st) {
     GemmArgs g{};
     g.A = Q;
     g.B = K;
-    g.C = S;
+    g.C = E;
+    g.st_m = st_m;
+    g.st_l = st_l;
     g.rs = qinv;
     g.cs = kinv;
     g.M = Lq;
@@ -733,10 +850,10 @@ hipError_t launch_gemm_qk(int f16, const uint16_t* Q, const uint16_t* K, const f
     const long total = (long)g.tiles_m * g.tiles_n * BH;
     const long grid = (total + 7) / 8 * 8;
     if (f16)
-        hipLaunchKernelGGL((k_gemm<true, false, kOutScoresF32>), dim3((unsigned)grid),
+        hipLaunchKernelGGL((k_gemm<true, false, kOutExpF16>), dim3((unsigned)grid),
                            dim3(kGemmThreads), 0, st, g);
     else
-        hipLaunchKernelGGL((k_gemm<false, false, kOutScoresF32>), dim3((unsigned)grid),
+        hipLaunchKernelGGL((k_gemm<false, false, kOutExpF16>), dim3((unsigned)grid),
                            dim3(kGemmThreads), 0, st, g);
     return hipGetLastError();
 }
@@ -814,29 +931,21 @@ hipError_t launch_encode_f16(int pek, const uint16_t* in, uint16_t* out, float* 
     return hipGetLastError();
 }
 
-hipError_t launch_softmax_bf16(const float* S, uint16_t* P, long rows, int Lk, hipStream_t st) {
-    const dim3 grid((unsigned)((rows + 3) / 4)), block(256);
-    if (Lk % 4 != 0 || Lk > 256 * 16)
-        hipLaunchKernelGGL(k_softmax_bf, grid, block, 0, st, S, P, rows, Lk);
-    else if (Lk <= 256)
-        hipLaunchKernelGGL(k_softmax_bf_regs<1>, grid, block, 0, st, S, P, rows, Lk);
-    else if (Lk <= 512)
-        hipLaunchKernelGGL(k_softmax_bf_regs<2>, grid, block, 0, st, S, P, rows, Lk);
-    else if (Lk <= 1024)
-        hipLaunchKernelGGL(k_softmax_bf_regs<4>, grid, block, 0, st, S, P, rows, Lk);
-    else if (Lk <= 2048)
-        hipLaunchKernelGGL(k_softmax_bf_regs<8>, grid, block, 0, st, S, P, rows, Lk);
-    else
-        hipLaunchKernelGGL(k_softmax_bf_regs<16>, grid, block, 0, st, S, P, rows, Lk);
+hipError_t launch_rowscale(const float* st_m, const float* st_l, float* ga, long rows, int T,
+                           hipStream_t st) {
+    hipLaunchKernelGGL(k_rowscale, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, st, st_m,
+                       st_l, ga, rows, T);
     return hipGetLastError();
 }
 
-hipError_t launch_gemm_pv(const uint16_t* P, const uint16_t* V, uint16_t* O, int BH, int Lq, int Lk,
-                          int D, hipStream_t st) {
+hipError_t launch_gemm_pv(const uint16_t* E, const float* ga, const uint16_t* V, uint16_t* O,
+                          int BH, int Lq, int Lk, int D, hipStream_t st) {
     GemmArgs g{};
-    g.A = P;
+    g.A = E;
     g.B = V;
     g.C = O;
+    g.ga = ga;
+    g.gt = (Lk + kBN - 1) / kBN;
     g.M = Lq;
     g.N = D;
     g.K = Lk;
@@ -852,8 +961,12 @@ hipError_t launch_gemm_pv(const uint16_t* P, const uint16_t* V, uint16_t* O, int
     g.scale = 1.f;
     const long total = (long)g.tiles_m * g.tiles_n * BH;
     const long grid = (total + 7) / 8 * 8;
-    hipLaunchKernelGGL((k_gemm<false, true, kOutBf16>), dim3((unsigned)grid), dim3(kGemmThreads), 0,
-                       st, g);
+    if (g.gt <= kFacTiles)
+        hipLaunchKernelGGL((k_gemm<false, true, kOutBf16, true>), dim3((unsigned)grid),
+                           dim3(kGemmThreads), 0, st, g);
+    else
+        hipLaunchKernelGGL((k_gemm<false, true, kOutBf16, false>), dim3((unsigned)grid),
+                           dim3(kGemmThreads), 0, st, g);
     return hipGetLastError();
 }
 

@@ -32,17 +32,19 @@ hipError_t launch_fused_small(int dtype, int pek, const void* Q, const void* K, 
                               unsigned* epochs, unsigned* done, int* status, int BH, int Lq,
                               int Lk, int D, int MB, int dc, int nchunk, int gather1, float scale,
                               const PeSide& pq, const PeSide& pk, hipStream_t st);
-// Long-sequence bf16 path (gemm_path.hip): S = scale Q K^T (fp32),
-// P = bf16(softmax(S)), O = P V.  Needs D % 8 == 0, Lk % 8 == 0 and 16-byte
-// aligned bases.
+// Long-sequence bf16 path (gemm_path.hip): E = exp(scale Q K^T - tile row
+// max) (fp16) with per-(row, 256-key tile) max and sum, per-row factors
+// g_t = exp(m_t - m) / l, O = (E g) V.  Needs D % 8 == 0, Lk % 8 == 0 and
+// 16-byte aligned bases.
 hipError_t launch_encode_f16(int pek, const uint16_t* in, uint16_t* out, float* inv, long n_rows,
                              int seq_len, int D, const PeSide& pe, hipStream_t st);
 hipError_t launch_gemm_qk(int f16, const uint16_t* Q, const uint16_t* K, const float* qinv,
-                          const float* kinv, float* S, int BH, int Lq, int Lk, int D, float scale,
-                          hipStream_t st);
-hipError_t launch_softmax_bf16(const float* S, uint16_t* P, long rows, int Lk, hipStream_t st);
-hipError_t launch_gemm_pv(const uint16_t* P, const uint16_t* V, uint16_t* O, int BH, int Lq, int Lk,
-                          int D, hipStream_t st);
+                          const float* kinv, uint16_t* E, float* st_m, float* st_l, int BH, int Lq,
+                          int Lk, int D, float scale, hipStream_t st);
+hipError_t launch_rowscale(const float* st_m, const float* st_l, float* ga, long rows, int T,
+                           hipStream_t st);
+hipError_t launch_gemm_pv(const uint16_t* E, const float* ga, const uint16_t* V, uint16_t* O,
+                          int BH, int Lq, int Lk, int D, hipStream_t st);
 
 hipError_t launch_pe_apply(int dtype, int pek, const void* in, void* out, long n_rows,
                            int seq_len, int D, const PeSide& pe, int vec_ok, hipStream_t st);
