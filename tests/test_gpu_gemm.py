@@ -80,3 +80,48 @@ def test_gemm_baseline_head_shapes(am, dev, cfg):
                               .reshape(-1, D)[r:r + 1] for r in rows])
         n, nrel, mabs = H.check_bf16(got[rows], ref)
         assert n == 0, f"head {h}: normwise rel {nrel}, max abs {mabs}"
+
+
+@pytest.mark.parametrize("shape", [(1, 1, 160, 2312, 64), (1, 2, 128, 4096, 128)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_gemm_path_long_key_rows(am, dev, shape):
+    """More than eight 256-key tiles per score row: the PV GEMM takes the
+    softmax factors with each A chunk instead of from its LDS table."""
+    import hip_rt
+    B, Hh, Lq, Lk, D = shape
+    print(f"[case] gemm long key rows {shape}", flush=True)
+    assert am.path(1, B, Hh, Lq, Lk, D) == am.ATN_PATH_GEMM
+    (q, k, v), (Q, K, V) = H.device_inputs((B, Hh, Lq, D), (B, Hh, Lk, D), 211 + Lk, "bf16")
+    out = H.empty(Q.shape, "bf16")
+    am.attention_ex(q, k, v, out)
+    hip_rt.synchronize()
+    n, nrel, mabs = H.check_bf16(out.numpy(), _ref("none", Q, K, V, Lq, Lk, D))
+    assert n == 0, f"normwise rel {nrel}, max abs {mabs}"
+
+
+@pytest.mark.parametrize("pe,sigma", [("none", 3.0), ("rope_half", 1.0)])
+def test_gemm_path_wide_score_range(am, dev, pe, sigma):
+    """Scores spread widely: one 256-key tile of keys is scaled x4, so in
+    many rows the other tiles sit far below the row maximum (with sigma 3
+    their softmax factors underflow to zero) while the maximum moves between
+    tiles from row to row.  Exact bf16 operands take sigma 3 (logits up to
+    ~+-40); the fp16-encoded RoPE operands take the config-4 input scale
+    (their per-element rounding of 2^-12 grows the logit error with the
+    logits' size)."""
+    import hip_rt
+    B, Hh, Lq, Lk, D = 1, 2, 200, 1104, 256
+    print(f"[case] gemm wide score range {pe} sigma {sigma}", flush=True)
+    rng = np.random.default_rng(17)
+    Qf = rng.standard_normal((B, Hh, Lq, D), dtype=np.float32) * np.float32(sigma)
+    Kf = rng.standard_normal((B, Hh, Lk, D), dtype=np.float32) * np.float32(sigma)
+    Kf[:, :, 300:556] *= 4.0  # one tile of keys with much larger scores
+    Vf = rng.standard_normal((B, Hh, Lk, D), dtype=np.float32)
+    q, k, v = (hip_rt.DeviceArray.from_numpy(x, "bf16") for x in (Qf, Kf, Vf))
+    Q, K, V = (t.numpy() for t in (q, k, v))
+    desc = _desc(am, pe)
+    assert am.path(1, B, Hh, Lq, Lk, D, desc) == am.ATN_PATH_GEMM
+    out = H.empty(Q.shape, "bf16")
+    am.attention_ex(q, k, v, out, pe=desc)
+    hip_rt.synchronize()
+    n, nrel, mabs = H.check_bf16(out.numpy(), _ref(pe, Q, K, V, Lq, Lk, D))
+    assert n == 0, f"normwise rel {nrel}, max abs {mabs}"
