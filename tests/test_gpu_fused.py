@@ -201,3 +201,27 @@ def test_fused_row_groups_and_exchanges(am, dev, monkeypatch, rows, exchange, sh
     else:
         n, mabs, mrel = H.check_f32(out.numpy(), oracle.attention(Q, K, V, nthreads=16))
         assert n == 0, f"{n} mismatches, max abs {mabs}, max rel {mrel}"
+
+
+@pytest.mark.parametrize("rows,exchange", [("64", "rsag"), ("", "")], ids=["rows64-rsag", "default"])
+def test_fused_uneven_slices(am, dev, monkeypatch, rows, exchange):
+    """36 heads with 7 D-slices each: with 64-row groups the reduce-scatter
+    owns 1171 entries per workgroup, so a thread reduces several entries
+    (4-byte words); by default the planner takes 32-row groups and the one
+    gather."""
+    import hip_rt
+    if rows:
+        monkeypatch.setenv("ATN_FUSED_ROWS", rows)
+        monkeypatch.setenv("ATN_FUSED_EXCHANGE", exchange)
+    B, Hh, Lq, Lk, D = 1, 36, 64, 128, 448
+    print(f"[case] fused uneven slices rows={rows or 'default'}", flush=True)
+    assert am.path(0, B, Hh, Lq, Lk, D) == am.ATN_PATH_FUSED_SMALL
+    (q, k, v), (Q, K, V) = H.device_inputs((B, Hh, Lq, D), (B, Hh, Lk, D), 131)
+    ws = _ws(am, 0, B, Hh, Lq, Lk, D)
+    out = H.empty(Q.shape)
+    for _ in range(3):
+        am.attention_ex(q, k, v, out, workspace=ws)
+    hip_rt.synchronize()
+    assert am.sync_status(ws, B, Hh) == 0
+    n, mabs, mrel = H.check_f32(out.numpy(), oracle.attention(Q, K, V, nthreads=16))
+    assert n == 0, f"{n} mismatches, max abs {mabs}, max rel {mrel}"
