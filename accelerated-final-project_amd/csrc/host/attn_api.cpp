@@ -127,9 +127,17 @@ struct Workspace {
     size_t bytes = 0;
 };
 
+// fp16 encoding tables of the GEMM path's fused K encoding, [npos][D]
+// 16-bit units: sinusoidal PE values, or (cos, sin) words per rotation pair.
+struct Table16 {
+    uint16_t* p = nullptr;
+    int npos = 0;
+};
+
 struct DeviceState {
     std::map<hipStream_t, Workspace> ws;
     std::map<std::tuple<int, int, uint32_t>, Table> tables;  // (kind, dim, base bits)
+    std::map<std::tuple<int, int, int, uint32_t>, Table16> tables16;  // (kind, D, rotary, base)
     int cus = 0;
     std::map<std::pair<int, int>, int> fused_cap;  // (dtype, LDS bytes) -> resident workgroups
 };
@@ -215,6 +223,58 @@ int get_table(DeviceState& ds, const PePlan& plan, int D, int npos, Table** out)
     return ATN_OK;
 }
 
+uint16_t f16_bits(float x) {
+    const _Float16 h = (_Float16)x;  // nearest even
+    uint16_t b;
+    std::memcpy(&b, &h, 2);
+    return b;
+}
+
+// The GEMM path's fp16 tables, from the same float expressions as the fp32
+// tables (build_rope_table, build_sin_table), each value rounded once:
+//   sinusoidal  [pos][D]: PE(pos, d) (sin of pair d / 2 on even d, cos on odd)
+//   RoPE        [pos][D/2] words (cos, sin) of pair i < r/2, (1, 0) past the
+//               rotary width (a pass-through rotation)
+// Built (synchronously) when missing or too short; caller holds g_mu.
+int get_table16(DeviceState& ds, const PePlan& plan, int D, int npos, Table16** out) {
+    const bool rope = plan.pek != atn::kPeSinusoidal;
+    uint32_t base_bits;
+    std::memcpy(&base_bits, &plan.base, 4);
+    const auto key = std::make_tuple(rope ? 1 : 2, D, rope ? plan.rotary : D, rope ? base_bits : 0u);
+    Table16& t = ds.tables16[key];
+    if (t.p == nullptr || t.npos < npos) {
+        const int want = npos < 64 ? 64 : npos;
+        std::vector<float> a, b;
+        std::vector<uint16_t> h((size_t)want * D);
+        if (rope) {
+            build_rope_table(a, b, want, plan.rotary, plan.base);
+            const int nf = plan.rotary / 2;
+            for (int pos = 0; pos < want; pos++)
+                for (int i = 0; i < D / 2; i++) {
+                    const bool on = i < nf;
+                    h[(size_t)pos * D + 2 * i] = f16_bits(on ? a[(size_t)pos * nf + i] : 1.0f);
+                    h[(size_t)pos * D + 2 * i + 1] = f16_bits(on ? b[(size_t)pos * nf + i] : 0.0f);
+                }
+        } else {
+            build_sin_table(a, b, want, D);
+            const int nf = (D + 1) / 2;
+            for (int pos = 0; pos < want; pos++)
+                for (int d = 0; d < D; d++)
+                    h[(size_t)pos * D + d] =
+                        f16_bits((d & 1) ? b[(size_t)pos * nf + d / 2] : a[(size_t)pos * nf + d / 2]);
+        }
+        if (t.p) {
+            ATN_HIP(hipFree(t.p));  // hipFree waits for in-flight work
+            t.p = nullptr;
+        }
+        ATN_HIP(hipMalloc(&t.p, h.size() * 2));
+        ATN_HIP(hipMemcpy(t.p, h.data(), h.size() * 2, hipMemcpyHostToDevice));
+        t.npos = want;
+    }
+    *out = &t;
+    return ATN_OK;
+}
+
 // Fills the PeSide table pointers (library tables or the caller's).
 int bind_tables(const atn_pe_desc* pe, PePlan& plan, int D, int npos) {
     if (plan.pek == atn::kPeNone) return ATN_OK;
@@ -294,10 +354,13 @@ int ensure_workspace(size_t bytes, hipStream_t stream, void** ws) {
 
 // ---------------------------------------------------------------- fused plan
 // Workspace layout (every path): a fixed 32 KiB sync region -- [0, 4) the
-// status word, [256, 8448) one epoch word per row group of the
-// single-launch kernel, [8448, 24832) two sets of 2048 per-workgroup done
-// words -- then scratch.  Fixed offsets keep the epoch words of one call
-// from landing elsewhere when shapes change between calls.
+// status word, [128, 132) the GEMM path's K-range word (raised when the
+// fused K encoding meets a value fp16 cannot hold), [256, 8448) one epoch
+// word per row group of the single-launch kernel, [8448, 24832) two sets of
+// 2048 per-workgroup done words -- then scratch.  Fixed offsets keep the
+// epoch words of one call from landing elsewhere when shapes change between
+// calls.
+constexpr size_t kSyncRangeOff = 128;
 constexpr size_t kSyncEpochOff = 256;
 constexpr size_t kSyncDoneOff = 8448;
 constexpr int kSyncMaxWorkgroups = 2048;
@@ -444,6 +507,7 @@ constexpr int kGemmMinL = 128;
 
 struct GemmPlan {
     bool ok = false, encoded = false;
+    int benc = 0;     // fused K encoding (atn::kGemmEnc*), 0 = K~ from k_encode_f16
     int tiles_k = 0;  // 256-key tiles per score row
     size_t q_off = 0, k_off = 0, qs_off = 0, ks_off = 0, e_off = 0, m_off = 0, l_off = 0,
            g_off = 0, bytes = 0;
@@ -467,6 +531,26 @@ GemmPlan gemm_plan(int dtype, const Shape& s, const PePlan& plan) {
         p.k_off = take((size_t)s.BH * s.Lk * s.D * 2);
         p.qs_off = take((size_t)s.BH * s.Lq * 4);
         p.ks_off = take((size_t)s.BH * s.Lk * 4);
+    }
+    // K's encoding fused into the QK^T GEMM (K~ as unscaled fp16 from the
+    // library's fp16 tables; the K~ pass stays as the fallback): an even
+    // number of 64-deep K steps, library tables, rotate-half over all of D,
+    // and at most two 256-row query tiles -- every query tile's workgroups
+    // encode their K tiles again, so with more of them the encoding costs
+    // the MFMA-bound GEMM more than the K~ pass does (config 4: 892 us fused
+    // vs 642 + 199 us; config 5, one query tile: 160 us vs 143 + 110 us).
+    // ATN_GEMM_FUSED_K=-1 turns it off, =1 forces it on (measurement).
+    const int fk = env_int("ATN_GEMM_FUSED_K");
+    if (p.encoded && s.D % 128 == 0 && !plan.caller_tables && fk >= 0 &&
+        (fk > 0 || (s.Lq + 255) / 256 <= 2)) {
+        if (!plan.k.on)
+            p.benc = atn::kGemmEncRaw;
+        else if (plan.pek == atn::kPeSinusoidal)
+            p.benc = atn::kGemmEncSin;
+        else if (plan.pek == atn::kPeRopeInterleaved)
+            p.benc = atn::kGemmEncRope;
+        else if (plan.pek == atn::kPeRopeHalf && plan.rotary == s.D)
+            p.benc = atn::kGemmEncRopeHalf;
     }
     p.tiles_k = (int)((s.Lk + 255) / 256);
     const size_t stats = (size_t)s.BH * s.Lq * p.tiles_k * 4;
@@ -538,29 +622,50 @@ int attention_core(int dtype, const void* Q, const void* K, const void* V, void*
         char* w = static_cast<char*>(ws);
         const uint16_t* qe = static_cast<const uint16_t*>(Q);
         const uint16_t* ke = static_cast<const uint16_t*>(K);
-        const float* qinv = nullptr;
-        const float* kinv = nullptr;
+        uint16_t* E = reinterpret_cast<uint16_t*>(w + gp.e_off);
+        float* st_m = reinterpret_cast<float*>(w + gp.m_off);
+        float* st_l = reinterpret_cast<float*>(w + gp.l_off);
+        float* ga = reinterpret_cast<float*>(w + gp.g_off);
+        unsigned* range = nullptr;
         if (gp.encoded) {
             uint16_t* qd = reinterpret_cast<uint16_t*>(w + gp.q_off);
             uint16_t* kd = reinterpret_cast<uint16_t*>(w + gp.k_off);
             float* qs = reinterpret_cast<float*>(w + gp.qs_off);
             float* ks = reinterpret_cast<float*>(w + gp.ks_off);
             ATN_HIP(atn::launch_encode_f16(plan.q.on ? plan.pek : atn::kPeNone, qe, qd, qs,
-                                           (long)(s.BH * Lq), Lq, D, plan.q, stream));
-            ATN_HIP(atn::launch_encode_f16(plan.k.on ? plan.pek : atn::kPeNone, ke, kd, ks,
-                                           (long)(s.BH * Lk), Lk, D, plan.k, stream));
-            qe = qd;
-            ke = kd;
-            qinv = qs;
-            kinv = ks;
+                                           (long)(s.BH * Lq), Lq, D, plan.q, nullptr, stream));
+            if (gp.benc != 0) {
+                // K encoded inside the QK^T GEMM; if some |K~| does not fit
+                // fp16 the range word is raised and the two gated launches
+                // (the K~ pass with row scales, the plain GEMM) redo the scores
+                range = reinterpret_cast<unsigned*>(w + kSyncRangeOff);
+                const uint16_t* tab = nullptr;
+                int tab_rows = 0;
+                if (gp.benc != atn::kGemmEncRaw) {
+                    std::lock_guard<std::mutex> lk(g_mu);
+                    Table16* t16 = nullptr;
+                    st = get_table16(g_dev[dev], plan, D, Lq > Lk ? Lq : Lk, &t16);
+                    if (st != ATN_OK) return st;
+                    tab = t16->p;
+                    tab_rows = t16->npos;
+                }
+                ATN_HIP(atn::launch_gemm_qk_enc(gp.benc, qd, ke, qs, tab, tab_rows, E, st_m, st_l,
+                                                range, (int)s.BH, Lq, Lk, D, scale, stream));
+                ATN_HIP(atn::launch_encode_f16(plan.k.on ? plan.pek : atn::kPeNone, ke, kd, ks,
+                                               (long)(s.BH * Lk), Lk, D, plan.k, range, stream));
+                ATN_HIP(atn::launch_gemm_qk(1, qd, kd, qs, ks, E, st_m, st_l, (int)s.BH, Lq, Lk, D,
+                                            scale, range, stream));
+            } else {
+                ATN_HIP(atn::launch_encode_f16(plan.k.on ? plan.pek : atn::kPeNone, ke, kd, ks,
+                                               (long)(s.BH * Lk), Lk, D, plan.k, nullptr, stream));
+                ATN_HIP(atn::launch_gemm_qk(1, qd, kd, qs, ks, E, st_m, st_l, (int)s.BH, Lq, Lk, D,
+                                            scale, nullptr, stream));
+            }
+        } else {
+            ATN_HIP(atn::launch_gemm_qk(0, qe, ke, nullptr, nullptr, E, st_m, st_l, (int)s.BH, Lq,
+                                        Lk, D, scale, nullptr, stream));
         }
-        uint16_t* E = reinterpret_cast<uint16_t*>(w + gp.e_off);
-        float* st_m = reinterpret_cast<float*>(w + gp.m_off);
-        float* st_l = reinterpret_cast<float*>(w + gp.l_off);
-        float* ga = reinterpret_cast<float*>(w + gp.g_off);
-        ATN_HIP(atn::launch_gemm_qk(gp.encoded ? 1 : 0, qe, ke, qinv, kinv, E, st_m, st_l,
-                                    (int)s.BH, Lq, Lk, D, scale, stream));
-        ATN_HIP(atn::launch_rowscale(st_m, st_l, ga, s.BH * Lq, gp.tiles_k, stream));
+        ATN_HIP(atn::launch_rowscale(st_m, st_l, ga, s.BH * Lq, gp.tiles_k, range, stream));
         ATN_HIP(atn::launch_gemm_pv(E, ga, static_cast<const uint16_t*>(V),
                                     static_cast<uint16_t*>(out), (int)s.BH, Lq, Lk, D, stream));
         return ATN_OK;

@@ -74,6 +74,23 @@ __device__ __forceinline__ v16f mfma_32x32x16(const uint4& a, const uint4& b, co
                                                        __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
 }
 
+// Raw buffer descriptor over one head's matrix of n 16-bit elements (the host
+// keeps it below 2^31 elements, so the byte count fits the 32-bit range).
+// The base and size are workgroup-uniform; readfirstlane states it, so the
+// descriptor lives in scalar registers.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t gemm_rsrc(const uint16_t* base, long n) {
+    const uint64_t b = (uint64_t)base;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)b);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(b >> 32));
+    const int bytes = __builtin_amdgcn_readfirstlane((int)(uint32_t)(2 * n));
+    return __builtin_amdgcn_make_buffer_rsrc(
+        reinterpret_cast<void*>(((uint64_t)hi << 32) | lo), 0, bytes, 0x00020000);
+}
+__device__ __forceinline__ uint4 buf_ld16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_bit_cast(
+        uint4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, __builtin_amdgcn_readfirstlane(soff), 0));
+}
+
 // Tile index of this workgroup with consecutive indices kept on one XCD:
 // hardware deals workgroup w to XCD w % 8, so XCD x gets tiles
 // [x * per, (x + 1) * per).
@@ -184,8 +201,106 @@ struct GemmArgs {
     long sa, sb, sc;              // head strides (elements)
     int tiles_m, tiles_n, heads;  // grid decomposition
     float scale;
+    const uint16_t* tab;          // fused K encoding: fp16 table (k_gemm_qk_enc)
+    int tab_rows;                 // positions in tab
+    unsigned* flag;               // fused K encoding: overflow word, raised on |K~| > 65504
+    const unsigned* gate;         // when set, the launch does nothing unless *gate != 0
 };
 
+// NT exp epilogue: scores S = scale * acc * (row scale) * (column scale) of
+// this 256-key tile; per row its maximum m_t over the tile's valid columns
+// and the sum l_t of E = exp(S - m_t).  A row's 256 columns are 32 lanes x
+// TJ tiles in each of the two column waves (wave % 2), combined through LDS
+// (red: 4 x 256 floats, free once every wave is done with the K loop).
+// Lane layout of acc[i][j]: column (lane % 32) and rows 8 (r / 4) +
+// 4 (lane / 32) + r % 4 of each 32 x 32 tile.
+template <int TI, int TJ>
+__device__ __forceinline__ void nt_exp_epilogue(const GemmArgs& g, v16f (&acc)[TI][TJ],
+                                                float* red, int bh, int m0, int n0, int tn,
+                                                int wm, int wn, int wave, int lane) {
+    __syncthreads();  // every wave is done with the LDS stages
+    const int half = lane >> 5, lc = lane & 31, cw = wave & 1;
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) {
+        const int col = n0 + wn + j * 32 + lc;
+        const float csc =
+            col < g.N ? (g.cs ? g.cs[(long)bh * g.N + col] * g.scale : g.scale) : 0.f;
+#pragma unroll
+        for (int i = 0; i < TI; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int row = m0 + wm + i * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+                float v = acc[i][j][r] * csc;
+                if (g.rs && row < g.M) v *= g.rs[(long)bh * g.M + row];
+                acc[i][j][r] = col < g.N ? v : -INFINITY;
+            }
+    }
+    float rm[TI][16], rl[TI][16];
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            float m = acc[i][0][r];
+#pragma unroll
+            for (int j = 1; j < TJ; ++j) m = fmaxf(m, acc[i][j][r]);
+            rm[i][r] = half_max(m);
+        }
+    auto rloc = [&](int i, int r) { return wm + i * 32 + 8 * (r >> 2) + 4 * half + (r & 3); };
+    if (lc == 0)
+#pragma unroll
+        for (int i = 0; i < TI; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) red[cw * kBM + rloc(i, r)] = rm[i][r];
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const float m = fmaxf(rm[i][r], red[(cw ^ 1) * kBM + rloc(i, r)]);
+            rm[i][r] = m;
+            float l = 0.f;
+#pragma unroll
+            for (int j = 0; j < TJ; ++j) {
+                // a row with no valid column keeps m = -inf: its E are 0
+                const float e = m == -INFINITY ? 0.f : __expf(acc[i][j][r] - m);
+                acc[i][j][r] = e;
+                l += e;
+            }
+            rl[i][r] = half_sum(l);
+        }
+    if (lc == 0)
+#pragma unroll
+        for (int i = 0; i < TI; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) red[(2 + cw) * kBM + rloc(i, r)] = rl[i][r];
+    __syncthreads();
+    if (cw == 0 && lc == 0)
+#pragma unroll
+        for (int i = 0; i < TI; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int row = m0 + rloc(i, r);
+                if (row >= g.M) continue;
+                const long si = ((long)bh * g.M + row) * g.tiles_n + tn;
+                g.st_m[si] = rm[i][r];
+                g.st_l[si] = rl[i][r] + red[3 * kBM + rloc(i, r)];
+            }
+    uint16_t* C = static_cast<uint16_t*>(g.C) + bh * g.sc;
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) {
+            const int col = n0 + wn + j * 32 + lc;
+            if (col >= g.N) continue;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int row = m0 + rloc(i, r);
+                if (row < g.M)
+                    C[(long)row * g.ldc + col] =
+                        __builtin_bit_cast(uint16_t, (_Float16)acc[i][j][r]);
+            }
+        }
+}
 // NN softmax factors of A's rows: kept in LDS ([256 rows][gt], read when a
 // chunk is stored) when a row has at most kFacTiles 256-key tiles, else
 // loaded with each chunk into the register stage.
@@ -200,13 +315,16 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm(GemmArgs g) {
     uint16_t(*As)[kTileElems] = reinterpret_cast<uint16_t(*)[kTileElems]>(lds);
     uint16_t(*Bs)[kTileElems] = reinterpret_cast<uint16_t(*)[kTileElems]>(lds + 2 * kTileElems);
 
+    // a gated launch (the fallback behind the fused K encoding) runs only
+    // when the overflow word was raised
+    if (g.gate != nullptr && *g.gate == 0u) return;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const long per_head = (long)g.tiles_m * g.tiles_n;
     const long total = per_head * g.heads;
     const long t = xcd_tile(blockIdx.x, total);
     if (t >= total) return;
-    const int bh = (int)(t / per_head);
+    const int bh = __builtin_amdgcn_readfirstlane((int)(t / per_head));
     const int rem = (int)(t - (long)bh * per_head);
     // within a head: NT runs row panels outer (neighbours share the Q
     // panel); NN runs row panels fastest, so the few workgroups of one V
@@ -219,7 +337,10 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm(GemmArgs g) {
         tm = rem / g.tiles_n;
         tn = rem - tm * g.tiles_n;
     }
-    const int m0 = tm * kBM, n0 = tn * kBN;
+    // the tile's coordinates are workgroup-uniform: keep them (and what is
+    // derived from them) in scalar registers
+    const int m0 = __builtin_amdgcn_readfirstlane(tm * kBM);
+    const int n0 = __builtin_amdgcn_readfirstlane(tn * kBN);
 
     const uint16_t* A = g.A + bh * g.sa;
     const uint16_t* B = g.B + bh * g.sb;
@@ -253,7 +374,47 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm(GemmArgs g) {
         return *reinterpret_cast<const uint4*>(base + off);
     };
     const float* ga = B_NN ? g.ga + (long)bh * g.M * g.gt : nullptr;
+    // Interior tiles load through buffer descriptors: one per-lane byte
+    // offset per operand, constant over the K loop, and the chunk's row and
+    // the step's k0 in the scalar offset, so the loads need no per-step
+    // address arithmetic and no 64-bit address registers.
+    const __amdgpu_buffer_rsrc_t ra = gemm_rsrc(A, (long)g.M * g.lda);
+    const __amdgpu_buffer_rsrc_t rb =
+        gemm_rsrc(B, B_NN ? (long)g.K * g.ldb : (long)g.N * g.ldb);
+    const uint32_t va = 2u * ((uint32_t)(tid / kChunkPerRow) * (uint32_t)g.lda +
+                              (uint32_t)((tid % kChunkPerRow) * 8));
+    const uint32_t vb =
+        B_NN ? 2u * ((uint32_t)(tid / kNNChunkPerRow) * (uint32_t)g.ldb +
+                     (uint32_t)((tid % kNNChunkPerRow) * 8))
+             : 2u * ((uint32_t)(tid / kChunkPerRow) * (uint32_t)g.ldb +
+                     (uint32_t)((tid % kChunkPerRow) * 8));
+    constexpr int kRowsPerPass = kGemmThreads / kChunkPerRow;     // A / NT B rows per u
+    constexpr int kKeysPerPass = kGemmThreads / kNNChunkPerRow;   // NN B keys per u
+    auto load_stage_buf = [&](Stage& r, int k0) {
+#pragma unroll
+        for (int u = 0; u < kChunks; ++u) {
+            const uint32_t so = 2u * ((uint32_t)(m0 + u * kRowsPerPass) * (uint32_t)g.lda +
+                                      (uint32_t)k0);
+            r.a[u] = buf_ld16(ra, va, so);
+            if constexpr (B_NN && !FAC_LDS) {
+                const int row = tid / kChunkPerRow + u * kRowsPerPass,
+                          k8 = (tid % kChunkPerRow) * 8;
+                r.ga[u] = ga[(uint32_t)(m0 + row) * (uint32_t)g.gt + (uint32_t)((k0 + k8) >> 8)];
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < kChunks; ++u) {
+            const uint32_t so =
+                B_NN ? 2u * ((uint32_t)(k0 + u * kKeysPerPass) * (uint32_t)g.ldb + (uint32_t)n0)
+                     : 2u * ((uint32_t)(n0 + u * kRowsPerPass) * (uint32_t)g.ldb + (uint32_t)k0);
+            r.b[u] = buf_ld16(rb, vb, so);
+        }
+    };
     auto load_stage = [&](Stage& r, int k0, auto edge) {
+        if constexpr (!decltype(edge)::value) {
+            load_stage_buf(r, k0);
+            return;
+        }
 #pragma unroll
         for (int u = 0; u < kChunks; ++u) {
             const int cidx = tid + u * kGemmThreads;
@@ -481,96 +642,385 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm(GemmArgs g) {
         }
         return;
     }
-    // NT: scores S = scale * acc * (row scale) * (column scale) of this
-    // 256-key tile; per row its maximum m_t over the tile's valid columns and
-    // the sum l_t of E = exp(S - m_t).  A row's 256 columns are 32 lanes x TJ
-    // tiles in each of the two column waves (wave % 2), combined through LDS.
+    // ---- NT epilogue (exp of the scores, tile row statistics)
     if constexpr (OUT == kOutExpF16) {
-    static_assert(!B_NN && WN == 2, "the exp epilogue is the NT product's");
-    __syncthreads();  // every wave is done with the LDS stages
-    float* red = reinterpret_cast<float*>(lds);  // [max | sum][column wave][256 rows]
-    const int half = lane >> 5, lc = lane & 31, cw = wave & 1;
-#pragma unroll
-    for (int j = 0; j < TJ; ++j) {
-        const int col = n0 + wn + j * 32 + lc;
-        const float csc =
-            col < g.N ? (g.cs ? g.cs[(long)bh * g.N + col] * g.scale : g.scale) : 0.f;
-#pragma unroll
-        for (int i = 0; i < TI; ++i)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int row = m0 + wm + i * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
-                float v = acc[i][j][r] * csc;
-                if (g.rs && row < g.M) v *= g.rs[(long)bh * g.M + row];
-                acc[i][j][r] = col < g.N ? v : -INFINITY;
-            }
+        static_assert(!B_NN && WN == 2, "the exp epilogue is the NT product's");
+        nt_exp_epilogue<TI, TJ>(g, acc, reinterpret_cast<float*>(lds), bh, m0, n0, tn, wm, wn,
+                                wave, lane);
     }
-    float rm[TI][16], rl[TI][16];
+}
+
+// ---------------------------------------------------------------------------
+// QK^T GEMM with K's encoding applied on its way to LDS (no K~ pass).
+//
+// B = raw bf16 K rows, read through the register stage together with 16
+// bytes of fp16 table per 16-byte chunk, and written to LDS as unscaled fp16
+// K~ (exact for raw values in fp16's range):
+//   kBEncRaw       K~ = K (the query side alone is encoded)
+//   kBEncSin       K~ = K + PE, table [pos][D]: sin on even dims, cos on odd
+//   kBEncRope      interleaved rotation of pairs (2i, 2i + 1), table [pos][D/2]
+//                  of (cos, sin) words, (1, 0) past the rotary width
+//   kBEncRopeHalf  rotate-half, pairs (i, i + D/2): each K step takes 32 dims
+//                  of the first half and their 32 partners (A's columns in the
+//                  same order), so both halves of a rotation are in one thread
+// Each value is rounded once to fp16; a workgroup that meets |K~| > 65504
+// raises the overflow word, and the host's gated fallback (k_encode_f16 with
+// row scales, then k_gemm) recomputes every score of the call.
+//
+// A = Q~ (k_encode_f16's fp16 rows, scales in rs) goes straight from memory
+// to LDS (buffer loads with the LDS destination, no register stage): each
+// wave instruction writes one 1 KiB run of 8 unpadded rows, chunk c of row r
+// stored at position c ^ key(r), key(r) = (r & 7) ^ ((r >> 3) & 1), so the
+// fragment reads (16 rows of one chunk per 16 lanes) hit distinct banks for
+// 32 or 64 banks.  Out-of-range rows and columns load from an offset past the
+// descriptor's range, which writes zeros.
+//
+// The stages are separate LDS arrays and the K loop runs two steps per
+// iteration, so every LDS access names its stage at compile time: the
+// compiler can tell the DMA's target from the tiles being read, and the one
+// barrier per step waits only for the DMA (the next step's K loads stay in
+// flight).
+constexpr int kBEncRaw = kGemmEncRaw, kBEncSin = kGemmEncSin, kBEncRope = kGemmEncRope,
+              kBEncRopeHalf = kGemmEncRopeHalf;
+
+// v_fma_mix_f32 forms: fp32 a times one fp16 half of t, plus fp32 c, rounded
+// once to fp32.
+__device__ __forceinline__ float fmix_lo(float a, uint32_t t, float c) {
+    float r;
+    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel_hi:[0,1,0]" : "=v"(r) : "v"(a), "v"(t), "v"(c));
+    return r;
+}
+__device__ __forceinline__ float fmix_hi(float a, uint32_t t, float c) {
+    float r;
+    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[0,1,0] op_sel_hi:[0,1,0]"
+        : "=v"(r) : "v"(a), "v"(t), "v"(c));
+    return r;
+}
+__device__ __forceinline__ float fmix_lo_sub(float a, uint32_t t, float c) {  // a lo(t) - c
+    float r;
+    asm("v_fma_mix_f32 %0, %1, %2, -%3 op_sel_hi:[0,1,0]" : "=v"(r) : "v"(a), "v"(t), "v"(c));
+    return r;
+}
+__device__ __forceinline__ float fmul_lo(float a, uint32_t t) {
+    float r;
+    asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel_hi:[0,1,0]" : "=v"(r) : "v"(a), "v"(t));
+    return r;
+}
+__device__ __forceinline__ float fmul_hi(float a, uint32_t t) {
+    float r;
+    asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel:[0,1,0] op_sel_hi:[0,1,0]" : "=v"(r) : "v"(a), "v"(t));
+    return r;
+}
+__device__ __forceinline__ float fadd_lo(float a, uint32_t t) {  // a + lo(t)
+    float r;
+    asm("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel_hi:[0,0,1]" : "=v"(r) : "v"(a), "v"(t));
+    return r;
+}
+__device__ __forceinline__ float fadd_hi(float a, uint32_t t) {  // a + hi(t)
+    float r;
+    asm("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel:[0,0,1] op_sel_hi:[0,0,1]"
+        : "=v"(r) : "v"(a), "v"(t));
+    return r;
+}
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pk_f16(float a, float b) {  // v_cvt_pk_f16_f32 (nearest even)
+    const f16x2_t v = {(_Float16)a, (_Float16)b};
+    return __builtin_bit_cast(uint32_t, v);
+}
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// 8 bf16 -> 8 fp16: as they are, or plus the chunk's table values (sinusoidal),
+// or rotated pairwise (interleaved RoPE); mx keeps the largest |K~|.
+template <int BENC>
+__device__ __forceinline__ uint4 enc_chunk(const uint4& w, const uint4& t, float& mx) {
+    const uint32_t x[4] = {w.x, w.y, w.z, w.w};
+    const uint32_t tt[4] = {t.x, t.y, t.z, t.w};
+    uint32_t y[4];
 #pragma unroll
-    for (int i = 0; i < TI; ++i)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            float m = acc[i][0][r];
-#pragma unroll
-            for (int j = 1; j < TJ; ++j) m = fmaxf(m, acc[i][j][r]);
-            rm[i][r] = half_max(m);
+    for (int i = 0; i < 4; ++i) {
+        float a = bf16_lo(x[i]), b = bf16_hi(x[i]);
+        if constexpr (BENC == kBEncSin) {
+            a = fadd_lo(a, tt[i]);
+            b = fadd_hi(b, tt[i]);
+        } else if constexpr (BENC == kBEncRope) {
+            // (a, b) = dims (2i', 2i' + 1); tt[i] = (cos, sin) of pair i'
+            const float a0 = a;
+            a = fmix_lo_sub(a0, tt[i], fmul_hi(b, tt[i]));  // a cos - b sin
+            b = fmix_hi(a0, tt[i], fmul_lo(b, tt[i]));      // a sin + b cos
         }
-    auto rloc = [&](int i, int r) { return wm + i * 32 + 8 * (r >> 2) + 4 * half + (r & 3); };
-    if (lc == 0)
-#pragma unroll
-        for (int i = 0; i < TI; ++i)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) red[cw * kBM + rloc(i, r)] = rm[i][r];
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < TI; ++i)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const float m = fmaxf(rm[i][r], red[(cw ^ 1) * kBM + rloc(i, r)]);
-            rm[i][r] = m;
-            float l = 0.f;
-#pragma unroll
-            for (int j = 0; j < TJ; ++j) {
-                // a row with no valid column keeps m = -inf: its E are 0
-                const float e = m == -INFINITY ? 0.f : __expf(acc[i][j][r] - m);
-                acc[i][j][r] = e;
-                l += e;
-            }
-            rl[i][r] = half_sum(l);
-        }
-    if (lc == 0)
-#pragma unroll
-        for (int i = 0; i < TI; ++i)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) red[(2 + cw) * kBM + rloc(i, r)] = rl[i][r];
-    __syncthreads();
-    if (cw == 0 && lc == 0)
-#pragma unroll
-        for (int i = 0; i < TI; ++i)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int row = m0 + rloc(i, r);
-                if (row >= g.M) continue;
-                const long si = ((long)bh * g.M + row) * g.tiles_n + tn;
-                g.st_m[si] = rm[i][r];
-                g.st_l[si] = rl[i][r] + red[3 * kBM + rloc(i, r)];
-            }
-    uint16_t* C = static_cast<uint16_t*>(g.C) + bh * g.sc;
-#pragma unroll
-    for (int i = 0; i < TI; ++i)
-#pragma unroll
-        for (int j = 0; j < TJ; ++j) {
-            const int col = n0 + wn + j * 32 + lc;
-            if (col >= g.N) continue;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int row = m0 + rloc(i, r);
-                if (row < g.M)
-                    C[(long)row * g.ldc + col] =
-                        __builtin_bit_cast(uint16_t, (_Float16)acc[i][j][r]);
-            }
-        }
+        mx = fmaxf(mx, fmaxf(fabsf(a), fabsf(b)));
+        y[i] = pk_f16(a, b);
     }
+    return make_uint4(y[0], y[1], y[2], y[3]);
+}
+
+// Rotate-half: w0 = 8 dims of the first half, w1 = their partners, t0/t1 =
+// (cos, sin) words of the 8 pairs; both chunks rewritten as fp16.
+__device__ __forceinline__ void enc_half(uint4& w0, uint4& w1, const uint4& t0, const uint4& t1,
+                                         float& mx) {
+    const uint32_t x0[4] = {w0.x, w0.y, w0.z, w0.w}, x1[4] = {w1.x, w1.y, w1.z, w1.w};
+    const uint32_t tt[8] = {t0.x, t0.y, t0.z, t0.w, t1.x, t1.y, t1.z, t1.w};
+    uint32_t y0[4], y1[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        float r0[2], r1[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const float a = h ? bf16_hi(x0[i]) : bf16_lo(x0[i]);
+            const float b = h ? bf16_hi(x1[i]) : bf16_lo(x1[i]);
+            const uint32_t w = tt[2 * i + h];
+            r0[h] = fmix_lo_sub(a, w, fmul_hi(b, w));  // a cos - b sin
+            r1[h] = fmix_hi(a, w, fmul_lo(b, w));      // a sin + b cos
+            mx = fmaxf(mx, fmaxf(fabsf(r0[h]), fabsf(r1[h])));
+        }
+        y0[i] = pk_f16(r0[0], r0[1]);
+        y1[i] = pk_f16(r1[0], r1[1]);
+    }
+    w0 = make_uint4(y0[0], y0[1], y0[2], y0[3]);
+    w1 = make_uint4(y1[0], y1[1], y1[2], y1[3]);
+}
+
+template <int BENC>
+__global__ __launch_bounds__(kGemmThreads) void k_gemm_qk_enc(GemmArgs g) {
+    constexpr bool kHalf = BENC == kBEncRopeHalf;
+    constexpr bool kTab = BENC != kBEncRaw;
+    constexpr int kAElems = kBM * kBK;  // unpadded, swizzled A stage
+    __shared__ __align__(16) uint16_t a0s[kAElems];
+    __shared__ __align__(16) uint16_t a1s[kAElems];
+    __shared__ __align__(16) uint16_t b0s[kTileElems];
+    __shared__ __align__(16) uint16_t b1s[kTileElems];
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    auto As = [&](auto S) -> uint16_t* {
+        if constexpr (decltype(S)::value == 0) return a0s; else return a1s;
+    };
+    auto Bs = [&](auto S) -> uint16_t* {
+        if constexpr (decltype(S)::value == 0) return b0s; else return b1s;
+    };
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const long per_head = (long)g.tiles_m * g.tiles_n;
+    const long total = per_head * g.heads;
+    const long t = xcd_tile(blockIdx.x, total);
+    if (t >= total) return;
+    const int bh = __builtin_amdgcn_readfirstlane((int)(t / per_head));
+    const int rem = (int)(t - (long)bh * per_head);
+    const int tm = rem / g.tiles_n, tn = rem - tm * g.tiles_n;
+    const int m0 = __builtin_amdgcn_readfirstlane(tm * kBM);
+    const int n0 = __builtin_amdgcn_readfirstlane(tn * kBN);
+
+    const __amdgpu_buffer_rsrc_t ra = gemm_rsrc(g.A + bh * g.sa, (long)g.M * g.lda);
+    const __amdgpu_buffer_rsrc_t rb = gemm_rsrc(g.B + bh * g.sb, (long)g.N * g.ldb);
+    const __amdgpu_buffer_rsrc_t rt = gemm_rsrc(g.tab, kTab ? (long)g.tab_rows * g.K : 0);
+    constexpr uint32_t kOut = 0xfffffff0u;  // an offset past every descriptor's range
+
+    // column of logical chunk c in a K step, and the step's first column
+    const int dh = kHalf ? g.K / 2 : 0;
+    auto colof = [&](int c) { return kHalf ? (c < 4 ? 8 * c : dh + 8 * (c - 4)) : 8 * c; };
+    auto kbase = [&](int kt) { return kHalf ? 32 * kt : 64 * kt; };
+
+    // ---- A: lane l of wave w, instruction u writes row 64 u + 8 w + l / 8 of
+    // the tile at physical chunk l % 8, i.e. logical chunk (l % 8) ^ key(row)
+    const int ar = 8 * wave + (lane >> 3);
+    const int ac = (lane & 7) ^ (lane >> 3) ^ (wave & 1);
+    const uint32_t a_vo = 2u * ((uint32_t)ar * (uint32_t)g.lda + (uint32_t)colof(ac));
+    auto dma_a = [&](auto S, int kt, auto edge) __attribute__((always_inline)) {
+        uint16_t* dst = As(S);
+        const int kb = kbase(kt);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            uint32_t vo = a_vo;
+            uint32_t so = 2u * ((uint32_t)(m0 + 64 * u) * (uint32_t)g.lda + (uint32_t)kb);
+            if constexpr (decltype(edge)::value) {
+                const int row = m0 + 64 * u + ar, col = kb + colof(ac);
+                vo = ((row < g.M) & (col < g.K))
+                         ? 2u * ((uint32_t)row * (uint32_t)g.lda + (uint32_t)col)
+                         : kOut;
+                so = 0;
+            }
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                ra, (__attribute__((address_space(3))) void*)(dst + (64 * u + 8 * wave) * kBK), 16,
+                vo, __builtin_amdgcn_readfirstlane(so), 0, 0);
+        }
+    };
+
+    // ---- B: this thread's chunks u = 0..3 are key row br + 128 (u / 2),
+    // logical chunk bc + 4 (u % 2) (a rotate-half pair for u = 2p, 2p + 1)
+    const int br = tid >> 2, bc = tid & 3;
+    const uint32_t b_vo[2] = {2u * ((uint32_t)br * (uint32_t)g.ldb + (uint32_t)colof(bc)),
+                              2u * ((uint32_t)br * (uint32_t)g.ldb + (uint32_t)colof(bc + 4))};
+    // table rows are positions with D 16-bit units each; sinusoidal and
+    // interleaved chunks sit where K's do, rotate-half takes 32 bytes of
+    // (cos, sin) words for the 8 pairs of a chunk pair
+    const uint32_t t_vo[2] = {2u * ((uint32_t)br * (uint32_t)g.K + (uint32_t)colof(bc)),
+                              2u * ((uint32_t)br * (uint32_t)g.K + (uint32_t)colof(bc + 4))};
+    const uint32_t th_vo = 2u * (uint32_t)br * (uint32_t)g.K + 32u * (uint32_t)bc;
+    struct Stage {
+        uint4 b[4], t[4];
+    };
+    auto load_b = [&](Stage& r, int kt, auto edge) __attribute__((always_inline)) {
+        constexpr bool E = decltype(edge)::value;
+        const int kb = kbase(kt);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int rr = 128 * (u >> 1);
+            uint32_t vo = b_vo[u & 1];
+            uint32_t so = 2u * ((uint32_t)(n0 + rr) * (uint32_t)g.ldb + (uint32_t)kb);
+            if constexpr (E) {
+                const int row = n0 + rr + br, col = kb + colof(bc + 4 * (u & 1));
+                vo = ((row < g.N) & (col < g.K))
+                         ? 2u * ((uint32_t)row * (uint32_t)g.ldb + (uint32_t)col)
+                         : kOut;
+                so = 0;
+            }
+            r.b[u] = buf_ld16(rb, vo, so);
+        }
+        if constexpr (kTab) {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int rr = 128 * (u >> 1);
+                uint32_t vo, so;
+                if constexpr (kHalf) {
+                    // words of pairs kb + 8 bc + 4 (u % 2) .. + 3
+                    vo = th_vo + 16u * (uint32_t)(u & 1);
+                    so = 2u * (uint32_t)(n0 + rr) * (uint32_t)g.K + 4u * (uint32_t)kb;
+                    if constexpr (E) {
+                        vo = (n0 + rr + br < g.N) ? vo + so : kOut;
+                        so = 0;
+                    }
+                } else {
+                    vo = t_vo[u & 1];
+                    so = 2u * ((uint32_t)(n0 + rr) * (uint32_t)g.K + (uint32_t)kb);
+                    if constexpr (E) {
+                        const int row = n0 + rr + br, col = kb + colof(bc + 4 * (u & 1));
+                        vo = ((row < g.N) & (col < g.K)) ? vo + so : kOut;
+                        so = 0;
+                    }
+                }
+                r.t[u] = buf_ld16(rt, vo, so);
+            }
+        }
+    };
+    float mx = 0.f;  // largest |K~| this thread wrote
+    // each chunk (pair) is stored as soon as it is encoded, which ends its
+    // registers' live range before the next one's temporaries
+    auto store_b = [&](auto S, Stage& r) __attribute__((always_inline)) {
+        uint16_t* dst = Bs(S);
+        auto put = [&](int u) {
+            *reinterpret_cast<uint4*>(&dst[(br + 128 * (u >> 1)) * kLdsRow + 8 * (bc + 4 * (u & 1))]) =
+                r.b[u];
+        };
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+            if constexpr (kHalf) {
+                enc_half(r.b[2 * p], r.b[2 * p + 1], r.t[2 * p], r.t[2 * p + 1], mx);
+            } else {
+                r.b[2 * p] = enc_chunk<BENC>(r.b[2 * p], r.t[2 * p], mx);
+                r.b[2 * p + 1] = enc_chunk<BENC>(r.b[2 * p + 1], r.t[2 * p + 1], mx);
+            }
+            put(2 * p);
+            put(2 * p + 1);
+        }
+    };
+
+    // ---- wave tile 64 x 128 (waves 4 x 2): 2 x 4 MFMA tiles of 32 x 32
+    constexpr int TI = 2, TJ = 4;
+    const int wm = (wave >> 1) * 64, wn = (wave & 1) * 128;
+    v16f acc[TI][TJ];
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int j = 0; j < TJ; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+    struct Frag {
+        uint4 a[TI], b[TJ];
+    };
+    const int lrow = lane & 31, lkh = (lane >> 5) * 8;
+    // sub-step q's A chunk of this lane: logical 2q + lane / 32, stored at
+    // (2q + lane / 32) ^ key(row) = 2q ^ akey (key(row) = key(lrow) here)
+    const int akey = ((lrow & 7) ^ ((lrow >> 3) & 1)) ^ (lane >> 5);
+    const int a_row = (wm + lrow) * kBK;
+    auto read_frag = [&](Frag& f, auto S, int q) __attribute__((always_inline)) {
+        const uint16_t* a = As(S);
+        const uint16_t* b = Bs(S);
+        const int ao = a_row + (((2 * q) ^ akey) << 3);
+#pragma unroll
+        for (int i = 0; i < TI; ++i) f.a[i] = *reinterpret_cast<const uint4*>(&a[ao + i * 32 * kBK]);
+#pragma unroll
+        for (int j = 0; j < TJ; ++j)
+            f.b[j] = *reinterpret_cast<const uint4*>(&b[(wn + j * 32 + lrow) * kLdsRow + 16 * q + lkh]);
+    };
+    auto mma = [&](const Frag& f) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < TI; ++i)
+#pragma unroll
+            for (int j = 0; j < TJ; ++j) acc[i][j] = mfma_32x32x16<true>(f.a[i], f.b[j], acc[i][j]);
+    };
+
+    // ---- K loop: the step of k_gemm (fragment reads one sub-step ahead, the
+    // next step's K tile written to LDS in sub-step 0 and its Q tile's DMA
+    // issued right after, the K loads of step kt + 2 in sub-step 1, one
+    // barrier before sub-step 3)
+    const int nk = (g.K + kBK - 1) / kBK;
+    constexpr int kReads = TI + TJ;
+    Stage st;
+    Frag f0, f1;
+    auto step = [&](int kt, auto S, auto next, auto next2, auto edge) __attribute__((always_inline)) {
+        constexpr int s = decltype(S)::value;
+        using S1 = std::integral_constant<int, s ^ 1>;
+        constexpr bool N1 = decltype(next)::value, N2 = decltype(next2)::value;
+        read_frag(f1, S, 1);
+        mma(f0);
+        if constexpr (N1) store_b(S1{}, st);
+        sched_mfma_reads<kReads>();
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (N1) dma_a(S1{}, kt + 1, edge);
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (N2) load_b(st, kt + 2, edge);
+        read_frag(f0, S, 2);
+        mma(f1);
+        sched_mfma_reads<kReads>();
+        __builtin_amdgcn_sched_barrier(0);
+        read_frag(f1, S, 3);
+        mma(f0);
+        sched_mfma_reads<kReads>();
+        __builtin_amdgcn_sched_barrier(0);
+        __syncthreads();
+        if constexpr (N1) read_frag(f0, S1{}, 0);
+        mma(f1);
+        if constexpr (N1) sched_mfma_reads<kReads>();
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    auto kloop = [&](auto edge) __attribute__((always_inline)) {
+        using T = std::integral_constant<bool, true>;
+        using F = std::integral_constant<bool, false>;
+        dma_a(I0{}, 0, edge);
+        load_b(st, 0, edge);
+        store_b(I0{}, st);
+        load_b(st, 1, edge);
+        __syncthreads();
+        read_frag(f0, I0{}, 0);
+        // nk is even (the host's condition for this kernel)
+        int kt = 0;
+        for (; kt + 2 < nk; kt += 2) {
+            step(kt, I0{}, T{}, T{}, edge);
+            step(kt + 1, I1{}, T{}, T{}, edge);
+        }
+        step(kt, I0{}, T{}, F{}, edge);
+        step(kt + 1, I1{}, F{}, F{}, edge);
+    };
+    if (m0 + kBM <= g.M && n0 + kBN <= g.N && g.K % kBK == 0)
+        kloop(std::integral_constant<bool, false>{});
+    else
+        kloop(std::integral_constant<bool, true>{});
+
+    // unscaled fp16 cannot hold this K~: the fallback recomputes the scores
+    if (mx > 65504.f) g.flag[0] = 1u;
+    nt_exp_epilogue<TI, TJ>(g, acc, reinterpret_cast<float*>(a0s), bh, m0, n0, tn, wm, wn, wave,
+                            lane);
 }
 
 // Encoded rows as fp16 with a power-of-two row scale: pass 1 finds the
@@ -581,8 +1031,10 @@ template <int PEK>
 __global__ __launch_bounds__(256) void k_encode_f16(const uint16_t* __restrict__ in,
                                                     uint16_t* __restrict__ out,
                                                     float* __restrict__ inv, long n_rows,
-                                                    int seq_len, int D, PeSide pe) {
+                                                    int seq_len, int D, PeSide pe,
+                                                    const unsigned* gate) {
     __shared__ float red[4];
+    if (gate != nullptr && *gate == 0u) return;  // gated fallback launch
     const int tid = threadIdx.x;
     for (long row = blockIdx.x; row < n_rows; row += gridDim.x) {
         const int pos = (int)(row % seq_len);
@@ -621,10 +1073,15 @@ __global__ __launch_bounds__(256) void k_encode_f16(const uint16_t* __restrict__
 // l_t exp(m_t - m) (the tiles' E sums brought to the common maximum), and
 // the factor g_t = exp(m_t - m) / l that turns tile t's E into the softmax
 // probabilities.  A row with no valid key (m = -inf) gets g = 0.
+//
+// It also lowers the fused K encoding's overflow word for the next call: it
+// runs after the gated fallback launches that read it.
 __global__ __launch_bounds__(256) void k_rowscale(const float* __restrict__ st_m,
                                                   const float* __restrict__ st_l,
-                                                  float* __restrict__ ga, long rows, int T) {
+                                                  float* __restrict__ ga, long rows, int T,
+                                                  unsigned* flag) {
     const long row = (long)blockIdx.x * 256 + threadIdx.x;
+    if (flag != nullptr && row == 0) *flag = 0u;
     if (row >= rows) return;
     const float* mr = st_m + row * T;
     const float* lr = st_l + row * T;
@@ -825,8 +1282,9 @@ __global__ __launch_bounds__(kEncThreads) void k_encode_f16_regs(const uint16_t*
 
 hipError_t launch_gemm_qk(int f16, const uint16_t* Q, const uint16_t* K, const float* qinv,
                           const float* kinv, uint16_t* E, float* st_m, float* st_l, int BH, int Lq,
-                          int Lk, int D, float scale, hipStream_t st) {
+                          int Lk, int D, float scale, const unsigned* gate, hipStream_t st) {
     GemmArgs g{};
+    g.gate = gate;
     g.A = Q;
     g.B = K;
     g.C = E;
@@ -858,6 +1316,59 @@ hipError_t launch_gemm_qk(int f16, const uint16_t* Q, const uint16_t* K, const f
     return hipGetLastError();
 }
 
+hipError_t launch_gemm_qk_enc(int benc, const uint16_t* Qe, const uint16_t* K, const float* qinv,
+                              const uint16_t* tab, int tab_rows, uint16_t* E, float* st_m,
+                              float* st_l, unsigned* flag, int BH, int Lq, int Lk, int D,
+                              float scale, hipStream_t st) {
+    // an even number of 64-deep K steps (the kernel runs them in pairs)
+    if (flag == nullptr || (benc != kBEncRaw && (tab == nullptr || tab_rows < Lk)) ||
+        D % 128 != 0)
+        return hipErrorInvalidValue;
+    GemmArgs g{};
+    g.A = Qe;
+    g.B = K;
+    g.C = E;
+    g.st_m = st_m;
+    g.st_l = st_l;
+    g.rs = qinv;
+    g.cs = nullptr;
+    g.M = Lq;
+    g.N = Lk;
+    g.K = D;
+    g.lda = D;
+    g.ldb = D;
+    g.ldc = Lk;
+    g.sa = (long)Lq * D;
+    g.sb = (long)Lk * D;
+    g.sc = (long)Lq * Lk;
+    g.tiles_m = (Lq + kBM - 1) / kBM;
+    g.tiles_n = (Lk + kBN - 1) / kBN;
+    g.heads = BH;
+    g.scale = scale;
+    g.tab = tab;
+    g.tab_rows = tab_rows;
+    g.flag = flag;
+    const long total = (long)g.tiles_m * g.tiles_n * BH;
+    const dim3 grid((unsigned)((total + 7) / 8 * 8)), block(kGemmThreads);
+    switch (benc) {
+        case kBEncRaw:
+            hipLaunchKernelGGL((k_gemm_qk_enc<kBEncRaw>), grid, block, 0, st, g);
+            break;
+        case kBEncSin:
+            hipLaunchKernelGGL((k_gemm_qk_enc<kBEncSin>), grid, block, 0, st, g);
+            break;
+        case kBEncRope:
+            hipLaunchKernelGGL((k_gemm_qk_enc<kBEncRope>), grid, block, 0, st, g);
+            break;
+        case kBEncRopeHalf:
+            hipLaunchKernelGGL((k_gemm_qk_enc<kBEncRopeHalf>), grid, block, 0, st, g);
+            break;
+        default:
+            return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
 template <int PEK>
 static void launch_encode_regs(int units, const uint16_t* in, uint16_t* out, float* inv,
                                long n_rows, int seq_len, int D, const PeSide& pe, hipStream_t st) {
@@ -875,8 +1386,11 @@ static void launch_encode_regs(int units, const uint16_t* in, uint16_t* out, flo
 }
 
 hipError_t launch_encode_f16(int pek, const uint16_t* in, uint16_t* out, float* inv, long n_rows,
-                             int seq_len, int D, const PeSide& pe, hipStream_t st) {
-    const long grid = n_rows < 65536 ? n_rows : 65536;
+                             int seq_len, int D, const PeSide& pe, const unsigned* gate,
+                             hipStream_t st) {
+    // a gated launch (the rarely taken fallback) uses the grid-stride form
+    // with a small grid, so that skipping it costs little
+    const long grid = gate ? (n_rows < 1024 ? n_rows : 1024) : (n_rows < 65536 ? n_rows : 65536);
     // register-resident form: D % 8 == 0, D <= 8192, the library's compact
     // tables, a rotary width that keeps 8-element units whole, and rows that
     // are whole sequences (n_rows a multiple of seq_len)
@@ -885,7 +1399,7 @@ hipError_t launch_encode_f16(int pek, const uint16_t* in, uint16_t* out, float* 
                       n_rows % seq_len == 0 &&
                       (pek == kPeNone || !pe.on || (pe.dup == 0 && pe.ld % 4 == 0)) &&
                       (!rope || !pe.on || pe.rotary % (pek == kPeRopeHalf ? 16 : 8) == 0);
-    if (fast) {
+    if (fast && gate == nullptr) {
         const int hu = (pek == kPeRopeHalf && pe.on) ? pe.rotary / 16 : 0;
         const int jobs = D / 8 - hu;
         const int units = (jobs + kEncThreads - 1) / kEncThreads;
@@ -911,19 +1425,19 @@ hipError_t launch_encode_f16(int pek, const uint16_t* in, uint16_t* out, float* 
     switch (pek) {
         case kPeNone:
             hipLaunchKernelGGL((k_encode_f16<kPeNone>), dim3((unsigned)grid), dim3(256), 0, st, in,
-                               out, inv, n_rows, seq_len, D, pe);
+                               out, inv, n_rows, seq_len, D, pe, gate);
             break;
         case kPeRopeInterleaved:
             hipLaunchKernelGGL((k_encode_f16<kPeRopeInterleaved>), dim3((unsigned)grid), dim3(256),
-                               0, st, in, out, inv, n_rows, seq_len, D, pe);
+                               0, st, in, out, inv, n_rows, seq_len, D, pe, gate);
             break;
         case kPeRopeHalf:
             hipLaunchKernelGGL((k_encode_f16<kPeRopeHalf>), dim3((unsigned)grid), dim3(256), 0, st,
-                               in, out, inv, n_rows, seq_len, D, pe);
+                               in, out, inv, n_rows, seq_len, D, pe, gate);
             break;
         case kPeSinusoidal:
             hipLaunchKernelGGL((k_encode_f16<kPeSinusoidal>), dim3((unsigned)grid), dim3(256), 0,
-                               st, in, out, inv, n_rows, seq_len, D, pe);
+                               st, in, out, inv, n_rows, seq_len, D, pe, gate);
             break;
         default:
             return hipErrorInvalidValue;
@@ -932,9 +1446,9 @@ hipError_t launch_encode_f16(int pek, const uint16_t* in, uint16_t* out, float* 
 }
 
 hipError_t launch_rowscale(const float* st_m, const float* st_l, float* ga, long rows, int T,
-                           hipStream_t st) {
+                           unsigned* flag, hipStream_t st) {
     hipLaunchKernelGGL(k_rowscale, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, st, st_m,
-                       st_l, ga, rows, T);
+                       st_l, ga, rows, T, flag);
     return hipGetLastError();
 }
 
