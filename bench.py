@@ -247,8 +247,12 @@ def main():
         peak = BF16_PEAK_TFLOPS if dtype == "bf16" else FP32_PEAK_TFLOPS
         roof = {"bound": "mfma", "achieved": round(tflops, 2), "peak": peak, "unit": "TFLOP/s",
                 "frac": round(tflops / peak, 4), "traffic": traffic}
-    roof["kernel"] = ("k_fused_small (one launch per step)" if path == am.ATN_PATH_FUSED_SMALL
-                      else "split-D pipeline (k_qk_partial + k_softmax + k_pv per step)")
+    roof["kernel"] = {
+        am.ATN_PATH_FUSED_SMALL: "k_fused_small (one launch per step)",
+        am.ATN_PATH_SPLIT_D: "split-D pipeline (k_qk_partial + k_softmax + k_pv per step)",
+        am.ATN_PATH_GEMM: ("GEMM path (encode, QK^T GEMM with exp epilogue, k_rowscale, PV GEMM "
+                           "per step; whole-step figure, per-kernel split in profiles/)"),
+    }.get(path, "unknown")
     roof["timing"] = "HIP events around one graph replay of all timed steps, on its stream"
     if traffic is not None:
         roof["traffic_note"] = ("bytes per launch from rocprofv3 FETCH_SIZE + WRITE_SIZE scaled by "
