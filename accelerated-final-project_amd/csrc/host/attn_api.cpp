@@ -354,13 +354,10 @@ int ensure_workspace(size_t bytes, hipStream_t stream, void** ws) {
 
 // ---------------------------------------------------------------- fused plan
 // Workspace layout (every path): a fixed 32 KiB sync region -- [0, 4) the
-// status word, [128, 132) the GEMM path's K-range word (raised when the
-// fused K encoding meets a value fp16 cannot hold), [256, 8448) one epoch
-// word per row group of the single-launch kernel, [8448, 24832) two sets of
-// 2048 per-workgroup done words -- then scratch.  Fixed offsets keep the
-// epoch words of one call from landing elsewhere when shapes change between
-// calls.
-constexpr size_t kSyncRangeOff = 128;
+// status word, [256, 8448) one epoch word per row group of the
+// single-launch kernel, [8448, 24832) two sets of 2048 per-workgroup done
+// words -- then scratch.  Fixed offsets keep the epoch words of one call
+// from landing elsewhere when shapes change between calls.
 constexpr size_t kSyncEpochOff = 256;
 constexpr size_t kSyncDoneOff = 8448;
 constexpr int kSyncMaxWorkgroups = 2048;
@@ -524,22 +521,16 @@ GemmPlan gemm_plan(int dtype, const Shape& s, const PePlan& plan) {
         return p;
     size_t off = kSyncBytes;
     auto take = [&](size_t b) { size_t o = off; off += round256(b); return o; };
-    // with a positional encoding both sides are re-encoded as scaled fp16
-    p.encoded = plan.pek != atn::kPeNone;
-    if (p.encoded) {
-        p.q_off = take((size_t)s.BH * s.Lq * s.D * 2);
-        p.k_off = take((size_t)s.BH * s.Lk * s.D * 2);
-        p.qs_off = take((size_t)s.BH * s.Lq * 4);
-        p.ks_off = take((size_t)s.BH * s.Lk * 4);
-    }
-    // K's encoding fused into the QK^T GEMM (K~ as unscaled fp16 from the
-    // library's fp16 tables; the K~ pass stays as the fallback): an even
-    // number of 64-deep K steps, library tables, rotate-half over all of D,
-    // and at most two 256-row query tiles -- every query tile's workgroups
-    // encode their K tiles again, so with more of them the encoding costs
-    // the MFMA-bound GEMM more than the K~ pass does (config 4: 892 us fused
-    // vs 642 + 199 us; config 5, one query tile: 160 us vs 143 + 110 us).
+    // with a positional encoding the query side is re-encoded as scaled fp16,
+    // and so is the key side unless its encoding runs inside the QK^T GEMM
+    // (k_gemm_qk_enc: fp16 tables, no K~ pass).  That takes an even number of
+    // 64-deep K steps, the library's tables, rotate-half over all of D, and
+    // at most two 256-row query tiles: every query tile's workgroups encode
+    // their K tiles again, so with more of them the encoding costs the
+    // MFMA-bound GEMM more than the K~ pass does (config 4: 892 us fused vs
+    // 642 + 199 us; config 5, one query tile: 160 us vs 143 + 110 us).
     // ATN_GEMM_FUSED_K=-1 turns it off, =1 forces it on (measurement).
+    p.encoded = plan.pek != atn::kPeNone;
     const int fk = env_int("ATN_GEMM_FUSED_K");
     if (p.encoded && s.D % 128 == 0 && !plan.caller_tables && fk >= 0 &&
         (fk > 0 || (s.Lq + 255) / 256 <= 2)) {
@@ -551,6 +542,14 @@ GemmPlan gemm_plan(int dtype, const Shape& s, const PePlan& plan) {
             p.benc = atn::kGemmEncRope;
         else if (plan.pek == atn::kPeRopeHalf && plan.rotary == s.D)
             p.benc = atn::kGemmEncRopeHalf;
+    }
+    if (p.encoded) {
+        p.q_off = take((size_t)s.BH * s.Lq * s.D * 2);
+        p.qs_off = take((size_t)s.BH * s.Lq * 4);
+        if (p.benc == 0) {
+            p.k_off = take((size_t)s.BH * s.Lk * s.D * 2);
+            p.ks_off = take((size_t)s.BH * s.Lk * 4);
+        }
     }
     p.tiles_k = (int)((s.Lk + 255) / 256);
     const size_t stats = (size_t)s.BH * s.Lq * p.tiles_k * 4;
@@ -626,19 +625,15 @@ int attention_core(int dtype, const void* Q, const void* K, const void* V, void*
         float* st_m = reinterpret_cast<float*>(w + gp.m_off);
         float* st_l = reinterpret_cast<float*>(w + gp.l_off);
         float* ga = reinterpret_cast<float*>(w + gp.g_off);
-        unsigned* range = nullptr;
         if (gp.encoded) {
             uint16_t* qd = reinterpret_cast<uint16_t*>(w + gp.q_off);
             uint16_t* kd = reinterpret_cast<uint16_t*>(w + gp.k_off);
             float* qs = reinterpret_cast<float*>(w + gp.qs_off);
             float* ks = reinterpret_cast<float*>(w + gp.ks_off);
             ATN_HIP(atn::launch_encode_f16(plan.q.on ? plan.pek : atn::kPeNone, qe, qd, qs,
-                                           (long)(s.BH * Lq), Lq, D, plan.q, nullptr, stream));
+                                           (long)(s.BH * Lq), Lq, D, plan.q, stream));
             if (gp.benc != 0) {
-                // K encoded inside the QK^T GEMM; if some |K~| does not fit
-                // fp16 the range word is raised and the two gated launches
-                // (the K~ pass with row scales, the plain GEMM) redo the scores
-                range = reinterpret_cast<unsigned*>(w + kSyncRangeOff);
+                // K encoded inside the QK^T GEMM
                 const uint16_t* tab = nullptr;
                 int tab_rows = 0;
                 if (gp.benc != atn::kGemmEncRaw) {
@@ -650,22 +645,18 @@ int attention_core(int dtype, const void* Q, const void* K, const void* V, void*
                     tab_rows = t16->npos;
                 }
                 ATN_HIP(atn::launch_gemm_qk_enc(gp.benc, qd, ke, qs, tab, tab_rows, E, st_m, st_l,
-                                                range, (int)s.BH, Lq, Lk, D, scale, stream));
-                ATN_HIP(atn::launch_encode_f16(plan.k.on ? plan.pek : atn::kPeNone, ke, kd, ks,
-                                               (long)(s.BH * Lk), Lk, D, plan.k, range, stream));
-                ATN_HIP(atn::launch_gemm_qk(1, qd, kd, qs, ks, E, st_m, st_l, (int)s.BH, Lq, Lk, D,
-                                            scale, range, stream));
+                                                (int)s.BH, Lq, Lk, D, scale, stream));
             } else {
                 ATN_HIP(atn::launch_encode_f16(plan.k.on ? plan.pek : atn::kPeNone, ke, kd, ks,
-                                               (long)(s.BH * Lk), Lk, D, plan.k, nullptr, stream));
+                                               (long)(s.BH * Lk), Lk, D, plan.k, stream));
                 ATN_HIP(atn::launch_gemm_qk(1, qd, kd, qs, ks, E, st_m, st_l, (int)s.BH, Lq, Lk, D,
-                                            scale, nullptr, stream));
+                                            scale, stream));
             }
         } else {
             ATN_HIP(atn::launch_gemm_qk(0, qe, ke, nullptr, nullptr, E, st_m, st_l, (int)s.BH, Lq,
-                                        Lk, D, scale, nullptr, stream));
+                                        Lk, D, scale, stream));
         }
-        ATN_HIP(atn::launch_rowscale(st_m, st_l, ga, s.BH * Lq, gp.tiles_k, range, stream));
+        ATN_HIP(atn::launch_rowscale(st_m, st_l, ga, s.BH * Lq, gp.tiles_k, stream));
         ATN_HIP(atn::launch_gemm_pv(E, ga, static_cast<const uint16_t*>(V),
                                     static_cast<uint16_t*>(out), (int)s.BH, Lq, Lk, D, stream));
         return ATN_OK;

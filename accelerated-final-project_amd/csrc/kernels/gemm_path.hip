@@ -205,8 +205,6 @@ struct GemmArgs {
     float scale;
     const uint16_t* tab;          // fused K encoding: fp16 table (k_gemm_qk_enc)
     int tab_rows;                 // positions in tab
-    unsigned* flag;               // fused K encoding: overflow word, raised on |K~| > 65504
-    const unsigned* gate;         // when set, the launch does nothing unless *gate != 0
 };
 
 // NT exp epilogue: scores S = scale * acc * (row scale) * (column scale) of
@@ -216,17 +214,21 @@ struct GemmArgs {
 // (red: 4 x 256 floats, free once every wave is done with the K loop).
 // Lane layout of acc[i][j]: column (lane % 32) and rows 8 (r / 4) +
 // 4 (lane / 32) + r % 4 of each 32 x 32 tile.
+// cs_lds (optional) replaces g.cs: the tile's 256 column scales in LDS.
 template <int TI, int TJ>
 __device__ __forceinline__ void nt_exp_epilogue(const GemmArgs& g, v16f (&acc)[TI][TJ],
                                                 float* red, int bh, int m0, int n0, int tn,
-                                                int wm, int wn, int wave, int lane) {
+                                                int wm, int wn, int wave, int lane,
+                                                const float* cs_lds = nullptr) {
     __syncthreads();  // every wave is done with the LDS stages
     const int half = lane >> 5, lc = lane & 31, cw = wave & 1;
 #pragma unroll
     for (int j = 0; j < TJ; ++j) {
         const int col = n0 + wn + j * 32 + lc;
         const float csc =
-            col < g.N ? (g.cs ? g.cs[(long)bh * g.N + col] * g.scale : g.scale) : 0.f;
+            col < g.N ? (cs_lds ? cs_lds[col - n0] * g.scale
+                                : (g.cs ? g.cs[(long)bh * g.N + col] * g.scale : g.scale))
+                      : 0.f;
 #pragma unroll
         for (int i = 0; i < TI; ++i)
 #pragma unroll
@@ -317,9 +319,6 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm(GemmArgs g) {
     uint16_t(*As)[kTileElems] = reinterpret_cast<uint16_t(*)[kTileElems]>(lds);
     uint16_t(*Bs)[kTileElems] = reinterpret_cast<uint16_t(*)[kTileElems]>(lds + 2 * kTileElems);
 
-    // a gated launch (the fallback behind the fused K encoding) runs only
-    // when the overflow word was raised
-    if (g.gate != nullptr && *g.gate == 0u) return;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const long per_head = (long)g.tiles_m * g.tiles_n;
@@ -665,9 +664,10 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm(GemmArgs g) {
 //   kBEncRopeHalf  rotate-half, pairs (i, i + D/2): each K step takes 32 dims
 //                  of the first half and their 32 partners (A's columns in the
 //                  same order), so both halves of a rotation are in one thread
-// Each value is rounded once to fp16; a workgroup that meets |K~| > 65504
-// raises the overflow word, and the host's gated fallback (k_encode_f16 with
-// row scales, then k_gemm) recomputes every score of the call.
+// Each value is rounded once to fp16.  A workgroup whose K tile holds a row
+// with |K~| > 65504 computes its tile a second time with per-row power-of-two
+// scales (the largest |K~| of each key row, tracked during the first pass,
+// placed in [2^14, 2^15) as k_encode_f16 does), so any input range works.
 //
 // A = Q~ (k_encode_f16's fp16 rows, scales in rs) goes straight from memory
 // to LDS (buffer loads with the LDS destination, no register stage): each
@@ -733,9 +733,12 @@ __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w 
 __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
 // 8 bf16 -> 8 fp16: as they are, or plus the chunk's table values (sinusoidal),
-// or rotated pairwise (interleaved RoPE); mx keeps the largest |K~|.
-template <int BENC>
-__device__ __forceinline__ uint4 enc_chunk(const uint4& w, const uint4& t, float& mx) {
+// or rotated pairwise (interleaved RoPE).  Unscaled (SC false), mx keeps the
+// largest |K~|; scaled, every value is multiplied by the row scale sc (a
+// power of two) before its one rounding to fp16.
+template <int BENC, bool SC = false>
+__device__ __forceinline__ uint4 enc_chunk(const uint4& w, const uint4& t, float& mx,
+                                           float sc = 1.f) {
     const uint32_t x[4] = {w.x, w.y, w.z, w.w};
     const uint32_t tt[4] = {t.x, t.y, t.z, t.w};
     uint32_t y[4];
@@ -751,7 +754,12 @@ __device__ __forceinline__ uint4 enc_chunk(const uint4& w, const uint4& t, float
             a = fmix_lo_sub(a0, tt[i], fmul_hi(b, tt[i]));  // a cos - b sin
             b = fmix_hi(a0, tt[i], fmul_lo(b, tt[i]));      // a sin + b cos
         }
-        mx = fmaxf(mx, fmaxf(fabsf(a), fabsf(b)));
+        if constexpr (SC) {
+            a *= sc;
+            b *= sc;
+        } else {
+            mx = fmaxf(mx, fmaxf(fabsf(a), fabsf(b)));
+        }
         y[i] = pk_f16(a, b);
     }
     return make_uint4(y[0], y[1], y[2], y[3]);
@@ -759,8 +767,9 @@ __device__ __forceinline__ uint4 enc_chunk(const uint4& w, const uint4& t, float
 
 // Rotate-half: w0 = 8 dims of the first half, w1 = their partners, t0/t1 =
 // (cos, sin) words of the 8 pairs; both chunks rewritten as fp16.
+template <bool SC = false>
 __device__ __forceinline__ void enc_half(uint4& w0, uint4& w1, const uint4& t0, const uint4& t1,
-                                         float& mx) {
+                                         float& mx, float sc = 1.f) {
     const uint32_t x0[4] = {w0.x, w0.y, w0.z, w0.w}, x1[4] = {w1.x, w1.y, w1.z, w1.w};
     const uint32_t tt[8] = {t0.x, t0.y, t0.z, t0.w, t1.x, t1.y, t1.z, t1.w};
     uint32_t y0[4], y1[4];
@@ -774,7 +783,12 @@ __device__ __forceinline__ void enc_half(uint4& w0, uint4& w1, const uint4& t0, 
             const uint32_t w = tt[2 * i + h];
             r0[h] = fmix_lo_sub(a, w, fmul_hi(b, w));  // a cos - b sin
             r1[h] = fmix_hi(a, w, fmul_lo(b, w));      // a sin + b cos
-            mx = fmaxf(mx, fmaxf(fabsf(r0[h]), fabsf(r1[h])));
+            if constexpr (SC) {
+                r0[h] *= sc;
+                r1[h] *= sc;
+            } else {
+                mx = fmaxf(mx, fmaxf(fabsf(r0[h]), fabsf(r1[h])));
+            }
         }
         y0[i] = pk_f16(r0[0], r0[1]);
         y1[i] = pk_f16(r1[0], r1[1]);
@@ -783,15 +797,29 @@ __device__ __forceinline__ void enc_half(uint4& w0, uint4& w1, const uint4& t0, 
     w1 = make_uint4(y1[0], y1[1], y1[2], y1[3]);
 }
 
-template <int BENC>
-__global__ __launch_bounds__(kGemmThreads) void k_gemm_qk_enc(GemmArgs g) {
+// LDS of k_gemm_qk_enc: A stages (unpadded, swizzled), B stages (padded
+// rows), and the inverse key-row scales of the scaled pass.  The kernel owns
+// the arrays; the tile code takes them as pointers, so that once inlined
+// into the kernel every access still names its array (and the compiler can
+// tell a DMA target from the tiles being read).
+constexpr int kQkAElems = kBM * kBK;
+struct QkEncLds {
+    uint16_t *a0, *a1, *b0, *b1;
+    float* kcs;
+};
+
+// One tile of k_gemm_qk_enc.  Unscaled (SC false) it returns true when a key
+// row of the tile exceeds fp16's range, having put the inverse row scales in
+// L.kcs; scaled, it reads its row scales there.
+template <int BENC, bool SC>
+__device__ __forceinline__ bool qk_enc_tile(const GemmArgs& g, const QkEncLds& L) {
     constexpr bool kHalf = BENC == kBEncRopeHalf;
     constexpr bool kTab = BENC != kBEncRaw;
-    constexpr int kAElems = kBM * kBK;  // unpadded, swizzled A stage
-    __shared__ __align__(16) uint16_t a0s[kAElems];
-    __shared__ __align__(16) uint16_t a1s[kAElems];
-    __shared__ __align__(16) uint16_t b0s[kTileElems];
-    __shared__ __align__(16) uint16_t b1s[kTileElems];
+    uint16_t* const a0s = L.a0;
+    uint16_t* const a1s = L.a1;
+    uint16_t* const b0s = L.b0;
+    uint16_t* const b1s = L.b1;
+    float* const kcs = L.kcs;
     using I0 = std::integral_constant<int, 0>;
     using I1 = std::integral_constant<int, 1>;
     auto As = [&](auto S) -> uint16_t* {
@@ -806,7 +834,7 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm_qk_enc(GemmArgs g) {
     const long per_head = (long)g.tiles_m * g.tiles_n;
     const long total = per_head * g.heads;
     const long t = xcd_tile(blockIdx.x, total);
-    if (t >= total) return;
+    if (t >= total) return false;
     const int bh = __builtin_amdgcn_readfirstlane((int)(t / per_head));
     const int rem = (int)(t - (long)bh * per_head);
     const int tm = rem / g.tiles_n, tn = rem - tm * g.tiles_n;
@@ -905,10 +933,16 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm_qk_enc(GemmArgs g) {
             }
         }
     };
-    float mx = 0.f;  // largest |K~| this thread wrote
+    float mx[2] = {0.f, 0.f};  // largest |K~| of key rows br, br + 128 (unscaled pass)
+    float ksc[2] = {1.f, 1.f};  // their row scales (scaled pass)
+    if constexpr (SC) {
+        ksc[0] = 1.0f / kcs[br];
+        ksc[1] = 1.0f / kcs[br + 128];
+    }
     // each chunk (pair) is stored as soon as it is encoded, which ends its
     // registers' live range before the next one's temporaries
-    auto store_b = [&](auto S, Stage& r) __attribute__((always_inline)) {
+    auto store_b = [&](auto S, Stage& r, auto scaled) __attribute__((always_inline)) {
+        constexpr bool kSc = decltype(scaled)::value;
         uint16_t* dst = Bs(S);
         auto put = [&](int u) {
             *reinterpret_cast<uint4*>(&dst[(br + 128 * (u >> 1)) * kLdsRow + 8 * (bc + 4 * (u & 1))]) =
@@ -917,10 +951,10 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm_qk_enc(GemmArgs g) {
 #pragma unroll
         for (int p = 0; p < 2; ++p) {
             if constexpr (kHalf) {
-                enc_half(r.b[2 * p], r.b[2 * p + 1], r.t[2 * p], r.t[2 * p + 1], mx);
+                enc_half<kSc>(r.b[2 * p], r.b[2 * p + 1], r.t[2 * p], r.t[2 * p + 1], mx[p], ksc[p]);
             } else {
-                r.b[2 * p] = enc_chunk<BENC>(r.b[2 * p], r.t[2 * p], mx);
-                r.b[2 * p + 1] = enc_chunk<BENC>(r.b[2 * p + 1], r.t[2 * p + 1], mx);
+                r.b[2 * p] = enc_chunk<BENC, kSc>(r.b[2 * p], r.t[2 * p], mx[p], ksc[p]);
+                r.b[2 * p + 1] = enc_chunk<BENC, kSc>(r.b[2 * p + 1], r.t[2 * p + 1], mx[p], ksc[p]);
             }
             put(2 * p);
             put(2 * p + 1);
@@ -970,13 +1004,14 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm_qk_enc(GemmArgs g) {
     constexpr int kReads = TI + TJ;
     Stage st;
     Frag f0, f1;
-    auto step = [&](int kt, auto S, auto next, auto next2, auto edge) __attribute__((always_inline)) {
+    auto step = [&](int kt, auto S, auto next, auto next2, auto edge, auto scaled)
+                    __attribute__((always_inline)) {
         constexpr int s = decltype(S)::value;
         using S1 = std::integral_constant<int, s ^ 1>;
         constexpr bool N1 = decltype(next)::value, N2 = decltype(next2)::value;
         read_frag(f1, S, 1);
         mma(f0);
-        if constexpr (N1) store_b(S1{}, st);
+        if constexpr (N1) store_b(S1{}, st, scaled);
         sched_mfma_reads<kReads>();
         __builtin_amdgcn_sched_barrier(0);
         if constexpr (N1) dma_a(S1{}, kt + 1, edge);
@@ -996,33 +1031,77 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm_qk_enc(GemmArgs g) {
         if constexpr (N1) sched_mfma_reads<kReads>();
         __builtin_amdgcn_sched_barrier(0);
     };
-    auto kloop = [&](auto edge) __attribute__((always_inline)) {
+    auto kloop = [&](auto edge, auto scaled) __attribute__((always_inline)) {
         using T = std::integral_constant<bool, true>;
         using F = std::integral_constant<bool, false>;
         dma_a(I0{}, 0, edge);
         load_b(st, 0, edge);
-        store_b(I0{}, st);
+        store_b(I0{}, st, scaled);
         load_b(st, 1, edge);
         __syncthreads();
         read_frag(f0, I0{}, 0);
         // nk is even (the host's condition for this kernel)
         int kt = 0;
         for (; kt + 2 < nk; kt += 2) {
-            step(kt, I0{}, T{}, T{}, edge);
-            step(kt + 1, I1{}, T{}, T{}, edge);
+            step(kt, I0{}, T{}, T{}, edge, scaled);
+            step(kt + 1, I1{}, T{}, T{}, edge, scaled);
         }
-        step(kt, I0{}, T{}, F{}, edge);
-        step(kt + 1, I1{}, F{}, F{}, edge);
+        step(kt, I0{}, T{}, F{}, edge, scaled);
+        step(kt + 1, I1{}, F{}, F{}, edge, scaled);
     };
     if (m0 + kBM <= g.M && n0 + kBN <= g.N && g.K % kBK == 0)
-        kloop(std::integral_constant<bool, false>{});
+        kloop(std::integral_constant<bool, false>{}, std::integral_constant<bool, SC>{});
     else
-        kloop(std::integral_constant<bool, true>{});
+        kloop(std::integral_constant<bool, true>{}, std::integral_constant<bool, SC>{});
 
-    // unscaled fp16 cannot hold this K~: the fallback recomputes the scores
-    if (mx > 65504.f) g.flag[0] = 1u;
+    // A key row beyond fp16's range (|K~| > 65504) in the unscaled pass: the
+    // tile is computed again (the scaled pass) with the row scales
+    // k_encode_f16 would use (largest |K~| of the row in [2^14, 2^15)), and
+    // that pass's epilogue multiplies the inverse scales back and overwrites
+    // this one's output.  The four threads of a key row are one lane quad.
+    bool redo = false;
+    if constexpr (!SC) {
+        float rmax[2];
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+            const float m = fmaxf(mx[p], dpp<kDppQuadXor1>(mx[p]));
+            rmax[p] = fmaxf(m, dpp<kDppQuadXor2>(m));
+        }
+        redo = __syncthreads_or((rmax[0] > 65504.f) | (rmax[1] > 65504.f));
+        if (redo) {
+#pragma unroll
+            for (int p = 0; p < 2; ++p) {
+                int e = 0;
+                if (rmax[p] > 0.f && rmax[p] <= 3.0e38f) e = 14 - ilogbf(rmax[p]);
+                e = max(-100, min(100, e));
+                if ((tid & 3) == 0) kcs[br + 128 * p] = ldexpf(1.0f, -e);
+            }
+        }
+    }
     nt_exp_epilogue<TI, TJ>(g, acc, reinterpret_cast<float*>(a0s), bh, m0, n0, tn, wm, wn, wave,
-                            lane);
+                            lane, SC ? kcs : nullptr);
+    return redo;
+}
+
+// The scaled pass: it only runs when a key row overflows, after the first
+// pass's epilogue, so nothing of the first pass is live across it.  (Out of
+// line, as a call, it made the kernel 2.6x slower: the callee's saved
+// registers gave every lane a 532-byte stack.)
+template <int BENC>
+__device__ __forceinline__ void qk_enc_scaled_tile(const GemmArgs& g, const QkEncLds& L) {
+    __syncthreads();  // every wave is done with the first pass's epilogue (LDS)
+    (void)qk_enc_tile<BENC, true>(g, L);
+}
+
+template <int BENC>
+__global__ __launch_bounds__(kGemmThreads) void k_gemm_qk_enc(GemmArgs g) {
+    __shared__ __align__(16) uint16_t a0s[kQkAElems];
+    __shared__ __align__(16) uint16_t a1s[kQkAElems];
+    __shared__ __align__(16) uint16_t b0s[kTileElems];
+    __shared__ __align__(16) uint16_t b1s[kTileElems];
+    __shared__ float kcs[kBN];
+    const QkEncLds L{a0s, a1s, b0s, b1s, kcs};
+    if (qk_enc_tile<BENC, false>(g, L)) qk_enc_scaled_tile<BENC>(g, L);
 }
 
 // Encoded rows as fp16 with a power-of-two row scale: pass 1 finds the
@@ -1033,10 +1112,8 @@ template <int PEK>
 __global__ __launch_bounds__(256) void k_encode_f16(const uint16_t* __restrict__ in,
                                                     uint16_t* __restrict__ out,
                                                     float* __restrict__ inv, long n_rows,
-                                                    int seq_len, int D, PeSide pe,
-                                                    const unsigned* gate) {
+                                                    int seq_len, int D, PeSide pe) {
     __shared__ float red[4];
-    if (gate != nullptr && *gate == 0u) return;  // gated fallback launch
     const int tid = threadIdx.x;
     for (long row = blockIdx.x; row < n_rows; row += gridDim.x) {
         const int pos = (int)(row % seq_len);
@@ -1075,15 +1152,10 @@ __global__ __launch_bounds__(256) void k_encode_f16(const uint16_t* __restrict__
 // l_t exp(m_t - m) (the tiles' E sums brought to the common maximum), and
 // the factor g_t = exp(m_t - m) / l that turns tile t's E into the softmax
 // probabilities.  A row with no valid key (m = -inf) gets g = 0.
-//
-// It also lowers the fused K encoding's overflow word for the next call: it
-// runs after the gated fallback launches that read it.
 __global__ __launch_bounds__(256) void k_rowscale(const float* __restrict__ st_m,
                                                   const float* __restrict__ st_l,
-                                                  float* __restrict__ ga, long rows, int T,
-                                                  unsigned* flag) {
+                                                  float* __restrict__ ga, long rows, int T) {
     const long row = (long)blockIdx.x * 256 + threadIdx.x;
-    if (flag != nullptr && row == 0) *flag = 0u;
     if (row >= rows) return;
     const float* mr = st_m + row * T;
     const float* lr = st_l + row * T;
@@ -1284,9 +1356,8 @@ __global__ __launch_bounds__(kEncThreads) void k_encode_f16_regs(const uint16_t*
 
 hipError_t launch_gemm_qk(int f16, const uint16_t* Q, const uint16_t* K, const float* qinv,
                           const float* kinv, uint16_t* E, float* st_m, float* st_l, int BH, int Lq,
-                          int Lk, int D, float scale, const unsigned* gate, hipStream_t st) {
+                          int Lk, int D, float scale, hipStream_t st) {
     GemmArgs g{};
-    g.gate = gate;
     g.A = Q;
     g.B = K;
     g.C = E;
@@ -1320,11 +1391,10 @@ hipError_t launch_gemm_qk(int f16, const uint16_t* Q, const uint16_t* K, const f
 
 hipError_t launch_gemm_qk_enc(int benc, const uint16_t* Qe, const uint16_t* K, const float* qinv,
                               const uint16_t* tab, int tab_rows, uint16_t* E, float* st_m,
-                              float* st_l, unsigned* flag, int BH, int Lq, int Lk, int D,
-                              float scale, hipStream_t st) {
+                              float* st_l, int BH, int Lq, int Lk, int D, float scale,
+                              hipStream_t st) {
     // an even number of 64-deep K steps (the kernel runs them in pairs)
-    if (flag == nullptr || (benc != kBEncRaw && (tab == nullptr || tab_rows < Lk)) ||
-        D % 128 != 0)
+    if ((benc != kBEncRaw && (tab == nullptr || tab_rows < Lk)) || D % 128 != 0)
         return hipErrorInvalidValue;
     GemmArgs g{};
     g.A = Qe;
@@ -1349,7 +1419,6 @@ hipError_t launch_gemm_qk_enc(int benc, const uint16_t* Qe, const uint16_t* K, c
     g.scale = scale;
     g.tab = tab;
     g.tab_rows = tab_rows;
-    g.flag = flag;
     const long total = (long)g.tiles_m * g.tiles_n * BH;
     const dim3 grid((unsigned)((total + 7) / 8 * 8)), block(kGemmThreads);
     switch (benc) {
@@ -1388,11 +1457,8 @@ static void launch_encode_regs(int units, const uint16_t* in, uint16_t* out, flo
 }
 
 hipError_t launch_encode_f16(int pek, const uint16_t* in, uint16_t* out, float* inv, long n_rows,
-                             int seq_len, int D, const PeSide& pe, const unsigned* gate,
-                             hipStream_t st) {
-    // a gated launch (the rarely taken fallback) uses the grid-stride form
-    // with a small grid, so that skipping it costs little
-    const long grid = gate ? (n_rows < 1024 ? n_rows : 1024) : (n_rows < 65536 ? n_rows : 65536);
+                             int seq_len, int D, const PeSide& pe, hipStream_t st) {
+    const long grid = n_rows < 65536 ? n_rows : 65536;
     // register-resident form: D % 8 == 0, D <= 8192, the library's compact
     // tables, a rotary width that keeps 8-element units whole, and rows that
     // are whole sequences (n_rows a multiple of seq_len)
@@ -1401,7 +1467,7 @@ hipError_t launch_encode_f16(int pek, const uint16_t* in, uint16_t* out, float* 
                       n_rows % seq_len == 0 &&
                       (pek == kPeNone || !pe.on || (pe.dup == 0 && pe.ld % 4 == 0)) &&
                       (!rope || !pe.on || pe.rotary % (pek == kPeRopeHalf ? 16 : 8) == 0);
-    if (fast && gate == nullptr) {
+    if (fast) {
         const int hu = (pek == kPeRopeHalf && pe.on) ? pe.rotary / 16 : 0;
         const int jobs = D / 8 - hu;
         const int units = (jobs + kEncThreads - 1) / kEncThreads;
@@ -1427,19 +1493,19 @@ hipError_t launch_encode_f16(int pek, const uint16_t* in, uint16_t* out, float* 
     switch (pek) {
         case kPeNone:
             hipLaunchKernelGGL((k_encode_f16<kPeNone>), dim3((unsigned)grid), dim3(256), 0, st, in,
-                               out, inv, n_rows, seq_len, D, pe, gate);
+                               out, inv, n_rows, seq_len, D, pe);
             break;
         case kPeRopeInterleaved:
             hipLaunchKernelGGL((k_encode_f16<kPeRopeInterleaved>), dim3((unsigned)grid), dim3(256),
-                               0, st, in, out, inv, n_rows, seq_len, D, pe, gate);
+                               0, st, in, out, inv, n_rows, seq_len, D, pe);
             break;
         case kPeRopeHalf:
             hipLaunchKernelGGL((k_encode_f16<kPeRopeHalf>), dim3((unsigned)grid), dim3(256), 0, st,
-                               in, out, inv, n_rows, seq_len, D, pe, gate);
+                               in, out, inv, n_rows, seq_len, D, pe);
             break;
         case kPeSinusoidal:
             hipLaunchKernelGGL((k_encode_f16<kPeSinusoidal>), dim3((unsigned)grid), dim3(256), 0,
-                               st, in, out, inv, n_rows, seq_len, D, pe, gate);
+                               st, in, out, inv, n_rows, seq_len, D, pe);
             break;
         default:
             return hipErrorInvalidValue;
@@ -1448,9 +1514,9 @@ hipError_t launch_encode_f16(int pek, const uint16_t* in, uint16_t* out, float* 
 }
 
 hipError_t launch_rowscale(const float* st_m, const float* st_l, float* ga, long rows, int T,
-                           unsigned* flag, hipStream_t st) {
+                           hipStream_t st) {
     hipLaunchKernelGGL(k_rowscale, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, st, st_m,
-                       st_l, ga, rows, T, flag);
+                       st_l, ga, rows, T);
     return hipGetLastError();
 }
 

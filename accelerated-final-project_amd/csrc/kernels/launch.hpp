@@ -36,25 +36,21 @@ hipError_t launch_fused_small(int dtype, int pek, const void* Q, const void* K, 
 // max) (fp16) with per-(row, 256-key tile) max and sum, per-row factors
 // g_t = exp(m_t - m) / l, O = (E g) V.  Needs D % 8 == 0, Lk % 8 == 0 and
 // 16-byte aligned bases.
-// gate: when non-null the launch does nothing unless *gate != 0 (the
-// fallback behind the fused K encoding)
 hipError_t launch_encode_f16(int pek, const uint16_t* in, uint16_t* out, float* inv, long n_rows,
-                             int seq_len, int D, const PeSide& pe, const unsigned* gate,
-                             hipStream_t st);
+                             int seq_len, int D, const PeSide& pe, hipStream_t st);
 hipError_t launch_gemm_qk(int f16, const uint16_t* Q, const uint16_t* K, const float* qinv,
                           const float* kinv, uint16_t* E, float* st_m, float* st_l, int BH, int Lq,
-                          int Lk, int D, float scale, const unsigned* gate, hipStream_t st);
+                          int Lk, int D, float scale, hipStream_t st);
 // QK^T GEMM on fp16 Q~ (row scales qinv) and raw bf16 K, K's encoding
 // applied in the kernel from an fp16 table (tab: tab_rows positions x D
-// 16-bit units); raises *flag when some |K~| exceeds fp16's range.
+// 16-bit units); needs D % 128 == 0.
 constexpr int kGemmEncRaw = 1, kGemmEncSin = 2, kGemmEncRope = 3, kGemmEncRopeHalf = 4;
 hipError_t launch_gemm_qk_enc(int benc, const uint16_t* Qe, const uint16_t* K, const float* qinv,
                               const uint16_t* tab, int tab_rows, uint16_t* E, float* st_m,
-                              float* st_l, unsigned* flag, int BH, int Lq, int Lk, int D,
-                              float scale, hipStream_t st);
-// flag (optional): lowered to 0 for the next call
+                              float* st_l, int BH, int Lq, int Lk, int D, float scale,
+                              hipStream_t st);
 hipError_t launch_rowscale(const float* st_m, const float* st_l, float* ga, long rows, int T,
-                           unsigned* flag, hipStream_t st);
+                           hipStream_t st);
 hipError_t launch_gemm_pv(const uint16_t* E, const float* ga, const uint16_t* V, uint16_t* O,
                           int BH, int Lq, int Lk, int D, hipStream_t st);
 

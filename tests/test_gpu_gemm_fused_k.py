@@ -9,10 +9,10 @@ against the CPU oracle: within rel 2e-2 of the fp32 oracle run on the
 bf16-rounded inputs (elementwise against |ref| and rms(ref), and
 norm-wise).
 
-Keys whose encoded magnitude exceeds fp16's range (65504) raise the range
-word; the gated launches then recompute the scores from the row-scaled K~,
-and the next call on ordinary inputs must come out right again (the word is
-lowered after every call).
+Keys whose encoded magnitude exceeds fp16's range (65504) make the
+workgroups whose key tiles hold them compute their tiles a second time with
+per-row power-of-two scales (those of the row-scaled K~ pass); tiles
+without such keys keep the first pass.
 """
 import os
 
@@ -50,13 +50,13 @@ def _ref(mode, Q, K, V, rows=None):
                                  rows=rows, nthreads=16)
 
 
-def _run(am, q, k, v, shape, desc, fused, ws=None):
+def _run(am, q, k, v, shape, desc, fused):
     import hip_rt
     old = os.environ.get("ATN_GEMM_FUSED_K")
     os.environ["ATN_GEMM_FUSED_K"] = "1" if fused else "-1"
     try:
         out = H.empty(shape, "bf16")
-        am.attention_ex(q, k, v, out, pe=desc, workspace=ws)
+        am.attention_ex(q, k, v, out, pe=desc)
         hip_rt.synchronize()
         return out.numpy()
     finally:
@@ -106,16 +106,16 @@ def test_fused_k_config4_head_shape(am, dev):
 
 
 @pytest.mark.parametrize("mode", ["rope_half", "rope_inter", "sin_k_only", "rope_q_only"])
-def test_fused_k_range_fallback(am, dev, mode):
+def test_fused_k_range_scaled_pass(am, dev, mode):
     """Two key rows carry ~1e5 (beyond fp16) in dims 8, 9, 8 + D/2, 9 + D/2,
     where every query is zero (so after the encodings, which pair dims
     within those sets, those products are exactly zero and the scores stay
-    well conditioned): the fused GEMM raises the range word and the gated
-    fallback recomputes the scores from row-scaled K~.  Then a call on
-    ordinary keys must be right, i.e. the word was lowered."""
+    well conditioned): the workgroups of those rows' key tiles redo their
+    tiles with row scales, the others do not.  Then a call on ordinary keys
+    must be right as well."""
     import hip_rt
     B, Hh, Lq, Lk, D = 1, 2, 256, 512, 256
-    print(f"[case] fused K range fallback {mode}", flush=True)
+    print(f"[case] fused K scaled pass {mode}", flush=True)
     desc = am.make_pe(**MODES[mode])
     rng = np.random.default_rng(5)
     Qf = rng.standard_normal((B, Hh, Lq, D), dtype=np.float32)
@@ -129,25 +129,11 @@ def test_fused_k_range_fallback(am, dev, mode):
     q, kb, v = (hip_rt.DeviceArray.from_numpy(x, "bf16") for x in (Qf, Kbig, Vf))
     Q, Kb, V = (t.numpy() for t in (q, kb, v))
     assert np.abs(Kb).max() > 65504
-    # caller workspace: the range word is float index 32 (byte 128)
-    nb = am.workspace_bytes(am.ATN_DTYPE_BF16, B, Hh, Lq, Lk, D, desc)
-    ws = hip_rt.DeviceArray.from_numpy(np.zeros(nb // 4, np.float32), "f32")
-    got = _run(am, q, kb, v, Q.shape, desc, True, ws)
+    got = _run(am, q, kb, v, Q.shape, desc, True)
     n, nrel, mabs = H.check_bf16(got, _ref(mode, Q, Kb, V))
     assert n == 0, f"large keys: normwise rel {nrel}, max abs {mabs}"
-    assert ws.numpy()[32] == 0.0, "range word left raised"
     k = hip_rt.DeviceArray.from_numpy(Kf, "bf16")
     K = k.numpy()
-    ref = _ref(mode, Q, K, V)
-    got = _run(am, q, k, v, Q.shape, desc, True, ws)
-    n, nrel, mabs = H.check_bf16(got, ref)
-    assert n == 0, f"after the fallback: normwise rel {nrel}, max abs {mabs}"
-    # a word found raised (e.g. a caller's workspace not zeroed) only costs
-    # the fallback: the result is right and the word is lowered
-    wsh = np.zeros(nb // 4, np.float32)
-    wsh[32] = 1.0
-    ws2 = hip_rt.DeviceArray.from_numpy(wsh, "f32")
-    got = _run(am, q, k, v, Q.shape, desc, True, ws2)
-    n, nrel, mabs = H.check_bf16(got, ref)
-    assert n == 0, f"raised on entry: normwise rel {nrel}, max abs {mabs}"
-    assert ws2.numpy()[32] == 0.0, "range word left raised"
+    got = _run(am, q, k, v, Q.shape, desc, True)
+    n, nrel, mabs = H.check_bf16(got, _ref(mode, Q, K, V))
+    assert n == 0, f"ordinary keys: normwise rel {nrel}, max abs {mabs}"
