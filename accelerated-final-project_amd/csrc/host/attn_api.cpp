@@ -656,8 +656,7 @@ int attention_core(int dtype, const void* Q, const void* K, const void* V, void*
             ATN_HIP(atn::launch_gemm_qk(0, qe, ke, nullptr, nullptr, E, st_m, st_l, (int)s.BH, Lq,
                                         Lk, D, scale, stream));
         }
-        ATN_HIP(atn::launch_rowscale(st_m, st_l, ga, s.BH * Lq, gp.tiles_k, stream));
-        ATN_HIP(atn::launch_gemm_pv(E, ga, static_cast<const uint16_t*>(V),
+        ATN_HIP(atn::launch_gemm_pv(E, st_m, st_l, ga, static_cast<const uint16_t*>(V),
                                     static_cast<uint16_t*>(out), (int)s.BH, Lq, Lk, D, stream));
         return ATN_OK;
     }

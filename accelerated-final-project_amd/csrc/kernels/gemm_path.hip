@@ -14,10 +14,12 @@
 //   k_gemm  (NT)  S = scale * Q K^T, kept on chip; per row of its 256-key
 //                 tile t the epilogue writes E = exp(S - m_t) (fp16, in
 //                 (0, 1]) and the tile's max m_t and sum l_t of E
-//   k_rowscale    per row: m = max_t m_t, l = sum_t l_t exp(m_t - m), and
-//                 g_t = exp(m_t - m) / l
-//   k_gemm  (NN)  O = P V with P = E g_t, applied to each A chunk on its
-//                 way to LDS (bf16 P, bf16 O)
+//   k_gemm  (NN)  O = P V with P = E g_t, the factors of each row
+//                 m = max_t m_t, l = sum_t l_t exp(m_t - m),
+//                 g_t = exp(m_t - m) / l computed by each workgroup for its
+//                 rows (k_rowscale does it beforehand for rows of more than
+//                 8 key tiles) and applied to each A chunk on its way to LDS
+//                 (bf16 P, bf16 O)
 //
 // so the row softmax is exact (max, exp, sum, divide as in the reference,
 // final/attention.cu:262-270) without an S round trip through HBM; every
@@ -589,10 +591,32 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm(GemmArgs g) {
         using T = std::integral_constant<bool, true>;
         using F = std::integral_constant<bool, false>;
         if constexpr (FAC_LDS) {
-            // this tile's rows' factors: [row][tile], kFacTiles >= gt
-            for (int e = tid; e < kBM * kFacTiles; e += kGemmThreads) {
-                const int r = e / kFacTiles, t = e - r * kFacTiles;
-                fac[e] = (m0 + r < g.M && t < g.gt) ? ga[(long)(m0 + r) * g.gt + t] : 0.f;
+            // the workgroup's rows' softmax factors ([row][tile], kFacTiles >=
+            // gt), from the QK^T epilogue's per-(row, 256-key tile) max m_t
+            // and sum l_t, with k_rowscale's arithmetic: m = max_t m_t,
+            // l = sum_t l_t exp(m_t - m), g_t = exp(m_t - m) / l (0 for a row
+            // with no valid key)
+            if (tid < kBM) {
+                const int row = m0 + tid;
+                const long base = ((long)bh * g.M + row) * g.gt;
+                float mt[kFacTiles], lt[kFacTiles];
+                float m = -INFINITY;
+#pragma unroll
+                for (int t = 0; t < kFacTiles; ++t) {
+                    const bool on = row < g.M && t < g.gt;
+                    mt[t] = on ? g.st_m[base + t] : -INFINITY;
+                    lt[t] = on ? g.st_l[base + t] : 0.f;
+                    m = fmaxf(m, mt[t]);
+                }
+                float l = 0.f;
+#pragma unroll
+                for (int t = 0; t < kFacTiles; ++t)
+                    if (t < g.gt) l += lt[t] * __expf(mt[t] - m);
+                const float inv = 1.0f / l;
+#pragma unroll
+                for (int t = 0; t < kFacTiles; ++t)
+                    fac[tid * kFacTiles + t] =
+                        (m == -INFINITY || t >= g.gt) ? 0.f : __expf(mt[t] - m) * inv;
             }
         }
         load_stage(st, 0, edge);
@@ -1513,21 +1537,26 @@ hipError_t launch_encode_f16(int pek, const uint16_t* in, uint16_t* out, float* 
     return hipGetLastError();
 }
 
-hipError_t launch_rowscale(const float* st_m, const float* st_l, float* ga, long rows, int T,
-                           hipStream_t st) {
-    hipLaunchKernelGGL(k_rowscale, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, st, st_m,
-                       st_l, ga, rows, T);
-    return hipGetLastError();
-}
-
-hipError_t launch_gemm_pv(const uint16_t* E, const float* ga, const uint16_t* V, uint16_t* O,
-                          int BH, int Lq, int Lk, int D, hipStream_t st) {
+hipError_t launch_gemm_pv(const uint16_t* E, float* st_m, float* st_l, float* ga,
+                          const uint16_t* V, uint16_t* O, int BH, int Lq, int Lk, int D,
+                          hipStream_t st) {
     GemmArgs g{};
     g.A = E;
     g.B = V;
     g.C = O;
+    g.st_m = st_m;
+    g.st_l = st_l;
     g.ga = ga;
     g.gt = (Lk + kBN - 1) / kBN;
+    // rows with at most kFacTiles key tiles: the PV workgroups turn the tile
+    // statistics into softmax factors themselves; longer rows take them,
+    // per chunk, from k_rowscale's output
+    if (g.gt > kFacTiles) {
+        hipLaunchKernelGGL(k_rowscale, dim3((unsigned)(((long)BH * Lq + 255) / 256)), dim3(256), 0,
+                           st, st_m, st_l, ga, (long)BH * Lq, g.gt);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
     g.M = Lq;
     g.N = D;
     g.K = Lk;

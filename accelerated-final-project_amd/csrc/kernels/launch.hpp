@@ -49,10 +49,11 @@ hipError_t launch_gemm_qk_enc(int benc, const uint16_t* Qe, const uint16_t* K, c
                               const uint16_t* tab, int tab_rows, uint16_t* E, float* st_m,
                               float* st_l, int BH, int Lq, int Lk, int D, float scale,
                               hipStream_t st);
-hipError_t launch_rowscale(const float* st_m, const float* st_l, float* ga, long rows, int T,
-                           hipStream_t st);
-hipError_t launch_gemm_pv(const uint16_t* E, const float* ga, const uint16_t* V, uint16_t* O,
-                          int BH, int Lq, int Lk, int D, hipStream_t st);
+// O = P V from E and the QK^T epilogue's tile statistics (st_m, st_l); ga
+// holds the softmax factors of rows with more than 8 key tiles.
+hipError_t launch_gemm_pv(const uint16_t* E, float* st_m, float* st_l, float* ga,
+                          const uint16_t* V, uint16_t* O, int BH, int Lq, int Lk, int D,
+                          hipStream_t st);
 
 hipError_t launch_pe_apply(int dtype, int pek, const void* in, void* out, long n_rows,
                            int seq_len, int D, const PeSide& pe, int vec_ok, hipStream_t st);
