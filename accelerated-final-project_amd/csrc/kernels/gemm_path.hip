@@ -35,7 +35,9 @@
 // Both GEMMs use 256 x 256 output tiles per workgroup of 512 threads (8
 // waves, each 64 x 128 (NT) or 128 x 64 (NN) = 8 tiles of
 // v_mfma_f32_32x32x16_{f16,bf16}), a K step of 64 in double-buffered LDS
-// (144 KiB) fed from a register stage two steps ahead, a software-pipelined
+// (144 KiB) fed from a register stage two steps ahead (the QK^T GEMM with
+// an even number of steps loads both tiles straight into LDS instead:
+// k_gemm_qk_dma, k_gemm_qk_enc), a software-pipelined
 // step (fragment reads, LDS writes and global loads interleaved with the
 // MFMAs, one barrier per step), and an
 // XCD-aware tile order: consecutive tile indices run on the same XCD
@@ -1128,6 +1130,166 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm_qk_enc(GemmArgs g) {
     if (qk_enc_tile<BENC, false>(g, L)) qk_enc_scaled_tile<BENC>(g, L);
 }
 
+// ---------------------------------------------------------------------------
+// QK^T GEMM with both operands loaded straight into LDS (8 waves).
+//
+// The tiling, fragment order and exp epilogue of k_gemm's NT form, with the
+// Q and K tiles both in the swizzled, unpadded layout of k_gemm_qk_enc's Q
+// tile (chunk c of row r at c ^ key(r)), filled by buffer -> LDS loads: no
+// register stage and no LDS write instructions.  The loads of step kt + 2
+// go into stage kt % 2 right after step kt's barrier (every wave is then
+// past its last read of it) and are waited for at step kt + 1's barrier.
+template <bool F16>
+__global__ __launch_bounds__(kGemmThreads) void k_gemm_qk_dma(GemmArgs g) {
+    constexpr int kAElems = kBM * kBK;
+    __shared__ __align__(16) uint16_t a0s[kAElems];
+    __shared__ __align__(16) uint16_t a1s[kAElems];
+    __shared__ __align__(16) uint16_t b0s[kAElems];
+    __shared__ __align__(16) uint16_t b1s[kAElems];
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    auto As = [&](auto S) -> uint16_t* {
+        if constexpr (decltype(S)::value == 0) return a0s; else return a1s;
+    };
+    auto Bs = [&](auto S) -> uint16_t* {
+        if constexpr (decltype(S)::value == 0) return b0s; else return b1s;
+    };
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const long per_head = (long)g.tiles_m * g.tiles_n;
+    const long total = per_head * g.heads;
+    const long t = xcd_tile(blockIdx.x, total);
+    if (t >= total) return;
+    const int bh = __builtin_amdgcn_readfirstlane((int)(t / per_head));
+    const int rem = (int)(t - (long)bh * per_head);
+    const int tm = rem / g.tiles_n, tn = rem - tm * g.tiles_n;
+    const int m0 = __builtin_amdgcn_readfirstlane(tm * kBM);
+    const int n0 = __builtin_amdgcn_readfirstlane(tn * kBN);
+
+    const __amdgpu_buffer_rsrc_t ra = gemm_rsrc(g.A + bh * g.sa, (long)g.M * g.lda);
+    const __amdgpu_buffer_rsrc_t rb = gemm_rsrc(g.B + bh * g.sb, (long)g.N * g.ldb);
+    constexpr uint32_t kOut = 0xfffffff0u;  // an offset past every descriptor's range
+
+    // lane l of wave w, instruction u writes row 64 u + 8 w + l / 8 of a tile
+    // at physical chunk l % 8 = logical chunk (l % 8) ^ key(row)
+    const int dr = 8 * wave + (lane >> 3);
+    const int dc = (lane & 7) ^ (lane >> 3) ^ (wave & 1);
+    const uint32_t a_vo = 2u * ((uint32_t)dr * (uint32_t)g.lda + 8u * (uint32_t)dc);
+    const uint32_t b_vo = 2u * ((uint32_t)dr * (uint32_t)g.ldb + 8u * (uint32_t)dc);
+    auto dma = [&](auto S, int kt, auto edge) __attribute__((always_inline)) {
+        uint16_t* da = As(S);
+        uint16_t* db = Bs(S);
+        const int k0 = kt * kBK;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            uint32_t va = a_vo, vb = b_vo;
+            uint32_t sa = 2u * ((uint32_t)(m0 + 64 * u) * (uint32_t)g.lda + (uint32_t)k0);
+            uint32_t sb = 2u * ((uint32_t)(n0 + 64 * u) * (uint32_t)g.ldb + (uint32_t)k0);
+            if constexpr (decltype(edge)::value) {
+                const int col = k0 + 8 * dc;
+                va = ((m0 + 64 * u + dr < g.M) & (col < g.K)) ? va + sa : kOut;
+                vb = ((n0 + 64 * u + dr < g.N) & (col < g.K)) ? vb + sb : kOut;
+                sa = sb = 0;
+            }
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                ra, (__attribute__((address_space(3))) void*)(da + (64 * u + 8 * wave) * kBK), 16,
+                va, __builtin_amdgcn_readfirstlane(sa), 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rb, (__attribute__((address_space(3))) void*)(db + (64 * u + 8 * wave) * kBK), 16,
+                vb, __builtin_amdgcn_readfirstlane(sb), 0, 0);
+        }
+    };
+
+    constexpr int TI = 2, TJ = 4;  // waves 4 x 2 of 64 x 128
+    const int wm = (wave >> 1) * 64, wn = (wave & 1) * 128;
+    v16f acc[TI][TJ];
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int j = 0; j < TJ; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+    struct Frag {
+        uint4 a[TI], b[TJ];
+    };
+    const int lrow = lane & 31;
+    const int akey = ((lrow & 7) ^ ((lrow >> 3) & 1)) ^ (lane >> 5);
+    const int a_row = (wm + lrow) * kBK, b_row = (wn + lrow) * kBK;
+    auto read_frag = [&](Frag& f, auto S, int q) __attribute__((always_inline)) {
+        const uint16_t* a = As(S);
+        const uint16_t* b = Bs(S);
+        const int co = ((2 * q) ^ akey) << 3;
+#pragma unroll
+        for (int i = 0; i < TI; ++i)
+            f.a[i] = *reinterpret_cast<const uint4*>(&a[a_row + co + i * 32 * kBK]);
+#pragma unroll
+        for (int j = 0; j < TJ; ++j)
+            f.b[j] = *reinterpret_cast<const uint4*>(&b[b_row + co + j * 32 * kBK]);
+    };
+    auto mma = [&](const Frag& f) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < TI; ++i)
+#pragma unroll
+            for (int j = 0; j < TJ; ++j) acc[i][j] = mfma_32x32x16<F16>(f.a[i], f.b[j], acc[i][j]);
+    };
+
+    const int nk = (g.K + kBK - 1) / kBK;
+    constexpr int kReads = TI + TJ;
+    Frag f0, f1;
+    auto step = [&](int kt, auto S, auto next, auto next2, auto edge) __attribute__((always_inline)) {
+        constexpr int s = decltype(S)::value;
+        using S1 = std::integral_constant<int, s ^ 1>;
+        constexpr bool N1 = decltype(next)::value, N2 = decltype(next2)::value;
+        read_frag(f1, S, 1);
+        mma(f0);
+        sched_mfma_reads<kReads>();
+        __builtin_amdgcn_sched_barrier(0);
+        read_frag(f0, S, 2);
+        mma(f1);
+        sched_mfma_reads<kReads>();
+        __builtin_amdgcn_sched_barrier(0);
+        read_frag(f1, S, 3);
+        mma(f0);
+        sched_mfma_reads<kReads>();
+        __builtin_amdgcn_sched_barrier(0);
+        // this wave's loads of step kt + 1 (issued one step earlier, in the
+        // previous loop iteration for every other step, where the compiler
+        // does not carry them to the barrier's wait) are complete; then the
+        // barrier makes every wave's complete
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+        __syncthreads();
+        if constexpr (N2) dma(S, kt + 2, edge);
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (N1) read_frag(f0, S1{}, 0);
+        mma(f1);
+        if constexpr (N1) sched_mfma_reads<kReads>();
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    auto kloop = [&](auto edge) __attribute__((always_inline)) {
+        using T = std::integral_constant<bool, true>;
+        using F = std::integral_constant<bool, false>;
+        dma(I0{}, 0, edge);
+        dma(I1{}, 1, edge);
+        __syncthreads();
+        read_frag(f0, I0{}, 0);
+        // nk is even (the host's condition for this kernel)
+        int kt = 0;
+        for (; kt + 2 < nk; kt += 2) {
+            step(kt, I0{}, T{}, T{}, edge);
+            step(kt + 1, I1{}, T{}, T{}, edge);
+        }
+        step(kt, I0{}, T{}, F{}, edge);
+        step(kt + 1, I1{}, F{}, F{}, edge);
+    };
+    if (m0 + kBM <= g.M && n0 + kBN <= g.N && g.K % kBK == 0)
+        kloop(std::integral_constant<bool, false>{});
+    else
+        kloop(std::integral_constant<bool, true>{});
+    nt_exp_epilogue<TI, TJ>(g, acc, reinterpret_cast<float*>(a0s), bh, m0, n0, tn, wm, wn, wave,
+                            lane);
+}
+
 // Encoded rows as fp16 with a power-of-two row scale: pass 1 finds the
 // largest magnitude m of the encoded row, pass 2 (re-reading the row, an L2
 // hit) writes fp16(x * 2^k) with m * 2^k in [2^14, 2^15) and stores
@@ -1404,6 +1566,17 @@ hipError_t launch_gemm_qk(int f16, const uint16_t* Q, const uint16_t* K, const f
     g.scale = scale;
     const long total = (long)g.tiles_m * g.tiles_n * BH;
     const long grid = (total + 7) / 8 * 8;
+    // an even number of 64-deep K steps: both operands straight into LDS
+    // (config 4's QK^T: 611 us against 635 us with the register stage)
+    if (D % 128 == 0) {
+        if (f16)
+            hipLaunchKernelGGL((k_gemm_qk_dma<true>), dim3((unsigned)grid), dim3(kGemmThreads), 0,
+                               st, g);
+        else
+            hipLaunchKernelGGL((k_gemm_qk_dma<false>), dim3((unsigned)grid), dim3(kGemmThreads), 0,
+                               st, g);
+        return hipGetLastError();
+    }
     if (f16)
         hipLaunchKernelGGL((k_gemm<true, false, kOutExpF16>), dim3((unsigned)grid),
                            dim3(kGemmThreads), 0, st, g);
