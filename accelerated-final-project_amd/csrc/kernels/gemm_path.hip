@@ -1290,6 +1290,253 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm_qk_dma(GemmArgs g) {
                             lane);
 }
 
+// ---------------------------------------------------------------------------
+// PV GEMM with V loaded straight into LDS (8 waves, rows of at most
+// kFacTiles key tiles, an even number of 64-key steps).
+//
+// O = P V as in k_gemm's NN form: the E chunks (fp16) go through the register
+// stage and are scaled by their row's softmax factor into bf16 P on their
+// way to LDS (factors computed by the workgroup into an LDS table), while the
+// V tile ([64 keys][256 columns], the transposing-read layout of nn_lds_off)
+// is filled by buffer -> LDS loads.  Wave instruction u of wave w writes key
+// rows 2 (w + 8u) and + 1 (1 KiB); lane l takes row + l / 32, physical
+// 16-byte slot l % 32 of that row, i.e. logical columns 16 ((l % 32) / 2 ^
+// swz(row)) + 8 (l % 2).  V's loads of step kt + 2 go into stage kt % 2
+// right after step kt's barrier and are waited for at step kt + 1's barrier.
+__global__ __launch_bounds__(kGemmThreads) void k_gemm_pv_dma(GemmArgs g) {
+    constexpr int kBElems = kBK * kBN;
+    __shared__ __align__(16) uint16_t a0s[kTileElems];
+    __shared__ __align__(16) uint16_t a1s[kTileElems];
+    __shared__ __align__(16) uint16_t b0s[kBElems];
+    __shared__ __align__(16) uint16_t b1s[kBElems];
+    __shared__ float fac[kBM * kFacTiles];
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    auto As = [&](auto S) -> uint16_t* {
+        if constexpr (decltype(S)::value == 0) return a0s; else return a1s;
+    };
+    auto Bs = [&](auto S) -> uint16_t* {
+        if constexpr (decltype(S)::value == 0) return b0s; else return b1s;
+    };
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const long per_head = (long)g.tiles_m * g.tiles_n;
+    const long total = per_head * g.heads;
+    const long t = xcd_tile(blockIdx.x, total);
+    if (t >= total) return;
+    const int bh = __builtin_amdgcn_readfirstlane((int)(t / per_head));
+    const int rem = (int)(t - (long)bh * per_head);
+    // row panels fastest: the few workgroups of one V panel run together
+    const int tn = rem / g.tiles_m, tm = rem - tn * g.tiles_m;
+    const int m0 = __builtin_amdgcn_readfirstlane(tm * kBM);
+    const int n0 = __builtin_amdgcn_readfirstlane(tn * kBN);
+
+    const __amdgpu_buffer_rsrc_t ra = gemm_rsrc(g.A + bh * g.sa, (long)g.M * g.lda);
+    const __amdgpu_buffer_rsrc_t rb = gemm_rsrc(g.B + bh * g.sb, (long)g.K * g.ldb);
+    constexpr uint32_t kOut = 0xfffffff0u;  // an offset past every descriptor's range
+
+    // ---- E chunks: thread's chunk u is row tid / 8 + 64 u, keys 8 (tid % 8) ..
+    constexpr int kChunks = 4;
+    const int er = tid / kChunkPerRow, ek = (tid % kChunkPerRow) * 8;
+    const uint32_t a_vo = 2u * ((uint32_t)er * (uint32_t)g.lda + (uint32_t)ek);
+    struct Stage {
+        uint4 a[kChunks];
+    };
+    auto load_a = [&](Stage& r, int kt, auto edge) __attribute__((always_inline)) {
+        const int k0 = kt * kBK;
+#pragma unroll
+        for (int u = 0; u < kChunks; ++u) {
+            uint32_t vo = a_vo;
+            uint32_t so = 2u * ((uint32_t)(m0 + 64 * u) * (uint32_t)g.lda + (uint32_t)k0);
+            if constexpr (decltype(edge)::value) {
+                vo = (m0 + 64 * u + er < g.M) ? vo + so : kOut;
+                so = 0;
+            }
+            r.a[u] = buf_ld16(ra, vo, so);
+        }
+    };
+    auto store_a = [&](auto S, const Stage& r, int kt) __attribute__((always_inline)) {
+        uint16_t* dst = As(S);
+        const int ft = (kt * kBK + ek) >> 8;  // the chunk's 256-key tile
+#pragma unroll
+        for (int u = 0; u < kChunks; ++u) {
+            const int row = er + 64 * u;
+            *reinterpret_cast<uint4*>(&dst[row * kLdsRow + ek]) =
+                scale_f16x8_to_bf16(r.a[u], fac[row * kFacTiles + ft]);
+        }
+    };
+
+    // ---- V: DMA into [64 keys][256 columns]
+    const int vrow = lane >> 5;  // + 2 (w + 8u)
+    const int vswz = (0x7520 >> (4 * ((2 * (wave & 1) + vrow) & 3))) & 0xf;  // {0,2,5,7}[row % 4]
+    const int vcol = ((((lane & 31) >> 1) ^ vswz) << 4) + 8 * (lane & 1);
+    const uint32_t b_vo = 2u * ((uint32_t)vrow * (uint32_t)g.ldb + (uint32_t)vcol);
+    auto dma_b = [&](auto S, int kt, auto edge) __attribute__((always_inline)) {
+        uint16_t* dst = Bs(S);
+        const int k0 = kt * kBK;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int r0 = 2 * (wave + 8 * u);
+            uint32_t vo = b_vo;
+            uint32_t so = 2u * ((uint32_t)(k0 + r0) * (uint32_t)g.ldb + (uint32_t)n0);
+            if constexpr (decltype(edge)::value) {
+                vo = (n0 + vcol < g.N) ? vo + so : kOut;
+                so = 0;
+            }
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rb, (__attribute__((address_space(3))) void*)(dst + r0 * kBN), 16, vo,
+                __builtin_amdgcn_readfirstlane(so), 0, 0);
+        }
+    };
+
+    // ---- wave tile 128 x 64 (waves 2 x 4): 4 x 2 MFMA tiles, transposed
+    // product (acc rows are output columns)
+    constexpr int TI = 4, TJ = 2;
+    const int wm = (wave >> 2) * 128, wn = (wave & 3) * 64;
+    v16f acc[TI][TJ];
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int j = 0; j < TJ; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+    struct Frag {
+        uint4 a[TI], b[TJ];
+    };
+    const int lrow = lane & 31, lkh = (lane >> 5) * 8;
+    auto read_frag = [&](Frag& f, auto S, int q) __attribute__((always_inline)) {
+        const uint16_t* a = As(S);
+        const uint16_t* b = Bs(S);
+        const int ks = 16 * q;
+#pragma unroll
+        for (int i = 0; i < TI; ++i)
+            f.a[i] = *reinterpret_cast<const uint4*>(&a[(wm + i * 32 + lrow) * kLdsRow + ks + lkh]);
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) {
+            const int kr = ks + 8 * (lane >> 5) + ((lane & 15) >> 2);
+            const int nc = wn + j * 32 + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+            const v4i16 lo = ds_read_tr16(&b[nn_lds_off(kr, nc)]);
+            const v4i16 hi = ds_read_tr16(&b[nn_lds_off(kr + 4, nc)]);
+            const uint2 l2 = __builtin_bit_cast(uint2, lo), h2 = __builtin_bit_cast(uint2, hi);
+            f.b[j] = make_uint4(l2.x, l2.y, h2.x, h2.y);
+        }
+    };
+    auto mma = [&](const Frag& f) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < TI; ++i)
+#pragma unroll
+            for (int j = 0; j < TJ; ++j) acc[i][j] = mfma_32x32x16<false>(f.b[j], f.a[i], acc[i][j]);
+    };
+
+    const int nk = (g.K + kBK - 1) / kBK;
+    constexpr int kReads = TI + 2 * TJ;
+    Stage st;
+    Frag f0, f1;
+    auto step = [&](int kt, auto S, auto next, auto next2, auto edge) __attribute__((always_inline)) {
+        constexpr int s = decltype(S)::value;
+        using S1 = std::integral_constant<int, s ^ 1>;
+        constexpr bool N1 = decltype(next)::value, N2 = decltype(next2)::value;
+        read_frag(f1, S, 1);
+        mma(f0);
+        if constexpr (N1) store_a(S1{}, st, kt + 1);
+        sched_mfma_reads<kReads>();
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (N2) load_a(st, kt + 2, edge);
+        read_frag(f0, S, 2);
+        mma(f1);
+        sched_mfma_reads<kReads>();
+        __builtin_amdgcn_sched_barrier(0);
+        read_frag(f1, S, 3);
+        mma(f0);
+        sched_mfma_reads<kReads>();
+        __builtin_amdgcn_sched_barrier(0);
+        // V of step kt + 1 (issued after the previous step's barrier, before
+        // this step's E loads) is in; then the barrier makes every wave's so
+        if constexpr (N2)
+            __builtin_amdgcn_s_waitcnt(0x0F74);  // vmcnt(4): this step's E loads may fly
+        else
+            __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+        __syncthreads();
+        if constexpr (N2) dma_b(S, kt + 2, edge);
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (N1) read_frag(f0, S1{}, 0);
+        mma(f1);
+        if constexpr (N1) sched_mfma_reads<kReads>();
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    auto kloop = [&](auto edge) __attribute__((always_inline)) {
+        using T = std::integral_constant<bool, true>;
+        using F = std::integral_constant<bool, false>;
+        // the workgroup's rows' softmax factors (as in k_gemm's NN form)
+        if (tid < kBM) {
+            const int row = m0 + tid;
+            const long base = ((long)bh * g.M + row) * g.gt;
+            float mt[kFacTiles], lt[kFacTiles];
+            float m = -INFINITY;
+#pragma unroll
+            for (int t2 = 0; t2 < kFacTiles; ++t2) {
+                const bool on = row < g.M && t2 < g.gt;
+                mt[t2] = on ? g.st_m[base + t2] : -INFINITY;
+                lt[t2] = on ? g.st_l[base + t2] : 0.f;
+                m = fmaxf(m, mt[t2]);
+            }
+            float l = 0.f;
+#pragma unroll
+            for (int t2 = 0; t2 < kFacTiles; ++t2)
+                if (t2 < g.gt) l += lt[t2] * __expf(mt[t2] - m);
+            const float inv = 1.0f / l;
+#pragma unroll
+            for (int t2 = 0; t2 < kFacTiles; ++t2)
+                fac[tid * kFacTiles + t2] =
+                    (m == -INFINITY || t2 >= g.gt) ? 0.f : __expf(mt[t2] - m) * inv;
+        }
+        dma_b(I0{}, 0, edge);
+        dma_b(I1{}, 1, edge);
+        load_a(st, 0, edge);
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+        __syncthreads();  // the factor table, V of steps 0 and 1
+        store_a(I0{}, st, 0);
+        load_a(st, 1, edge);
+        __syncthreads();
+        read_frag(f0, I0{}, 0);
+        // nk is even (the host's condition for this kernel)
+        int kt = 0;
+        for (; kt + 2 < nk; kt += 2) {
+            step(kt, I0{}, T{}, T{}, edge);
+            step(kt + 1, I1{}, T{}, T{}, edge);
+        }
+        step(kt, I0{}, T{}, F{}, edge);
+        step(kt + 1, I1{}, F{}, F{}, edge);
+    };
+    if (m0 + kBM <= g.M && n0 + kBN <= g.N)
+        kloop(std::integral_constant<bool, false>{});
+    else
+        kloop(std::integral_constant<bool, true>{});
+
+    // lane: output row m0 + wm + 32 i + lane % 32, columns n0 + wn + 32 j +
+    // 8 (r / 4) + 4 (lane / 32) + r % 4: four consecutive bf16 per group of r
+    uint16_t* C = static_cast<uint16_t*>(g.C) + bh * g.sc;
+#pragma unroll
+    for (int i = 0; i < TI; ++i) {
+        const int row = m0 + wm + i * 32 + (lane & 31);
+        if (row >= g.M) continue;
+#pragma unroll
+        for (int j = 0; j < TJ; ++j)
+#pragma unroll
+            for (int rg = 0; rg < 4; ++rg) {
+                const int col = n0 + wn + j * 32 + 8 * rg + 4 * (lane >> 5);
+                if (col >= g.N) continue;
+                uint2 w;
+                w.x = (uint32_t)f32_to_bf16_bits(acc[i][j][4 * rg]) |
+                      ((uint32_t)f32_to_bf16_bits(acc[i][j][4 * rg + 1]) << 16);
+                w.y = (uint32_t)f32_to_bf16_bits(acc[i][j][4 * rg + 2]) |
+                      ((uint32_t)f32_to_bf16_bits(acc[i][j][4 * rg + 3]) << 16);
+                *reinterpret_cast<uint2*>(C + (long)row * g.ldc + col) = w;
+            }
+    }
+}
+
 // Encoded rows as fp16 with a power-of-two row scale: pass 1 finds the
 // largest magnitude m of the encoded row, pass 2 (re-reading the row, an L2
 // hit) writes fp16(x * 2^k) with m * 2^k in [2^14, 2^15) and stores
@@ -1745,7 +1992,10 @@ hipError_t launch_gemm_pv(const uint16_t* E, float* st_m, float* st_l, float* ga
     g.scale = 1.f;
     const long total = (long)g.tiles_m * g.tiles_n * BH;
     const long grid = (total + 7) / 8 * 8;
-    if (g.gt <= kFacTiles)
+    // an even number of 64-key steps: V straight into LDS
+    if (g.gt <= kFacTiles && Lk % 128 == 0)
+        hipLaunchKernelGGL(k_gemm_pv_dma, dim3((unsigned)grid), dim3(kGemmThreads), 0, st, g);
+    else if (g.gt <= kFacTiles)
         hipLaunchKernelGGL((k_gemm<false, true, kOutBf16, true>), dim3((unsigned)grid),
                            dim3(kGemmThreads), 0, st, g);
     else
