@@ -125,3 +125,47 @@ def test_gemm_path_wide_score_range(am, dev, pe, sigma):
     hip_rt.synchronize()
     n, nrel, mabs = H.check_bf16(out.numpy(), _ref(pe, Q, K, V, Lq, Lk, D))
     assert n == 0, f"normwise rel {nrel}, max abs {mabs}"
+
+
+@pytest.mark.parametrize("shape,pe", [((1, 2, 256, 512, 256), "sinusoidal"),
+                                      ((1, 1, 1024, 256, 128), "rope_half"),
+                                      ((1, 2, 256, 384, 136), "none")],
+                         ids=["fusedK", "qkdma-encK", "register-stage"])
+def test_gemm_graph_replays_match_eager(am, dev, shape, pe):
+    """Captured HIP graph of three calls on one workspace, replayed four times
+    with eager work and synchronizations in between: every replay equals the
+    eager result bit for bit.  The shapes take the K encoding inside the
+    QK^T GEMM, the K~ pass with the both-tiles-in-LDS QK^T GEMM, and the
+    register-staged GEMMs."""
+    import hip_rt
+    B, Hh, Lq, Lk, D = shape
+    print(f"[case] gemm graph replay {shape} {pe}", flush=True)
+    desc = _desc(am, pe)
+    assert am.path(1, B, Hh, Lq, Lk, D, desc) == am.ATN_PATH_GEMM
+    (q, k, v), (Q, K, V) = H.device_inputs((B, Hh, Lq, D), (B, Hh, Lk, D), 77, "bf16",
+                                           0.5 if pe == "sinusoidal" else 1.0)
+    nb = am.workspace_bytes(am.ATN_DTYPE_BF16, B, Hh, Lq, Lk, D, desc)
+    ws = hip_rt.DeviceArray.from_numpy(np.zeros(nb // 4 + 1, np.float32), "f32")
+    st = hip_rt.Stream()
+    eager = H.empty(Q.shape, "bf16")
+    am.attention_ex(q, k, v, eager, pe=desc, workspace=ws, stream=st)
+    st.synchronize()
+    ref = eager.bits()
+    outs = [H.empty(Q.shape, "bf16") for _ in range(3)]
+    g = hip_rt.Graph(st, lambda: [am.attention_ex(q, k, v, o, pe=desc, workspace=ws, stream=st)
+                                  for o in outs])
+    for rep in range(4):
+        for o in outs:
+            o.fill_nan()
+        hip_rt.synchronize()
+        g.launch()
+        st.synchronize()
+        for o in outs:
+            assert np.array_equal(o.bits(), ref), f"replay {rep} differs from eager"
+        am.attention_ex(q, k, v, eager, pe=desc, workspace=ws, stream=st)
+        st.synchronize()
+        assert np.array_equal(eager.bits(), ref)
+    g.destroy()
+    st.destroy()
+    n, nrel, mabs = H.check_bf16(eager.numpy(), _ref(pe, Q, K, V, Lq, Lk, D))
+    assert n == 0, f"normwise rel {nrel}, max abs {mabs}"

@@ -137,3 +137,17 @@ def test_fused_k_range_scaled_pass(am, dev, mode):
     got = _run(am, q, k, v, Q.shape, desc, True)
     n, nrel, mabs = H.check_bf16(got, _ref(mode, Q, K, V))
     assert n == 0, f"ordinary keys: normwise rel {nrel}, max abs {mabs}"
+
+
+@pytest.mark.parametrize("mode", ["sinusoidal", "rope_half"])
+def test_fused_k_batch_and_heads(am, dev, mode):
+    """B = 2 and H = 2 (head strides of Q~, K, the table rows shared by every
+    head) through the fused form."""
+    B, Hh, Lq, Lk, D = 2, 2, 256, 512, 256
+    print(f"[case] fused K batch x heads {mode}", flush=True)
+    desc = am.make_pe(**MODES[mode])
+    sigma = 0.5 if MODES[mode]["kind"] == "sinusoidal" else 1.0
+    (q, k, v), (Q, K, V) = H.device_inputs((B, Hh, Lq, D), (B, Hh, Lk, D), 55, "bf16", sigma)
+    got = _run(am, q, k, v, Q.shape, desc, True)
+    n, nrel, mabs = H.check_bf16(got, _ref(mode, Q, K, V))
+    assert n == 0, f"normwise rel {nrel}, max abs {mabs}"
