@@ -215,31 +215,46 @@ struct GemmArgs {
 // this 256-key tile; per row its maximum m_t over the tile's valid columns
 // and the sum l_t of E = exp(S - m_t).  A row's 256 columns are 32 lanes x
 // TJ tiles in each of the two column waves (wave % 2), combined through LDS
-// (red: 4 x 256 floats, free once every wave is done with the K loop).
-// Lane layout of acc[i][j]: column (lane % 32) and rows 8 (r / 4) +
-// 4 (lane / 32) + r % 4 of each 32 x 32 tile.
+// (red: 6 x 256 floats, free once every wave is done with the K loop: the
+// row maxima and sums of both column waves, then the tile's row and column
+// scales).  Lane layout of acc[i][j]: column (lane % 32) and rows
+// 8 (r / 4) + 4 (lane / 32) + r % 4 of each 32 x 32 tile.
 // cs_lds (optional) replaces g.cs: the tile's 256 column scales in LDS.
 template <int TI, int TJ>
 __device__ __forceinline__ void nt_exp_epilogue(const GemmArgs& g, v16f (&acc)[TI][TJ],
                                                 float* red, int bh, int m0, int n0, int tn,
                                                 int wm, int wn, int wave, int lane,
                                                 const float* cs_lds = nullptr) {
+    static_assert(kGemmThreads == kBM + kBN, "one scale per thread");
+    // Each thread fetches one of the tile's 256 row or 256 column scales
+    // before the barrier (its latency overlaps the wait) and puts it in LDS:
+    // per element, each a load from memory behind a branch, they were
+    // waited for one at a time.
+    const int tid = wave * 64 + lane;
+    float sv;
+    if (tid < kBM) {
+        const int row = m0 + tid;
+        sv = (g.rs && row < g.M) ? g.rs[(long)bh * g.M + row] : 1.f;
+    } else {
+        const int col = n0 + tid - kBM;
+        sv = col < g.N ? (cs_lds ? cs_lds[col - n0] : (g.cs ? g.cs[(long)bh * g.N + col] : 1.f))
+                       : 0.f;
+    }
     __syncthreads();  // every wave is done with the LDS stages
+    red[4 * kBM + tid] = sv;
+    __syncthreads();
+    const float* rsl = red + 4 * kBM;
+    const float* csl = red + 5 * kBM;
     const int half = lane >> 5, lc = lane & 31, cw = wave & 1;
 #pragma unroll
     for (int j = 0; j < TJ; ++j) {
         const int col = n0 + wn + j * 32 + lc;
-        const float csc =
-            col < g.N ? (cs_lds ? cs_lds[col - n0] * g.scale
-                                : (g.cs ? g.cs[(long)bh * g.N + col] * g.scale : g.scale))
-                      : 0.f;
+        const float csc = csl[wn + j * 32 + lc] * g.scale;
 #pragma unroll
         for (int i = 0; i < TI; ++i)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const int row = m0 + wm + i * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
-                float v = acc[i][j][r] * csc;
-                if (g.rs && row < g.M) v *= g.rs[(long)bh * g.M + row];
+                const float v = acc[i][j][r] * csc * rsl[wm + i * 32 + 8 * (r >> 2) + 4 * half + (r & 3)];
                 acc[i][j][r] = col < g.N ? v : -INFINITY;
             }
     }
