@@ -220,25 +220,31 @@ struct GemmArgs {
 // scales).  Lane layout of acc[i][j]: column (lane % 32) and rows
 // 8 (r / 4) + 4 (lane / 32) + r % 4 of each 32 x 32 tile.
 // cs_lds (optional) replaces g.cs: the tile's 256 column scales in LDS.
+//
+// The row factor f = scale * (row scale) is positive, so with
+// u = acc * (column scale) the row maximum of S is (max u) * f, and
+// E = exp(u f - (max u) f) = exp2(u f log2(e) - (max u) f log2(e)): one fma
+// and one exp2 per element.
 template <int TI, int TJ>
 __device__ __forceinline__ void nt_exp_epilogue(const GemmArgs& g, v16f (&acc)[TI][TJ],
                                                 float* red, int bh, int m0, int n0, int tn,
                                                 int wm, int wn, int wave, int lane,
                                                 const float* cs_lds = nullptr) {
     static_assert(kGemmThreads == kBM + kBN, "one scale per thread");
+    constexpr float kLog2e = 1.4426950408889634f;
     // Each thread fetches one of the tile's 256 row or 256 column scales
     // before the barrier (its latency overlaps the wait) and puts it in LDS:
     // per element, each a load from memory behind a branch, they were
     // waited for one at a time.
     const int tid = wave * 64 + lane;
-    float sv;
+    const bool col_scales = cs_lds != nullptr || g.cs != nullptr;
+    float sv = 1.f;
     if (tid < kBM) {
         const int row = m0 + tid;
-        sv = (g.rs && row < g.M) ? g.rs[(long)bh * g.M + row] : 1.f;
+        if (g.rs && row < g.M) sv = g.rs[(long)bh * g.M + row];
     } else {
         const int col = n0 + tid - kBM;
-        sv = col < g.N ? (cs_lds ? cs_lds[col - n0] : (g.cs ? g.cs[(long)bh * g.N + col] : 1.f))
-                       : 0.f;
+        if (col_scales && col < g.N) sv = cs_lds ? cs_lds[col - n0] : g.cs[(long)bh * g.N + col];
     }
     __syncthreads();  // every wave is done with the LDS stages
     red[4 * kBM + tid] = sv;
@@ -246,17 +252,19 @@ __device__ __forceinline__ void nt_exp_epilogue(const GemmArgs& g, v16f (&acc)[T
     const float* rsl = red + 4 * kBM;
     const float* csl = red + 5 * kBM;
     const int half = lane >> 5, lc = lane & 31, cw = wave & 1;
+    const bool interior = m0 + kBM <= g.M && n0 + kBN <= g.N;
+    // u = acc * (column scale); columns past N are -inf
+    if (col_scales || !interior) {
 #pragma unroll
-    for (int j = 0; j < TJ; ++j) {
-        const int col = n0 + wn + j * 32 + lc;
-        const float csc = csl[wn + j * 32 + lc] * g.scale;
+        for (int j = 0; j < TJ; ++j) {
+            const int cl = wn + j * 32 + lc;
+            const bool ok = n0 + cl < g.N;
+            const float c = csl[cl];
 #pragma unroll
-        for (int i = 0; i < TI; ++i)
+            for (int i = 0; i < TI; ++i)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const float v = acc[i][j][r] * csc * rsl[wm + i * 32 + 8 * (r >> 2) + 4 * half + (r & 3)];
-                acc[i][j][r] = col < g.N ? v : -INFINITY;
-            }
+                for (int r = 0; r < 16; ++r) acc[i][j][r] = ok ? acc[i][j][r] * c : -INFINITY;
+        }
     }
     float rm[TI][16], rl[TI][16];
 #pragma unroll
@@ -279,13 +287,14 @@ __device__ __forceinline__ void nt_exp_epilogue(const GemmArgs& g, v16f (&acc)[T
     for (int i = 0; i < TI; ++i)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-            const float m = fmaxf(rm[i][r], red[(cw ^ 1) * kBM + rloc(i, r)]);
-            rm[i][r] = m;
+            const float mu = fmaxf(rm[i][r], red[(cw ^ 1) * kBM + rloc(i, r)]);
+            const float gl = g.scale * rsl[rloc(i, r)] * kLog2e;
+            // a row with no valid column keeps max u = -inf: its E are 0
+            const float nb = mu == -INFINITY ? 0.f : -(mu * gl);
             float l = 0.f;
 #pragma unroll
             for (int j = 0; j < TJ; ++j) {
-                // a row with no valid column keeps m = -inf: its E are 0
-                const float e = m == -INFINITY ? 0.f : __expf(acc[i][j][r] - m);
+                const float e = __builtin_amdgcn_exp2f(fmaf(acc[i][j][r], gl, nb));
                 acc[i][j][r] = e;
                 l += e;
             }
@@ -297,18 +306,35 @@ __device__ __forceinline__ void nt_exp_epilogue(const GemmArgs& g, v16f (&acc)[T
 #pragma unroll
             for (int r = 0; r < 16; ++r) red[(2 + cw) * kBM + rloc(i, r)] = rl[i][r];
     __syncthreads();
-    if (cw == 0 && lc == 0)
+    // statistics, one row per thread: m_t = (max u) f, l_t
+    if (tid < kBM && m0 + tid < g.M) {
+        const float mu = fmaxf(red[tid], red[kBM + tid]);
+        const long si = ((long)bh * g.M + m0 + tid) * g.tiles_n + tn;
+        g.st_m[si] = mu * (g.scale * rsl[tid]);
+        g.st_l[si] = red[2 * kBM + tid] + red[3 * kBM + tid];
+    }
+    uint16_t* C = static_cast<uint16_t*>(g.C) + bh * g.sc;
+    if (interior) {
+        // buffer stores: the lane's (i, j) offset in a register, the row
+        // offset of r in a scalar register
+        const __amdgpu_buffer_rsrc_t rc = gemm_rsrc(C, (long)g.M * g.ldc);
+        const uint32_t ldc = (uint32_t)g.ldc;
 #pragma unroll
         for (int i = 0; i < TI; ++i)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int row = m0 + rloc(i, r);
-                if (row >= g.M) continue;
-                const long si = ((long)bh * g.M + row) * g.tiles_n + tn;
-                g.st_m[si] = rm[i][r];
-                g.st_l[si] = rl[i][r] + red[3 * kBM + rloc(i, r)];
+            for (int j = 0; j < TJ; ++j) {
+                const uint32_t vo =
+                    2u * ((uint32_t)(m0 + wm + i * 32 + 4 * half) * ldc + (uint32_t)(n0 + wn + j * 32 + lc));
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const uint32_t so = 2u * (uint32_t)(8 * (r >> 2) + (r & 3)) * ldc;
+                    __builtin_amdgcn_raw_buffer_store_b16(
+                        __builtin_bit_cast(uint16_t, (_Float16)acc[i][j][r]), rc, (int)vo,
+                        (int)__builtin_amdgcn_readfirstlane(so), 0);
+                }
             }
-    uint16_t* C = static_cast<uint16_t*>(g.C) + bh * g.sc;
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < TI; ++i)
 #pragma unroll
@@ -1483,6 +1509,11 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm_pv_dma(GemmArgs g) {
     auto kloop = [&](auto edge) __attribute__((always_inline)) {
         using T = std::integral_constant<bool, true>;
         using F = std::integral_constant<bool, false>;
+        // V of steps 0 and 1 and E of step 0 are issued first, so that the
+        // statistics' loads below share one memory round trip with them
+        dma_b(I0{}, 0, edge);
+        dma_b(I1{}, 1, edge);
+        load_a(st, 0, edge);
         // the workgroup's rows' softmax factors (as in k_gemm's NN form)
         if (tid < kBM) {
             const int row = m0 + tid;
@@ -1506,9 +1537,6 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm_pv_dma(GemmArgs g) {
                 fac[tid * kFacTiles + t2] =
                     (m == -INFINITY || t2 >= g.gt) ? 0.f : __expf(mt[t2] - m) * inv;
         }
-        dma_b(I0{}, 0, edge);
-        dma_b(I1{}, 1, edge);
-        load_a(st, 0, edge);
         __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
         __syncthreads();  // the factor table, V of steps 0 and 1
         store_a(I0{}, st, 0);
