@@ -172,20 +172,36 @@ __device__ __forceinline__ uint4 scale_f16x8_to_bf16(const uint4& w, float f) {
     return make_uint4(y[0], y[1], y[2], y[3]);
 }
 
+// Lane permutations by DPP with bound_ctrl set: the controls used here read
+// in-range lanes only, so no old value is needed (and the compiler keeps no
+// zeroed destination for it).
+template <int Ctrl>
+__device__ __forceinline__ float dppb(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), Ctrl, 0xF, 0xF, true));
+}
+// max of two floats as one v_max_f32: fmaxf's IEEE semantics make the
+// compiler canonicalize both operands first (two more instructions); the
+// values here are never signalling NaNs
+__device__ __forceinline__ float vmaxf(float a, float b) {
+    float d;
+    asm("v_max_f32 %0, %1, %2" : "=v"(d) : "v"(a), "v"(b));
+    return d;
+}
+
 // Max / sum over each half-wave (lanes with the same lane / 32): DPP within
 // quads, 8 and 16 lanes, then the 16-lane hop by ds_swizzle.
 __device__ __forceinline__ float half_max(float v) {
-    v = fmaxf(v, dpp<kDppQuadXor1>(v));
-    v = fmaxf(v, dpp<kDppQuadXor2>(v));
-    v = fmaxf(v, dpp<kDppRowHalfMirror>(v));
-    v = fmaxf(v, dpp<kDppRowMirror>(v));
-    return fmaxf(v, swz_xor16(v));
+    v = vmaxf(v, dppb<kDppQuadXor1>(v));
+    v = vmaxf(v, dppb<kDppQuadXor2>(v));
+    v = vmaxf(v, dppb<kDppRowHalfMirror>(v));
+    v = vmaxf(v, dppb<kDppRowMirror>(v));
+    return vmaxf(v, swz_xor16(v));
 }
 __device__ __forceinline__ float half_sum(float v) {
-    v += dpp<kDppQuadXor1>(v);
-    v += dpp<kDppQuadXor2>(v);
-    v += dpp<kDppRowHalfMirror>(v);
-    v += dpp<kDppRowMirror>(v);
+    v += dppb<kDppQuadXor1>(v);
+    v += dppb<kDppQuadXor2>(v);
+    v += dppb<kDppRowHalfMirror>(v);
+    v += dppb<kDppRowMirror>(v);
     return v + swz_xor16(v);
 }
 
@@ -273,7 +289,7 @@ __device__ __forceinline__ void nt_exp_epilogue(const GemmArgs& g, v16f (&acc)[T
         for (int r = 0; r < 16; ++r) {
             float m = acc[i][0][r];
 #pragma unroll
-            for (int j = 1; j < TJ; ++j) m = fmaxf(m, acc[i][j][r]);
+            for (int j = 1; j < TJ; ++j) m = vmaxf(m, acc[i][j][r]);
             rm[i][r] = half_max(m);
         }
     auto rloc = [&](int i, int r) { return wm + i * 32 + 8 * (r >> 2) + 4 * half + (r & 3); };
@@ -287,7 +303,7 @@ __device__ __forceinline__ void nt_exp_epilogue(const GemmArgs& g, v16f (&acc)[T
     for (int i = 0; i < TI; ++i)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-            const float mu = fmaxf(rm[i][r], red[(cw ^ 1) * kBM + rloc(i, r)]);
+            const float mu = vmaxf(rm[i][r], red[(cw ^ 1) * kBM + rloc(i, r)]);
             const float gl = g.scale * rsl[rloc(i, r)] * kLog2e;
             // a row with no valid column keeps max u = -inf: its E are 0
             const float nb = mu == -INFINITY ? 0.f : -(mu * gl);
@@ -1063,10 +1079,11 @@ __device__ __forceinline__ bool qk_enc_tile(const GemmArgs& g, const QkEncLds& L
             for (int j = 0; j < TJ; ++j) acc[i][j] = mfma_32x32x16<true>(f.a[i], f.b[j], acc[i][j]);
     };
 
-    // ---- K loop: the step of k_gemm (fragment reads one sub-step ahead, the
-    // next step's K tile written to LDS in sub-step 0 and its Q tile's DMA
-    // issued right after, the K loads of step kt + 2 in sub-step 1, one
-    // barrier before sub-step 3)
+    // ---- K loop: fragment reads one sub-step ahead; the next step's Q tile
+    // DMA issued in sub-step 0; the next step's K tile encoded and written to
+    // LDS in sub-step 2, and the K loads of step kt + 2 issued right after it
+    // into the freed register stage (a whole step before they are needed);
+    // one barrier before sub-step 3
     const int nk = (g.K + kBK - 1) / kBK;
     constexpr int kReads = TI + TJ;
     Stage st;
@@ -1078,19 +1095,20 @@ __device__ __forceinline__ bool qk_enc_tile(const GemmArgs& g, const QkEncLds& L
         constexpr bool N1 = decltype(next)::value, N2 = decltype(next2)::value;
         read_frag(f1, S, 1);
         mma(f0);
-        if constexpr (N1) store_b(S1{}, st, scaled);
         sched_mfma_reads<kReads>();
         __builtin_amdgcn_sched_barrier(0);
         if constexpr (N1) dma_a(S1{}, kt + 1, edge);
         __builtin_amdgcn_sched_barrier(0);
-        if constexpr (N2) load_b(st, kt + 2, edge);
         read_frag(f0, S, 2);
         mma(f1);
         sched_mfma_reads<kReads>();
         __builtin_amdgcn_sched_barrier(0);
         read_frag(f1, S, 3);
         mma(f0);
+        if constexpr (N1) store_b(S1{}, st, scaled);
         sched_mfma_reads<kReads>();
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (N2) load_b(st, kt + 2, edge);
         __builtin_amdgcn_sched_barrier(0);
         __syncthreads();
         if constexpr (N1) read_frag(f0, S1{}, 0);
