@@ -48,6 +48,9 @@
 // along K (= keys); V rows are contiguous along D, so the V tile is stored
 // in LDS as it lies in memory and the MFMA operand is gathered across keys
 // by gfx950's transposing LDS read (ds_read_b64_tr_b16).
+#include <algorithm>
+#include <atomic>
+
 #include "common.hpp"
 #include "launch.hpp"
 
@@ -151,6 +154,7 @@ constexpr int kOutBf16 = 1;       // C = bf16(acc), row stride ldc
 // fp32, with a zero addend: the rounding of the product itself), and each
 // pair is rounded to bf16 (nearest even) by gfx950's v_cvt_pk_bf16_f32.
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ float f16lo_mul(uint32_t x, float f) {
     float r;
     asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(x), "v"(f));
@@ -1362,6 +1366,7 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm_qk_dma(GemmArgs g) {
 // 16-byte slot l % 32 of that row, i.e. logical columns 16 ((l % 32) / 2 ^
 // swz(row)) + 8 (l % 2).  V's loads of step kt + 2 go into stage kt % 2
 // right after step kt's barrier and are waited for at step kt + 1's barrier.
+template <bool ALL_INTERIOR>
 __global__ __launch_bounds__(kGemmThreads) void k_gemm_pv_dma(GemmArgs g) {
     constexpr int kBElems = kBK * kBN;
     __shared__ __align__(16) uint16_t a0s[kTileElems];
@@ -1382,17 +1387,31 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm_pv_dma(GemmArgs g) {
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const long per_head = (long)g.tiles_m * g.tiles_n;
     const long total = per_head * g.heads;
-    const long t = xcd_tile(blockIdx.x, total);
-    if (t >= total) return;
-    const int bh = __builtin_amdgcn_readfirstlane((int)(t / per_head));
-    const int rem = (int)(t - (long)bh * per_head);
-    // row panels fastest: the few workgroups of one V panel run together
-    const int tn = rem / g.tiles_m, tm = rem - tn * g.tiles_m;
-    const int m0 = __builtin_amdgcn_readfirstlane(tm * kBM);
-    const int n0 = __builtin_amdgcn_readfirstlane(tn * kBN);
-
-    const __amdgpu_buffer_rsrc_t ra = gemm_rsrc(g.A + bh * g.sa, (long)g.M * g.lda);
-    const __amdgpu_buffer_rsrc_t rb = gemm_rsrc(g.B + bh * g.sb, (long)g.K * g.ldb);
+    // Persistent: workgroup w takes the virtual ids w, w + G, ... (G =
+    // gridDim.x, a multiple of 8, so every id of w maps to w's XCD); each
+    // tile's first loads are issued before the previous tile's output is
+    // stored.
+    const long vend = (total + 7) / 8 * 8;
+    int bh = 0, m0 = 0, n0 = 0;
+    bool interior = true;
+    __amdgpu_buffer_rsrc_t ra, rb;
+    auto set_tile = [&](long t) __attribute__((always_inline)) {
+        bh = __builtin_amdgcn_readfirstlane((int)(t / per_head));
+        const int rem = (int)(t - (long)bh * per_head);
+        // row panels fastest: the few tiles of one V panel run together
+        const int tn = rem / g.tiles_m, tm = rem - tn * g.tiles_m;
+        m0 = __builtin_amdgcn_readfirstlane(tm * kBM);
+        n0 = __builtin_amdgcn_readfirstlane(tn * kBN);
+        interior = ALL_INTERIOR || (m0 + kBM <= g.M && n0 + kBN <= g.N);
+        ra = gemm_rsrc(g.A + bh * g.sa, (long)g.M * g.lda);
+        rb = gemm_rsrc(g.B + bh * g.sb, (long)g.K * g.ldb);
+    };
+    long vt = blockIdx.x;
+    {
+        const long t = xcd_tile(vt, total);
+        if (t >= total) return;
+        set_tile(t);
+    }
     constexpr uint32_t kOut = 0xfffffff0u;  // an offset past every descriptor's range
 
     // ---- E chunks: thread's chunk u is row tid / 8 + 64 u, keys 8 (tid % 8) ..
@@ -1454,12 +1473,6 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm_pv_dma(GemmArgs g) {
     constexpr int TI = 4, TJ = 2;
     const int wm = (wave >> 2) * 128, wn = (wave & 3) * 64;
     v16f acc[TI][TJ];
-#pragma unroll
-    for (int i = 0; i < TI; ++i)
-#pragma unroll
-        for (int j = 0; j < TJ; ++j)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
     struct Frag {
         uint4 a[TI], b[TJ];
     };
@@ -1492,6 +1505,19 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm_pv_dma(GemmArgs g) {
     constexpr int kReads = TI + 2 * TJ;
     Stage st;
     Frag f0, f1;
+    float mt[kFacTiles], lt[kFacTiles];  // the tile statistics of row m0 + tid
+    auto load_stats = [&]() __attribute__((always_inline)) {
+        if (tid < kBM) {
+            const int row = m0 + tid;
+            const long base = ((long)bh * g.M + row) * g.gt;
+#pragma unroll
+            for (int t2 = 0; t2 < kFacTiles; ++t2) {
+                const bool on = row < g.M && t2 < g.gt;
+                mt[t2] = on ? g.st_m[base + t2] : -INFINITY;
+                lt[t2] = on ? g.st_l[base + t2] : 0.f;
+            }
+        }
+    };
     auto step = [&](int kt, auto S, auto next, auto next2, auto edge) __attribute__((always_inline)) {
         constexpr int s = decltype(S)::value;
         using S1 = std::integral_constant<int, s ^ 1>;
@@ -1524,27 +1550,23 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm_pv_dma(GemmArgs g) {
         if constexpr (N1) sched_mfma_reads<kReads>();
         __builtin_amdgcn_sched_barrier(0);
     };
-    auto kloop = [&](auto edge) __attribute__((always_inline)) {
-        using T = std::integral_constant<bool, true>;
-        using F = std::integral_constant<bool, false>;
-        // V of steps 0 and 1 and E of step 0 are issued first, so that the
-        // statistics' loads below share one memory round trip with them
+    // a tile's first loads: V of steps 0 and 1, E of step 0 and (persistent
+    // form) the rows' tile statistics: one memory round trip for all of them
+    auto issue = [&](auto edge) __attribute__((always_inline)) {
         dma_b(I0{}, 0, edge);
         dma_b(I1{}, 1, edge);
         load_a(st, 0, edge);
-        // the workgroup's rows' softmax factors (as in k_gemm's NN form)
+        if constexpr (ALL_INTERIOR) load_stats();
+    };
+    // the rows' softmax factors (as in k_gemm's NN form) into the LDS table,
+    // then E of step 0 to LDS; vmcnt(pending) leaves the previous tile's
+    // output stores (issued after this tile's loads) in flight
+    auto finish = [&](auto edge, auto pending) __attribute__((always_inline)) {
+        if constexpr (!ALL_INTERIOR) load_stats();
         if (tid < kBM) {
-            const int row = m0 + tid;
-            const long base = ((long)bh * g.M + row) * g.gt;
-            float mt[kFacTiles], lt[kFacTiles];
             float m = -INFINITY;
 #pragma unroll
-            for (int t2 = 0; t2 < kFacTiles; ++t2) {
-                const bool on = row < g.M && t2 < g.gt;
-                mt[t2] = on ? g.st_m[base + t2] : -INFINITY;
-                lt[t2] = on ? g.st_l[base + t2] : 0.f;
-                m = fmaxf(m, mt[t2]);
-            }
+            for (int t2 = 0; t2 < kFacTiles; ++t2) m = fmaxf(m, mt[t2]);
             float l = 0.f;
 #pragma unroll
             for (int t2 = 0; t2 < kFacTiles; ++t2)
@@ -1555,12 +1577,19 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm_pv_dma(GemmArgs g) {
                 fac[tid * kFacTiles + t2] =
                     (m == -INFINITY || t2 >= g.gt) ? 0.f : __expf(mt[t2] - m) * inv;
         }
-        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+        if constexpr (decltype(pending)::value == 32)
+            __builtin_amdgcn_s_waitcnt(0x8F70);  // vmcnt(32)
+        else
+            __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
         __syncthreads();  // the factor table, V of steps 0 and 1
         store_a(I0{}, st, 0);
         load_a(st, 1, edge);
         __syncthreads();
         read_frag(f0, I0{}, 0);
+    };
+    auto kloop = [&](auto edge) __attribute__((always_inline)) {
+        using T = std::integral_constant<bool, true>;
+        using F = std::integral_constant<bool, false>;
         // nk is even (the host's condition for this kernel)
         int kt = 0;
         for (; kt + 2 < nk; kt += 2) {
@@ -1570,31 +1599,104 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm_pv_dma(GemmArgs g) {
         step(kt, I0{}, T{}, F{}, edge);
         step(kt + 1, I1{}, F{}, F{}, edge);
     };
-    if (m0 + kBM <= g.M && n0 + kBN <= g.N)
-        kloop(std::integral_constant<bool, false>{});
-    else
-        kloop(std::integral_constant<bool, true>{});
+    using EdgeF = std::integral_constant<bool, false>;
+    using EdgeT = std::integral_constant<bool, true>;
+    using P0 = std::integral_constant<int, 0>;
+    using P32 = std::integral_constant<int, 32>;
 
     // lane: output row m0 + wm + 32 i + lane % 32, columns n0 + wn + 32 j +
     // 8 (r / 4) + 4 (lane / 32) + r % 4: four consecutive bf16 per group of r
-    uint16_t* C = static_cast<uint16_t*>(g.C) + bh * g.sc;
+    // (converted two at a time by the hardware, round to nearest even).
+    // Interior tiles issue exactly TI * TJ * 4 = 32 stores.
+    auto pack4 = [&](const v16f& a, int rg) __attribute__((always_inline)) {
+        const bf16x2_t lo = {(__bf16)a[4 * rg], (__bf16)a[4 * rg + 1]};
+        const bf16x2_t hi = {(__bf16)a[4 * rg + 2], (__bf16)a[4 * rg + 3]};
+        return u32x2{__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi)};
+    };
+    static_assert(TI * TJ * 4 == 32, "interior output stores per lane");
+    auto store_out = [&](int obh, int om0, int on0, bool oint) __attribute__((always_inline)) {
+        uint16_t* C = static_cast<uint16_t*>(g.C) + obh * g.sc;
+        if (oint) {
+            // buffer stores: the lane's row offset in a register, the column
+            // group's offset in a scalar register
+            const __amdgpu_buffer_rsrc_t rc = gemm_rsrc(C, (long)g.M * g.ldc);
+            const uint32_t ldc = (uint32_t)g.ldc;
 #pragma unroll
-    for (int i = 0; i < TI; ++i) {
-        const int row = m0 + wm + i * 32 + (lane & 31);
-        if (row >= g.M) continue;
+            for (int i = 0; i < TI; ++i) {
+                const uint32_t vo = 2u * ((uint32_t)(om0 + wm + i * 32 + (lane & 31)) * ldc +
+                                          (uint32_t)(on0 + wn + 4 * (lane >> 5)));
 #pragma unroll
-        for (int j = 0; j < TJ; ++j)
+                for (int j = 0; j < TJ; ++j)
 #pragma unroll
-            for (int rg = 0; rg < 4; ++rg) {
-                const int col = n0 + wn + j * 32 + 8 * rg + 4 * (lane >> 5);
-                if (col >= g.N) continue;
-                uint2 w;
-                w.x = (uint32_t)f32_to_bf16_bits(acc[i][j][4 * rg]) |
-                      ((uint32_t)f32_to_bf16_bits(acc[i][j][4 * rg + 1]) << 16);
-                w.y = (uint32_t)f32_to_bf16_bits(acc[i][j][4 * rg + 2]) |
-                      ((uint32_t)f32_to_bf16_bits(acc[i][j][4 * rg + 3]) << 16);
-                *reinterpret_cast<uint2*>(C + (long)row * g.ldc + col) = w;
+                    for (int rg = 0; rg < 4; ++rg)
+                        __builtin_amdgcn_raw_buffer_store_b64(
+                            pack4(acc[i][j], rg), rc, (int)vo,
+                            (int)__builtin_amdgcn_readfirstlane(2u * (uint32_t)(j * 32 + 8 * rg)),
+                            0);
             }
+            return;
+        }
+#pragma unroll
+        for (int i = 0; i < TI; ++i) {
+            const int row = om0 + wm + i * 32 + (lane & 31);
+            if (row >= g.M) continue;
+#pragma unroll
+            for (int j = 0; j < TJ; ++j)
+#pragma unroll
+                for (int rg = 0; rg < 4; ++rg) {
+                    const int col = on0 + wn + j * 32 + 8 * rg + 4 * (lane >> 5);
+                    if (col >= g.N) continue;
+                    *reinterpret_cast<u32x2*>(C + (long)row * g.ldc + col) = pack4(acc[i][j], rg);
+                }
+        }
+    };
+
+    auto zero_acc = [&]() __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < TI; ++i)
+#pragma unroll
+            for (int j = 0; j < TJ; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+    };
+    if constexpr (!ALL_INTERIOR) {
+        // ragged shapes: one tile per workgroup (the grid covers them all)
+        auto body = [&](auto edge) __attribute__((always_inline)) {
+            issue(edge);
+            finish(edge, P0{});
+            zero_acc();
+            kloop(edge);
+        };
+        if (interior)
+            body(EdgeF{});
+        else
+            body(EdgeT{});
+        store_out(bh, m0, n0, interior);
+    } else {
+        issue(EdgeF{});
+        // vmcnt(32) is right once the previous tile's 32 stores were issued
+        // after the loads being waited for
+        bool first = true;
+        for (;;) {
+            if (first)
+                finish(EdgeF{}, P0{});
+            else
+                finish(EdgeF{}, P32{});
+            zero_acc();
+            kloop(EdgeF{});
+            const int obh = bh, om0 = m0, on0 = n0;
+            vt += gridDim.x;
+            const long tn = vt < vend ? xcd_tile(vt, total) : total;
+            const bool more = tn < total;
+            __syncthreads();  // every wave is done with the stages and the factor table
+            if (more) {
+                set_tile(tn);
+                issue(EdgeF{});
+            }
+            store_out(obh, om0, on0, true);
+            if (!more) break;
+            first = false;
+        }
     }
 }
 
@@ -1846,6 +1948,22 @@ __global__ __launch_bounds__(kEncThreads) void k_encode_f16_regs(const uint16_t*
     }
 }
 
+// Compute units of the current device (cached per device): the persistent
+// PV GEMM runs one workgroup per CU.
+int device_cus() {
+    static std::atomic<int> cache[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    int n = cache[dev].load(std::memory_order_relaxed);
+    if (n == 0) {
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            n <= 0)
+            n = 256;
+        cache[dev].store(n, std::memory_order_relaxed);
+    }
+    return n;
+}
+
 }  // namespace
 
 hipError_t launch_gemm_qk(int f16, const uint16_t* Q, const uint16_t* K, const float* qinv,
@@ -2053,9 +2171,18 @@ hipError_t launch_gemm_pv(const uint16_t* E, float* st_m, float* st_l, float* ga
     g.scale = 1.f;
     const long total = (long)g.tiles_m * g.tiles_n * BH;
     const long grid = (total + 7) / 8 * 8;
-    // an even number of 64-key steps: V straight into LDS
-    if (g.gt <= kFacTiles && Lk % 128 == 0)
-        hipLaunchKernelGGL(k_gemm_pv_dma, dim3((unsigned)grid), dim3(kGemmThreads), 0, st, g);
+    // an even number of 64-key steps: V straight into LDS; with every tile
+    // interior, one persistent workgroup per CU (a multiple of 8 of them,
+    // for the XCD-aware order), else one workgroup per tile
+    if (g.gt <= kFacTiles && Lk % 128 == 0) {
+        const long cus = std::max(8, device_cus() / 8 * 8);
+        if (Lq % kBM == 0 && D % kBN == 0)
+            hipLaunchKernelGGL(k_gemm_pv_dma<true>, dim3((unsigned)std::min(grid, cus)),
+                               dim3(kGemmThreads), 0, st, g);
+        else
+            hipLaunchKernelGGL(k_gemm_pv_dma<false>, dim3((unsigned)grid), dim3(kGemmThreads), 0,
+                               st, g);
+    }
     else if (g.gt <= kFacTiles)
         hipLaunchKernelGGL((k_gemm<false, true, kOutBf16, true>), dim3((unsigned)grid),
                            dim3(kGemmThreads), 0, st, g);

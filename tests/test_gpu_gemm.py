@@ -99,6 +99,28 @@ def test_gemm_path_long_key_rows(am, dev, shape):
     assert n == 0, f"normwise rel {nrel}, max abs {mabs}"
 
 
+@pytest.mark.parametrize("shape,pe", [((2, 8, 300, 512, 2304), "none"),
+                                      ((2, 8, 300, 512, 2304), "rope_half"),
+                                      ((4, 16, 512, 512, 1024), "none")],
+                         ids=lambda v: "x".join(map(str, v)) if isinstance(v, tuple) else v)
+def test_gemm_pv_more_tiles_than_cus(am, dev, shape, pe):
+    """More PV output tiles than compute units (288 and 512 tiles): the
+    persistent PV workgroups take several tiles each, the next tile's loads
+    overlapping the previous tile's output stores; 2304 columns and 300 rows
+    mix edge and interior tiles within one workgroup's sequence."""
+    import hip_rt
+    B, Hh, Lq, Lk, D = shape
+    print(f"[case] gemm pv persistent {shape} {pe}", flush=True)
+    desc = _desc(am, pe)
+    assert am.path(1, B, Hh, Lq, Lk, D, desc) == am.ATN_PATH_GEMM
+    (q, k, v), (Q, K, V) = H.device_inputs((B, Hh, Lq, D), (B, Hh, Lk, D), 307 + D, "bf16")
+    out = H.empty(Q.shape, "bf16")
+    am.attention_ex(q, k, v, out, pe=desc)
+    hip_rt.synchronize()
+    n, nrel, mabs = H.check_bf16(out.numpy(), _ref(pe, Q, K, V, Lq, Lk, D))
+    assert n == 0, f"normwise rel {nrel}, max abs {mabs}"
+
+
 @pytest.mark.parametrize("pe,sigma", [("none", 3.0), ("rope_half", 1.0)])
 def test_gemm_path_wide_score_range(am, dev, pe, sigma):
     """Scores spread widely: one 256-key tile of keys is scaled x4, so in
