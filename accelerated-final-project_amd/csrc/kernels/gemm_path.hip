@@ -42,7 +42,10 @@
 // MFMAs, one barrier per step), and an
 // XCD-aware tile order: consecutive tile indices run on the same XCD
 // (workgroups are dealt round-robin to the 8 XCDs), so concurrent
-// workgroups of one head share their Q/K/V panels in that XCD's L2.
+// workgroups of one head share their Q/K/V panels in that XCD's L2.  The
+// PV GEMM with V loaded straight into LDS (k_gemm_pv_dma) runs one
+// persistent workgroup per CU when every tile is interior, each tile's
+// first loads issued before the previous tile's output stores.
 //
 // V enters the second GEMM as the B operand, which MFMA wants contiguous
 // along K (= keys); V rows are contiguous along D, so the V tile is stored
