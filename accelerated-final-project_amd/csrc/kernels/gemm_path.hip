@@ -195,6 +195,14 @@ __device__ __forceinline__ float vmaxf(float a, float b) {
     return d;
 }
 
+// max(m, |a|, |b|) as one v_max3_f32 with absolute-value modifiers (the
+// running magnitude maximum of the fused K encoding)
+__device__ __forceinline__ float vmax3abs(float m, float a, float b) {
+    float d;
+    asm("v_max3_f32 %0, %1, |%2|, |%3|" : "=v"(d) : "v"(m), "v"(a), "v"(b));
+    return d;
+}
+
 // Max / sum over each half-wave (lanes with the same lane / 32): DPP within
 // quads, 8 and 16 lanes, then the 16-lane hop by ds_swizzle.
 __device__ __forceinline__ float half_max(float v) {
@@ -848,7 +856,7 @@ __device__ __forceinline__ uint4 enc_chunk(const uint4& w, const uint4& t, float
             a *= sc;
             b *= sc;
         } else {
-            mx = fmaxf(mx, fmaxf(fabsf(a), fabsf(b)));
+            mx = vmax3abs(mx, a, b);
         }
         y[i] = pk_f16(a, b);
     }
@@ -877,7 +885,7 @@ __device__ __forceinline__ void enc_half(uint4& w0, uint4& w1, const uint4& t0, 
                 r0[h] *= sc;
                 r1[h] *= sc;
             } else {
-                mx = fmaxf(mx, fmaxf(fabsf(r0[h]), fabsf(r1[h])));
+                mx = vmax3abs(mx, r0[h], r1[h]);
             }
         }
         y0[i] = pk_f16(r0[0], r0[1]);
