@@ -525,15 +525,16 @@ GemmPlan gemm_plan(int dtype, const Shape& s, const PePlan& plan) {
     // and so is the key side unless its encoding runs inside the QK^T GEMM
     // (k_gemm_qk_enc: fp16 tables, no K~ pass).  That takes an even number of
     // 64-deep K steps, the library's tables, rotate-half over all of D, and
-    // at most two 256-row query tiles: every query tile's workgroups encode
-    // their K tiles again, so with more of them the encoding costs the
-    // MFMA-bound GEMM more than the K~ pass does (config 4: 892 us fused vs
-    // 642 + 199 us; config 5, one query tile: 160 us vs 143 + 110 us).
+    // at most four 256-row query tiles: every query tile's workgroups encode
+    // their K tiles again, so the in-GEMM encoding grows with Lq while the
+    // K~ pass does not (config 4, four query tiles: 724 us fused against
+    // 545 + 198 us, so the break-even is near 1100 rows; config 5, one query
+    // tile: 112 us against 143 + 110 us).
     // ATN_GEMM_FUSED_K=-1 turns it off, =1 forces it on (measurement).
     p.encoded = plan.pek != atn::kPeNone;
     const int fk = env_int("ATN_GEMM_FUSED_K");
     if (p.encoded && s.D % 128 == 0 && !plan.caller_tables && fk >= 0 &&
-        (fk > 0 || (s.Lq + 255) / 256 <= 2)) {
+        (fk > 0 || (s.Lq + 255) / 256 <= 4)) {
         if (!plan.k.on)
             p.benc = atn::kGemmEncRaw;
         else if (plan.pek == atn::kPeSinusoidal)

@@ -9,7 +9,7 @@
 //
 //   k_encode_f16  (with a positional encoding) Q~, K~ = encoded Q, K as
 //                 fp16 rows with a power-of-two scale per row; with at most
-//                 two 256-row query tiles K is not encoded here but inside
+//                 four 256-row query tiles K is not encoded here but inside
 //                 the GEMM (k_gemm_qk_enc: fp16 tables, no K~ round trip)
 //   k_gemm  (NT)  S = scale * Q K^T, kept on chip; per row of its 256-key
 //                 tile t the epilogue writes E = exp(S - m_t) (fp16, in

@@ -150,15 +150,16 @@ def test_gemm_path_wide_score_range(am, dev, pe, sigma):
 
 
 @pytest.mark.parametrize("shape,pe", [((1, 2, 256, 512, 256), "sinusoidal"),
-                                      ((1, 1, 1024, 256, 128), "rope_half"),
+                                      ((1, 1, 1280, 256, 128), "rope_half"),
                                       ((1, 2, 256, 384, 136), "none")],
                          ids=["fusedK", "qkdma-encK", "register-stage"])
 def test_gemm_graph_replays_match_eager(am, dev, shape, pe):
     """Captured HIP graph of three calls on one workspace, replayed four times
     with eager work and synchronizations in between: every replay equals the
     eager result bit for bit.  The shapes take the K encoding inside the
-    QK^T GEMM, the K~ pass with the both-tiles-in-LDS QK^T GEMM, and the
-    register-staged GEMMs."""
+    QK^T GEMM, the K~ pass with the both-tiles-in-LDS QK^T GEMM (five query
+    tiles: past the fused encoding's limit of four), and the register-staged
+    GEMMs."""
     import hip_rt
     B, Hh, Lq, Lk, D = shape
     print(f"[case] gemm graph replay {shape} {pe}", flush=True)

@@ -1,7 +1,7 @@
 """GPU parity of the GEMM path's fused K encoding and of its gated fallback.
 
 With a positional encoding, D % 128 == 0, the library's tables and at most
-two 256-row query tiles, the QK^T GEMM reads raw bf16 K and encodes it on
+four 256-row query tiles, the QK^T GEMM reads raw bf16 K and encodes it on
 its way to LDS from fp16 tables (no K~ pass).  Every case here runs twice,
 with the fusion forced on (ATN_GEMM_FUSED_K=1) and switched off (=-1: K~
 from the row-scaled encoder), and both results must meet the bf16 bar
