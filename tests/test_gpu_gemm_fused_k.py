@@ -87,6 +87,24 @@ def test_fused_k_encoding(am, dev, shape, mode):
         assert n == 0, f"fused={fused}: normwise rel {nrel}, max abs {mabs}"
 
 
+@pytest.mark.parametrize("mode", list(MODES))
+def test_fused_k_four_query_tiles(am, dev, mode):
+    """1000 query rows are four 256-row query tiles, the most the planner
+    fuses (the last one ragged), over 520 keys (a ragged key tile); fused
+    and K~-pass results both meet the bf16 bar against the oracle."""
+    B, Hh, Lq, Lk, D = 1, 1, 1000, 520, 256
+    print(f"[case] fused K four query tiles {mode}", flush=True)
+    desc = am.make_pe(**MODES[mode])
+    assert am.path(1, B, Hh, Lq, Lk, D, desc) == am.ATN_PATH_GEMM
+    sigma = 0.5 if MODES[mode]["kind"] == "sinusoidal" else 1.0
+    (q, k, v), (Q, K, V) = H.device_inputs((B, Hh, Lq, D), (B, Hh, Lk, D), 1031, "bf16", sigma)
+    ref = _ref(mode, Q, K, V)
+    for fused in (True, False):
+        got = _run(am, q, k, v, Q.shape, desc, fused)
+        n, nrel, mabs = H.check_bf16(got, ref)
+        assert n == 0, f"fused={fused}: normwise rel {nrel}, max abs {mabs}"
+
+
 def test_fused_k_config4_head_shape(am, dev):
     """The fused rotate-half GEMM forced on at config 4's per-head shape
     (1024 x 1024, D = 4096: interior tiles only, 64 K steps), two heads;
