@@ -1570,8 +1570,10 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm_pv_dma(GemmArgs g) {
         if constexpr (ALL_INTERIOR) load_stats();
     };
     // the rows' softmax factors (as in k_gemm's NN form) into the LDS table,
-    // then E of step 0 to LDS; vmcnt(pending) leaves the previous tile's
-    // output stores (issued after this tile's loads) in flight
+    // then E of step 0 to LDS.  vmcnt(pending) waits only for this tile's
+    // loads (the previous tile's 32 output stores were issued after them);
+    // the compiler's own waits for the statistics registers at the loop head
+    // (in the first four waves) still cover every outstanding operation.
     auto finish = [&](auto edge, auto pending) __attribute__((always_inline)) {
         if constexpr (!ALL_INTERIOR) load_stats();
         if (tid < kBM) {
@@ -1685,8 +1687,8 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm_pv_dma(GemmArgs g) {
         store_out(bh, m0, n0, interior);
     } else {
         issue(EdgeF{});
-        // vmcnt(32) is right once the previous tile's 32 stores were issued
-        // after the loads being waited for
+        // vmcnt(32) covers this tile's loads once the previous tile's 32
+        // stores were issued after them
         bool first = true;
         for (;;) {
             if (first)
