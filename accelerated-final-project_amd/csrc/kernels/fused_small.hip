@@ -302,8 +302,12 @@ __device__ __forceinline__ bf16x8 lds8(const uint16_t* p) {
     return __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(p));
 }
 
+// two floats to packed bf16 by the hardware conversion (round to nearest
+// even, as f32_to_bf16_bits)
+typedef __bf16 bf16x2_hw __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
-    return (uint32_t)f32_to_bf16_bits(a) | ((uint32_t)f32_to_bf16_bits(b) << 16);
+    const bf16x2_hw v = {(__bf16)a, (__bf16)b};
+    return __builtin_bit_cast(uint32_t, v);
 }
 
 // NT independent 16x16 fp32 MFMA accumulations sharing one A operand:
@@ -520,10 +524,11 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
                 *reinterpret_cast<uint2*>(hi + off) = w;
                 if constexpr (kSplit) {
                     uint16_t* lo = reinterpret_cast<uint16_t*>(smem + (isq ? g.ql_off : g.kl_off));
-                    float r4[4];
-#pragma unroll
-                    for (int e = 0; e < 4; ++e)
-                        r4[e] = e4[e] - bf16_bits_to_f32(f32_to_bf16_bits(e4[e]));
+                    // residuals against the hi parts just packed
+                    const float r4[4] = {e4[0] - __uint_as_float(w.x << 16),
+                                         e4[1] - __uint_as_float(w.x & 0xffff0000u),
+                                         e4[2] - __uint_as_float(w.y << 16),
+                                         e4[3] - __uint_as_float(w.y & 0xffff0000u)};
                     uint2 wl;
                     wl.x = pack_bf16x2(r4[0], r4[1]);
                     wl.y = pack_bf16x2(r4[2], r4[3]);
@@ -875,11 +880,11 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
                 const float p0 = v[u] * inv, p1 = v[u + 1] * inv;
                 if constexpr (kBf16) {
                     uint16_t* ph = reinterpret_cast<uint16_t*>(smem + g.p_off);
-                    const uint16_t h0 = f32_to_bf16_bits(p0), h1 = f32_to_bf16_bits(p1);
-                    *reinterpret_cast<uint32_t*>(&ph[i * g.pstr + j0 + u]) =
-                        (uint32_t)h0 | ((uint32_t)h1 << 16);
+                    const uint32_t h = pack_bf16x2(p0, p1);
+                    *reinterpret_cast<uint32_t*>(&ph[i * g.pstr + j0 + u]) = h;
                     *reinterpret_cast<uint32_t*>(&ph[(MQ + i) * g.pstr + j0 + u]) =
-                        pack_bf16x2(p0 - bf16_bits_to_f32(h0), p1 - bf16_bits_to_f32(h1));
+                        pack_bf16x2(p0 - __uint_as_float(h << 16),
+                                    p1 - __uint_as_float(h & 0xffff0000u));
                 } else {
                     *reinterpret_cast<float2*>(
                         &reinterpret_cast<float*>(smem + g.p_off)[i * g.pstr + j0 + u]) =
@@ -948,7 +953,11 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
                         const int i = rb * 16 + lk * 4 + r;
-                        if (i < Lq) Elem<T>::st(O, (orow0 + i) * D + dd, acc[u][r]);
+                        if (i >= Lq) continue;
+                        if constexpr (kBf16)
+                            O[(orow0 + i) * D + dd] = __builtin_bit_cast(uint16_t, (__bf16)acc[u][r]);
+                        else
+                            O[(orow0 + i) * D + dd] = acc[u][r];
                     }
                 }
             };
