@@ -389,7 +389,8 @@ int rsag_words(int E, int n) {
 }
 
 // Tuning overrides (environment): ATN_FUSED_ROWS = query rows per row group
-// (16, 32 or 64), ATN_FUSED_EXCHANGE = "gather" or "rsag".  A plan the
+// (16, 32 or 64), ATN_FUSED_EXCHANGE = "gather" or "rsag", ATN_FUSED_DC =
+// D-slice width (a multiple of 32); ATN_FUSED_TRACE prints the plan.  A plan the
 // override makes impossible falls back to the default choice.
 int env_int(const char* name) {
     const char* v = std::getenv(name);
@@ -399,10 +400,10 @@ int env_int(const char* name) {
 // Cuts each head's query rows into row groups of MB rows and D into slices
 // so that about one workgroup per CU runs and the whole grid is resident at
 // once (the kernel's exchange waits need that).  Capacity is the device's
-// CU count x resident workgroups per CU for the chosen LDS size.  Preferred:
-// the one-gather exchange (one memory round trip) with at least half the
-// CUs busy, largest row group first (fewest K/V re-reads); otherwise the
-// whole head as one row group with reduce-scatter + all-gather.
+// CU count x resident workgroups per CU for the chosen LDS size.  Among the
+// plans (row groups of 64, 32 or 16 rows) that keep at least half the CUs
+// busy, the one of least estimated time is taken; otherwise the whole head
+// as one row group.
 FusedPlan fused_plan(int dtype, int pek, const Shape& s, bool query_device) {
     FusedPlan none;
     if (s.Lq > kFusedMaxLq || s.Lk > kFusedMaxLk || s.D % 4 != 0) return none;
@@ -425,6 +426,8 @@ FusedPlan fused_plan(int dtype, int pek, const Shape& s, bool query_device) {
         return c;
     };
     const int MQ = (int)(s.Lq + 15) / 16 * 16, NK = (int)(s.Lk + 31) / 32 * 32;
+    int force_dc = env_int("ATN_FUSED_DC");
+    if (force_dc < 32 || force_dc % 32 != 0) force_dc = 0;
     // the smallest slice width that fits LDS and the device for row groups of MB rows
     auto plan_rows = [&](int MB) {
         FusedPlan p;
@@ -432,13 +435,17 @@ FusedPlan fused_plan(int dtype, int pek, const Shape& s, bool query_device) {
         if (groups > cus) return p;
         const int64_t per_group = cus / groups;
         int64_t dc = (s.D + per_group - 1) / per_group;
-        dc = (dc + 31) / 32 * 32;
+        dc = force_dc > 0 ? force_dc : (dc + 31) / 32 * 32;
         for (;; dc += 32) {
+            if (force_dc > 0 && dc != force_dc) return p;
             if (dc > 1024) return p;  // one 4-element column group per thread at most
             const int lds = atn::fused_small_lds_bytes(dtype, pek, MB, (int)s.Lk, (int)dc);
             if (lds > kLdsLimit) return p;
             const int64_t n = (s.D + dc - 1) / dc;
-            int cap = (int)cus;  // one workgroup per CU is always resident
+            // one workgroup per CU is always resident; a size query (no
+            // device) allows the most any plan may launch, so that the
+            // workspace it reports bounds a forced narrower slice too
+            int cap = query_device ? (int)cus : kSyncMaxWorkgroups;
             if (query_device && n > 1) {
                 cap = capacity(lds);
                 if (cap <= 0) return p;
@@ -467,11 +474,21 @@ FusedPlan fused_plan(int dtype, int pek, const Shape& s, bool query_device) {
     const int force_rows = env_int("ATN_FUSED_ROWS");
     const char* xe = std::getenv("ATN_FUSED_EXCHANGE");
     const int force_x = xe == nullptr ? -1 : (std::strcmp(xe, "gather") == 0 ? 1 : 0);
+    // with an override or ATN_FUSED_TRACE set, the device plan goes to stderr
+    const bool trace = query_device && (force_rows > 0 || xe != nullptr || force_dc > 0 ||
+                                        std::getenv("ATN_FUSED_TRACE") != nullptr);
+    auto report = [&](const FusedPlan& p) {
+        if (trace && p.ok)
+            std::fprintf(stderr, "atn: fused plan rows %d slice %d x %d %s, %d workgroups\n",
+                         p.MB, p.dc, p.nchunk,
+                         p.nchunk == 1 ? "none" : (p.gather1 ? "gather" : "rsag"), p.workgroups);
+        return p;
+    };
     auto pick = [&](const FusedPlan& p) {
         return p.ok && (force_x < 0 || p.nchunk == 1 || p.gather1 == force_x) &&
                (force_rows == 0 || p.MB == force_rows);
     };
-    if (force_rows > 0 || force_x >= 0) {
+    if (force_rows > 0 || force_x >= 0 || force_dc > 0) {
         for (int MB : {64, 32, 16}) {
             if (MB > MQ && MB != 16) continue;
             FusedPlan p = plan_rows(MB);
@@ -483,16 +500,28 @@ FusedPlan fused_plan(int dtype, int pek, const Shape& s, bool query_device) {
                     p.bytes = kSyncBytes + round256(p.part_words * 4) + p.red_words * 4;
                 }
             }
-            if (pick(p)) return p;
+            if (pick(p)) return report(p);
         }
+        std::fprintf(stderr, "atn: fused plan override not possible, default plan\n");
     }
+    // Estimated time in us beyond the fixed cost: each workgroup's Q, K and V
+    // slice loads (0.096 us per KiB), the exchange's waits and reads per
+    // slice (0.146 us) and reduce-scatter's second round trip (0.9 us);
+    // fitted to config-2-shaped fp32 runs (B=1, H=4, Lq=Lk=64, D 512-4096)
+    // on MI355X, where it ranks first the plan that measured fastest.
+    auto cost = [&](const FusedPlan& p) {
+        const double kib = (double)(std::min(p.MB, MQ) + 2 * NK) * p.dc *
+                           (dtype == ATN_DTYPE_F32 ? 4 : 2) / 1024.0;
+        return 0.096 * kib + 0.146 * p.nchunk + (p.nchunk > 1 && !p.gather1 ? 0.9 : 0.0);
+    };
+    FusedPlan best;
     for (int MB : {64, 32, 16}) {
         if (MB > MQ) continue;
         const FusedPlan p = plan_rows(MB);
-        if (p.ok && (p.nchunk == 1 || p.gather1) && 2 * p.workgroups >= std::min(cus, 2048))
-            return p;
+        if (p.ok && 2 * p.workgroups >= std::min(cus, 2048) && (!best.ok || cost(p) < cost(best)))
+            best = p;
     }
-    return plan_rows(MQ);
+    return report(best.ok ? best : plan_rows(MQ));
 }
 
 // ---------------------------------------------------------------- gemm plan
