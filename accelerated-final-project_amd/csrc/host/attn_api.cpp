@@ -398,13 +398,12 @@ int env_int(const char* name) {
 }
 
 // Cuts each head's query rows into row groups of MB rows and D into slices
-// so that about one workgroup per CU runs and the whole grid is resident at
-// once (the kernel's exchange waits need that).  Capacity is the device's
-// CU count x resident workgroups per CU for the chosen LDS size.  Among the
-// plans (row groups of 64, 32 or 16 rows) that keep at least half the CUs
-// busy, the one of least estimated time is taken; otherwise the whole head
-// as one row group.
-FusedPlan fused_plan(int dtype, int pek, const Shape& s, bool query_device) {
+// of dc dims, one workgroup each, with the whole grid resident at once (the
+// kernel's exchange waits need that: capacity is the device's CU count x
+// resident workgroups per CU for the plan's LDS size).  Of every plan that
+// fits LDS, the device and the exchange's per-thread limits, the one of least
+// estimated time is taken.
+FusedPlan fused_plan_uncached(int dtype, int pek, const Shape& s, bool query_device) {
     FusedPlan none;
     if (s.Lq > kFusedMaxLq || s.Lk > kFusedMaxLk || s.D % 4 != 0) return none;
     int cus = 256;
@@ -426,102 +425,125 @@ FusedPlan fused_plan(int dtype, int pek, const Shape& s, bool query_device) {
         return c;
     };
     const int MQ = (int)(s.Lq + 15) / 16 * 16, NK = (int)(s.Lk + 31) / 32 * 32;
-    int force_dc = env_int("ATN_FUSED_DC");
-    if (force_dc < 32 || force_dc % 32 != 0) force_dc = 0;
-    // the smallest slice width that fits LDS and the device for row groups of MB rows
-    auto plan_rows = [&](int MB) {
+    const int es = dtype == ATN_DTYPE_F32 ? 4 : 2;
+    // one plan: row groups of MB rows, slices of dc dims, the one-gather
+    // exchange (gather = 1) or reduce-scatter + all-gather (0)
+    auto make = [&](int MB, int dc, int gather) {
         FusedPlan p;
         const int64_t groups = s.BH * ((s.Lq + MB - 1) / MB);
-        if (groups > cus) return p;
-        const int64_t per_group = cus / groups;
-        int64_t dc = (s.D + per_group - 1) / per_group;
-        dc = force_dc > 0 ? force_dc : (dc + 31) / 32 * 32;
-        for (;; dc += 32) {
-            if (force_dc > 0 && dc != force_dc) return p;
-            if (dc > 1024) return p;  // one 4-element column group per thread at most
-            const int lds = atn::fused_small_lds_bytes(dtype, pek, MB, (int)s.Lk, (int)dc);
-            if (lds > kLdsLimit) return p;
-            const int64_t n = (s.D + dc - 1) / dc;
-            // one workgroup per CU is always resident; a size query (no
-            // device) allows the most any plan may launch, so that the
-            // workspace it reports bounds a forced narrower slice too
-            int cap = query_device ? (int)cus : kSyncMaxWorkgroups;
-            if (query_device && n > 1) {
-                cap = capacity(lds);
-                if (cap <= 0) return p;
-            }
-            if (groups * n > kSyncMaxWorkgroups) return p;
-            if (n == 1 || groups * n <= cap) {
-                p.MB = MB;
-                p.dc = (int)dc;
-                p.nchunk = (int)n;
-                p.lds = lds;
-                p.workgroups = (int)(groups * n);
-                break;
-            }
+        const int64_t n = (s.D + dc - 1) / dc;
+        if (groups > cus || dc > 1024 || groups * n > kSyncMaxWorkgroups) return p;
+        if (n == 1 && gather) return p;  // a single slice has no exchange
+        const int lds = atn::fused_small_lds_bytes(dtype, pek, MB, (int)s.Lk, dc);
+        if (lds > kLdsLimit) return p;
+        // the exchange waits need every workgroup resident; a size query (no
+        // device) allows the most any plan may launch, so that the workspace
+        // it reports bounds every plan the device may take
+        if (n > 1) {
+            const int cap = query_device ? capacity(lds) : kSyncMaxWorkgroups;
+            if (cap <= 0 || groups * n > cap) return p;
         }
         const int E = MB * NK;
-        if (p.nchunk > 1) {
-            p.gather1 = gather1_words(E, p.nchunk) <= kFusedMaxWords ? 1 : 0;
-            if (!p.gather1 && rsag_words(E, p.nchunk) > kFusedMaxWords) return FusedPlan{};
-            p.part_words = (size_t)groups * p.nchunk * E;
-            p.red_words = p.gather1 ? 0 : (size_t)groups * E;
+        if (n > 1) {
+            if ((gather ? gather1_words(E, (int)n) : rsag_words(E, (int)n)) > kFusedMaxWords)
+                return p;
+            p.part_words = (size_t)(groups * n * E);
+            p.red_words = gather ? 0 : (size_t)groups * E;
         }
+        p.MB = MB;
+        p.dc = dc;
+        p.nchunk = (int)n;
+        p.lds = lds;
+        p.gather1 = n > 1 ? gather : 0;
+        p.workgroups = (int)(groups * n);
         p.bytes = kSyncBytes + round256(p.part_words * 4) + p.red_words * 4;
         p.ok = true;
         return p;
     };
+    // Estimated time in us beyond the fixed cost, fitted by least squares to
+    // 105 timed plans of 13 fp32/bf16 shapes (B*H 1-16, Lq 16-64, Lk 16-128,
+    // D 512-8192) on MI355X, where it ranks first the plan that measured
+    // fastest on every shape: each CU's Q/K/V slice loads (0.0242 us per
+    // KiB), the slices (0.0373 us each), reduce-scatter's second round trip
+    // (8.72 us), each CU's exchange reads (0.1288 us per KiB) and the
+    // workgroup count (0.358 us per CU's worth).
+    auto cost = [&](const FusedPlan& p) {
+        const double per_cu = (double)((p.workgroups + cus - 1) / cus);
+        const double kib = (double)(std::min(p.MB, MQ) + 2 * NK) * p.dc * es / 1024.0;
+        const double E = (double)p.MB * NK;
+        const double xkib = p.nchunk == 1 ? 0.0 : (p.gather1 ? E * p.nchunk : 2.0 * E) * 4 / 1024.0;
+        return 0.0242 * kib * per_cu + 0.0373 * p.nchunk +
+               (p.nchunk > 1 && !p.gather1 ? 8.72 : 0.0) + 0.1288 * xkib * per_cu +
+               0.358 * p.workgroups / cus;
+    };
+    // overrides (tuning): row group size, slice width, exchange
     const int force_rows = env_int("ATN_FUSED_ROWS");
+    int force_dc = env_int("ATN_FUSED_DC");
+    if (force_dc < 32 || force_dc % 32 != 0) force_dc = 0;
     const char* xe = std::getenv("ATN_FUSED_EXCHANGE");
     const int force_x = xe == nullptr ? -1 : (std::strcmp(xe, "gather") == 0 ? 1 : 0);
-    // with an override or ATN_FUSED_TRACE set, the device plan goes to stderr
-    const bool trace = query_device && (force_rows > 0 || xe != nullptr || force_dc > 0 ||
-                                        std::getenv("ATN_FUSED_TRACE") != nullptr);
-    auto report = [&](const FusedPlan& p) {
-        if (trace && p.ok)
-            std::fprintf(stderr, "atn: fused plan rows %d slice %d x %d %s, %d workgroups\n",
-                         p.MB, p.dc, p.nchunk,
-                         p.nchunk == 1 ? "none" : (p.gather1 ? "gather" : "rsag"), p.workgroups);
-        return p;
-    };
-    auto pick = [&](const FusedPlan& p) {
-        return p.ok && (force_x < 0 || p.nchunk == 1 || p.gather1 == force_x) &&
-               (force_rows == 0 || p.MB == force_rows);
-    };
-    if (force_rows > 0 || force_x >= 0 || force_dc > 0) {
-        for (int MB : {64, 32, 16}) {
-            if (MB > MQ && MB != 16) continue;
-            FusedPlan p = plan_rows(MB);
-            if (force_x == 0 && p.ok && p.gather1) {  // rebuild as reduce-scatter + all-gather
-                const int E = MB * NK;
-                if (rsag_words(E, p.nchunk) <= kFusedMaxWords) {
-                    p.gather1 = 0;
-                    p.red_words = (size_t)s.BH * ((s.Lq + MB - 1) / MB) * E;
-                    p.bytes = kSyncBytes + round256(p.part_words * 4) + p.red_words * 4;
-                }
+    const bool forced = force_rows > 0 || force_dc > 0 || force_x >= 0;
+    const bool trace = query_device && (forced || std::getenv("ATN_FUSED_TRACE") != nullptr);
+    // candidates: row groups of 64, 32 or 16 rows (48: the whole padded head
+    // of 33-48 rows), slices of 32-512 dims and the width that gives one
+    // workgroup per CU
+    FusedPlan best, best_forced;
+    size_t max_bytes = 0;
+    for (int MB : {64, 48, 32, 16}) {
+        if (MB > MQ || (MB == 48 && MQ != 48)) continue;
+        const int64_t groups = s.BH * ((s.Lq + MB - 1) / MB);
+        if (groups > cus) continue;
+        const int64_t per_group = cus / groups;
+        const int natural = (int)(((s.D + per_group - 1) / per_group + 31) / 32 * 32);
+        const int whole = (int)((s.D + 31) / 32 * 32);
+        for (int dc : {32, 64, 128, 256, 512, natural}) {
+            dc = std::min(dc, whole);
+            for (int gather : {1, 0}) {
+                const FusedPlan p = make(MB, dc, gather);
+                if (!p.ok) continue;
+                max_bytes = std::max(max_bytes, p.bytes);
+                if (!best.ok || cost(p) < cost(best)) best = p;
+                if (forced && (force_rows == 0 || p.MB == force_rows) &&
+                    (force_dc == 0 || p.dc == force_dc) &&
+                    (force_x < 0 || p.nchunk == 1 || p.gather1 == force_x) &&
+                    (!best_forced.ok || cost(p) < cost(best_forced)))
+                    best_forced = p;
             }
-            if (pick(p)) return report(p);
         }
+    }
+    if (forced && !best_forced.ok && trace)
         std::fprintf(stderr, "atn: fused plan override not possible, default plan\n");
+    FusedPlan p = best_forced.ok ? best_forced : best;
+    if (!query_device && p.ok) p.bytes = max_bytes;
+    if (trace && p.ok)
+        std::fprintf(stderr, "atn: fused plan rows %d slice %d x %d %s, %d workgroups\n", p.MB,
+                     p.dc, p.nchunk, p.nchunk == 1 ? "none" : (p.gather1 ? "gather" : "rsag"),
+                     p.workgroups);
+    return p;
+}
+
+// Plans are cached per (device, dtype, encoding, shape), the size query's
+// under device -1; tuning overrides and tracing bypass the cache.
+std::map<std::tuple<int, int, int, int64_t, int64_t, int64_t, int64_t>, FusedPlan> g_fused_plans;
+
+FusedPlan fused_plan(int dtype, int pek, const Shape& s, bool query_device) {
+    int dev = -1;
+    if (query_device && hipGetDevice(&dev) != hipSuccess) return FusedPlan{};
+    if (std::getenv("ATN_FUSED_ROWS") || std::getenv("ATN_FUSED_DC") ||
+        std::getenv("ATN_FUSED_EXCHANGE") || std::getenv("ATN_FUSED_TRACE"))
+        return fused_plan_uncached(dtype, pek, s, query_device);
+    const auto key = std::make_tuple(dev, dtype, pek, (int64_t)s.BH, (int64_t)s.Lq,
+                                     (int64_t)s.Lk, (int64_t)s.D);
+    {
+        std::lock_guard<std::mutex> lk(g_mu);
+        const auto it = g_fused_plans.find(key);
+        if (it != g_fused_plans.end()) return it->second;
     }
-    // Estimated time in us beyond the fixed cost: each workgroup's Q, K and V
-    // slice loads (0.096 us per KiB), the exchange's waits and reads per
-    // slice (0.146 us) and reduce-scatter's second round trip (0.9 us);
-    // fitted to config-2-shaped fp32 runs (B=1, H=4, Lq=Lk=64, D 512-4096)
-    // on MI355X, where it ranks first the plan that measured fastest.
-    auto cost = [&](const FusedPlan& p) {
-        const double kib = (double)(std::min(p.MB, MQ) + 2 * NK) * p.dc *
-                           (dtype == ATN_DTYPE_F32 ? 4 : 2) / 1024.0;
-        return 0.096 * kib + 0.146 * p.nchunk + (p.nchunk > 1 && !p.gather1 ? 0.9 : 0.0);
-    };
-    FusedPlan best;
-    for (int MB : {64, 32, 16}) {
-        if (MB > MQ) continue;
-        const FusedPlan p = plan_rows(MB);
-        if (p.ok && 2 * p.workgroups >= std::min(cus, 2048) && (!best.ok || cost(p) < cost(best)))
-            best = p;
-    }
-    return report(best.ok ? best : plan_rows(MQ));
+    const FusedPlan p = fused_plan_uncached(dtype, pek, s, query_device);
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (g_fused_plans.size() >= 4096) g_fused_plans.clear();
+    g_fused_plans.emplace(key, p);
+    return p;
 }
 
 // ---------------------------------------------------------------- gemm plan

@@ -205,14 +205,15 @@ def test_fused_row_groups_and_exchanges(am, dev, monkeypatch, rows, exchange, sh
 
 @pytest.mark.parametrize("rows,exchange", [("64", "rsag"), ("", "")], ids=["rows64-rsag", "default"])
 def test_fused_uneven_slices(am, dev, monkeypatch, rows, exchange):
-    """36 heads with 7 D-slices each: with 64-row groups the reduce-scatter
-    owns 1171 entries per workgroup, so a thread reduces several entries
-    (4-byte words); by default the planner takes 32-row groups and the one
-    gather."""
+    """36 heads with 7 D-slices each: with 64-row groups and slices of 64 the
+    reduce-scatter owns 1171 entries per workgroup, so a thread reduces
+    several entries (4-byte words); by default the planner makes its own
+    choice."""
     import hip_rt
     if rows:
         monkeypatch.setenv("ATN_FUSED_ROWS", rows)
         monkeypatch.setenv("ATN_FUSED_EXCHANGE", exchange)
+        monkeypatch.setenv("ATN_FUSED_DC", "64")
     B, Hh, Lq, Lk, D = 1, 36, 64, 128, 448
     print(f"[case] fused uneven slices rows={rows or 'default'}", flush=True)
     assert am.path(0, B, Hh, Lq, Lk, D) == am.ATN_PATH_FUSED_SMALL
@@ -225,3 +226,32 @@ def test_fused_uneven_slices(am, dev, monkeypatch, rows, exchange):
     assert am.sync_status(ws, B, Hh) == 0
     n, mabs, mrel = H.check_f32(out.numpy(), oracle.attention(Q, K, V, nthreads=16))
     assert n == 0, f"{n} mismatches, max abs {mabs}, max rel {mrel}"
+
+
+@pytest.mark.parametrize("shape,dtype", [((1, 1, 16, 16, 8192), "f32"), ((1, 2, 32, 32, 4096), "f32"),
+                                         ((1, 1, 64, 64, 2048), "f32"), ((2, 4, 64, 64, 2048), "f32"),
+                                         ((1, 8, 64, 64, 1024), "f32"), ((1, 1, 32, 128, 8192), "bf16"),
+                                         ((1, 3, 48, 100, 3072), "bf16")],
+                         ids=lambda v: "x".join(map(str, v)) if isinstance(v, tuple) else v)
+def test_fused_planner_shapes(am, dev, shape, dtype):
+    """Shapes on which the planner's time estimate takes wide slices with few
+    workgroups (down to 32 for one head), several workgroups per CU, or the
+    whole padded head of 48 rows: the oracle's result on each."""
+    import hip_rt
+    B, Hh, Lq, Lk, D = shape
+    print(f"[case] fused planner shape {shape} {dtype}", flush=True)
+    dcode = 0 if dtype == "f32" else 1
+    assert am.path(dcode, B, Hh, Lq, Lk, D) == am.ATN_PATH_FUSED_SMALL
+    (q, k, v), (Q, K, V) = H.device_inputs((B, Hh, Lq, D), (B, Hh, Lk, D), 401 + D, dtype)
+    ws = _ws(am, dcode, B, Hh, Lq, Lk, D)
+    out = H.empty(Q.shape, dtype)
+    am.attention_ex(q, k, v, out, workspace=ws)
+    hip_rt.synchronize()
+    assert am.sync_status(ws, B, Hh) == 0
+    ref = oracle.attention(Q, K, V, nthreads=16)
+    if dtype == "f32":
+        n, mabs, mrel = H.check_f32(out.numpy(), ref)
+        assert n == 0, f"{n} mismatches, max abs {mabs}, max rel {mrel}"
+    else:
+        n, nrel, mabs = H.check_bf16(out.numpy(), ref)
+        assert n == 0, f"normwise rel {nrel}, max abs {mabs}"
