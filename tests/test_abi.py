@@ -129,6 +129,22 @@ def test_workspace_bytes(am):
     assert am.workspace_bytes(0, 1, 4, 64, 64, 2048, am.make_pe("rope", rotary_dim=3)) == 0
 
 
+@pytest.mark.parametrize("dtype,shape", [(0, (1, 4, 64, 64, 2048)), (0, (1, 16, 64, 64, 512)),
+                                         (0, (1, 1, 16, 16, 8192)), (1, (1, 4, 32, 128, 8192))])
+def test_workspace_bytes_bound_every_plan(am, monkeypatch, dtype, shape):
+    """The size query reports the largest workspace of every single-launch
+    plan it could take, so that a plan forced through the tuning overrides
+    (or chosen for a device of another capacity) never needs more."""
+    base = am.workspace_bytes(dtype, *shape)
+    assert base > 0
+    for rows, dc, x in [("16", "32", "gather"), ("16", "32", "rsag"), ("32", "64", "rsag"),
+                        ("64", "128", "rsag"), ("16", "256", "gather")]:
+        monkeypatch.setenv("ATN_FUSED_ROWS", rows)
+        monkeypatch.setenv("ATN_FUSED_DC", dc)
+        monkeypatch.setenv("ATN_FUSED_EXCHANGE", x)
+        assert am.workspace_bytes(dtype, *shape) == base, (rows, dc, x)
+
+
 def test_path_selection_without_device(am):
     """Short sequences take the single-launch kernel, long ones the pipeline."""
     assert am.path(0, 1, 4, 64, 64, 2048) == am.ATN_PATH_FUSED_SMALL       # config 2

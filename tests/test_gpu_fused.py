@@ -255,3 +255,23 @@ def test_fused_planner_shapes(am, dev, shape, dtype):
     else:
         n, nrel, mabs = H.check_bf16(out.numpy(), ref)
         assert n == 0, f"normwise rel {nrel}, max abs {mabs}"
+
+
+def test_fused_forced_plan_fits_default_workspace(am, dev, monkeypatch):
+    """A plan forced to narrow slices (16-row groups, 32-dim slices, 1024
+    workgroups, several per CU) runs in the workspace the size query reported
+    without overrides, and gives the oracle's result."""
+    import hip_rt
+    B, Hh, Lq, Lk, D = 1, 4, 64, 64, 2048
+    print("[case] fused forced narrow plan in the default workspace", flush=True)
+    (q, k, v), (Q, K, V) = H.device_inputs((B, Hh, Lq, D), (B, Hh, Lk, D), 613)
+    ws = _ws(am, 0, B, Hh, Lq, Lk, D)
+    monkeypatch.setenv("ATN_FUSED_ROWS", "16")
+    monkeypatch.setenv("ATN_FUSED_DC", "32")
+    monkeypatch.setenv("ATN_FUSED_EXCHANGE", "rsag")
+    out = H.empty(Q.shape)
+    am.attention_ex(q, k, v, out, workspace=ws)
+    hip_rt.synchronize()
+    assert am.sync_status(ws, B, Hh) == 0
+    n, mabs, mrel = H.check_f32(out.numpy(), oracle.attention(Q, K, V, nthreads=16))
+    assert n == 0, f"{n} mismatches, max abs {mabs}, max rel {mrel}"
