@@ -275,3 +275,40 @@ def test_fused_forced_plan_fits_default_workspace(am, dev, monkeypatch):
     assert am.sync_status(ws, B, Hh) == 0
     n, mabs, mrel = H.check_f32(out.numpy(), oracle.attention(Q, K, V, nthreads=16))
     assert n == 0, f"{n} mismatches, max abs {mabs}, max rel {mrel}"
+
+
+@pytest.mark.parametrize("shape,dtype,pe", [((1, 1, 32, 128, 8192), "bf16", "rope_half"),
+                                            ((1, 2, 32, 32, 4096), "f32", "sinusoidal"),
+                                            ((1, 1, 16, 16, 8192), "f32", "rope_inter"),
+                                            ((1, 1, 64, 64, 2048), "bf16", "sinusoidal")],
+                         ids=lambda v: "x".join(map(str, v)) if isinstance(v, tuple) else v)
+def test_fused_planner_shapes_with_encoding(am, dev, shape, dtype, pe):
+    """The few-workgroup, wide-slice plans with the positional encoding
+    applied to Q and K at load: the oracle's result."""
+    import hip_rt
+    B, Hh, Lq, Lk, D = shape
+    print(f"[case] fused planner shape {shape} {dtype} {pe}", flush=True)
+    dcode = 0 if dtype == "f32" else 1
+    desc = {"rope_half": am.make_pe("rope", pairing="half"), "rope_inter": am.make_pe("rope"),
+            "sinusoidal": am.make_pe("sinusoidal")}[pe]
+    assert am.path(dcode, B, Hh, Lq, Lk, D, desc) == am.ATN_PATH_FUSED_SMALL
+    sigma = 0.5 if pe == "sinusoidal" else 1.0
+    (q, k, v), (Q, K, V) = H.device_inputs((B, Hh, Lq, D), (B, Hh, Lk, D), 523 + D, dtype, sigma)
+    ws = _ws(am, dcode, B, Hh, Lq, Lk, D, desc)
+    out = H.empty(Q.shape, dtype)
+    am.attention_ex(q, k, v, out, pe=desc, workspace=ws)
+    hip_rt.synchronize()
+    assert am.sync_status(ws, B, Hh) == 0
+    if pe == "sinusoidal":
+        st, ct = oracle.sinusoidal_table(max(Lq, Lk), D)
+        ref = oracle.attention_sinusoidal(Q, K, V, st, ct, nthreads=16)
+    else:
+        c, s_ = oracle.rope_cache(max(Lq, Lk), D)
+        ref = oracle.attention_rope(Q, K, V, c, s_, nthreads=16,
+                                    pairing="half" if pe == "rope_half" else "interleaved")
+    if dtype == "f32":
+        n, mabs, mrel = H.check_f32(out.numpy(), ref)
+        assert n == 0, f"{n} mismatches, max abs {mabs}, max rel {mrel}"
+    else:
+        n, nrel, mabs = H.check_bf16(out.numpy(), ref)
+        assert n == 0, f"normwise rel {nrel}, max abs {mabs}"
