@@ -38,6 +38,7 @@ ATN_ERR_WORKSPACE = -8
 ATN_ERR_BAD_ARGUMENT = -9
 ATN_ERR_MISALIGNED = -10
 ATN_ERR_DEVICE_TIMEOUT = -11
+ATN_ERR_CAPTURE = -12
 
 ATN_DTYPE_F32 = 0
 ATN_DTYPE_BF16 = 1

@@ -136,6 +136,10 @@ struct Table16 {
 
 struct DeviceState {
     std::map<hipStream_t, Workspace> ws;
+    // Superseded library workspaces and tables.  Enqueued work, and HIP graphs
+    // captured from it, keep their device addresses, so they are never freed
+    // (they are released with the process).
+    std::vector<void*> retired;
     std::map<std::tuple<int, int, uint32_t>, Table> tables;  // (kind, dim, base bits)
     std::map<std::tuple<int, int, int, uint32_t>, Table16> tables16;  // (kind, D, rotary, base)
     int cus = 0;
@@ -154,6 +158,15 @@ int current_device(int* dev) {
     }
     ATN_HIP(hipGetDevice(dev));
     return ATN_OK;
+}
+
+// Library allocations (first use or growth of a workspace or table) are
+// synchronous and cannot be recorded into a graph: while `stream` is being
+// captured they are refused with ATN_ERR_CAPTURE.
+int refuse_if_capturing(hipStream_t stream) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    ATN_HIP(hipStreamIsCapturing(stream, &cs));
+    return cs == hipStreamCaptureStatusNone ? ATN_OK : ATN_ERR_CAPTURE;
 }
 
 // Host-side angle tables with the reference CPU path's float expressions
@@ -189,13 +202,16 @@ void build_sin_table(std::vector<float>& a, std::vector<float>& b, int npos, int
 
 // Returns the device tables for this encoding, building or growing them
 // (synchronously) when needed.  Caller holds g_mu.
-int get_table(DeviceState& ds, const PePlan& plan, int D, int npos, Table** out) {
+int get_table(DeviceState& ds, const PePlan& plan, int D, int npos, hipStream_t stream,
+              Table** out) {
     const bool rope = plan.pek != atn::kPeSinusoidal;
     uint32_t base_bits;
     std::memcpy(&base_bits, &plan.base, 4);
     const auto key = std::make_tuple(rope ? 1 : 2, rope ? plan.rotary : D, rope ? base_bits : 0u);
     Table& t = ds.tables[key];
     if (t.a == nullptr || t.npos < npos) {
+        const int st = refuse_if_capturing(stream);
+        if (st != ATN_OK) return st;
         const int want = npos < 64 ? 64 : npos;
         std::vector<float> a, b;
         int nf;
@@ -207,8 +223,8 @@ int get_table(DeviceState& ds, const PePlan& plan, int D, int npos, Table** out)
             nf = (D + 1) / 2;
         }
         if (t.a) {
-            ATN_HIP(hipFree(t.a));  // hipFree waits for in-flight work
-            ATN_HIP(hipFree(t.b));
+            ds.retired.push_back(t.a);
+            ds.retired.push_back(t.b);
             t.a = t.b = nullptr;
         }
         const size_t bytes = a.size() * sizeof(float);
@@ -236,13 +252,16 @@ uint16_t f16_bits(float x) {
 //   RoPE        [pos][D/2] words (cos, sin) of pair i < r/2, (1, 0) past the
 //               rotary width (a pass-through rotation)
 // Built (synchronously) when missing or too short; caller holds g_mu.
-int get_table16(DeviceState& ds, const PePlan& plan, int D, int npos, Table16** out) {
+int get_table16(DeviceState& ds, const PePlan& plan, int D, int npos, hipStream_t stream,
+                Table16** out) {
     const bool rope = plan.pek != atn::kPeSinusoidal;
     uint32_t base_bits;
     std::memcpy(&base_bits, &plan.base, 4);
     const auto key = std::make_tuple(rope ? 1 : 2, D, rope ? plan.rotary : D, rope ? base_bits : 0u);
     Table16& t = ds.tables16[key];
     if (t.p == nullptr || t.npos < npos) {
+        const int st = refuse_if_capturing(stream);
+        if (st != ATN_OK) return st;
         const int want = npos < 64 ? 64 : npos;
         std::vector<float> a, b;
         std::vector<uint16_t> h((size_t)want * D);
@@ -264,7 +283,7 @@ int get_table16(DeviceState& ds, const PePlan& plan, int D, int npos, Table16** 
                         f16_bits((d & 1) ? b[(size_t)pos * nf + d / 2] : a[(size_t)pos * nf + d / 2]);
         }
         if (t.p) {
-            ATN_HIP(hipFree(t.p));  // hipFree waits for in-flight work
+            ds.retired.push_back(t.p);
             t.p = nullptr;
         }
         ATN_HIP(hipMalloc(&t.p, h.size() * 2));
@@ -276,7 +295,7 @@ int get_table16(DeviceState& ds, const PePlan& plan, int D, int npos, Table16** 
 }
 
 // Fills the PeSide table pointers (library tables or the caller's).
-int bind_tables(const atn_pe_desc* pe, PePlan& plan, int D, int npos) {
+int bind_tables(const atn_pe_desc* pe, PePlan& plan, int D, int npos, hipStream_t stream) {
     if (plan.pek == atn::kPeNone) return ATN_OK;
     if (plan.caller_tables) {
         const bool rope = plan.pek != atn::kPeSinusoidal;
@@ -293,7 +312,7 @@ int bind_tables(const atn_pe_desc* pe, PePlan& plan, int D, int npos) {
     if (st != ATN_OK) return st;
     std::lock_guard<std::mutex> lk(g_mu);
     Table* t = nullptr;
-    st = get_table(g_dev[dev], plan, D, npos, &t);
+    st = get_table(g_dev[dev], plan, D, npos, stream, &t);
     if (st != ATN_OK) return st;
     for (atn::PeSide* s : {&plan.q, &plan.k}) {
         s->a = t->a;
@@ -337,10 +356,13 @@ int ensure_workspace(size_t bytes, hipStream_t stream, void** ws) {
     int st = current_device(&dev);
     if (st != ATN_OK) return st;
     std::lock_guard<std::mutex> lk(g_mu);
-    Workspace& w = g_dev[dev].ws[stream];
+    DeviceState& ds = g_dev[dev];
+    Workspace& w = ds.ws[stream];
     if (w.bytes < bytes) {
+        st = refuse_if_capturing(stream);
+        if (st != ATN_OK) return st;
         if (w.ptr) {
-            ATN_HIP(hipFree(w.ptr));  // waits for in-flight work using it
+            ds.retired.push_back(w.ptr);
             w.ptr = nullptr;
             w.bytes = 0;
         }
@@ -632,12 +654,11 @@ int attention_core(int dtype, const void* Q, const void* K, const void* V, void*
     PePlan plan;
     st = check_pe(pe, D, &plan);
     if (st != ATN_OK) return st;
-    const FusedPlan fp = fused_plan(dtype, plan.pek, s, false);
     const GemmPlan gp = gemm_plan(dtype, s, plan);
     const StreamPlan sp = stream_plan(s);
-    const size_t need_upper = std::max({fp.ok ? fp.bytes : (size_t)0,
-                                        gp.ok ? gp.bytes : (size_t)0, kSyncBytes + sp.bytes});
-    if (workspace != nullptr && workspace_bytes < need_upper) return ATN_ERR_WORKSPACE;
+    // every path needs at least the sync region; the path-specific size is
+    // checked once the device has chosen the path
+    if (workspace != nullptr && workspace_bytes < kSyncBytes) return ATN_ERR_WORKSPACE;
     const int64_t tiles = s.BH * ((Lq + 63) / 64) * ((Lk + 63) / 64) * sp.nsplit;
     const int64_t pv_tiles = s.BH * ((Lq + 63) / 64) * ((D + 63) / 64);
     if (tiles > (1LL << 24) || pv_tiles > (1LL << 24)) return ATN_ERR_SIZE_OVERFLOW;
@@ -645,7 +666,7 @@ int attention_core(int dtype, const void* Q, const void* K, const void* V, void*
     int dev;
     st = current_device(&dev);
     if (st != ATN_OK) return st;
-    st = bind_tables(pe, plan, D, Lq > Lk ? Lq : Lk);
+    st = bind_tables(pe, plan, D, Lq > Lk ? Lq : Lk, stream);
     if (st != ATN_OK) return st;
     // the device's own capacity decides between the single-launch kernel
     // and the three-kernel pipeline
@@ -660,7 +681,7 @@ int attention_core(int dtype, const void* Q, const void* K, const void* V, void*
         use_fused ? fd.bytes : (use_gemm ? gp.bytes : kSyncBytes + sp.bytes);
     void* ws = workspace;
     if (ws == nullptr) {
-        st = ensure_workspace(need_upper > need ? need_upper : need, stream, &ws);
+        st = ensure_workspace(need, stream, &ws);
         if (st != ATN_OK) return st;
     } else if (workspace_bytes < need) {
         return ATN_ERR_WORKSPACE;
@@ -691,7 +712,7 @@ int attention_core(int dtype, const void* Q, const void* K, const void* V, void*
                 if (gp.benc != atn::kGemmEncRaw) {
                     std::lock_guard<std::mutex> lk(g_mu);
                     Table16* t16 = nullptr;
-                    st = get_table16(g_dev[dev], plan, D, Lq > Lk ? Lq : Lk, &t16);
+                    st = get_table16(g_dev[dev], plan, D, Lq > Lk ? Lq : Lk, stream, &t16);
                     if (st != ATN_OK) return st;
                     tab = t16->p;
                     tab_rows = t16->npos;
@@ -752,7 +773,7 @@ int pe_apply_core(int dtype, const void* in, void* out, long n_rows, int seq_len
     int dev;
     st = current_device(&dev);
     if (st != ATN_OK) return st;
-    st = bind_tables(&d, plan, D, seq_len);
+    st = bind_tables(&d, plan, D, seq_len, stream);
     if (st != ATN_OK) return st;
     const size_t va = dtype == ATN_DTYPE_F32 ? 16 : 8;
     const int vec = (D % 4 == 0) && aligned(in, va) && aligned(out, va);
@@ -854,6 +875,7 @@ const char* atn_status_string(int status) {
         case ATN_ERR_BAD_ARGUMENT: return "bad argument";
         case ATN_ERR_MISALIGNED: return "pointer not aligned to its element size";
         case ATN_ERR_DEVICE_TIMEOUT: return "device-side wait timed out (outputs are NaN)";
+        case ATN_ERR_CAPTURE: return "library allocation needed while the stream is being captured";
         default: return "unknown status";
     }
 }
@@ -926,7 +948,7 @@ int atn_prepare_pe_ex(const atn_pe_desc* pe, int head_d, int max_positions) {
     int st = check_pe(pe, head_d, &plan);
     if (st != ATN_OK) return st;
     if (plan.pek == atn::kPeNone || plan.caller_tables) return ATN_OK;
-    return bind_tables(pe, plan, head_d, max_positions);
+    return bind_tables(pe, plan, head_d, max_positions, nullptr);
 }
 
 // ---- drop-ins ----

@@ -89,6 +89,13 @@ def copy_d2d(dst: "DeviceArray", src: "DeviceArray", nbytes: int) -> None:
     check(hip().hipMemcpy(_vp(dst.ptr), _vp(src.ptr), nbytes, D2D), "hipMemcpy D2D")
 
 
+def copy_d2d_async(dst: "DeviceArray", src: "DeviceArray", nbytes: int, stream: "Stream") -> None:
+    """Asynchronous device-to-device copy on `stream` (capturable into a graph)."""
+    assert nbytes <= min(dst.nbytes, src.nbytes)
+    check(hip().hipMemcpyAsync(_vp(dst.ptr), _vp(src.ptr), nbytes, D2D, _vp(stream.handle)),
+          "hipMemcpyAsync D2D")
+
+
 def synchronize() -> None:
     check(hip().hipDeviceSynchronize(), "hipDeviceSynchronize")
 

@@ -1,20 +1,26 @@
 """Benchmark of the large-head-dim fused attention hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 2] [--head-dim D]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config N] [--head-dim D]
 
 A "step" is one call of the hot path (atn_attention_fwd_ex, asynchronous,
 on one HIP stream) over one batch of synthetic input already resident in
-HBM.  The default workload is BASELINE config 2: fp32 SDPA, batch 1, 4
-heads, len_q = len_k = 64, head_dim 2048, Q/K/V iid N(0,1).  --config 3/4/5
-and --head-dim select the other BASELINE shapes for profiling; the default
-line is config 2.
+HBM.  The headline workload (`value`) is BASELINE config 2: fp32 SDPA,
+batch 1, 4 heads, len_q = len_k = 64, head_dim 2048, Q/K/V iid N(0,1).
+
+With no --config, the same line also carries `per_config`: configs 1, 3, 4
+and 5 and the config-2 head_dim sweep (512 / 4096 / 8192), each timed the
+same way, checked against the CPU oracle on sampled rows of the first, a
+middle and the last head, and with its own CPU baseline.  --config N (and
+--head-dim D) print one config's line only (for profiling).
 
 Printed: ONE JSON line.  `value` is the algorithmic HBM throughput
 (Q + K + V read once + O written once, bytes / second) of the whole job;
 TFLOP/s use 4*B*H*Lq*Lk*D.  `roofline` times the dominant kernel with HIP
 events on the stream it runs on; `cpu_baseline` times the CPU oracle (the
 restatement of the reference's single-threaded attention_cpu,
-final/attention.cu:228-283) on a bounded sample of the same workload.
+final/attention.cu:228-283, and its RoPE / sinusoidal siblings) on a bounded
+sample of the same workload.  The exit status is 1 when any sampled output
+misses its tolerance (fp32: abs > 1e-4 AND rel > 1e-4; bf16: rel 2e-2).
 """
 from __future__ import annotations
 
@@ -34,15 +40,16 @@ for sub in ("accelerated-final-project_amd", "oracle"):
 import numpy as np  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
-
-# HBM traffic per launch of the dominant kernel, measured with rocprofv3
-# FETCH_SIZE / WRITE_SIZE and scaled by a known-size device copy
-# (profiles/fused_small_cfg2_traffic.md).  Keyed by (config, head_dim).
-MEASURED_TRAFFIC_BYTES = {
-    (2, 2048): (14845 + 3081) * 1024,
-}
 BF16_PEAK_TFLOPS = 2500.0
 FP32_PEAK_TFLOPS = 157.3
+MALL_FLUSH_MIB = 512  # > the 256 MiB MALL: a copy this large evicts it
+
+# HBM traffic per launch of the dominant kernel, measured with rocprofv3
+# FETCH_SIZE / WRITE_SIZE and scaled by a known-size device copy; keyed by
+# (config, head_dim), with the profile that holds the counts.
+MEASURED_TRAFFIC = {
+    (2, 2048): ((14845 + 3081) * 1024, "profiles/fused_small_cfg2_traffic.md"),
+}
 
 # (name, dtype, B, H, Lq, Lk, D, pe, sigma)
 CONFIGS = {
@@ -54,6 +61,9 @@ CONFIGS = {
     5: ("cfg5 bf16 sinusoidal cross (4,16,256,2048,1024)", "bf16", 4, 16, 256, 2048, 1024,
         "sinusoidal", 0.5),
 }
+SWEEP_D = (512, 4096, 8192)
+
+F32_ABS, F32_REL, BF16_REL = 1e-4, 1e-4, 2e-2
 
 
 def parse():
@@ -61,10 +71,13 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--config", type=int, default=2, choices=sorted(CONFIGS))
+    ap.add_argument("--config", type=int, default=0, choices=[0] + sorted(CONFIGS),
+                    help="one config only (0 = headline config 2 plus every other config)")
     ap.add_argument("--head-dim", type=int, default=0, help="override D (config-2 sweep)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
-                    help="target CPU-oracle sample time (0 = skip)")
+                    help="CPU-oracle sample time of the headline (0 = skip every CPU baseline)")
+    ap.add_argument("--cpu-seconds-other", type=float, default=3.0,
+                    help="CPU-oracle sample time of each per_config entry")
     ap.add_argument("--seed", type=int, default=2)
     ap.add_argument("--calib-copy", type=int, default=0, metavar="MIB",
                     help="also run 5 device-to-device copies of MIB MiB (the HIP runtime's "
@@ -72,17 +85,45 @@ def parse():
     return ap.parse_args()
 
 
+def host_info():
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except AttributeError:
+        usable = os.cpu_count()
+    libc = platform.libc_ver()
+    return {"cpu_model": model or platform.processor() or platform.machine(),
+            "nproc_usable": usable, "cpu_count": os.cpu_count(),
+            "glibc": f"{libc[0]} {libc[1]}".strip()}
+
+
 def make_inputs(dtype, B, H, Lq, Lk, D, sigma, seed):
     """Seeded N(0, sigma) inputs generated on the host with numpy PCG64,
-    uploaded once (they stay resident for every step)."""
+    uploaded once (they stay resident for every step).  Returns the device
+    arrays and float32 host copies of exactly the values the kernel sees."""
     import hip_rt
     rng = np.random.default_rng(seed)
     dev, host = [], []
     for shape in ((B, H, Lq, D), (B, H, Lk, D), (B, H, Lk, D)):
-        x = rng.standard_normal(shape, dtype=np.float32) * np.float32(sigma)
-        d = hip_rt.DeviceArray.from_numpy(x, dtype)
+        x = rng.standard_normal(shape, dtype=np.float32)
+        if sigma != 1.0:
+            x *= np.float32(sigma)
+        if dtype == "f32":
+            d = hip_rt.DeviceArray.from_numpy(x, "f32")
+        else:
+            bits = hip_rt.f32_to_bf16_bits(x)
+            d = hip_rt.DeviceArray.from_numpy(bits, "bf16")
+            x = hip_rt.bf16_bits_to_f32(bits)
         dev.append(d)
-        host.append(x if dtype == "f32" else hip_rt.bf16_bits_to_f32(hip_rt.f32_to_bf16_bits(x)))
+        host.append(x)
     return dev, host
 
 
@@ -96,71 +137,127 @@ def pe_desc(am, pe):
     raise ValueError(pe)
 
 
+def oracle_rows(cfg, host, bh, r0, r1, nthreads=1):
+    """CPU oracle output rows [r0, r1) of head bh (flattened b*H + h) as
+    float32 [r1 - r0, D].  Only that head's Q, K, V are handed over, so the
+    positions (row index within the head) are those of the full tensors."""
+    import oracle
+    _, _, B, H, Lq, Lk, D, pe, _ = cfg
+    b, h = divmod(bh, H)
+    Q, K, V = (np.ascontiguousarray(t[b:b + 1, h:h + 1]) for t in host)
+    rows = (r0, r1)
+    if pe == "none":
+        out = oracle.attention(Q, K, V, rows=rows, nthreads=nthreads)
+    elif pe == "rope_half":
+        c, s = oracle.rope_cache(max(Lq, Lk), D)
+        out = oracle.attention_rope(Q, K, V, c, s, pairing="half", rows=rows, nthreads=nthreads)
+    else:
+        st, ct = oracle.sinusoidal_table(max(Lq, Lk), D)
+        out = oracle.attention_sinusoidal(Q, K, V, st, ct, rows=rows, nthreads=nthreads)
+    return out.reshape(Lq, D)[r0:r1]
+
+
+def sampled_check(cfg, host, got_rows_fn):
+    """Sampled-row parity: rows of the first, a middle and the last head --
+    the first 4, 4 from the middle and the last 8 rows of each (the last row
+    tile included) -- against the CPU oracle.  Returns a summary dict."""
+    name, dtype, B, H, Lq, Lk, D, pe, _ = cfg
+    BH = B * H
+    heads = sorted({0, BH // 2, BH - 1})
+    spans = sorted({(0, min(4, Lq)), (Lq // 2, min(Lq, Lq // 2 + 4)), (max(0, Lq - 8), Lq)})
+    nfail, maxabs, num, den, nrows = 0, 0.0, 0.0, 0.0, 0
+    worst_el = 0.0
+    for bh in heads:
+        for r0, r1 in spans:
+            if r1 <= r0:
+                continue
+            ref = oracle_rows(cfg, host, bh, r0, r1, nthreads=8).astype(np.float64)
+            got = got_rows_fn(bh, r0, r1).astype(np.float64)
+            err = np.abs(got - ref)
+            maxabs = max(maxabs, float(err.max()))
+            nrows += r1 - r0
+            if dtype == "f32":
+                bad = (err > F32_ABS) & (err / (np.abs(ref) + 1e-8) > F32_REL)
+            else:
+                rms = float(np.sqrt(np.mean(ref * ref)))
+                bad = (err > BF16_REL * np.abs(ref)) & (err > BF16_REL * rms)
+                worst_el = max(worst_el, float((err / max(rms, 1e-30)).max()))
+                num += float(np.sum(err * err))
+                den += float(np.sum(ref * ref))
+            nfail += int(bad.sum()) + int((~np.isfinite(got)).sum())
+    out = {"rows_checked": nrows, "heads_checked": heads, "max_abs": maxabs, "fails": nfail}
+    if dtype == "f32":
+        out["bar"] = "abs > 1e-4 AND rel > 1e-4 fails (vs the fp32 oracle)"
+        out["ok"] = nfail == 0
+    else:
+        nrel = (num ** 0.5) / max(den ** 0.5, 1e-30)
+        out["normwise_rel"] = nrel
+        out["bar"] = ("err > 2e-2*|ref| AND err > 2e-2*rms(ref) fails; normwise <= 2e-2 "
+                      "(vs the fp32 oracle on the bf16-rounded inputs)")
+        out["ok"] = nfail == 0 and nrel <= BF16_REL
+    return out
+
+
 def cpu_baseline(cfg, host, target_s):
     """Single-threaded CPU oracle on a bounded row sample of the workload;
-    returns (value in GB/s of the same algorithmic bytes, sample text)."""
-    import oracle
+    returns (value in GB/s of the same algorithmic bytes, sample text).
+    Rows are taken head by head (the RoPE / sinusoidal oracles encode a
+    head's K once per head, as the reference's CPU paths do)."""
     name, dtype, B, H, Lq, Lk, D, pe, _ = cfg
-    Q, K, V = host
     rows_total = B * H * Lq
     es = 4 if dtype == "f32" else 2
+    alg_bytes = (2 * B * H * Lq * D + 2 * B * H * Lk * D) * es
 
-    def run(rows):
-        if pe == "none":
-            return oracle.attention(Q, K, V, rows=rows)
-        if pe == "rope_half":
-            c, s = oracle.rope_cache(max(Lq, Lk), D)
-            return oracle.attention_rope(Q, K, V, c, s, pairing="half", rows=rows)
-        st, ct = oracle.sinusoidal_table(max(Lq, Lk), D)
-        return oracle.attention_sinusoidal(Q, K, V, st, ct, rows=rows)
+    def run_head_rows(bh, n):
+        oracle_rows(cfg, host, bh, 0, n, nthreads=1)
 
-    # per-row cost estimate from one row, then a sample of whole rows
+    # cost of one head's first row (includes the per-head encoding of K)
     t0 = time.perf_counter()
-    run((0, 1))
+    run_head_rows(0, 1)
     t1 = max(time.perf_counter() - t0, 1e-6)
-    nrows = int(max(1, min(rows_total, target_s / t1)))
-    reps = 1
-    t0 = time.perf_counter()
-    run((0, nrows))
-    el = time.perf_counter() - t0
-    if nrows == rows_total:
-        # whole workload is cheap: repeat it until the target time
-        reps = int(max(1, target_s / max(el, 1e-6)))
+    if t1 * Lq <= target_s:
+        # whole heads, as many as fit the target (all of them if cheap)
         t0 = time.perf_counter()
-        for _ in range(reps):
-            run((0, nrows))
+        run_head_rows(0, Lq)
+        th = max(time.perf_counter() - t0, 1e-6)
+        nheads = int(max(1, min(B * H, target_s / th)))
+        reps = 1
+        t0 = time.perf_counter()
+        for bh in range(nheads):
+            run_head_rows(bh, Lq)
+        el = time.perf_counter() - t0
+        if nheads == B * H:
+            reps = int(max(1, target_s / max(el, 1e-6)))
+            if reps > 1:
+                t0 = time.perf_counter()
+                for _ in range(reps):
+                    for bh in range(nheads):
+                        run_head_rows(bh, Lq)
+                el = time.perf_counter() - t0
+        nrows = nheads * Lq
+    else:
+        # part of one head
+        nrows = int(max(1, min(Lq, target_s / t1)))
+        reps = 1
+        t0 = time.perf_counter()
+        run_head_rows(0, nrows)
         el = time.perf_counter() - t0
     frac = nrows / rows_total
-    alg_bytes = (2 * B * H * Lq * D + 2 * B * H * Lk * D) * es
     sec_per_job = el / reps / frac
     sample = (f"{nrows}/{rows_total} query rows x {reps} rep(s) of {name}, single thread; "
               f"{el:.2f} s measured, whole job = {sec_per_job * 1e3:.2f} ms"
-              + (" (extrapolated linearly)" if frac < 1 else ""))
-    return alg_bytes / sec_per_job / 1e9, sample
+              + (" (extrapolated linearly from the sample)" if frac < 1 else ""))
+    return alg_bytes / sec_per_job / 1e9, sec_per_job * 1e3, sample
 
 
-def main():
-    a = parse()
-    if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py: this build measures one GPU only (the hot path is per-GPU; heads "
-              "shard across GPUs with no exchange); run with --gpus 1", file=sys.stderr)
-        sys.exit(2)
-    import attn_mi355x as am
-    import hip_rt
-
-    am.lib()
-    if hip_rt.device_count() < 1:
-        print("bench.py: no HIP device visible", file=sys.stderr)
-        sys.exit(1)
-    cfg = list(CONFIGS[a.config])
-    if a.head_dim:
-        cfg[6] = a.head_dim
-        cfg[0] = cfg[0].split(" (")[0] + f" ({cfg[2]},{cfg[3]},{cfg[4]},{cfg[5]},{cfg[6]})"
+def run_config(am, hip_rt, cfg, steps, warmup, seed, cold):
+    """Times one config: `steps` calls captured as one HIP graph and replayed
+    (HIP events on the call's stream), and, with `cold`, the same with the
+    256 MiB MALL flushed before every call (a 512 MiB device copy; the
+    copies' own time, measured alone, is subtracted).  Returns the timing
+    dict, the host inputs and a row reader of the final output."""
     name, dtype, B, H, Lq, Lk, D, pe, sigma = cfg
-    print(f"[bench] {name} steps={a.steps} warmup={a.warmup} device={hip_rt.device_name(0)}",
-          file=sys.stderr, flush=True)
-
-    (q, k, v), host = make_inputs(dtype, B, H, Lq, Lk, D, sigma, a.seed)
+    (q, k, v), host = make_inputs(dtype, B, H, Lq, Lk, D, sigma, seed)
     out = hip_rt.DeviceArray((B, H, Lq, D), dtype)
     desc = pe_desc(am, pe)
     dcode = am.ATN_DTYPE_F32 if dtype == "f32" else am.ATN_DTYPE_BF16
@@ -176,38 +273,108 @@ def main():
     def step():
         am.attention_ex(q, k, v, out, pe=desc, workspace=ws, stream=stream)
 
-    for _ in range(a.warmup):
+    for _ in range(warmup):
         step()
     hip_rt.synchronize()
 
-    # eager: one Python-driven call per step (host-bound for small shapes)
     e0, e1 = hip_rt.Event(), hip_rt.Event()
+    # eager: one Python-driven call per step (host-bound for small shapes)
     e0.record(stream)
-    for _ in range(a.steps):
+    for _ in range(steps):
         step()
     e1.record(stream)
     e1.synchronize()
-    eager_ms = e0.elapsed_ms(e1) / a.steps
+    eager_ms = e0.elapsed_ms(e1) / steps
+
+    def timed_graph(fn):
+        g = hip_rt.Graph(stream, fn)
+        g.launch()  # warm replay
+        stream.synchronize()
+        hip_rt.synchronize()
+        t0 = time.perf_counter()
+        e0.record(stream)
+        g.launch()
+        e1.record(stream)
+        e1.synchronize()
+        wall = time.perf_counter() - t0
+        g.destroy()
+        return e0.elapsed_ms(e1), wall
 
     # timed region: the K steps captured once as a HIP graph and replayed,
     # so the GPU runs them back to back with no host work in between
-    graph = hip_rt.Graph(stream, lambda: [step() for _ in range(a.steps)])
-    graph.launch()  # warm replay
-    stream.synchronize()
-    hip_rt.synchronize()
-    t0 = time.perf_counter()
-    e0.record(stream)
-    graph.launch()
-    e1.record(stream)
-    e1.synchronize()
-    hip_rt.synchronize()
-    wall = time.perf_counter() - t0
-    ev_ms = e0.elapsed_ms(e1)
-    graph.destroy()
+    ev_ms, wall = timed_graph(lambda: [step() for _ in range(steps)])
     st = am.lib().atn_sync_status_ex(ws.ptr, B, H, stream.handle)
     if st != 0:
-        raise am.AtnError(st, "device status after the timed region")
-    path = am.path(dcode, B, H, Lq, Lk, D, desc)
+        raise am.AtnError(st, f"device status after the timed region ({name})")
+    res = {"ms_per_step": ev_ms / steps, "eager_ms": eager_ms, "wall_s": wall,
+           "path": am.path(dcode, B, H, Lq, Lk, D, desc)}
+    if cold:
+        n = MALL_FLUSH_MIB << 20
+        src = hip_rt.DeviceArray((n // 4,), "f32", fill=0)
+        dst = hip_rt.DeviceArray((n // 4,), "f32")
+        flush_ms, _ = timed_graph(lambda: [hip_rt.copy_d2d_async(dst, src, n, stream)
+                                           for _ in range(steps)])
+        both_ms, _ = timed_graph(lambda: [(hip_rt.copy_d2d_async(dst, src, n, stream), step())
+                                          for _ in range(steps)])
+        st = am.lib().atn_sync_status_ex(ws.ptr, B, H, stream.handle)
+        if st != 0:
+            raise am.AtnError(st, f"device status after the cold run ({name})")
+        res["cold_ms_per_step"] = max(both_ms - flush_ms, 0.0) / steps
+        src.free()
+        dst.free()
+    hip_rt.synchronize()
+    bits = out.numpy()
+
+    def rows_fn(bh, r0, r1):
+        return bits.reshape(B * H, Lq, D)[bh, r0:r1]
+
+    stream.destroy()
+    for t in (q, k, v, out, ws):
+        t.free()
+    return res, host, rows_fn
+
+
+def summarize(cfg, res):
+    name, dtype, B, H, Lq, Lk, D, pe, _ = cfg
+    es = 4 if dtype == "f32" else 2
+    alg_bytes = (2 * B * H * Lq * D + 2 * B * H * Lk * D) * es
+    flops = 4 * B * H * Lq * Lk * D
+    ms = res["ms_per_step"]
+    gbs = alg_bytes / (ms * 1e-3) / 1e9
+    tflops = flops / (ms * 1e-3) / 1e12
+    bound = "hbm" if flops / alg_bytes < (312 if dtype == "bf16" else 19.7) else "mfma"
+    if bound == "hbm":
+        frac = gbs / HBM_PEAK_GBS
+    else:
+        frac = tflops / (BF16_PEAK_TFLOPS if dtype == "bf16" else FP32_PEAK_TFLOPS)
+    return alg_bytes, flops, gbs, tflops, bound, frac
+
+
+def main():
+    a = parse()
+    if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py: this build measures one GPU only (the hot path is per-GPU; heads "
+              "shard across GPUs with no exchange); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    import attn_mi355x as am
+    import hip_rt
+
+    am.lib()
+    if hip_rt.device_count() < 1:
+        print("bench.py: no HIP device visible", file=sys.stderr)
+        sys.exit(1)
+    head_cfg_id = a.config or 2
+    cfg = list(CONFIGS[head_cfg_id])
+    if a.head_dim:
+        cfg[6] = a.head_dim
+        cfg[0] = cfg[0].split(" (")[0] + f" ({cfg[2]},{cfg[3]},{cfg[4]},{cfg[5]},{cfg[6]})"
+    cfg = tuple(cfg)
+    name, dtype, B, H, Lq, Lk, D, pe, sigma = cfg
+    print(f"[bench] {name} steps={a.steps} warmup={a.warmup} device={hip_rt.device_name(0)}",
+          file=sys.stderr, flush=True)
+
+    res, host, rows_fn = run_config(am, hip_rt, cfg, a.steps, a.warmup, a.seed,
+                                    cold=head_cfg_id <= 3)
     if a.calib_copy > 0:
         n = a.calib_copy << 20
         src, dst = hip_rt.DeviceArray((n // 4,), "f32", fill=0), hip_rt.DeviceArray((n // 4,), "f32")
@@ -215,56 +382,76 @@ def main():
             hip_rt.copy_d2d(dst, src, n)
         hip_rt.synchronize()
         print(f"[bench] calibration: 5 device copies of {a.calib_copy} MiB", file=sys.stderr)
+    check = sampled_check(cfg, host, rows_fn)
+    alg_bytes, flops, gbs, tflops, bound, frac = summarize(cfg, res)
+    ms = res["ms_per_step"]
 
-    es = 4 if dtype == "f32" else 2
-    alg_bytes = (2 * B * H * Lq * D + 2 * B * H * Lk * D) * es
-    flops = 4 * B * H * Lq * Lk * D
-    ms = ev_ms / a.steps
-    gbs = alg_bytes / (ms * 1e-3) / 1e9
-    tflops = flops / (ms * 1e-3) / 1e12
-
-    # sanity: the last output against the oracle on a few rows
-    import oracle
-    ref_rows = (0, min(4, B * H * Lq))
-    got = out.numpy().reshape(-1, D)[ref_rows[0]:ref_rows[1]]
-    if pe == "none":
-        ref = oracle.attention(*host, rows=ref_rows)
-    elif pe == "rope_half":
-        c, s = oracle.rope_cache(max(Lq, Lk), D)
-        ref = oracle.attention_rope(*host, c, s, pairing="half", rows=ref_rows)
-    else:
-        st_, ct_ = oracle.sinusoidal_table(max(Lq, Lk), D)
-        ref = oracle.attention_sinusoidal(*host, st_, ct_, rows=ref_rows)
-    ref = ref.reshape(-1, D)[ref_rows[0]:ref_rows[1]]
-    err = float(np.max(np.abs(got - ref)))
-
-    bound = "hbm" if flops / alg_bytes < (312 if dtype == "bf16" else 19.7) else "mfma"
-    traffic = MEASURED_TRAFFIC_BYTES.get((a.config, D))
+    traffic, traffic_src = MEASURED_TRAFFIC.get((head_cfg_id, D), (None, None))
     if bound == "hbm":
         roof = {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic}
+                "frac": round(frac, 4), "traffic": traffic}
     else:
         peak = BF16_PEAK_TFLOPS if dtype == "bf16" else FP32_PEAK_TFLOPS
         roof = {"bound": "mfma", "achieved": round(tflops, 2), "peak": peak, "unit": "TFLOP/s",
-                "frac": round(tflops / peak, 4), "traffic": traffic}
+                "frac": round(frac, 4), "traffic": traffic}
+    path = res["path"]
     roof["kernel"] = {
         am.ATN_PATH_FUSED_SMALL: "k_fused_small (one launch per step)",
         am.ATN_PATH_SPLIT_D: "split-D pipeline (k_qk_partial + k_softmax + k_pv per step)",
-        am.ATN_PATH_GEMM: ("GEMM path (encode, QK^T GEMM with exp epilogue, k_rowscale, PV GEMM "
-                           "per step; whole-step figure, per-kernel split in profiles/)"),
+        am.ATN_PATH_GEMM: ("GEMM path (encode, QK^T GEMM with exp epilogue, PV GEMM per step; "
+                           "whole-step figure, per-kernel split in profiles/)"),
     }.get(path, "unknown")
     roof["timing"] = "HIP events around one graph replay of all timed steps, on its stream"
     if traffic is not None:
         roof["traffic_note"] = ("bytes per launch from rocprofv3 FETCH_SIZE + WRITE_SIZE scaled by "
-                                "a known-size device copy (profiles/fused_small_cfg2_traffic.md); "
-                                "measured for this build's kernel")
+                                f"a known-size device copy ({traffic_src})")
 
+    hinfo = host_info()
     cpu = None
     if a.cpu_seconds > 0:
-        v_cpu, sample = cpu_baseline(cfg, host, a.cpu_seconds)
+        v_cpu, job_ms, sample = cpu_baseline(cfg, host, a.cpu_seconds)
         cpu = {"value": round(v_cpu, 4), "unit": "GB/s", "cores": 1, "kind": "port",
-               "sample": sample, "host": platform.processor() or platform.machine()}
+               "job_ms": round(job_ms, 3), "sample": sample, "host": hinfo}
+    del host
 
+    all_ok = check["ok"]
+    per_config = None
+    if a.config == 0:
+        per_config = {}
+        others = [(f"cfg2_D{d}", 2, d) for d in SWEEP_D] + [(f"cfg{c}", c, 0) for c in (1, 3, 4, 5)]
+        for key, cid, dov in others:
+            c = list(CONFIGS[cid])
+            if dov:
+                c[6] = dov
+                c[0] = c[0].split(" (")[0] + f" ({c[2]},{c[3]},{c[4]},{c[5]},{c[6]})"
+            c = tuple(c)
+            print(f"[bench] per_config {key}: {c[0]}", file=sys.stderr, flush=True)
+            r, h, rf = run_config(am, hip_rt, c, a.steps, a.warmup, a.seed, cold=cid <= 3)
+            chk = sampled_check(c, h, rf)
+            ab, fl, g, tf, bd, fr = summarize(c, r)
+            ent = {"workload": c[0], "dtype": c[1], "pe": c[7], "ms_per_step": round(r["ms_per_step"], 6),
+                   "tflops": round(tf, 3), "gbs": round(g, 2), "roofline_bound": bd,
+                   "roofline_frac": round(fr, 4), "alg_bytes": ab, "flops": fl,
+                   "check": chk}
+            if "cold_ms_per_step" in r:
+                ent["cold_ms_per_step"] = round(r["cold_ms_per_step"], 6)
+            if a.cpu_seconds > 0:
+                v_cpu, job_ms, sample = cpu_baseline(c, h, a.cpu_seconds_other)
+                ent["cpu_baseline"] = {"value": round(v_cpu, 4), "unit": "GB/s", "cores": 1,
+                                       "kind": "port", "job_ms": round(job_ms, 3),
+                                       "sample": sample,
+                                       "gpu_speedup": round(job_ms / r["ms_per_step"], 1)}
+            per_config[key] = ent
+            all_ok = all_ok and chk["ok"]
+            del h
+
+    cfg_out = {"workload": name, "batch": B, "heads": H, "len_q": Lq, "len_k": Lk,
+               "head_dim": D, "pe": pe, "alg_bytes": alg_bytes, "flops": flops,
+               "check": check}
+    if "cold_ms_per_step" in res:
+        cfg_out["cold_ms_per_step"] = round(res["cold_ms_per_step"], 6)
+        cfg_out["cold_note"] = (f"MALL flushed by a {MALL_FLUSH_MIB} MiB device copy before every "
+                                "step; the copies' own time is subtracted")
     line = {
         "metric": "attention ms + TFLOPS + HBM GB/s (% roofline) at hdim 512-8192, 1 GPU",
         "value": round(gbs, 2),
@@ -273,22 +460,28 @@ def main():
         "steps": a.steps,
         "warmup": a.warmup,
         "ms_per_step": round(ms, 6),
-        "ms_per_step_eager_python": round(eager_ms, 6),
+        "ms_per_step_eager_python": round(res["eager_ms"], 6),
         "tflops": round(tflops, 4),
         "pct_hbm_roofline": round(100 * gbs / HBM_PEAK_GBS, 2),
-        "wall_s": round(wall, 4),
+        "wall_s": round(res["wall_s"], 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32" if dtype == "f32" else "bf16 storage, f32 math",
         "data": "synthetic N(0,%g), numpy PCG64 seed %d, resident in HBM" % (sigma, a.seed),
-        "config": {"workload": name, "batch": B, "heads": H, "len_q": Lq, "len_k": Lk,
-                   "head_dim": D, "pe": pe, "alg_bytes": alg_bytes, "flops": flops,
-                   "check_max_abs_vs_oracle": err},
+        "config": cfg_out,
         "roofline": roof,
         "cpu_baseline": cpu,
+        "host": hinfo,
+        "parity_ok": all_ok,
     }
+    if per_config is not None:
+        line["per_config"] = per_config
     print(json.dumps(line), flush=True)
+    if not all_ok:
+        print("bench.py: a sampled output missed its tolerance (see check / per_config.*.check)",
+              file=sys.stderr)
+        sys.exit(1)
 
 
 if __name__ == "__main__":

@@ -50,6 +50,7 @@ typedef uint16_t atn_bf16;
 #define ATN_ERR_BAD_ARGUMENT (-9)   /* enum out of range, bad table size ... */
 #define ATN_ERR_MISALIGNED (-10)    /* pointer not aligned to its element size */
 #define ATN_ERR_DEVICE_TIMEOUT (-11) /* a kernel's bounded cross-workgroup wait expired */
+#define ATN_ERR_CAPTURE (-12)        /* a library allocation was needed during graph capture */
 
 /* Text for a status code (static storage). */
 const char *atn_status_string(int status);
@@ -210,7 +211,12 @@ void precompute_sinusoidal_table(float *sin_table, float *cos_table, int seqlen,
  * must not be re-initialized while in use).  Calls that run at the same
  * time must not share a workspace.  Enqueued on stream; asynchronous; the
  * enqueued work may be captured into a HIP graph and replayed (the kernel
- * arguments of a call do not depend on earlier calls).
+ * arguments of a call do not depend on earlier calls, and library memory a
+ * call has used is never freed).  A call that needs a library allocation
+ * (the first call on a stream with workspace == NULL, a larger shape, or the
+ * first use of an encoding's tables) returns ATN_ERR_CAPTURE while its
+ * stream is being captured: make one uncaptured call of the shape first, or
+ * pass a workspace and call atn_prepare_pe_ex beforehand.
  * Shapes with len_q <= 64 and len_k <= 128 run as one kernel whose
  * workgroups meet at bounded device-side barriers; if such a wait ever
  * expires the outputs of that call are NaN and atn_sync_status_ex reports

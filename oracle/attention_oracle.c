@@ -34,6 +34,10 @@
  *   oracle_sinusoidal_table,
  *   oracle_attention_sinusoidal  PE(pos 0) = [0,1,0,1,...], linearity
  *                             attn_sin(Q,K,V) == attn(Q+PE, K+PE, V).
+ *   oracle_rope_freqs,
+ *   oracle_sinusoidal_freqs   float64 1/base^(2i/r) and 1/1e4^(2(d/2)/D),
+ *                             and the pinned tables' position-1 rows hold
+ *                             cos/sin of exactly these frequencies.
  */
 #include <math.h>
 #include <stddef.h>

@@ -201,6 +201,45 @@ def test_rope_cache_matches_float64_math(npos, r):
         assert np.all(np.abs(tab[:, 0::2] - fn(th)) <= tol)
 
 
+@pytest.mark.parametrize("r,base", [(8, 10000.0), (128, 10000.0), (4096, 10000.0), (64, 500.0)])
+def test_rope_freqs_match_float64_and_cache(r, base):
+    """oracle_rope_freqs (final/rope.cu:96-98, :132-134): freq_i =
+    1/base^(2i/r) within float32 rounding of powf and the division, and at
+    position 1 the (separately pinned) cache holds exactly cos/sin of these
+    frequencies, since theta = 1 * freq_i."""
+    f = oracle.rope_freqs(r, base)
+    exact = 1.0 / base ** (2.0 * np.arange(r // 2, dtype=np.float64) / r)
+    assert f.shape == (r // 2,) and f[0] == 1.0
+    assert np.all(np.abs(f / exact - 1.0) <= 4e-7)
+    c, s = oracle.rope_cache(2, r, base)
+    f64 = f.astype(np.float64)
+    assert np.all(np.abs(c[1, 0::2] - np.cos(f64)) <= 1.2e-7)
+    assert np.all(np.abs(s[1, 0::2] - np.sin(f64)) <= 1.2e-7)
+    # a frequency table off by one pair index (the exponent of pair i + 1)
+    # fails the float64 check
+    shifted = 1.0 / base ** (2.0 * (np.arange(r // 2, dtype=np.float64) + 1) / r)
+    assert not np.all(np.abs(f / shifted - 1.0) <= 4e-7)
+
+
+@pytest.mark.parametrize("D", [8, 7, 1024, 8192])
+def test_sinusoidal_freqs_match_float64_and_table(D):
+    """oracle_sinusoidal_freqs (final/sinusoidal.cu:112-114): freq[d] =
+    1/1e4^(2*(d//2)/D), equal on each (even, odd) pair, and at position 1 the
+    (separately pinned) table holds sin (even d) / cos (odd d) of them."""
+    f = oracle.sinusoidal_freqs(D)
+    d = np.arange(D)
+    exact = 1.0 / 10000.0 ** (2.0 * (d // 2) / D)
+    assert np.all(np.abs(f / exact - 1.0) <= 4e-7)
+    assert np.array_equal(f[0:D - 1:2], f[1:D:2])
+    st, ct = oracle.sinusoidal_table(2, D)
+    f64 = f.astype(np.float64)
+    assert np.all(np.abs(st[1] - np.sin(f64)) <= 1.2e-7)
+    assert np.all(np.abs(ct[1] - np.cos(f64)) <= 1.2e-7)
+    # using d instead of d // 2 in the exponent fails the float64 check
+    wrong = 1.0 / 10000.0 ** (2.0 * d / D)
+    assert D < 3 or not np.all(np.abs(f / wrong - 1.0) <= 4e-7)
+
+
 def test_rope_planted_swap_fails_table_check():
     oracle.set_mutation(2)
     c, _ = oracle.rope_cache(16, 8)
