@@ -143,7 +143,7 @@ struct DeviceState {
     std::map<std::tuple<int, int, uint32_t>, Table> tables;  // (kind, dim, base bits)
     std::map<std::tuple<int, int, int, uint32_t>, Table16> tables16;  // (kind, D, rotary, base)
     int cus = 0;
-    std::map<std::pair<int, int>, int> fused_cap;  // (dtype, LDS bytes) -> resident workgroups
+    std::map<std::pair<int, int>, int> fused_per_cu;  // (dtype, LDS bytes) -> workgroups per CU
 };
 
 std::mutex g_mu;
@@ -375,21 +375,25 @@ int ensure_workspace(size_t bytes, hipStream_t stream, void** ws) {
 }
 
 // ---------------------------------------------------------------- fused plan
-// Workspace layout (every path): a fixed 32 KiB sync region -- [0, 4) the
+// Workspace layout (every path): a fixed 40 KiB sync region -- [0, 4) the
 // status word, [256, 8448) one epoch word per row group of the
 // single-launch kernel, [8448, 24832) two sets of 2048 per-workgroup done
-// words -- then scratch.  Fixed offsets keep the epoch words of one call
+// words, [32768, 40960) the XCD-local arrival counters (1 KiB per XCD) --
+// then scratch.  Fixed offsets keep the epoch words and counters of one call
 // from landing elsewhere when shapes change between calls.
 constexpr size_t kSyncEpochOff = 256;
 constexpr size_t kSyncDoneOff = 8448;
+constexpr size_t kSyncXcdOff = 32768;
 constexpr int kSyncMaxWorkgroups = 2048;
-constexpr size_t kSyncBytes = 32768;
+constexpr size_t kSyncBytes = 40960;
+static_assert(kSyncXcdOff + 8 * atn::kXcdCtrWords * 4 <= kSyncBytes, "sync region");
 
 size_t round256(size_t b) { return (b + 255) / 256 * 256; }
 
 struct FusedPlan {
     bool ok = false;
-    int MB = 0, dc = 0, nchunk = 0, lds = 0, gather1 = 0, workgroups = 0;
+    int MB = 0, dc = 0, nchunk = 0, lds = 0, gather1 = 0, xcd = 0, workgroups = 0;
+    int per_cu = 0;  // workgroups the busiest CU runs (one round when resident)
     size_t part_words = 0, red_words = 0, bytes = 0;
 };
 
@@ -412,7 +416,8 @@ int rsag_words(int E, int n) {
 
 // Tuning overrides (environment): ATN_FUSED_ROWS = query rows per row group
 // (16, 32 or 64), ATN_FUSED_EXCHANGE = "gather" or "rsag", ATN_FUSED_DC =
-// D-slice width (a multiple of 32); ATN_FUSED_TRACE prints the plan.  A plan the
+// D-slice width (a multiple of 32), ATN_FUSED_XCD = 1 (XCD-local exchange)
+// or 0 (device-scope exchange); ATN_FUSED_TRACE prints the plan.  A plan the
 // override makes impossible falls back to the default choice.
 int env_int(const char* name) {
     const char* v = std::getenv(name);
@@ -422,7 +427,8 @@ int env_int(const char* name) {
 // Cuts each head's query rows into row groups of MB rows and D into slices
 // of dc dims, one workgroup each, with the whole grid resident at once (the
 // kernel's exchange waits need that: capacity is the device's CU count x
-// resident workgroups per CU for the plan's LDS size).  Of every plan that
+// resident workgroups per CU for the plan's LDS size; an XCD-local plan
+// needs each XCD's share resident on that XCD's CUs).  Of every plan that
 // fits LDS, the device and the exchange's per-thread limits, the one of least
 // estimated time is taken.
 FusedPlan fused_plan_uncached(int dtype, int pek, const Shape& s, bool query_device) {
@@ -430,6 +436,7 @@ FusedPlan fused_plan_uncached(int dtype, int pek, const Shape& s, bool query_dev
     if (s.Lq > kFusedMaxLq || s.Lk > kFusedMaxLk || s.D % 4 != 0) return none;
     int cus = 256;
     int dev = 0;
+    bool xl_ok = true;
     if (query_device) {
         if (hipGetDevice(&dev) != hipSuccess) return none;
         std::lock_guard<std::mutex> lk(g_mu);
@@ -439,31 +446,37 @@ FusedPlan fused_plan_uncached(int dtype, int pek, const Shape& s, bool query_dev
                 hipSuccess)
             return none;
         cus = ds.cus;
+        xl_ok = cus % 8 == 0;
     }
-    auto capacity = [&](int lds) {
+    auto per_cu_cap = [&](int lds) {
         std::lock_guard<std::mutex> lk(g_mu);
-        int& c = g_dev[dev].fused_cap[std::make_pair(dtype, lds)];
-        if (c == 0) c = atn::fused_small_capacity(dtype, pek, lds);
+        int& c = g_dev[dev].fused_per_cu[std::make_pair(dtype, lds)];
+        if (c == 0) c = atn::fused_small_per_cu(dtype, pek, lds);
         return c;
     };
     const int MQ = (int)(s.Lq + 15) / 16 * 16, NK = (int)(s.Lk + 31) / 32 * 32;
     const int es = dtype == ATN_DTYPE_F32 ? 4 : 2;
     // one plan: row groups of MB rows, slices of dc dims, the one-gather
-    // exchange (gather = 1) or reduce-scatter + all-gather (0)
-    auto make = [&](int MB, int dc, int gather) {
+    // exchange (gather = 1) or reduce-scatter + all-gather (0), exchanged at
+    // device scope (xcd = 0) or inside each XCD's L2 (xcd = 1)
+    auto make = [&](int MB, int dc, int gather, int xcd) {
         FusedPlan p;
         const int64_t groups = s.BH * ((s.Lq + MB - 1) / MB);
         const int64_t n = (s.D + dc - 1) / dc;
         if (groups > cus || dc > 1024 || groups * n > kSyncMaxWorkgroups) return p;
-        if (n == 1 && gather) return p;  // a single slice has no exchange
+        if (n == 1 && (gather || xcd)) return p;  // a single slice has no exchange
+        const int64_t gpx = (groups + 7) / 8;     // XL: row groups on the busiest XCD
+        if (xcd && (!xl_ok || gpx > atn::kXcdGroupsPerXcd)) return p;
         const int lds = atn::fused_small_lds_bytes(dtype, pek, MB, (int)s.Lk, dc);
         if (lds > kLdsLimit) return p;
         // the exchange waits need every workgroup resident; a size query (no
         // device) allows the most any plan may launch, so that the workspace
         // it reports bounds every plan the device may take
+        const int per = query_device ? per_cu_cap(lds) : 8;
         if (n > 1) {
-            const int cap = query_device ? capacity(lds) : kSyncMaxWorkgroups;
-            if (cap <= 0 || groups * n > cap) return p;
+            if (per <= 0) return p;
+            if (xcd ? gpx * n > (int64_t)(cus / 8) * per : groups * n > (int64_t)cus * per)
+                return p;
         }
         const int E = MB * NK;
         if (n > 1) {
@@ -477,7 +490,10 @@ FusedPlan fused_plan_uncached(int dtype, int pek, const Shape& s, bool query_dev
         p.nchunk = (int)n;
         p.lds = lds;
         p.gather1 = n > 1 ? gather : 0;
+        p.xcd = xcd;
         p.workgroups = (int)(groups * n);
+        p.per_cu = xcd ? (int)((gpx * n + cus / 8 - 1) / (cus / 8))
+                       : (int)((groups * n + cus - 1) / cus);
         p.bytes = kSyncBytes + round256(p.part_words * 4) + p.red_words * 4;
         p.ok = true;
         return p;
@@ -489,11 +505,17 @@ FusedPlan fused_plan_uncached(int dtype, int pek, const Shape& s, bool query_dev
     // KiB), the slices (0.0373 us each), reduce-scatter's second round trip
     // (8.72 us), each CU's exchange reads (0.1288 us per KiB) and the
     // workgroup count (0.358 us per CU's worth).
+    // XCD-local plans: about 1.5 us less for the first exchange step, 2.5 us
+    // for reduce-scatter's second step and 0.015 us per KiB of exchange
+    // reads (L2), from forced plans of config 2 at D = 512 / 2048 / 4096.
     auto cost = [&](const FusedPlan& p) {
-        const double per_cu = (double)((p.workgroups + cus - 1) / cus);
+        const double per_cu = (double)p.per_cu;
         const double kib = (double)(std::min(p.MB, MQ) + 2 * NK) * p.dc * es / 1024.0;
         const double E = (double)p.MB * NK;
         const double xkib = p.nchunk == 1 ? 0.0 : (p.gather1 ? E * p.nchunk : 2.0 * E) * 4 / 1024.0;
+        if (p.xcd)
+            return 0.0242 * kib * per_cu + 0.0373 * p.nchunk + (!p.gather1 ? 2.5 : 0.0) +
+                   0.015 * xkib * per_cu + 0.358 * p.workgroups / cus - 1.5;
         return 0.0242 * kib * per_cu + 0.0373 * p.nchunk +
                (p.nchunk > 1 && !p.gather1 ? 8.72 : 0.0) + 0.1288 * xkib * per_cu +
                0.358 * p.workgroups / cus;
@@ -504,7 +526,9 @@ FusedPlan fused_plan_uncached(int dtype, int pek, const Shape& s, bool query_dev
     if (force_dc < 32 || force_dc % 32 != 0) force_dc = 0;
     const char* xe = std::getenv("ATN_FUSED_EXCHANGE");
     const int force_x = xe == nullptr ? -1 : (std::strcmp(xe, "gather") == 0 ? 1 : 0);
-    const bool forced = force_rows > 0 || force_dc > 0 || force_x >= 0;
+    const char* xx = std::getenv("ATN_FUSED_XCD");
+    const int force_xcd = xx == nullptr ? -1 : (std::atoi(xx) != 0 ? 1 : 0);
+    const bool forced = force_rows > 0 || force_dc > 0 || force_x >= 0 || force_xcd >= 0;
     const bool trace = query_device && (forced || std::getenv("ATN_FUSED_TRACE") != nullptr);
     // candidates: row groups of 64, 32 or 16 rows (48: the whole padded head
     // of 33-48 rows), slices of 32-512 dims and the width that gives one
@@ -520,17 +544,19 @@ FusedPlan fused_plan_uncached(int dtype, int pek, const Shape& s, bool query_dev
         const int whole = (int)((s.D + 31) / 32 * 32);
         for (int dc : {32, 64, 128, 256, 512, natural}) {
             dc = std::min(dc, whole);
-            for (int gather : {1, 0}) {
-                const FusedPlan p = make(MB, dc, gather);
-                if (!p.ok) continue;
-                max_bytes = std::max(max_bytes, p.bytes);
-                if (!best.ok || cost(p) < cost(best)) best = p;
-                if (forced && (force_rows == 0 || p.MB == force_rows) &&
-                    (force_dc == 0 || p.dc == force_dc) &&
-                    (force_x < 0 || p.nchunk == 1 || p.gather1 == force_x) &&
-                    (!best_forced.ok || cost(p) < cost(best_forced)))
-                    best_forced = p;
-            }
+            for (int gather : {1, 0})
+                for (int xcd : {0, 1}) {
+                    const FusedPlan p = make(MB, dc, gather, xcd);
+                    if (!p.ok) continue;
+                    max_bytes = std::max(max_bytes, p.bytes);
+                    if (!best.ok || cost(p) < cost(best)) best = p;
+                    if (forced && (force_rows == 0 || p.MB == force_rows) &&
+                        (force_dc == 0 || p.dc == force_dc) &&
+                        (force_x < 0 || p.nchunk == 1 || p.gather1 == force_x) &&
+                        (force_xcd < 0 || p.nchunk == 1 || p.xcd == force_xcd) &&
+                        (!best_forced.ok || cost(p) < cost(best_forced)))
+                        best_forced = p;
+                }
         }
     }
     if (forced && !best_forced.ok && trace)
@@ -538,9 +564,9 @@ FusedPlan fused_plan_uncached(int dtype, int pek, const Shape& s, bool query_dev
     FusedPlan p = best_forced.ok ? best_forced : best;
     if (!query_device && p.ok) p.bytes = max_bytes;
     if (trace && p.ok)
-        std::fprintf(stderr, "atn: fused plan rows %d slice %d x %d %s, %d workgroups\n", p.MB,
+        std::fprintf(stderr, "atn: fused plan rows %d slice %d x %d %s%s, %d workgroups\n", p.MB,
                      p.dc, p.nchunk, p.nchunk == 1 ? "none" : (p.gather1 ? "gather" : "rsag"),
-                     p.workgroups);
+                     p.xcd ? " xcd" : "", p.workgroups);
     return p;
 }
 
@@ -552,7 +578,8 @@ FusedPlan fused_plan(int dtype, int pek, const Shape& s, bool query_device) {
     int dev = -1;
     if (query_device && hipGetDevice(&dev) != hipSuccess) return FusedPlan{};
     if (std::getenv("ATN_FUSED_ROWS") || std::getenv("ATN_FUSED_DC") ||
-        std::getenv("ATN_FUSED_EXCHANGE") || std::getenv("ATN_FUSED_TRACE"))
+        std::getenv("ATN_FUSED_EXCHANGE") || std::getenv("ATN_FUSED_XCD") ||
+        std::getenv("ATN_FUSED_TRACE"))
         return fused_plan_uncached(dtype, pek, s, query_device);
     const auto key = std::make_tuple(dev, dtype, pek, (int64_t)s.BH, (int64_t)s.Lq,
                                      (int64_t)s.Lk, (int64_t)s.D);
@@ -738,9 +765,11 @@ int attention_core(int dtype, const void* Q, const void* K, const void* V, void*
         float* part = reinterpret_cast<float*>((char*)ws + kSyncBytes);
         float* red = reinterpret_cast<float*>((char*)ws + kSyncBytes + round256(fd.part_words * 4));
         unsigned* done = reinterpret_cast<unsigned*>((char*)ws + kSyncDoneOff);
+        unsigned* xctr = reinterpret_cast<unsigned*>((char*)ws + kSyncXcdOff);
         ATN_HIP(atn::launch_fused_small(dtype, plan.pek, Q, K, V, out, part, red, epochs, done,
-                                        status, (int)s.BH, Lq, Lk, D, fd.MB, fd.dc, fd.nchunk,
-                                        fd.gather1, scale, plan.q, plan.k, stream));
+                                        status, xctr, (int)s.BH, Lq, Lk, D, fd.MB, fd.dc,
+                                        fd.nchunk, fd.gather1, fd.xcd, scale, plan.q, plan.k,
+                                        stream));
         return ATN_OK;
     }
     float* S = scratch;
@@ -797,12 +826,13 @@ int pe_apply_core(int dtype, const void* in, void* out, long n_rows, int seq_len
 // library's own for `stream` when ws == NULL).  An exchange timeout is
 // reported once; the status word is cleared and every epoch word moves one
 // step on, past the epoch whose exchange words the failed call may have
-// left behind, which re-enables the single-launch kernel.
+// left behind, which re-enables the single-launch kernel (XCD-local
+// counters stay consistent by themselves).
 int workspace_status(void* ws, hipStream_t stream) {
+    int dev;
+    int st = current_device(&dev);
+    if (st != ATN_OK) return st;
     if (ws == nullptr) {
-        int dev;
-        int st = current_device(&dev);
-        if (st != ATN_OK) return st;
         std::lock_guard<std::mutex> lk(g_mu);
         auto& m = g_dev[dev].ws;
         auto it = m.find(stream);

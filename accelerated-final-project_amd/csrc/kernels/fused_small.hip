@@ -50,6 +50,29 @@
 // fail closed the same way until the host clears the status word (and
 // moves every epoch past the failed call's).  The host launches at most as
 // many workgroups as the device holds at once.
+//
+// XCD-local exchange (XL plans).  The dispatcher deals consecutive
+// workgroup ids to the 8 XCDs round robin, each XCD with its own L2, but
+// the XCD that receives id 0 varies from dispatch to dispatch (measured:
+// usually XCD 0, sometimes not).  So an XL workgroup takes its XCD x from
+// the XCC_ID hardware register and its place on that XCD from id / 8: with
+// a grid that is a multiple of 8, every XCD receives each place 0 ..
+// grid/8 - 1 exactly once whatever the starting XCD.  Place gi * n + c runs
+// slice c of the XCD's gi-th row group, and each XCD takes a contiguous
+// block of row groups (heads stay together, so their K/V slices are fetched
+// by as few XCDs as possible).  The exchange then stays inside that XCD's
+// L2: plain stores, `sc0 nt` loads (which always read L2, never a CU's
+// vector L1), and one arrival counter per row group and exchange step,
+// added to atomically at the L2.  Every call adds exactly kXcdUnits to each
+// counter (slice c < n - 1 adds c + 1, the last slice the rest), on every
+// path including failures, so a counter is a multiple of kXcdUnits between
+// calls and its value at a call's start is the arrival's old value rounded
+// down; no epoch, tag or reset is needed.  A wait ends when the count is
+// exactly complete: since the shares differ, a slice that arrived twice or
+// never makes the wait time out (reported) rather than pass early.
+// Counter words are indexed by the physical XCD, so only that XCD's L2
+// ever holds their lines.
+#include <algorithm>
 #include <atomic>
 #include <type_traits>
 
@@ -65,6 +88,14 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
 constexpr int kThreads = 256;
 constexpr int kSpinLimit = 1 << 18;  // polls (each >= one memory round trip): ~0.3 s bound
+// Units every call adds to an XCD-local arrival counter: a power of two (so
+// 32-bit wraparound keeps counters multiples of it) above the shares 1 ..
+// n - 1 of the first n - 1 slices (n <= 2048).
+constexpr unsigned kXcdUnits = 1u << 23;
+static_assert(2048u * 2047u / 2u < kXcdUnits, "XCD-local shares");
+// Buffer cache policy of XCD-local exchange loads: sc0 | nt, served by the
+// XCD's L2 on every access.
+constexpr int kAuxL2 = 3;
 
 // Positional encoding of the 4 consecutive elements v = x[d..d+3] of one
 // row (row pointer xr, position pos); d is a multiple of 4 and d + 3 < D.
@@ -171,6 +202,8 @@ struct FusedArgs {
     int Lq, Lk, D, dc, nchunk;
     int MB, QB;        // query rows per row group, row groups per head
     int gather1;       // 1: one-gather exchange, 0: reduce-scatter + all-gather
+    int G;             // row groups (heads x QB)
+    unsigned* xctr;    // XL plans: arrival counters, kXcdCtrWords per XCD
     float scale;
     PeSide pq, pk;
 };
@@ -184,6 +217,26 @@ __device__ __forceinline__ void st_dev(float* p, float v) {
 }
 __device__ __forceinline__ float ld_dev(const float* p) {
     return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Exchange stores and loads of either plan: device scope (the coherence
+// point past every L2), or XCD-local (plain stores; sc0 nt loads from L2).
+template <bool XL>
+__device__ __forceinline__ void st_x(float* p, float v) {
+    if constexpr (XL) *p = v;
+    else st_dev(p, v);
+}
+template <bool XL>
+__device__ __forceinline__ float ld_x(const float* p) {
+    if constexpr (XL) return __builtin_nontemporal_load(p);
+    else return ld_dev(p);
+}
+
+// The XCD this wave runs on (hardware register XCC_ID, gfx94x / gfx950).
+__device__ __forceinline__ unsigned xcc_id() {
+    unsigned x;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(x));
+    return x & 0xfu;
 }
 
 // Tag of the done words of row group rg (< 2048) at `epoch`: the top bit is
@@ -209,11 +262,58 @@ __device__ __forceinline__ float4 ld_dev4(__amdgpu_buffer_rsrc_t r, int off) {
                        __uint_as_float(v[3]));
 }
 
+// 16 bytes at byte offset `off` from this XCD's L2 (sc0 nt).
+__device__ __forceinline__ float4 ld_l2_4(__amdgpu_buffer_rsrc_t r, int off) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kAuxL2);
+    return make_float4(__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]),
+                       __uint_as_float(v[3]));
+}
+template <bool XL>
+__device__ __forceinline__ float4 ld_x4(__amdgpu_buffer_rsrc_t r, int off) {
+    if constexpr (XL) return ld_l2_4(r, off);
+    else return ld_dev4(r, off);
+}
+
 // Reads the words base[u * stride], u < cnt, all in flight at once.
-template <int NW>
+template <bool XL, int NW>
 __device__ __forceinline__ void ld_words(const float* base, int stride, int cnt, float (&w)[NW]) {
 #pragma unroll
-    for (int u = 0; u < NW; ++u) w[u] = u < cnt ? ld_dev(base + u * stride) : 0.f;
+    for (int u = 0; u < NW; ++u) w[u] = u < cnt ? ld_x<XL>(base + u * stride) : 0.f;
+}
+
+// XL plans.  Wave 0: lane 0 adds `share` to the row group's arrival counter
+// k (an atomic add performed at this XCD's L2, returning the prior value,
+// whose multiple of kXcdUnits is the call's base); with `wait`, the wave
+// then polls the counter through L2 until exactly every slice's units of
+// this call have arrived.  The other waves wait at the barrier.  A workgroup arrives
+// only after every wave's exchange stores have completed (s_waitcnt before
+// the barrier), so they are in L2 once the count is complete.  Returns false
+// for the whole workgroup on timeout.
+__device__ bool xcd_arrive(__amdgpu_buffer_rsrc_t rc, int k, unsigned share, bool wait,
+                           int* flag_lds) {
+    if (threadIdx.x < 64) {
+        unsigned old = 0;
+        if (threadIdx.x == 0)
+            old = (unsigned)__builtin_amdgcn_raw_ptr_buffer_atomic_add_i32((int)share, rc, 4 * k,
+                                                                           0, 0);
+        const unsigned base = __builtin_amdgcn_readlane(old, 0) & ~(kXcdUnits - 1u);
+        bool ok = true;
+        if (wait) {
+            for (int it = 0;; ++it) {
+                const unsigned v = __builtin_amdgcn_readfirstlane(
+                    __builtin_amdgcn_raw_buffer_load_b32(rc, 4 * k, 0, kAuxL2));
+                if (v - base == kXcdUnits) break;
+                if (it > kSpinLimit) {
+                    ok = false;
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(1);
+            }
+        }
+        if (threadIdx.x == 0 && !ok) *flag_lds = 0;
+    }
+    __syncthreads();
+    return *flag_lds != 0;
 }
 
 // Wave 0 polls the done words done[0..n) until each carries `tag`, while
@@ -431,7 +531,7 @@ __device__ __forceinline__ int wave_tiles(int wave, int nrb, int tiles, int* rb,
     return (tiles - *c0 + wpr - 1) / wpr;
 }
 
-template <typename T, int PEK>
+template <typename T, int PEK, bool XL>
 __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
     constexpr bool kBf16 = sizeof(T) == 2;
     constexpr bool kSplit = kBf16 && PEK != kPeNone;
@@ -441,12 +541,27 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar)
     const int lr = lane & 15, lk = lane >> 4;
-    // workgroup id -> (row group qb, head bh, slice c): id = qb * W + bh * n + c
     const int n = a.nchunk;
-    const int W = (int)gridDim.x / a.QB;  // (head, slice) pairs
-    const int qb = (int)blockIdx.x / W, hc = (int)blockIdx.x - qb * W;
-    const int bh = hc / n, c = hc - bh * n;
-    const int rg = bh * a.QB + qb;  // row group (epoch word, exchange region, tag)
+    int rg, c, xcd_slot = 0;
+    if constexpr (XL) {
+        // place id / 8 = gi * n + c on XCD x: slice c of the XCD's gi-th row
+        // group; XCD x holds row groups [x * base + min(x, rem), + cnt)
+        const int x = (int)xcc_id(), local = (int)blockIdx.x >> 3;
+        const int gi = local / n;
+        c = local - gi * n;
+        const int base = a.G >> 3, rem = a.G & 7;
+        if (gi >= base + (x < rem ? 1 : 0)) return;  // no row group here (whole workgroup)
+        rg = x * base + min(x, rem) + gi;
+        xcd_slot = x * kXcdCtrWords + 2 * gi;
+    } else {
+        // id = qb * W + bh * n + c
+        const int W = (int)gridDim.x / a.QB;  // (head, slice) pairs
+        const int qb_ = (int)blockIdx.x / W, hc = (int)blockIdx.x - qb_ * W;
+        const int bh_ = hc / n;
+        c = hc - bh_ * n;
+        rg = bh_ * a.QB + qb_;  // row group (epoch word, exchange region, tag)
+    }
+    const int bh = rg / a.QB, qb = rg - bh * a.QB;
     const int q0 = qb * a.MB;       // first query row of the group
     const int Lq = min(a.MB, a.Lq - q0), Lk = a.Lk, D = a.D, dc = a.dc;
     const int d0 = c * dc;
@@ -468,10 +583,13 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
         sh_epoch = 0;
         sh_failed = 0;
         if (n > 1) {
-            sh_epoch = __hip_atomic_load(a.epochs + rg, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if constexpr (!XL)
+                sh_epoch =
+                    __hip_atomic_load(a.epochs + rg, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             sh_failed = __hip_atomic_load(a.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
+
 
     // ---- 1. Q, K, V slices -> LDS.  Thread t owns 4-element column group
     // t % vpr of rows t / vpr + k * rstep of each tensor.  Loads are raw
@@ -613,7 +731,7 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
             for (int r = 0; r < 4; ++r) {
                 const int i = rb * 16 + lk * 4 + r;
                 const int e = i * NK + j;
-                if (n > 1) st_dev(part + (e >> 8) * (n * 256) + (e & 255), acc[r]);
+                if (n > 1) st_x<XL>(part + (e >> 8) * (n * 256) + (e & 255), acc[r]);
                 else S[i * g.sstr + j] = acc[r];
             }
         };
@@ -649,14 +767,41 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
         else if (cnt > 4) run(std::integral_constant<int, 8>{});
     }
 
-    // ---- 3. all-reduce of S over the group's slices (tagged words)
+    // ---- 3. all-reduce of S over the group's slices (tagged words, or
+    // XCD-local arrival counters)
     if (n > 1) {
         unsigned* done1 = a.done + rg * n;
         unsigned* done2 = a.done + 2048 + rg * n;
+        // XL: this slice's share of the call's units, the group's counters
+        const unsigned share =
+            c < n - 1 ? (unsigned)c + 1u : kXcdUnits - (unsigned)(n - 1) * (unsigned)n / 2u;
+        const __amdgpu_buffer_rsrc_t rc = make_rsrc(a.xctr + xcd_slot, 8);
+        // reduce-scatter: this workgroup owns entries [e0, e1) of the group
+        const int per_rs = (E + n - 1) / n;
+        const int e0_rs = min(E, c * per_rs), e1_rs = min(E, e0_rs + per_rs);
+        // XL, on a path that leaves early: NaN into this workgroup's reduced
+        // entries (late slices of the group read them), then the second
+        // arrival, so the counter still gains its units
+        auto xl_leave_before_step2 = [&]() {
+            if (!a.gather1) {
+                const float nan = __int_as_float(0x7fc00000);
+                for (int e = e0_rs + tid; e < e1_rs; e += kThreads) a.red[(size_t)rg * E + e] = nan;
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+                __builtin_amdgcn_s_waitcnt(0);
+                __syncthreads();
+                xcd_arrive(rc, 1, share, false, &flag);
+            }
+        };
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");  // stores stay above the wait
         __builtin_amdgcn_s_waitcnt(0);  // this wave's partials have completed
         __syncthreads();
-        if (tid == 0) st_done(done1 + c, tag);
+        if constexpr (!XL)
+            if (tid == 0) st_done(done1 + c, tag);
         if (sh_failed) {  // an earlier call timed out: fail closed
+            if constexpr (XL) {
+                xcd_arrive(rc, 0, share, false, &flag);
+                xl_leave_before_step2();
+            }
             poison_slice<T>(O, orow0, Lq, D, d0, dc);
             return;
         }
@@ -666,10 +811,16 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
             const int i = e / NK, j = e - i * NK;
             S[i * g.sstr + j] = v;
         };
-        // returns false (for the whole workgroup) on a timeout
+        // returns false (for the whole workgroup) on a timeout; step = the
+        // exchange step that timed out
+        int step = 1;
         auto exchange = [&]() -> bool {
             float w[kMaxWords];
-            if (!wait_done(done1, n, tag, &flag)) return false;
+            if constexpr (XL) {
+                if (!xcd_arrive(rc, 0, share, true, &flag)) return false;
+            } else {
+                if (!wait_done(done1, n, tag, &flag)) return false;
+            }
             if (a.gather1) {
                 // one gather, 16-byte words: thread t sums entries 4 (t % 64)
                 // .. + 3 of 256-entry blocks t / 64 + 4 i, every slice's
@@ -682,7 +833,7 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
 #pragma unroll
                 for (int u = 0; u < kMaxWords / 4; ++u) {
                     const int i = u / n, p = u - i * n;  // n is uniform: scalar math
-                    w4[u] = u < cnt ? ld_dev4(rs, voff + (4 * i * n + p) * 1024)
+                    w4[u] = u < cnt ? ld_x4<XL>(rs, voff + (4 * i * n + p) * 1024)
                                     : make_float4(0.f, 0.f, 0.f, 0.f);
                 }
                 float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -709,8 +860,7 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
                 return true;
             }
             // reduce-scatter: this workgroup owns entries [e0, e1)
-            const int per = (E + n - 1) / n;
-            const int e0 = c * per, e1 = min(E, e0 + per);
+            const int e0 = e0_rs, e1 = e1_rs;
             const int cnt_e = max(0, e1 - e0);
             float* redl = reinterpret_cast<float*>(smem + g.red_off);
             const __amdgpu_buffer_rsrc_t rs = make_rsrc(pg, n * E * 4);
@@ -728,7 +878,7 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
                 float4 w4[kMaxWords / 4];
 #pragma unroll
                 for (int u = 0; u < kMaxWords / 4; ++u)
-                    w4[u] = u < cnt ? ld_dev4(rs, voff + u * G * 1024)
+                    w4[u] = u < cnt ? ld_x4<XL>(rs, voff + u * G * 1024)
                                     : make_float4(0.f, 0.f, 0.f, 0.f);
                 float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
@@ -752,10 +902,10 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
                         sum.w += v.w;
                     }
                     float* dst = rd + e0 + 4 * tid;
-                    st_dev(dst, sum.x);
-                    st_dev(dst + 1, sum.y);
-                    st_dev(dst + 2, sum.z);
-                    st_dev(dst + 3, sum.w);
+                    st_x<XL>(dst, sum.x);
+                    st_x<XL>(dst + 1, sum.y);
+                    st_x<XL>(dst + 2, sum.z);
+                    st_x<XL>(dst + 3, sum.w);
                 }
             } else if (cnt_e <= kThreads) {
                 // G groups of cnt_e threads; group q sums slices q, q + G, ...
@@ -764,7 +914,8 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
                 const int grp = cnt_e > 0 ? tid / cnt_e : G;
                 const int cnt = grp < G ? (n - grp + G - 1) / G : 0;
                 const int e = e0 + el;
-                ld_words<kMaxWords>(pg + ((e >> 8) * n + grp) * 256 + (e & 255), G * 256, cnt, w);
+                ld_words<XL, kMaxWords>(pg + ((e >> 8) * n + grp) * 256 + (e & 255), G * 256, cnt,
+                                        w);
                 float acc = 0.f;
 #pragma unroll
                 for (int u = 0; u < kMaxWords; ++u)
@@ -774,7 +925,7 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
                 if (tid < cnt_e) {
                     float sum = 0.f;
                     for (int q = 0; q < G; ++q) sum += redl[q * cnt_e + tid];
-                    st_dev(rd + e0 + tid, sum);
+                    st_x<XL>(rd + e0 + tid, sum);
                 }
             } else {
                 // entries e0 + tid + 256 k, every slice of each; word
@@ -782,7 +933,7 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
                 const int ne = tid < cnt_e ? (cnt_e - tid + kThreads - 1) / kThreads : 0;
                 const int cnt = ne * n;
                 const int e = e0 + tid;
-                ld_words<kMaxWords>(pg + (e >> 8) * n * 256 + (e & 255), 256, cnt, w);
+                ld_words<XL, kMaxWords>(pg + (e >> 8) * n * 256 + (e & 255), 256, cnt, w);
                 float acc = 0.f;
                 int p = 0, k = 0;
 #pragma unroll
@@ -790,7 +941,7 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
                     if (u < cnt) {
                         acc += w[u];
                         if (++p == n) {
-                            st_dev(rd + e + k * kThreads, acc);
+                            st_x<XL>(rd + e + k * kThreads, acc);
                             acc = 0.f;
                             p = 0;
                             ++k;
@@ -798,18 +949,24 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
                     }
                 }
             }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
             __builtin_amdgcn_s_waitcnt(0);  // this wave's reduced words have completed
             __syncthreads();
-            if (tid == 0) st_done(done2 + c, tag);
             // all-gather: the reduced S into LDS, 16-byte words (E is a
             // multiple of 512): vectors tid + 256 u
-            if (!wait_done(done2, n, tag, &flag)) return false;
+            step = 2;
+            if constexpr (XL) {
+                if (!xcd_arrive(rc, 1, share, true, &flag)) return false;
+            } else {
+                if (tid == 0) st_done(done2 + c, tag);
+                if (!wait_done(done2, n, tag, &flag)) return false;
+            }
             const __amdgpu_buffer_rsrc_t rr = make_rsrc(rd, E * 4);
             const int cnt = tid < (E >> 2) ? ((E >> 2) - tid + kThreads - 1) / kThreads : 0;
             float4 w4[kMaxWords / 4];
 #pragma unroll
             for (int u = 0; u < kMaxWords / 4; ++u)
-                w4[u] = u < cnt ? ld_dev4(rr, (tid + u * kThreads) * 16)
+                w4[u] = u < cnt ? ld_x4<XL>(rr, (tid + u * kThreads) * 16)
                                 : make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
             for (int u = 0; u < kMaxWords / 4; ++u) {
@@ -825,15 +982,18 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
         };
         if (!exchange()) {
             if (tid == 0)
-                __hip_atomic_store(a.status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_fetch_or(a.status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if constexpr (XL)
+                if (step == 1) xl_leave_before_step2();
             poison_slice<T>(O, orow0, Lq, D, d0, dc);
             return;
         }
         // this workgroup has seen words of every slice of the group, so every
         // workgroup of the group has read `epoch`: advance it
-        if (c == 0 && tid == 0)
-            __hip_atomic_store(a.epochs + rg, epoch + 1u, __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
+        if constexpr (!XL)
+            if (c == 0 && tid == 0)
+                __hip_atomic_store(a.epochs + rg, epoch + 1u, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
     }
     if (defer_v) {
 #pragma unroll
@@ -971,37 +1131,36 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
 
 // Raises the kernel's dynamic-LDS limit once to the largest size used
 // (160 KiB per workgroup on gfx950).
-template <typename T, int PEK>
+template <typename T, int PEK, bool XL>
 hipError_t ensure_lds_limit(int lds) {
     static std::atomic<int> set{0};
     if (lds <= set.load(std::memory_order_acquire)) return hipSuccess;
     const int want = 160 * 1024 - 256;
-    hipError_t e = hipFuncSetAttribute((const void*)k_fused_small<T, PEK>,
+    hipError_t e = hipFuncSetAttribute((const void*)k_fused_small<T, PEK, XL>,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, want);
     if (e == hipSuccess) set.store(want, std::memory_order_release);
     return e;
 }
 
-template <typename T, int PEK>
-hipError_t launch_t(const FusedArgs& a, int BH, int lds, hipStream_t st) {
-    hipError_t e = ensure_lds_limit<T, PEK>(lds);
+template <typename T, int PEK, bool XL>
+hipError_t launch_t(const FusedArgs& a, int lds, hipStream_t st) {
+    hipError_t e = ensure_lds_limit<T, PEK, XL>(lds);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((k_fused_small<T, PEK>), dim3((unsigned)(BH * a.QB * a.nchunk)),
-                       dim3(kThreads), lds, st, a);
+    // XL: 8 XCDs x (row groups per XCD, rounded up) x slices
+    const unsigned grid = XL ? (unsigned)(8 * ((a.G + 7) / 8) * a.nchunk)
+                             : (unsigned)(a.G * a.nchunk);
+    hipLaunchKernelGGL((k_fused_small<T, PEK, XL>), dim3(grid), dim3(kThreads), lds, st, a);
     return hipGetLastError();
 }
 
-template <typename T, int PEK>
-int capacity_t(int lds) {
-    int dev = 0, cus = 0, per = 0;
-    if (hipGetDevice(&dev) != hipSuccess) return 0;
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+template <typename T, int PEK, bool XL>
+int per_cu_t(int lds) {
+    int per = 0;
+    if (ensure_lds_limit<T, PEK, XL>(lds) != hipSuccess) return 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, k_fused_small<T, PEK, XL>, kThreads,
+                                                     lds) != hipSuccess)
         return 0;
-    if (ensure_lds_limit<T, PEK>(lds) != hipSuccess) return 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, k_fused_small<T, PEK>, kThreads, lds) !=
-        hipSuccess)
-        return 0;
-    return cus * per;
+    return per;
 }
 
 }  // namespace
@@ -1011,35 +1170,49 @@ int fused_small_lds_bytes(int dtype, int pek, int MB, int Lk, int dc) {
     return make_geo(bf16, bf16 && pek != kPeNone, MB, Lk, dc).bytes;
 }
 
-int fused_small_capacity(int dtype, int pek, int lds) {
+int fused_small_per_cu(int dtype, int pek, int lds) {
     // occupancy depends on LDS and registers; the encoded variants use the
-    // most registers, so their figure is the safe one for every variant
+    // most registers, so the smallest of their figures is safe for every
+    // variant of either exchange
     (void)pek;
-    return dtype == kDtypeF32 ? capacity_t<float, kPeRopeHalf>(lds)
-                              : capacity_t<uint16_t, kPeRopeHalf>(lds);
+    if (dtype == kDtypeF32)
+        return std::min(per_cu_t<float, kPeRopeHalf, false>(lds),
+                        per_cu_t<float, kPeRopeHalf, true>(lds));
+    return std::min(per_cu_t<uint16_t, kPeRopeHalf, false>(lds),
+                    per_cu_t<uint16_t, kPeRopeHalf, true>(lds));
 }
 
 hipError_t launch_fused_small(int dtype, int pek, const void* Q, const void* K, const void* V,
                               void* O, float* part, float* red,
-                              unsigned* epochs, unsigned* done, int* status, int BH, int Lq,
-                              int Lk, int D, int MB, int dc, int nchunk, int gather1, float scale,
-                              const PeSide& pq, const PeSide& pk, hipStream_t st) {
+                              unsigned* epochs, unsigned* done, int* status, unsigned* xctr,
+                              int BH, int Lq, int Lk, int D, int MB, int dc, int nchunk,
+                              int gather1, int xcd, float scale, const PeSide& pq,
+                              const PeSide& pk, hipStream_t st) {
+    const int QB = (Lq + MB - 1) / MB;
     FusedArgs a{Q, K, V, O, part, red, epochs, done, status, Lq, Lk, D, dc, nchunk,
-                MB, (Lq + MB - 1) / MB, gather1, scale, pq, pk};
+                MB, QB, gather1, BH * QB, xctr, scale, pq, pk};
     const int lds = fused_small_lds_bytes(dtype, pek, MB, Lk, dc);
-#define ATN_FUSED_CASE(T)                                                                \
-    switch (pek) {                                                                       \
-        case kPeNone: return launch_t<T, kPeNone>(a, BH, lds, st);                       \
-        case kPeRopeInterleaved: return launch_t<T, kPeRopeInterleaved>(a, BH, lds, st); \
-        case kPeRopeHalf: return launch_t<T, kPeRopeHalf>(a, BH, lds, st);               \
-        case kPeSinusoidal: return launch_t<T, kPeSinusoidal>(a, BH, lds, st);           \
-        default: return hipErrorInvalidValue;                                            \
+    // an XL plan with one slice has no exchange: the plain form does the same
+    const bool xl = xcd != 0 && nchunk > 1;
+#define ATN_FUSED_PE(T, XLV)                                                                \
+    switch (pek) {                                                                          \
+        case kPeNone: return launch_t<T, kPeNone, XLV>(a, lds, st);                         \
+        case kPeRopeInterleaved: return launch_t<T, kPeRopeInterleaved, XLV>(a, lds, st);   \
+        case kPeRopeHalf: return launch_t<T, kPeRopeHalf, XLV>(a, lds, st);                 \
+        case kPeSinusoidal: return launch_t<T, kPeSinusoidal, XLV>(a, lds, st);             \
+        default: return hipErrorInvalidValue;                                               \
     }
     if (dtype == kDtypeF32) {
-        ATN_FUSED_CASE(float)
+        if (xl) {
+            ATN_FUSED_PE(float, true)
+        }
+        ATN_FUSED_PE(float, false)
     }
-    ATN_FUSED_CASE(uint16_t)
-#undef ATN_FUSED_CASE
+    if (xl) {
+        ATN_FUSED_PE(uint16_t, true)
+    }
+    ATN_FUSED_PE(uint16_t, false)
+#undef ATN_FUSED_PE
 }
 
 }  // namespace atn

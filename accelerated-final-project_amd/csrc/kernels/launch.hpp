@@ -24,14 +24,20 @@ hipError_t launch_pv(int dtype, const float* P, const void* V, void* O, int BH, 
 // Single-launch split-D kernel for len_q <= 64, len_k <= 128 (fused_small.hip):
 // row groups of MB query rows, D slices of dc dims; gather1 selects the
 // one-gather exchange (each thread polls (MB*NK/256) * nchunk <= 64 words)
-// over reduce-scatter + all-gather.
+// over reduce-scatter + all-gather; xcd selects the XCD-local exchange
+// (every slice of a row group on one XCD, arrival counters in xctr, at most
+// kXcdGroupsPerXcd row groups per XCD).
+constexpr int kXcdCtrWords = 256;                    // counter words per XCD (1 KiB)
+constexpr int kXcdGroupsPerXcd = kXcdCtrWords / 2;  // two counters per row group
 int fused_small_lds_bytes(int dtype, int pek, int MB, int Lk, int dc);
-int fused_small_capacity(int dtype, int pek, int lds);
+// resident workgroups per CU for this LDS size (either exchange)
+int fused_small_per_cu(int dtype, int pek, int lds);
 hipError_t launch_fused_small(int dtype, int pek, const void* Q, const void* K, const void* V,
                               void* O, float* part, float* red,
-                              unsigned* epochs, unsigned* done, int* status, int BH, int Lq,
-                              int Lk, int D, int MB, int dc, int nchunk, int gather1, float scale,
-                              const PeSide& pq, const PeSide& pk, hipStream_t st);
+                              unsigned* epochs, unsigned* done, int* status, unsigned* xctr,
+                              int BH, int Lq, int Lk, int D, int MB, int dc, int nchunk,
+                              int gather1, int xcd, float scale, const PeSide& pq,
+                              const PeSide& pk, hipStream_t st);
 // Long-sequence bf16 path (gemm_path.hip): E = exp(scale Q K^T - tile row
 // max) (fp16) with per-(row, 256-key tile) max and sum, per-row factors
 // g_t = exp(m_t - m) / l, O = (E g) V.  Needs D % 8 == 0, Lk % 8 == 0 and

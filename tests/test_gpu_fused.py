@@ -120,16 +120,19 @@ def test_fused_with_encodings_bf16(am, dev, pe):
     assert n == 0, f"normwise rel {nrel}, max abs {mabs}"
 
 
+@pytest.mark.parametrize("xcd", ["0", "1", ""], ids=["device", "xcd", "default"])
 @pytest.mark.parametrize("shape", [(1, 4, 64, 64, 2048), (1, 2, 130, 70, 256)],
                          ids=lambda s: "x".join(map(str, s)))
-def test_graph_replays_match_eager(am, dev, shape):
+def test_graph_replays_match_eager(am, dev, monkeypatch, shape, xcd):
     """Captured HIP graph of three calls, replayed four times with eager work
     and synchronizations in between; every replay must equal the eager
     result bit for bit (the single-launch kernel keeps its barrier epochs in
     device memory, so replayed arguments stay valid)."""
     import hip_rt
+    if xcd:
+        monkeypatch.setenv("ATN_FUSED_XCD", xcd)
     B, Hh, Lq, Lk, D = shape
-    print(f"[case] graph replay {shape}", flush=True)
+    print(f"[case] graph replay {shape} xcd={xcd or 'default'}", flush=True)
     (q, k, v), (Q, K, V) = H.device_inputs((B, Hh, Lq, D), (B, Hh, Lk, D), 91)
     ws = _ws(am, 0, B, Hh, Lq, Lk, D)
     st = hip_rt.Stream()
@@ -158,24 +161,31 @@ def test_graph_replays_match_eager(am, dev, shape):
     st.destroy()
 
 
-@pytest.mark.parametrize("rows,exchange", [("16", "gather"), ("16", "rsag"), ("32", "rsag"),
-                                           ("64", "rsag"), ("", "")],
+@pytest.mark.parametrize("rows,exchange,xcd", [("16", "gather", "0"), ("16", "rsag", "0"),
+                                               ("32", "rsag", "0"), ("64", "rsag", "0"),
+                                               ("16", "gather", "1"), ("16", "rsag", "1"),
+                                               ("32", "rsag", "1"), ("64", "rsag", "1"),
+                                               ("32", "gather", "1"), ("", "", "")],
                          ids=lambda v: v or "default")
 @pytest.mark.parametrize("shape,dtype,pe", [((1, 4, 64, 64, 2048), "f32", None),
                                             ((1, 3, 40, 72, 1024), "f32", None),
                                             ((1, 2, 48, 96, 1024), "bf16", "rope_half")],
                          ids=["cfg2", "ragged", "bf16rope"])
-def test_fused_row_groups_and_exchanges(am, dev, monkeypatch, rows, exchange, shape, dtype, pe):
+def test_fused_row_groups_and_exchanges(am, dev, monkeypatch, rows, exchange, xcd, shape, dtype,
+                                        pe):
     """Every row-group size and both exchange forms (one gather; reduce-scatter
-    + all-gather), forced through the planner's tuning overrides, give the
+    + all-gather), each at device scope (xcd 0) and inside one XCD's L2 (xcd
+    1; the ragged shape's 9 row groups leave XCDs with different counts and
+    idle workgroups), forced through the planner's tuning overrides, give the
     oracle's result, and repeated calls on one workspace are bit-identical."""
     import hip_rt
     if rows:
         monkeypatch.setenv("ATN_FUSED_ROWS", rows)
         monkeypatch.setenv("ATN_FUSED_EXCHANGE", exchange)
+        monkeypatch.setenv("ATN_FUSED_XCD", xcd)
     B, Hh, Lq, Lk, D = shape
     print(f"[case] fused rows={rows or 'default'} exchange={exchange or 'default'} "
-          f"{dtype} {shape} pe={pe}", flush=True)
+          f"xcd={xcd or 'default'} {dtype} {shape} pe={pe}", flush=True)
     dcode = 0 if dtype == "f32" else 1
     desc = am.make_pe("rope", pairing="half") if pe else None
     assert am.path(dcode, B, Hh, Lq, Lk, D, desc) == am.ATN_PATH_FUSED_SMALL
@@ -190,8 +200,18 @@ def test_fused_row_groups_and_exchanges(am, dev, monkeypatch, rows, exchange, sh
             got = out.bits()
             if first is None:
                 first = got
-            else:
-                assert np.array_equal(first, got), "results differ between calls"
+            elif not np.array_equal(first, got):
+                word = int(ws.bits().ravel()[:1].view(np.uint32)[0])
+                st = am.sync_status(ws, B, Hh)
+                f32 = (first if dtype == "f32" else hip_rt.bf16_bits_to_f32(first)).reshape(-1, D)
+                g32 = (got if dtype == "f32" else hip_rt.bf16_bits_to_f32(got)).reshape(-1, D)
+                diff = np.abs(np.nan_to_num(f32, nan=1e9) - np.nan_to_num(g32, nan=1e9))
+                rows_d = np.where(diff.max(1) > 0)[0]
+                raise AssertionError(
+                    f"results differ between calls: status {st} (word {word:#x}), NaNs first "
+                    f"{np.isnan(f32).sum()} "
+                    f"last {np.isnan(g32).sum()}, {len(rows_d)} rows differ {rows_d[:12].tolist()}, "
+                    f"max diff {diff.max():.3g}")
     assert am.sync_status(ws, B, Hh) == 0
     if pe:
         c, s = oracle.rope_cache(max(Lq, Lk), D)
@@ -312,3 +332,43 @@ def test_fused_planner_shapes_with_encoding(am, dev, shape, dtype, pe):
     else:
         n, nrel, mabs = H.check_bf16(out.numpy(), ref)
         assert n == 0, f"normwise rel {nrel}, max abs {mabs}"
+
+
+def test_fused_exchange_scopes_share_one_workspace(am, dev, monkeypatch):
+    """One workspace, calls alternating between device-scope and XCD-local
+    plans of different shapes (different slice counts per row group, so the
+    XCD-local counters are shared by plans of different sizes) and both
+    exchange forms: every call keeps the oracle's result, bit for bit from
+    call to call, and no wait times out."""
+    import hip_rt
+    shapes = [(1, 4, 64, 64, 2048), (1, 8, 32, 64, 1024), (1, 3, 40, 72, 1024)]
+    cases = []
+    for i, shp in enumerate(shapes):
+        B, Hh, Lq, Lk, D = shp
+        (q, k, v), host = H.device_inputs((B, Hh, Lq, D), (B, Hh, Lk, D), 700 + i)
+        cases.append((shp, (q, k, v), oracle.attention(*host, nthreads=16)))
+    nbytes = max(am.workspace_bytes(0, *shp) for shp in shapes)
+    ws = hip_rt.DeviceArray((nbytes // 4,), "f32", fill=0)
+    first = {}
+    plans = [("1", "gather", "16"), ("0", "gather", "16"), ("1", "rsag", "32"),
+             ("0", "rsag", "16"), ("1", "rsag", "16"), ("1", "gather", "32")]
+    for rnd in range(3):
+        for xcd, ex, rows in plans:
+            monkeypatch.setenv("ATN_FUSED_XCD", xcd)
+            monkeypatch.setenv("ATN_FUSED_EXCHANGE", ex)
+            monkeypatch.setenv("ATN_FUSED_ROWS", rows)
+            for shp, ins, ref in cases:
+                print(f"[case] shared workspace round {rnd} xcd={xcd} {ex} rows={rows} {shp}",
+                      flush=True)
+                out = H.empty(ref.shape)
+                am.attention_ex(*ins, out, workspace=ws)
+                hip_rt.synchronize()
+                got = out.bits()
+                n, mabs, mrel = H.check_f32(got, ref)
+                assert n == 0, f"{n} mismatches, max abs {mabs}, max rel {mrel}"
+                key = (xcd, ex, rows, shp)
+                if key in first:
+                    assert np.array_equal(first[key], got)
+                else:
+                    first[key] = got
+    assert am.sync_status(ws, 1, 1) == 0
