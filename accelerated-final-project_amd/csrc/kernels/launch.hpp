@@ -61,6 +61,15 @@ hipError_t launch_gemm_pv(const uint16_t* E, float* st_m, float* st_l, float* ga
                           const uint16_t* V, uint16_t* O, int BH, int Lq, int Lk, int D,
                           hipStream_t st);
 
+// Allocation-free entry point: the per-device scratch array (noalloc.hip),
+// kNoAllocScratchBytes long.  noalloc_scratch() returns its device address
+// for device `dev` (hipGetSymbolAddress, taken once per device) and, on the
+// first call for that device, enqueues a fill kernel on `st` that zeroes its
+// first sync_bytes; noalloc_ready() tells whether that set-up has happened.
+constexpr size_t kNoAllocScratchBytes = (size_t)64 << 20;
+bool noalloc_ready(int dev);
+hipError_t noalloc_scratch(int dev, size_t sync_bytes, hipStream_t st, void** ptr);
+
 hipError_t launch_pe_apply(int dtype, int pek, const void* in, void* out, long n_rows,
                            int seq_len, int D, const PeSide& pe, int vec_ok, hipStream_t st);
 

@@ -372,3 +372,46 @@ def test_fused_exchange_scopes_share_one_workspace(am, dev, monkeypatch):
                 else:
                     first[key] = got
     assert am.sync_status(ws, 1, 1) == 0
+
+
+@pytest.mark.parametrize("xcd,exchange", [("0", "gather"), ("0", "rsag"), ("1", "gather"),
+                                          ("1", "rsag")])
+def test_fail_closed_then_recovers(am, dev, monkeypatch, xcd, exchange):
+    """The fail-closed path, forced from the host: the workspace's status word
+    is preset (as a timed-out call would leave it), so every workgroup of the
+    next call takes the fail-closed exit -- no wait is entered, every
+    workgroup ends normally.  That call's outputs are NaN and
+    atn_sync_status_ex reports ATN_ERR_DEVICE_TIMEOUT once (clearing the word
+    and moving the epochs on); the call after it gives the oracle's result,
+    on device-scope and XCD-local plans, one gather and reduce-scatter."""
+    import hip_rt
+    monkeypatch.setenv("ATN_FUSED_XCD", xcd)
+    monkeypatch.setenv("ATN_FUSED_EXCHANGE", exchange)
+    monkeypatch.setenv("ATN_FUSED_ROWS", "16")
+    B, Hh, Lq, Lk, D = 1, 4, 64, 64, 2048
+    print(f"[case] fail closed xcd={xcd} {exchange}", flush=True)
+    (q, k, v), (Q, K, V) = H.device_inputs((B, Hh, Lq, D), (B, Hh, Lk, D), 808)
+    ref = oracle.attention(Q, K, V, nthreads=16)
+    ws = _ws(am, 0, B, Hh, Lq, Lk, D)
+    out = H.empty(Q.shape)
+    am.attention_ex(q, k, v, out, workspace=ws)  # one good call first
+    hip_rt.synchronize()
+    assert am.sync_status(ws, B, Hh) == 0
+    word = np.zeros(ws.shape, dtype=np.float32)
+    word[...] = ws.bits()
+    word.view(np.uint32)[0] = 1  # the status word, as a timeout leaves it
+    ws.upload(word)
+    out.fill_nan()
+    am.attention_ex(q, k, v, out, workspace=ws)
+    hip_rt.synchronize()
+    got = out.numpy()
+    assert np.isnan(got).all(), "fail-closed call wrote non-NaN outputs"
+    assert am.sync_status(ws, B, Hh) == am.ATN_ERR_DEVICE_TIMEOUT
+    assert am.sync_status(ws, B, Hh) == 0  # reported once
+    for _ in range(3):
+        out.fill_nan()
+        am.attention_ex(q, k, v, out, workspace=ws)
+        hip_rt.synchronize()
+        n, mabs, mrel = H.check_f32(out.numpy(), ref)
+        assert n == 0, f"after recovery: {n} mismatches, max abs {mabs}"
+    assert am.sync_status(ws, B, Hh) == 0
