@@ -39,6 +39,8 @@ ATN_ERR_BAD_ARGUMENT = -9
 ATN_ERR_MISALIGNED = -10
 ATN_ERR_DEVICE_TIMEOUT = -11
 ATN_ERR_CAPTURE = -12
+ATN_ERR_SCRATCH_LIMIT = -13
+ATN_ERR_NOT_PREPARED = -14
 
 ATN_DTYPE_F32 = 0
 ATN_DTYPE_BF16 = 1
@@ -92,6 +94,8 @@ _SIGS = {
     "atn_device_count": ([], _i),
     "atn_attention_fwd_ex": ([_i, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i,
                               ctypes.POINTER(PeDesc), _vp, ctypes.c_size_t, _vp], _i),
+    "atn_attention_fwd_noalloc_ex": ([_i, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i,
+                                      ctypes.POINTER(PeDesc), _vp], _i),
     "atn_attention_workspace_bytes": ([_i, _i, _i, _i, _i, _i, ctypes.POINTER(PeDesc)],
                                       ctypes.c_size_t),
     "atn_pe_apply_ex": ([_i, _vp, _vp, ctypes.c_long, _i, _i, ctypes.POINTER(PeDesc), _vp], _i),
@@ -216,6 +220,27 @@ def attention_ex(Q, K, V, out=None, pe: PeDesc | None = None, workspace=None, st
                                     ws_ptr, ws_bytes, _stream_handle(stream))
     if st != ATN_OK:
         raise AtnError(st, "atn_attention_fwd_ex")
+    return out
+
+
+def attention_noalloc_ex(Q, K, V, out=None, pe: PeDesc | None = None, stream=None):
+    """atn_attention_fwd_noalloc_ex (scratch in the library's per-device
+    static array, no allocation); raises AtnError."""
+    from hip_rt import DeviceArray
+    B, H, Lq, D = Q.shape
+    Lk = K.shape[2]
+    _check(Q, Q.dtype, (B, H, Lq, D), "Q")
+    _check(K, Q.dtype, (B, H, Lk, D), "K")
+    _check(V, Q.dtype, (B, H, Lk, D), "V")
+    if out is None:
+        out = DeviceArray(Q.shape, Q.dtype)
+    _check(out, Q.dtype, (B, H, Lq, D), "out")
+    st = lib().atn_attention_fwd_noalloc_ex(_dtype_code(Q), _ptr(Q), _ptr(K), _ptr(V), _ptr(out),
+                                            B, H, Lq, Lk, D,
+                                            ctypes.byref(pe) if pe is not None else None,
+                                            _stream_handle(stream))
+    if st != ATN_OK:
+        raise AtnError(st, "atn_attention_fwd_noalloc_ex")
     return out
 
 

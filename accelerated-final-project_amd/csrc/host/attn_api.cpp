@@ -203,13 +203,14 @@ void build_sin_table(std::vector<float>& a, std::vector<float>& b, int npos, int
 // Returns the device tables for this encoding, building or growing them
 // (synchronously) when needed.  Caller holds g_mu.
 int get_table(DeviceState& ds, const PePlan& plan, int D, int npos, hipStream_t stream,
-              Table** out) {
+              bool no_alloc, Table** out) {
     const bool rope = plan.pek != atn::kPeSinusoidal;
     uint32_t base_bits;
     std::memcpy(&base_bits, &plan.base, 4);
     const auto key = std::make_tuple(rope ? 1 : 2, rope ? plan.rotary : D, rope ? base_bits : 0u);
     Table& t = ds.tables[key];
     if (t.a == nullptr || t.npos < npos) {
+        if (no_alloc) return ATN_ERR_NOT_PREPARED;
         const int st = refuse_if_capturing(stream);
         if (st != ATN_OK) return st;
         const int want = npos < 64 ? 64 : npos;
@@ -253,13 +254,14 @@ uint16_t f16_bits(float x) {
 //               rotary width (a pass-through rotation)
 // Built (synchronously) when missing or too short; caller holds g_mu.
 int get_table16(DeviceState& ds, const PePlan& plan, int D, int npos, hipStream_t stream,
-                Table16** out) {
+                bool no_alloc, Table16** out) {
     const bool rope = plan.pek != atn::kPeSinusoidal;
     uint32_t base_bits;
     std::memcpy(&base_bits, &plan.base, 4);
     const auto key = std::make_tuple(rope ? 1 : 2, D, rope ? plan.rotary : D, rope ? base_bits : 0u);
     Table16& t = ds.tables16[key];
     if (t.p == nullptr || t.npos < npos) {
+        if (no_alloc) return ATN_ERR_NOT_PREPARED;
         const int st = refuse_if_capturing(stream);
         if (st != ATN_OK) return st;
         const int want = npos < 64 ? 64 : npos;
@@ -295,7 +297,8 @@ int get_table16(DeviceState& ds, const PePlan& plan, int D, int npos, hipStream_
 }
 
 // Fills the PeSide table pointers (library tables or the caller's).
-int bind_tables(const atn_pe_desc* pe, PePlan& plan, int D, int npos, hipStream_t stream) {
+int bind_tables(const atn_pe_desc* pe, PePlan& plan, int D, int npos, hipStream_t stream,
+                bool no_alloc = false) {
     if (plan.pek == atn::kPeNone) return ATN_OK;
     if (plan.caller_tables) {
         const bool rope = plan.pek != atn::kPeSinusoidal;
@@ -312,7 +315,7 @@ int bind_tables(const atn_pe_desc* pe, PePlan& plan, int D, int npos, hipStream_
     if (st != ATN_OK) return st;
     std::lock_guard<std::mutex> lk(g_mu);
     Table* t = nullptr;
-    st = get_table(g_dev[dev], plan, D, npos, stream, &t);
+    st = get_table(g_dev[dev], plan, D, npos, stream, no_alloc, &t);
     if (st != ATN_OK) return st;
     for (atn::PeSide* s : {&plan.q, &plan.k}) {
         s->a = t->a;
@@ -664,9 +667,12 @@ GemmPlan gemm_plan(int dtype, const Shape& s, const PePlan& plan) {
 }
 
 // ---------------------------------------------------------------- core
+// no_alloc: the allocation-free form -- scratch is the device's static
+// array, and a call that would need a library allocation (tables not yet
+// built) or more scratch than the array holds is refused.
 int attention_core(int dtype, const void* Q, const void* K, const void* V, void* out, int B,
                    int H, int Lq, int Lk, int D, const atn_pe_desc* pe, void* workspace,
-                   size_t workspace_bytes, hipStream_t stream) {
+                   size_t workspace_bytes, hipStream_t stream, bool no_alloc = false) {
     if (dtype != ATN_DTYPE_F32 && dtype != ATN_DTYPE_BF16) return ATN_ERR_BAD_ARGUMENT;
     if (!Q || !K || !V || !out) return ATN_ERR_NULL_POINTER;
     Shape s;
@@ -693,7 +699,7 @@ int attention_core(int dtype, const void* Q, const void* K, const void* V, void*
     int dev;
     st = current_device(&dev);
     if (st != ATN_OK) return st;
-    st = bind_tables(pe, plan, D, Lq > Lk ? Lq : Lk, stream);
+    st = bind_tables(pe, plan, D, Lq > Lk ? Lq : Lk, stream, no_alloc);
     if (st != ATN_OK) return st;
     // the device's own capacity decides between the single-launch kernel
     // and the three-kernel pipeline
@@ -707,7 +713,16 @@ int attention_core(int dtype, const void* Q, const void* K, const void* V, void*
     const size_t need =
         use_fused ? fd.bytes : (use_gemm ? gp.bytes : kSyncBytes + sp.bytes);
     void* ws = workspace;
-    if (ws == nullptr) {
+    if (no_alloc) {
+        if (need > atn::kNoAllocScratchBytes) return ATN_ERR_SCRATCH_LIMIT;
+        if (!atn::noalloc_ready(dev)) {
+            // set-up (symbol address, sync region cleared) runs once per
+            // device, outside capture
+            st = refuse_if_capturing(stream);
+            if (st != ATN_OK) return st;
+        }
+        ATN_HIP(atn::noalloc_scratch(dev, kSyncBytes, stream, &ws));
+    } else if (ws == nullptr) {
         st = ensure_workspace(need, stream, &ws);
         if (st != ATN_OK) return st;
     } else if (workspace_bytes < need) {
@@ -739,7 +754,8 @@ int attention_core(int dtype, const void* Q, const void* K, const void* V, void*
                 if (gp.benc != atn::kGemmEncRaw) {
                     std::lock_guard<std::mutex> lk(g_mu);
                     Table16* t16 = nullptr;
-                    st = get_table16(g_dev[dev], plan, D, Lq > Lk ? Lq : Lk, stream, &t16);
+                    st = get_table16(g_dev[dev], plan, D, Lq > Lk ? Lq : Lk, stream, no_alloc,
+                                     &t16);
                     if (st != ATN_OK) return st;
                     tab = t16->p;
                     tab_rows = t16->npos;
@@ -833,11 +849,23 @@ int workspace_status(void* ws, hipStream_t stream) {
     int st = current_device(&dev);
     if (st != ATN_OK) return st;
     if (ws == nullptr) {
-        std::lock_guard<std::mutex> lk(g_mu);
-        auto& m = g_dev[dev].ws;
-        auto it = m.find(stream);
-        if (it == m.end() || it->second.ptr == nullptr) return ATN_OK;
-        ws = it->second.ptr;
+        // the stream's library workspace, then the device's allocation-free
+        // scratch (once it is set up)
+        void* lib_ws = nullptr;
+        {
+            std::lock_guard<std::mutex> lk(g_mu);
+            auto& m = g_dev[dev].ws;
+            auto it = m.find(stream);
+            if (it != m.end()) lib_ws = it->second.ptr;
+        }
+        const int a = lib_ws != nullptr ? workspace_status(lib_ws, stream) : ATN_OK;
+        int b = ATN_OK;
+        if (atn::noalloc_ready(dev)) {
+            void* sc = nullptr;
+            ATN_HIP(atn::noalloc_scratch(dev, kSyncBytes, stream, &sc));
+            b = workspace_status(sc, stream);
+        }
+        return a != ATN_OK ? a : b;
     }
     int word = 0;
     ATN_HIP(hipMemcpy(&word, ws, sizeof(int), hipMemcpyDeviceToHost));
@@ -906,6 +934,10 @@ const char* atn_status_string(int status) {
         case ATN_ERR_MISALIGNED: return "pointer not aligned to its element size";
         case ATN_ERR_DEVICE_TIMEOUT: return "device-side wait timed out (outputs are NaN)";
         case ATN_ERR_CAPTURE: return "library allocation needed while the stream is being captured";
+        case ATN_ERR_SCRATCH_LIMIT:
+            return "shape needs more scratch than the allocation-free entry point holds";
+        case ATN_ERR_NOT_PREPARED:
+            return "encoding tables not prepared (call atn_prepare_pe_ex first)";
         default: return "unknown status";
     }
 }
@@ -924,6 +956,13 @@ int atn_attention_fwd_ex(int dtype, const void* Q, const void* K, const void* V,
                          void* stream) {
     return attention_core(dtype, Q, K, V, out, batch, heads, len_q, len_k, head_d, pe, workspace,
                           workspace_bytes, (hipStream_t)stream);
+}
+
+int atn_attention_fwd_noalloc_ex(int dtype, const void* Q, const void* K, const void* V,
+                                 void* out, int batch, int heads, int len_q, int len_k,
+                                 int head_d, const atn_pe_desc* pe, void* stream) {
+    return attention_core(dtype, Q, K, V, out, batch, heads, len_q, len_k, head_d, pe, nullptr, 0,
+                          (hipStream_t)stream, true);
 }
 
 size_t atn_attention_workspace_bytes(int dtype, int batch, int heads, int len_q, int len_k,
@@ -978,7 +1017,15 @@ int atn_prepare_pe_ex(const atn_pe_desc* pe, int head_d, int max_positions) {
     int st = check_pe(pe, head_d, &plan);
     if (st != ATN_OK) return st;
     if (plan.pek == atn::kPeNone || plan.caller_tables) return ATN_OK;
-    return bind_tables(pe, plan, head_d, max_positions, nullptr);
+    st = bind_tables(pe, plan, head_d, max_positions, nullptr);
+    if (st != ATN_OK) return st;
+    // and the fp16 tables of the GEMM path's in-GEMM K encoding
+    int dev;
+    st = current_device(&dev);
+    if (st != ATN_OK) return st;
+    std::lock_guard<std::mutex> lk(g_mu);
+    Table16* t16 = nullptr;
+    return get_table16(g_dev[dev], plan, head_d, max_positions, nullptr, false, &t16);
 }
 
 // ---- drop-ins ----

@@ -66,7 +66,7 @@ hipError_t launch_gemm_pv(const uint16_t* E, float* st_m, float* st_l, float* ga
 // for device `dev` (hipGetSymbolAddress, taken once per device) and, on the
 // first call for that device, enqueues a fill kernel on `st` that zeroes its
 // first sync_bytes; noalloc_ready() tells whether that set-up has happened.
-constexpr size_t kNoAllocScratchBytes = (size_t)64 << 20;
+constexpr size_t kNoAllocScratchBytes = (size_t)64 << 20;  // ATN_NOALLOC_SCRATCH_BYTES
 bool noalloc_ready(int dev);
 hipError_t noalloc_scratch(int dev, size_t sync_bytes, hipStream_t st, void** ptr);
 

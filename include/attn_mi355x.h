@@ -51,6 +51,8 @@ typedef uint16_t atn_bf16;
 #define ATN_ERR_MISALIGNED (-10)    /* pointer not aligned to its element size */
 #define ATN_ERR_DEVICE_TIMEOUT (-11) /* a kernel's bounded cross-workgroup wait expired */
 #define ATN_ERR_CAPTURE (-12)        /* a library allocation was needed during graph capture */
+#define ATN_ERR_SCRATCH_LIMIT (-13)  /* shape needs more than the allocation-free scratch */
+#define ATN_ERR_NOT_PREPARED (-14)   /* encoding tables not built (atn_prepare_pe_ex) */
 
 /* Text for a status code (static storage). */
 const char *atn_status_string(int status);
@@ -226,6 +228,32 @@ int atn_attention_fwd_ex(int dtype, const void *Q, const void *K, const void *V,
                          const atn_pe_desc *pe, void *workspace, size_t workspace_bytes,
                          void *stream);
 
+/* Allocation-free form of atn_attention_fwd_ex.  It has no counterpart in
+ * the reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  It calls no hipMalloc, hipFree or allocating library routine:
+ * its scratch is a file-scope device array of ATN_NOALLOC_SCRATCH_BYTES
+ * (64 MiB) on each GPU the library runs on, held until the process ends.
+ * Same arguments, results and asynchronous semantics as atn_attention_fwd_ex
+ * without the workspace, plus these limits:
+ *   - a shape whose workspace (atn_attention_workspace_bytes for the path the
+ *     device takes) exceeds the array returns ATN_ERR_SCRATCH_LIMIT;
+ *   - an encoding with library tables needs them built beforehand
+ *     (atn_prepare_pe_ex), else ATN_ERR_NOT_PREPARED; caller tables need
+ *     nothing;
+ *   - the first call on a device sets the array up (its address, and a
+ *     fill kernel clearing its synchronization words) and must not be
+ *     captured (ATN_ERR_CAPTURE); later calls may be;
+ *   - every call on one GPU shares that GPU's array, so calls that overlap
+ *     in time on one GPU (other streams, other threads) race: serialize
+ *     them;
+ *   - a device-side wait timeout is reported by atn_sync_status_ex with
+ *     workspace == NULL. */
+#define ATN_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+int atn_attention_fwd_noalloc_ex(int dtype, const void *Q, const void *K, const void *V,
+                                 void *out, int batch, int heads, int len_q, int len_k,
+                                 int head_d, const atn_pe_desc *pe, void *stream);
+
 /* Scratch bytes atn_attention_fwd_ex needs for this shape (0 on bad input). */
 size_t atn_attention_workspace_bytes(int dtype, int batch, int heads, int len_q, int len_k,
                                      int head_d, const atn_pe_desc *pe);
@@ -236,14 +264,15 @@ int atn_pe_apply_ex(int dtype, const void *in, void *out, long n_rows, int seq_l
                     const atn_pe_desc *pe, void *stream);
 
 /* Synchronizes `stream` and reports whether a call that used `workspace`
- * (NULL: the library's workspace of that stream) hit a device-side wait
- * timeout: ATN_OK or ATN_ERR_DEVICE_TIMEOUT (the status word is then
- * cleared).  batch and heads are accepted for interface stability and not
+ * (NULL: the library's workspace of that stream and the current device's
+ * allocation-free scratch) hit a device-side wait timeout: ATN_OK or
+ * ATN_ERR_DEVICE_TIMEOUT (the status word is then cleared).  batch and heads are accepted for interface stability and not
  * used. */
 int atn_sync_status_ex(void *workspace, int batch, int heads, void *stream);
 
 /* Prepares the library's angle tables for this encoding and shape on the
- * current device (otherwise built on first use, which synchronizes). */
+ * current device -- the fp32 tables and the fp16 tables of the long-sequence
+ * path -- otherwise built on first use, which synchronizes. */
 int atn_prepare_pe_ex(const atn_pe_desc *pe, int head_d, int max_positions);
 
 /* Which kernels atn_attention_fwd_ex runs for this shape on the current
