@@ -470,7 +470,7 @@ FusedPlan fused_plan_uncached(int dtype, int pek, const Shape& s, bool query_dev
         if (n == 1 && (gather || xcd)) return p;  // a single slice has no exchange
         const int64_t gpx = (groups + 7) / 8;     // XL: row groups on the busiest XCD
         if (xcd && (!xl_ok || gpx > atn::kXcdGroupsPerXcd)) return p;
-        const int lds = atn::fused_small_lds_bytes(dtype, pek, MB, (int)s.Lk, dc);
+        const int lds = atn::fused_small_lds_bytes(dtype, pek, MB, (int)s.Lk, dc, (int)n);
         if (lds > kLdsLimit) return p;
         // the exchange waits need every workgroup resident; a size query (no
         // device) allows the most any plan may launch, so that the workspace
@@ -511,14 +511,24 @@ FusedPlan fused_plan_uncached(int dtype, int pek, const Shape& s, bool query_dev
     // XCD-local plans: about 1.5 us less for the first exchange step, 2.5 us
     // for reduce-scatter's second step and 0.015 us per KiB of exchange
     // reads (L2), from forced plans of config 2 at D = 512 / 2048 / 4096.
+    // Their XCDs also fetch whole heads' K and V (each XCD holds a block of
+    // row groups), where device-scope plans spread every head over all 8:
+    // the extra bytes per XCD cost about 1 us per 0.7 MB (config 3: 2 MiB
+    // more per XCD, 3 us slower).
+    const double kv_head = 2.0 * (double)s.Lk * (double)s.D * es;
     auto cost = [&](const FusedPlan& p) {
         const double per_cu = (double)p.per_cu;
         const double kib = (double)(std::min(p.MB, MQ) + 2 * NK) * p.dc * es / 1024.0;
         const double E = (double)p.MB * NK;
         const double xkib = p.nchunk == 1 ? 0.0 : (p.gather1 ? E * p.nchunk : 2.0 * E) * 4 / 1024.0;
-        if (p.xcd)
+        if (p.xcd) {
+            const int QB = (int)((s.Lq + p.MB - 1) / p.MB);
+            const int64_t G = s.BH * QB, gpx = (G + 7) / 8;
+            const double heads_x = (double)std::max<int64_t>(1, (gpx + QB - 1) / QB);
+            const double kv_extra = std::max(0.0, heads_x * kv_head - (double)s.BH * kv_head / 8.0);
             return 0.0242 * kib * per_cu + 0.0373 * p.nchunk + (!p.gather1 ? 2.5 : 0.0) +
-                   0.015 * xkib * per_cu + 0.358 * p.workgroups / cus - 1.5;
+                   0.015 * xkib * per_cu + 0.358 * p.workgroups / cus - 1.5 + kv_extra / 0.7e6;
+        }
         return 0.0242 * kib * per_cu + 0.0373 * p.nchunk +
                (p.nchunk > 1 && !p.gather1 ? 8.72 : 0.0) + 0.1288 * xkib * per_cu +
                0.358 * p.workgroups / cus;
@@ -599,15 +609,15 @@ FusedPlan fused_plan(int dtype, int pek, const Shape& s, bool query_device) {
 }
 
 // ---------------------------------------------------------------- gemm plan
-// Long-sequence bf16 shapes: two MFMA GEMMs around an exact row softmax.
-// Workspace after the sync region: encoded Q and K (fp16 with per-row
-// scales, when a positional encoding is on), E = exp(S - tile row max)
-// (fp16), per-(row, 256-key tile) max, sum and softmax factor (fp32).
-constexpr int kGemmMinL = 128;
-
+// bf16 shapes outside the single-launch kernel's window: two MFMA GEMMs
+// around an exact row softmax.  Workspace after the sync region: encoded Q
+// and K (fp16 with per-row scales, when a positional encoding is on), E =
+// exp(S - tile row max) (fp16, rows padded to ldE = Lk rounded up to 8 keys),
+// per-(row, 256-key tile) max, sum and softmax factor (fp32).
 struct GemmPlan {
     bool ok = false, encoded = false;
     int benc = 0;     // fused K encoding (atn::kGemmEnc*), 0 = K~ from k_encode_f16
+    int ldE = 0;      // E row stride (elements)
     int tiles_k = 0;  // 256-key tiles per score row
     size_t q_off = 0, k_off = 0, qs_off = 0, ks_off = 0, e_off = 0, m_off = 0, l_off = 0,
            g_off = 0, bytes = 0;
@@ -615,12 +625,11 @@ struct GemmPlan {
 
 GemmPlan gemm_plan(int dtype, const Shape& s, const PePlan& plan) {
     GemmPlan p;
-    if (dtype != ATN_DTYPE_BF16 || s.Lq < kGemmMinL || s.Lk < kGemmMinL || s.D % 8 != 0 ||
-        s.Lk % 8 != 0)
-        return p;
+    if (dtype != ATN_DTYPE_BF16 || s.D % 8 != 0) return p;
+    p.ldE = (int)((s.Lk + 7) / 8 * 8);
     // the GEMM kernels address one head's matrix with 32-bit element offsets
     const int64_t lim = (int64_t)1 << 31;
-    if ((int64_t)s.Lq * s.D >= lim || (int64_t)s.Lk * s.D >= lim || (int64_t)s.Lq * s.Lk >= lim)
+    if ((int64_t)s.Lq * s.D >= lim || (int64_t)s.Lk * s.D >= lim || (int64_t)s.Lq * p.ldE >= lim)
         return p;
     size_t off = kSyncBytes;
     auto take = [&](size_t b) { size_t o = off; off += round256(b); return o; };
@@ -657,7 +666,7 @@ GemmPlan gemm_plan(int dtype, const Shape& s, const PePlan& plan) {
     }
     p.tiles_k = (int)((s.Lk + 255) / 256);
     const size_t stats = (size_t)s.BH * s.Lq * p.tiles_k * 4;
-    p.e_off = take((size_t)s.BH * s.Lq * s.Lk * 2);
+    p.e_off = take((size_t)s.BH * s.Lq * p.ldE * 2);
     p.m_off = take(stats);
     p.l_off = take(stats);
     p.g_off = take(stats);
@@ -760,19 +769,19 @@ int attention_core(int dtype, const void* Q, const void* K, const void* V, void*
                     tab = t16->p;
                     tab_rows = t16->npos;
                 }
-                ATN_HIP(atn::launch_gemm_qk_enc(gp.benc, qd, ke, qs, tab, tab_rows, E, st_m, st_l,
-                                                (int)s.BH, Lq, Lk, D, scale, stream));
+                ATN_HIP(atn::launch_gemm_qk_enc(gp.benc, qd, ke, qs, tab, tab_rows, E, gp.ldE, st_m,
+                                                st_l, (int)s.BH, Lq, Lk, D, scale, stream));
             } else {
                 ATN_HIP(atn::launch_encode_f16(plan.k.on ? plan.pek : atn::kPeNone, ke, kd, ks,
                                                (long)(s.BH * Lk), Lk, D, plan.k, stream));
-                ATN_HIP(atn::launch_gemm_qk(1, qd, kd, qs, ks, E, st_m, st_l, (int)s.BH, Lq, Lk, D,
-                                            scale, stream));
+                ATN_HIP(atn::launch_gemm_qk(1, qd, kd, qs, ks, E, gp.ldE, st_m, st_l, (int)s.BH, Lq,
+                                            Lk, D, scale, stream));
             }
         } else {
-            ATN_HIP(atn::launch_gemm_qk(0, qe, ke, nullptr, nullptr, E, st_m, st_l, (int)s.BH, Lq,
-                                        Lk, D, scale, stream));
+            ATN_HIP(atn::launch_gemm_qk(0, qe, ke, nullptr, nullptr, E, gp.ldE, st_m, st_l,
+                                        (int)s.BH, Lq, Lk, D, scale, stream));
         }
-        ATN_HIP(atn::launch_gemm_pv(E, st_m, st_l, ga, static_cast<const uint16_t*>(V),
+        ATN_HIP(atn::launch_gemm_pv(E, gp.ldE, st_m, st_l, ga, static_cast<const uint16_t*>(V),
                                     static_cast<uint16_t*>(out), (int)s.BH, Lq, Lk, D, stream));
         return ATN_OK;
     }

@@ -10,10 +10,15 @@
 //   1. loads its Q rows' slice and the head's K/V slices once (16-byte
 //      loads, all in flight before the first LDS store; the positional
 //      encoding is applied to Q and K at load) into LDS;
-//   2. computes the partial scores S_c = Q[rows, c] K[:, c]^T on MFMA
-//      (fp32: v_mfma_f32_16x16x4_f32; bf16: v_mfma_f32_16x16x32_bf16, with
-//      encoded Q/K split into hi + lo bf16 parts so nothing is lost to
-//      re-rounding), up to eight independent 16x16 tiles per wave;
+//   2. computes the partial scores S_c = Q[rows, c] K[:, c]^T on bf16 MFMA
+//      (v_mfma_f32_16x16x32_bf16), up to eight independent 16x16 tiles per
+//      wave.  Values that are not bf16 -- fp32 inputs, and bf16 inputs
+//      after a positional encoding -- are split into hi + lo bf16 parts and
+//      multiplied as a_hi b_hi + a_hi b_lo + a_lo b_hi (fp32 accumulation),
+//      which keeps about 16 significant bits of every product: for fp32 that
+//      is far inside the 1e-4 bar and about five times the throughput of
+//      fp32 MFMA (v_mfma_f32_16x16x4_f32), whose dependent chains bounded
+//      this phase;
 //   3. all-reduces S over the group's slices through global memory, either
 //      in one gather (every workgroup reads every slice's partial of its
 //      group: one memory round trip) or, when that volume is too large, as
@@ -21,8 +26,8 @@
 //      always summed in slice order, so results are bit-reproducible;
 //   4. exact softmax of scale * S per row (max, exp, sum, divide;
 //      final/attention.cu:262-270), four threads per row;
-//   5. O[rows, slice] = P V[:, slice] on MFMA (bf16: P split into hi + lo
-//      bf16 parts), one store per output element.
+//   5. O[rows, slice] = P V[:, slice] on bf16 MFMA, P split into hi + lo
+//      bf16 parts (and fp32 V too), one store per output element.
 //
 // Q and O are touched once; K and V once per row group, and the QB
 // workgroups that share a K/V slice get workgroup ids QB apart by a
@@ -142,48 +147,51 @@ __device__ __forceinline__ float4 encode4(float4 v4, const T* __restrict__ xr, i
     return make_float4(v[0], v[1], v[2], v[3]);
 }
 
-// LDS geometry of one workgroup.  Element strides are chosen so that the
-// MFMA operand reads are free of bank conflicts: fp32 A operands (Q, P)
-// read 16 rows x 2 columns per half-wave -> row stride = 2 (mod 32); fp32 V
-// (B operand of PV) reads 2 rows x 16 columns -> stride = 16 (mod 32); the
-// softmax reads 8 rows x 4 columns of S -> stride = 4 (mod 32).  bf16 Q, K
-// and P rows are padded by 8 elements (16-byte aligned 8-element reads);
-// bf16 V is kept [key][dim] with a row stride of dc + 16 elements, i.e. 32
-// or 96 bytes (mod 128), so the 4 rows x 32 bytes that each 16-lane group of
-// a transposing read (ds_read_b64_tr_b16) touches fall in distinct banks.
+// LDS geometry of one workgroup (MFMA operands as bf16).  Q, K and P rows
+// are padded by 8 elements (16-byte aligned 8-element reads); V is kept
+// [key][dim] with a row stride of dc + 16 elements, i.e. 32 or 96 bytes
+// (mod 128), so the 4 rows x 32 bytes that each 16-lane group of a
+// transposing read (ds_read_b64_tr_b16) touches fall in distinct banks; the
+// softmax reads 8 rows x 4 columns of fp32 S -> stride = 4 (mod 32).  With
+// an exchange (s_over_qk), S lies over the Q and K regions: it is written
+// only by the exchange, after the barrier that follows the last read of Q
+// and K; a single slice writes S straight from the accumulators, so S then
+// has a region of its own.
 struct Geo {
     int MQ, NK, dc;
     int qstr, kstr, vstr, sstr, pstr;
-    int q_off, k_off, ql_off, kl_off, v_off, s_off, p_off, red_off;  // byte offsets
+    int q_off, k_off, ql_off, kl_off, v_off, vl_off, s_off, p_off, red_off;  // byte offsets
     int bytes;
 };
 
-// split: bf16 Q/K are kept as hi + lo parts (encoded inputs).
-__host__ __device__ inline Geo make_geo(bool bf16, bool split, int Lq, int Lk, int dc) {
+// f32: fp32 inputs (Q, K and V kept as hi + lo bf16 parts); encoded: a
+// positional encoding makes Q/K non-bf16 (hi + lo parts for bf16 inputs).
+__host__ __device__ inline Geo make_geo(bool f32, bool encoded, bool s_over_qk, int Lq, int Lk,
+                                        int dc) {
     Geo g{};
     g.MQ = (Lq + 15) / 16 * 16;
     g.NK = (Lk + 31) / 32 * 32;
     g.dc = dc;
-    const int es = bf16 ? 2 : 4;
-    if (bf16) {
-        g.qstr = g.kstr = dc + 8;
-        g.vstr = dc + 16;   // V stored [key][dim], read transposed
-        g.pstr = g.NK + 8;  // P hi and lo, [row][key]
-    } else {
-        g.qstr = g.kstr = dc + 2;
-        g.vstr = dc + 16;   // V stored [key][dim]
-        g.pstr = g.NK + 2;
-    }
+    const bool split = f32 || encoded;
+    g.qstr = g.kstr = dc + 8;
+    g.vstr = dc + 16;   // V stored [key][dim], read transposed
+    g.pstr = g.NK + 8;  // P hi and lo, [row][key]
     g.sstr = g.NK + 4;
     int off = 0;
     auto take = [&](int b) { int o = off; off += (b + 15) / 16 * 16; return o; };
-    g.q_off = take(g.MQ * g.qstr * es);
-    g.k_off = take(g.NK * g.kstr * es);
-    g.ql_off = (bf16 && split) ? take(g.MQ * g.qstr * es) : g.q_off;
-    g.kl_off = (bf16 && split) ? take(g.NK * g.kstr * es) : g.k_off;
-    g.v_off = take(g.NK * g.vstr * es);
-    g.s_off = take(g.MQ * g.sstr * 4);
-    g.p_off = take(bf16 ? 2 * g.MQ * g.pstr * 2 : g.MQ * g.pstr * 4);
+    g.q_off = take(g.MQ * g.qstr * 2);
+    g.k_off = take(g.NK * g.kstr * 2);
+    g.ql_off = split ? take(g.MQ * g.qstr * 2) : g.q_off;
+    g.kl_off = split ? take(g.NK * g.kstr * 2) : g.k_off;
+    if (s_over_qk) {
+        g.s_off = 0;
+        off = off > g.MQ * g.sstr * 4 ? off : g.MQ * g.sstr * 4;
+    } else {
+        g.s_off = take(g.MQ * g.sstr * 4);
+    }
+    g.v_off = take(g.NK * g.vstr * 2);
+    g.vl_off = f32 ? take(g.NK * g.vstr * 2) : g.v_off;
+    g.p_off = take(2 * g.MQ * g.pstr * 2);
     g.red_off = take(kThreads * 16);
     g.bytes = off;
     return g;
@@ -410,36 +418,13 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
     return __builtin_bit_cast(uint32_t, v);
 }
 
-// NT independent 16x16 fp32 MFMA accumulations sharing one A operand:
-// acc[u] += sum_k A[k] B_u[k] over k in [0, kdim) step 4, where lane
-// (lr, lk) reads A at a[kk * ak] and tile u's B at b[u * bstep + kk * bk]
-// (a, b already offset to the lane's row and k = lk).  kdim is a multiple
-// of 32: the operands of 8 k-steps are read from LDS first, then the 8 x NT
-// MFMAs issue back to back (no control flow inside, so the accumulators
-// stay in place).
-template <int NT>
-__device__ __forceinline__ void mma_f32(const float* a, int ak, const float* b, int bstep,
-                                        int bk, int kdim, v4f (&acc)[NT]) {
-    for (int kb = 0; kb < kdim; kb += 32) {
-        float av[8], bv[8][NT];
-#pragma unroll
-        for (int st = 0; st < 8; ++st) {
-            const int kk = kb + 4 * st;
-            av[st] = a[kk * ak];
-#pragma unroll
-            for (int u = 0; u < NT; ++u) bv[st][u] = b[u * bstep + kk * bk];
-        }
-#pragma unroll
-        for (int st = 0; st < 8; ++st)
-#pragma unroll
-            for (int u = 0; u < NT; ++u)
-                acc[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[st], bv[st][u], acc[u], 0, 0, 0);
-    }
-}
-
-// bf16 form (k step 32, 8 elements per lane, contiguous along k), same
-// prefetch scheme.  With ALO the A operand is a_hi + a_lo (two MFMAs); with
-// BLO as well the three-term product a_hi b + a_hi b_lo + a_lo b.
+// NT independent 16x16 bf16 MFMA accumulations sharing one A operand (k
+// step 32, 8 elements per lane, contiguous along k): acc[u] += A B_u^T over
+// k in [0, kdim), where lane (lr, lk) reads A at a and tile u's B at b + u *
+// bstep (a, b already offset to the lane's row and k = 8 lk); the operands
+// of the next k step are read from LDS before this step's MFMAs issue.  With
+// ALO the A operand is a_hi + a_lo (two MFMAs); with BLO as well the
+// three-term product a_hi b + a_hi b_lo + a_lo b.
 template <int NT, bool ALO, bool BLO>
 __device__ __forceinline__ void mma_bf16(const uint16_t* a, const uint16_t* a_lo,
                                          const uint16_t* b, const uint16_t* b_lo, int bstep,
@@ -488,30 +473,37 @@ __device__ __forceinline__ v4i16 ds_read_tr16(const uint16_t* p) {
 
 // PV form of mma_bf16 (A = P as hi + lo parts): the B operand comes from V
 // kept [key][dim] in LDS (row stride vstr; vb points at tile 0's first
-// column, tile u's columns start nstep later).  Lane (lr, lk) needs keys
-// kk + 8 lk + 0..7 of column lr: in each 16-lane group lane L supplies the
-// address of key kk + 8 lk + 4 h + (L % 16) / 4, columns 4 (L % 4) .. + 3,
-// and the transposing read (ds_read_b64_tr_b16) hands lane L keys 4 h +
-// 0..3 of column L % 16 -- half h of its operand.
-template <int NT>
+// column, tile u's columns start nstep later; with VLO, V's lo part lies
+// vlo_d elements further).  Lane (lr, lk) needs keys kk + 8 lk + 0..7 of
+// column lr: in each 16-lane group lane L supplies the address of key kk +
+// 8 lk + 4 h + (L % 16) / 4, columns 4 (L % 4) .. + 3, and the transposing
+// read (ds_read_b64_tr_b16) hands lane L keys 4 h + 0..3 of column L % 16 --
+// half h of its operand.
+template <int NT, bool VLO>
 __device__ __forceinline__ void mma_bf16_vt(const uint16_t* a, const uint16_t* a_lo,
-                                            const uint16_t* vb, int vstr, int nstep, int kdim,
-                                            v4f (&acc)[NT]) {
+                                            const uint16_t* vb, int vlo_d, int vstr, int nstep,
+                                            int kdim, v4f (&acc)[NT]) {
     const int lane = threadIdx.x & 63;
     const uint16_t* vl = vb + (8 * (lane >> 4) + ((lane & 15) >> 2)) * vstr + 4 * (lane & 3);
+    auto vread = [&](const uint16_t* p) {
+        const uint2 lo = __builtin_bit_cast(uint2, ds_read_tr16(p));
+        const uint2 hi = __builtin_bit_cast(uint2, ds_read_tr16(p + 4 * vstr));
+        return __builtin_bit_cast(bf16x8, make_uint4(lo.x, lo.y, hi.x, hi.y));
+    };
     for (int kk = 0; kk < kdim; kk += 32) {
         const bf16x8 ah = lds8(a + kk), al = lds8(a_lo + kk);
-        bf16x8 bv[NT];
+        bf16x8 bv[NT], bl[NT];
 #pragma unroll
         for (int u = 0; u < NT; ++u) {
             const uint16_t* p = vl + kk * vstr + u * nstep;
-            const uint2 lo = __builtin_bit_cast(uint2, ds_read_tr16(p));
-            const uint2 hi = __builtin_bit_cast(uint2, ds_read_tr16(p + 4 * vstr));
-            bv[u] = __builtin_bit_cast(bf16x8, make_uint4(lo.x, lo.y, hi.x, hi.y));
+            bv[u] = vread(p);
+            if constexpr (VLO) bl[u] = vread(p + vlo_d);
         }
 #pragma unroll
         for (int u = 0; u < NT; ++u) {
             acc[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bv[u], acc[u], 0, 0, 0);
+            if constexpr (VLO)
+                acc[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bl[u], acc[u], 0, 0, 0);
             acc[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bv[u], acc[u], 0, 0, 0);
         }
     }
@@ -534,7 +526,10 @@ __device__ __forceinline__ int wave_tiles(int wave, int nrb, int tiles, int* rb,
 template <typename T, int PEK, bool XL>
 __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
     constexpr bool kBf16 = sizeof(T) == 2;
-    constexpr bool kSplit = kBf16 && PEK != kPeNone;
+    // Q and K carry lo parts (fp32 inputs, or encoded bf16 inputs); V does
+    // for fp32 inputs
+    constexpr bool kSplit = !kBf16 || PEK != kPeNone;
+    constexpr bool kVlo = !kBf16;
     extern __shared__ __align__(16) unsigned char smem[];
     __shared__ int flag;
 
@@ -565,7 +560,7 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
     const int q0 = qb * a.MB;       // first query row of the group
     const int Lq = min(a.MB, a.Lq - q0), Lk = a.Lk, D = a.D, dc = a.dc;
     const int d0 = c * dc;
-    const Geo g = make_geo(kBf16, kSplit, a.MB, Lk, dc);
+    const Geo g = make_geo(!kBf16, PEK != kPeNone, a.nchunk > 1, a.MB, Lk, dc);
     const int MQ = g.MQ, NK = g.NK, E = MQ * NK, nrb = MQ / 16;
     const size_t orow0 = (size_t)bh * a.Lq + q0;  // output row of the group's row 0
 
@@ -612,15 +607,27 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
     const int ckv = r0 < rstep ? (NK - r0 + rstep - 1) / rstep : 0;
     const bool defer_v = (MQ + rstep - 1) / rstep <= kQ && (NK + rstep - 1) / rstep <= kKV;
     Raw bv[kKV];
+    // hi (rounded to nearest even) and lo (the residual, rounded) bf16
+    // parts of 4 values
+    auto split4 = [](const float (&e4)[4], uint2& w, uint2& wl) {
+        w.x = pack_bf16x2(e4[0], e4[1]);
+        w.y = pack_bf16x2(e4[2], e4[3]);
+        wl.x = pack_bf16x2(e4[0] - __uint_as_float(w.x << 16),
+                           e4[1] - __uint_as_float(w.x & 0xffff0000u));
+        wl.y = pack_bf16x2(e4[2] - __uint_as_float(w.y << 16),
+                           e4[3] - __uint_as_float(w.y & 0xffff0000u));
+    };
     auto store_v = [&](int row, Raw raw) {
+        uint16_t* dst = reinterpret_cast<uint16_t*>(smem + g.v_off) + row * g.vstr + col;
         if constexpr (kBf16) {
             // the raw bf16 bits, [key][dim]
-            *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(smem + g.v_off) +
-                                      row * g.vstr + col) = raw;
+            *reinterpret_cast<uint2*>(dst) = raw;
         } else {
-            float* dst = reinterpret_cast<float*>(smem + g.v_off) + row * g.vstr + col;
-            *reinterpret_cast<float2*>(dst) = make_float2(raw.x, raw.y);
-            *reinterpret_cast<float2*>(dst + 2) = make_float2(raw.z, raw.w);
+            const float e4[4] = {raw.x, raw.y, raw.z, raw.w};
+            uint2 w, wl;
+            split4(e4, w, wl);
+            *reinterpret_cast<uint2*>(dst) = w;
+            *reinterpret_cast<uint2*>(dst + (g.vl_off - g.v_off) / 2) = wl;
         }
     };
     {
@@ -633,30 +640,14 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
         // one encoded row vector of Q (isq) or K into its LDS rows
         auto store_qk = [&](bool isq, int row, float4 f) {
             const float e4[4] = {f.x, f.y, f.z, f.w};
-            if constexpr (kBf16) {
-                const int off = row * (isq ? g.qstr : g.kstr) + col;
-                uint16_t* hi = reinterpret_cast<uint16_t*>(smem + (isq ? g.q_off : g.k_off));
-                uint2 w;
-                w.x = pack_bf16x2(e4[0], e4[1]);
-                w.y = pack_bf16x2(e4[2], e4[3]);
-                *reinterpret_cast<uint2*>(hi + off) = w;
-                if constexpr (kSplit) {
-                    uint16_t* lo = reinterpret_cast<uint16_t*>(smem + (isq ? g.ql_off : g.kl_off));
-                    // residuals against the hi parts just packed
-                    const float r4[4] = {e4[0] - __uint_as_float(w.x << 16),
-                                         e4[1] - __uint_as_float(w.x & 0xffff0000u),
-                                         e4[2] - __uint_as_float(w.y << 16),
-                                         e4[3] - __uint_as_float(w.y & 0xffff0000u)};
-                    uint2 wl;
-                    wl.x = pack_bf16x2(r4[0], r4[1]);
-                    wl.y = pack_bf16x2(r4[2], r4[3]);
-                    *reinterpret_cast<uint2*>(lo + off) = wl;
-                }
-            } else {
-                float* dst = reinterpret_cast<float*>(smem + (isq ? g.q_off : g.k_off)) +
-                             row * (isq ? g.qstr : g.kstr) + col;
-                *reinterpret_cast<float2*>(dst) = make_float2(e4[0], e4[1]);
-                *reinterpret_cast<float2*>(dst + 2) = make_float2(e4[2], e4[3]);
+            const int off = row * (isq ? g.qstr : g.kstr) + col;
+            uint16_t* hi = reinterpret_cast<uint16_t*>(smem + (isq ? g.q_off : g.k_off));
+            uint2 w, wl;
+            split4(e4, w, wl);
+            *reinterpret_cast<uint2*>(hi + off) = w;
+            if constexpr (kSplit) {
+                uint16_t* lo = reinterpret_cast<uint16_t*>(smem + (isq ? g.ql_off : g.kl_off));
+                *reinterpret_cast<uint2*>(lo + off) = wl;
             }
         };
         // round j: loads of Q rows j*kQ.. and K/V rows j*kKV.. (all in
@@ -742,21 +733,13 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
             for (int u = 0; u < NT; ++u) acc[u] = v4f{0.f, 0.f, 0.f, 0.f};
             // tiles past cnt repeat the last valid tile (computed, not stored)
             const int bstep_rows = (cnt > 1 ? cs : 0) * 16;
-            if constexpr (kBf16) {
-                const uint16_t* qh = reinterpret_cast<const uint16_t*>(smem + g.q_off) +
-                                     (rb * 16 + lr) * g.qstr + lk * 8;
-                const uint16_t* kh = reinterpret_cast<const uint16_t*>(smem + g.k_off) +
-                                     (c0 * 16 + lr) * g.kstr + lk * 8;
-                const int ql_d = (g.ql_off - g.q_off) / 2, kl_d = (g.kl_off - g.k_off) / 2;
-                mma_bf16<NT, kSplit, kSplit>(qh, qh + ql_d, kh, kh + kl_d, bstep_rows * g.kstr,
-                                             dc, acc);
-            } else {
-                const float* qp = reinterpret_cast<const float*>(smem + g.q_off) +
-                                  (rb * 16 + lr) * g.qstr + lk;
-                const float* kp = reinterpret_cast<const float*>(smem + g.k_off) +
-                                  (c0 * 16 + lr) * g.kstr + lk;
-                mma_f32<NT>(qp, 1, kp, bstep_rows * g.kstr, 1, dc, acc);
-            }
+            const uint16_t* qh = reinterpret_cast<const uint16_t*>(smem + g.q_off) +
+                                 (rb * 16 + lr) * g.qstr + lk * 8;
+            const uint16_t* kh = reinterpret_cast<const uint16_t*>(smem + g.k_off) +
+                                 (c0 * 16 + lr) * g.kstr + lk * 8;
+            const int ql_d = (g.ql_off - g.q_off) / 2, kl_d = (g.kl_off - g.k_off) / 2;
+            mma_bf16<NT, kSplit, kSplit>(qh, qh + ql_d, kh, kh + kl_d, bstep_rows * g.kstr, dc,
+                                         acc);
 #pragma unroll
             for (int u = 0; u < NT; ++u)
                 if (u < cnt) store(u, acc[u]);
@@ -1038,18 +1021,11 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
 #pragma unroll
             for (int u = 0; u < W; u += 2) {
                 const float p0 = v[u] * inv, p1 = v[u + 1] * inv;
-                if constexpr (kBf16) {
-                    uint16_t* ph = reinterpret_cast<uint16_t*>(smem + g.p_off);
-                    const uint32_t h = pack_bf16x2(p0, p1);
-                    *reinterpret_cast<uint32_t*>(&ph[i * g.pstr + j0 + u]) = h;
-                    *reinterpret_cast<uint32_t*>(&ph[(MQ + i) * g.pstr + j0 + u]) =
-                        pack_bf16x2(p0 - __uint_as_float(h << 16),
-                                    p1 - __uint_as_float(h & 0xffff0000u));
-                } else {
-                    *reinterpret_cast<float2*>(
-                        &reinterpret_cast<float*>(smem + g.p_off)[i * g.pstr + j0 + u]) =
-                        make_float2(p0, p1);
-                }
+                uint16_t* ph = reinterpret_cast<uint16_t*>(smem + g.p_off);
+                const uint32_t h = pack_bf16x2(p0, p1);
+                *reinterpret_cast<uint32_t*>(&ph[i * g.pstr + j0 + u]) = h;
+                *reinterpret_cast<uint32_t*>(&ph[(MQ + i) * g.pstr + j0 + u]) =
+                    pack_bf16x2(p0 - __uint_as_float(h << 16), p1 - __uint_as_float(h & 0xffff0000u));
             }
         };
         using std::integral_constant;
@@ -1092,19 +1068,11 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
 #pragma unroll
                 for (int u = 0; u < NT; ++u) acc[u] = v4f{0.f, 0.f, 0.f, 0.f};
                 const int step = (left > 1 ? cs : 0) * 16;  // repeats past `left`, unstored
-                if constexpr (kBf16) {
-                    const uint16_t* ph = reinterpret_cast<const uint16_t*>(smem + g.p_off) +
-                                         (rb * 16 + lr) * g.pstr + lk * 8;
-                    const uint16_t* vb = reinterpret_cast<const uint16_t*>(smem + g.v_off) +
-                                         tc * 16;
-                    mma_bf16_vt<NT>(ph, ph + MQ * g.pstr, vb, g.vstr, step, NK, acc);
-                } else {
-                    const float* pp = reinterpret_cast<const float*>(smem + g.p_off) +
-                                      (rb * 16 + lr) * g.pstr + lk;
-                    const float* vp = reinterpret_cast<const float*>(smem + g.v_off) +
-                                      lk * g.vstr + tc * 16 + lr;
-                    mma_f32<NT>(pp, 1, vp, step, g.vstr, NK, acc);
-                }
+                const uint16_t* ph = reinterpret_cast<const uint16_t*>(smem + g.p_off) +
+                                     (rb * 16 + lr) * g.pstr + lk * 8;
+                const uint16_t* vb = reinterpret_cast<const uint16_t*>(smem + g.v_off) + tc * 16;
+                mma_bf16_vt<NT, kVlo>(ph, ph + MQ * g.pstr, vb, (g.vl_off - g.v_off) / 2, g.vstr,
+                                      step, NK, acc);
 #pragma unroll
                 for (int u = 0; u < NT; ++u) {
                     if (u >= left) break;
@@ -1165,9 +1133,9 @@ int per_cu_t(int lds) {
 
 }  // namespace
 
-int fused_small_lds_bytes(int dtype, int pek, int MB, int Lk, int dc) {
+int fused_small_lds_bytes(int dtype, int pek, int MB, int Lk, int dc, int nchunk) {
     const bool bf16 = dtype == kDtypeBF16;
-    return make_geo(bf16, bf16 && pek != kPeNone, MB, Lk, dc).bytes;
+    return make_geo(!bf16, pek != kPeNone, nchunk > 1, MB, Lk, dc).bytes;
 }
 
 int fused_small_per_cu(int dtype, int pek, int lds) {
@@ -1191,7 +1159,7 @@ hipError_t launch_fused_small(int dtype, int pek, const void* Q, const void* K, 
     const int QB = (Lq + MB - 1) / MB;
     FusedArgs a{Q, K, V, O, part, red, epochs, done, status, Lq, Lk, D, dc, nchunk,
                 MB, QB, gather1, BH * QB, xctr, scale, pq, pk};
-    const int lds = fused_small_lds_bytes(dtype, pek, MB, Lk, dc);
+    const int lds = fused_small_lds_bytes(dtype, pek, MB, Lk, dc, nchunk);
     // an XL plan with one slice has no exchange: the plain form does the same
     const bool xl = xcd != 0 && nchunk > 1;
 #define ATN_FUSED_PE(T, XLV)                                                                \

@@ -366,12 +366,15 @@ __device__ __forceinline__ void nt_exp_epilogue(const GemmArgs& g, v16f (&acc)[T
             }
         return;
     }
+    // edge tile: columns past N (E = exp(-inf) = 0) are written too up to
+    // the row stride ldc, so the padding of an E row (ldc = N rounded up to
+    // 8 keys) holds zeros for the PV GEMM's 8-key chunks
 #pragma unroll
     for (int i = 0; i < TI; ++i)
 #pragma unroll
         for (int j = 0; j < TJ; ++j) {
             const int col = n0 + wn + j * 32 + lc;
-            if (col >= g.N) continue;
+            if (col >= g.ldc) continue;
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int row = m0 + rloc(i, r);
@@ -1980,8 +1983,8 @@ int device_cus() {
 }  // namespace
 
 hipError_t launch_gemm_qk(int f16, const uint16_t* Q, const uint16_t* K, const float* qinv,
-                          const float* kinv, uint16_t* E, float* st_m, float* st_l, int BH, int Lq,
-                          int Lk, int D, float scale, hipStream_t st) {
+                          const float* kinv, uint16_t* E, int ldE, float* st_m, float* st_l,
+                          int BH, int Lq, int Lk, int D, float scale, hipStream_t st) {
     GemmArgs g{};
     g.A = Q;
     g.B = K;
@@ -1995,10 +1998,10 @@ hipError_t launch_gemm_qk(int f16, const uint16_t* Q, const uint16_t* K, const f
     g.K = D;
     g.lda = D;
     g.ldb = D;
-    g.ldc = Lk;
+    g.ldc = ldE;
     g.sa = (long)Lq * D;
     g.sb = (long)Lk * D;
-    g.sc = (long)Lq * Lk;
+    g.sc = (long)Lq * ldE;
     g.tiles_m = (Lq + kBM - 1) / kBM;
     g.tiles_n = (Lk + kBN - 1) / kBN;
     g.heads = BH;
@@ -2026,9 +2029,9 @@ hipError_t launch_gemm_qk(int f16, const uint16_t* Q, const uint16_t* K, const f
 }
 
 hipError_t launch_gemm_qk_enc(int benc, const uint16_t* Qe, const uint16_t* K, const float* qinv,
-                              const uint16_t* tab, int tab_rows, uint16_t* E, float* st_m,
-                              float* st_l, int BH, int Lq, int Lk, int D, float scale,
-                              hipStream_t st) {
+                              const uint16_t* tab, int tab_rows, uint16_t* E, int ldE,
+                              float* st_m, float* st_l, int BH, int Lq, int Lk, int D,
+                              float scale, hipStream_t st) {
     // an even number of 64-deep K steps (the kernel runs them in pairs)
     if ((benc != kBEncRaw && (tab == nullptr || tab_rows < Lk)) || D % 128 != 0)
         return hipErrorInvalidValue;
@@ -2045,10 +2048,10 @@ hipError_t launch_gemm_qk_enc(int benc, const uint16_t* Qe, const uint16_t* K, c
     g.K = D;
     g.lda = D;
     g.ldb = D;
-    g.ldc = Lk;
+    g.ldc = ldE;
     g.sa = (long)Lq * D;
     g.sb = (long)Lk * D;
-    g.sc = (long)Lq * Lk;
+    g.sc = (long)Lq * ldE;
     g.tiles_m = (Lq + kBM - 1) / kBM;
     g.tiles_n = (Lk + kBN - 1) / kBN;
     g.heads = BH;
@@ -2149,7 +2152,7 @@ hipError_t launch_encode_f16(int pek, const uint16_t* in, uint16_t* out, float* 
     return hipGetLastError();
 }
 
-hipError_t launch_gemm_pv(const uint16_t* E, float* st_m, float* st_l, float* ga,
+hipError_t launch_gemm_pv(const uint16_t* E, int ldE, float* st_m, float* st_l, float* ga,
                           const uint16_t* V, uint16_t* O, int BH, int Lq, int Lk, int D,
                           hipStream_t st) {
     GemmArgs g{};
@@ -2172,10 +2175,10 @@ hipError_t launch_gemm_pv(const uint16_t* E, float* st_m, float* st_l, float* ga
     g.M = Lq;
     g.N = D;
     g.K = Lk;
-    g.lda = Lk;
+    g.lda = ldE;
     g.ldb = D;
     g.ldc = D;
-    g.sa = (long)Lq * Lk;
+    g.sa = (long)Lq * ldE;
     g.sb = (long)Lk * D;
     g.sc = (long)Lq * D;
     g.tiles_m = (Lq + kBM - 1) / kBM;

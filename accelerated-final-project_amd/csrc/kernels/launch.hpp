@@ -29,7 +29,7 @@ hipError_t launch_pv(int dtype, const float* P, const void* V, void* O, int BH, 
 // kXcdGroupsPerXcd row groups per XCD).
 constexpr int kXcdCtrWords = 256;                    // counter words per XCD (1 KiB)
 constexpr int kXcdGroupsPerXcd = kXcdCtrWords / 2;  // two counters per row group
-int fused_small_lds_bytes(int dtype, int pek, int MB, int Lk, int dc);
+int fused_small_lds_bytes(int dtype, int pek, int MB, int Lk, int dc, int nchunk);
 // resident workgroups per CU for this LDS size (either exchange)
 int fused_small_per_cu(int dtype, int pek, int lds);
 hipError_t launch_fused_small(int dtype, int pek, const void* Q, const void* K, const void* V,
@@ -39,25 +39,25 @@ hipError_t launch_fused_small(int dtype, int pek, const void* Q, const void* K, 
                               int gather1, int xcd, float scale, const PeSide& pq,
                               const PeSide& pk, hipStream_t st);
 // Long-sequence bf16 path (gemm_path.hip): E = exp(scale Q K^T - tile row
-// max) (fp16) with per-(row, 256-key tile) max and sum, per-row factors
-// g_t = exp(m_t - m) / l, O = (E g) V.  Needs D % 8 == 0, Lk % 8 == 0 and
-// 16-byte aligned bases.
+// max) (fp16, rows ldE = Lk rounded up to 8 apart, zero past Lk) with
+// per-(row, 256-key tile) max and sum, per-row factors g_t = exp(m_t - m) /
+// l, O = (E g) V.  Needs D % 8 == 0 and 16-byte aligned bases.
 hipError_t launch_encode_f16(int pek, const uint16_t* in, uint16_t* out, float* inv, long n_rows,
                              int seq_len, int D, const PeSide& pe, hipStream_t st);
 hipError_t launch_gemm_qk(int f16, const uint16_t* Q, const uint16_t* K, const float* qinv,
-                          const float* kinv, uint16_t* E, float* st_m, float* st_l, int BH, int Lq,
-                          int Lk, int D, float scale, hipStream_t st);
+                          const float* kinv, uint16_t* E, int ldE, float* st_m, float* st_l,
+                          int BH, int Lq, int Lk, int D, float scale, hipStream_t st);
 // QK^T GEMM on fp16 Q~ (row scales qinv) and raw bf16 K, K's encoding
 // applied in the kernel from an fp16 table (tab: tab_rows positions x D
 // 16-bit units); needs D % 128 == 0.
 constexpr int kGemmEncRaw = 1, kGemmEncSin = 2, kGemmEncRope = 3, kGemmEncRopeHalf = 4;
 hipError_t launch_gemm_qk_enc(int benc, const uint16_t* Qe, const uint16_t* K, const float* qinv,
-                              const uint16_t* tab, int tab_rows, uint16_t* E, float* st_m,
-                              float* st_l, int BH, int Lq, int Lk, int D, float scale,
-                              hipStream_t st);
+                              const uint16_t* tab, int tab_rows, uint16_t* E, int ldE,
+                              float* st_m, float* st_l, int BH, int Lq, int Lk, int D,
+                              float scale, hipStream_t st);
 // O = P V from E and the QK^T epilogue's tile statistics (st_m, st_l); ga
 // holds the softmax factors of rows with more than 8 key tiles.
-hipError_t launch_gemm_pv(const uint16_t* E, float* st_m, float* st_l, float* ga,
+hipError_t launch_gemm_pv(const uint16_t* E, int ldE, float* st_m, float* st_l, float* ga,
                           const uint16_t* V, uint16_t* O, int BH, int Lq, int Lk, int D,
                           hipStream_t st);
 

@@ -282,7 +282,8 @@ int atn_prepare_pe_ex(const atn_pe_desc *pe, int head_d, int max_positions);
  * units. */
 #define ATN_PATH_FUSED_SMALL 1 /* one launch: split-D slices + device-side S all-reduce */
 #define ATN_PATH_SPLIT_D 2     /* three launches: partial QK^T, softmax, PV */
-#define ATN_PATH_GEMM 3        /* bf16, len_q/len_k >= 128: MFMA QK^T GEMM, row softmax, MFMA PV GEMM */
+#define ATN_PATH_GEMM 3        /* bf16, D % 8 == 0, outside the single-launch window: MFMA QK^T GEMM,
+                                  row softmax, MFMA PV GEMM */
 int atn_attention_path_ex(int dtype, int batch, int heads, int len_q, int len_k, int head_d,
                           const atn_pe_desc *pe);
 

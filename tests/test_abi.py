@@ -153,6 +153,13 @@ def test_path_selection_without_device(am):
     assert am.path(0, 4, 32, 512, 512, 128) == am.ATN_PATH_SPLIT_D
     assert am.path(0, 1, 1, 3, 129, 36) == am.ATN_PATH_SPLIT_D
     assert am.path(0, 1, 300, 16, 16, 64) == am.ATN_PATH_SPLIT_D           # more heads than CUs
+    # bf16 outside the single-launch window runs on the MFMA GEMM path
+    # whenever D % 8 == 0, whatever len_q and len_k are
+    assert am.path(1, 8, 8, 1024, 1024, 4096) == am.ATN_PATH_GEMM          # config 4
+    assert am.path(1, 1, 8, 64, 4096, 2048) == am.ATN_PATH_GEMM
+    assert am.path(1, 1, 4, 100, 100, 2048) == am.ATN_PATH_GEMM
+    assert am.path(1, 1, 2, 200, 20, 512) == am.ATN_PATH_GEMM
+    assert am.path(1, 1, 2, 200, 20, 36) == am.ATN_PATH_SPLIT_D           # D % 8 != 0
     assert am.path(0, 0, 4, 64, 64, 2048) == -2
 
 

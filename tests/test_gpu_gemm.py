@@ -192,3 +192,35 @@ def test_gemm_graph_replays_match_eager(am, dev, shape, pe):
     st.destroy()
     n, nrel, mabs = H.check_bf16(eager.numpy(), _ref(pe, Q, K, V, Lq, Lk, D))
     assert n == 0, f"normwise rel {nrel}, max abs {mabs}"
+
+
+GAP_SHAPES = [(1, 8, 64, 4096, 2048), (1, 4, 100, 100, 2048), (1, 2, 16, 300, 256),
+              (2, 3, 70, 40, 128), (1, 1, 1, 200, 64), (1, 2, 200, 20, 512)]
+
+
+@pytest.mark.parametrize("shape", GAP_SHAPES, ids=lambda s: "x".join(map(str, s)))
+@pytest.mark.parametrize("pe", ["none", "rope_half", "sinusoidal"])
+def test_gemm_path_covers_gap_shapes(am, dev, shape, pe):
+    """bf16 shapes outside the single-launch window (len_q <= 64 with
+    len_k > 128, or 64 < len_q < 128) and below 128 rows or keys, including
+    key counts that are not a multiple of 8 (E rows padded to 8 keys, the
+    padding written as zeros): they run on the MFMA GEMM path, not the VALU
+    split-D pipeline, and match the oracle."""
+    import hip_rt
+    B, Hh, Lq, Lk, D = shape
+    print(f"[case] gemm gap shape {shape} {pe}", flush=True)
+    desc = _desc(am, pe)
+    assert am.path(1, B, Hh, Lq, Lk, D, desc) == am.ATN_PATH_GEMM
+    sigma = 0.5 if pe == "sinusoidal" else 1.0
+    (q, k, v), (Q, K, V) = H.device_inputs((B, Hh, Lq, D), (B, Hh, Lk, D), 313 + Lk, "bf16",
+                                           sigma)
+    out = H.empty(Q.shape, "bf16")
+    am.attention_ex(q, k, v, out, pe=desc)
+    hip_rt.synchronize()
+    rows = None if B * Hh * Lq <= 512 else (0, 64)
+    ref = _ref(pe, Q, K, V, Lq, Lk, D, rows=rows)
+    got = out.numpy()
+    if rows is not None:
+        got, ref = got.reshape(-1, D)[rows[0]:rows[1]], ref.reshape(-1, D)[rows[0]:rows[1]]
+    n, nrel, mabs = H.check_bf16(got, ref)
+    assert n == 0, f"normwise rel {nrel}, max abs {mabs}"
