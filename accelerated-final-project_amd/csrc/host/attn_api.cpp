@@ -676,40 +676,82 @@ GemmPlan gemm_plan(int dtype, const Shape& s, const PePlan& plan) {
 }
 
 // ---------------------------------------------------------------- core
-// no_alloc: the allocation-free form -- scratch is the device's static
-// array, and a call that would need a library allocation (tables not yet
-// built) or more scratch than the array holds is refused.
-int attention_core(int dtype, const void* Q, const void* K, const void* V, void* out, int B,
-                   int H, int Lq, int Lk, int D, const atn_pe_desc* pe, void* workspace,
-                   size_t workspace_bytes, hipStream_t stream, bool no_alloc = false) {
-    if (dtype != ATN_DTYPE_F32 && dtype != ATN_DTYPE_BF16) return ATN_ERR_BAD_ARGUMENT;
-    if (!Q || !K || !V || !out) return ATN_ERR_NULL_POINTER;
-    Shape s;
-    int st = check_shape(B, H, Lq, Lk, D, &s);
-    if (st != ATN_OK) return st;
-    const size_t es = elem_size(dtype);
-    for (const void* p : {Q, K, V, (const void*)out})
-        if (!aligned(p, es)) return ATN_ERR_MISALIGNED;
-    const int64_t qb = s.nq * (int64_t)es, kb = s.nk * (int64_t)es;
-    if (overlaps(out, qb, Q, qb) || overlaps(out, qb, K, kb) || overlaps(out, qb, V, kb))
-        return ATN_ERR_ALIASING;
-    PePlan plan;
-    st = check_pe(pe, D, &plan);
-    if (st != ATN_OK) return st;
+// Scratch the library may use for one call before splitting it: the
+// caller's workspace size, the allocation-free array, or this cap for the
+// library's own workspace (ATN_WORKSPACE_CAP_MIB overrides, for tests).
+size_t library_cap() {
+    const int mib = env_int("ATN_WORKSPACE_CAP_MIB");
+    return mib > 0 ? (size_t)mib << 20 : (size_t)1 << 30;
+}
+
+// Scratch bytes of the path a call of shape s takes: fused (when planned and
+// vector-aligned), else GEMM (when planned and 16-byte aligned), else the
+// split-D pipeline.  vec / a16: the alignment of the call's pointers; pass
+// -1 for "unknown" and get the largest of the candidate paths instead.
+size_t path_need(int dtype, const Shape& s, const PePlan& plan, bool query_device, int vec,
+                 int a16) {
+    const FusedPlan fp = fused_plan(dtype, plan.pek, s, query_device);
+    const GemmPlan gp = gemm_plan(dtype, s, plan);
+    const size_t split = kSyncBytes + stream_plan(s).bytes;
+    if (vec < 0 || a16 < 0)
+        return std::max({fp.ok ? fp.bytes : (size_t)0, gp.ok ? gp.bytes : (size_t)0, split});
+    if (fp.ok && vec) return fp.bytes;
+    if (gp.ok && a16) return gp.bytes;
+    return split;
+}
+
+// How a call too large for its scratch is split: chunks of `heads`
+// consecutive (batch, head) pairs, or, when one head is still too large,
+// chunks of `rows` query rows of one head (K and V whole).  Each chunk is an
+// independent attention call: rows depend only on their own query row and
+// all keys.
+struct Chunking {
+    int heads = 0, rows = 0;  // heads == 0: no chunk fits
+    size_t need = 0;          // largest chunk's scratch
+};
+
+Chunking plan_chunks(int dtype, const Shape& s, const PePlan& plan, size_t cap,
+                     bool query_device, int vec, int a16) {
+    auto need_of = [&](int h, int rows) {
+        Shape c;
+        check_shape(1, h, rows, s.Lk, s.D, &c);
+        return path_need(dtype, c, plan, query_device, vec, a16);
+    };
+    Chunking ch;
+    int h = (int)s.BH;
+    size_t n = need_of(h, s.Lq);
+    while (h > 1 && n > cap) {
+        h = (h + 1) / 2;
+        n = need_of(h, s.Lq);
+    }
+    if (n <= cap) {
+        ch.heads = h;
+        ch.rows = s.Lq;
+        ch.need = n;
+        return ch;
+    }
+    int r = s.Lq;
+    while (r > 1 && n > cap) {
+        r = (r + 1) / 2;
+        n = need_of(1, r);
+    }
+    if (n <= cap) {
+        ch.heads = 1;
+        ch.rows = r;
+        ch.need = n;
+    }
+    return ch;
+}
+
+// One call of the chosen path on (a chunk of) the job, tables already
+// bound; plan.q's tables start at the chunk's first query position.
+int attention_run(int dtype, const void* Q, const void* K, const void* V, void* out,
+                  const Shape& s, const PePlan& plan, int dev, void* workspace,
+                  size_t workspace_bytes, hipStream_t stream, bool no_alloc) {
+    const int Lq = s.Lq, Lk = s.Lk, D = s.D;
+    int st = ATN_OK;
     const GemmPlan gp = gemm_plan(dtype, s, plan);
     const StreamPlan sp = stream_plan(s);
-    // every path needs at least the sync region; the path-specific size is
-    // checked once the device has chosen the path
-    if (workspace != nullptr && workspace_bytes < kSyncBytes) return ATN_ERR_WORKSPACE;
-    const int64_t tiles = s.BH * ((Lq + 63) / 64) * ((Lk + 63) / 64) * sp.nsplit;
-    const int64_t pv_tiles = s.BH * ((Lq + 63) / 64) * ((D + 63) / 64);
-    if (tiles > (1LL << 24) || pv_tiles > (1LL << 24)) return ATN_ERR_SIZE_OVERFLOW;
-
-    int dev;
-    st = current_device(&dev);
-    if (st != ATN_OK) return st;
-    st = bind_tables(pe, plan, D, Lq > Lk ? Lq : Lk, stream, no_alloc);
-    if (st != ATN_OK) return st;
     // the device's own capacity decides between the single-launch kernel
     // and the three-kernel pipeline
     const FusedPlan fd = fused_plan(dtype, plan.pek, s, true);
@@ -804,6 +846,88 @@ int attention_core(int dtype, const void* Q, const void* K, const void* V, void*
     ATN_HIP(atn::launch_softmax(S, P, s.BH * Lq, Lk, sp.nsplit, (size_t)s.BH * Lq * Lk, scale,
                                 stream));
     ATN_HIP(atn::launch_pv(dtype, P, V, out, (int)s.BH, Lq, Lk, D, vec_vo, stream));
+    return ATN_OK;
+}
+
+
+// no_alloc: the allocation-free form -- scratch is the device's static
+// array, and a call that would need a library allocation (tables not yet
+// built) is refused.  A call whose scratch would exceed the cap (the
+// caller's workspace, the static array, or library_cap()) is run in chunks
+// of heads or query rows that fit it.
+int attention_core(int dtype, const void* Q, const void* K, const void* V, void* out, int B,
+                   int H, int Lq, int Lk, int D, const atn_pe_desc* pe, void* workspace,
+                   size_t workspace_bytes, hipStream_t stream, bool no_alloc = false) {
+    if (dtype != ATN_DTYPE_F32 && dtype != ATN_DTYPE_BF16) return ATN_ERR_BAD_ARGUMENT;
+    if (!Q || !K || !V || !out) return ATN_ERR_NULL_POINTER;
+    Shape s;
+    int st = check_shape(B, H, Lq, Lk, D, &s);
+    if (st != ATN_OK) return st;
+    const size_t es = elem_size(dtype);
+    for (const void* p : {Q, K, V, (const void*)out})
+        if (!aligned(p, es)) return ATN_ERR_MISALIGNED;
+    const int64_t qb = s.nq * (int64_t)es, kb = s.nk * (int64_t)es;
+    if (overlaps(out, qb, Q, qb) || overlaps(out, qb, K, kb) || overlaps(out, qb, V, kb))
+        return ATN_ERR_ALIASING;
+    PePlan plan;
+    st = check_pe(pe, D, &plan);
+    if (st != ATN_OK) return st;
+    // every path needs at least the sync region; the path-specific size is
+    // checked once the device has chosen the path
+    if (workspace != nullptr && workspace_bytes < kSyncBytes) return ATN_ERR_WORKSPACE;
+    {
+        const StreamPlan sp = stream_plan(s);
+        const int64_t tiles = s.BH * ((Lq + 63) / 64) * ((Lk + 63) / 64) * sp.nsplit;
+        const int64_t pv_tiles = s.BH * ((Lq + 63) / 64) * ((D + 63) / 64);
+        if (tiles > (1LL << 24) || pv_tiles > (1LL << 24)) return ATN_ERR_SIZE_OVERFLOW;
+    }
+
+    int dev;
+    st = current_device(&dev);
+    if (st != ATN_OK) return st;
+    st = bind_tables(pe, plan, D, Lq > Lk ? Lq : Lk, stream, no_alloc);
+    if (st != ATN_OK) return st;
+
+    const size_t cap = no_alloc ? atn::kNoAllocScratchBytes
+                                : (workspace != nullptr ? workspace_bytes : library_cap());
+    // chunk pointers keep the base alignment when a row is a multiple of 16
+    // bytes; otherwise plan for the largest path
+    const size_t va = dtype == ATN_DTYPE_F32 ? 16 : 8;
+    const bool rows16 = ((size_t)D * es) % 16 == 0;
+    const int vec = rows16 ? ((D % 4 == 0) && aligned(Q, va) && aligned(K, va) &&
+                              aligned(V, va) && aligned(out, va))
+                           : -1;
+    const int a16 = rows16 ? (aligned(Q, 16) && aligned(K, 16) && aligned(V, 16) &&
+                              aligned(out, 16))
+                           : -1;
+    if (path_need(dtype, s, plan, true, vec, a16) <= cap)
+        return attention_run(dtype, Q, K, V, out, s, plan, dev, workspace, workspace_bytes,
+                             stream, no_alloc);
+    const Chunking ch = plan_chunks(dtype, s, plan, cap, true, vec, a16);
+    if (ch.heads == 0) return no_alloc ? ATN_ERR_SCRATCH_LIMIT : ATN_ERR_WORKSPACE;
+    const char* q8 = static_cast<const char*>(Q);
+    const char* k8 = static_cast<const char*>(K);
+    const char* v8 = static_cast<const char*>(V);
+    char* o8 = static_cast<char*>(out);
+    const size_t qrow = (size_t)D * es;
+    for (int64_t bh0 = 0; bh0 < s.BH; bh0 += ch.heads) {
+        const int h = (int)std::min<int64_t>(ch.heads, s.BH - bh0);
+        for (int r0 = 0; r0 < Lq; r0 += ch.rows) {
+            const int rows = std::min(ch.rows, Lq - r0);
+            Shape c;
+            check_shape(1, h, rows, Lk, D, &c);
+            PePlan pc = plan;
+            if (r0 > 0 && pc.pek != atn::kPeNone) {
+                // positions of this chunk's query rows start at r0
+                pc.q.a += (size_t)r0 * pc.q.ld;
+                pc.q.b += (size_t)r0 * pc.q.ld;
+            }
+            const size_t qoff = ((size_t)bh0 * Lq + r0) * qrow, koff = (size_t)bh0 * Lk * qrow;
+            st = attention_run(dtype, q8 + qoff, k8 + koff, v8 + koff, o8 + qoff, c, pc, dev,
+                               workspace, workspace_bytes, stream, no_alloc);
+            if (st != ATN_OK) return st;
+        }
+    }
     return ATN_OK;
 }
 
@@ -981,10 +1105,12 @@ size_t atn_attention_workspace_bytes(int dtype, int batch, int heads, int len_q,
     if (check_shape(batch, heads, len_q, len_k, head_d, &s) != ATN_OK) return 0;
     PePlan plan;
     if (check_pe(pe, head_d, &plan) != ATN_OK) return 0;
-    const FusedPlan fp = fused_plan(dtype, plan.pek, s, false);
-    const GemmPlan gp = gemm_plan(dtype, s, plan);
-    return std::max({fp.ok ? fp.bytes : (size_t)0, gp.ok ? gp.bytes : (size_t)0,
-                     kSyncBytes + stream_plan(s).bytes});
+    // the largest workspace of every plan the call could take, or, when that
+    // exceeds the library's cap, of the chunks the call then runs in
+    const size_t full = path_need(dtype, s, plan, false, -1, -1);
+    if (full <= library_cap()) return full;
+    const Chunking ch = plan_chunks(dtype, s, plan, library_cap(), false, -1, -1);
+    return ch.heads > 0 ? ch.need : full;
 }
 
 int atn_pe_apply_ex(int dtype, const void* in, void* out, long n_rows, int seq_len, int head_d,

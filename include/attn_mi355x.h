@@ -254,7 +254,11 @@ int atn_attention_fwd_noalloc_ex(int dtype, const void *Q, const void *K, const 
                                  void *out, int batch, int heads, int len_q, int len_k,
                                  int head_d, const atn_pe_desc *pe, void *stream);
 
-/* Scratch bytes atn_attention_fwd_ex needs for this shape (0 on bad input). */
+/* Scratch bytes atn_attention_fwd_ex needs for this shape (0 on bad input).
+ * Scratch is bounded: a call whose scratch would exceed its cap -- the
+ * caller's workspace_bytes, or 1 GiB for the library's own workspace -- runs
+ * in chunks of consecutive (batch, head) pairs, or of query rows of one head,
+ * that fit; this query never reports more than the cap. */
 size_t atn_attention_workspace_bytes(int dtype, int batch, int heads, int len_q, int len_k,
                                      int head_d, const atn_pe_desc *pe);
 

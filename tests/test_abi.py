@@ -214,3 +214,16 @@ def test_python_binding_checks_shapes(am):
     with pytest.raises(ValueError):
         am._check(Fake(), "f32", (1,), "Q")
     assert hip_rt.bf16_bits_to_f32(hip_rt.f32_to_bf16_bits(np.float32([1.5])))[0] == 1.5
+
+
+def test_workspace_bytes_bounded_by_the_cap(am, monkeypatch):
+    """The size query never asks for more than the library's scratch cap
+    (1 GiB by default): a larger shape runs in chunks of heads or query rows,
+    and the query reports the largest chunk's need."""
+    big = am.workspace_bytes(1, 1, 64, 8192, 8192, 128)   # E alone would be 8 GiB
+    assert 0 < big <= 1 << 30
+    small = am.workspace_bytes(1, 1, 4, 512, 512, 128)
+    assert small < 1 << 30
+    monkeypatch.setenv("ATN_WORKSPACE_CAP_MIB", "1")
+    assert am.workspace_bytes(1, 1, 4, 512, 512, 128) <= 1 << 20
+    assert am.workspace_bytes(1, 1, 64, 8192, 8192, 128) <= 1 << 20

@@ -4,9 +4,10 @@ Its kernels are the ones atn_attention_fwd_ex runs, with scratch in the
 library's per-device static array instead of a workspace, so its outputs must
 equal atn_attention_fwd_ex's bit for bit.  Each case makes two calls in a
 row -- the second with a smaller input -- so the second call runs on the
-array the first one left behind.  Calls beyond the array's 64 MiB and
-encodings whose tables were never prepared are refused with their status
-codes, with nothing launched.
+array the first one left behind.  Larger shapes run in chunks that fit the
+array's 64 MiB; a shape whose smallest chunk does not fit, and encodings
+whose tables were never prepared, are refused with their status codes, with
+nothing launched.
 """
 import numpy as np
 import pytest
@@ -56,24 +57,34 @@ def test_noalloc_matches_ex_two_calls(am, dev, first, second, dtype, pe):
         _pair(am, shp, dtype, desc, 900 + i)
 
 
+def test_noalloc_chunks_large_shapes(am, dev):
+    """A shape whose scratch exceeds the 64 MiB array (E alone is 128 MiB
+    here) runs in chunks of heads that fit it, with the same bits as the
+    unchunked atn_attention_fwd_ex."""
+    shape = (4, 8, 1024, 2048, 256)
+    print(f"[case] noalloc chunked {shape}", flush=True)
+    _pair(am, shape, "bf16", None, 950)
+
+
 def test_noalloc_refuses_what_it_cannot_do(am, dev):
     import hip_rt
     print("[case] noalloc refusals", flush=True)
     L_ = am.lib()
-    # config 4 needs far more than 64 MiB of scratch (E alone is 128 MiB):
-    # refused before anything is launched
-    B, Hh, L, D = 8, 8, 1024, 4096
-    desc = am.make_pe("rope", pairing="half")
-    assert L_.atn_prepare_pe_ex(desc, D, L) == 0
-    q, k, v, o = (hip_rt.DeviceArray((B, Hh, L, D), "bf16") for _ in range(4))
-    st = L_.atn_attention_fwd_noalloc_ex(1, q.ptr, k.ptr, v.ptr, o.ptr, B, Hh, L, L, D, desc, None)
+    # one query row against 32 Mi keys: even a one-row chunk needs 64 MiB of
+    # scores -- refused before anything is launched
+    Lk = 1 << 25
+    q, o = hip_rt.DeviceArray((1, 1, 1, 8), "bf16"), hip_rt.DeviceArray((1, 1, 1, 8), "bf16")
+    k, v = hip_rt.DeviceArray((1, 1, Lk, 8), "bf16"), hip_rt.DeviceArray((1, 1, Lk, 8), "bf16")
+    st = L_.atn_attention_fwd_noalloc_ex(1, q.ptr, k.ptr, v.ptr, o.ptr, 1, 1, 1, Lk, 8, None,
+                                         None)
     assert st == am.ATN_ERR_SCRATCH_LIMIT, st
     # an encoding base whose tables were never built
     odd = am.make_pe("rope", pairing="half", base=1234.5)
-    st = L_.atn_attention_fwd_noalloc_ex(1, q.ptr, k.ptr, v.ptr, o.ptr, 1, 1, 64, 64, 256, odd,
-                                         None)
+    qs, os_ = (hip_rt.DeviceArray((1, 1, 64, 256), "bf16") for _ in range(2))
+    st = L_.atn_attention_fwd_noalloc_ex(1, qs.ptr, qs.ptr, qs.ptr, os_.ptr, 1, 1, 64, 64, 256,
+                                         odd, None)
     assert st == am.ATN_ERR_NOT_PREPARED, st
     hip_rt.synchronize()
     assert am.sync_status() == 0
-    for t in (q, k, v, o):
+    for t in (q, o, k, v, qs, os_):
         t.free()
