@@ -15,6 +15,14 @@ caches (final/rope.cu:20-40, final/sinusoidal.cu:838-855), then attends.
 
 The printed max |difference| against torch SDPA is context only; parity is
 established against the CPU oracle by the test suite.
+
+One HIP runtime.  This process hands torch's device pointers and stream to
+the library, which is only sound if both use the same HIP runtime.  torch's
+bundled libamdhip64 and /opt/rocm's carry the same SONAME
+(libamdhip64.so.7), so once torch is imported the loader binds the library
+to torch's copy; hip_runtimes_mapped() reads /proc/self/maps to confirm that
+exactly one libamdhip64 is mapped, the run stops otherwise, and the path is
+printed and recorded in the JSON output.
 """
 from __future__ import annotations
 
@@ -41,6 +49,17 @@ SHAPES = [
     ("cfg4 rope-half", "bf16", 8, 8, 1024, 1024, 4096, "rope_half"),
     ("cfg5 sinusoidal", "bf16", 4, 16, 256, 2048, 1024, "sinusoidal"),
 ]
+
+
+def hip_runtimes_mapped() -> list[str]:
+    """Distinct libamdhip64 files mapped into this process."""
+    paths = set()
+    with open("/proc/self/maps") as f:
+        for line in f:
+            parts = line.split()
+            if len(parts) >= 6 and "libamdhip64" in os.path.basename(parts[-1]):
+                paths.add(parts[-1])
+    return sorted(paths)
 
 
 def tables(torch, pe, npos, D, dev):
@@ -83,8 +102,13 @@ def main():
         sys.exit(1)
     dev = torch.device("cuda:0")
     lib = am.lib()
+    runtimes = hip_runtimes_mapped()
+    if len(runtimes) != 1:
+        print(f"torch_compare.py: {len(runtimes)} HIP runtimes mapped ({runtimes}); torch's "
+              "device pointers cannot be handed to the library", file=sys.stderr)
+        sys.exit(1)
     print(f"GPU: {torch.cuda.get_device_name(0)}  torch {torch.__version__}  "
-          f"HIP {torch.version.hip}", flush=True)
+          f"HIP {torch.version.hip}  runtime {runtimes[0]}", flush=True)
 
     def timed(fn):
         for _ in range(a.warmup):
@@ -160,7 +184,8 @@ def main():
         diff = float((out.float() - ref.float()).abs().max())
         flops = 4 * B * H * Lq * Lk * D
         alg_bytes = (2 * B * H * Lq * D + 2 * B * H * Lk * D) * (4 if dt == "f32" else 2)
-        row = {"shape": name, "dtype": dt, "B": B, "H": H, "Lq": Lq, "Lk": Lk, "D": D, "pe": pe,
+        row = {"shape": name, "hip_runtime": runtimes[0], "dtype": dt, "B": B, "H": H, "Lq": Lq,
+               "Lk": Lk, "D": D, "pe": pe,
                "ours_ms": t_ours, "torch_sdpa_ms": t_sdpa, "torch_naive_ms": t_naive,
                "ours_tflops": flops / t_ours / 1e9, "ours_gbs": alg_bytes / t_ours / 1e6,
                "speedup_vs_sdpa": t_sdpa / t_ours, "max_abs_diff_vs_sdpa": diff}

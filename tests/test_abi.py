@@ -227,3 +227,16 @@ def test_workspace_bytes_bounded_by_the_cap(am, monkeypatch):
     monkeypatch.setenv("ATN_WORKSPACE_CAP_MIB", "1")
     assert am.workspace_bytes(1, 1, 4, 512, 512, 128) <= 1 << 20
     assert am.workspace_bytes(1, 1, 64, 8192, 8192, 128) <= 1 << 20
+
+
+def test_torch_and_library_share_one_hip_runtime():
+    """torch's bundled libamdhip64 and /opt/rocm's share the SONAME
+    libamdhip64.so.7: with torch imported first, loading the library maps no
+    second HIP runtime (what torch_compare.py relies on to pass torch's
+    device pointers in)."""
+    code = ("import torch, sys; sys.path.insert(0, %r); import attn_mi355x as am; am.lib(); "
+            "import torch_compare as tc; r = tc.hip_runtimes_mapped(); print(len(r), r)"
+            % os.path.join(ROOT, "accelerated-final-project_amd"))
+    r = _child(code)
+    assert r.returncode == 0, r.stderr[-2000:]
+    assert r.stdout.split()[0] == "1", r.stdout
