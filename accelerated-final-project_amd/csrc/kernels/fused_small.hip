@@ -297,29 +297,39 @@ __device__ __forceinline__ void ld_words(const float* base, int stride, int cnt,
 // only after every wave's exchange stores have completed (s_waitcnt before
 // the barrier), so they are in L2 once the count is complete.  Returns false
 // for the whole workgroup on timeout.
-__device__ bool xcd_arrive(__amdgpu_buffer_rsrc_t rc, int k, unsigned share, bool wait,
-                           int* flag_lds) {
+__device__ __forceinline__ unsigned xcd_arrive_only(__amdgpu_buffer_rsrc_t rc, int k,
+                                                    unsigned share) {
+    unsigned old = 0;
+    if (threadIdx.x == 0)
+        old = (unsigned)__builtin_amdgcn_raw_ptr_buffer_atomic_add_i32((int)share, rc, 4 * k, 0,
+                                                                       0);
+    return __builtin_amdgcn_readlane(old, 0) & ~(kXcdUnits - 1u);  // wave 0's is the base
+}
+
+// The wait of xcd_arrive on its own, given wave 0's base.
+__device__ bool xcd_wait(__amdgpu_buffer_rsrc_t rc, int k, unsigned base, int* flag_lds) {
     if (threadIdx.x < 64) {
-        unsigned old = 0;
-        if (threadIdx.x == 0)
-            old = (unsigned)__builtin_amdgcn_raw_ptr_buffer_atomic_add_i32((int)share, rc, 4 * k,
-                                                                           0, 0);
-        const unsigned base = __builtin_amdgcn_readlane(old, 0) & ~(kXcdUnits - 1u);
         bool ok = true;
-        if (wait) {
-            for (int it = 0;; ++it) {
-                const unsigned v = __builtin_amdgcn_readfirstlane(
-                    __builtin_amdgcn_raw_buffer_load_b32(rc, 4 * k, 0, kAuxL2));
-                if (v - base == kXcdUnits) break;
-                if (it > kSpinLimit) {
-                    ok = false;
-                    break;
-                }
-                __builtin_amdgcn_s_sleep(1);
+        for (int it = 0;; ++it) {
+            const unsigned v = __builtin_amdgcn_readfirstlane(
+                __builtin_amdgcn_raw_buffer_load_b32(rc, 4 * k, 0, kAuxL2));
+            if (v - base == kXcdUnits) break;
+            if (it > kSpinLimit) {
+                ok = false;
+                break;
             }
+            __builtin_amdgcn_s_sleep(1);
         }
         if (threadIdx.x == 0 && !ok) *flag_lds = 0;
     }
+    __syncthreads();
+    return *flag_lds != 0;
+}
+
+__device__ bool xcd_arrive(__amdgpu_buffer_rsrc_t rc, int k, unsigned share, bool wait,
+                           int* flag_lds) {
+    const unsigned base = xcd_arrive_only(rc, k, share);
+    if (wait) return xcd_wait(rc, k, base, flag_lds);
     __syncthreads();
     return *flag_lds != 0;
 }
@@ -593,9 +603,10 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
     // gets an offset past the buffer); branch-free loads let the compiler
     // count them, so a round issues up to kQ row loads of Q and kKV of K and
     // of V before the first is encoded and stored, and when everything fits
-    // one round, V is only written to LDS after the exchange (its latency
-    // hides behind the exchange's).  (The host sends this kernel only shapes
-    // with D % 4 == 0 and aligned bases.)
+    // one round, V is only written to LDS once this workgroup's partial
+    // scores are out, while it waits for the other slices (its loads' latency
+    // and its stores both hide behind the exchange).  (The host sends this
+    // kernel only shapes with D % 4 == 0 and aligned bases.)
     typedef typename Raw4<T>::type Raw;
     constexpr int kQ = 8, kKV = 16;
     const int vpr = dc >> 2;
@@ -778,15 +789,22 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");  // stores stay above the wait
         __builtin_amdgcn_s_waitcnt(0);  // this wave's partials have completed
         __syncthreads();
-        if constexpr (!XL)
-            if (tid == 0) st_done(done1 + c, tag);
+        unsigned base1 = 0;
+        if constexpr (XL) base1 = xcd_arrive_only(rc, 0, share);
+        else if (tid == 0) st_done(done1 + c, tag);
         if (sh_failed) {  // an earlier call timed out: fail closed
             if constexpr (XL) {
-                xcd_arrive(rc, 0, share, false, &flag);
+                __syncthreads();
                 xl_leave_before_step2();
             }
             poison_slice<T>(O, orow0, Lq, D, d0, dc);
             return;
+        }
+        // V into LDS while the other slices of the group arrive
+        if (defer_v) {
+#pragma unroll
+            for (int u = 0; u < kKV; ++u)
+                if (u < ckv) store_v(r0 + u * rstep, bv[u]);
         }
         const float* pg = a.part + (size_t)rg * n * E;
         float* rd = a.red + (size_t)rg * E;
@@ -800,7 +818,7 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
         auto exchange = [&]() -> bool {
             float w[kMaxWords];
             if constexpr (XL) {
-                if (!xcd_arrive(rc, 0, share, true, &flag)) return false;
+                if (!xcd_wait(rc, 0, base1, &flag)) return false;
             } else {
                 if (!wait_done(done1, n, tag, &flag)) return false;
             }
@@ -978,7 +996,7 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
                 __hip_atomic_store(a.epochs + rg, epoch + 1u, __ATOMIC_RELAXED,
                                    __HIP_MEMORY_SCOPE_AGENT);
     }
-    if (defer_v) {
+    if (defer_v && n == 1) {
 #pragma unroll
         for (int u = 0; u < kKV; ++u)
             if (u < ckv) store_v(r0 + u * rstep, bv[u]);
