@@ -48,7 +48,8 @@ MALL_FLUSH_MIB = 512  # > the 256 MiB MALL: a copy this large evicts it
 # FETCH_SIZE / WRITE_SIZE and scaled by a known-size device copy; keyed by
 # (config, head_dim), with the profile that holds the counts.
 MEASURED_TRAFFIC = {
-    (2, 2048): ((14845 + 3081) * 1024, "profiles/fused_small_cfg2_traffic.md"),
+    (2, 2048): ((11839 + 3080) * 1024, "profiles/fused_small_cfg2_traffic.md"),
+    (3, 8192): ((21633 + 4368) * 1024, "profiles/fused_small_cfg3_kernel_trace.md"),
 }
 
 # (name, dtype, B, H, Lq, Lk, D, pe, sigma)

@@ -208,7 +208,7 @@ void precompute_sinusoidal_table(float *sin_table, float *cos_table, int seqlen,
  * (pe == NULL: plain SDPA).  workspace == NULL: library-managed scratch, one
  * per (device, stream), allocated zero-filled on first use and grown as
  * needed; else caller scratch of at least atn_attention_workspace_bytes(...)
- * bytes that was zero-filled once before its first use (its first 32 KiB
+ * bytes that was zero-filled once before its first use (its first 40 KiB
  * then hold synchronization words that stay valid from call to call, so it
  * must not be re-initialized while in use).  Calls that run at the same
  * time must not share a workspace.  Enqueued on stream; asynchronous; the
@@ -236,8 +236,10 @@ int atn_attention_fwd_ex(int dtype, const void *Q, const void *K, const void *V,
  * (64 MiB) on each GPU the library runs on, held until the process ends.
  * Same arguments, results and asynchronous semantics as atn_attention_fwd_ex
  * without the workspace, plus these limits:
- *   - a shape whose workspace (atn_attention_workspace_bytes for the path the
- *     device takes) exceeds the array returns ATN_ERR_SCRATCH_LIMIT;
+ *   - a shape whose scratch exceeds the array runs in chunks of (batch,
+ *     head) pairs or of query rows, as atn_attention_fwd_ex does with a
+ *     small workspace; a shape that no chunk fits (one head's rows too long
+ *     for the array) returns ATN_ERR_SCRATCH_LIMIT;
  *   - an encoding with library tables needs them built beforehand
  *     (atn_prepare_pe_ex), else ATN_ERR_NOT_PREPARED; caller tables need
  *     nothing;
