@@ -375,10 +375,6 @@ __device__ void poison_slice(T* O, size_t row0, int lq, int D, int d0, int dc) {
     }
 }
 
-// Buffer-load cache-policy operand bit that marks the access volatile for
-// the compiler (kept in program order, never sunk or merged).
-constexpr int kAuxVolatile = (int)(1u << 31);
-
 // 4 consecutive elements as loaded (fp32: 16 bytes; bf16: 8 bytes of raw
 // bits), widened to fp32 on demand.
 template <typename T>
@@ -533,7 +529,17 @@ __device__ __forceinline__ int wave_tiles(int wave, int nrb, int tiles, int* rb,
     return (tiles - *c0 + wpr - 1) / wpr;
 }
 
-template <typename T, int PEK, bool XL>
+// Whether every Q row and K/V row of a workgroup's slice fits one load
+// round (kQ row loads of Q, kKV of K and of V per thread): then V is loaded
+// with Q and K but written to LDS only while the workgroup waits for the
+// other slices.  The host picks the kernel variant by the same test.
+constexpr int kRoundQ = 8, kRoundKV = 16;
+__host__ __device__ inline bool fused_defer_v(int MQ, int NK, int dc) {
+    const int rstep = kThreads / (dc >> 2);
+    return (MQ + rstep - 1) / rstep <= kRoundQ && (NK + rstep - 1) / rstep <= kRoundKV;
+}
+
+template <typename T, int PEK, bool XL, bool DEFER>
 __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
     constexpr bool kBf16 = sizeof(T) == 2;
     // Q and K carry lo parts (fp32 inputs, or encoded bf16 inputs); V does
@@ -542,6 +548,21 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
     constexpr bool kVlo = !kBf16;
     extern __shared__ __align__(16) unsigned char smem[];
     __shared__ int flag;
+
+    // Every kernel argument in one batch of scalar loads, waited for once,
+    // here.  Left alone the compiler issues each load at its first use, and
+    // each argument line the scalar cache misses then costs a memory round
+    // trip in series: two or three of them before the first slice load was
+    // issued (2.4 us at config 2, 5.4 us at config 3, measured from the
+    // kernel's first instruction).
+    asm volatile("" ::"s"(a.Q), "s"(a.K), "s"(a.V), "s"(a.O), "s"(a.part), "s"(a.red),
+                 "s"(a.epochs), "s"(a.done), "s"(a.status), "s"(a.xctr), "s"(a.Lq), "s"(a.Lk),
+                 "s"(a.D), "s"(a.dc), "s"(a.nchunk), "s"(a.MB), "s"(a.QB), "s"(a.gather1),
+                 "s"(a.G), "s"(a.scale), "s"(gridDim.x));
+    if constexpr (PEK != kPeNone)
+        asm volatile("" ::"s"(a.pq.a), "s"(a.pq.b), "s"(a.pq.ld), "s"(a.pq.dup), "s"(a.pq.rotary),
+                     "s"(a.pq.on), "s"(a.pk.a), "s"(a.pk.b), "s"(a.pk.ld), "s"(a.pk.dup),
+                     "s"(a.pk.rotary), "s"(a.pk.on));
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar)
@@ -579,21 +600,17 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
     const T* __restrict__ V = static_cast<const T*>(a.V) + (size_t)bh * Lk * D;
     T* __restrict__ O = static_cast<T*>(a.O);
 
-    // the group's epoch and the status word, read once (thread 0) while the
-    // slices load, and handed to every thread through LDS
+    // The group's epoch and the status word, read once by thread 0 with
+    // device-scope loads.  Every workgroup reads the same status word (and
+    // a row group's workgroups the same epoch word), so these loads queue at
+    // one memory channel: they take microseconds.  They are issued right
+    // after the slice loads and consumed only once the partial scores are
+    // out (handed to every thread through LDS at the barrier before the
+    // exchange), which hides them behind the loads and the MFMA phase.
     __shared__ unsigned sh_epoch;
     __shared__ int sh_failed;
-    if (tid == 0) {
-        flag = 1;
-        sh_epoch = 0;
-        sh_failed = 0;
-        if (n > 1) {
-            if constexpr (!XL)
-                sh_epoch =
-                    __hip_atomic_load(a.epochs + rg, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            sh_failed = __hip_atomic_load(a.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-    }
+    unsigned ep_r = 0;
+    int failed_r = 0;
 
 
     // ---- 1. Q, K, V slices -> LDS.  Thread t owns 4-element column group
@@ -608,7 +625,7 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
     // and its stores both hide behind the exchange).  (The host sends this
     // kernel only shapes with D % 4 == 0 and aligned bases.)
     typedef typename Raw4<T>::type Raw;
-    constexpr int kQ = 8, kKV = 16;
+    constexpr int kQ = kRoundQ, kKV = kRoundKV;
     const int vpr = dc >> 2;
     const int rstep = kThreads / vpr;
     const int cg = tid % vpr, r0 = tid / vpr;
@@ -616,7 +633,9 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
     const bool lane_ok = r0 < rstep && d < D;
     const int cq = r0 < rstep ? (MQ - r0 + rstep - 1) / rstep : 0;
     const int ckv = r0 < rstep ? (NK - r0 + rstep - 1) / rstep : 0;
-    const bool defer_v = (MQ + rstep - 1) / rstep <= kQ && (NK + rstep - 1) / rstep <= kKV;
+    // one round (DEFER, a template parameter so that the one-round code is
+    // straight-line code of its own) or several
+    constexpr bool defer_v = DEFER;
     Raw bv[kKV];
     // hi (rounded to nearest even) and lo (the residual, rounded) bf16
     // parts of 4 values
@@ -674,9 +693,25 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
             for (int u = 0; u < kKV; ++u)
                 bk[u] = Raw4<T>::ld_buf(rk, lane_ok ? off0 + (j * kKV + u) * ostep : kOob);
 #pragma unroll
-            for (int u = 0; u < kKV; ++u)  // volatile: issued here, not sunk to the use
-                vr[u] = Raw4<T>::template ld_buf<kAuxVolatile>(
-                    rv, lane_ok ? off0 + (j * kKV + u) * ostep : kOob);
+            for (int u = 0; u < kKV; ++u)
+                vr[u] = Raw4<T>::ld_buf(rv, lane_ok ? off0 + (j * kKV + u) * ostep : kOob);
+            // Every load stays here, in issue order: a store after them keeps
+            // the compiler from sinking one into the (conditional) block that
+            // first uses it, and the scheduling barrier from moving one down
+            // to shorten its live range.  Either way the first Q load was
+            // issued last, and waiting for it waited for every K and V load
+            // before the first LDS store.  (Volatile loads, the other way to
+            // pin them, become system-scope loads that bypass the L2.)  The
+            // word is this thread's slot of the reduction area, unused until
+            // after the next barrier.
+            reinterpret_cast<int*>(smem + g.red_off)[4 * tid] = 0;
+            __builtin_amdgcn_sched_barrier(0);
+            if (j == 0 && tid == 0 && n > 1) {
+                if constexpr (!XL)
+                    ep_r = __hip_atomic_load(a.epochs + rg, __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_AGENT);
+                failed_r = __hip_atomic_load(a.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
 #pragma unroll
             for (int u = 0; u < kQ; ++u) {
                 const int k = j * kQ + u, row = r0 + k * rstep;
@@ -701,7 +736,7 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
                 }
             }
         };
-        if (defer_v) {
+        if constexpr (defer_v) {
             round(0, bv, false);
         } else {
             for (int j = 0; j * kQ < cq || j * kKV < ckv; ++j) {
@@ -710,10 +745,8 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
             }
         }
     }
+    if (tid == 0) flag = 1;
     __syncthreads();
-
-    const unsigned epoch = sh_epoch;
-    const unsigned tag = exchange_tag(epoch, rg);
 
     // ---- 2. partial scores S_c on MFMA.  Each wave owns one 16-row block
     // and up to 8 column tiles; the row block's A operand is read once per
@@ -788,7 +821,13 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
         };
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");  // stores stay above the wait
         __builtin_amdgcn_s_waitcnt(0);  // this wave's partials have completed
+        if (tid == 0) {
+            sh_epoch = ep_r;
+            sh_failed = failed_r;
+        }
         __syncthreads();
+        const unsigned epoch = sh_epoch;
+        const unsigned tag = exchange_tag(epoch, rg);
         unsigned base1 = 0;
         if constexpr (XL) base1 = xcd_arrive_only(rc, 0, share);
         else if (tid == 0) st_done(done1 + c, tag);
@@ -801,7 +840,7 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
             return;
         }
         // V into LDS while the other slices of the group arrive
-        if (defer_v) {
+        if constexpr (defer_v) {
 #pragma unroll
             for (int u = 0; u < kKV; ++u)
                 if (u < ckv) store_v(r0 + u * rstep, bv[u]);
@@ -1117,34 +1156,34 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
 
 // Raises the kernel's dynamic-LDS limit once to the largest size used
 // (160 KiB per workgroup on gfx950).
-template <typename T, int PEK, bool XL>
+template <typename T, int PEK, bool XL, bool DEFER>
 hipError_t ensure_lds_limit(int lds) {
     static std::atomic<int> set{0};
     if (lds <= set.load(std::memory_order_acquire)) return hipSuccess;
     const int want = 160 * 1024 - 256;
-    hipError_t e = hipFuncSetAttribute((const void*)k_fused_small<T, PEK, XL>,
+    hipError_t e = hipFuncSetAttribute((const void*)k_fused_small<T, PEK, XL, DEFER>,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, want);
     if (e == hipSuccess) set.store(want, std::memory_order_release);
     return e;
 }
 
-template <typename T, int PEK, bool XL>
+template <typename T, int PEK, bool XL, bool DEFER>
 hipError_t launch_t(const FusedArgs& a, int lds, hipStream_t st) {
-    hipError_t e = ensure_lds_limit<T, PEK, XL>(lds);
+    hipError_t e = ensure_lds_limit<T, PEK, XL, DEFER>(lds);
     if (e != hipSuccess) return e;
     // XL: 8 XCDs x (row groups per XCD, rounded up) x slices
     const unsigned grid = XL ? (unsigned)(8 * ((a.G + 7) / 8) * a.nchunk)
                              : (unsigned)(a.G * a.nchunk);
-    hipLaunchKernelGGL((k_fused_small<T, PEK, XL>), dim3(grid), dim3(kThreads), lds, st, a);
+    hipLaunchKernelGGL((k_fused_small<T, PEK, XL, DEFER>), dim3(grid), dim3(kThreads), lds, st, a);
     return hipGetLastError();
 }
 
-template <typename T, int PEK, bool XL>
+template <typename T, int PEK, bool XL, bool DEFER>
 int per_cu_t(int lds) {
     int per = 0;
-    if (ensure_lds_limit<T, PEK, XL>(lds) != hipSuccess) return 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, k_fused_small<T, PEK, XL>, kThreads,
-                                                     lds) != hipSuccess)
+    if (ensure_lds_limit<T, PEK, XL, DEFER>(lds) != hipSuccess) return 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, k_fused_small<T, PEK, XL, DEFER>,
+                                                     kThreads, lds) != hipSuccess)
         return 0;
     return per;
 }
@@ -1159,13 +1198,17 @@ int fused_small_lds_bytes(int dtype, int pek, int MB, int Lk, int dc, int nchunk
 int fused_small_per_cu(int dtype, int pek, int lds) {
     // occupancy depends on LDS and registers; the encoded variants use the
     // most registers, so the smallest of their figures is safe for every
-    // variant of either exchange
+    // variant of either exchange and load form
     (void)pek;
     if (dtype == kDtypeF32)
-        return std::min(per_cu_t<float, kPeRopeHalf, false>(lds),
-                        per_cu_t<float, kPeRopeHalf, true>(lds));
-    return std::min(per_cu_t<uint16_t, kPeRopeHalf, false>(lds),
-                    per_cu_t<uint16_t, kPeRopeHalf, true>(lds));
+        return std::min(std::min(per_cu_t<float, kPeRopeHalf, false, false>(lds),
+                                 per_cu_t<float, kPeRopeHalf, true, false>(lds)),
+                        std::min(per_cu_t<float, kPeRopeHalf, false, true>(lds),
+                                 per_cu_t<float, kPeRopeHalf, true, true>(lds)));
+    return std::min(std::min(per_cu_t<uint16_t, kPeRopeHalf, false, false>(lds),
+                             per_cu_t<uint16_t, kPeRopeHalf, true, false>(lds)),
+                    std::min(per_cu_t<uint16_t, kPeRopeHalf, false, true>(lds),
+                             per_cu_t<uint16_t, kPeRopeHalf, true, true>(lds)));
 }
 
 hipError_t launch_fused_small(int dtype, int pek, const void* Q, const void* K, const void* V,
@@ -1180,24 +1223,31 @@ hipError_t launch_fused_small(int dtype, int pek, const void* Q, const void* K, 
     const int lds = fused_small_lds_bytes(dtype, pek, MB, Lk, dc, nchunk);
     // an XL plan with one slice has no exchange: the plain form does the same
     const bool xl = xcd != 0 && nchunk > 1;
-#define ATN_FUSED_PE(T, XLV)                                                                \
-    switch (pek) {                                                                          \
-        case kPeNone: return launch_t<T, kPeNone, XLV>(a, lds, st);                         \
-        case kPeRopeInterleaved: return launch_t<T, kPeRopeInterleaved, XLV>(a, lds, st);   \
-        case kPeRopeHalf: return launch_t<T, kPeRopeHalf, XLV>(a, lds, st);                 \
-        case kPeSinusoidal: return launch_t<T, kPeSinusoidal, XLV>(a, lds, st);             \
-        default: return hipErrorInvalidValue;                                               \
+    const bool defer = fused_defer_v((MB + 15) / 16 * 16, (Lk + 31) / 32 * 32, dc);
+#define ATN_FUSED_PE(T, XLV, DV)                                                              \
+    switch (pek) {                                                                            \
+        case kPeNone: return launch_t<T, kPeNone, XLV, DV>(a, lds, st);                       \
+        case kPeRopeInterleaved: return launch_t<T, kPeRopeInterleaved, XLV, DV>(a, lds, st); \
+        case kPeRopeHalf: return launch_t<T, kPeRopeHalf, XLV, DV>(a, lds, st);               \
+        case kPeSinusoidal: return launch_t<T, kPeSinusoidal, XLV, DV>(a, lds, st);           \
+        default: return hipErrorInvalidValue;                                                 \
     }
+#define ATN_FUSED_DV(T, XLV)             \
+    if (defer) {                         \
+        ATN_FUSED_PE(T, XLV, true)       \
+    }                                    \
+    ATN_FUSED_PE(T, XLV, false)
     if (dtype == kDtypeF32) {
         if (xl) {
-            ATN_FUSED_PE(float, true)
+            ATN_FUSED_DV(float, true)
         }
-        ATN_FUSED_PE(float, false)
+        ATN_FUSED_DV(float, false)
     }
     if (xl) {
-        ATN_FUSED_PE(uint16_t, true)
+        ATN_FUSED_DV(uint16_t, true)
     }
-    ATN_FUSED_PE(uint16_t, false)
+    ATN_FUSED_DV(uint16_t, false)
+#undef ATN_FUSED_DV
 #undef ATN_FUSED_PE
 }
 
