@@ -891,37 +891,50 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
             if (a.gather1) {
                 // one gather, 16-byte words: thread t sums entries 4 (t % 64)
                 // .. + 3 of 256-entry blocks t / 64 + 4 i, every slice's
-                // partial of each in slice order; vector u = i * n + slice
+                // partial of each in slice order; vector u = i * n + slice.
+                // Every vector slot is loaded (slots past this wave's
+                // blocks from an offset past the buffer, which reads
+                // zeros), so the loads carry no branches; the block and
+                // slice counters are wave-uniform (scalar).
                 const int nblk = E >> 8, b0 = tid >> 6;  // 256-entry blocks
-                const int cnt = (b0 < nblk ? (nblk - b0 + 3) / 4 : 0) * n;
+                const int nb =
+                    __builtin_amdgcn_readfirstlane(b0 < nblk ? (nblk - b0 + 3) / 4 : 0);
+                const int cnt = nb * n;
                 const __amdgpu_buffer_rsrc_t rs = make_rsrc(pg, n * E * 4);
-                const int voff = ((tid >> 6) * n * 256 + (tid & 63) * 4) * 4;
+                const int voff = (b0 * n * 256 + (tid & 63) * 4) * 4;
+                constexpr int kOobX = 0x7ffffff0;  // past every buffer
                 float4 w4[kMaxWords / 4];
+                {
+                    int i = 0, p = 0;
 #pragma unroll
-                for (int u = 0; u < kMaxWords / 4; ++u) {
-                    const int i = u / n, p = u - i * n;  // n is uniform: scalar math
-                    w4[u] = u < cnt ? ld_x4<XL>(rs, voff + (4 * i * n + p) * 1024)
-                                    : make_float4(0.f, 0.f, 0.f, 0.f);
+                    for (int u = 0; u < kMaxWords / 4; ++u) {
+                        w4[u] = ld_x4<XL>(rs, u < cnt ? voff + (4 * i * n + p) * 1024 : kOobX);
+                        if (++p == n) {
+                            p = 0;
+                            ++i;
+                        }
+                    }
                 }
+                // sums in slice order (the zeros past the last block are
+                // never stored); 4 consecutive entries share one row of S
+                const int e0 = b0 * 256 + (tid & 63) * 4;
                 float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
                 int p = 0, i = 0;
 #pragma unroll
                 for (int u = 0; u < kMaxWords / 4; ++u) {
-                    if (u < cnt) {
-                        acc.x += w4[u].x;
-                        acc.y += w4[u].y;
-                        acc.z += w4[u].z;
-                        acc.w += w4[u].w;
-                        if (++p == n) {
-                            const int e = (tid >> 6) * 256 + i * 1024 + (tid & 63) * 4;
-                            put_s(e, acc.x);
-                            put_s(e + 1, acc.y);
-                            put_s(e + 2, acc.z);
-                            put_s(e + 3, acc.w);
-                            acc = make_float4(0.f, 0.f, 0.f, 0.f);
-                            p = 0;
-                            ++i;
+                    acc.x += w4[u].x;
+                    acc.y += w4[u].y;
+                    acc.z += w4[u].z;
+                    acc.w += w4[u].w;
+                    if (++p == n) {
+                        if (i < nb) {
+                            const int e = e0 + i * 1024;
+                            const int r = e / NK;
+                            *reinterpret_cast<float4*>(&S[r * g.sstr + (e - r * NK)]) = acc;
                         }
+                        acc = make_float4(0.f, 0.f, 0.f, 0.f);
+                        p = 0;
+                        ++i;
                     }
                 }
                 return true;
