@@ -304,6 +304,22 @@ __device__ __forceinline__ float4 ld_x4(__amdgpu_buffer_rsrc_t r, int off) {
     else return ld_dev4(r, off);
 }
 
+// Exchange stores at byte offset `off` of a buffer resource: XL plans store
+// plainly (the line stays in this XCD's L2), device-scope plans with the
+// cache policy of agent-scope atomic stores (sc1), so the words reach the
+// coherence point; a 16-byte store is four single-copy-atomic elements.
+template <bool XL>
+__device__ __forceinline__ void st_xb(float v, __amdgpu_buffer_rsrc_t r, int off) {
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, off, 0, XL ? 0 : 16);
+}
+template <bool XL>
+__device__ __forceinline__ void st_xb4(float4 v, __amdgpu_buffer_rsrc_t r, int off) {
+    typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+    const u32x4 w = {__float_as_uint(v.x), __float_as_uint(v.y), __float_as_uint(v.z),
+                     __float_as_uint(v.w)};
+    __builtin_amdgcn_raw_buffer_store_b128(w, r, off, 0, XL ? 0 : 16);
+}
+
 // Reads the words base[u * stride], u < cnt, all in flight at once.
 template <bool XL, int NW>
 __device__ __forceinline__ void ld_words(const float* base, int stride, int cnt, float (&w)[NW]) {
@@ -783,7 +799,10 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
     // multiple of 512), so that every read pattern of step 3 is one base
     // address plus a uniform stride per word.
     float* S = reinterpret_cast<float*>(smem + g.s_off);
-    float* part = a.part + (size_t)rg * n * E + (size_t)c * 256;
+    // the group's partials: byte offset 4 ((e / 256) n 256 + c 256 + e % 256)
+    // of entry e of slice c
+    const __amdgpu_buffer_rsrc_t rpart =
+        make_rsrc(a.part + (size_t)rg * n * E, n > 1 ? n * E * 4 : 0);
     {
         int rb, c0, cs;
         const int cnt = wave_tiles(wave, nrb, NK / 16, &rb, &c0, &cs);
@@ -793,7 +812,8 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
             for (int r = 0; r < 4; ++r) {
                 const int i = rb * 16 + lk * 4 + r;
                 const int e = i * NK + j;
-                if (n > 1) st_x<XL>(part + (e >> 8) * (n * 256) + (e & 255), acc[r]);
+                if (n > 1)
+                    st_xb<XL>(acc[r], rpart, ((e >> 8) * (n * 256) + c * 256 + (e & 255)) * 4);
                 else S[i * g.sstr + j] = acc[r];
             }
         };
@@ -874,10 +894,6 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
         }
         const float* pg = a.part + (size_t)rg * n * E;
         float* rd = a.red + (size_t)rg * E;
-        auto put_s = [&](int e, float v) {
-            const int i = e / NK, j = e - i * NK;
-            S[i * g.sstr + j] = v;
-        };
         // returns false (for the whole workgroup) on a timeout; step = the
         // exchange step that timed out
         int step = 1;
@@ -955,20 +971,23 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
                 const int cnt = grp < G ? (n - grp + G - 1) / G : 0;
                 const int e = e0 + 4 * el4;
                 const int voff = (((e >> 8) * n + grp) * 256 + (e & 255)) * 4;
+                // slots up to the wave's largest count are loaded (a
+                // wave-uniform branch; a lane's absent slots read zeros from
+                // past the buffer) and every slot is summed
+                constexpr int kOobX = 0x7ffffff0;
+                const int cmax = __builtin_amdgcn_readfirstlane(cnt);  // lane 0: smallest group
                 float4 w4[kMaxWords / 4];
 #pragma unroll
                 for (int u = 0; u < kMaxWords / 4; ++u)
-                    w4[u] = u < cnt ? ld_x4<XL>(rs, voff + u * G * 1024)
-                                    : make_float4(0.f, 0.f, 0.f, 0.f);
+                    w4[u] = u < cmax ? ld_x4<XL>(rs, u < cnt ? voff + u * G * 1024 : kOobX)
+                                     : make_float4(0.f, 0.f, 0.f, 0.f);
                 float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
                 for (int u = 0; u < kMaxWords / 4; ++u) {
-                    if (u < cnt) {
-                        acc.x += w4[u].x;
-                        acc.y += w4[u].y;
-                        acc.z += w4[u].z;
-                        acc.w += w4[u].w;
-                    }
+                    acc.x += w4[u].x;
+                    acc.y += w4[u].y;
+                    acc.z += w4[u].z;
+                    acc.w += w4[u].w;
                 }
                 reinterpret_cast<float4*>(redl)[tid] = acc;
                 __syncthreads();
@@ -981,11 +1000,7 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
                         sum.z += v.z;
                         sum.w += v.w;
                     }
-                    float* dst = rd + e0 + 4 * tid;
-                    st_x<XL>(dst, sum.x);
-                    st_x<XL>(dst + 1, sum.y);
-                    st_x<XL>(dst + 2, sum.z);
-                    st_x<XL>(dst + 3, sum.w);
+                    st_xb4<XL>(sum, make_rsrc(rd, E * 4), (e0 + 4 * tid) * 4);
                 }
             } else if (cnt_e <= kThreads) {
                 // G groups of cnt_e threads; group q sums slices q, q + G, ...
@@ -1041,21 +1056,24 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
                 if (tid == 0) st_done(done2 + c, tag);
                 if (!wait_done(done2, n, tag, &flag)) return false;
             }
+            // vectors tid + 256 u, u < nv (a wave-uniform bound; a lane's
+            // vectors past E read zeros from past the buffer); 4
+            // consecutive entries share one row of S.  E <= 64 x 128, so
+            // nv <= 8.
+            constexpr int kAgMax = 8;
             const __amdgpu_buffer_rsrc_t rr = make_rsrc(rd, E * 4);
-            const int cnt = tid < (E >> 2) ? ((E >> 2) - tid + kThreads - 1) / kThreads : 0;
-            float4 w4[kMaxWords / 4];
+            const int nv = __builtin_amdgcn_readfirstlane(((E >> 2) + kThreads - 1) / kThreads);
+            float4 w4[kAgMax];
 #pragma unroll
-            for (int u = 0; u < kMaxWords / 4; ++u)
-                w4[u] = u < cnt ? ld_x4<XL>(rr, (tid + u * kThreads) * 16)
-                                : make_float4(0.f, 0.f, 0.f, 0.f);
+            for (int u = 0; u < kAgMax; ++u)
+                w4[u] = u < nv ? ld_x4<XL>(rr, (tid + u * kThreads) * 16)
+                               : make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-            for (int u = 0; u < kMaxWords / 4; ++u) {
-                if (u < cnt) {
-                    const int e = 4 * (tid + u * kThreads);
-                    put_s(e, w4[u].x);
-                    put_s(e + 1, w4[u].y);
-                    put_s(e + 2, w4[u].z);
-                    put_s(e + 3, w4[u].w);
+            for (int u = 0; u < kAgMax; ++u) {
+                const int e = 4 * (tid + u * kThreads);
+                if (u < nv && e < E) {
+                    const int r = e / NK;
+                    *reinterpret_cast<float4*>(&S[r * g.sstr + (e - r * NK)]) = w4[u];
                 }
             }
             return true;
@@ -1156,6 +1174,11 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
     {
         int rb, c0, cs;
         const int cnt = wave_tiles(wave, nrb, dc / 16, &rb, &c0, &cs);
+        // output stores through a buffer resource over the group's rows:
+        // 32-bit offsets, and rows past the sequence fall past its range
+        constexpr int es = (int)sizeof(T);
+        const __amdgpu_buffer_rsrc_t ro = make_rsrc(O + orow0 * D, Lq * D * es);
+        const int obase = (rb * 16 + lk * 4) * D + d0 + lr;  // element of row 0 of the lane
         for (int t0 = 0; t0 < cnt; t0 += 8) {
             const int left = cnt - t0;
             const int tc = c0 + t0 * cs;  // first tile of this group
@@ -1173,16 +1196,17 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
 #pragma unroll
                 for (int u = 0; u < NT; ++u) {
                     if (u >= left) break;
-                    const int dd = d0 + (tc + u * cs) * 16 + lr;
-                    if (dd >= D) continue;
+                    const int col = (tc + u * cs) * 16;
+                    if (d0 + col + lr >= D) continue;
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
-                        const int i = rb * 16 + lk * 4 + r;
-                        if (i >= Lq) continue;
+                        const int off = (obase + r * D + col) * es;
                         if constexpr (kBf16)
-                            O[(orow0 + i) * D + dd] = __builtin_bit_cast(uint16_t, (__bf16)acc[u][r]);
+                            __builtin_amdgcn_raw_buffer_store_b16(
+                                __builtin_bit_cast(uint16_t, (__bf16)acc[u][r]), ro, off, 0, 0);
                         else
-                            O[(orow0 + i) * D + dd] = acc[u][r];
+                            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(acc[u][r]), ro,
+                                                                  off, 0, 0);
                     }
                 }
             };
