@@ -636,10 +636,7 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
     const int q0 = qb * a.MB;       // first query row of the group
     const int Lq = min(a.MB, a.Lq - q0), Lk = a.Lk, D = a.D, dc = a.dc;
     const int d0 = c * dc;
-    const Geo g = make_geo(!kBf16, PEK != kPeNone, a.nchunk > 1, a.MB, Lk, dc);
-    const int MQ = g.MQ, NK = g.NK, E = MQ * NK, nrb = MQ / 16;
     const size_t orow0 = (size_t)bh * a.Lq + q0;  // output row of the group's row 0
-
     const T* __restrict__ Q = static_cast<const T*>(a.Q) + orow0 * D;
     const T* __restrict__ K = static_cast<const T*>(a.K) + (size_t)bh * Lk * D;
     const T* __restrict__ V = static_cast<const T*>(a.V) + (size_t)bh * Lk * D;
@@ -650,36 +647,80 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
     // the slice loads, so that none of wave 0's slice loads waits behind
     // them, and consumed only once the partial scores are out (handed to
     // every thread through LDS at the barrier before the exchange).
+    // (Only thread 0 reads ep_r and failed_r, and only when it loaded them:
+    // left without an initial value, they need no register copy at the end
+    // of its branch, which would wait for the loads -- and, in order, for
+    // every slice load issued before them.  XL plans use no epoch.)
     __shared__ unsigned sh_epoch;
     __shared__ int sh_failed;
-    unsigned ep_r = 0;
-    int failed_r = 0;
-
+    unsigned ep_r;
+    int failed_r;
+    if constexpr (XL) ep_r = 0;
 
     // ---- 1. Q, K, V slices -> LDS.  Thread t owns 4-element column group
     // t % vpr of rows t / vpr + k * rstep of each tensor.  Loads are raw
     // buffer loads over each tensor's rows of this group or head, so rows
     // past the sequence read as zeros without a branch (a column past D
     // gets an offset past the buffer); branch-free loads let the compiler
-    // count them, so a round issues up to kQ row loads of Q and kKV of K and
-    // of V before the first is encoded and stored, and when everything fits
-    // one round, V is only written to LDS once this workgroup's partial
-    // scores are out, while it waits for the other slices (its loads' latency
-    // and its stores both hide behind the exchange).  (The host sends this
-    // kernel only shapes with D % 4 == 0 and aligned bases.)
+    // count them, so a round issues kQ row loads of Q and kKV of K and of V
+    // before the first is encoded and stored.  With one round (FORM != 0, a
+    // template parameter, so that the one-round code is straight-line code
+    // of its own) the loads are issued first thing, before the LDS geometry
+    // and the rest of the set-up, and V is only written to LDS once this
+    // workgroup's partial scores are out, while it waits for the other
+    // slices (its loads' latency and its stores both hide behind the
+    // exchange).  (The host sends this kernel only shapes with D % 4 == 0
+    // and aligned bases.)
     typedef typename Raw4<T>::type Raw;
     constexpr int kQ = LoadForm<FORM>::kQ, kKV = LoadForm<FORM>::kKV;
+    constexpr bool defer_v = FORM != 0;
+    constexpr int es = (int)sizeof(T);
+    constexpr int kOob = 0x7ffffff0;  // past every buffer
     const int vpr = dc >> 2;
     const int rstep = kThreads / vpr;
     const int cg = tid % vpr, r0 = tid / vpr;
     const int col = cg * 4, d = d0 + col;
     const bool lane_ok = r0 < rstep && d < D;
+    const __amdgpu_buffer_rsrc_t rq = make_rsrc(Q, Lq * D * es);
+    const __amdgpu_buffer_rsrc_t rk = make_rsrc(K, Lk * D * es);
+    const __amdgpu_buffer_rsrc_t rv = make_rsrc(V, Lk * D * es);
+    const int off0 = (r0 * D + d) * es, ostep = rstep * D * es;
+    // loads of round j: Q rows j*kQ.., K and V rows j*kKV.. (all in flight)
+    auto issue = [&](int j, Raw (&q)[kQ], Raw (&k)[kKV], Raw (&v)[kKV]) {
+#pragma unroll
+        for (int u = 0; u < kQ; ++u)
+            q[u] = Raw4<T>::ld_buf(rq, lane_ok ? off0 + (j * kQ + u) * ostep : kOob);
+        // all K loads, then all V loads: the K stores wait only for the loads
+        // issued before the last K load
+#pragma unroll
+        for (int u = 0; u < kKV; ++u)
+            k[u] = Raw4<T>::ld_buf(rk, lane_ok ? off0 + (j * kKV + u) * ostep : kOob);
+#pragma unroll
+        for (int u = 0; u < kKV; ++u)
+            v[u] = Raw4<T>::ld_buf(rv, lane_ok ? off0 + (j * kKV + u) * ostep : kOob);
+        // Every load stays here, in issue order: a store after them keeps the
+        // compiler from sinking one into the (conditional) block that first
+        // uses it, and the scheduling barrier from moving one down to shorten
+        // its live range.  Either way the first Q load was issued last, and
+        // waiting for it waited for every K and V load before the first LDS
+        // store.  (Volatile loads, the other way to pin them, become
+        // system-scope loads that bypass the L2.)  The store writes the value
+        // `flag` is given before its first use anyway.
+        flag = 1;
+        __builtin_amdgcn_sched_barrier(0);
+        if (j == 0 && tid == 0 && n > 1) {
+            if constexpr (!XL)
+                ep_r = __hip_atomic_load(a.epochs + rg, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            failed_r = __hip_atomic_load(a.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    };
+    Raw bq[kQ], bk[kKV], bv[kKV];
+    if constexpr (defer_v) issue(0, bq, bk, bv);
+
+    const Geo g = make_geo(!kBf16, PEK != kPeNone, a.nchunk > 1, a.MB, Lk, dc);
+    const int MQ = g.MQ, NK = g.NK, E = MQ * NK, nrb = MQ / 16;
     const int cq = r0 < rstep ? (MQ - r0 + rstep - 1) / rstep : 0;
     const int ckv = r0 < rstep ? (NK - r0 + rstep - 1) / rstep : 0;
-    // one round (a template parameter, so that the one-round code is
-    // straight-line code of its own) or several
-    constexpr bool defer_v = FORM != 0;
-    Raw bv[kKV];
     // hi (rounded to nearest even) and lo (the residual, rounded) bf16
     // parts of 4 values
     auto split4 = [](const float (&e4)[4], uint2& w, uint2& wl) {
@@ -704,12 +745,6 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
         }
     };
     {
-        constexpr int es = (int)sizeof(T);
-        constexpr int kOob = 0x7ffffff0;  // past every buffer
-        const __amdgpu_buffer_rsrc_t rq = make_rsrc(Q, Lq * D * es);
-        const __amdgpu_buffer_rsrc_t rk = make_rsrc(K, Lk * D * es);
-        const __amdgpu_buffer_rsrc_t rv = make_rsrc(V, Lk * D * es);
-        const int off0 = (r0 * D + d) * es, ostep = rstep * D * es;
         // one encoded row vector of Q (isq) or K into its LDS rows
         auto store_qk = [&](bool isq, int row, float4 f) {
             const float e4[4] = {f.x, f.y, f.z, f.w};
@@ -723,43 +758,14 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
                 *reinterpret_cast<uint2*>(lo + off) = wl;
             }
         };
-        // round j: loads of Q rows j*kQ.. and K/V rows j*kKV.. (all in
-        // flight), then Q and K (and, unless deferred, V) into LDS
-        auto round = [&](int j, Raw (&vr)[kKV], bool store_v_now) {
-            Raw bq[kQ], bk[kKV];
-#pragma unroll
-            for (int u = 0; u < kQ; ++u)
-                bq[u] = Raw4<T>::ld_buf(rq, lane_ok ? off0 + (j * kQ + u) * ostep : kOob);
-            // all K loads, then all V loads: the K stores below wait only for
-            // the loads issued before the last K load
-#pragma unroll
-            for (int u = 0; u < kKV; ++u)
-                bk[u] = Raw4<T>::ld_buf(rk, lane_ok ? off0 + (j * kKV + u) * ostep : kOob);
-#pragma unroll
-            for (int u = 0; u < kKV; ++u)
-                vr[u] = Raw4<T>::ld_buf(rv, lane_ok ? off0 + (j * kKV + u) * ostep : kOob);
-            // Every load stays here, in issue order: a store after them keeps
-            // the compiler from sinking one into the (conditional) block that
-            // first uses it, and the scheduling barrier from moving one down
-            // to shorten its live range.  Either way the first Q load was
-            // issued last, and waiting for it waited for every K and V load
-            // before the first LDS store.  (Volatile loads, the other way to
-            // pin them, become system-scope loads that bypass the L2.)  The
-            // word is this thread's slot of the reduction area, unused until
-            // after the next barrier.
-            reinterpret_cast<int*>(smem + g.red_off)[4 * tid] = 0;
-            __builtin_amdgcn_sched_barrier(0);
-            if (j == 0 && tid == 0 && n > 1) {
-                if constexpr (!XL)
-                    ep_r = __hip_atomic_load(a.epochs + rg, __ATOMIC_RELAXED,
-                                             __HIP_MEMORY_SCOPE_AGENT);
-                failed_r = __hip_atomic_load(a.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            }
+        // round j into LDS: Q and K (and, unless deferred, V)
+        auto store_round = [&](int j, Raw (&q)[kQ], Raw (&k)[kKV], Raw (&v)[kKV],
+                               bool store_v_now) {
 #pragma unroll
             for (int u = 0; u < kQ; ++u) {
-                const int k = j * kQ + u, row = r0 + k * rstep;
-                if (k < cq) {
-                    float4 f = Raw4<T>::f4(bq[u]);
+                const int kk = j * kQ + u, row = r0 + kk * rstep;
+                if (kk < cq) {
+                    float4 f = Raw4<T>::f4(q[u]);
                     if constexpr (PEK != kPeNone)
                         if (lane_ok && row < Lq)
                             f = encode4<T, PEK>(f, Q + (size_t)row * D, q0 + row, d, a.pq);
@@ -768,23 +774,24 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
             }
 #pragma unroll
             for (int u = 0; u < kKV; ++u) {
-                const int k = j * kKV + u, row = r0 + k * rstep;
-                if (k < ckv) {
-                    float4 f = Raw4<T>::f4(bk[u]);
+                const int kk = j * kKV + u, row = r0 + kk * rstep;
+                if (kk < ckv) {
+                    float4 f = Raw4<T>::f4(k[u]);
                     if constexpr (PEK != kPeNone)
                         if (lane_ok && row < Lk)
                             f = encode4<T, PEK>(f, K + (size_t)row * D, row, d, a.pk);
                     store_qk(false, row, f);
-                    if (store_v_now) store_v(row, vr[u]);
+                    if (store_v_now) store_v(row, v[u]);
                 }
             }
         };
         if constexpr (defer_v) {
-            round(0, bv, false);
+            store_round(0, bq, bk, bv, false);
         } else {
             for (int j = 0; j * kQ < cq || j * kKV < ckv; ++j) {
-                Raw vr[kKV];
-                round(j, vr, true);
+                Raw q[kQ], k[kKV], v[kKV];
+                issue(j, q, k, v);
+                store_round(j, q, k, v, true);
             }
         }
     }
@@ -868,10 +875,14 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
         };
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");  // stores stay above the wait
         __builtin_amdgcn_s_waitcnt(0);  // this wave's partials have completed
-        if (tid == 0) {
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Wuninitialized"
+#pragma clang diagnostic ignored "-Wsometimes-uninitialized"
+        if (tid == 0) {  // thread 0 loaded both (n > 1)
             sh_epoch = ep_r;
             sh_failed = failed_r;
         }
+#pragma clang diagnostic pop
         __syncthreads();
         const unsigned epoch = sh_epoch;
         const unsigned tag = exchange_tag(epoch, rg);
