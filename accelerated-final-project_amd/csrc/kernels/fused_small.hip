@@ -26,12 +26,16 @@ hipError_t launch_fused_small(int dtype, int pek, const void* Q, const void* K, 
                               int gather1, int xcd, float scale, const PeSide& pq,
                               const PeSide& pk, hipStream_t st) {
     const int QB = (Lq + MB - 1) / MB;
+    const int MQ = (MB + 15) / 16 * 16, NK = (Lk + 31) / 32 * 32;
+    const int vpr = dc / 4, rstep = 256 / vpr;
     FusedArgs a{Q, K, V, O, part, red, epochs, done, status, Lq, Lk, D, dc, nchunk,
-                MB, QB, gather1, BH * QB, xctr, scale, pq, pk};
+                MB, QB, gather1, BH * QB, xctr, scale, pq, pk,
+                rstep, fused_div_magic(nchunk), fused_div_magic(QB), fused_div_magic(BH),
+                fused_div_magic(vpr), fused_div_magic(rstep), fused_div_magic(NK)};
     const int lds = fused_small_lds_bytes(dtype, pek, MB, Lk, dc, nchunk);
     // an XL plan with one slice has no exchange: the plain form does the same
     const bool xl = xcd != 0 && nchunk > 1;
-    const int form = fused_load_form((MB + 15) / 16 * 16, (Lk + 31) / 32 * 32, dc);
+    const int form = fused_load_form(MQ, NK, dc);
     if (dtype == kDtypeF32)
         return xl ? fused_small_launch_f32_xl(a, pek, form, lds, st)
                   : fused_small_launch_f32(a, pek, form, lds, st);

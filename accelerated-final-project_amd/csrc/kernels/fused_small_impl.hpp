@@ -107,7 +107,17 @@ struct FusedArgs {
     unsigned* xctr;    // XL plans: arrival counters, kXcdCtrWords per XCD
     float scale;
     PeSide pq, pk;
+    // Division by the plan's divisors without a division sequence: for the
+    // small non-negative dividends of this kernel x / d = umulhi(x, m_d),
+    // m_d = 2^32 / d rounded up (exact while x * d < 2^32; d = 1 has m = 0
+    // and is taken apart).  Set by the host (fused_div_magic).
+    int rstep;      // Q/K/V rows loaded per pass: 256 / (dc / 4)
+    unsigned m_n, m_qb, m_bh, m_vpr, m_rstep, m_nk;
 };
+
+__host__ __device__ inline unsigned fused_div_magic(int d) {
+    return d <= 1 ? 0u : (unsigned)(0xFFFFFFFFull / (unsigned)d + 1ull);
+}
 
 // One translation unit per (element type, exchange scope) instantiates the
 // kernel's encoding and load-form variants (fused_small_<type>[_xl].hip), so
@@ -553,18 +563,26 @@ __device__ __forceinline__ void mma_bf16_vt(const uint16_t* a, const uint16_t* a
     }
 }
 
+// x / d for the kernel's small non-negative dividends, m = fused_div_magic(d).
+__device__ __forceinline__ int fdiv(int x, int d, unsigned m) {
+    return d == 1 ? x : (int)__umulhi((unsigned)x, m);
+}
+
 // Wave -> (16-row block, set of 16-column tiles) for an output of nrb row
 // blocks and `tiles` column tiles: waves w and w + nrb share a row block and
 // take every (4 / nrb)-th column tile.  Returns the number of tiles (0 for
-// an idle wave).
+// an idle wave).  wave < 4 and nrb <= 4, so the quotients are selects and
+// the waves per row block (4, 2, 1 or 1) a power of two.
 __device__ __forceinline__ int wave_tiles(int wave, int nrb, int tiles, int* rb, int* c0,
                                           int* cstep) {
-    const int wpr = 4 / nrb;  // waves per row block (nrb <= 4)
-    *rb = wave % nrb;
-    *c0 = wave / nrb;
+    const int q = nrb == 1 ? wave : (nrb == 2 ? wave >> 1 : (nrb == 3 ? (wave == 3) : 0));
+    const int lg = nrb == 1 ? 2 : (nrb == 2 ? 1 : 0);  // log2 of the waves per row block
+    const int wpr = 1 << lg;
+    *rb = wave - q * nrb;
+    *c0 = q;
     *cstep = wpr;
-    if (wave >= nrb * wpr || *c0 >= tiles) return 0;
-    return (tiles - *c0 + wpr - 1) / wpr;
+    if (wave >= nrb * wpr || q >= tiles) return 0;
+    return (tiles - q + wpr - 1) >> lg;
 }
 
 // Load form of a plan: how many row loads of Q (kQ) and of K and of V (kKV)
@@ -618,21 +636,21 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
         // place id / 8 = gi * n + c on XCD x: slice c of the XCD's gi-th row
         // group; XCD x holds row groups [x * base + min(x, rem), + cnt)
         const int x = (int)xcc_id(), local = (int)blockIdx.x >> 3;
-        const int gi = local / n;
+        const int gi = fdiv(local, n, a.m_n);
         c = local - gi * n;
         const int base = a.G >> 3, rem = a.G & 7;
         if (gi >= base + (x < rem ? 1 : 0)) return;  // no row group here (whole workgroup)
         rg = x * base + min(x, rem) + gi;
         xcd_slot = x * kXcdCtrWords + 2 * gi;
     } else {
-        // id = qb * W + bh * n + c
-        const int W = (int)gridDim.x / a.QB;  // (head, slice) pairs
-        const int qb_ = (int)blockIdx.x / W, hc = (int)blockIdx.x - qb_ * W;
-        const int bh_ = hc / n;
-        c = hc - bh_ * n;
+        // id = (qb * BH + bh) * n + c
+        const int BH = a.G / a.QB;
+        const int t = fdiv((int)blockIdx.x, n, a.m_n);
+        c = (int)blockIdx.x - t * n;
+        const int qb_ = fdiv(t, BH, a.m_bh), bh_ = t - qb_ * BH;
         rg = bh_ * a.QB + qb_;  // row group (epoch word, exchange region, tag)
     }
-    const int bh = rg / a.QB, qb = rg - bh * a.QB;
+    const int bh = fdiv(rg, a.QB, a.m_qb), qb = rg - bh * a.QB;
     const int q0 = qb * a.MB;       // first query row of the group
     const int Lq = min(a.MB, a.Lq - q0), Lk = a.Lk, D = a.D, dc = a.dc;
     const int d0 = c * dc;
@@ -677,8 +695,8 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
     constexpr int es = (int)sizeof(T);
     constexpr int kOob = 0x7ffffff0;  // past every buffer
     const int vpr = dc >> 2;
-    const int rstep = kThreads / vpr;
-    const int cg = tid % vpr, r0 = tid / vpr;
+    const int rstep = a.rstep;  // kThreads / vpr
+    const int r0 = fdiv(tid, vpr, a.m_vpr), cg = tid - r0 * vpr;
     const int col = cg * 4, d = d0 + col;
     const bool lane_ok = r0 < rstep && d < D;
     const __amdgpu_buffer_rsrc_t rq = make_rsrc(Q, Lq * D * es);
@@ -719,8 +737,8 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
 
     const Geo g = make_geo(!kBf16, PEK != kPeNone, a.nchunk > 1, a.MB, Lk, dc);
     const int MQ = g.MQ, NK = g.NK, E = MQ * NK, nrb = MQ / 16;
-    const int cq = r0 < rstep ? (MQ - r0 + rstep - 1) / rstep : 0;
-    const int ckv = r0 < rstep ? (NK - r0 + rstep - 1) / rstep : 0;
+    const int cq = r0 < rstep ? fdiv(MQ - r0 + rstep - 1, rstep, a.m_rstep) : 0;
+    const int ckv = r0 < rstep ? fdiv(NK - r0 + rstep - 1, rstep, a.m_rstep) : 0;
     // hi (rounded to nearest even) and lo (the residual, rounded) bf16
     // parts of 4 values
     auto split4 = [](const float (&e4)[4], uint2& w, uint2& wl) {
@@ -858,7 +876,7 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
             c < n - 1 ? (unsigned)c + 1u : kXcdUnits - (unsigned)(n - 1) * (unsigned)n / 2u;
         const __amdgpu_buffer_rsrc_t rc = make_rsrc(a.xctr + xcd_slot, 8);
         // reduce-scatter: this workgroup owns entries [e0, e1) of the group
-        const int per_rs = (E + n - 1) / n;
+        const int per_rs = fdiv(E + n - 1, n, a.m_n);
         const int e0_rs = min(E, c * per_rs), e1_rs = min(E, e0_rs + per_rs);
         // XL, on a path that leaves early: NaN into this workgroup's reduced
         // entries (late slices of the group read them), then the second
@@ -956,7 +974,7 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
                     if (++p == n) {
                         if (i < nb) {
                             const int e = e0 + i * 1024;
-                            const int r = e / NK;
+                            const int r = fdiv(e, NK, a.m_nk);
                             *reinterpret_cast<float4*>(&S[r * g.sstr + (e - r * NK)]) = acc;
                         }
                         acc = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -977,9 +995,10 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
                 // consecutive entries (a 4-aligned run never crosses a
                 // 256-entry block); group q sums slices q, q + G, ...
                 const int c4 = cnt_e >> 2;
-                const int G = kThreads / c4;
-                const int el4 = tid % c4, grp = tid / c4;
-                const int cnt = grp < G ? (n - grp + G - 1) / G : 0;
+                const int G = kThreads / c4;  // scalar divisions, then multipliers
+                const unsigned mc4 = fused_div_magic(c4), mg = fused_div_magic(G);
+                const int grp = fdiv(tid, c4, mc4), el4 = tid - grp * c4;
+                const int cnt = grp < G ? fdiv(n - grp + G - 1, G, mg) : 0;
                 const int e = e0 + 4 * el4;
                 const int voff = (((e >> 8) * n + grp) * 256 + (e & 255)) * 4;
                 // slots up to the wave's largest count are loaded (a
@@ -1083,7 +1102,7 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
             for (int u = 0; u < kAgMax; ++u) {
                 const int e = 4 * (tid + u * kThreads);
                 if (u < nv && e < E) {
-                    const int r = e / NK;
+                    const int r = fdiv(e, NK, a.m_nk);
                     *reinterpret_cast<float4*>(&S[r * g.sstr + (e - r * NK)]) = w4[u];
                 }
             }
