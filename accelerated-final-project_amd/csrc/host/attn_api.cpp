@@ -502,20 +502,17 @@ FusedPlan fused_plan_uncached(int dtype, int pek, const Shape& s, bool query_dev
         return p;
     };
     // Estimated time in us beyond the fixed cost.  Device-scope plans: each
-    // CU's Q/K/V slice loads (0.0242 us per KiB), the slices (0.0373 us
-    // each), reduce-scatter's second round trip (4.5 us), each CU's exchange
-    // reads (0.1288 us per KiB) and the workgroup count (0.358 us per CU's
-    // worth) -- first fitted by least squares to 105 timed plans of 13
-    // shapes, then checked against a sweep of every plan of 15 fp32/bf16
-    // shapes (272 timed plans, B*H 1-16, Lq 16-64, Lk 16-128, D 512-8192),
-    // where these coefficients pick plans within 0.23 us in total of the
-    // fastest measured on each shape.
-    // XCD-local plans: about 1.5 us less for the first exchange step, 2.5 us
-    // for reduce-scatter's second step and 0.015 us per KiB of exchange
-    // reads (L2).  Their XCDs also fetch whole heads' K and V (each XCD holds
-    // a block of row groups), where device-scope plans spread every head
-    // over all 8: the extra bytes per XCD cost about 3 us per MB (config 3:
-    // 2 MiB more per XCD, 3 us slower than the device-scope plan).
+    // CU's Q/K/V slice loads (0.055 us per KiB), the slices (0.0373 us
+    // each), reduce-scatter's second round trip (2.5 us), each CU's exchange
+    // reads (0.04 us per KiB) and the workgroup count (0.358 us per CU's
+    // worth).  XCD-local plans: 2.5 us less, reduce-scatter's second step
+    // 2.5 us and 0.015 us per KiB of exchange reads (L2); their XCDs also
+    // fetch whole heads' K and V (each XCD holds a block of row groups),
+    // where device-scope plans spread every head over all 8: the extra bytes
+    // per XCD cost about 1 us per MB.  The coefficients were chosen against
+    // a sweep that timed every plan of 15 fp32/bf16 shapes (244 plans, B*H
+    // 1-16, Lq 16-64, Lk 16-128, D 512-8192): on it they pick plans within
+    // 0.3 us in total of the fastest measured on each shape.
     const double kv_head = 2.0 * (double)s.Lk * (double)s.D * es;
     auto cost = [&](const FusedPlan& p) {
         const double per_cu = (double)p.per_cu;
@@ -527,11 +524,11 @@ FusedPlan fused_plan_uncached(int dtype, int pek, const Shape& s, bool query_dev
             const int64_t G = s.BH * QB, gpx = (G + 7) / 8;
             const double heads_x = (double)std::max<int64_t>(1, (gpx + QB - 1) / QB);
             const double kv_extra = std::max(0.0, heads_x * kv_head - (double)s.BH * kv_head / 8.0);
-            return 0.0242 * kib * per_cu + 0.0373 * p.nchunk + (!p.gather1 ? 2.5 : 0.0) +
-                   0.015 * xkib * per_cu + 0.358 * p.workgroups / cus - 1.5 + kv_extra * 3e-6;
+            return 0.055 * kib * per_cu + 0.0373 * p.nchunk + (!p.gather1 ? 2.5 : 0.0) +
+                   0.015 * xkib * per_cu + 0.358 * p.workgroups / cus - 2.5 + kv_extra * 1e-6;
         }
-        return 0.0242 * kib * per_cu + 0.0373 * p.nchunk +
-               (p.nchunk > 1 && !p.gather1 ? 4.5 : 0.0) + 0.1288 * xkib * per_cu +
+        return 0.055 * kib * per_cu + 0.0373 * p.nchunk +
+               (p.nchunk > 1 && !p.gather1 ? 2.5 : 0.0) + 0.04 * xkib * per_cu +
                0.358 * p.workgroups / cus;
     };
     // overrides (tuning): row group size, slice width, exchange
