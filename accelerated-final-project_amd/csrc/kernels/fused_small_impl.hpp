@@ -25,7 +25,7 @@
 //      a reduce-scatter then an all-gather (two round trips).  Partials are
 //      always summed in slice order, so results are bit-reproducible;
 //   4. exact softmax of scale * S per row (max, exp, sum, divide;
-//      final/attention.cu:262-270), four threads per row;
+//      final/attention.cu:262-270), 16, 8 or 4 threads per row;
 //   5. O[rows, slice] = P V[:, slice] on bf16 MFMA, P split into hi + lo
 //      bf16 parts (and fp32 V too), one store per output element.
 //

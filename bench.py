@@ -48,8 +48,8 @@ MALL_FLUSH_MIB = 512  # > the 256 MiB MALL: a copy this large evicts it
 # FETCH_SIZE / WRITE_SIZE and scaled by a known-size device copy; keyed by
 # (config, head_dim), with the profile that holds the counts.
 MEASURED_TRAFFIC = {
-    (2, 2048): ((11839 + 3080) * 1024, "profiles/fused_small_cfg2_traffic.md"),
-    (3, 8192): ((21633 + 4368) * 1024, "profiles/fused_small_cfg3_kernel_trace.md"),
+    (2, 2048): ((11621 + 3080) * 1024, "profiles/fused_small_cfg2_traffic.md"),
+    (3, 8192): ((23538 + 6224) * 1024, "profiles/fused_small_cfg3_kernel_trace.md"),
 }
 
 # (name, dtype, B, H, Lq, Lk, D, pe, sigma)
@@ -253,10 +253,10 @@ def cpu_baseline(cfg, host, target_s):
 
 def run_config(am, hip_rt, cfg, steps, warmup, seed, cold):
     """Times one config: `steps` calls captured as one HIP graph and replayed
-    (HIP events on the call's stream), and, with `cold`, the same with the
-    256 MiB MALL flushed before every call (a 512 MiB device copy; the
-    copies' own time, measured alone, is subtracted).  Returns the timing
-    dict, the host inputs and a row reader of the final output."""
+    (HIP events on the call's stream), and, with `cold`, the median single
+    call between events of its own, with and without the 256 MiB MALL
+    flushed before it (a 512 MiB device copy outside the events).  Returns
+    the timing dict, the host inputs and a row reader of the final output."""
     name, dtype, B, H, Lq, Lk, D, pe, sigma = cfg
     (q, k, v), host = make_inputs(dtype, B, H, Lq, Lk, D, sigma, seed)
     out = hip_rt.DeviceArray((B, H, Lq, D), dtype)
@@ -313,14 +313,31 @@ def run_config(am, hip_rt, cfg, steps, warmup, seed, cold):
         n = MALL_FLUSH_MIB << 20
         src = hip_rt.DeviceArray((n // 4,), "f32", fill=0)
         dst = hip_rt.DeviceArray((n // 4,), "f32")
-        flush_ms, _ = timed_graph(lambda: [hip_rt.copy_d2d_async(dst, src, n, stream)
-                                           for _ in range(steps)])
-        both_ms, _ = timed_graph(lambda: [(hip_rt.copy_d2d_async(dst, src, n, stream), step())
-                                          for _ in range(steps)])
+
+        def bracketed(flush):
+            # median over `steps` calls, each between two events of its own;
+            # with `flush`, a MALL-sized device copy runs before each call,
+            # outside its events (a difference of whole-run timings would
+            # carry the copies' own spread, larger than a short kernel)
+            evs = [(hip_rt.Event(), hip_rt.Event()) for _ in range(steps)]
+            for b, e in evs:
+                if flush:
+                    hip_rt.copy_d2d_async(dst, src, n, stream)
+                b.record(stream)
+                step()
+                e.record(stream)
+            evs[-1][1].synchronize()
+            t = sorted(b.elapsed_ms(e) for b, e in evs)
+            for b, e in evs:
+                b.destroy()
+                e.destroy()
+            return t[len(t) // 2]
+
+        res["bracketed_ms_per_step"] = bracketed(False)
+        res["cold_ms_per_step"] = bracketed(True)
         st = am.lib().atn_sync_status_ex(ws.ptr, B, H, stream.handle)
         if st != 0:
             raise am.AtnError(st, f"device status after the cold run ({name})")
-        res["cold_ms_per_step"] = max(both_ms - flush_ms, 0.0) / steps
         src.free()
         dst.free()
     hip_rt.synchronize()
@@ -436,6 +453,7 @@ def main():
                    "check": chk}
             if "cold_ms_per_step" in r:
                 ent["cold_ms_per_step"] = round(r["cold_ms_per_step"], 6)
+                ent["bracketed_ms_per_step"] = round(r["bracketed_ms_per_step"], 6)
             if a.cpu_seconds > 0:
                 v_cpu, job_ms, sample = cpu_baseline(c, h, a.cpu_seconds_other)
                 ent["cpu_baseline"] = {"value": round(v_cpu, 4), "unit": "GB/s", "cores": 1,
@@ -451,8 +469,11 @@ def main():
                "check": check}
     if "cold_ms_per_step" in res:
         cfg_out["cold_ms_per_step"] = round(res["cold_ms_per_step"], 6)
-        cfg_out["cold_note"] = (f"MALL flushed by a {MALL_FLUSH_MIB} MiB device copy before every "
-                                "step; the copies' own time is subtracted")
+        cfg_out["bracketed_ms_per_step"] = round(res["bracketed_ms_per_step"], 6)
+        cfg_out["cold_note"] = (f"median of single calls between events of their own, each after a "
+                                f"{MALL_FLUSH_MIB} MiB device copy (MALL flushed); "
+                                "bracketed_ms_per_step is the same without the copies, so the "
+                                "events' own overhead shows against ms_per_step")
     line = {
         "metric": "attention ms + TFLOPS + HBM GB/s (% roofline) at hdim 512-8192, 1 GPU",
         "value": round(gbs, 2),
