@@ -703,8 +703,15 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
     const __amdgpu_buffer_rsrc_t rk = make_rsrc(K, Lk * D * es);
     const __amdgpu_buffer_rsrc_t rv = make_rsrc(V, Lk * D * es);
     const int off0 = (r0 * D + d) * es, ostep = rstep * D * es;
-    // loads of round j: Q rows j*kQ.., K and V rows j*kKV.. (all in flight)
-    auto issue = [&](int j, Raw (&q)[kQ], Raw (&k)[kKV], Raw (&v)[kKV]) {
+    // loads of round j: V rows j*kKV.. (all in flight)
+    auto issue_v = [&](int j, Raw (&v)[kKV]) {
+#pragma unroll
+        for (int u = 0; u < kKV; ++u)
+            v[u] = Raw4<T>::ld_buf(rv, lane_ok ? off0 + (j * kKV + u) * ostep : kOob);
+    };
+    // loads of round j: Q rows j*kQ.., K rows j*kKV.. and, with `with_v`, V
+    // rows j*kKV.. (all in flight)
+    auto issue = [&](int j, Raw (&q)[kQ], Raw (&k)[kKV], Raw (&v)[kKV], bool with_v) {
 #pragma unroll
         for (int u = 0; u < kQ; ++u)
             q[u] = Raw4<T>::ld_buf(rq, lane_ok ? off0 + (j * kQ + u) * ostep : kOob);
@@ -713,9 +720,7 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
 #pragma unroll
         for (int u = 0; u < kKV; ++u)
             k[u] = Raw4<T>::ld_buf(rk, lane_ok ? off0 + (j * kKV + u) * ostep : kOob);
-#pragma unroll
-        for (int u = 0; u < kKV; ++u)
-            v[u] = Raw4<T>::ld_buf(rv, lane_ok ? off0 + (j * kKV + u) * ostep : kOob);
+        if (with_v) issue_v(j, v);
         // Every load stays here, in issue order: a store after them keeps the
         // compiler from sinking one into the (conditional) block that first
         // uses it, and the scheduling barrier from moving one down to shorten
@@ -732,8 +737,13 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
             failed_r = __hip_atomic_load(a.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     };
+    // One round with an exchange: V is loaded only once the partial scores
+    // are out (its loads land while the workgroup waits for the group's other
+    // slices, and the Q and K loads, which every workgroup issues at once,
+    // do not share the memory system with them).  A single slice has no wait
+    // to hide them behind, so it loads V with Q and K.
     Raw bq[kQ], bk[kKV], bv[kKV];
-    if constexpr (defer_v) issue(0, bq, bk, bv);
+    if constexpr (defer_v) issue(0, bq, bk, bv, n == 1);
 
     const Geo g = make_geo(!kBf16, PEK != kPeNone, a.nchunk > 1, a.MB, Lk, dc);
     const int MQ = g.MQ, NK = g.NK, E = MQ * NK, nrb = MQ / 16;
@@ -808,7 +818,7 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
         } else {
             for (int j = 0; j * kQ < cq || j * kKV < ckv; ++j) {
                 Raw q[kQ], k[kKV], v[kKV];
-                issue(j, q, k, v);
+                issue(j, q, k, v, true);
                 store_round(j, q, k, v, true);
             }
         }
@@ -865,6 +875,16 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
         else if (cnt > 2 && cnt <= 4) run(std::integral_constant<int, 4>{});
         else if (cnt > 4) run(std::integral_constant<int, 8>{});
     }
+    if constexpr (defer_v) {
+        if (n > 1) {
+            // after the partial stores, in issue order (kept there as the
+            // slice loads are)
+            __builtin_amdgcn_sched_barrier(0);
+            issue_v(0, bv);
+            flag = 1;
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
 
     // ---- 3. all-reduce of S over the group's slices (tagged words, or
     // XCD-local arrival counters)
@@ -892,7 +912,14 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
             }
         };
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");  // stores stay above the wait
-        __builtin_amdgcn_s_waitcnt(0);  // this wave's partials have completed
+        // this wave's partials have completed: every vector memory operation
+        // but the kKV V loads issued after them (vmcnt counts in issue order)
+        if constexpr (defer_v) {
+            static_assert(kKV == 8 || kKV == 16, "vmcnt encoding below");
+            __builtin_amdgcn_s_waitcnt(kKV == 8 ? 0x0F78 : 0x4F70);  // vmcnt(kKV)
+        } else {
+            __builtin_amdgcn_s_waitcnt(0);
+        }
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Wuninitialized"
 #pragma clang diagnostic ignored "-Wsometimes-uninitialized"
