@@ -287,7 +287,7 @@ def run_config(am, hip_rt, cfg, steps, warmup, seed, cold):
     e1.synchronize()
     eager_ms = e0.elapsed_ms(e1) / steps
 
-    def timed_graph(fn):
+    def timed_graph(fn, extra=0):
         g = hip_rt.Graph(stream, fn)
         g.launch()  # warm replay
         stream.synchronize()
@@ -298,16 +298,26 @@ def run_config(am, hip_rt, cfg, steps, warmup, seed, cold):
         e1.record(stream)
         e1.synchronize()
         wall = time.perf_counter() - t0
+        ms = e0.elapsed_ms(e1)
+        trials = [ms]
+        for _ in range(extra):  # further replays, after the timed region
+            e0.record(stream)
+            g.launch()
+            e1.record(stream)
+            e1.synchronize()
+            trials.append(e0.elapsed_ms(e1))
         g.destroy()
-        return e0.elapsed_ms(e1), wall
+        return ms, wall, trials
 
     # timed region: the K steps captured once as a HIP graph and replayed,
-    # so the GPU runs them back to back with no host work in between
-    ev_ms, wall = timed_graph(lambda: [step() for _ in range(steps)])
+    # so the GPU runs them back to back with no host work in between; four
+    # more replays give the median of five trials beside it
+    ev_ms, wall, trials = timed_graph(lambda: [step() for _ in range(steps)], extra=4)
     st = am.lib().atn_sync_status_ex(ws.ptr, B, H, stream.handle)
     if st != 0:
         raise am.AtnError(st, f"device status after the timed region ({name})")
     res = {"ms_per_step": ev_ms / steps, "eager_ms": eager_ms, "wall_s": wall,
+           "median5_ms_per_step": sorted(trials)[len(trials) // 2] / steps,
            "path": am.path(dcode, B, H, Lq, Lk, D, desc)}
     if cold:
         n = MALL_FLUSH_MIB << 20
@@ -340,6 +350,18 @@ def run_config(am, hip_rt, cfg, steps, warmup, seed, cold):
             raise am.AtnError(st, f"device status after the cold run ({name})")
         src.free()
         dst.free()
+    if pe == "none":
+        # the synchronous drop-in (the reference's host entry point: launch,
+        # then wait for the device), host wall clock per call, median
+        fn = am.attention_forward_optimized if dtype == "f32" else am.attention_forward_bf16
+        for _ in range(3):
+            fn(q, k, v, out)
+        ts = []
+        for _ in range(max(steps, 20)):
+            t0 = time.perf_counter()
+            fn(q, k, v, out)
+            ts.append(time.perf_counter() - t0)
+        res["dropin_sync_ms"] = sorted(ts)[len(ts) // 2] * 1e3
     hip_rt.synchronize()
     bits = out.numpy()
 
@@ -448,12 +470,15 @@ def main():
             chk = sampled_check(c, h, rf)
             ab, fl, g, tf, bd, fr = summarize(c, r)
             ent = {"workload": c[0], "dtype": c[1], "pe": c[7], "ms_per_step": round(r["ms_per_step"], 6),
+                   "ms_per_step_median5": round(r["median5_ms_per_step"], 6),
                    "tflops": round(tf, 3), "gbs": round(g, 2), "roofline_bound": bd,
                    "roofline_frac": round(fr, 4), "alg_bytes": ab, "flops": fl,
                    "check": chk}
             if "cold_ms_per_step" in r:
                 ent["cold_ms_per_step"] = round(r["cold_ms_per_step"], 6)
                 ent["bracketed_ms_per_step"] = round(r["bracketed_ms_per_step"], 6)
+            if "dropin_sync_ms" in r:
+                ent["dropin_sync_ms"] = round(r["dropin_sync_ms"], 6)
             if a.cpu_seconds > 0:
                 v_cpu, job_ms, sample = cpu_baseline(c, h, a.cpu_seconds_other)
                 ent["cpu_baseline"] = {"value": round(v_cpu, 4), "unit": "GB/s", "cores": 1,
@@ -474,6 +499,11 @@ def main():
                                 f"{MALL_FLUSH_MIB} MiB device copy (MALL flushed); "
                                 "bracketed_ms_per_step is the same without the copies, so the "
                                 "events' own overhead shows against ms_per_step")
+    if "dropin_sync_ms" in res:
+        cfg_out["dropin_sync_ms"] = round(res["dropin_sync_ms"], 6)
+        cfg_out["dropin_note"] = ("median host wall clock of one synchronous drop-in call "
+                                  "(attention_forward_optimized / attention_forward_bf16: "
+                                  "launch, then wait for the device)")
     line = {
         "metric": "attention ms + TFLOPS + HBM GB/s (% roofline) at hdim 512-8192, 1 GPU",
         "value": round(gbs, 2),
@@ -482,6 +512,7 @@ def main():
         "steps": a.steps,
         "warmup": a.warmup,
         "ms_per_step": round(ms, 6),
+        "ms_per_step_median5": round(res["median5_ms_per_step"], 6),
         "ms_per_step_eager_python": round(res["eager_ms"], 6),
         "tflops": round(tflops, 4),
         "pct_hbm_roofline": round(100 * gbs / HBM_PEAK_GBS, 2),
