@@ -144,6 +144,10 @@ struct DeviceState {
     std::map<std::tuple<int, int, int, uint32_t>, Table16> tables16;  // (kind, D, rotary, base)
     int cus = 0;
     std::map<std::pair<int, int>, int> fused_per_cu;  // (dtype, LDS bytes) -> workgroups per CU
+    // Two pinned host words that receive the status words of the null
+    // stream's library workspace and of the allocation-free scratch behind
+    // each synchronous drop-in call (allocated once, kept).
+    int* status_host = nullptr;
 };
 
 std::mutex g_mu;
@@ -1010,16 +1014,63 @@ int workspace_status(void* ws, hipStream_t stream) {
     return ATN_ERR_DEVICE_TIMEOUT;
 }
 
+// Completion of a synchronous drop-in call (enqueued on the null stream):
+// the status words of the workspaces such a call can use (the null stream's
+// library workspace, the allocation-free scratch) are copied into pinned
+// host words behind the call, so the one device synchronization covers the
+// call and its status check.  A set word runs the recovery of
+// workspace_status() and ends the process like any other failure.
 void sync_or_die(int status, const char* where) {
     if (status != ATN_OK) die(status, where);
     hipError_t e = hipGetLastError();
-    if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e != hipSuccess) {
         g_last_hip_error = (int)e;
         die(ATN_ERR_HIP, where);
     }
-    const int ws = workspace_status(nullptr, nullptr);
-    if (ws != ATN_OK) die(ws, where);
+    int dev;
+    int st = current_device(&dev);
+    if (st != ATN_OK) die(st, where);
+    void* lib_ws = nullptr;
+    int* host = nullptr;
+    {
+        std::lock_guard<std::mutex> lk(g_mu);
+        DeviceState& ds = g_dev[dev];
+        auto it = ds.ws.find(nullptr);
+        if (it != ds.ws.end()) lib_ws = it->second.ptr;
+        if (ds.status_host == nullptr) {
+            void* p = nullptr;
+            if (hipHostMalloc(&p, 2 * sizeof(int), hipHostMallocDefault) == hipSuccess)
+                ds.status_host = static_cast<int*>(p);
+        }
+        host = ds.status_host;
+    }
+    void* sc = nullptr;
+    if (atn::noalloc_ready(dev)) {
+        e = atn::noalloc_scratch(dev, kSyncBytes, nullptr, &sc);
+        if (e != hipSuccess) {
+            g_last_hip_error = (int)e;
+            die(ATN_ERR_HIP, where);
+        }
+    }
+    bool copied = host != nullptr;
+    if (copied && lib_ws != nullptr)
+        copied = hipMemcpyAsync(&host[0], lib_ws, sizeof(int), hipMemcpyDeviceToHost, nullptr) ==
+                 hipSuccess;
+    if (copied && sc != nullptr)
+        copied = hipMemcpyAsync(&host[1], sc, sizeof(int), hipMemcpyDeviceToHost, nullptr) ==
+                 hipSuccess;
+    e = hipDeviceSynchronize();
+    if (e != hipSuccess) {
+        g_last_hip_error = (int)e;
+        die(ATN_ERR_HIP, where);
+    }
+    // without the pinned words (or a failed copy), the blocking reads
+    const bool clean =
+        copied && (lib_ws == nullptr || host[0] == 0) && (sc == nullptr || host[1] == 0);
+    if (!clean) {
+        const int ws = workspace_status(nullptr, nullptr);
+        if (ws != ATN_OK) die(ws, where);
+    }
 }
 
 atn_pe_desc rope_desc(int rotary, int pairing, bool q, bool k, const float* c, const float* s) {
