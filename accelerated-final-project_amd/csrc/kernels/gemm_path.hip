@@ -158,6 +158,7 @@ constexpr int kOutBf16 = 1;       // C = bf16(acc), row stride ldc
 // pair is rounded to bf16 (nearest even) by gfx950's v_cvt_pk_bf16_f32.
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ float f16lo_mul(uint32_t x, float f) {
     float r;
     asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(x), "v"(f));
@@ -1574,7 +1575,8 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm_pv_dma(GemmArgs g) {
     };
     // the rows' softmax factors (as in k_gemm's NN form) into the LDS table,
     // then E of step 0 to LDS.  vmcnt(pending) waits only for this tile's
-    // loads (the previous tile's 32 output stores were issued after them);
+    // loads (the previous tile's kOutStores output stores were issued after
+    // them);
     // the compiler's own waits for the statistics registers at the loop head
     // (in the first four waves) still cover every outstanding operation.
     auto finish = [&](auto edge, auto pending) __attribute__((always_inline)) {
@@ -1593,8 +1595,8 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm_pv_dma(GemmArgs g) {
                 fac[tid * kFacTiles + t2] =
                     (m == -INFINITY || t2 >= g.gt) ? 0.f : __expf(mt[t2] - m) * inv;
         }
-        if constexpr (decltype(pending)::value == 32)
-            __builtin_amdgcn_s_waitcnt(0x8F70);  // vmcnt(32)
+        if constexpr (decltype(pending)::value == 16)
+            __builtin_amdgcn_s_waitcnt(0x4F70);  // vmcnt(16)
         else
             __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
         __syncthreads();  // the factor table, V of steps 0 and 1
@@ -1618,7 +1620,8 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm_pv_dma(GemmArgs g) {
     using EdgeF = std::integral_constant<bool, false>;
     using EdgeT = std::integral_constant<bool, true>;
     using P0 = std::integral_constant<int, 0>;
-    using P32 = std::integral_constant<int, 32>;
+    constexpr int kOutStores = 16;  // output stores per thread and tile (store_out_lds)
+    using P16 = std::integral_constant<int, kOutStores>;
 
     // lane: output row m0 + wm + 32 i + lane % 32, columns n0 + wn + 32 j +
     // 8 (r / 4) + 4 (lane / 32) + r % 4: four consecutive bf16 per group of r
@@ -1667,6 +1670,59 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm_pv_dma(GemmArgs g) {
         }
     };
 
+    // Persistent form: the interior output through LDS.  Between the K loop
+    // and the next tile's first E chunk the A stages are free (the next
+    // tile's first V loads go to the B stages): two halves of 128 rows, each
+    // written by its four waves as bf16 rows of 256 elements padded to
+    // kOutRow (rows 0-63 of the half in a0s, 64-127 in a1s; every address is
+    // a per-lane base plus an immediate offset), then read back and stored
+    // 16 contiguous bytes per thread: a wave store
+    // writes two whole 512-byte output rows, instead of 32 row pieces of 16
+    // bytes 8 KiB or more apart, which the store path handles far more
+    // slowly.  Each thread issues kOutStores stores.
+    constexpr int kOutRow = kBN + 8;  // elements: 528-byte rows, 4 banks apart
+    static_assert(64 * kOutRow <= kTileElems, "a half-tile's 64 rows fit one A stage");
+    auto store_out_lds = [&](int obh, int om0, int on0) __attribute__((always_inline)) {
+        uint16_t* C = static_cast<uint16_t*>(g.C) + obh * g.sc;
+        const __amdgpu_buffer_rsrc_t rc = gemm_rsrc(C, (long)g.M * g.ldc);
+        const uint32_t ldc = (uint32_t)g.ldc;
+        const int rr = tid >> 5, ch = tid & 31;  // read: rows rr + 16 k, chunk ch
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            if ((wave >> 2) == h) {
+#pragma unroll
+                for (int i = 0; i < TI; ++i) {
+                    uint16_t* dst = i < 2 ? a0s : a1s;
+                    const int r = (i & 1) * 32 + (lane & 31);  // row in the stage
+#pragma unroll
+                    for (int j = 0; j < TJ; ++j)
+#pragma unroll
+                        for (int rg = 0; rg < 4; ++rg)
+                            *reinterpret_cast<u32x2*>(
+                                &dst[r * kOutRow + wn + j * 32 + 8 * rg + 4 * (lane >> 5)]) =
+                                pack4(acc[i][j], rg);
+                }
+            }
+            __syncthreads();
+            // four reads in flight at a time (the other half's accumulators,
+            // and the next tile's first loads, are live here)
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const int r = rr + 16 * (k & 3);  // row in the stage
+                const uint16_t* src = (k < 4 ? a0s : a1s) + r * kOutRow + 8 * ch;
+                const u32x4 v = *reinterpret_cast<const u32x4*>(src);
+                const uint32_t vo =
+                    2u * ((uint32_t)(om0 + 128 * h + 64 * (k >> 2) + r) * ldc +
+                          (uint32_t)(on0 + 8 * ch));
+                __builtin_amdgcn_raw_buffer_store_b128(v, rc, (int)vo, 0, 0);
+                if ((k & 3) == 3) __builtin_amdgcn_sched_barrier(0);
+            }
+            // the second half overwrites the stages; after it, the next
+            // tile's first E chunk does, behind finish()'s barrier
+            if (h == 0) __syncthreads();
+        }
+    };
+
     auto zero_acc = [&]() __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < TI; ++i)
@@ -1690,14 +1746,14 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm_pv_dma(GemmArgs g) {
         store_out(bh, m0, n0, interior);
     } else {
         issue(EdgeF{});
-        // vmcnt(32) covers this tile's loads once the previous tile's 32
-        // stores were issued after them
+        // vmcnt(kOutStores) covers this tile's loads once the previous tile's
+        // output stores were issued after them
         bool first = true;
         for (;;) {
             if (first)
                 finish(EdgeF{}, P0{});
             else
-                finish(EdgeF{}, P32{});
+                finish(EdgeF{}, P16{});
             zero_acc();
             kloop(EdgeF{});
             const int obh = bh, om0 = m0, on0 = n0;
@@ -1709,7 +1765,7 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm_pv_dma(GemmArgs g) {
                 set_tile(tn);
                 issue(EdgeF{});
             }
-            store_out(obh, om0, on0, true);
+            store_out_lds(obh, om0, on0);
             if (!more) break;
             first = false;
         }
