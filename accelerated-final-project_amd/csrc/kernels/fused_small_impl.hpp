@@ -875,7 +875,7 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
         else if (cnt > 2 && cnt <= 4) run(std::integral_constant<int, 4>{});
         else if (cnt > 4) run(std::integral_constant<int, 8>{});
     }
-    if constexpr (defer_v) {
+    if constexpr (defer_v && !XL) {
         if (n > 1) {
             // after the partial stores, in issue order (kept there as the
             // slice loads are)
@@ -913,8 +913,9 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
         };
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");  // stores stay above the wait
         // this wave's partials have completed: every vector memory operation
-        // but the kKV V loads issued after them (vmcnt counts in issue order)
-        if constexpr (defer_v) {
+        // but the kKV V loads issued after them (vmcnt counts in issue order;
+        // XL plans issue V later)
+        if constexpr (defer_v && !XL) {
             static_assert(kKV == 8 || kKV == 16, "vmcnt encoding below");
             __builtin_amdgcn_s_waitcnt(kKV == 8 ? 0x0F78 : 0x4F70);  // vmcnt(kKV)
         } else {
@@ -942,11 +943,29 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
             poison_slice<T>(O, orow0, Lq, D, d0, dc);
             return;
         }
-        // V into LDS while the other slices of the group arrive
-        if constexpr (defer_v) {
+        // V into LDS while the other slices of the group arrive.  XL plans:
+        // waves 1-3 load V only now, once the arrival is out; wave 0, which
+        // polls, only once its wait is over (its atomic's return and its
+        // polls would otherwise wait for V: vmcnt retires in issue order);
+        // every wave then writes V to LDS while its exchange loads are in
+        // flight.
+        auto store_v_all = [&]() __attribute__((always_inline)) {
 #pragma unroll
             for (int u = 0; u < kKV; ++u)
                 if (u < ckv) store_v(r0 + u * rstep, bv[u]);
+        };
+        if constexpr (defer_v) {
+            if constexpr (XL) {
+                if (wave != 0) {
+                    __builtin_amdgcn_sched_barrier(0);
+                    issue_v(0, bv);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            } else {
+#pragma unroll
+                for (int u = 0; u < kKV; ++u)
+                    if (u < ckv) store_v(r0 + u * rstep, bv[u]);
+            }
         }
         const float* pg = a.part + (size_t)rg * n * E;
         float* rd = a.red + (size_t)rg * E;
@@ -957,6 +976,12 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
             float w[kMaxWords];
             if constexpr (XL) {
                 if (!xcd_wait(rc, 0, base1, &flag)) return false;
+                if constexpr (defer_v)
+                    if (wave == 0) {
+                        __builtin_amdgcn_sched_barrier(0);
+                        issue_v(0, bv);
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
             } else {
                 if (!wait_done(done1, n, tag, &flag)) return false;
             }
@@ -987,6 +1012,7 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
                         }
                     }
                 }
+                if constexpr (XL && defer_v) store_v_all();
                 // sums in slice order (the zeros past the last block are
                 // never stored); 4 consecutive entries share one row of S
                 const int e0 = b0 * 256 + (tid & 63) * 4;
@@ -1108,7 +1134,9 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
             // multiple of 512): vectors tid + 256 u
             step = 2;
             if constexpr (XL) {
-                if (!xcd_arrive(rc, 1, share, true, &flag)) return false;
+                const unsigned base2 = xcd_arrive_only(rc, 1, share);
+                if constexpr (defer_v) store_v_all();
+                if (!xcd_wait(rc, 1, base2, &flag)) return false;
             } else {
                 if (tid == 0) st_done(done2 + c, tag);
                 if (!wait_done(done2, n, tag, &flag)) return false;
