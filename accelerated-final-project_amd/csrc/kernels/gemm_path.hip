@@ -1889,14 +1889,19 @@ __device__ __forceinline__ void ld4f(const float* p, float* v) {
     v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
 }
 
-template <int PEK, int U>
+// S = 2 (rows of at most 128 units, U = 1): the two halves of the workgroup
+// take two rows of the group at once, so no thread idles.
+template <int PEK, int U, int S = 1>
 __global__ __launch_bounds__(kEncThreads) void k_encode_f16_regs(const uint16_t* __restrict__ in,
                                                                  uint16_t* __restrict__ out,
                                                                  float* __restrict__ inv,
                                                                  long n_rows, int seq_len, int D,
                                                                  PeSide pe) {
+    static_assert(S == 1 || (S == 2 && U == 1), "split rows: one unit per thread");
     __shared__ float red[2][kEncRows][kEncThreads / 64];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int sub = S == 2 ? (int)threadIdx.x >> 7 : 0;  // this half's row of a pair
+    const int tid = S == 2 ? (int)threadIdx.x & 127 : (int)threadIdx.x;  // job index
     const int pos = (int)(blockIdx.x % (unsigned)seq_len);
     const long h0 = (long)(blockIdx.x / (unsigned)seq_len) * kEncGroup;  // first row group member
     const long nh = n_rows / seq_len;
@@ -1940,14 +1945,16 @@ __global__ __launch_bounds__(kEncThreads) void k_encode_f16_regs(const uint16_t*
         }
     }
 
-    for (int i = 0; i < nrow; i += kEncRows) {
-        const int par = (i / kEncRows) & 1;  // red[] parity: one barrier per batch of rows
+    // row of slot rr in the batch starting at i
+    auto rix = [&](int i, int rr) { return i + S * rr + sub; };
+    for (int i = 0; i < nrow; i += kEncRows * S) {
+        const int par = (i / (kEncRows * S)) & 1;  // red[] parity: one barrier per batch
         float v[kEncRows][U][2][8];
         // all loads of the batch first
 #pragma unroll
         for (int rr = 0; rr < kEncRows; ++rr) {
-            if (i + rr >= nrow) continue;
-            const uint16_t* xr = in + ((h0 + i + rr) * seq_len + pos) * D;
+            if (rix(i, rr) >= nrow) continue;
+            const uint16_t* xr = in + ((h0 + rix(i, rr)) * seq_len + pos) * D;
 #pragma unroll
             for (int k = 0; k < U; ++k) {
                 if (d0[k] >= 0) unpack_bf16x8(*reinterpret_cast<const uint4*>(xr + d0[k]), v[rr][k][0]);
@@ -1958,7 +1965,7 @@ __global__ __launch_bounds__(kEncThreads) void k_encode_f16_regs(const uint16_t*
 #pragma unroll
         for (int rr = 0; rr < kEncRows; ++rr) {
             m[rr] = 0.f;
-            if (i + rr >= nrow) continue;
+            if (rix(i, rr) >= nrow) continue;
 #pragma unroll
             for (int k = 0; k < U; ++k) {
                 if (d0[k] < 0) continue;
@@ -2001,14 +2008,17 @@ __global__ __launch_bounds__(kEncThreads) void k_encode_f16_regs(const uint16_t*
         __syncthreads();
 #pragma unroll
         for (int rr = 0; rr < kEncRows; ++rr) {
-            if (i + rr >= nrow) continue;
-            const float mr = fmaxf(fmaxf(red[par][rr][0], red[par][rr][1]),
-                                   fmaxf(red[par][rr][2], red[par][rr][3]));
+            if (rix(i, rr) >= nrow) continue;
+            // the row's waves: all four, or this half's two
+            const float mr =
+                S == 2 ? fmaxf(red[par][rr][2 * sub], red[par][rr][2 * sub + 1])
+                       : fmaxf(fmaxf(red[par][rr][0], red[par][rr][1]),
+                               fmaxf(red[par][rr][2], red[par][rr][3]));
             int kexp = 0;
             if (mr > 0.f && mr <= 3.0e38f) kexp = 14 - ilogbf(mr);
             kexp = max(-100, min(100, kexp));
             const float up = ldexpf(1.0f, kexp);
-            const long row = (h0 + i + rr) * seq_len + pos;
+            const long row = (h0 + rix(i, rr)) * seq_len + pos;
             if (tid == 0) inv[row] = ldexpf(1.0f, -kexp);
             uint16_t* yr = out + row * D;
 #pragma unroll
@@ -2136,11 +2146,15 @@ hipError_t launch_gemm_qk_enc(int benc, const uint16_t* Qe, const uint16_t* K, c
 }
 
 template <int PEK>
-static void launch_encode_regs(int units, const uint16_t* in, uint16_t* out, float* inv,
+static void launch_encode_regs(int jobs, const uint16_t* in, uint16_t* out, float* inv,
                                long n_rows, int seq_len, int D, const PeSide& pe, hipStream_t st) {
+    const int units = (jobs + kEncThreads - 1) / kEncThreads;
     const long groups = (n_rows / seq_len + kEncGroup - 1) / kEncGroup;
     const dim3 grid((unsigned)(groups * seq_len)), block(kEncThreads);
-    if (units <= 1)
+    if (jobs <= kEncThreads / 2)
+        hipLaunchKernelGGL((k_encode_f16_regs<PEK, 1, 2>), grid, block, 0, st, in, out, inv,
+                           n_rows, seq_len, D, pe);
+    else if (units <= 1)
         hipLaunchKernelGGL((k_encode_f16_regs<PEK, 1>), grid, block, 0, st, in, out, inv, n_rows,
                            seq_len, D, pe);
     else if (units == 2)
@@ -2165,20 +2179,19 @@ hipError_t launch_encode_f16(int pek, const uint16_t* in, uint16_t* out, float* 
     if (fast) {
         const int hu = (pek == kPeRopeHalf && pe.on) ? pe.rotary / 16 : 0;
         const int jobs = D / 8 - hu;
-        const int units = (jobs + kEncThreads - 1) / kEncThreads;
         switch (pek) {
             case kPeNone:
-                launch_encode_regs<kPeNone>(units, in, out, inv, n_rows, seq_len, D, pe, st);
+                launch_encode_regs<kPeNone>(jobs, in, out, inv, n_rows, seq_len, D, pe, st);
                 break;
             case kPeRopeInterleaved:
-                launch_encode_regs<kPeRopeInterleaved>(units, in, out, inv, n_rows, seq_len, D, pe,
+                launch_encode_regs<kPeRopeInterleaved>(jobs, in, out, inv, n_rows, seq_len, D, pe,
                                                        st);
                 break;
             case kPeRopeHalf:
-                launch_encode_regs<kPeRopeHalf>(units, in, out, inv, n_rows, seq_len, D, pe, st);
+                launch_encode_regs<kPeRopeHalf>(jobs, in, out, inv, n_rows, seq_len, D, pe, st);
                 break;
             case kPeSinusoidal:
-                launch_encode_regs<kPeSinusoidal>(units, in, out, inv, n_rows, seq_len, D, pe, st);
+                launch_encode_regs<kPeSinusoidal>(jobs, in, out, inv, n_rows, seq_len, D, pe, st);
                 break;
             default:
                 return hipErrorInvalidValue;
