@@ -387,14 +387,14 @@ __device__ bool xcd_arrive(__amdgpu_buffer_rsrc_t rc, int k, unsigned share, boo
 // after its exchange words have completed (s_waitcnt), so they can be read
 // once every done word is seen.  Returns false for the whole workgroup on
 // timeout.
-__device__ bool wait_done(const unsigned* done, int n, unsigned tag, int* flag_lds) {
+__device__ bool wait_done(const unsigned* done, int n, int stride, unsigned tag, int* flag_lds) {
     if (threadIdx.x < 64) {
         bool ok = true;
         for (int it = 0;; ++it) {
             bool mine = true;
             for (int i = threadIdx.x; i < n; i += 64)
-                mine &= __hip_atomic_load(const_cast<unsigned*>(done + i), __ATOMIC_RELAXED,
-                                          __HIP_MEMORY_SCOPE_AGENT) == tag;
+                mine &= __hip_atomic_load(const_cast<unsigned*>(done + i * stride),
+                                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == tag;
             if (__all(mine)) break;
             if (it > kSpinLimit) {
                 ok = false;
@@ -889,8 +889,13 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
     // ---- 3. all-reduce of S over the group's slices (tagged words, or
     // XCD-local arrival counters)
     if (n > 1) {
-        unsigned* done1 = a.done + rg * n;
-        unsigned* done2 = a.done + 2048 + rg * n;
+        // done word of slice c: rg + 32 c when the group's slices fit (each
+        // in its own 128-byte line, instead of n words in one or two lines
+        // that every slice of the group stores to and polls), else rg n + c
+        const bool spread = n <= 64 && a.G <= 32;
+        const int dstride = spread ? 32 : 1;
+        unsigned* done1 = a.done + (spread ? rg : rg * n);
+        unsigned* done2 = done1 + 2048;
         // XL: this slice's share of the call's units, the group's counters
         const unsigned share =
             c < n - 1 ? (unsigned)c + 1u : kXcdUnits - (unsigned)(n - 1) * (unsigned)n / 2u;
@@ -934,7 +939,7 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
         const unsigned tag = exchange_tag(epoch, rg);
         unsigned base1 = 0;
         if constexpr (XL) base1 = xcd_arrive_only(rc, 0, share);
-        else if (tid == 0) st_done(done1 + c, tag);
+        else if (tid == 0) st_done(done1 + c * dstride, tag);
         if (sh_failed) {  // an earlier call timed out: fail closed
             if constexpr (XL) {
                 __syncthreads();
@@ -983,7 +988,7 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
                         __builtin_amdgcn_sched_barrier(0);
                     }
             } else {
-                if (!wait_done(done1, n, tag, &flag)) return false;
+                if (!wait_done(done1, n, dstride, tag, &flag)) return false;
             }
             if (a.gather1) {
                 // one gather, 16-byte words: thread t sums entries 4 (t % 64)
@@ -1138,8 +1143,8 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
                 if constexpr (defer_v) store_v_all();
                 if (!xcd_wait(rc, 1, base2, &flag)) return false;
             } else {
-                if (tid == 0) st_done(done2 + c, tag);
-                if (!wait_done(done2, n, tag, &flag)) return false;
+                if (tid == 0) st_done(done2 + c * dstride, tag);
+                if (!wait_done(done2, n, dstride, tag, &flag)) return false;
             }
             // vectors tid + 256 u, u < nv (a wave-uniform bound; a lane's
             // vectors past E read zeros from past the buffer); 4
