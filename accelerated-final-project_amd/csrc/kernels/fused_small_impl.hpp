@@ -338,7 +338,7 @@ __device__ __forceinline__ void ld_words(const float* base, int stride, int cnt,
 }
 
 // XL plans.  Wave 0: lane 0 adds `share` to the row group's arrival counter
-// k (an atomic add performed at this XCD's L2, returning the prior value,
+// at word k of rc (an atomic add performed at this XCD's L2, returning the prior value,
 // whose multiple of kXcdUnits is the call's base); with `wait`, the wave
 // then polls the counter through L2 until exactly every slice's units of
 // this call have arrived.  The other waves wait at the barrier.  A workgroup arrives
@@ -631,7 +631,7 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar)
     const int lr = lane & 15, lk = lane >> 4;
     const int n = a.nchunk;
-    int rg, c, xcd_slot = 0;
+    int rg, c, xcd_slot = 0, xk1 = 1;
     if constexpr (XL) {
         // place id / 8 = gi * n + c on XCD x: slice c of the XCD's gi-th row
         // group; XCD x holds row groups [x * base + min(x, rem), + cnt)
@@ -641,7 +641,12 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
         const int base = a.G >> 3, rem = a.G & 7;
         if (gi >= base + (x < rem ? 1 : 0)) return;  // no row group here (whole workgroup)
         rg = x * base + min(x, rem) + gi;
-        xcd_slot = x * kXcdCtrWords + 2 * gi;
+        // the row group's two counters: 32 words apart, and groups 64 apart
+        // (each counter in a 128-byte line of its own) when an XCD holds at
+        // most 4 row groups, else packed
+        const bool spread = a.G <= 32;
+        xcd_slot = x * kXcdCtrWords + (spread ? 64 * gi : 2 * gi);
+        xk1 = spread ? 32 : 1;
     } else {
         // id = (qb * BH + bh) * n + c
         const int BH = a.G / a.QB;
@@ -899,7 +904,7 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
         // XL: this slice's share of the call's units, the group's counters
         const unsigned share =
             c < n - 1 ? (unsigned)c + 1u : kXcdUnits - (unsigned)(n - 1) * (unsigned)n / 2u;
-        const __amdgpu_buffer_rsrc_t rc = make_rsrc(a.xctr + xcd_slot, 8);
+        const __amdgpu_buffer_rsrc_t rc = make_rsrc(a.xctr + xcd_slot, 4 * xk1 + 4);
         // reduce-scatter: this workgroup owns entries [e0, e1) of the group
         const int per_rs = fdiv(E + n - 1, n, a.m_n);
         const int e0_rs = min(E, c * per_rs), e1_rs = min(E, e0_rs + per_rs);
@@ -913,7 +918,7 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
                 __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
                 __builtin_amdgcn_s_waitcnt(0);
                 __syncthreads();
-                xcd_arrive(rc, 1, share, false, &flag);
+                xcd_arrive(rc, xk1, share, false, &flag);
             }
         };
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");  // stores stay above the wait
@@ -1139,9 +1144,9 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
             // multiple of 512): vectors tid + 256 u
             step = 2;
             if constexpr (XL) {
-                const unsigned base2 = xcd_arrive_only(rc, 1, share);
+                const unsigned base2 = xcd_arrive_only(rc, xk1, share);
                 if constexpr (defer_v) store_v_all();
-                if (!xcd_wait(rc, 1, base2, &flag)) return false;
+                if (!xcd_wait(rc, xk1, base2, &flag)) return false;
             } else {
                 if (tid == 0) st_done(done2 + c * dstride, tag);
                 if (!wait_done(done2, n, dstride, tag, &flag)) return false;
