@@ -223,6 +223,64 @@ def test_fused_row_groups_and_exchanges(am, dev, monkeypatch, rows, exchange, xc
         assert n == 0, f"{n} mismatches, max abs {mabs}, max rel {mrel}"
 
 
+# (shape, forced plan): each of the two layouts of the exchange's sync words.
+# Device scope: a group's done words one per 128-byte line (n <= 64 slices
+# and at most 32 row groups), or packed (more slices, or more groups).
+# XL: a group's arrival counters one per line (at most 32 row groups), or
+# packed.
+_LAYOUTS = [
+    ((1, 4, 64, 64, 2048), {"ATN_FUSED_ROWS": "16", "ATN_FUSED_EXCHANGE": "rsag",
+                            "ATN_FUSED_XCD": "0"}),  # device, spread
+    ((1, 1, 16, 16, 8192), {"ATN_FUSED_ROWS": "16", "ATN_FUSED_DC": "64",
+                            "ATN_FUSED_EXCHANGE": "rsag", "ATN_FUSED_XCD": "0"}),  # 128 slices
+    ((1, 36, 64, 128, 448), {"ATN_FUSED_ROWS": "64", "ATN_FUSED_EXCHANGE": "rsag",
+                             "ATN_FUSED_XCD": "0"}),  # device, 36 groups
+    ((1, 4, 64, 64, 2048), {"ATN_FUSED_ROWS": "16", "ATN_FUSED_EXCHANGE": "gather",
+                            "ATN_FUSED_XCD": "1"}),  # XL, spread
+    ((1, 36, 64, 128, 448), {"ATN_FUSED_ROWS": "64", "ATN_FUSED_EXCHANGE": "rsag",
+                             "ATN_FUSED_XCD": "1"}),  # XL, 36 groups
+]
+
+
+def test_fused_sync_word_layouts_share_a_workspace(am, dev, monkeypatch):
+    """The exchange's sync words are laid out one per cache line or packed,
+    depending on the plan; calls of every layout, alternating on one
+    workspace (sized for the largest), each give the oracle's result three
+    times over, and no wait times out: a word one layout leaves behind never
+    passes for another layout's (done words carry call tags; every call adds
+    exactly its units to each counter it uses)."""
+    import hip_rt
+    cases = []
+    for shape, env in _LAYOUTS:
+        B, Hh, Lq, Lk, D = shape
+        ins, host = H.device_inputs((B, Hh, Lq, D), (B, Hh, Lk, D), 701 + D + Hh)
+        ref = oracle.attention(*host, nthreads=16)
+        cases.append((shape, env, ins, ref))
+    need = 0
+    for shape, env, _, _ in cases:
+        for k, v in env.items():
+            monkeypatch.setenv(k, v)
+        need = max(need, am.workspace_bytes(0, *shape))
+        for k in env:
+            monkeypatch.delenv(k)
+    ws = hip_rt.DeviceArray((need // 4,), "f32", fill=0)
+    for rnd in range(3):
+        for shape, env, (q, k_, v), ref in cases:
+            print(f"[case] sync word layout round {rnd} {shape} {env}", flush=True)
+            for k, val in env.items():
+                monkeypatch.setenv(k, val)
+            B, Hh, Lq, Lk, D = shape
+            assert am.path(0, B, Hh, Lq, Lk, D) == am.ATN_PATH_FUSED_SMALL
+            out = H.empty((B, Hh, Lq, D))
+            am.attention_ex(q, k_, v, out, workspace=ws)
+            hip_rt.synchronize()
+            assert am.sync_status(ws, B, Hh) == 0
+            n, mabs, mrel = H.check_f32(out.numpy(), ref)
+            assert n == 0, f"{shape} {env}: {n} mismatches, max abs {mabs}, max rel {mrel}"
+            for k in env:
+                monkeypatch.delenv(k)
+
+
 @pytest.mark.parametrize("rows,exchange", [("64", "rsag"), ("", "")], ids=["rows64-rsag", "default"])
 def test_fused_uneven_slices(am, dev, monkeypatch, rows, exchange):
     """36 heads with 7 D-slices each: with 64-row groups and slices of 64 the
