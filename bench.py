@@ -48,8 +48,8 @@ MALL_FLUSH_MIB = 512  # > the 256 MiB MALL: a copy this large evicts it
 # FETCH_SIZE / WRITE_SIZE and scaled by a known-size device copy; keyed by
 # (config, head_dim), with the profile that holds the counts.
 MEASURED_TRAFFIC = {
-    (2, 2048): ((11617 + 3080) * 1024, "profiles/fused_small_cfg2_traffic.md"),
-    (3, 8192): ((23546 + 6224) * 1024, "profiles/fused_small_cfg3_kernel_trace.md"),
+    (2, 2048): ((11611 + 3080) * 1024, "profiles/fused_small_cfg2_traffic.md"),
+    (3, 8192): ((23758 + 6224) * 1024, "profiles/fused_small_cfg3_kernel_trace.md"),
 }
 
 # (name, dtype, B, H, Lq, Lk, D, pe, sigma)
