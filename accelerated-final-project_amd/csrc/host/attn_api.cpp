@@ -506,17 +506,18 @@ FusedPlan fused_plan_uncached(int dtype, int pek, const Shape& s, bool query_dev
         return p;
     };
     // Estimated time in us beyond the fixed cost.  Device-scope plans: each
-    // CU's Q/K/V slice loads (0.055 us per KiB), the slices (0.0373 us
-    // each), reduce-scatter's second round trip (2.5 us), each CU's exchange
-    // reads (0.04 us per KiB) and the workgroup count (0.358 us per CU's
-    // worth).  XCD-local plans: 2.5 us less, reduce-scatter's second step
-    // 2.5 us and 0.015 us per KiB of exchange reads (L2); their XCDs also
-    // fetch whole heads' K and V (each XCD holds a block of row groups),
-    // where device-scope plans spread every head over all 8: the extra bytes
-    // per XCD cost about 1 us per MB.  The coefficients were chosen against
-    // a sweep that timed every plan of 15 fp32/bf16 shapes (244 plans, B*H
-    // 1-16, Lq 16-64, Lk 16-128, D 512-8192): on it they pick plans within
-    // 0.3 us in total of the fastest measured on each shape.
+    // CU's Q/K/V slice loads (0.03 us per KiB), the slices (0.02 us each),
+    // reduce-scatter's second round trip (1 us), each CU's exchange reads
+    // (0.04 us per KiB) and the workgroup count (0.358 us per CU's worth).
+    // XCD-local plans: 2 us less, reduce-scatter's second step 2.5 us, and
+    // exchange reads from L2 no cost of their own at this resolution; their
+    // XCDs also fetch whole heads' K and V (each XCD holds a block of row
+    // groups), where device-scope plans spread every head over all 8: the
+    // extra bytes per XCD cost about 1 us per MB.  The coefficients were
+    // chosen against a sweep that timed every plan of 15 fp32/bf16 shapes
+    // (269 plans, B*H 1-16, Lq 16-64, Lk 16-128, D 512-8192): on it they pick
+    // the fastest measured plan of every shape, and fitted on 14 shapes they
+    // lose 0.6 us in total on the 15 held out in turn.
     const double kv_head = 2.0 * (double)s.Lk * (double)s.D * es;
     auto cost = [&](const FusedPlan& p) {
         const double per_cu = (double)p.per_cu;
@@ -528,12 +529,11 @@ FusedPlan fused_plan_uncached(int dtype, int pek, const Shape& s, bool query_dev
             const int64_t G = s.BH * QB, gpx = (G + 7) / 8;
             const double heads_x = (double)std::max<int64_t>(1, (gpx + QB - 1) / QB);
             const double kv_extra = std::max(0.0, heads_x * kv_head - (double)s.BH * kv_head / 8.0);
-            return 0.055 * kib * per_cu + 0.0373 * p.nchunk + (!p.gather1 ? 2.5 : 0.0) +
-                   0.015 * xkib * per_cu + 0.358 * p.workgroups / cus - 2.5 + kv_extra * 1e-6;
+            return 0.03 * kib * per_cu + 0.02 * p.nchunk + (!p.gather1 ? 2.5 : 0.0) +
+                   0.358 * p.workgroups / cus - 2.0 + kv_extra * 1e-6;
         }
-        return 0.055 * kib * per_cu + 0.0373 * p.nchunk +
-               (p.nchunk > 1 && !p.gather1 ? 2.5 : 0.0) + 0.04 * xkib * per_cu +
-               0.358 * p.workgroups / cus;
+        return 0.03 * kib * per_cu + 0.02 * p.nchunk + (p.nchunk > 1 && !p.gather1 ? 1.0 : 0.0) +
+               0.04 * xkib * per_cu + 0.358 * p.workgroups / cus;
     };
     // overrides (tuning): row group size, slice width, exchange
     const int force_rows = env_int("ATN_FUSED_ROWS");
