@@ -41,7 +41,10 @@
 // writer waits for its exchange stores to complete (s_waitcnt), then
 // publishes one done word per workgroup and step; wave 0 of each reader
 // polls the n done words of its group (one small word per writer keeps the
-// polling traffic low) and the exchange words are then read once.  Done
+// polling traffic low; where the plan allows, each word has a 128-byte line
+// of its own, since one line that every slice of a group stores to and
+// polls is a hot spot at the coherence point) and the exchange words are
+// then read once.  Done
 // words carry a tag made of the row group g (< 2048) and the group's epoch
 // word in the workspace's sync region, read at start (exchange_tag below):
 // a call that has seen every slice's done word of its group knows that
@@ -76,7 +79,8 @@
 // exactly complete: since the shares differ, a slice that arrived twice or
 // never makes the wait time out (reported) rather than pass early.
 // Counter words are indexed by the physical XCD, so only that XCD's L2
-// ever holds their lines.
+// ever holds their lines; with at most 4 row groups per XCD each counter
+// has a line of its own.
 #pragma once
 
 #include <algorithm>
@@ -589,9 +593,9 @@ __device__ __forceinline__ int wave_tiles(int wave, int nrb, int tiles, int* rb,
 // each thread issues per round.  Forms 1-3 hold every row of the slice in
 // one round of (2, 8), (4, 16) or (8, 16) loads -- the smallest that fits,
 // so that no load instruction is issued for rows that do not exist -- and
-// then V is loaded with Q and K but written to LDS only while the workgroup
-// waits for the other slices; form 0 loops over rounds of (8, 16).  The
-// host picks the kernel variant with this function.
+// then V is loaded and written to LDS around the exchange (see the kernel);
+// form 0 loops over rounds of (8, 16).  The host picks the kernel variant
+// with this function.
 template <int FORM>
 struct LoadForm {
     static constexpr int kQ = FORM == 1 ? 2 : (FORM == 2 ? 4 : 8);
@@ -688,12 +692,10 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
     // count them, so a round issues kQ row loads of Q and kKV of K and of V
     // before the first is encoded and stored.  With one round (FORM != 0, a
     // template parameter, so that the one-round code is straight-line code
-    // of its own) the loads are issued first thing, before the LDS geometry
-    // and the rest of the set-up, and V is only written to LDS once this
-    // workgroup's partial scores are out, while it waits for the other
-    // slices (its loads' latency and its stores both hide behind the
-    // exchange).  (The host sends this kernel only shapes with D % 4 == 0
-    // and aligned bases.)
+    // of its own) the Q and K loads are issued first thing, before the LDS
+    // geometry and the rest of the set-up, and V's loads and LDS stores
+    // hide behind the exchange (the placements below).  (The host sends this
+    // kernel only shapes with D % 4 == 0 and aligned bases.)
     typedef typename Raw4<T>::type Raw;
     constexpr int kQ = LoadForm<FORM>::kQ, kKV = LoadForm<FORM>::kKV;
     constexpr bool defer_v = FORM != 0;
@@ -745,8 +747,10 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
     // One round with an exchange: V is loaded only once the partial scores
     // are out (its loads land while the workgroup waits for the group's other
     // slices, and the Q and K loads, which every workgroup issues at once,
-    // do not share the memory system with them).  A single slice has no wait
-    // to hide them behind, so it loads V with Q and K.
+    // do not share the memory system with them): at device scope right after
+    // the partial stores, in an XL plan after the arrival (wave 0 only once
+    // its wait is over).  A single slice has no wait to hide them behind, so
+    // it loads V with Q and K.
     Raw bq[kQ], bk[kKV], bv[kKV];
     if constexpr (defer_v) issue(0, bq, bk, bv, n == 1);
 
