@@ -15,10 +15,12 @@
 //      wave.  Values that are not bf16 -- fp32 inputs, and bf16 inputs
 //      after a positional encoding -- are split into hi + lo bf16 parts and
 //      multiplied as a_hi b_hi + a_hi b_lo + a_lo b_hi (fp32 accumulation),
-//      which keeps about 16 significant bits of every product: for fp32 that
-//      is far inside the 1e-4 bar and about five times the throughput of
-//      fp32 MFMA (v_mfma_f32_16x16x4_f32), whose dependent chains bounded
-//      this phase;
+//      which keeps about 16 significant bits of every product, at about
+//      five times the throughput of fp32 MFMA (v_mfma_f32_16x16x4_f32),
+//      whose dependent chains bounded this phase.  For fp32 inputs the
+//      logit error grows with the logits' size: the 1e-4 bar holds for
+//      logits up to about +-10 (inputs of sigma 1.5 at D = 512-8192); at
+//      +-18 (sigma 2) up to about two elements in 10^4 exceed it;
 //   3. all-reduces S over the group's slices through global memory, either
 //      in one gather (every workgroup reads every slice's partial of its
 //      group: one memory round trip) or, when that volume is too large, as
