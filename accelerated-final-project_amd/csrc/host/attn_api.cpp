@@ -80,6 +80,9 @@ struct PePlan {
     float base = 10000.0f;
     int pairing = ATN_ROPE_INTERLEAVED;
     bool caller_tables = false;
+    // the call may not take the single-launch kernel (a synchronous call's
+    // second attempt after that kernel's exchange timed out)
+    bool no_fused = false;
 };
 
 int check_pe(const atn_pe_desc* pe, int D, PePlan* plan) {
@@ -692,7 +695,7 @@ size_t library_cap() {
 // -1 for "unknown" and get the largest of the candidate paths instead.
 size_t path_need(int dtype, const Shape& s, const PePlan& plan, bool query_device, int vec,
                  int a16) {
-    const FusedPlan fp = fused_plan(dtype, plan.pek, s, query_device);
+    const FusedPlan fp = plan.no_fused ? FusedPlan{} : fused_plan(dtype, plan.pek, s, query_device);
     const GemmPlan gp = gemm_plan(dtype, s, plan);
     const size_t split = kSyncBytes + stream_plan(s).bytes;
     if (vec < 0 || a16 < 0)
@@ -756,7 +759,7 @@ int attention_run(int dtype, const void* Q, const void* K, const void* V, void* 
     const StreamPlan sp = stream_plan(s);
     // the device's own capacity decides between the single-launch kernel
     // and the three-kernel pipeline
-    const FusedPlan fd = fused_plan(dtype, plan.pek, s, true);
+    const FusedPlan fd = plan.no_fused ? FusedPlan{} : fused_plan(dtype, plan.pek, s, true);
     const size_t va = dtype == ATN_DTYPE_F32 ? 16 : 8;
     const int vec_qk = (D % 4 == 0) && aligned(Q, va) && aligned(K, va);
     const int vec_vo = (D % 4 == 0) && aligned(V, va) && aligned(out, va);
@@ -835,6 +838,13 @@ int attention_run(int dtype, const void* Q, const void* K, const void* V, void* 
         float* red = reinterpret_cast<float*>((char*)ws + kSyncBytes + round256(fd.part_words * 4));
         unsigned* done = reinterpret_cast<unsigned*>((char*)ws + kSyncDoneOff);
         unsigned* xctr = reinterpret_cast<unsigned*>((char*)ws + kSyncXcdOff);
+        if (std::getenv("ATN_FUSED_PRESET_STATUS") != nullptr) {
+            // testing: the status word set as a timed-out call leaves it, so
+            // that every workgroup takes the fail-closed exit (no wait is
+            // entered)
+            static const int kSet = 1;
+            ATN_HIP(hipMemcpyAsync(status, &kSet, sizeof(int), hipMemcpyHostToDevice, stream));
+        }
         ATN_HIP(atn::launch_fused_small(dtype, plan.pek, Q, K, V, out, part, red, epochs, done,
                                         status, xctr, (int)s.BH, Lq, Lk, D, fd.MB, fd.dc,
                                         fd.nchunk, fd.gather1, fd.xcd, scale, plan.q, plan.k,
@@ -859,7 +869,8 @@ int attention_run(int dtype, const void* Q, const void* K, const void* V, void* 
 // of heads or query rows that fit it.
 int attention_core(int dtype, const void* Q, const void* K, const void* V, void* out, int B,
                    int H, int Lq, int Lk, int D, const atn_pe_desc* pe, void* workspace,
-                   size_t workspace_bytes, hipStream_t stream, bool no_alloc = false) {
+                   size_t workspace_bytes, hipStream_t stream, bool no_alloc = false,
+                   bool no_fused = false) {
     if (dtype != ATN_DTYPE_F32 && dtype != ATN_DTYPE_BF16) return ATN_ERR_BAD_ARGUMENT;
     if (!Q || !K || !V || !out) return ATN_ERR_NULL_POINTER;
     Shape s;
@@ -874,6 +885,7 @@ int attention_core(int dtype, const void* Q, const void* K, const void* V, void*
     PePlan plan;
     st = check_pe(pe, D, &plan);
     if (st != ATN_OK) return st;
+    plan.no_fused = no_fused;
     // every path needs at least the sync region; the path-specific size is
     // checked once the device has chosen the path
     if (workspace != nullptr && workspace_bytes < kSyncBytes) return ATN_ERR_WORKSPACE;
@@ -1019,8 +1031,9 @@ int workspace_status(void* ws, hipStream_t stream) {
 // library workspace, the allocation-free scratch) are copied into pinned
 // host words behind the call, so the one device synchronization covers the
 // call and its status check.  A set word runs the recovery of
-// workspace_status() and ends the process like any other failure.
-void sync_or_die(int status, const char* where) {
+// workspace_status() and returns ATN_ERR_DEVICE_TIMEOUT; any other failure
+// ends the process (the reference's CUDA_CHECK, final/attention.cu:12-21).
+int finish_sync(int status, const char* where) {
     if (status != ATN_OK) die(status, where);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
@@ -1069,8 +1082,30 @@ void sync_or_die(int status, const char* where) {
         copied && (lib_ws == nullptr || host[0] == 0) && (sc == nullptr || host[1] == 0);
     if (!clean) {
         const int ws = workspace_status(nullptr, nullptr);
-        if (ws != ATN_OK) die(ws, where);
+        if (ws != ATN_OK && ws != ATN_ERR_DEVICE_TIMEOUT) die(ws, where);
+        return ws;
     }
+    return ATN_OK;
+}
+
+void sync_or_die(int status, const char* where) {
+    const int st = finish_sync(status, where);
+    if (st != ATN_OK) die(st, where);
+}
+
+// A synchronous attention call (the drop-ins).  When the single-launch
+// kernel's exchange timed out -- its waits need the whole grid resident, and
+// work elsewhere on the device held CUs the grid needed -- the workspace has
+// been recovered and the call runs once more without that kernel, on kernels
+// that wait on no other workgroup; a second failure ends the process.
+void dropin_attention(const char* where, int dtype, const void* Q, const void* K, const void* V,
+                      void* out, int B, int H, int Lq, int Lk, int D, const atn_pe_desc* pe) {
+    if (finish_sync(attention_core(dtype, Q, K, V, out, B, H, Lq, Lk, D, pe, nullptr, 0, nullptr),
+                    where) == ATN_OK)
+        return;
+    sync_or_die(attention_core(dtype, Q, K, V, out, B, H, Lq, Lk, D, pe, nullptr, 0, nullptr,
+                               false, true),
+                where);
 }
 
 atn_pe_desc rope_desc(int rotary, int pairing, bool q, bool k, const float* c, const float* s) {
@@ -1215,16 +1250,14 @@ int atn_prepare_pe_ex(const atn_pe_desc* pe, int head_d, int max_positions) {
 // ---- drop-ins ----
 void attention_forward_optimized(const float* Q, const float* K, const float* V, float* out,
                                  int batch_sz, int num_heads, int len_q, int len_k, int head_d) {
-    sync_or_die(attention_core(ATN_DTYPE_F32, Q, K, V, out, batch_sz, num_heads, len_q, len_k,
-                               head_d, nullptr, nullptr, 0, nullptr),
-                "attention_forward_optimized");
+    dropin_attention("attention_forward_optimized", ATN_DTYPE_F32, Q, K, V, out,
+                     batch_sz, num_heads, len_q, len_k, head_d, nullptr);
 }
 
 void attention_forward(const float* Q, const float* K, const float* V, float* out, int batch_sz,
                        int num_heads, int len_q, int len_k, int head_d) {
-    sync_or_die(attention_core(ATN_DTYPE_F32, Q, K, V, out, batch_sz, num_heads, len_q, len_k,
-                               head_d, nullptr, nullptr, 0, nullptr),
-                "attention_forward");
+    dropin_attention("attention_forward", ATN_DTYPE_F32, Q, K, V, out,
+                     batch_sz, num_heads, len_q, len_k, head_d, nullptr);
 }
 
 void attention_forward_rope_fused(const float* Q, const float* K, const float* V, float* out,
@@ -1232,9 +1265,8 @@ void attention_forward_rope_fused(const float* Q, const float* K, const float* V
                                   int num_heads, int len_q, int len_k, int head_d) {
     if (!cos_cache || !sin_cache) die(ATN_ERR_NULL_POINTER, "attention_forward_rope_fused");
     const atn_pe_desc d = rope_desc(head_d, ATN_ROPE_INTERLEAVED, true, true, cos_cache, sin_cache);
-    sync_or_die(attention_core(ATN_DTYPE_F32, Q, K, V, out, batch_sz, num_heads, len_q, len_k,
-                               head_d, &d, nullptr, 0, nullptr),
-                "attention_forward_rope_fused");
+    dropin_attention("attention_forward_rope_fused", ATN_DTYPE_F32, Q, K, V, out,
+                     batch_sz, num_heads, len_q, len_k, head_d, &d);
 }
 
 void attention_forward_rope_fused_v7_hybrid(const float* Q, const float* K_rotated,
@@ -1243,9 +1275,8 @@ void attention_forward_rope_fused_v7_hybrid(const float* Q, const float* K_rotat
                                             int rotary_dim) {
     const atn_pe_desc d = rope_desc(rotary_dim, ATN_ROPE_INTERLEAVED, true, false, nullptr, nullptr);
     if (rotary_dim == 0) die(ATN_ERR_BAD_ROTARY, "attention_forward_rope_fused_v7_hybrid");
-    sync_or_die(attention_core(ATN_DTYPE_F32, Q, K_rotated, V, out, batch_sz, num_heads, len_q,
-                               len_k, head_d, &d, nullptr, 0, nullptr),
-                "attention_forward_rope_fused_v7_hybrid");
+    dropin_attention("attention_forward_rope_fused_v7_hybrid", ATN_DTYPE_F32, Q, K_rotated, V, out,
+                     batch_sz, num_heads, len_q, len_k, head_d, &d);
 }
 
 void attention_forward_separate_rope(const float* Q, const float* K, const float* V,
@@ -1264,9 +1295,8 @@ void attention_forward_separate_rope(const float* Q, const float* K, const float
     if (st != ATN_OK) die(st, w);
     st = pe_apply_core(ATN_DTYPE_F32, K, K_rope, (long)(s.BH * len_k), len_k, head_d, &d, nullptr);
     if (st != ATN_OK) die(st, w);
-    sync_or_die(attention_core(ATN_DTYPE_F32, Q_rope, K_rope, V, out, batch_sz, num_heads, len_q,
-                               len_k, head_d, nullptr, nullptr, 0, nullptr),
-                w);
+    dropin_attention(w, ATN_DTYPE_F32, Q_rope, K_rope, V, out,
+                     batch_sz, num_heads, len_q, len_k, head_d, nullptr);
 }
 
 void rope_forward(const float* input, float* output, const float* cos_cache,
@@ -1294,9 +1324,8 @@ void attention_forward_sinusoidal_fused(const float* Q, const float* K, const fl
                                         float* out, int batch_sz, int num_heads, int len_q,
                                         int len_k, int head_d) {
     const atn_pe_desc d = sin_desc(true, true, nullptr, nullptr);
-    sync_or_die(attention_core(ATN_DTYPE_F32, Q, K, V, out, batch_sz, num_heads, len_q, len_k,
-                               head_d, &d, nullptr, 0, nullptr),
-                "attention_forward_sinusoidal_fused");
+    dropin_attention("attention_forward_sinusoidal_fused", ATN_DTYPE_F32, Q, K, V, out,
+                     batch_sz, num_heads, len_q, len_k, head_d, &d);
 }
 
 void attention_forward_sinusoidal_hybrid(const float* Q, const float* K, const float* V,
@@ -1312,9 +1341,8 @@ void attention_forward_sinusoidal_hybrid(const float* Q, const float* K, const f
     st = pe_apply_core(ATN_DTYPE_F32, K, K_emb, (long)(s.BH * len_k), len_k, head_d, &dk, nullptr);
     if (st != ATN_OK) die(st, w);
     const atn_pe_desc dq = sin_desc(true, false, sin_table, cos_table);
-    sync_or_die(attention_core(ATN_DTYPE_F32, Q, K_emb, V, out, batch_sz, num_heads, len_q, len_k,
-                               head_d, &dq, nullptr, 0, nullptr),
-                w);
+    dropin_attention(w, ATN_DTYPE_F32, Q, K_emb, V, out,
+                     batch_sz, num_heads, len_q, len_k, head_d, &dq);
 }
 
 void attention_forward_sinusoidal_separate(const float* Q, const float* K, const float* V,
@@ -1331,16 +1359,14 @@ void attention_forward_sinusoidal_separate(const float* Q, const float* K, const
     if (st != ATN_OK) die(st, w);
     st = pe_apply_core(ATN_DTYPE_F32, K, K_emb, (long)(s.BH * len_k), len_k, head_d, &d, nullptr);
     if (st != ATN_OK) die(st, w);
-    sync_or_die(attention_core(ATN_DTYPE_F32, Q_emb, K_emb, V, out, batch_sz, num_heads, len_q,
-                               len_k, head_d, nullptr, nullptr, 0, nullptr),
-                w);
+    dropin_attention(w, ATN_DTYPE_F32, Q_emb, K_emb, V, out,
+                     batch_sz, num_heads, len_q, len_k, head_d, nullptr);
 }
 
 void attention_forward_bf16(const atn_bf16* Q, const atn_bf16* K, const atn_bf16* V,
                             atn_bf16* out, int bs, int nh, int len_q, int len_k, int head_d) {
-    sync_or_die(attention_core(ATN_DTYPE_BF16, Q, K, V, out, bs, nh, len_q, len_k, head_d,
-                               nullptr, nullptr, 0, nullptr),
-                "attention_forward_bf16");
+    dropin_attention("attention_forward_bf16", ATN_DTYPE_BF16, Q, K, V, out,
+                     bs, nh, len_q, len_k, head_d, nullptr);
 }
 
 void attention_forward_rope_bf16(const atn_bf16* Q, const atn_bf16* K_rotated,
@@ -1348,27 +1374,24 @@ void attention_forward_rope_bf16(const atn_bf16* Q, const atn_bf16* K_rotated,
                                  int len_k, int head_d, int rotary_dim) {
     if (rotary_dim == 0) die(ATN_ERR_BAD_ROTARY, "attention_forward_rope_bf16");
     const atn_pe_desc d = rope_desc(rotary_dim, ATN_ROPE_INTERLEAVED, true, false, nullptr, nullptr);
-    sync_or_die(attention_core(ATN_DTYPE_BF16, Q, K_rotated, V, out, bs, nh, len_q, len_k, head_d,
-                               &d, nullptr, 0, nullptr),
-                "attention_forward_rope_bf16");
+    dropin_attention("attention_forward_rope_bf16", ATN_DTYPE_BF16, Q, K_rotated, V, out,
+                     bs, nh, len_q, len_k, head_d, &d);
 }
 
 void attention_forward_rope_fused_bf16(const atn_bf16* Q, const atn_bf16* K, const atn_bf16* V,
                                        atn_bf16* out, int bs, int nh, int len_q, int len_k,
                                        int head_d) {
     const atn_pe_desc d = rope_desc(head_d, ATN_ROPE_INTERLEAVED, true, true, nullptr, nullptr);
-    sync_or_die(attention_core(ATN_DTYPE_BF16, Q, K, V, out, bs, nh, len_q, len_k, head_d, &d,
-                               nullptr, 0, nullptr),
-                "attention_forward_rope_fused_bf16");
+    dropin_attention("attention_forward_rope_fused_bf16", ATN_DTYPE_BF16, Q, K, V, out,
+                     bs, nh, len_q, len_k, head_d, &d);
 }
 
 void attention_forward_sinusoidal_bf16(const atn_bf16* Q, const atn_bf16* K, const atn_bf16* V,
                                        atn_bf16* out, int bs, int nh, int len_q, int len_k,
                                        int head_d) {
     const atn_pe_desc d = sin_desc(true, true, nullptr, nullptr);
-    sync_or_die(attention_core(ATN_DTYPE_BF16, Q, K, V, out, bs, nh, len_q, len_k, head_d, &d,
-                               nullptr, 0, nullptr),
-                "attention_forward_sinusoidal_bf16");
+    dropin_attention("attention_forward_sinusoidal_bf16", ATN_DTYPE_BF16, Q, K, V, out,
+                     bs, nh, len_q, len_k, head_d, &d);
 }
 
 void precompute_rope_cache(float* cos_cache, float* sin_cache, int max_seq_len, int rotary_dim,

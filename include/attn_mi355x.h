@@ -11,7 +11,10 @@
  *     cudaDeviceSynchronize, final/attention.cu:219-220) and, on any error,
  *     prints "attn_mi355x error <code> (<text>) at <entry point>" to stderr
  *     and calls exit(EXIT_FAILURE) like the reference's CUDA_CHECK
- *     (final/attention.cu:12-21).
+ *     (final/attention.cu:12-21) -- except for a timed-out wait of the
+ *     single-launch kernel (ATN_ERR_DEVICE_TIMEOUT: other work held CUs its
+ *     grid needed), after which an attention call runs once more on kernels
+ *     that wait on no other workgroup and exits only if that fails too.
  * The atn_*_ex entry points are the asynchronous, non-exiting forms: they
  * validate every argument before any HIP call, return an ATN_* status and
  * enqueue on the given stream (a hipStream_t passed as void*; NULL = the

@@ -473,3 +473,40 @@ def test_fail_closed_then_recovers(am, dev, monkeypatch, xcd, exchange):
         n, mabs, mrel = H.check_f32(out.numpy(), ref)
         assert n == 0, f"after recovery: {n} mismatches, max abs {mabs}"
     assert am.sync_status(ws, B, Hh) == 0
+
+
+@pytest.mark.parametrize("dtype,shape", [("f32", (1, 4, 64, 64, 2048)), ("bf16", (1, 4, 32, 128, 8192))],
+                         ids=["cfg2-f32", "cfg3-bf16"])
+def test_dropin_reruns_after_a_failed_exchange(am, dev, monkeypatch, dtype, shape):
+    """A synchronous drop-in whose single-launch call fails closed -- forced
+    from the host: ATN_FUSED_PRESET_STATUS presets the call's status word as
+    a timed-out call leaves it, so every workgroup takes the fail-closed exit
+    and no wait is entered -- recovers the workspace and runs the call once
+    more without the single-launch kernel: the process goes on and the
+    output is the oracle's.  Without the switch the next drop-in takes the
+    single-launch kernel again."""
+    import hip_rt
+    B, Hh, Lq, Lk, D = shape
+    print(f"[case] drop-in rerun {dtype} {shape}", flush=True)
+    assert am.path(0 if dtype == "f32" else 1, B, Hh, Lq, Lk, D) == am.ATN_PATH_FUSED_SMALL
+    (q, k, v), (Q, K, V) = H.device_inputs((B, Hh, Lq, D), (B, Hh, Lk, D), 909, dtype)
+    ref = oracle.attention(Q, K, V, nthreads=16)
+    fn = am.attention_forward_optimized if dtype == "f32" else am.attention_forward_bf16
+    check = H.check_f32 if dtype == "f32" else H.check_bf16
+
+    def call():
+        out = H.empty((B, Hh, Lq, D), dtype)
+        fn(q, k, v, out)
+        hip_rt.synchronize()
+        n, a, b = check(out.numpy(), ref)
+        assert n == 0, (n, a, b)
+        return out.numpy()
+
+    monkeypatch.setenv("ATN_FUSED_PRESET_STATUS", "1")
+    rerun = call()
+    monkeypatch.delenv("ATN_FUSED_PRESET_STATUS")
+    again = call()
+    assert am.sync_status(None, B, Hh) == 0
+    if dtype == "f32":  # the single-launch kernel and the split-D pipeline agree to the bar only
+        n, mabs, _ = H.check_f32(rerun, again)
+        assert n == 0, mabs
