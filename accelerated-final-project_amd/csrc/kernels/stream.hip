@@ -18,7 +18,8 @@
 //
 // All math is fp32; bf16 storage is widened at load and rounded (RNE) once
 // at the final store.  Workgroups are 256 threads (4 waves) computing 64x64
-// tiles with 4x4 register blocks from LDS-staged 16-deep slices.
+// tiles, a 32x32 quadrant per wave on fp32 MFMA, from LDS-staged 16-deep
+// slices.
 #include "common.hpp"
 #include "launch.hpp"
 
@@ -29,6 +30,31 @@ namespace {
 constexpr int kTile = 64;   // rows x cols of an output tile
 constexpr int kDepth = 16;  // contraction slice staged in LDS per step
 constexpr int kPad = 4;     // LDS row padding (floats), keeps float4 alignment
+
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+// One 16-deep slice of a 64 x 64 tile on fp32 MFMA: wave w owns the 32 x 32
+// quadrant (wm, wn) = (32 (w / 2), 32 (w % 2)); As[k][row] and Bs[k][col]
+// hold the slice k-major.  v_mfma_f32_32x32x2f32 takes A[row][k] from lane
+// row + 32 k and B[k][col] from lane col + 32 k, one float each (fp32
+// products, fp32 accumulation, twice the VALU fp32 rate).
+__device__ __forceinline__ void mfma_slice(const float (*As)[kTile + kPad],
+                                           const float (*Bs)[kTile + kPad], int wm, int wn,
+                                           int lane, v16f& acc) {
+    const int lr = lane & 31, lh = lane >> 5;
+#pragma unroll
+    for (int k2 = 0; k2 < kDepth / 2; ++k2) {
+        const float a = As[2 * k2 + lh][wm + lr];
+        const float b = Bs[2 * k2 + lh][wn + lr];
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, acc, 0, 0, 0);
+    }
+}
+
+// Row of the tile held in accumulator register r of the lane (its column is
+// wn + lane % 32).
+__device__ __forceinline__ int mfma_row(int wm, int lane, int r) {
+    return wm + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+}
 
 template <typename T, int PEK>
 __global__ __launch_bounds__(256) void k_qk_partial(const T* __restrict__ Q,
@@ -55,18 +81,17 @@ __global__ __launch_bounds__(256) void k_qk_partial(const T* __restrict__ Q,
 
     const int lrow = tid >> 2;       // loader: row within tile
     const int lcol = (tid & 3) * 4;  // loader: first of 4 depth slots
-    const int ty = tid >> 4, tx = tid & 15;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int wm = (wave >> 1) * 32, wn = (wave & 1) * 32;
 
     const int qi = q0 + lrow, kj = k0 + lrow;
     const T* qrow = Q + ((size_t)bh * Lq + (qi < Lq ? qi : 0)) * D;
     const T* krow = K + ((size_t)bh * Lk + (kj < Lk ? kj : 0)) * D;
     const bool vec = vec_ok != 0;
 
-    float acc[4][4];
+    v16f acc;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = 0.f;
+    for (int r = 0; r < 16; ++r) acc[r] = 0.f;
 
     for (int d0 = dbeg; d0 < dend; d0 += kDepth) {
         float4 qv = make_float4(0.f, 0.f, 0.f, 0.f), kv = qv;
@@ -78,29 +103,15 @@ __global__ __launch_bounds__(256) void k_qk_partial(const T* __restrict__ Q,
         Ks[lcol + 0][lrow] = kv.x; Ks[lcol + 1][lrow] = kv.y;
         Ks[lcol + 2][lrow] = kv.z; Ks[lcol + 3][lrow] = kv.w;
         __syncthreads();
-#pragma unroll
-        for (int dd = 0; dd < kDepth; ++dd) {
-            const float4 a = *reinterpret_cast<const float4*>(&Qs[dd][ty * 4]);
-            const float4 b = *reinterpret_cast<const float4*>(&Ks[dd][tx * 4]);
-            const float av[4] = {a.x, a.y, a.z, a.w};
-            const float bv[4] = {b.x, b.y, b.z, b.w};
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(av[i], bv[j], acc[i][j]);
-        }
+        mfma_slice(Qs, Ks, wm, wn, lane, acc);
     }
 
     float* Sp = S + ((size_t)split * BH + bh) * (size_t)Lq * Lk;
+    const int c = k0 + wn + (lane & 31);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int r = q0 + ty * 4 + i;
-        if (r >= Lq) continue;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int c = k0 + tx * 4 + j;
-            if (c < Lk) Sp[(size_t)r * Lk + c] = acc[i][j];
-        }
+    for (int r = 0; r < 16; ++r) {
+        const int row = q0 + mfma_row(wm, lane, r);
+        if (row < Lq && c < Lk) Sp[(size_t)row * Lk + c] = acc[r];
     }
 }
 
@@ -159,7 +170,8 @@ __global__ __launch_bounds__(256) void k_pv(const float* __restrict__ P, const T
     const int tq = (int)(wg % tiles_q);
     const int bh = (int)(wg / tiles_q);
     const int q0 = tq * kTile, d0 = td * kTile;
-    const int ty = tid >> 4, tx = tid & 15;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int wm = (wave >> 1) * 32, wn = (wave & 1) * 32;
 
     // P loader: 64 rows x 16 keys, 4 keys per thread
     const int prow = tid >> 2, pk = (tid & 3) * 4;
@@ -171,11 +183,9 @@ __global__ __launch_bounds__(256) void k_pv(const float* __restrict__ P, const T
     const float* prow_ptr = P + ((size_t)bh * Lq + (q0 + prow < Lq ? q0 + prow : 0)) * Lk;
     const T* Vh = V + (size_t)bh * Lk * D;
 
-    float acc[4][4];
+    v16f acc;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = 0.f;
+    for (int r = 0; r < 16; ++r) acc[r] = 0.f;
 
     for (int k0 = 0; k0 < Lk; k0 += kDepth) {
         float pv[4] = {0.f, 0.f, 0.f, 0.f};
@@ -209,32 +219,14 @@ __global__ __launch_bounds__(256) void k_pv(const float* __restrict__ P, const T
         for (int c = 0; c < 4; ++c) Ps[pk + c][prow] = pv[c];
         *reinterpret_cast<float4*>(&Vs[vkey][vd]) = make_float4(vv[0], vv[1], vv[2], vv[3]);
         __syncthreads();
-#pragma unroll
-        for (int kk = 0; kk < kDepth; ++kk) {
-            const float4 a = *reinterpret_cast<const float4*>(&Ps[kk][ty * 4]);
-            const float4 b = *reinterpret_cast<const float4*>(&Vs[kk][tx * 4]);
-            const float av[4] = {a.x, a.y, a.z, a.w};
-            const float bv[4] = {b.x, b.y, b.z, b.w};
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(av[i], bv[j], acc[i][j]);
-        }
+        mfma_slice(Ps, Vs, wm, wn, lane, acc);
     }
 
+    const int dd = d0 + wn + (lane & 31);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int r = q0 + ty * 4 + i;
-        if (r >= Lq) continue;
-        T* orow = O + ((size_t)bh * Lq + r) * D;
-        const int dd = d0 + tx * 4;
-        if (vec && dd + 3 < D) {
-            Elem<T>::st4(orow, dd, make_float4(acc[i][0], acc[i][1], acc[i][2], acc[i][3]));
-        } else {
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-                if (dd + j < D) Elem<T>::st(orow, dd + j, acc[i][j]);
-        }
+    for (int r = 0; r < 16; ++r) {
+        const int row = q0 + mfma_row(wm, lane, r);
+        if (row < Lq && dd < D) Elem<T>::st(O + ((size_t)bh * Lq + row) * D, dd, acc[r]);
     }
 }
 
