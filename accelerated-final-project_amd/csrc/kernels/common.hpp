@@ -188,7 +188,9 @@ __device__ __forceinline__ float4 load_row4_pe(const T* __restrict__ xr, int pos
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
                 const int e = d + c;
-                if (e < pe.rotary) {
+                // (past dend the element stays 0: its partner is loaded from
+                // the row itself, which would make it nonzero)
+                if (e < pe.rotary && e < dend) {
                     const bool lo = e < h;
                     const int f = lo ? e : e - h;
                     const float xp = Elem<T>::ld(xr, lo ? e + h : e - h);

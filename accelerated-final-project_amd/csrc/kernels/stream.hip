@@ -18,7 +18,7 @@
 //
 // All math is fp32; bf16 storage is widened at load and rounded (RNE) once
 // at the final store.  Workgroups are 256 threads (4 waves) computing 64x64
-// tiles, a 32x32 quadrant per wave on fp32 MFMA, from LDS-staged 16-deep
+// tiles, a 32x32 quadrant per wave on fp32 MFMA, from LDS-staged 32-deep
 // slices.
 #include "common.hpp"
 #include "launch.hpp"
@@ -28,12 +28,12 @@ namespace atn {
 namespace {
 
 constexpr int kTile = 64;   // rows x cols of an output tile
-constexpr int kDepth = 16;  // contraction slice staged in LDS per step
+constexpr int kDepth = 32;  // contraction slice staged in LDS per step (two 16-deep halves per loader)
 constexpr int kPad = 4;     // LDS row padding (floats), keeps float4 alignment
 
 typedef float v16f __attribute__((ext_vector_type(16)));
 
-// One 16-deep slice of a 64 x 64 tile on fp32 MFMA: wave w owns the 32 x 32
+// One kDepth-deep slice of a 64 x 64 tile on fp32 MFMA: wave w owns the 32 x 32
 // quadrant (wm, wn) = (32 (w / 2), 32 (w % 2)); As[k][row] and Bs[k][col]
 // hold the slice k-major.  v_mfma_f32_32x32x2f32 takes A[row][k] from lane
 // row + 32 k and B[k][col] from lane col + 32 k, one float each (fp32
@@ -94,14 +94,24 @@ __global__ __launch_bounds__(256) void k_qk_partial(const T* __restrict__ Q,
     for (int r = 0; r < 16; ++r) acc[r] = 0.f;
 
     for (int d0 = dbeg; d0 < dend; d0 += kDepth) {
-        float4 qv = make_float4(0.f, 0.f, 0.f, 0.f), kv = qv;
-        if (qi < Lq) qv = load_row4_pe<T, PEK>(qrow, qi, d0 + lcol, dend, pq, vec);
-        if (kj < Lk) kv = load_row4_pe<T, PEK>(krow, kj, d0 + lcol, dend, pk, vec);
+        float4 qv[2], kv[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            qv[h] = make_float4(0.f, 0.f, 0.f, 0.f);
+            kv[h] = qv[h];
+            const int d = d0 + 16 * h + lcol;
+            if (qi < Lq) qv[h] = load_row4_pe<T, PEK>(qrow, qi, d, dend, pq, vec);
+            if (kj < Lk) kv[h] = load_row4_pe<T, PEK>(krow, kj, d, dend, pk, vec);
+        }
         __syncthreads();
-        Qs[lcol + 0][lrow] = qv.x; Qs[lcol + 1][lrow] = qv.y;
-        Qs[lcol + 2][lrow] = qv.z; Qs[lcol + 3][lrow] = qv.w;
-        Ks[lcol + 0][lrow] = kv.x; Ks[lcol + 1][lrow] = kv.y;
-        Ks[lcol + 2][lrow] = kv.z; Ks[lcol + 3][lrow] = kv.w;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int r = 16 * h + lcol;
+            Qs[r + 0][lrow] = qv[h].x; Qs[r + 1][lrow] = qv[h].y;
+            Qs[r + 2][lrow] = qv[h].z; Qs[r + 3][lrow] = qv[h].w;
+            Ks[r + 0][lrow] = kv[h].x; Ks[r + 1][lrow] = kv[h].y;
+            Ks[r + 2][lrow] = kv[h].z; Ks[r + 3][lrow] = kv[h].w;
+        }
         __syncthreads();
         mfma_slice(Qs, Ks, wm, wn, lane, acc);
     }
@@ -188,36 +198,44 @@ __global__ __launch_bounds__(256) void k_pv(const float* __restrict__ P, const T
     for (int r = 0; r < 16; ++r) acc[r] = 0.f;
 
     for (int k0 = 0; k0 < Lk; k0 += kDepth) {
-        float pv[4] = {0.f, 0.f, 0.f, 0.f};
-        if (q0 + prow < Lq) {
-            const int kk = k0 + pk;
-            if (p_vec && kk + 3 < Lk) {
-                const float4 t = *reinterpret_cast<const float4*>(prow_ptr + kk);
-                pv[0] = t.x; pv[1] = t.y; pv[2] = t.z; pv[3] = t.w;
-            } else {
+        float pv[2][4], vv[2][4];
 #pragma unroll
-                for (int c = 0; c < 4; ++c)
-                    if (kk + c < Lk) pv[c] = prow_ptr[kk + c];
+        for (int h = 0; h < 2; ++h) {
+#pragma unroll
+            for (int c = 0; c < 4; ++c) pv[h][c] = vv[h][c] = 0.f;
+            if (q0 + prow < Lq) {
+                const int kk = k0 + 16 * h + pk;
+                if (p_vec && kk + 3 < Lk) {
+                    const float4 t = *reinterpret_cast<const float4*>(prow_ptr + kk);
+                    pv[h][0] = t.x; pv[h][1] = t.y; pv[h][2] = t.z; pv[h][3] = t.w;
+                } else {
+#pragma unroll
+                    for (int c = 0; c < 4; ++c)
+                        if (kk + c < Lk) pv[h][c] = prow_ptr[kk + c];
+                }
             }
-        }
-        float vv[4] = {0.f, 0.f, 0.f, 0.f};
-        const int key = k0 + vkey;
-        if (key < Lk) {
-            const T* vr = Vh + (size_t)key * D;
-            const int dd = d0 + vd;
-            if (vec && dd + 3 < D) {
-                const float4 t = Elem<T>::ld4(vr, dd);
-                vv[0] = t.x; vv[1] = t.y; vv[2] = t.z; vv[3] = t.w;
-            } else {
+            const int key = k0 + 16 * h + vkey;
+            if (key < Lk) {
+                const T* vr = Vh + (size_t)key * D;
+                const int dd = d0 + vd;
+                if (vec && dd + 3 < D) {
+                    const float4 t = Elem<T>::ld4(vr, dd);
+                    vv[h][0] = t.x; vv[h][1] = t.y; vv[h][2] = t.z; vv[h][3] = t.w;
+                } else {
 #pragma unroll
-                for (int c = 0; c < 4; ++c)
-                    if (dd + c < D) vv[c] = Elem<T>::ld(vr, dd + c);
+                    for (int c = 0; c < 4; ++c)
+                        if (dd + c < D) vv[h][c] = Elem<T>::ld(vr, dd + c);
+                }
             }
         }
         __syncthreads();
 #pragma unroll
-        for (int c = 0; c < 4; ++c) Ps[pk + c][prow] = pv[c];
-        *reinterpret_cast<float4*>(&Vs[vkey][vd]) = make_float4(vv[0], vv[1], vv[2], vv[3]);
+        for (int h = 0; h < 2; ++h) {
+#pragma unroll
+            for (int c = 0; c < 4; ++c) Ps[16 * h + pk + c][prow] = pv[h][c];
+            *reinterpret_cast<float4*>(&Vs[16 * h + vkey][vd]) =
+                make_float4(vv[h][0], vv[h][1], vv[h][2], vv[h][3]);
+        }
         __syncthreads();
         mfma_slice(Ps, Vs, wm, wn, lane, acc);
     }
