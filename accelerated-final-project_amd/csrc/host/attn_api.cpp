@@ -343,14 +343,17 @@ struct StreamPlan {
 StreamPlan stream_plan(const Shape& s) {
     StreamPlan p{};
     const int64_t tiles = s.BH * ((s.Lq + 63) / 64) * ((s.Lk + 63) / 64);
+    // D-chunks until about 1024 workgroups run (four per CU, so that one
+    // workgroup's slice loads overlap another's MFMAs), chunks of at least 64
+    // dims, rounded to the kernels' 32-deep slices
     int nsplit = 1;
-    if (tiles < 256) {
-        const int64_t want = (512 + tiles - 1) / tiles;
+    if (tiles < 1024) {
+        const int64_t want = (1024 + tiles - 1) / tiles;
         const int64_t maxs = s.D / 64 > 1 ? s.D / 64 : 1;
         nsplit = (int)(want < maxs ? want : maxs);
     }
     int dchunk = (s.D + nsplit - 1) / nsplit;
-    dchunk = (dchunk + 15) / 16 * 16;
+    dchunk = (dchunk + 31) / 32 * 32;
     nsplit = (s.D + dchunk - 1) / dchunk;
     p.nsplit = nsplit;
     p.dchunk = dchunk;
