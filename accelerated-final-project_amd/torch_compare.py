@@ -48,6 +48,10 @@ SHAPES = [
     ("cfg3", "bf16", 1, 4, 32, 128, 8192, "none"),
     ("cfg4 rope-half", "bf16", 8, 8, 1024, 1024, 4096, "rope_half"),
     ("cfg5 sinusoidal", "bf16", 4, 16, 256, 2048, 1024, "sinusoidal"),
+    # fp32 beyond the single-launch window (split-D pipeline): the reference's
+    # own long-sequence test shape (final/attention.cu:522) and a large-head one
+    ("ref llama (4,32,512,128)", "f32", 4, 32, 512, 512, 128, "none"),
+    ("f32 long (1,4,512,512,2048)", "f32", 1, 4, 512, 512, 2048, "none"),
 ]
 
 
