@@ -28,7 +28,7 @@ namespace atn {
 namespace {
 
 constexpr int kTile = 64;   // rows x cols of an output tile
-constexpr int kDepth = 32;  // contraction slice staged in LDS per step (two 16-deep halves per loader)
+constexpr int kDepth = 32;  // contraction slice staged in LDS per step (loaded in two halves)
 constexpr int kPad = 4;     // LDS row padding (floats), keeps float4 alignment
 
 typedef float v16f __attribute__((ext_vector_type(16)));
