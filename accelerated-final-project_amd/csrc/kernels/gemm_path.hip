@@ -332,23 +332,12 @@ __device__ __forceinline__ void nt_exp_epilogue(const GemmArgs& g, v16f (&acc)[T
             }
             rl[i][r] = half_sum(l);
         }
-    if (lc == 0)
-#pragma unroll
-        for (int i = 0; i < TI; ++i)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) red[(2 + cw) * kBM + rloc(i, r)] = rl[i][r];
-    __syncthreads();
-    // statistics, one row per thread: m_t = (max u) f, l_t
-    if (tid < kBM && m0 + tid < g.M) {
-        const float mu = fmaxf(red[tid], red[kBM + tid]);
-        const long si = ((long)bh * g.M + m0 + tid) * g.tiles_n + tn;
-        g.st_m[si] = mu * (g.scale * rsl[tid]);
-        g.st_l[si] = red[2 * kBM + tid] + red[3 * kBM + tid];
-    }
     uint16_t* C = static_cast<uint16_t*>(g.C) + bh * g.sc;
     if (interior) {
-        // buffer stores: the lane's (i, j) offset in a register, the row
-        // offset of r in a scalar register
+        // E of an interior tile, stored before the row sums' exchange and
+        // the statistics (the stores drain meanwhile): buffer stores, the
+        // lane's (i, j) offset in a register, the row offset of r in a
+        // scalar register
         const __amdgpu_buffer_rsrc_t rc = gemm_rsrc(C, (long)g.M * g.ldc);
         const uint32_t ldc = (uint32_t)g.ldc;
 #pragma unroll
@@ -365,8 +354,21 @@ __device__ __forceinline__ void nt_exp_epilogue(const GemmArgs& g, v16f (&acc)[T
                         (int)__builtin_amdgcn_readfirstlane(so), 0);
                 }
             }
-        return;
     }
+    if (lc == 0)
+#pragma unroll
+        for (int i = 0; i < TI; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) red[(2 + cw) * kBM + rloc(i, r)] = rl[i][r];
+    __syncthreads();
+    // statistics, one row per thread: m_t = (max u) f, l_t
+    if (tid < kBM && m0 + tid < g.M) {
+        const float mu = fmaxf(red[tid], red[kBM + tid]);
+        const long si = ((long)bh * g.M + m0 + tid) * g.tiles_n + tn;
+        g.st_m[si] = mu * (g.scale * rsl[tid]);
+        g.st_l[si] = red[2 * kBM + tid] + red[3 * kBM + tid];
+    }
+    if (interior) return;
     // edge tile: columns past N (E = exp(-inf) = 0) are written too up to
     // the row stride ldc, so the padding of an E row (ldc = N rounded up to
     // 8 keys) holds zeros for the PV GEMM's 8-key chunks
