@@ -888,7 +888,10 @@ int attention_core(int dtype, const void* Q, const void* K, const void* V, void*
     PePlan plan;
     st = check_pe(pe, D, &plan);
     if (st != ATN_OK) return st;
-    plan.no_fused = no_fused;
+    // ATN_F32_FULL: fp32 calls in full fp32 products (the split-D pipeline)
+    // instead of the single-launch kernel's hi + lo bf16 parts, for logits
+    // beyond that kernel's accuracy range; slower
+    plan.no_fused = no_fused || (dtype == ATN_DTYPE_F32 && std::getenv("ATN_F32_FULL") != nullptr);
     // every path needs at least the sync region; the path-specific size is
     // checked once the device has chosen the path
     if (workspace != nullptr && workspace_bytes < kSyncBytes) return ATN_ERR_WORKSPACE;
@@ -1216,7 +1219,8 @@ int atn_attention_path_ex(int dtype, int batch, int heads, int len_q, int len_k,
     if (st != ATN_OK) return st;
     int n = 0;
     const bool dev = hipGetDeviceCount(&n) == hipSuccess && n > 0;
-    if (fused_plan(dtype, plan.pek, s, dev).ok) return ATN_PATH_FUSED_SMALL;
+    const bool full = dtype == ATN_DTYPE_F32 && std::getenv("ATN_F32_FULL") != nullptr;
+    if (!full && fused_plan(dtype, plan.pek, s, dev).ok) return ATN_PATH_FUSED_SMALL;
     if (gemm_plan(dtype, s, plan).ok) return ATN_PATH_GEMM;
     return ATN_PATH_SPLIT_D;
 }

@@ -78,6 +78,26 @@ def test_sdpa_f32_wider_logits(am, dev, shape):
     assert n == 0, f"{n} mismatches, max abs {mabs}"
 
 
+@pytest.mark.parametrize("shape", [(1, 4, 64, 64, 512), (1, 4, 64, 64, 2048), (1, 4, 64, 64, 8192),
+                                   (1, 4, 32, 128, 2048)], ids=lambda s: "x".join(map(str, s)))
+def test_sdpa_f32_full_precision_switch(am, dev, monkeypatch, shape):
+    """ATN_F32_FULL=1: fp32 calls take full fp32 products (the split-D
+    pipeline) instead of the single-launch kernel's hi + lo bf16 parts, so
+    inputs of sigma 3 (logits up to about +-40, outside that kernel's
+    envelope) meet the 1e-4 bar.  An element fails only if it misses the bar
+    against the oracle and against the exact float64 result (the oracle's own
+    float32 sums drift by up to 7e-4 at D = 8192 there)."""
+    B, Hh, Lq, Lk, D = shape
+    print(f"[case] sdpa f32 full precision, sigma 3 {shape}", flush=True)
+    monkeypatch.setenv("ATN_F32_FULL", "1")
+    assert am.path(0, B, Hh, Lq, Lk, D) == am.ATN_PATH_SPLIT_D
+    Q, K, V = H.rng_inputs((B, Hh, Lq, D), (B, Hh, Lk, D), seed=7 + D, sigma=3.0)
+    got = _f32_call(am.attention_forward_optimized, Q, K, V)
+    ref = oracle.attention(Q, K, V, nthreads=16)
+    n, mabs, mtruth = H.check_f32_or_truth(got, ref, H.sdpa64(Q, K, V))
+    assert n == 0, f"{n} mismatches, max abs {mabs} (oracle), {mtruth} (exact)"
+
+
 def test_sdpa_llama_shape(am, dev):
     B, Hh, L, D = 4, 32, 512, 128  # final/attention.cu:522
     print("[case] sdpa f32 llama (4,32,512,128)", flush=True)
