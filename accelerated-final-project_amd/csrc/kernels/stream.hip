@@ -20,6 +20,8 @@
 // at the final store.  Workgroups are 256 threads (4 waves) computing 64x64
 // tiles, a 32x32 quadrant per wave on fp32 MFMA, from LDS-staged 32-deep
 // slices.
+#include <algorithm>
+
 #include "common.hpp"
 #include "launch.hpp"
 
@@ -163,6 +165,48 @@ __global__ __launch_bounds__(256) void k_softmax(const float* __restrict__ S, fl
         l = (red_sum[0] + red_sum[1]) + (red_sum[2] + red_sum[3]);
         for (int j = tid; j < Lk; j += 256) p[j] = p[j] / l;
         __syncthreads();  // red_* reused by the next row
+    }
+}
+
+// Rows of at most 64 NPL keys: one wave per row, the row in registers (lane
+// l holds keys l + 64 u), so the scores are read once and P written once;
+// four rows per workgroup.
+template <int NPL>
+__global__ __launch_bounds__(256) void k_softmax_rows(const float* __restrict__ S, float* P,
+                                                      long rows, int Lk, int nsplit,
+                                                      size_t split_stride, float scale) {
+    const int lane = threadIdx.x & 63;
+    const long wave = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+    for (long r = wave; r < rows; r += (long)gridDim.x * 4) {
+        const float* s = S + (size_t)r * Lk;
+        float* p = P + (size_t)r * Lk;
+        float v[NPL];
+        float m = -INFINITY;
+#pragma unroll
+        for (int u = 0; u < NPL; ++u) {
+            const int j = lane + 64 * u;
+            float acc = -INFINITY;
+            if (j < Lk) {
+                acc = s[j];
+                for (int sp = 1; sp < nsplit; ++sp) acc += s[(size_t)sp * split_stride + j];
+                acc *= scale;
+            }
+            v[u] = acc;
+            m = fmaxf(m, acc);
+        }
+        m = wave_max(m);
+        float l = 0.f;
+#pragma unroll
+        for (int u = 0; u < NPL; ++u) {
+            v[u] = lane + 64 * u < Lk ? expf(v[u] - m) : 0.f;
+            l += v[u];
+        }
+        l = wave_sum(l);
+#pragma unroll
+        for (int u = 0; u < NPL; ++u) {
+            const int j = lane + 64 * u;
+            if (j < Lk) p[j] = v[u] / l;
+        }
     }
 }
 
@@ -342,6 +386,25 @@ hipError_t launch_qk_partial(int dtype, int pek, const void* Q, const void* K, f
 
 hipError_t launch_softmax(const float* S, float* P, long rows, int Lk, int nsplit,
                           size_t split_stride, float scale, hipStream_t st) {
+    // a wave per row pays off where each element is one partial; summing many
+    // D-chunks' partials wants more threads per row (the kernel below)
+    if (Lk <= 64 * 32 && nsplit == 1) {
+        const long nwg = std::min<long>((rows + 3) / 4, 65536);
+        const dim3 grid((unsigned)nwg), block(256);
+        if (Lk <= 64 * 4)
+            hipLaunchKernelGGL(k_softmax_rows<4>, grid, block, 0, st, S, P, rows, Lk, nsplit,
+                               split_stride, scale);
+        else if (Lk <= 64 * 8)
+            hipLaunchKernelGGL(k_softmax_rows<8>, grid, block, 0, st, S, P, rows, Lk, nsplit,
+                               split_stride, scale);
+        else if (Lk <= 64 * 16)
+            hipLaunchKernelGGL(k_softmax_rows<16>, grid, block, 0, st, S, P, rows, Lk, nsplit,
+                               split_stride, scale);
+        else
+            hipLaunchKernelGGL(k_softmax_rows<32>, grid, block, 0, st, S, P, rows, Lk, nsplit,
+                               split_stride, scale);
+        return hipGetLastError();
+    }
     const long nwg = rows < 65536 ? rows : 65536;
     hipLaunchKernelGGL(k_softmax, dim3((unsigned)nwg), dim3(256), 0, st, S, P, rows, Lk, nsplit,
                        split_stride, scale);
