@@ -164,6 +164,25 @@ def test_sdpa_bf16(am, dev, shape):
     assert n == 0, f"normwise rel {nrel}, max abs {mabs}"
 
 
+@pytest.mark.parametrize("shape", [(1, 4, 32, 128, 8192), (2, 4, 64, 64, 512), (1, 2, 16, 100, 2048)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_sdpa_bf16_wide_logits(am, dev, shape):
+    """bf16 inputs of sigma 3 (logits to about +-40) on the single-launch
+    kernel: bf16 operands are exact MFMA inputs and P goes in as hi + lo
+    parts, so the bf16 bar holds far outside the unit-scale inputs."""
+    import hip_rt
+    B, Hh, Lq, Lk, D = shape
+    print(f"[case] sdpa bf16 sigma 3 {shape}", flush=True)
+    assert am.path(1, B, Hh, Lq, Lk, D) == am.ATN_PATH_FUSED_SMALL
+    (q, k, v), (Q, K, V) = H.device_inputs((B, Hh, Lq, D), (B, Hh, Lk, D), 13, "bf16", 3.0)
+    out = H.empty(Q.shape, "bf16")
+    am.attention_forward_bf16(q, k, v, out)
+    hip_rt.synchronize()
+    ref = oracle.attention(Q, K, V, nthreads=16)
+    n, nrel, mabs = H.check_bf16(out.numpy(), ref)
+    assert n == 0, f"normwise rel {nrel}, max abs {mabs}"
+
+
 # ---------------------------------------------------------------- RoPE
 ROPE_SHAPES = [(1, 1, 4, 8), (1, 2, 8, 16), (2, 4, 32, 32), (1, 4, 16, 64), (1, 4, 64, 128),
                (1, 4, 64, 512), (1, 4, 64, 2048)]  # final/rope.cu:1911-1923
