@@ -68,6 +68,19 @@ class PeDesc(ctypes.Structure):
     ]
 
 
+class Tuning(ctypes.Structure):
+    """atn_tuning (process-wide overrides for measurement and tests)."""
+    _fields_ = [(n, ctypes.c_int) for n in (
+        "fused_rows", "fused_dc", "fused_exchange", "fused_xcd", "no_fused", "gemm_fused_k",
+        "workspace_cap_mib", "model_cus", "model_xccs", "preset_status")]
+
+
+class FusedPlanInfo(ctypes.Structure):
+    """atn_fused_plan_info."""
+    _fields_ = [(n, ctypes.c_int) for n in (
+        "rows", "dc", "nchunk", "gather1", "xcd", "workgroups", "lds")]
+
+
 class AtnError(RuntimeError):
     def __init__(self, status: int, where: str):
         self.status = status
@@ -102,6 +115,13 @@ _SIGS = {
     "atn_prepare_pe_ex": ([ctypes.POINTER(PeDesc), _i, _i], _i),
     "atn_sync_status_ex": ([_vp, _i, _i, _vp], _i),
     "atn_attention_path_ex": ([_i] * 6 + [ctypes.POINTER(PeDesc)], _i),
+    "atn_set_tuning_ex": ([ctypes.POINTER(Tuning)], _i),
+    "atn_get_tuning_ex": ([ctypes.POINTER(Tuning)], _i),
+    "atn_fused_plan_ex": ([_i] * 6 + [ctypes.POINTER(PeDesc), ctypes.POINTER(FusedPlanInfo)],
+                          _i),
+    "atn_rerun_count": ([_i], ctypes.c_long),
+    "atn_retained_bytes_ex": ([], ctypes.c_size_t),
+    "atn_release_ex": ([], _i),
     "attention_forward_optimized": ([_vp] * 4 + [_i] * 5, None),
     "attention_forward": ([_vp] * 4 + [_i] * 5, None),
     "attention_forward_rope_fused": ([_vp] * 6 + [_i] * 5, None),
@@ -151,6 +171,76 @@ def header_functions(path: str = HEADER_PATH) -> list[str]:
 
 def device_count() -> int:
     return lib().atn_device_count()
+
+
+# ---------------------------------------------------------------- tuning
+_EXCHANGE = {None: 0, "gather": 1, "rsag": 2}
+_SCOPE = {None: 0, "xcd": 1, "device": 2}
+_FUSED_K = {None: 0, "on": 1, "off": 2}
+
+
+def set_tuning(fused_rows: int = 0, fused_dc: int = 0, fused_exchange: str | None = None,
+               fused_xcd: str | None = None, no_fused: bool = False,
+               gemm_fused_k: str | None = None, workspace_cap_mib: int = 0, model_cus: int = 0,
+               model_xccs: int = 0, preset_status: bool = False) -> None:
+    """atn_set_tuning_ex with named fields (every field not given is reset)."""
+    t = Tuning(fused_rows, fused_dc, _EXCHANGE[fused_exchange], _SCOPE[fused_xcd],
+               int(no_fused), _FUSED_K[gemm_fused_k], workspace_cap_mib, model_cus,
+               model_xccs, int(preset_status))
+    st = lib().atn_set_tuning_ex(ctypes.byref(t))
+    if st != ATN_OK:
+        raise AtnError(st, "atn_set_tuning_ex")
+
+
+def get_tuning() -> Tuning:
+    t = Tuning()
+    lib().atn_get_tuning_ex(ctypes.byref(t))
+    return t
+
+
+class tuning:
+    """Context manager: overrides for the block, the previous ones restored
+    after it (``with tuning(fused_rows=16): ...``)."""
+
+    def __init__(self, **kw):
+        self.kw = kw
+
+    def __enter__(self):
+        self.saved = get_tuning()
+        set_tuning(**self.kw)
+        return self
+
+    def __exit__(self, *exc):
+        lib().atn_set_tuning_ex(ctypes.byref(self.saved))
+        return False
+
+
+def fused_plan(dtype_code: int, B, H, Lq, Lk, D, pe: PeDesc | None = None) -> dict | None:
+    """The single-launch kernel's plan for the shape (None when the shape
+    does not run on it)."""
+    info = FusedPlanInfo()
+    r = lib().atn_fused_plan_ex(dtype_code, B, H, Lq, Lk, D,
+                                ctypes.byref(pe) if pe is not None else None,
+                                ctypes.byref(info))
+    if r < 0:
+        raise AtnError(r, "atn_fused_plan_ex")
+    if r == 0:
+        return None
+    return {n: getattr(info, n) for n, _ in FusedPlanInfo._fields_}
+
+
+def rerun_count(reset: bool = False) -> int:
+    return lib().atn_rerun_count(int(reset))
+
+
+def retained_bytes() -> int:
+    return lib().atn_retained_bytes_ex()
+
+
+def release() -> None:
+    st = lib().atn_release_ex()
+    if st != ATN_OK:
+        raise AtnError(st, "atn_release_ex")
 
 
 # ---------------------------------------------------------------- array helpers

@@ -14,7 +14,9 @@
 #include <ctime>
 #include <unistd.h>
 #include <algorithm>
+#include <atomic>
 #include <map>
+#include <memory>
 #include <mutex>
 #include <tuple>
 #include <vector>
@@ -36,6 +38,20 @@ int hip_fail(hipError_t e) {
         hipError_t e_ = (call);                        \
         if (e_ != hipSuccess) return hip_fail(e_);     \
     } while (0)
+
+// ---------------------------------------------------------------- tuning
+// The process-wide overrides (atn_set_tuning_ex): an immutable snapshot
+// behind an atomic pointer, so that every call reads them without a lock.
+// Replaced snapshots are kept (a concurrent call may still read one); they
+// are a few dozen bytes each and replaced only by tests and measurement.
+std::atomic<const atn_tuning*> g_tune{new atn_tuning{}};
+std::vector<std::unique_ptr<const atn_tuning>> g_tune_old;
+std::mutex g_tune_mu;
+
+const atn_tuning& tune() { return *g_tune.load(std::memory_order_acquire); }
+
+// Synchronous drop-in calls rerun without the single-launch kernel.
+std::atomic<long> g_reruns{0};
 
 // ---------------------------------------------------------------- validation
 bool mul_ok(int64_t a, int64_t b, int64_t* out) {
@@ -120,6 +136,7 @@ struct Table {
     float* b = nullptr;
     int npos = 0;
     int nfreq = 0;
+    bool captured = false;  // bound by a call under stream capture at least once
 };
 
 // Library-managed scratch, one per (device, stream) so that calls on
@@ -128,6 +145,7 @@ struct Table {
 struct Workspace {
     void* ptr = nullptr;
     size_t bytes = 0;
+    bool captured = false;  // enqueued into a stream capture at least once
 };
 
 // fp16 encoding tables of the GEMM path's fused K encoding, [npos][D]
@@ -135,17 +153,21 @@ struct Workspace {
 struct Table16 {
     uint16_t* p = nullptr;
     int npos = 0;
+    bool captured = false;
 };
 
 struct DeviceState {
     std::map<hipStream_t, Workspace> ws;
-    // Superseded library workspaces and tables.  Enqueued work, and HIP graphs
-    // captured from it, keep their device addresses, so they are never freed
-    // (they are released with the process).
-    std::vector<void*> retired;
+    // Superseded library workspaces and tables that captured work used: HIP
+    // graphs keep their device addresses, so they are freed only by
+    // atn_release_ex (or with the process).  Buffers no capture used are
+    // freed when superseded.
+    std::vector<std::pair<void*, size_t>> retired;
+    size_t live_bytes = 0;  // workspaces and tables in use
     std::map<std::tuple<int, int, uint32_t>, Table> tables;  // (kind, dim, base bits)
     std::map<std::tuple<int, int, int, uint32_t>, Table16> tables16;  // (kind, D, rotary, base)
     int cus = 0;
+    int xccs = 0;  // XCDs the device reports (8 on a whole MI355X)
     std::map<std::pair<int, int>, int> fused_per_cu;  // (dtype, LDS bytes) -> workgroups per CU
     // Two pinned host words that receive the status words of the null
     // stream's library workspace and of the allocation-free scratch behind
@@ -174,6 +196,33 @@ int refuse_if_capturing(hipStream_t stream) {
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
     ATN_HIP(hipStreamIsCapturing(stream, &cs));
     return cs == hipStreamCaptureStatusNone ? ATN_OK : ATN_ERR_CAPTURE;
+}
+
+bool is_capturing(hipStream_t stream) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    return hipStreamIsCapturing(stream, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone;
+}
+
+// Growth of a library buffer: at least double the old size, so that the
+// superseded buffers of a growing sequence of shapes add up to less than
+// the final one.
+size_t grown(size_t old_bytes, size_t need) { return std::max(need, 2 * old_bytes); }
+
+// A superseded library buffer: freed once the work that may use it has
+// drained (`stream`'s, or the device's for tables shared by every stream),
+// unless captured work used it, which keeps it until atn_release_ex.
+// Called only outside capture.  Caller holds g_mu.
+int supersede(DeviceState& ds, void* p, size_t bytes, bool captured, hipStream_t stream,
+              bool device_wide) {
+    if (p == nullptr) return ATN_OK;
+    ds.live_bytes -= std::min(ds.live_bytes, bytes);
+    if (captured) {
+        ds.retired.emplace_back(p, bytes);
+        return ATN_OK;
+    }
+    ATN_HIP(device_wide ? hipDeviceSynchronize() : hipStreamSynchronize(stream));
+    ATN_HIP(hipFree(p));
+    return ATN_OK;
 }
 
 // Host-side angle tables with the reference CPU path's float expressions
@@ -218,9 +267,9 @@ int get_table(DeviceState& ds, const PePlan& plan, int D, int npos, hipStream_t 
     Table& t = ds.tables[key];
     if (t.a == nullptr || t.npos < npos) {
         if (no_alloc) return ATN_ERR_NOT_PREPARED;
-        const int st = refuse_if_capturing(stream);
+        int st = refuse_if_capturing(stream);
         if (st != ATN_OK) return st;
-        const int want = npos < 64 ? 64 : npos;
+        const int want = std::max({64, npos, t.a ? 2 * t.npos : 0});
         std::vector<float> a, b;
         int nf;
         if (rope) {
@@ -231,13 +280,17 @@ int get_table(DeviceState& ds, const PePlan& plan, int D, int npos, hipStream_t 
             nf = (D + 1) / 2;
         }
         if (t.a) {
-            ds.retired.push_back(t.a);
-            ds.retired.push_back(t.b);
+            const size_t old = (size_t)t.npos * t.nfreq * sizeof(float);
+            st = supersede(ds, t.a, old, t.captured, stream, true);
+            if (st == ATN_OK) st = supersede(ds, t.b, old, t.captured, stream, true);
             t.a = t.b = nullptr;
+            t.captured = false;
+            if (st != ATN_OK) return st;
         }
         const size_t bytes = a.size() * sizeof(float);
         ATN_HIP(hipMalloc(&t.a, bytes));
         ATN_HIP(hipMalloc(&t.b, bytes));
+        ds.live_bytes += 2 * bytes;
         ATN_HIP(hipMemcpy(t.a, a.data(), bytes, hipMemcpyHostToDevice));
         ATN_HIP(hipMemcpy(t.b, b.data(), bytes, hipMemcpyHostToDevice));
         t.npos = want;
@@ -269,9 +322,9 @@ int get_table16(DeviceState& ds, const PePlan& plan, int D, int npos, hipStream_
     Table16& t = ds.tables16[key];
     if (t.p == nullptr || t.npos < npos) {
         if (no_alloc) return ATN_ERR_NOT_PREPARED;
-        const int st = refuse_if_capturing(stream);
+        int st = refuse_if_capturing(stream);
         if (st != ATN_OK) return st;
-        const int want = npos < 64 ? 64 : npos;
+        const int want = std::max({64, npos, t.p ? 2 * t.npos : 0});
         std::vector<float> a, b;
         std::vector<uint16_t> h((size_t)want * D);
         if (rope) {
@@ -292,10 +345,13 @@ int get_table16(DeviceState& ds, const PePlan& plan, int D, int npos, hipStream_
                         f16_bits((d & 1) ? b[(size_t)pos * nf + d / 2] : a[(size_t)pos * nf + d / 2]);
         }
         if (t.p) {
-            ds.retired.push_back(t.p);
+            st = supersede(ds, t.p, (size_t)t.npos * D * 2, t.captured, stream, true);
             t.p = nullptr;
+            t.captured = false;
+            if (st != ATN_OK) return st;
         }
         ATN_HIP(hipMalloc(&t.p, h.size() * 2));
+        ds.live_bytes += h.size() * 2;
         ATN_HIP(hipMemcpy(t.p, h.data(), h.size() * 2, hipMemcpyHostToDevice));
         t.npos = want;
     }
@@ -324,6 +380,7 @@ int bind_tables(const atn_pe_desc* pe, PePlan& plan, int D, int npos, hipStream_
     Table* t = nullptr;
     st = get_table(g_dev[dev], plan, D, npos, stream, no_alloc, &t);
     if (st != ATN_OK) return st;
+    if (!t->captured && is_capturing(stream)) t->captured = true;
     for (atn::PeSide* s : {&plan.q, &plan.k}) {
         s->a = t->a;
         s->b = t->b;
@@ -374,14 +431,20 @@ int ensure_workspace(size_t bytes, hipStream_t stream, void** ws) {
     if (w.bytes < bytes) {
         st = refuse_if_capturing(stream);
         if (st != ATN_OK) return st;
+        const size_t want = grown(w.bytes, bytes);
         if (w.ptr) {
-            ds.retired.push_back(w.ptr);
+            st = supersede(ds, w.ptr, w.bytes, w.captured, stream, false);
             w.ptr = nullptr;
             w.bytes = 0;
+            w.captured = false;
+            if (st != ATN_OK) return st;
         }
-        ATN_HIP(hipMalloc(&w.ptr, bytes));
-        ATN_HIP(hipMemset(w.ptr, 0, bytes));
-        w.bytes = bytes;
+        ATN_HIP(hipMalloc(&w.ptr, want));
+        ATN_HIP(hipMemset(w.ptr, 0, want));
+        w.bytes = want;
+        ds.live_bytes += want;
+    } else if (!w.captured && is_capturing(stream)) {
+        w.captured = true;
     }
     *ws = w.ptr;
     return ATN_OK;
@@ -427,16 +490,6 @@ int rsag_words(int E, int n) {
     return std::max(rs, E / kFusedThreads);
 }
 
-// Tuning overrides (environment): ATN_FUSED_ROWS = query rows per row group
-// (16, 32 or 64), ATN_FUSED_EXCHANGE = "gather" or "rsag", ATN_FUSED_DC =
-// D-slice width (a multiple of 32), ATN_FUSED_XCD = 1 (XCD-local exchange)
-// or 0 (device-scope exchange); ATN_FUSED_TRACE prints the plan.  A plan the
-// override makes impossible falls back to the default choice.
-int env_int(const char* name) {
-    const char* v = std::getenv(name);
-    return v ? std::atoi(v) : 0;
-}
-
 // Cuts each head's query rows into row groups of MB rows and D into slices
 // of dc dims, one workgroup each, with the whole grid resident at once (the
 // kernel's exchange waits need that: capacity is the device's CU count x
@@ -447,9 +500,10 @@ int env_int(const char* name) {
 FusedPlan fused_plan_uncached(int dtype, int pek, const Shape& s, bool query_device) {
     FusedPlan none;
     if (s.Lq > kFusedMaxLq || s.Lk > kFusedMaxLk || s.D % 4 != 0) return none;
-    int cus = 256;
+    const atn_tuning& tn = tune();
+    int cus = tn.model_cus > 0 ? tn.model_cus : 256;
+    int xccs = tn.model_xccs > 0 ? tn.model_xccs : 8;
     int dev = 0;
-    bool xl_ok = true;
     if (query_device) {
         if (hipGetDevice(&dev) != hipSuccess) return none;
         std::lock_guard<std::mutex> lk(g_mu);
@@ -458,9 +512,16 @@ FusedPlan fused_plan_uncached(int dtype, int pek, const Shape& s, bool query_dev
             hipDeviceGetAttribute(&ds.cus, hipDeviceAttributeMultiprocessorCount, dev) !=
                 hipSuccess)
             return none;
+        if (ds.xccs == 0 &&
+            hipDeviceGetAttribute(&ds.xccs, hipDeviceAttributeNumberOfXccs, dev) != hipSuccess)
+            ds.xccs = 1;  // unknown: no XCD-local plans
         cus = ds.cus;
-        xl_ok = cus % 8 == 0;
+        xccs = ds.xccs;
     }
+    // XCD-local plans assume the whole chip: 8 XCDs, each receiving every
+    // eighth workgroup id and 1/8 of the CUs.  A partitioned MI355X (each
+    // partition a device of 1, 2 or 4 XCDs) gets device-scope plans only.
+    const bool xl_ok = xccs == 8 && cus % 8 == 0;
     auto per_cu_cap = [&](int lds) {
         std::lock_guard<std::mutex> lk(g_mu);
         int& c = g_dev[dev].fused_per_cu[std::make_pair(dtype, lds)];
@@ -541,16 +602,12 @@ FusedPlan fused_plan_uncached(int dtype, int pek, const Shape& s, bool query_dev
         return 0.03 * kib * per_cu + 0.02 * p.nchunk + (p.nchunk > 1 && !p.gather1 ? 1.0 : 0.0) +
                0.04 * xkib * per_cu + 0.358 * p.workgroups / cus;
     };
-    // overrides (tuning): row group size, slice width, exchange
-    const int force_rows = env_int("ATN_FUSED_ROWS");
-    int force_dc = env_int("ATN_FUSED_DC");
-    if (force_dc < 32 || force_dc % 32 != 0) force_dc = 0;
-    const char* xe = std::getenv("ATN_FUSED_EXCHANGE");
-    const int force_x = xe == nullptr ? -1 : (std::strcmp(xe, "gather") == 0 ? 1 : 0);
-    const char* xx = std::getenv("ATN_FUSED_XCD");
-    const int force_xcd = xx == nullptr ? -1 : (std::atoi(xx) != 0 ? 1 : 0);
+    // overrides (atn_tuning): row group size, slice width, exchange, scope
+    const int force_rows = tn.fused_rows > 0 ? tn.fused_rows : 0;
+    const int force_dc = tn.fused_dc >= 32 && tn.fused_dc % 32 == 0 ? tn.fused_dc : 0;
+    const int force_x = tn.fused_exchange == 1 ? 1 : (tn.fused_exchange == 2 ? 0 : -1);
+    const int force_xcd = tn.fused_xcd == 1 ? 1 : (tn.fused_xcd == 2 ? 0 : -1);
     const bool forced = force_rows > 0 || force_dc > 0 || force_x >= 0 || force_xcd >= 0;
-    const bool trace = query_device && (forced || std::getenv("ATN_FUSED_TRACE") != nullptr);
     // candidates: row groups of 64, 32 or 16 rows (48: the whole padded head
     // of 33-48 rows), slices of 32-512 dims and the width that gives one
     // workgroup per CU
@@ -580,28 +637,18 @@ FusedPlan fused_plan_uncached(int dtype, int pek, const Shape& s, bool query_dev
                 }
         }
     }
-    if (forced && !best_forced.ok && trace)
-        std::fprintf(stderr, "atn: fused plan override not possible, default plan\n");
     FusedPlan p = best_forced.ok ? best_forced : best;
     if (!query_device && p.ok) p.bytes = max_bytes;
-    if (trace && p.ok)
-        std::fprintf(stderr, "atn: fused plan rows %d slice %d x %d %s%s, %d workgroups\n", p.MB,
-                     p.dc, p.nchunk, p.nchunk == 1 ? "none" : (p.gather1 ? "gather" : "rsag"),
-                     p.xcd ? " xcd" : "", p.workgroups);
     return p;
 }
 
 // Plans are cached per (device, dtype, encoding, shape), the size query's
-// under device -1; tuning overrides and tracing bypass the cache.
+// under device -1; atn_set_tuning_ex drops the cache.
 std::map<std::tuple<int, int, int, int64_t, int64_t, int64_t, int64_t>, FusedPlan> g_fused_plans;
 
 FusedPlan fused_plan(int dtype, int pek, const Shape& s, bool query_device) {
     int dev = -1;
     if (query_device && hipGetDevice(&dev) != hipSuccess) return FusedPlan{};
-    if (std::getenv("ATN_FUSED_ROWS") || std::getenv("ATN_FUSED_DC") ||
-        std::getenv("ATN_FUSED_EXCHANGE") || std::getenv("ATN_FUSED_XCD") ||
-        std::getenv("ATN_FUSED_TRACE"))
-        return fused_plan_uncached(dtype, pek, s, query_device);
     const auto key = std::make_tuple(dev, dtype, pek, (int64_t)s.BH, (int64_t)s.Lq,
                                      (int64_t)s.Lk, (int64_t)s.D);
     {
@@ -650,11 +697,11 @@ GemmPlan gemm_plan(int dtype, const Shape& s, const PePlan& plan) {
     // K~ pass does not (config 4, four query tiles: 724 us fused against
     // 545 + 198 us, so the break-even is near 1100 rows; config 5, one query
     // tile: 112 us against 143 + 110 us).
-    // ATN_GEMM_FUSED_K=-1 turns it off, =1 forces it on (measurement).
+    // atn_tuning.gemm_fused_k turns it off (2) or on wherever it can run (1).
     p.encoded = plan.pek != atn::kPeNone;
-    const int fk = env_int("ATN_GEMM_FUSED_K");
-    if (p.encoded && s.D % 128 == 0 && !plan.caller_tables && fk >= 0 &&
-        (fk > 0 || (s.Lq + 255) / 256 <= 4)) {
+    const int fk = tune().gemm_fused_k;
+    if (p.encoded && s.D % 128 == 0 && !plan.caller_tables && fk != 2 &&
+        (fk == 1 || (s.Lq + 255) / 256 <= 4)) {
         if (!plan.k.on)
             p.benc = atn::kGemmEncRaw;
         else if (plan.pek == atn::kPeSinusoidal)
@@ -686,9 +733,9 @@ GemmPlan gemm_plan(int dtype, const Shape& s, const PePlan& plan) {
 // ---------------------------------------------------------------- core
 // Scratch the library may use for one call before splitting it: the
 // caller's workspace size, the allocation-free array, or this cap for the
-// library's own workspace (ATN_WORKSPACE_CAP_MIB overrides, for tests).
+// library's own workspace (atn_tuning.workspace_cap_mib overrides it).
 size_t library_cap() {
-    const int mib = env_int("ATN_WORKSPACE_CAP_MIB");
+    const int mib = tune().workspace_cap_mib;
     return mib > 0 ? (size_t)mib << 20 : (size_t)1 << 30;
 }
 
@@ -816,6 +863,7 @@ int attention_run(int dtype, const void* Q, const void* K, const void* V, void* 
                     st = get_table16(g_dev[dev], plan, D, Lq > Lk ? Lq : Lk, stream, no_alloc,
                                      &t16);
                     if (st != ATN_OK) return st;
+                    if (!t16->captured && is_capturing(stream)) t16->captured = true;
                     tab = t16->p;
                     tab_rows = t16->npos;
                 }
@@ -841,12 +889,13 @@ int attention_run(int dtype, const void* Q, const void* K, const void* V, void* 
         float* red = reinterpret_cast<float*>((char*)ws + kSyncBytes + round256(fd.part_words * 4));
         unsigned* done = reinterpret_cast<unsigned*>((char*)ws + kSyncDoneOff);
         unsigned* xctr = reinterpret_cast<unsigned*>((char*)ws + kSyncXcdOff);
-        if (std::getenv("ATN_FUSED_PRESET_STATUS") != nullptr) {
-            // testing: the status word set as a timed-out call leaves it, so
-            // that every workgroup takes the fail-closed exit (no wait is
-            // entered)
-            static const int kSet = 1;
-            ATN_HIP(hipMemcpyAsync(status, &kSet, sizeof(int), hipMemcpyHostToDevice, stream));
+        if (tune().preset_status) {
+            // test control (atn_tuning.preset_status): the status word set as
+            // a timed-out call leaves it, so that every workgroup takes the
+            // fail-closed exit (no wait is entered); never recorded into a
+            // graph
+            if (is_capturing(stream)) return ATN_ERR_CAPTURE;
+            ATN_HIP(hipMemsetAsync(status, 0x01, 1, stream));
         }
         ATN_HIP(atn::launch_fused_small(dtype, plan.pek, Q, K, V, out, part, red, epochs, done,
                                         status, xctr, (int)s.BH, Lq, Lk, D, fd.MB, fd.dc,
@@ -888,10 +937,7 @@ int attention_core(int dtype, const void* Q, const void* K, const void* V, void*
     PePlan plan;
     st = check_pe(pe, D, &plan);
     if (st != ATN_OK) return st;
-    // ATN_F32_FULL: fp32 calls in full fp32 products (the split-D pipeline)
-    // instead of the single-launch kernel's hi + lo bf16 parts, for logits
-    // beyond that kernel's accuracy range; slower
-    plan.no_fused = no_fused || (dtype == ATN_DTYPE_F32 && std::getenv("ATN_F32_FULL") != nullptr);
+    plan.no_fused = no_fused || tune().no_fused != 0;
     // every path needs at least the sync region; the path-specific size is
     // checked once the device has chosen the path
     if (workspace != nullptr && workspace_bytes < kSyncBytes) return ATN_ERR_WORKSPACE;
@@ -1033,12 +1079,14 @@ int workspace_status(void* ws, hipStream_t stream) {
 }
 
 // Completion of a synchronous drop-in call (enqueued on the null stream):
-// the status words of the workspaces such a call can use (the null stream's
-// library workspace, the allocation-free scratch) are copied into pinned
-// host words behind the call, so the one device synchronization covers the
-// call and its status check.  A set word runs the recovery of
-// workspace_status() and returns ATN_ERR_DEVICE_TIMEOUT; any other failure
-// ends the process (the reference's CUDA_CHECK, final/attention.cu:12-21).
+// the status word of the null stream's library workspace, the only
+// workspace a drop-in uses, is copied into a pinned host word behind the
+// call, so the one device synchronization covers the call and its status
+// check.  A set word runs the recovery of workspace_status() and returns
+// ATN_ERR_DEVICE_TIMEOUT; any other failure ends the process (the
+// reference's CUDA_CHECK, final/attention.cu:12-21).  The allocation-free
+// scratch is not looked at: its status belongs to the noalloc callers, who
+// query it with atn_sync_status_ex.
 int finish_sync(int status, const char* where) {
     if (status != ATN_OK) die(status, where);
     hipError_t e = hipGetLastError();
@@ -1063,31 +1111,18 @@ int finish_sync(int status, const char* where) {
         }
         host = ds.status_host;
     }
-    void* sc = nullptr;
-    if (atn::noalloc_ready(dev)) {
-        e = atn::noalloc_scratch(dev, kSyncBytes, nullptr, &sc);
-        if (e != hipSuccess) {
-            g_last_hip_error = (int)e;
-            die(ATN_ERR_HIP, where);
-        }
-    }
     bool copied = host != nullptr;
     if (copied && lib_ws != nullptr)
         copied = hipMemcpyAsync(&host[0], lib_ws, sizeof(int), hipMemcpyDeviceToHost, nullptr) ==
-                 hipSuccess;
-    if (copied && sc != nullptr)
-        copied = hipMemcpyAsync(&host[1], sc, sizeof(int), hipMemcpyDeviceToHost, nullptr) ==
                  hipSuccess;
     e = hipDeviceSynchronize();
     if (e != hipSuccess) {
         g_last_hip_error = (int)e;
         die(ATN_ERR_HIP, where);
     }
-    // without the pinned words (or a failed copy), the blocking reads
-    const bool clean =
-        copied && (lib_ws == nullptr || host[0] == 0) && (sc == nullptr || host[1] == 0);
-    if (!clean) {
-        const int ws = workspace_status(nullptr, nullptr);
+    // without the pinned word (or after a failed copy), the blocking read
+    if (lib_ws != nullptr && (!copied || host[0] != 0)) {
+        const int ws = workspace_status(lib_ws, nullptr);
         if (ws != ATN_OK && ws != ATN_ERR_DEVICE_TIMEOUT) die(ws, where);
         return ws;
     }
@@ -1109,6 +1144,11 @@ void dropin_attention(const char* where, int dtype, const void* Q, const void* K
     if (finish_sync(attention_core(dtype, Q, K, V, out, B, H, Lq, Lk, D, pe, nullptr, 0, nullptr),
                     where) == ATN_OK)
         return;
+    g_reruns.fetch_add(1, std::memory_order_relaxed);
+    std::fprintf(stderr,
+                 "attn_mi355x: %s: the single-launch kernel's wait timed out; running the call "
+                 "again without it\n",
+                 where);
     sync_or_die(attention_core(dtype, Q, K, V, out, B, H, Lq, Lk, D, pe, nullptr, 0, nullptr,
                                false, true),
                 where);
@@ -1173,6 +1213,75 @@ int atn_device_count(void) {
     return n;
 }
 
+int atn_set_tuning_ex(const atn_tuning* t) {
+    std::unique_ptr<const atn_tuning> fresh(new atn_tuning(t ? *t : atn_tuning{}));
+    std::lock_guard<std::mutex> tl(g_tune_mu);
+    const atn_tuning* old = g_tune.exchange(fresh.release(), std::memory_order_acq_rel);
+    g_tune_old.emplace_back(old);
+    std::lock_guard<std::mutex> lk(g_mu);
+    g_fused_plans.clear();
+    return ATN_OK;
+}
+
+int atn_get_tuning_ex(atn_tuning* t) {
+    if (!t) return ATN_ERR_NULL_POINTER;
+    *t = tune();
+    return ATN_OK;
+}
+
+int atn_fused_plan_ex(int dtype, int batch, int heads, int len_q, int len_k, int head_d,
+                      const atn_pe_desc* pe, atn_fused_plan_info* info) {
+    if (!info) return ATN_ERR_NULL_POINTER;
+    if (dtype != ATN_DTYPE_F32 && dtype != ATN_DTYPE_BF16) return ATN_ERR_BAD_ARGUMENT;
+    Shape s;
+    int st = check_shape(batch, heads, len_q, len_k, head_d, &s);
+    if (st != ATN_OK) return st;
+    PePlan plan;
+    st = check_pe(pe, head_d, &plan);
+    if (st != ATN_OK) return st;
+    *info = atn_fused_plan_info{};
+    if (tune().no_fused) return 0;
+    int n = 0;
+    const bool dev = hipGetDeviceCount(&n) == hipSuccess && n > 0;
+    const FusedPlan p = fused_plan(dtype, plan.pek, s, dev);
+    if (!p.ok) return 0;
+    info->rows = p.MB;
+    info->dc = p.dc;
+    info->nchunk = p.nchunk;
+    info->gather1 = p.gather1;
+    info->xcd = p.xcd;
+    info->workgroups = p.workgroups;
+    info->lds = p.lds;
+    return 1;
+}
+
+long atn_rerun_count(int reset) {
+    return reset ? g_reruns.exchange(0) : g_reruns.load();
+}
+
+size_t atn_retained_bytes_ex(void) {
+    int dev;
+    if (current_device(&dev) != ATN_OK) return 0;
+    std::lock_guard<std::mutex> lk(g_mu);
+    const DeviceState& ds = g_dev[dev];
+    size_t b = ds.live_bytes;
+    for (const auto& r : ds.retired) b += r.second;
+    return b;
+}
+
+int atn_release_ex(void) {
+    int dev;
+    int st = current_device(&dev);
+    if (st != ATN_OK) return st;
+    std::lock_guard<std::mutex> lk(g_mu);
+    DeviceState& ds = g_dev[dev];
+    if (ds.retired.empty()) return ATN_OK;
+    ATN_HIP(hipDeviceSynchronize());
+    for (const auto& r : ds.retired) ATN_HIP(hipFree(r.first));
+    ds.retired.clear();
+    return ATN_OK;
+}
+
 int atn_attention_fwd_ex(int dtype, const void* Q, const void* K, const void* V, void* out,
                          int batch, int heads, int len_q, int len_k, int head_d,
                          const atn_pe_desc* pe, void* workspace, size_t workspace_bytes,
@@ -1219,8 +1328,7 @@ int atn_attention_path_ex(int dtype, int batch, int heads, int len_q, int len_k,
     if (st != ATN_OK) return st;
     int n = 0;
     const bool dev = hipGetDeviceCount(&n) == hipSuccess && n > 0;
-    const bool full = dtype == ATN_DTYPE_F32 && std::getenv("ATN_F32_FULL") != nullptr;
-    if (!full && fused_plan(dtype, plan.pek, s, dev).ok) return ATN_PATH_FUSED_SMALL;
+    if (!tune().no_fused && fused_plan(dtype, plan.pek, s, dev).ok) return ATN_PATH_FUSED_SMALL;
     if (gemm_plan(dtype, s, plan).ok) return ATN_PATH_GEMM;
     return ATN_PATH_SPLIT_D;
 }

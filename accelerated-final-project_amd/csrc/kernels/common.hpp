@@ -89,6 +89,24 @@ __device__ __forceinline__ float lane_read(float v, int lane) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
 }
 
+// max of two floats as one v_max_f32: fmaxf's IEEE semantics make the
+// compiler canonicalize both operands first (two more instructions); the
+// values here are never signalling NaNs
+__device__ __forceinline__ float vmaxf(float a, float b) {
+    float d;
+    asm("v_max_f32 %0, %1, %2" : "=v"(d) : "v"(a), "v"(b));
+    return d;
+}
+
+// max(m, |a|, |b|) as one v_max3_f32 with absolute-value modifiers (running
+// magnitude maxima: the fp16 range checks of the fused K encoding and of the
+// single-launch kernel's fp32 operands)
+__device__ __forceinline__ float vmax3abs(float m, float a, float b) {
+    float d;
+    asm("v_max3_f32 %0, %1, |%2|, |%3|" : "=v"(d) : "v"(m), "v"(a), "v"(b));
+    return d;
+}
+
 // Full-wave max; result is wave-uniform.
 __device__ __forceinline__ float wave_max(float v) {
     v = fmaxf(v, dpp<kDppQuadXor1>(v));

@@ -10,17 +10,21 @@
 //   1. loads its Q rows' slice and the head's K/V slices once (16-byte
 //      loads, all in flight before the first LDS store; the positional
 //      encoding is applied to Q and K at load) into LDS;
-//   2. computes the partial scores S_c = Q[rows, c] K[:, c]^T on bf16 MFMA
-//      (v_mfma_f32_16x16x32_bf16), up to eight independent 16x16 tiles per
-//      wave.  Values that are not bf16 -- fp32 inputs, and bf16 inputs
-//      after a positional encoding -- are split into hi + lo bf16 parts and
-//      multiplied as a_hi b_hi + a_hi b_lo + a_lo b_hi (fp32 accumulation),
-//      which keeps about 16 significant bits of every product, at about
-//      five times the throughput of fp32 MFMA (v_mfma_f32_16x16x4_f32),
-//      whose dependent chains bounded this phase.  For fp32 inputs the
-//      logit error grows with the logits' size: the 1e-4 bar holds for
-//      logits up to about +-10 (inputs of sigma 1.5 at D = 512-8192); at
-//      +-18 (sigma 2) up to about two elements in 10^4 exceed it;
+//   2. computes the partial scores S_c = Q[rows, c] K[:, c]^T on 16-bit
+//      MFMA, up to eight independent 16x16 tiles per wave.  fp32 inputs are
+//      split into hi + lo fp16 parts (split2_f16: 22 significant bits, and
+//      subnormal parts, which the MFMA keeps, hold small values to 2^-25)
+//      and multiplied as a_hi b_hi + a_hi b_lo + a_lo b_hi on
+//      v_mfma_f32_16x16x32_f16 (exact products, fp32 accumulation; the
+//      dropped a_lo b_lo is below 2^-20 of the product), at about five
+//      times the throughput of fp32 MFMA
+//      (v_mfma_f32_16x16x4_f32), whose dependent chains bounded this phase.
+//      The split needs |x| < 65504: each workgroup tracks the largest
+//      magnitude it stores, and one whose Q/K (or V) slice exceeds that
+//      range stages the slice again scaled by a power of two (exact) and
+//      multiplies the results back.  bf16 inputs are exact bf16 MFMA
+//      operands (v_mfma_f32_16x16x32_bf16); after a positional encoding
+//      they are split into hi + lo bf16 parts;
 //   3. all-reduces S over the group's slices through global memory, either
 //      in one gather (every workgroup reads every slice's partial of its
 //      group: one memory round trip) or, when that volume is too large, as
@@ -28,8 +32,10 @@
 //      always summed in slice order, so results are bit-reproducible;
 //   4. exact softmax of scale * S per row (max, exp, sum, divide;
 //      final/attention.cu:262-270), 16, 8 or 4 threads per row;
-//   5. O[rows, slice] = P V[:, slice] on bf16 MFMA, P split into hi + lo
-//      bf16 parts (and fp32 V too), one store per output element.
+//   5. O[rows, slice] = P V[:, slice] on MFMA, P split into hi + lo parts
+//      (fp32: fp16 parts of 2^15 P, exact power-of-two scaling, and fp32 V
+//      split as Q and K are; bf16: bf16 parts), one store per output
+//      element.
 //
 // Q and O are touched once; K and V once per row group, and the QB
 // workgroups that share a K/V slice get workgroup ids QB apart by a
@@ -146,6 +152,8 @@ namespace {
 
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kThreads = 256;
 constexpr int kSpinLimit = 1 << 18;  // polls (each >= one memory round trip): ~0.3 s bound
@@ -203,7 +211,7 @@ __device__ __forceinline__ float4 encode4(float4 v4, const T* __restrict__ xr, i
     return make_float4(v[0], v[1], v[2], v[3]);
 }
 
-// LDS geometry of one workgroup (MFMA operands as bf16).  Q, K and P rows
+// LDS geometry of one workgroup (MFMA operands as 16-bit parts).  Q, K and P rows
 // are padded by 8 elements (16-byte aligned 8-element reads); V is kept
 // [key][dim] with a row stride of dc + 16 elements, i.e. 32 or 96 bytes
 // (mod 128), so the 4 rows x 32 bytes that each 16-lane group of a
@@ -220,8 +228,9 @@ struct Geo {
     int bytes;
 };
 
-// f32: fp32 inputs (Q, K and V kept as hi + lo bf16 parts); encoded: a
-// positional encoding makes Q/K non-bf16 (hi + lo parts for bf16 inputs).
+// f32: fp32 inputs (Q, K and V kept as hi + lo fp16 parts); encoded: a
+// positional encoding makes Q/K non-bf16 (hi + lo bf16 parts for bf16
+// inputs).
 __host__ __device__ inline Geo make_geo(bool f32, bool encoded, bool s_over_qk, int Lq, int Lk,
                                         int dc) {
     Geo g{};
@@ -466,8 +475,18 @@ struct Raw4<uint16_t> {
     }
 };
 
-__device__ __forceinline__ bf16x8 lds8(const uint16_t* p) {
-    return __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(p));
+// 8 consecutive 16-bit MFMA operand elements (bf16x8 or f16x8) from LDS
+template <typename VT>
+__device__ __forceinline__ VT lds8(const uint16_t* p) {
+    return __builtin_bit_cast(VT, *reinterpret_cast<const uint4*>(p));
+}
+
+// 16x16x32 MFMA with fp32 accumulation on bf16 or fp16 operands
+__device__ __forceinline__ v4f mfma16(const bf16x8& a, const bf16x8& b, const v4f& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ v4f mfma16(const f16x8& a, const f16x8& b, const v4f& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
 // two floats to packed bf16 by the hardware conversion (round to nearest
@@ -478,43 +497,89 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
     return __builtin_bit_cast(uint32_t, v);
 }
 
-// NT independent 16x16 bf16 MFMA accumulations sharing one A operand (k
-// step 32, 8 elements per lane, contiguous along k): acc[u] += A B_u^T over
-// k in [0, kdim), where lane (lr, lk) reads A at a and tile u's B at b + u *
-// bstep (a, b already offset to the lane's row and k = 8 lk); the operands
-// of the next k step are read from LDS before this step's MFMAs issue.  With
-// ALO the A operand is a_hi + a_lo (two MFMAs); with BLO as well the
-// three-term product a_hi b + a_hi b_lo + a_lo b.
-template <int NT, bool ALO, bool BLO>
-__device__ __forceinline__ void mma_bf16(const uint16_t* a, const uint16_t* a_lo,
-                                         const uint16_t* b, const uint16_t* b_lo, int bstep,
-                                         int kdim, v4f (&acc)[NT]) {
-    bf16x8 ah = lds8(a), al{};
-    if constexpr (ALO) al = lds8(a_lo);
-    bf16x8 bv[NT], bl[NT];
+// hi + lo parts of two values, packed: bf16 parts (hi rounded to nearest
+// even, lo the residual rounded; 16 significant bits) ...
+__device__ __forceinline__ void split2_bf16(float a, float b, uint32_t& h, uint32_t& l) {
+    h = pack_bf16x2(a, b);
+    l = pack_bf16x2(a - __uint_as_float(h << 16), b - __uint_as_float(h & 0xffff0000u));
+}
+// ... or fp16 parts: hi = x rounded toward zero (v_cvt_pkrtz_f16_f32, whose
+// result the residuals are formed from), lo = the residual rounded to
+// nearest even (v_cvt_pk_f16_f32; fp16 subnormals are kept, and the MFMA
+// keeps them): |x - hi - lo| <= 2^-22 |x| for |x| >= 2^-3 (hi then 11
+// significant bits, the residual below one fp16 ulp of x) and <= 2^-25
+// below; needs |x| < 65504.
+__device__ __forceinline__ void split2_f16(float a, float b, uint32_t& h, uint32_t& l) {
+    const f16x2 hh = __builtin_bit_cast(f16x2, __builtin_amdgcn_cvt_pkrtz(a, b));
+    const f16x2 lv = {(_Float16)(a - (float)hh[0]), (_Float16)(b - (float)hh[1])};
+    h = __builtin_bit_cast(uint32_t, hh);
+    l = __builtin_bit_cast(uint32_t, lv);
+}
+
+// Largest magnitude an fp32 operand may have for the fp16 split.
+constexpr float kF16Range = 65504.0f;
+
+// Power-of-two scale s for a slice of largest magnitude m (m >= 0) that
+// does not fit the fp16 split: m s in [2^14, 2^15) (s = 2^(14 - e) for m in
+// [2^e, 2^(e+1)), kept within [2^-114, 2^126]), so every scaled value
+// converts without overflow; the unit 1 / s undoes it exactly.
+__device__ __forceinline__ float pow2_scale(float m) {
+    int eb = (__float_as_int(m) >> 23) & 0xff;
+    if (eb == 0) return 1.f;
+    eb = eb < 15 ? 15 : eb;
+    return __int_as_float((268 - eb) << 23);
+}
+// The largest finite magnitude of m and the 4 values (infinities and NaNs
+// count as 0: they stay non-finite through the scaling, and must not set the
+// scale of the finite values beside them).
+__device__ __forceinline__ float max_finite4(float m, float4 f) {
+    auto fa = [](float x) {
+        const float a = fabsf(x);
+        return a < INFINITY ? a : 0.f;
+    };
+    return fmaxf(fmaxf(m, fmaxf(fa(f.x), fa(f.y))), fmaxf(fa(f.z), fa(f.w)));
+}
+__device__ __forceinline__ float pow2_unit(float m) {
+    int eb = (__float_as_int(m) >> 23) & 0xff;
+    if (eb == 0) return 1.f;
+    eb = eb < 15 ? 15 : eb;
+    return __int_as_float((eb - 14) << 23);
+}
+
+// NT independent 16x16 MFMA accumulations sharing one A operand (k step
+// 32, 8 elements per lane, contiguous along k; VT = bf16x8 or f16x8):
+// acc[u] += A B_u^T over k in [0, kdim), where lane (lr, lk) reads A at a
+// and tile u's B at b + u * bstep (a, b already offset to the lane's row and
+// k = 8 lk); the operands of the next k step are read from LDS before this
+// step's MFMAs issue.  With ALO the A operand is a_hi + a_lo (two MFMAs);
+// with BLO as well the three-term product a_hi b + a_hi b_lo + a_lo b.
+template <typename VT, int NT, bool ALO, bool BLO>
+__device__ __forceinline__ void mma16(const uint16_t* a, const uint16_t* a_lo, const uint16_t* b,
+                                      const uint16_t* b_lo, int bstep, int kdim, v4f (&acc)[NT]) {
+    VT ah = lds8<VT>(a), al{};
+    if constexpr (ALO) al = lds8<VT>(a_lo);
+    VT bv[NT], bl[NT];
 #pragma unroll
     for (int u = 0; u < NT; ++u) {
-        bv[u] = lds8(b + u * bstep);
-        if constexpr (BLO) bl[u] = lds8(b_lo + u * bstep);
+        bv[u] = lds8<VT>(b + u * bstep);
+        if constexpr (BLO) bl[u] = lds8<VT>(b_lo + u * bstep);
     }
     for (int kk = 0; kk < kdim; kk += 32) {
         const int kn = min(kk + 32, kdim - 32);
-        const bf16x8 ahn = lds8(a + kn);
-        bf16x8 aln{};
-        if constexpr (ALO) aln = lds8(a_lo + kn);
-        bf16x8 bvn[NT], bln[NT];
+        const VT ahn = lds8<VT>(a + kn);
+        VT aln{};
+        if constexpr (ALO) aln = lds8<VT>(a_lo + kn);
+        VT bvn[NT], bln[NT];
 #pragma unroll
         for (int u = 0; u < NT; ++u) {
-            bvn[u] = lds8(b + u * bstep + kn);
-            if constexpr (BLO) bln[u] = lds8(b_lo + u * bstep + kn);
+            bvn[u] = lds8<VT>(b + u * bstep + kn);
+            if constexpr (BLO) bln[u] = lds8<VT>(b_lo + u * bstep + kn);
         }
 #pragma unroll
         for (int u = 0; u < NT; ++u) {
-            acc[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bv[u], acc[u], 0, 0, 0);
-            if constexpr (BLO)
-                acc[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bl[u], acc[u], 0, 0, 0);
-            if constexpr (ALO)
-                acc[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bv[u], acc[u], 0, 0, 0);
+            acc[u] = mfma16(ah, bv[u], acc[u]);
+            if constexpr (BLO) acc[u] = mfma16(ah, bl[u], acc[u]);
+            if constexpr (ALO) acc[u] = mfma16(al, bv[u], acc[u]);
         }
         ah = ahn;
         if constexpr (ALO) al = aln;
@@ -531,28 +596,28 @@ __device__ __forceinline__ v4i16 ds_read_tr16(const uint16_t* p) {
     return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4i16*)(p));
 }
 
-// PV form of mma_bf16 (A = P as hi + lo parts): the B operand comes from V
+// PV form of mma16 (A = P as hi + lo parts): the B operand comes from V
 // kept [key][dim] in LDS (row stride vstr; vb points at tile 0's first
 // column, tile u's columns start nstep later; with VLO, V's lo part lies
 // vlo_d elements further).  Lane (lr, lk) needs keys kk + 8 lk + 0..7 of
 // column lr: in each 16-lane group lane L supplies the address of key kk +
 // 8 lk + 4 h + (L % 16) / 4, columns 4 (L % 4) .. + 3, and the transposing
-// read (ds_read_b64_tr_b16) hands lane L keys 4 h + 0..3 of column L % 16 --
-// half h of its operand.
-template <int NT, bool VLO>
-__device__ __forceinline__ void mma_bf16_vt(const uint16_t* a, const uint16_t* a_lo,
-                                            const uint16_t* vb, int vlo_d, int vstr, int nstep,
-                                            int kdim, v4f (&acc)[NT]) {
+// read (ds_read_b64_tr_b16, a 16-bit move of either type) hands lane L keys
+// 4 h + 0..3 of column L % 16 -- half h of its operand.
+template <typename VT, int NT, bool VLO>
+__device__ __forceinline__ void mma16_vt(const uint16_t* a, const uint16_t* a_lo,
+                                         const uint16_t* vb, int vlo_d, int vstr, int nstep,
+                                         int kdim, v4f (&acc)[NT]) {
     const int lane = threadIdx.x & 63;
     const uint16_t* vl = vb + (8 * (lane >> 4) + ((lane & 15) >> 2)) * vstr + 4 * (lane & 3);
     auto vread = [&](const uint16_t* p) {
         const uint2 lo = __builtin_bit_cast(uint2, ds_read_tr16(p));
         const uint2 hi = __builtin_bit_cast(uint2, ds_read_tr16(p + 4 * vstr));
-        return __builtin_bit_cast(bf16x8, make_uint4(lo.x, lo.y, hi.x, hi.y));
+        return __builtin_bit_cast(VT, make_uint4(lo.x, lo.y, hi.x, hi.y));
     };
     for (int kk = 0; kk < kdim; kk += 32) {
-        const bf16x8 ah = lds8(a + kk), al = lds8(a_lo + kk);
-        bf16x8 bv[NT], bl[NT];
+        const VT ah = lds8<VT>(a + kk), al = lds8<VT>(a_lo + kk);
+        VT bv[NT], bl[NT];
 #pragma unroll
         for (int u = 0; u < NT; ++u) {
             const uint16_t* p = vl + kk * vstr + u * nstep;
@@ -561,10 +626,9 @@ __device__ __forceinline__ void mma_bf16_vt(const uint16_t* a, const uint16_t* a
         }
 #pragma unroll
         for (int u = 0; u < NT; ++u) {
-            acc[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bv[u], acc[u], 0, 0, 0);
-            if constexpr (VLO)
-                acc[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bl[u], acc[u], 0, 0, 0);
-            acc[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bv[u], acc[u], 0, 0, 0);
+            acc[u] = mfma16(ah, bv[u], acc[u]);
+            if constexpr (VLO) acc[u] = mfma16(ah, bl[u], acc[u]);
+            acc[u] = mfma16(al, bv[u], acc[u]);
         }
     }
 }
@@ -616,11 +680,18 @@ template <typename T, int PEK, bool XL, int FORM>
 __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
     constexpr bool kBf16 = sizeof(T) == 2;
     // Q and K carry lo parts (fp32 inputs, or encoded bf16 inputs); V does
-    // for fp32 inputs
+    // for fp32 inputs.  MFMA operands: fp16 parts for fp32 inputs, bf16 for
+    // bf16 inputs.
     constexpr bool kSplit = !kBf16 || PEK != kPeNone;
     constexpr bool kVlo = !kBf16;
+    typedef std::conditional_t<kBf16, bf16x8, f16x8> VT;
     extern __shared__ __align__(16) unsigned char smem[];
     __shared__ int flag;
+    // fp32: per wave, whether a Q/K value (0-3) or a V value (4-7) it stored
+    // is outside the fp16 split's range; the slices' largest magnitudes when
+    // a slice is staged again (sh_big)
+    __shared__ __align__(16) int sh_over[8];
+    __shared__ float sh_big[8];
 
     // Every kernel argument in one batch of scalar loads, waited for once,
     // here; left alone the compiler issues each load at its first use.
@@ -760,43 +831,51 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
     const int MQ = g.MQ, NK = g.NK, E = MQ * NK, nrb = MQ / 16;
     const int cq = r0 < rstep ? fdiv(MQ - r0 + rstep - 1, rstep, a.m_rstep) : 0;
     const int ckv = r0 < rstep ? fdiv(NK - r0 + rstep - 1, rstep, a.m_rstep) : 0;
-    // hi (rounded to nearest even) and lo (the residual, rounded) bf16
-    // parts of 4 values
+    // hi and lo parts of 4 values: fp16 parts for fp32 inputs, bf16 parts
+    // for bf16 inputs after a positional encoding
     auto split4 = [](const float (&e4)[4], uint2& w, uint2& wl) {
-        w.x = pack_bf16x2(e4[0], e4[1]);
-        w.y = pack_bf16x2(e4[2], e4[3]);
-        wl.x = pack_bf16x2(e4[0] - __uint_as_float(w.x << 16),
-                           e4[1] - __uint_as_float(w.x & 0xffff0000u));
-        wl.y = pack_bf16x2(e4[2] - __uint_as_float(w.y << 16),
-                           e4[3] - __uint_as_float(w.y & 0xffff0000u));
+        if constexpr (kBf16) {
+            split2_bf16(e4[0], e4[1], w.x, wl.x);
+            split2_bf16(e4[2], e4[3], w.y, wl.y);
+        } else {
+            split2_f16(e4[0], e4[1], w.x, wl.x);
+            split2_f16(e4[2], e4[3], w.y, wl.y);
+        }
     };
-    auto store_v = [&](int row, Raw raw) {
+    // fp32: the largest magnitudes of the Q/K values and of the V values
+    // this thread stores (the fp16 split's range check)
+    float big_qk = 0.f, big_v = 0.f;
+    // one V row vector into LDS; s scales it by a power of two (a slice
+    // staged again)
+    auto store_v = [&](int row, Raw raw, float s = 1.f) {
         uint16_t* dst = reinterpret_cast<uint16_t*>(smem + g.v_off) + row * g.vstr + col;
         if constexpr (kBf16) {
             // the raw bf16 bits, [key][dim]
             *reinterpret_cast<uint2*>(dst) = raw;
         } else {
-            const float e4[4] = {raw.x, raw.y, raw.z, raw.w};
+            const float e4[4] = {raw.x * s, raw.y * s, raw.z * s, raw.w * s};
+            big_v = vmax3abs(vmax3abs(big_v, e4[0], e4[1]), e4[2], e4[3]);
             uint2 w, wl;
             split4(e4, w, wl);
             *reinterpret_cast<uint2*>(dst) = w;
             *reinterpret_cast<uint2*>(dst + (g.vl_off - g.v_off) / 2) = wl;
         }
     };
+    // one encoded row vector of Q (isq) or K into its LDS rows, scaled by s
+    auto store_qk = [&](bool isq, int row, float4 f, float s = 1.f) {
+        const float e4[4] = {f.x * s, f.y * s, f.z * s, f.w * s};
+        if constexpr (!kBf16) big_qk = vmax3abs(vmax3abs(big_qk, e4[0], e4[1]), e4[2], e4[3]);
+        const int off = row * (isq ? g.qstr : g.kstr) + col;
+        uint16_t* hi = reinterpret_cast<uint16_t*>(smem + (isq ? g.q_off : g.k_off));
+        uint2 w, wl;
+        split4(e4, w, wl);
+        *reinterpret_cast<uint2*>(hi + off) = w;
+        if constexpr (kSplit) {
+            uint16_t* lo = reinterpret_cast<uint16_t*>(smem + (isq ? g.ql_off : g.kl_off));
+            *reinterpret_cast<uint2*>(lo + off) = wl;
+        }
+    };
     {
-        // one encoded row vector of Q (isq) or K into its LDS rows
-        auto store_qk = [&](bool isq, int row, float4 f) {
-            const float e4[4] = {f.x, f.y, f.z, f.w};
-            const int off = row * (isq ? g.qstr : g.kstr) + col;
-            uint16_t* hi = reinterpret_cast<uint16_t*>(smem + (isq ? g.q_off : g.k_off));
-            uint2 w, wl;
-            split4(e4, w, wl);
-            *reinterpret_cast<uint2*>(hi + off) = w;
-            if constexpr (kSplit) {
-                uint16_t* lo = reinterpret_cast<uint16_t*>(smem + (isq ? g.ql_off : g.kl_off));
-                *reinterpret_cast<uint2*>(lo + off) = wl;
-            }
-        };
         // round j into LDS: Q and K (and, unless deferred, V)
         auto store_round = [&](int j, Raw (&q)[kQ], Raw (&k)[kKV], Raw (&v)[kKV],
                                bool store_v_now) {
@@ -834,8 +913,76 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
             }
         }
     }
+    if constexpr (!kBf16) {
+        const bool over = __ballot(!(big_qk < kF16Range)) != 0;  // NaN counts as over
+        if (lane == 0) sh_over[wave] = over;
+    }
     if (tid == 0) flag = 1;
     __syncthreads();
+
+    // fp32 slices with a value outside the fp16 split's range (rare): the
+    // slice is loaded again and staged scaled by a power of two from its
+    // largest finite magnitude, so that every scaled finite value converts;
+    // the unit returned undoes the scaling exactly.  Rows past the sequence and
+    // columns past D read as zeros, as in the staging above.
+    auto load_row = [&](const __amdgpu_buffer_rsrc_t& r, int row) -> float4 {
+        return Raw4<T>::f4(Raw4<T>::ld_buf(r, lane_ok ? (row * D + d) * es : kOob));
+    };
+    auto slice_max = [&](float m0, float m1, int slot) {
+        // workgroup maxima of two per-thread values (slots slot, slot + 4)
+        m0 = wave_max(m0);
+        m1 = wave_max(m1);
+        if (lane == 0) {
+            sh_big[slot + wave] = m0;
+            sh_big[slot + 4 + wave] = m1;
+        }
+        __syncthreads();
+    };
+    auto max4 = [&](int slot) {
+        return fmaxf(fmaxf(sh_big[slot], sh_big[slot + 1]),
+                     fmaxf(sh_big[slot + 2], sh_big[slot + 3]));
+    };
+    auto restage_qk = [&]() -> float {
+        auto enc_row = [&](bool isq, int row) {
+            float4 f = load_row(isq ? rq : rk, row);
+            if constexpr (PEK != kPeNone)
+                if (lane_ok && row < (isq ? Lq : Lk))
+                    f = isq ? encode4<T, PEK>(f, Q + (size_t)row * D, q0 + row, d, a.pq)
+                            : encode4<T, PEK>(f, K + (size_t)row * D, row, d, a.pk);
+            return f;
+        };
+        // (loops kept rolled: this path must not raise the kernel's
+        // register count, which sets its occupancy)
+        float mq = 0.f, mk = 0.f;
+        if (r0 < rstep) {
+#pragma unroll 1
+            for (int row = r0; row < MQ; row += rstep) {
+                mq = max_finite4(mq, enc_row(true, row));
+            }
+#pragma unroll 1
+            for (int row = r0; row < NK; row += rstep) {
+                mk = max_finite4(mk, enc_row(false, row));
+            }
+        }
+        slice_max(mq, mk, 0);
+        mq = max4(0);
+        mk = max4(4);
+        const float sq = pow2_scale(mq), sk = pow2_scale(mk);
+        if (r0 < rstep) {
+#pragma unroll 1
+            for (int row = r0; row < MQ; row += rstep) store_qk(true, row, enc_row(true, row), sq);
+#pragma unroll 1
+            for (int row = r0; row < NK; row += rstep) store_qk(false, row, enc_row(false, row), sk);
+        }
+        __syncthreads();
+        return pow2_unit(mq) * pow2_unit(mk);
+    };
+    // unit of the partial scores: 1, or 1 / (sq sk) after a rescaled staging
+    float unit_qk = 1.f;
+    if constexpr (!kBf16) {
+        const int4 ov = *reinterpret_cast<const int4*>(sh_over);
+        if (ov.x | ov.y | ov.z | ov.w) unit_qk = restage_qk();
+    }
 
     // ---- 2. partial scores S_c on MFMA.  Each wave owns one 16-row block
     // and up to 8 column tiles; the row block's A operand is read once per
@@ -858,9 +1005,10 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
             for (int r = 0; r < 4; ++r) {
                 const int i = rb * 16 + lk * 4 + r;
                 const int e = i * NK + j;
+                const float v = kBf16 ? acc[r] : acc[r] * unit_qk;
                 if (n > 1)
-                    st_xb<XL>(acc[r], rpart, ((e >> 8) * (n * 256) + c * 256 + (e & 255)) * 4);
-                else S[i * g.sstr + j] = acc[r];
+                    st_xb<XL>(v, rpart, ((e >> 8) * (n * 256) + c * 256 + (e & 255)) * 4);
+                else S[i * g.sstr + j] = v;
             }
         };
         auto run = [&](auto nt_tag) {
@@ -875,8 +1023,8 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
             const uint16_t* kh = reinterpret_cast<const uint16_t*>(smem + g.k_off) +
                                  (c0 * 16 + lr) * g.kstr + lk * 8;
             const int ql_d = (g.ql_off - g.q_off) / 2, kl_d = (g.kl_off - g.k_off) / 2;
-            mma_bf16<NT, kSplit, kSplit>(qh, qh + ql_d, kh, kh + kl_d, bstep_rows * g.kstr, dc,
-                                         acc);
+            mma16<VT, NT, kSplit, kSplit>(qh, qh + ql_d, kh, kh + kl_d, bstep_rows * g.kstr, dc,
+                                          acc);
 #pragma unroll
             for (int u = 0; u < NT; ++u)
                 if (u < cnt) store(u, acc[u]);
@@ -1199,6 +1347,10 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
         for (int u = 0; u < kKV; ++u)
             if (u < ckv) store_v(r0 + u * rstep, bv[u]);
     }
+    if constexpr (!kBf16) {
+        const bool over = __ballot(!(big_v < kF16Range)) != 0;  // NaN counts as over
+        if (lane == 0) sh_over[4 + wave] = over;
+    }
     __syncthreads();
 
     // ---- 4. softmax of scale * S: T = 16, 8 or 4 consecutive threads per
@@ -1233,15 +1385,18 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
             l += dpp<kDppQuadXor2>(l);
             if constexpr (TT >= 8) l += dpp<kDppRowHalfMirror>(l);
             if constexpr (TT >= 16) l += dpp<kDppRowMirror>(l);
-            const float inv = row_ok ? 1.0f / l : 0.f;
+            // fp32: P scaled by 2^15 (exact; every p <= 1 converts, and small
+            // p keep their bits), undone with the output
+            const float inv = row_ok ? (kBf16 ? 1.0f : 32768.0f) / l : 0.f;
 #pragma unroll
             for (int u = 0; u < W; u += 2) {
                 const float p0 = v[u] * inv, p1 = v[u + 1] * inv;
                 uint16_t* ph = reinterpret_cast<uint16_t*>(smem + g.p_off);
-                const uint32_t h = pack_bf16x2(p0, p1);
+                uint32_t h, lo;
+                if constexpr (kBf16) split2_bf16(p0, p1, h, lo);
+                else split2_f16(p0, p1, h, lo);
                 *reinterpret_cast<uint32_t*>(&ph[i * g.pstr + j0 + u]) = h;
-                *reinterpret_cast<uint32_t*>(&ph[(MQ + i) * g.pstr + j0 + u]) =
-                    pack_bf16x2(p0 - __uint_as_float(h << 16), p1 - __uint_as_float(h & 0xffff0000u));
+                *reinterpret_cast<uint32_t*>(&ph[(MQ + i) * g.pstr + j0 + u]) = lo;
             }
         };
         using std::integral_constant;
@@ -1270,6 +1425,30 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
     }
     __syncthreads();
 
+    // fp32: V staged again, scaled, when a V value is outside the fp16
+    // split's range (rare; see restage_qk); unit_o undoes P's 2^15 and V's
+    // scale in the output
+    float unit_o = 1.f;
+    if constexpr (!kBf16) {
+        unit_o = 1.0f / 32768.0f;
+        const int4 ov = *reinterpret_cast<const int4*>(sh_over + 4);
+        if (ov.x | ov.y | ov.z | ov.w) {
+            float mv = 0.f;
+            if (r0 < rstep)
+#pragma unroll 1
+                for (int row = r0; row < NK; row += rstep) mv = max_finite4(mv, load_row(rv, row));
+            slice_max(mv, 0.f, 0);
+            mv = max4(0);
+            const float sv = pow2_scale(mv);
+            if (r0 < rstep)
+#pragma unroll 1
+                for (int row = r0; row < NK; row += rstep)
+                    store_v(row, Raw4<T>::ld_buf(rv, lane_ok ? (row * D + d) * es : kOob), sv);
+            __syncthreads();
+            unit_o *= pow2_unit(mv);
+        }
+    }
+
     // ---- 5. O[:, slice] = P V[:, slice] on MFMA: each wave owns one 16-row
     // block and every (4 / nrb)-th 16-dim tile, 8 tiles at a time
     {
@@ -1292,8 +1471,8 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
                 const uint16_t* ph = reinterpret_cast<const uint16_t*>(smem + g.p_off) +
                                      (rb * 16 + lr) * g.pstr + lk * 8;
                 const uint16_t* vb = reinterpret_cast<const uint16_t*>(smem + g.v_off) + tc * 16;
-                mma_bf16_vt<NT, kVlo>(ph, ph + MQ * g.pstr, vb, (g.vl_off - g.v_off) / 2, g.vstr,
-                                      step, NK, acc);
+                mma16_vt<VT, NT, kVlo>(ph, ph + MQ * g.pstr, vb, (g.vl_off - g.v_off) / 2, g.vstr,
+                                       step, NK, acc);
 #pragma unroll
                 for (int u = 0; u < NT; ++u) {
                     if (u >= left) break;
@@ -1306,8 +1485,8 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
                             __builtin_amdgcn_raw_buffer_store_b16(
                                 __builtin_bit_cast(uint16_t, (__bf16)acc[u][r]), ro, off, 0, 0);
                         else
-                            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(acc[u][r]), ro,
-                                                                  off, 0, 0);
+                            __builtin_amdgcn_raw_buffer_store_b32(
+                                __float_as_uint(acc[u][r] * unit_o), ro, off, 0, 0);
                     }
                 }
             };
@@ -1374,15 +1553,22 @@ hipError_t fused_dispatch(const FusedArgs& a, int pek, int form, int lds, hipStr
 #undef ATN_FUSED_PE
 }
 
-// Occupancy of variant (T, XL): the encoded variants use the most
-// registers, so the smallest figure over their load forms is safe for every
-// variant.
+// Occupancy of variant (T, XL): the smallest figure over every encoding and
+// load form, so that the plan's residency holds for whichever variant a
+// call launches.
+template <typename T, bool XL, int PEK>
+int fused_per_cu_pek(int lds) {
+    int m = per_cu_t<T, PEK, XL, 0>(lds);
+    m = std::min(m, per_cu_t<T, PEK, XL, 1>(lds));
+    m = std::min(m, per_cu_t<T, PEK, XL, 2>(lds));
+    return std::min(m, per_cu_t<T, PEK, XL, 3>(lds));
+}
 template <typename T, bool XL>
 int fused_per_cu_forms(int lds) {
-    int m = per_cu_t<T, kPeRopeHalf, XL, 0>(lds);
-    m = std::min(m, per_cu_t<T, kPeRopeHalf, XL, 1>(lds));
-    m = std::min(m, per_cu_t<T, kPeRopeHalf, XL, 2>(lds));
-    return std::min(m, per_cu_t<T, kPeRopeHalf, XL, 3>(lds));
+    return std::min(std::min(fused_per_cu_pek<T, XL, kPeNone>(lds),
+                             fused_per_cu_pek<T, XL, kPeRopeInterleaved>(lds)),
+                    std::min(fused_per_cu_pek<T, XL, kPeRopeHalf>(lds),
+                             fused_per_cu_pek<T, XL, kPeSinusoidal>(lds)));
 }
 
 }  // namespace

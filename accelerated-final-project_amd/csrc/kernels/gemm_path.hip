@@ -187,23 +187,6 @@ template <int Ctrl>
 __device__ __forceinline__ float dppb(float v) {
     return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), Ctrl, 0xF, 0xF, true));
 }
-// max of two floats as one v_max_f32: fmaxf's IEEE semantics make the
-// compiler canonicalize both operands first (two more instructions); the
-// values here are never signalling NaNs
-__device__ __forceinline__ float vmaxf(float a, float b) {
-    float d;
-    asm("v_max_f32 %0, %1, %2" : "=v"(d) : "v"(a), "v"(b));
-    return d;
-}
-
-// max(m, |a|, |b|) as one v_max3_f32 with absolute-value modifiers (the
-// running magnitude maximum of the fused K encoding)
-__device__ __forceinline__ float vmax3abs(float m, float a, float b) {
-    float d;
-    asm("v_max3_f32 %0, %1, |%2|, |%3|" : "=v"(d) : "v"(m), "v"(a), "v"(b));
-    return d;
-}
-
 // Max / sum over each half-wave (lanes with the same lane / 32): DPP within
 // quads, 8 and 16 lanes, then the 16-lane hop by ds_swizzle.
 __device__ __forceinline__ float half_max(float v) {

@@ -263,7 +263,9 @@ int atn_attention_fwd_noalloc_ex(int dtype, const void *Q, const void *K, const 
  * Scratch is bounded: a call whose scratch would exceed its cap -- the
  * caller's workspace_bytes, or 1 GiB for the library's own workspace -- runs
  * in chunks of consecutive (batch, head) pairs, or of query rows of one head,
- * that fit; this query never reports more than the cap. */
+ * that fit, and this query then reports the largest chunk's need.  Only a
+ * shape whose single query row of one head exceeds the cap reports its full
+ * need, above the cap: such a call fails with ATN_ERR_WORKSPACE. */
 size_t atn_attention_workspace_bytes(int dtype, int batch, int heads, int len_q, int len_k,
                                      int head_d, const atn_pe_desc *pe);
 
@@ -298,6 +300,72 @@ int atn_attention_path_ex(int dtype, int batch, int heads, int len_q, int len_k,
 
 /* Number of visible HIP devices (0 when none); never aborts. */
 int atn_device_count(void);
+
+/* ==================== tuning, test controls and introspection ====================
+ * None of these has a counterpart in the reference (whose launchers take no
+ * options).  They exist for measurement and tests; a program that never
+ * calls them gets the library's own choices.  The library reads no
+ * environment variables. */
+
+/* Process-wide overrides, applied to calls made after the change.  Zero
+ * fields keep the library's choice. */
+typedef struct atn_tuning {
+    int fused_rows;        /* single-launch kernel: query rows per row group (16, 32, 48 or 64) */
+    int fused_dc;          /* single-launch kernel: D-slice width (a multiple of 32) */
+    int fused_exchange;    /* 1: one gather, 2: reduce-scatter + all-gather */
+    int fused_xcd;         /* 1: exchange inside one XCD's L2, 2: at device scope */
+    int no_fused;          /* nonzero: never the single-launch kernel (the other paths) */
+    int gemm_fused_k;      /* long-sequence path: 1 K's encoding inside the QK^T GEMM
+                              wherever it can run there, 2 never */
+    int workspace_cap_mib; /* cap of the library's own workspace before a call is chunked
+                              (default 1024) */
+    int model_cus;         /* planning without a device (size and path queries): CU count
+                              (default 256) */
+    int model_xccs;        /* ... and XCD count (default 8) */
+    int preset_status;     /* test only: nonzero makes every single-launch call start with
+                              its workspace's status word set, as a timed-out call leaves
+                              it, so its workgroups take the fail-closed exit (no wait is
+                              entered) */
+} atn_tuning;
+/* Replaces the overrides (NULL: all zero) and drops cached plans.  Plans
+ * that a forced setting makes impossible fall back to the library's
+ * choice. */
+int atn_set_tuning_ex(const atn_tuning *t);
+int atn_get_tuning_ex(atn_tuning *t);
+
+/* Plan of the single-launch kernel for this shape on the current device
+ * (without a device: the atn_tuning model, default 256 CUs in 8 XCDs).
+ * Returns 1 and fills the fields when the shape runs on that kernel, 0 when
+ * it does not, or a negative status.  Exchanges inside one XCD's L2 are
+ * planned only on a device that reports 8 XCDs and a CU count divisible by
+ * 8 (a whole MI355X, not a partition of it). */
+typedef struct atn_fused_plan_info {
+    int rows;       /* query rows per row group */
+    int dc;         /* D-slice width */
+    int nchunk;     /* slices per row group */
+    int gather1;    /* 1: one-gather exchange, 0: reduce-scatter + all-gather (or none) */
+    int xcd;        /* 1: exchange inside one XCD's L2 */
+    int workgroups; /* grid size */
+    int lds;        /* LDS bytes per workgroup */
+} atn_fused_plan_info;
+int atn_fused_plan_ex(int dtype, int batch, int heads, int len_q, int len_k, int head_d,
+                      const atn_pe_desc *pe, atn_fused_plan_info *info);
+
+/* Synchronous drop-in calls that were run a second time without the
+ * single-launch kernel after its wait timed out (each such rerun also
+ * prints one line to stderr).  reset != 0 sets the count back to 0. */
+long atn_rerun_count(int reset);
+
+/* Device memory the library holds on the current device: live workspaces
+ * and tables, and superseded buffers it keeps because work captured into a
+ * HIP graph may still use them. */
+size_t atn_retained_bytes_ex(void);
+
+/* Synchronizes the current device and frees the superseded buffers.  A HIP
+ * graph captured before a workspace or table it used was superseded must
+ * not be replayed afterwards.  Buffers that no captured work used are freed
+ * as soon as they are superseded. */
+int atn_release_ex(void);
 
 #ifdef __cplusplus
 }

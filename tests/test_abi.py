@@ -131,17 +131,15 @@ def test_workspace_bytes(am):
 
 @pytest.mark.parametrize("dtype,shape", [(0, (1, 4, 64, 64, 2048)), (0, (1, 16, 64, 64, 512)),
                                          (0, (1, 1, 16, 16, 8192)), (1, (1, 4, 32, 128, 8192))])
-def test_workspace_bytes_bound_every_plan(am, monkeypatch, dtype, shape):
+def test_workspace_bytes_bound_every_plan(am, tuner, dtype, shape):
     """The size query reports the largest workspace of every single-launch
     plan it could take, so that a plan forced through the tuning overrides
     (or chosen for a device of another capacity) never needs more."""
     base = am.workspace_bytes(dtype, *shape)
     assert base > 0
-    for rows, dc, x in [("16", "32", "gather"), ("16", "32", "rsag"), ("32", "64", "rsag"),
-                        ("64", "128", "rsag"), ("16", "256", "gather")]:
-        monkeypatch.setenv("ATN_FUSED_ROWS", rows)
-        monkeypatch.setenv("ATN_FUSED_DC", dc)
-        monkeypatch.setenv("ATN_FUSED_EXCHANGE", x)
+    for rows, dc, x in [(16, 32, "gather"), (16, 32, "rsag"), (32, 64, "rsag"),
+                        (64, 128, "rsag"), (16, 256, "gather")]:
+        tuner.set(fused_rows=rows, fused_dc=dc, fused_exchange=x)
         assert am.workspace_bytes(dtype, *shape) == base, (rows, dc, x)
 
 
@@ -216,7 +214,7 @@ def test_python_binding_checks_shapes(am):
     assert hip_rt.bf16_bits_to_f32(hip_rt.f32_to_bf16_bits(np.float32([1.5])))[0] == 1.5
 
 
-def test_workspace_bytes_bounded_by_the_cap(am, monkeypatch):
+def test_workspace_bytes_bounded_by_the_cap(am, tuner):
     """The size query never asks for more than the library's scratch cap
     (1 GiB by default): a larger shape runs in chunks of heads or query rows,
     and the query reports the largest chunk's need."""
@@ -224,7 +222,7 @@ def test_workspace_bytes_bounded_by_the_cap(am, monkeypatch):
     assert 0 < big <= 1 << 30
     small = am.workspace_bytes(1, 1, 4, 512, 512, 128)
     assert small < 1 << 30
-    monkeypatch.setenv("ATN_WORKSPACE_CAP_MIB", "1")
+    tuner.set(workspace_cap_mib=1)
     assert am.workspace_bytes(1, 1, 4, 512, 512, 128) <= 1 << 20
     assert am.workspace_bytes(1, 1, 64, 8192, 8192, 128) <= 1 << 20
 
@@ -240,3 +238,67 @@ def test_torch_and_library_share_one_hip_runtime():
     r = _child(code)
     assert r.returncode == 0, r.stderr[-2000:]
     assert r.stdout.split()[0] == "1", r.stdout
+
+
+def test_tuning_round_trip_and_plan_overrides(am, tuner):
+    """atn_set_tuning_ex / atn_get_tuning_ex round trip; a forced plan is
+    taken where it is possible, an impossible one falls back to the
+    planner's choice; the reset restores the default plan."""
+    default = am.fused_plan(0, 1, 4, 64, 64, 2048)
+    assert default is not None and default["rows"] == 16
+    tuner.set(fused_rows=32, fused_exchange="rsag", fused_xcd="device")
+    t = am.get_tuning()
+    assert (t.fused_rows, t.fused_exchange, t.fused_xcd) == (32, 2, 2)
+    p = am.fused_plan(0, 1, 4, 64, 64, 2048)
+    assert (p["rows"], p["gather1"], p["xcd"]) == (32, 0, 0)
+    tuner.set(fused_rows=48)  # 48-row groups only for a padded head of 33-48 rows
+    assert am.fused_plan(0, 1, 4, 64, 64, 2048)["rows"] in (16, 32, 64)
+    tuner.clear()
+    assert am.fused_plan(0, 1, 4, 64, 64, 2048) == default
+    tuner.set(no_fused=True)
+    assert am.fused_plan(0, 1, 4, 64, 64, 2048) is None
+    assert am.path(0, 1, 4, 64, 64, 2048) == am.ATN_PATH_SPLIT_D
+
+
+@pytest.mark.parametrize("cus,xccs", [(32, 1), (64, 2), (128, 4), (256, 4), (252, 8), (256, 8)])
+def test_xcd_local_plans_need_the_whole_chip(am, tuner, cus, xccs):
+    """Exchanges inside one XCD's L2 assume 8 XCDs dealt workgroup ids round
+    robin; a partitioned MI355X (a device of 1, 2 or 4 XCDs) or a CU count
+    not divisible by 8 gets device-scope plans only, also when such a plan
+    is forced."""
+    tuner.set(model_cus=cus, model_xccs=xccs)
+    whole = cus % 8 == 0 and xccs == 8
+    for shape in [(1, 4, 64, 64, 2048), (1, 4, 64, 64, 512), (1, 8, 32, 64, 1024),
+                  (1, 1, 16, 16, 8192)]:
+        p = am.fused_plan(0, *shape)
+        assert p is not None, shape
+        assert p["workgroups"] <= cus * 8
+        if not whole:
+            assert p["xcd"] == 0, (shape, p)
+    tuner.set(fused_xcd="xcd")
+    p = am.fused_plan(0, 1, 4, 64, 64, 2048)
+    assert p["xcd"] == (1 if whole else 0)
+
+
+def test_library_reads_no_environment(am):
+    """Tuning is an API call, never an environment variable: a child process
+    with the former override variables set plans exactly as without them."""
+    code = ("import attn_mi355x as am; p = am.fused_plan(0, 1, 4, 64, 64, 2048); "
+            "print(p['rows'], p['dc'], p['gather1'], p['xcd'], "
+            "am.path(0, 1, 4, 64, 64, 2048), am.workspace_bytes(1, 1, 64, 8192, 8192, 128))")
+    plain = _child(code)
+    assert plain.returncode == 0, plain.stderr[-2000:]
+    env_code = ("import os; os.environ.update(ATN_FUSED_ROWS='64', ATN_FUSED_DC='512', "
+                "ATN_FUSED_EXCHANGE='rsag', ATN_FUSED_XCD='0', ATN_F32_FULL='1', "
+                "ATN_WORKSPACE_CAP_MIB='1', ATN_FUSED_PRESET_STATUS='1'); " + code)
+    forced = _child(env_code)
+    assert forced.returncode == 0, forced.stderr[-2000:]
+    assert forced.stdout == plain.stdout
+    src = open(os.path.join(ROOT, "accelerated-final-project_amd", "csrc", "host",
+                            "attn_api.cpp")).read()
+    assert "getenv" not in src
+
+
+def test_rerun_counter_starts_at_zero(am):
+    assert am.rerun_count() == 0
+    assert am.rerun_count(reset=True) == 0

@@ -123,14 +123,14 @@ def test_fused_with_encodings_bf16(am, dev, pe):
 @pytest.mark.parametrize("xcd", ["0", "1", ""], ids=["device", "xcd", "default"])
 @pytest.mark.parametrize("shape", [(1, 4, 64, 64, 2048), (1, 2, 130, 70, 256)],
                          ids=lambda s: "x".join(map(str, s)))
-def test_graph_replays_match_eager(am, dev, monkeypatch, shape, xcd):
+def test_graph_replays_match_eager(am, dev, tuner, shape, xcd):
     """Captured HIP graph of three calls, replayed four times with eager work
     and synchronizations in between; every replay must equal the eager
     result bit for bit (the single-launch kernel keeps its barrier epochs in
     device memory, so replayed arguments stay valid)."""
     import hip_rt
     if xcd:
-        monkeypatch.setenv("ATN_FUSED_XCD", xcd)
+        tuner.set(fused_xcd={"0": "device", "1": "xcd"}[xcd])
     B, Hh, Lq, Lk, D = shape
     print(f"[case] graph replay {shape} xcd={xcd or 'default'}", flush=True)
     (q, k, v), (Q, K, V) = H.device_inputs((B, Hh, Lq, D), (B, Hh, Lk, D), 91)
@@ -171,8 +171,7 @@ def test_graph_replays_match_eager(am, dev, monkeypatch, shape, xcd):
                                             ((1, 3, 40, 72, 1024), "f32", None),
                                             ((1, 2, 48, 96, 1024), "bf16", "rope_half")],
                          ids=["cfg2", "ragged", "bf16rope"])
-def test_fused_row_groups_and_exchanges(am, dev, monkeypatch, rows, exchange, xcd, shape, dtype,
-                                        pe):
+def test_fused_row_groups_and_exchanges(am, dev, tuner, rows, exchange, xcd, shape, dtype, pe):
     """Every row-group size and both exchange forms (one gather; reduce-scatter
     + all-gather), each at device scope (xcd 0) and inside one XCD's L2 (xcd
     1; the ragged shape's 9 row groups leave XCDs with different counts and
@@ -180,9 +179,8 @@ def test_fused_row_groups_and_exchanges(am, dev, monkeypatch, rows, exchange, xc
     oracle's result, and repeated calls on one workspace are bit-identical."""
     import hip_rt
     if rows:
-        monkeypatch.setenv("ATN_FUSED_ROWS", rows)
-        monkeypatch.setenv("ATN_FUSED_EXCHANGE", exchange)
-        monkeypatch.setenv("ATN_FUSED_XCD", xcd)
+        tuner.set(fused_rows=int(rows), fused_exchange=exchange,
+                  fused_xcd={"0": "device", "1": "xcd"}[xcd])
     B, Hh, Lq, Lk, D = shape
     print(f"[case] fused rows={rows or 'default'} exchange={exchange or 'default'} "
           f"xcd={xcd or 'default'} {dtype} {shape} pe={pe}", flush=True)
@@ -229,20 +227,20 @@ def test_fused_row_groups_and_exchanges(am, dev, monkeypatch, rows, exchange, xc
 # XL: a group's arrival counters one per line (at most 32 row groups), or
 # packed.
 _LAYOUTS = [
-    ((1, 4, 64, 64, 2048), {"ATN_FUSED_ROWS": "16", "ATN_FUSED_EXCHANGE": "rsag",
-                            "ATN_FUSED_XCD": "0"}),  # device, spread
-    ((1, 1, 16, 16, 8192), {"ATN_FUSED_ROWS": "16", "ATN_FUSED_DC": "64",
-                            "ATN_FUSED_EXCHANGE": "rsag", "ATN_FUSED_XCD": "0"}),  # 128 slices
-    ((1, 36, 64, 128, 448), {"ATN_FUSED_ROWS": "64", "ATN_FUSED_EXCHANGE": "rsag",
-                             "ATN_FUSED_XCD": "0"}),  # device, 36 groups
-    ((1, 4, 64, 64, 2048), {"ATN_FUSED_ROWS": "16", "ATN_FUSED_EXCHANGE": "gather",
-                            "ATN_FUSED_XCD": "1"}),  # XL, spread
-    ((1, 36, 64, 128, 448), {"ATN_FUSED_ROWS": "64", "ATN_FUSED_EXCHANGE": "rsag",
-                             "ATN_FUSED_XCD": "1"}),  # XL, 36 groups
+    ((1, 4, 64, 64, 2048), dict(fused_rows=16, fused_exchange="rsag",
+                                fused_xcd="device")),  # device, spread
+    ((1, 1, 16, 16, 8192), dict(fused_rows=16, fused_dc=64, fused_exchange="rsag",
+                                fused_xcd="device")),  # 128 slices
+    ((1, 36, 64, 128, 448), dict(fused_rows=64, fused_exchange="rsag",
+                                 fused_xcd="device")),  # device, 36 groups
+    ((1, 4, 64, 64, 2048), dict(fused_rows=16, fused_exchange="gather",
+                                fused_xcd="xcd")),  # XL, spread
+    ((1, 36, 64, 128, 448), dict(fused_rows=64, fused_exchange="rsag",
+                                 fused_xcd="xcd")),  # XL, 36 groups
 ]
 
 
-def test_fused_sync_word_layouts_share_a_workspace(am, dev, monkeypatch):
+def test_fused_sync_word_layouts_share_a_workspace(am, dev, tuner):
     """The exchange's sync words are laid out one per cache line or packed,
     depending on the plan; calls of every layout, alternating on one
     workspace (sized for the largest), each give the oracle's result three
@@ -258,17 +256,14 @@ def test_fused_sync_word_layouts_share_a_workspace(am, dev, monkeypatch):
         cases.append((shape, env, ins, ref))
     need = 0
     for shape, env, _, _ in cases:
-        for k, v in env.items():
-            monkeypatch.setenv(k, v)
+        tuner.set(**env)
         need = max(need, am.workspace_bytes(0, *shape))
-        for k in env:
-            monkeypatch.delenv(k)
+        tuner.clear()
     ws = hip_rt.DeviceArray((need // 4,), "f32", fill=0)
     for rnd in range(3):
         for shape, env, (q, k_, v), ref in cases:
             print(f"[case] sync word layout round {rnd} {shape} {env}", flush=True)
-            for k, val in env.items():
-                monkeypatch.setenv(k, val)
+            tuner.set(**env)
             B, Hh, Lq, Lk, D = shape
             assert am.path(0, B, Hh, Lq, Lk, D) == am.ATN_PATH_FUSED_SMALL
             out = H.empty((B, Hh, Lq, D))
@@ -277,21 +272,18 @@ def test_fused_sync_word_layouts_share_a_workspace(am, dev, monkeypatch):
             assert am.sync_status(ws, B, Hh) == 0
             n, mabs, mrel = H.check_f32(out.numpy(), ref)
             assert n == 0, f"{shape} {env}: {n} mismatches, max abs {mabs}, max rel {mrel}"
-            for k in env:
-                monkeypatch.delenv(k)
+            tuner.clear()
 
 
 @pytest.mark.parametrize("rows,exchange", [("64", "rsag"), ("", "")], ids=["rows64-rsag", "default"])
-def test_fused_uneven_slices(am, dev, monkeypatch, rows, exchange):
+def test_fused_uneven_slices(am, dev, tuner, rows, exchange):
     """36 heads with 7 D-slices each: with 64-row groups and slices of 64 the
     reduce-scatter owns 1171 entries per workgroup, so a thread reduces
     several entries (4-byte words); by default the planner makes its own
     choice."""
     import hip_rt
     if rows:
-        monkeypatch.setenv("ATN_FUSED_ROWS", rows)
-        monkeypatch.setenv("ATN_FUSED_EXCHANGE", exchange)
-        monkeypatch.setenv("ATN_FUSED_DC", "64")
+        tuner.set(fused_rows=int(rows), fused_exchange=exchange, fused_dc=64)
     B, Hh, Lq, Lk, D = 1, 36, 64, 128, 448
     print(f"[case] fused uneven slices rows={rows or 'default'}", flush=True)
     assert am.path(0, B, Hh, Lq, Lk, D) == am.ATN_PATH_FUSED_SMALL
@@ -335,7 +327,7 @@ def test_fused_planner_shapes(am, dev, shape, dtype):
         assert n == 0, f"normwise rel {nrel}, max abs {mabs}"
 
 
-def test_fused_forced_plan_fits_default_workspace(am, dev, monkeypatch):
+def test_fused_forced_plan_fits_default_workspace(am, dev, tuner):
     """A plan forced to narrow slices (16-row groups, 32-dim slices, 1024
     workgroups, several per CU) runs in the workspace the size query reported
     without overrides, and gives the oracle's result."""
@@ -344,9 +336,7 @@ def test_fused_forced_plan_fits_default_workspace(am, dev, monkeypatch):
     print("[case] fused forced narrow plan in the default workspace", flush=True)
     (q, k, v), (Q, K, V) = H.device_inputs((B, Hh, Lq, D), (B, Hh, Lk, D), 613)
     ws = _ws(am, 0, B, Hh, Lq, Lk, D)
-    monkeypatch.setenv("ATN_FUSED_ROWS", "16")
-    monkeypatch.setenv("ATN_FUSED_DC", "32")
-    monkeypatch.setenv("ATN_FUSED_EXCHANGE", "rsag")
+    tuner.set(fused_rows=16, fused_dc=32, fused_exchange="rsag")
     out = H.empty(Q.shape)
     am.attention_ex(q, k, v, out, workspace=ws)
     hip_rt.synchronize()
@@ -392,7 +382,7 @@ def test_fused_planner_shapes_with_encoding(am, dev, shape, dtype, pe):
         assert n == 0, f"normwise rel {nrel}, max abs {mabs}"
 
 
-def test_fused_exchange_scopes_share_one_workspace(am, dev, monkeypatch):
+def test_fused_exchange_scopes_share_one_workspace(am, dev, tuner):
     """One workspace, calls alternating between device-scope and XCD-local
     plans of different shapes (different slice counts per row group, so the
     XCD-local counters are shared by plans of different sizes) and both
@@ -412,9 +402,8 @@ def test_fused_exchange_scopes_share_one_workspace(am, dev, monkeypatch):
              ("0", "rsag", "16"), ("1", "rsag", "16"), ("1", "gather", "32")]
     for rnd in range(3):
         for xcd, ex, rows in plans:
-            monkeypatch.setenv("ATN_FUSED_XCD", xcd)
-            monkeypatch.setenv("ATN_FUSED_EXCHANGE", ex)
-            monkeypatch.setenv("ATN_FUSED_ROWS", rows)
+            tuner.set(fused_xcd={"0": "device", "1": "xcd"}[xcd], fused_exchange=ex,
+                      fused_rows=int(rows))
             for shp, ins, ref in cases:
                 print(f"[case] shared workspace round {rnd} xcd={xcd} {ex} rows={rows} {shp}",
                       flush=True)
@@ -434,7 +423,7 @@ def test_fused_exchange_scopes_share_one_workspace(am, dev, monkeypatch):
 
 @pytest.mark.parametrize("xcd,exchange", [("0", "gather"), ("0", "rsag"), ("1", "gather"),
                                           ("1", "rsag")])
-def test_fail_closed_then_recovers(am, dev, monkeypatch, xcd, exchange):
+def test_fail_closed_then_recovers(am, dev, tuner, xcd, exchange):
     """The fail-closed path, forced from the host: the workspace's status word
     is preset (as a timed-out call would leave it), so every workgroup of the
     next call takes the fail-closed exit -- no wait is entered, every
@@ -443,9 +432,7 @@ def test_fail_closed_then_recovers(am, dev, monkeypatch, xcd, exchange):
     and moving the epochs on); the call after it gives the oracle's result,
     on device-scope and XCD-local plans, one gather and reduce-scatter."""
     import hip_rt
-    monkeypatch.setenv("ATN_FUSED_XCD", xcd)
-    monkeypatch.setenv("ATN_FUSED_EXCHANGE", exchange)
-    monkeypatch.setenv("ATN_FUSED_ROWS", "16")
+    tuner.set(fused_xcd={"0": "device", "1": "xcd"}[xcd], fused_exchange=exchange, fused_rows=16)
     B, Hh, Lq, Lk, D = 1, 4, 64, 64, 2048
     print(f"[case] fail closed xcd={xcd} {exchange}", flush=True)
     (q, k, v), (Q, K, V) = H.device_inputs((B, Hh, Lq, D), (B, Hh, Lk, D), 808)
@@ -477,14 +464,15 @@ def test_fail_closed_then_recovers(am, dev, monkeypatch, xcd, exchange):
 
 @pytest.mark.parametrize("dtype,shape", [("f32", (1, 4, 64, 64, 2048)), ("bf16", (1, 4, 32, 128, 8192))],
                          ids=["cfg2-f32", "cfg3-bf16"])
-def test_dropin_reruns_after_a_failed_exchange(am, dev, monkeypatch, dtype, shape):
+def test_dropin_reruns_after_a_failed_exchange(am, dev, tuner, dtype, shape):
     """A synchronous drop-in whose single-launch call fails closed -- forced
-    from the host: ATN_FUSED_PRESET_STATUS presets the call's status word as
-    a timed-out call leaves it, so every workgroup takes the fail-closed exit
-    and no wait is entered -- recovers the workspace and runs the call once
-    more without the single-launch kernel: the process goes on and the
-    output is the oracle's.  Without the switch the next drop-in takes the
-    single-launch kernel again."""
+    from the host: the test control atn_tuning.preset_status presets the
+    call's status word as a timed-out call leaves it, so every workgroup
+    takes the fail-closed exit and no wait is entered -- recovers the
+    workspace and runs the call once more without the single-launch kernel:
+    the process goes on, the output is the oracle's and the rerun is
+    counted.  Without the control the next drop-in takes the single-launch
+    kernel again."""
     import hip_rt
     B, Hh, Lq, Lk, D = shape
     print(f"[case] drop-in rerun {dtype} {shape}", flush=True)
@@ -502,10 +490,13 @@ def test_dropin_reruns_after_a_failed_exchange(am, dev, monkeypatch, dtype, shap
         assert n == 0, (n, a, b)
         return out.numpy()
 
-    monkeypatch.setenv("ATN_FUSED_PRESET_STATUS", "1")
+    am.rerun_count(reset=True)
+    tuner.set(preset_status=True)
     rerun = call()
-    monkeypatch.delenv("ATN_FUSED_PRESET_STATUS")
+    tuner.clear()
+    assert am.rerun_count(reset=True) == 1
     again = call()
+    assert am.rerun_count() == 0
     assert am.sync_status(None, B, Hh) == 0
     if dtype == "f32":  # the single-launch kernel and the split-D pipeline agree to the bar only
         n, mabs, _ = H.check_f32(rerun, again)

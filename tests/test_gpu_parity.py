@@ -61,41 +61,107 @@ def test_sdpa_f32(am, dev, shape):
     assert np.array_equal(got, got2)
 
 
-@pytest.mark.parametrize("shape", [(1, 4, 64, 64, 512), (1, 4, 64, 64, 2048), (1, 4, 64, 64, 8192),
-                                   (1, 4, 32, 128, 2048)], ids=lambda s: "x".join(map(str, s)))
-def test_sdpa_f32_wider_logits(am, dev, shape):
-    """Inputs of sigma 1.5 (logits up to about +-10): the edge of the
-    single-launch kernel's fp32 envelope.  Its products keep about 16
-    significant bits (hi + lo bf16 parts, three products), so logit errors
-    grow with the logits' size; at sigma 2 (logits to about +-18) up to about
-    two elements in 10^4 exceed the 1e-4 bar, by up to 1.7e-4."""
+_WIDE_SHAPES = [(1, 4, 64, 64, 512), (1, 4, 64, 64, 2048), (1, 4, 64, 64, 8192),
+                (1, 4, 32, 128, 2048)]
+
+
+@pytest.mark.parametrize("sigma", [1.5, 2.0, 3.0])
+@pytest.mark.parametrize("shape", _WIDE_SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_sdpa_f32_wider_logits(am, dev, shape, sigma):
+    """Inputs of sigma 1.5, 2 and 3 (logits up to about +-10, +-18 and +-40)
+    on the default path (the single-launch kernel at these shapes): its fp32
+    products come from hi + lo fp16 parts (22 significant bits each, exact
+    products), so the 1e-4 bar holds whatever the logits' size.  At sigma 3
+    and D >= 2048 the oracle's own sequential float32 sums miss the bar
+    against the exact result (7, 233 and 8153 elements on these shapes, up to
+    6.7e-4: test_oracle.py::test_oracle_drift_at_wide_logits), so there an
+    element fails only if it misses the bar against the oracle and against
+    the exact float64 result; everywhere else the oracle alone is the
+    referee."""
     B, Hh, Lq, Lk, D = shape
-    print(f"[case] sdpa f32 sigma 1.5 {shape}", flush=True)
-    Q, K, V = H.rng_inputs((B, Hh, Lq, D), (B, Hh, Lk, D), seed=7 + D, sigma=1.5)
+    print(f"[case] sdpa f32 sigma {sigma} {shape}", flush=True)
+    assert am.path(0, B, Hh, Lq, Lk, D) == am.ATN_PATH_FUSED_SMALL
+    Q, K, V = H.rng_inputs((B, Hh, Lq, D), (B, Hh, Lk, D), seed=7 + D, sigma=sigma)
     got = _f32_call(am.attention_forward_optimized, Q, K, V)
     ref = oracle.attention(Q, K, V, nthreads=16)
-    n, mabs, _ = H.check_f32(got, ref)
-    assert n == 0, f"{n} mismatches, max abs {mabs}"
+    if D >= 2048 and sigma == 3.0:
+        n, mabs, mtruth = H.check_f32_or_truth(got, ref, H.sdpa64(Q, K, V))
+        assert n == 0, f"{n} mismatches, max abs {mabs} (oracle), {mtruth} (exact)"
+    else:
+        n, mabs, _ = H.check_f32(got, ref)
+        assert n == 0, f"{n} mismatches, max abs {mabs}"
 
 
-@pytest.mark.parametrize("shape", [(1, 4, 64, 64, 512), (1, 4, 64, 64, 2048), (1, 4, 64, 64, 8192),
-                                   (1, 4, 32, 128, 2048)], ids=lambda s: "x".join(map(str, s)))
-def test_sdpa_f32_full_precision_switch(am, dev, monkeypatch, shape):
-    """ATN_F32_FULL=1: fp32 calls take full fp32 products (the split-D
-    pipeline) instead of the single-launch kernel's hi + lo bf16 parts, so
-    inputs of sigma 3 (logits up to about +-40, outside that kernel's
-    envelope) meet the 1e-4 bar.  An element fails only if it misses the bar
-    against the oracle and against the exact float64 result (the oracle's own
-    float32 sums drift by up to 7e-4 at D = 8192 there)."""
+@pytest.mark.parametrize("shape", _WIDE_SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_sdpa_f32_split_d_wide_logits(am, dev, tuner, shape):
+    """The split-D pipeline (fp32 MFMA products; forced here with
+    atn_tuning.no_fused) at sigma 3, against the oracle with the exact
+    float64 result as second referee (the oracle's drift at D = 8192)."""
     B, Hh, Lq, Lk, D = shape
-    print(f"[case] sdpa f32 full precision, sigma 3 {shape}", flush=True)
-    monkeypatch.setenv("ATN_F32_FULL", "1")
+    print(f"[case] sdpa f32 split-D sigma 3 {shape}", flush=True)
+    tuner.set(no_fused=True)
     assert am.path(0, B, Hh, Lq, Lk, D) == am.ATN_PATH_SPLIT_D
     Q, K, V = H.rng_inputs((B, Hh, Lq, D), (B, Hh, Lk, D), seed=7 + D, sigma=3.0)
     got = _f32_call(am.attention_forward_optimized, Q, K, V)
     ref = oracle.attention(Q, K, V, nthreads=16)
     n, mabs, mtruth = H.check_f32_or_truth(got, ref, H.sdpa64(Q, K, V))
     assert n == 0, f"{n} mismatches, max abs {mabs} (oracle), {mtruth} (exact)"
+
+
+@pytest.mark.parametrize("exps", [(17, -17, 0), (-17, 17, 0), (0, 0, 19), (17, -17, 21),
+                                  (-9, -9, -9)],
+                         ids=["q-big", "k-big", "v-big", "all-big", "all-small"])
+@pytest.mark.parametrize("shape", [(1, 4, 64, 64, 2048), (1, 3, 40, 72, 1024),
+                                   (1, 2, 16, 128, 8192)], ids=lambda s: "x".join(map(str, s)))
+def test_sdpa_f32_outside_fp16_range(am, dev, shape, exps):
+    """The single-launch kernel's fp16 split needs |x| < 65504: a workgroup
+    whose Q/K or V slice holds a larger value stages that slice again scaled
+    by a power of two and multiplies the results back.  Head 1 of each call
+    has Q, K and V multiplied by 2^eq, 2^ek and 2^ev (the other heads stay
+    N(0,1), so both kinds of workgroup run in one call).  Scaling by powers
+    of two is exact, so attention(2^eq Q, 2^ek K, 2^ev V) = 2^ev attention(
+    2^eq Q, 2^ek K, V) in the oracle's float32 arithmetic too: the output of
+    head 1 is compared, in units of 2^ev, with the oracle on the unscaled V
+    (an absolute 1e-4 bar on outputs of magnitude 2^19 would be finer than
+    float32 itself).  Also small inputs (2^-9: many fp16 subnormal lo
+    parts)."""
+    B, Hh, Lq, Lk, D = shape
+    eq, ek, ev = exps
+    print(f"[case] sdpa f32 outside the fp16 range 2^{exps} {shape}", flush=True)
+    assert am.path(0, B, Hh, Lq, Lk, D) == am.ATN_PATH_FUSED_SMALL
+    Q, K, V = H.rng_inputs((B, Hh, Lq, D), (B, Hh, Lk, D), seed=31 + D)
+    Q[:, 1] *= np.float32(2.0 ** eq)
+    K[:, 1] *= np.float32(2.0 ** ek)
+    Vs = V.copy()
+    Vs[:, 1] *= np.float32(2.0 ** ev)
+    got = _f32_call(am.attention_forward_optimized, Q, K, Vs)
+    assert np.isfinite(got).all()
+    got[:, 1] *= np.float32(2.0 ** -ev)
+    ref = oracle.attention(Q, K, V, nthreads=16)
+    n, mabs, mrel = H.check_f32(got, ref)
+    assert n == 0, f"{n} mismatches, max abs {mabs}, max rel {mrel}"
+
+
+def test_sdpa_f32_nonfinite_inputs_propagate(am, dev):
+    """An infinite query element makes its own output row non-finite, as in
+    the reference (exp(inf - inf) in its softmax); the other rows of that
+    row group, whose slice is then staged scaled by its largest finite
+    magnitude, and the other heads keep the bar.  A NaN value element makes
+    its output column NaN, as in the reference."""
+    B, Hh, Lq, Lk, D = 1, 4, 64, 64, 2048
+    print("[case] sdpa f32 non-finite inputs", flush=True)
+    Q, K, V = H.rng_inputs((B, Hh, Lq, D), (B, Hh, Lk, D), seed=77)
+    Q[0, 2, 5, 100] = np.inf
+    V[0, 1, 9, 33] = np.nan
+    got = _f32_call(am.attention_forward_optimized, Q, K, V)
+    ref = oracle.attention(Q, K, V, nthreads=16)
+    assert not np.isfinite(ref[0, 2, 5]).any() and not np.isfinite(got[0, 2, 5]).any()
+    assert np.isnan(ref[0, 1, :, 33]).all() and np.isnan(got[0, 1, :, 33]).all()
+    keep = np.ones((Hh, Lq, D), dtype=bool)
+    keep[2, 5, :] = False
+    keep[1, :, 33] = False
+    n, mabs, _ = H.check_f32(got[0][keep], ref[0][keep])
+    assert n == 0, mabs
 
 
 @pytest.mark.parametrize("shape", [(1, 1, 70, 1, 64), (1, 3, 65, 255, 40), (1, 8, 70, 1025, 64),
