@@ -1,6 +1,7 @@
 """Context numbers: this library next to PyTorch-ROCm on the same MI355X.
 
     python accelerated-final-project_amd/torch_compare.py [--iters 100] [--json out.json]
+        [--shapes cfg2,"ref hdim=512"] [--save DIR]
 
 The reference's PyTorch harness (final/benchmark_pytorch_wrapper.cu:25-130)
 times F.scaled_dot_product_attention ("optimized") and matmul -> softmax ->
@@ -14,7 +15,9 @@ with elementwise ops from tables built the way the reference builds its
 caches (final/rope.cu:20-40, final/sinusoidal.cu:838-855), then attends.
 
 The printed max |difference| against torch SDPA is context only; parity is
-established against the CPU oracle by the test suite.
+established against the CPU oracle by the test suite (--save writes each
+shape's inputs and this library's output as .npy files, which
+tests/test_gpu_torch_harness.py checks against the oracle).
 
 One HIP runtime.  This process hands torch's device pointers and stream to
 the library, which is only sound if both use the same HIP runtime.  torch's
@@ -94,7 +97,16 @@ def main():
     ap.add_argument("--iters", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--json", default="")
+    ap.add_argument("--shapes", default="",
+                    help="comma-separated shape names to run (default: all)")
+    ap.add_argument("--save", default="",
+                    help="directory for each shape's inputs and this library's output (.npy)")
     a = ap.parse_args()
+    wanted = [w.strip() for w in a.shapes.split(",") if w.strip()]
+    shapes = [sh for sh in SHAPES if not wanted or sh[0] in wanted]
+    if wanted and len(shapes) != len(wanted):
+        print(f"torch_compare.py: unknown shape in {wanted}", file=sys.stderr)
+        sys.exit(2)
 
     import torch
     import torch.nn.functional as F
@@ -129,7 +141,7 @@ def main():
 
     rows = []
     g = torch.Generator(device=dev).manual_seed(0)
-    for name, dt, B, H, Lq, Lk, D, pe in SHAPES:
+    for idx, (name, dt, B, H, Lq, Lk, D, pe) in enumerate(shapes):
         tdt = torch.float32 if dt == "f32" else torch.bfloat16
         sigma = 0.5 if pe == "sinusoidal" else 1.0
         Q = (torch.randn(B, H, Lq, D, device=dev, generator=g) * sigma).to(tdt)
@@ -193,6 +205,12 @@ def main():
                "ours_ms": t_ours, "torch_sdpa_ms": t_sdpa, "torch_naive_ms": t_naive,
                "ours_tflops": flops / t_ours / 1e9, "ours_gbs": alg_bytes / t_ours / 1e6,
                "speedup_vs_sdpa": t_sdpa / t_ours, "max_abs_diff_vs_sdpa": diff}
+        if a.save:
+            import numpy as np
+            os.makedirs(a.save, exist_ok=True)
+            for tag, t in (("Q", Q), ("K", K), ("V", V), ("out", out)):
+                np.save(os.path.join(a.save, f"{idx}_{tag}.npy"), t.float().cpu().numpy())
+            row["saved"] = f"{idx}_{{Q,K,V,out}}.npy"
         rows.append(row)
         print(f"{name:16s} {dt:4s} ours {t_ours:9.4f} ms  sdpa {t_sdpa:9.4f} ms  "
               f"naive {t_naive:9.4f} ms  x{t_sdpa / t_ours:6.2f} vs sdpa  "
