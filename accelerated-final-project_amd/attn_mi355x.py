@@ -52,6 +52,7 @@ ATN_ROPE_HALF = 1
 ATN_PATH_FUSED_SMALL = 1
 ATN_PATH_SPLIT_D = 2
 ATN_PATH_GEMM = 3
+ATN_PATH_FLASH = 4
 
 
 class PeDesc(ctypes.Structure):
@@ -71,7 +72,8 @@ class PeDesc(ctypes.Structure):
 class Tuning(ctypes.Structure):
     """atn_tuning (process-wide overrides for measurement and tests)."""
     _fields_ = [(n, ctypes.c_int) for n in (
-        "fused_rows", "fused_dc", "fused_exchange", "fused_xcd", "no_fused", "gemm_fused_k",
+        "fused_rows", "fused_dc", "fused_exchange", "fused_xcd", "no_fused", "no_flash",
+        "gemm_fused_k",
         "workspace_cap_mib", "model_cus", "model_xccs", "preset_status")]
 
 
@@ -180,13 +182,13 @@ _FUSED_K = {None: 0, "on": 1, "off": 2}
 
 
 def set_tuning(fused_rows: int = 0, fused_dc: int = 0, fused_exchange: str | None = None,
-               fused_xcd: str | None = None, no_fused: bool = False,
+               fused_xcd: str | None = None, no_fused: bool = False, no_flash: bool = False,
                gemm_fused_k: str | None = None, workspace_cap_mib: int = 0, model_cus: int = 0,
                model_xccs: int = 0, preset_status: bool = False) -> None:
     """atn_set_tuning_ex with named fields (every field not given is reset)."""
     t = Tuning(fused_rows, fused_dc, _EXCHANGE[fused_exchange], _SCOPE[fused_xcd],
-               int(no_fused), _FUSED_K[gemm_fused_k], workspace_cap_mib, model_cus,
-               model_xccs, int(preset_status))
+               int(no_fused), int(no_flash), _FUSED_K[gemm_fused_k], workspace_cap_mib,
+               model_cus, model_xccs, int(preset_status))
     st = lib().atn_set_tuning_ex(ctypes.byref(t))
     if st != ATN_OK:
         raise AtnError(st, "atn_set_tuning_ex")

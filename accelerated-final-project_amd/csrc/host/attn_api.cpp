@@ -99,6 +99,7 @@ struct PePlan {
     // the call may not take the single-launch kernel (a synchronous call's
     // second attempt after that kernel's exchange timed out)
     bool no_fused = false;
+    bool no_flash = false;  // nor the flash kernel (atn_tuning.no_flash)
 };
 
 int check_pe(const atn_pe_desc* pe, int D, PePlan* plan) {
@@ -739,6 +740,15 @@ size_t library_cap() {
     return mib > 0 ? (size_t)mib << 20 : (size_t)1 << 30;
 }
 
+// The flash kernel takes fp32 calls with head_d <= 256 (128 with an
+// encoding), head_d % 4 == 0 and 16-byte aligned bases (checked by the
+// caller), whose per-head Q and K/V byte offsets fit 32 bits.
+bool flash_ok(int dtype, const Shape& s, const PePlan& plan) {
+    const int64_t lim = (int64_t)1 << 31;
+    return !plan.no_flash && atn::flash_supported(dtype, plan.pek, s.D) &&
+           (int64_t)s.Lq * s.D * 4 < lim && (int64_t)s.Lk * s.D * 4 < lim;
+}
+
 // Scratch bytes of the path a call of shape s takes: fused (when planned and
 // vector-aligned), else GEMM (when planned and 16-byte aligned), else the
 // split-D pipeline.  vec / a16: the alignment of the call's pointers; pass
@@ -751,6 +761,7 @@ size_t path_need(int dtype, const Shape& s, const PePlan& plan, bool query_devic
     if (vec < 0 || a16 < 0)
         return std::max({fp.ok ? fp.bytes : (size_t)0, gp.ok ? gp.bytes : (size_t)0, split});
     if (fp.ok && vec) return fp.bytes;
+    if (a16 && flash_ok(dtype, s, plan)) return kSyncBytes;  // the flash kernel: no scratch
     if (gp.ok && a16) return gp.bytes;
     return split;
 }
@@ -814,10 +825,13 @@ int attention_run(int dtype, const void* Q, const void* K, const void* V, void* 
     const int vec_qk = (D % 4 == 0) && aligned(Q, va) && aligned(K, va);
     const int vec_vo = (D % 4 == 0) && aligned(V, va) && aligned(out, va);
     const bool use_fused = fd.ok && vec_qk && vec_vo;
-    const bool use_gemm = !use_fused && gp.ok && aligned(Q, 16) && aligned(K, 16) &&
+    const bool a16 = aligned(Q, 16) && aligned(K, 16) && aligned(V, 16) && aligned(out, 16);
+    const bool use_flash = !use_fused && a16 && flash_ok(dtype, s, plan);
+    const bool use_gemm = !use_fused && !use_flash && gp.ok && aligned(Q, 16) && aligned(K, 16) &&
                           aligned(V, 16) && aligned(out, 16);
     const size_t need =
-        use_fused ? fd.bytes : (use_gemm ? gp.bytes : kSyncBytes + sp.bytes);
+        use_fused ? fd.bytes
+                  : (use_flash ? kSyncBytes : (use_gemm ? gp.bytes : kSyncBytes + sp.bytes));
     void* ws = workspace;
     if (no_alloc) {
         if (need > atn::kNoAllocScratchBytes) return ATN_ERR_SCRATCH_LIMIT;
@@ -903,6 +917,13 @@ int attention_run(int dtype, const void* Q, const void* K, const void* V, void* 
                                         stream));
         return ATN_OK;
     }
+    if (use_flash) {
+        ATN_HIP(atn::launch_flash(plan.pek, static_cast<const float*>(Q),
+                                  static_cast<const float*>(K), static_cast<const float*>(V),
+                                  static_cast<float*>(out), (int)s.BH, Lq, Lk, D, scale, plan.q,
+                                  plan.k, stream));
+        return ATN_OK;
+    }
     float* S = scratch;
     float* P = sp.nsplit > 1 ? S + sp.s_elems : S;
     ATN_HIP(atn::launch_qk_partial(dtype, plan.pek, Q, K, S, (int)s.BH, Lq, Lk, D, sp.dchunk,
@@ -938,6 +959,7 @@ int attention_core(int dtype, const void* Q, const void* K, const void* V, void*
     st = check_pe(pe, D, &plan);
     if (st != ATN_OK) return st;
     plan.no_fused = no_fused || tune().no_fused != 0;
+    plan.no_flash = tune().no_flash != 0;
     // every path needs at least the sync region; the path-specific size is
     // checked once the device has chosen the path
     if (workspace != nullptr && workspace_bytes < kSyncBytes) return ATN_ERR_WORKSPACE;
@@ -1329,6 +1351,8 @@ int atn_attention_path_ex(int dtype, int batch, int heads, int len_q, int len_k,
     int n = 0;
     const bool dev = hipGetDeviceCount(&n) == hipSuccess && n > 0;
     if (!tune().no_fused && fused_plan(dtype, plan.pek, s, dev).ok) return ATN_PATH_FUSED_SMALL;
+    plan.no_flash = tune().no_flash != 0;
+    if (flash_ok(dtype, s, plan)) return ATN_PATH_FLASH;
     if (gemm_plan(dtype, s, plan).ok) return ATN_PATH_GEMM;
     return ATN_PATH_SPLIT_D;
 }

@@ -1,0 +1,433 @@
+// Flash-style fp32 attention for head_dim <= 256 at any sequence length
+// (gfx950).
+//
+// The reference's kernel (final/attention.cu:84-191) walks the keys of one
+// query row in 64-key tiles with an online softmax and keeps the running
+// output in global memory.  Here a workgroup owns 64 query rows (16 per
+// wave) of one head and walks the head's keys in tiles of KT keys (64 for
+// D <= 128 without an encoding, else 32), with the running output of its
+// rows in registers:
+//
+//   per tile: K and V rows are loaded (16-byte loads, the next tile's in
+//   flight while this one computes), K scaled by a power of two from the
+//   tile's largest finite magnitude (V only when it exceeds the fp16
+//   range: its scale carries over into the running output) and stored to
+//   LDS as hi + lo
+//   fp16 parts (the fp32 split of the single-launch kernel: 22 significant
+//   bits per operand, exact products on v_mfma_f32_16x16x32_f16, fp32
+//   accumulation);
+//   each wave computes S^T = K Q^T for its 16 query rows (Q in registers,
+//   split once, scaled by a power of two per wave) -- transposed, so that a
+//   lane holds 16 scores of ONE query: the online-softmax statistics (running
+//   max m, running sum l) of a query live in the lanes that hold its scores
+//   and its output row, and reductions over a tile's keys are 16 values in
+//   registers plus two cross-lane steps;
+//   P = exp(S - m) (scaled by 2^15, exact) stays in registers, where the
+//   accumulator layout of S^T is already the B operand of O^T += V^T P^T
+//   (the keys of each 32-key block in the order 4g + 0..3, 16 + 4g + 0..3 for
+//   lane group g; V's transposing LDS read, ds_read_b64_tr_b16, takes the
+//   same order), and O^T (16 dims x 16 queries per MFMA tile) accumulates
+//   in registers, rescaled per tile by exp(m_old - m_new) and by the ratio
+//   of consecutive V tiles' scales.
+//
+// The score matrix never reaches memory: per call the kernel reads Q once
+// and K and V once per 64-row query block, and writes O once.  Positional
+// encodings (RoPE, sinusoidal) are applied to Q and K at load.
+#include <algorithm>
+
+#include "common.hpp"
+#include "launch.hpp"
+
+namespace atn {
+
+namespace {
+
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+
+constexpr int kFlashThreads = 256;
+constexpr int kFlashRows = 64;  // query rows per workgroup, 16 per wave
+
+// Tiling for head dims padded to DP (32, 64, 128 or 256); with a
+// positional encoding (PE) the key tile is 32 keys (the encoding's table
+// loads need the registers of half the prefetched rows).
+template <int DP, bool PE>
+struct FlashGeo {
+    static constexpr int KT = DP <= 128 && !PE ? 64 : 32;  // keys per tile
+    static constexpr int KS = DP / 32;              // 32-deep steps of Q K^T
+    static constexpr int NJ = KT / 16;              // 16-key tiles of S^T
+    static constexpr int NB = KT / 32;              // 32-key blocks of P V
+    static constexpr int NDT = DP / 16;             // 16-dim tiles of O^T
+    static constexpr int VPR = DP / 4;              // 16-byte vectors per row
+    static constexpr int RSTEP = kFlashThreads / VPR;  // rows per load round
+    static constexpr int NLD = KT / RSTEP;             // load rounds per tile
+    // LDS rows in 16-bit elements: K padded by 8 (16-byte fragment reads),
+    // V by 16 (the transposing read's 4 rows x 32 bytes in distinct banks)
+    static constexpr int KSTR = DP + 8, VSTR = DP + 16;
+    static constexpr int K_HI = 0, K_LO = KT * KSTR, V_HI = 2 * KT * KSTR,
+                         V_LO = V_HI + KT * VSTR;
+    static constexpr int BYTES = 2 * (2 * KT * KSTR + 2 * KT * VSTR);
+    static_assert(KT % RSTEP == 0, "whole load rounds");
+};
+
+// hi + lo fp16 parts of two values (|x| < 65504): hi rounded toward zero,
+// lo the residual rounded to nearest even (|x - hi - lo| <= 2^-22 |x|, and
+// 2^-25 absolute below 2^-3; fp16 subnormals are kept by the conversion and
+// by the MFMA)
+__device__ __forceinline__ void split2(float a, float b, uint32_t& h, uint32_t& l) {
+    const f16x2 hh = __builtin_bit_cast(f16x2, __builtin_amdgcn_cvt_pkrtz(a, b));
+    const f16x2 lv = {(_Float16)(a - (float)hh[0]), (_Float16)(b - (float)hh[1])};
+    h = __builtin_bit_cast(uint32_t, hh);
+    l = __builtin_bit_cast(uint32_t, lv);
+}
+
+__device__ __forceinline__ v4f mfma(const f16x8& a, const f16x8& b, const v4f& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ f16x8 lds8(const uint16_t* p) {
+    return __builtin_bit_cast(f16x8, *reinterpret_cast<const uint4*>(p));
+}
+
+__device__ __forceinline__ uint2 ds_read_tr16(const uint16_t* p) {
+    return __builtin_bit_cast(
+        uint2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4i16*)(p)));
+}
+
+// Power-of-two scale s for values of largest finite magnitude m: m s in
+// [2^14, 2^15) (s within [2^-114, 2^126]); 1 for m == 0.  unit = 1 / s.
+__device__ __forceinline__ float p2_scale(float m) {
+    int eb = (__float_as_int(m) >> 23) & 0xff;
+    if (eb == 0) return 1.f;
+    eb = eb < 15 ? 15 : eb;
+    return __int_as_float((268 - eb) << 23);
+}
+__device__ __forceinline__ float p2_unit(float m) {
+    int eb = (__float_as_int(m) >> 23) & 0xff;
+    if (eb == 0) return 1.f;
+    eb = eb < 15 ? 15 : eb;
+    return __int_as_float((eb - 14) << 23);
+}
+
+// V's scale: 1 while the tile fits the fp16 split (so that consecutive
+// tiles' scales, whose ratio rescales the running output, stay equal on
+// ordinary data), else a power of two as for K
+__device__ __forceinline__ float v_scale(float m) { return m < 65504.0f ? 1.f : p2_scale(m); }
+__device__ __forceinline__ float v_unit(float m) { return m < 65504.0f ? 1.f : p2_unit(m); }
+
+// largest finite magnitude of m and 4 values (infinities and NaNs count as 0)
+__device__ __forceinline__ float max_fin4(float m, float4 f) {
+    auto fa = [](float x) {
+        const float a = fabsf(x);
+        return a < INFINITY ? a : 0.f;
+    };
+    return fmaxf(fmaxf(m, fmaxf(fa(f.x), fa(f.y))), fmaxf(fa(f.z), fa(f.w)));
+}
+
+__device__ __forceinline__ float4 ld_buf4(__amdgpu_buffer_rsrc_t r, int off) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+    return make_float4(__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]),
+                       __uint_as_float(v[3]));
+}
+
+// lanes L, L ^ 16, L ^ 32, L ^ 48 (the four lane groups of one query)
+__device__ __forceinline__ float xgroup_max(float v) {
+    v = fmaxf(v, swz_xor16(v));
+    return fmaxf(v, __shfl_xor(v, 32));
+}
+__device__ __forceinline__ float xgroup_sum(float v) {
+    v += swz_xor16(v);
+    return v + __shfl_xor(v, 32);
+}
+
+template <int DP, int PEK>
+__global__ __launch_bounds__(kFlashThreads, 2) void k_flash_f32(const float* __restrict__ Qg,
+                                                                 const float* __restrict__ Kg,
+                                                                 const float* __restrict__ Vg,
+                                                                 float* __restrict__ Og, int Lq,
+                                                                 int Lk, int D, int qblocks,
+                                                                 float scale, PeSide pq,
+                                                                 PeSide pk) {
+    using G = FlashGeo<DP, PEK != kPeNone>;
+    extern __shared__ __align__(16) unsigned char smem_raw[];
+    uint16_t* smem = reinterpret_cast<uint16_t*>(smem_raw);
+    __shared__ float slot[8];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lr = lane & 15, lg = lane >> 4;
+    // workgroup -> (head, query block); with a grid that is a multiple of 8
+    // the query blocks of a head are consecutive on one XCD (the dispatcher
+    // deals ids to the 8 XCDs round robin), so its K and V stay in that L2
+    const int nwg = (int)gridDim.x;
+    int id = (int)blockIdx.x;
+    if ((nwg & 7) == 0) id = (id & 7) * (nwg >> 3) + (id >> 3);
+    const int bh = id / qblocks, qb = id - bh * qblocks;
+    const int q0 = qb * kFlashRows;
+    const float* Qh = Qg + (size_t)bh * Lq * D;
+    const float* Kh = Kg + (size_t)bh * Lk * D;
+    const float* Vh = Vg + (size_t)bh * Lk * D;
+    constexpr int kOob = 0x7ffffff0;
+
+    // ---- Q: this wave's 16 rows as the B operand of S^T = K Q^T: lane
+    // (query lr, group lg) holds dims 32 ks + 8 lg + 0..7, scaled by a
+    // power of two from the wave's largest finite magnitude
+    const int qrow = q0 + 16 * wave + lr;
+    f16x8 qh[G::KS], ql[G::KS];
+    float uq;
+    {
+        float4 qv[G::KS][2];
+        float mq = 0.f;
+        const __amdgpu_buffer_rsrc_t rq =
+            __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(Qh), 0, Lq * D * 4, 0x00020000);
+#pragma unroll
+        for (int ks = 0; ks < G::KS; ++ks)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int d = 32 * ks + 8 * lg + 4 * h;
+                if constexpr (PEK == kPeNone) {
+                    qv[ks][h] = ld_buf4(rq, d < D ? (qrow * D + d) * 4 : kOob);
+                } else {
+                    qv[ks][h] = make_float4(0.f, 0.f, 0.f, 0.f);
+                    if (qrow < Lq && d < D)
+                        qv[ks][h] = load_row4_pe<float, PEK>(Qh + (size_t)qrow * D, qrow, d, D, pq,
+                                                             true);
+                }
+                mq = max_fin4(mq, qv[ks][h]);
+            }
+        mq = wave_max(mq);
+        const float sq = p2_scale(mq);
+        uq = p2_unit(mq);
+#pragma unroll
+        for (int ks = 0; ks < G::KS; ++ks) {
+            uint32_t h[4], l[4];
+            split2(qv[ks][0].x * sq, qv[ks][0].y * sq, h[0], l[0]);
+            split2(qv[ks][0].z * sq, qv[ks][0].w * sq, h[1], l[1]);
+            split2(qv[ks][1].x * sq, qv[ks][1].y * sq, h[2], l[2]);
+            split2(qv[ks][1].z * sq, qv[ks][1].w * sq, h[3], l[3]);
+            qh[ks] = __builtin_bit_cast(f16x8, make_uint4(h[0], h[1], h[2], h[3]));
+            ql[ks] = __builtin_bit_cast(f16x8, make_uint4(l[0], l[1], l[2], l[3]));
+        }
+    }
+
+    // ---- K/V tile loads: thread t holds 16-byte vector t % VPR of rows
+    // t / VPR + RSTEP i (rows past Lk and columns past D read as zeros)
+    const int lrow = tid / G::VPR, lcol = (tid % G::VPR) * 4;
+    const __amdgpu_buffer_rsrc_t rk =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(Kh), 0, Lk * D * 4, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rv =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(Vh), 0, Lk * D * 4, 0x00020000);
+    float4 kr[G::NLD], vr[G::NLD];
+    auto issue = [&](int k0) {
+#pragma unroll
+        for (int i = 0; i < G::NLD; ++i) {
+            const int key = k0 + lrow + G::RSTEP * i;
+            const int off = lcol < D ? (key * D + lcol) * 4 : kOob;
+            if constexpr (PEK == kPeNone) {
+                kr[i] = ld_buf4(rk, off);
+            } else {
+                kr[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (key < Lk && lcol < D)
+                    kr[i] = load_row4_pe<float, PEK>(Kh + (size_t)key * D, key, lcol, D, pk, true);
+            }
+            vr[i] = ld_buf4(rv, off);
+        }
+    };
+
+    // running statistics of this lane's query and its output rows (O^T
+    // tiles: lane holds dims 16 t + 4 lg + 0..3 of query lr), in units of
+    // uv / 2^15 for the current V tile's unit uv = 1 / sv
+    float m_run = -INFINITY, l_run = 0.f, uv_prev = 1.f;
+    v4f o[G::NDT];
+#pragma unroll
+    for (int t = 0; t < G::NDT; ++t) o[t] = v4f{0.f, 0.f, 0.f, 0.f};
+
+    const int ntiles = (Lk + G::KT - 1) / G::KT;
+    issue(0);
+    for (int t = 0; t < ntiles; ++t) {
+        const int k0 = t * G::KT;
+        // tile scales: workgroup maxima of the loaded K and V values (the
+        // slots are read after the barrier that also ends the previous
+        // tile's LDS reads)
+        float mk = 0.f, mv = 0.f;
+#pragma unroll
+        for (int i = 0; i < G::NLD; ++i) {
+            mk = max_fin4(mk, kr[i]);
+            mv = max_fin4(mv, vr[i]);
+        }
+        mk = wave_max(mk);
+        mv = wave_max(mv);
+        if (lane == 0) {
+            slot[wave] = mk;
+            slot[4 + wave] = mv;
+        }
+        __syncthreads();
+        mk = fmaxf(fmaxf(slot[0], slot[1]), fmaxf(slot[2], slot[3]));
+        mv = fmaxf(fmaxf(slot[4], slot[5]), fmaxf(slot[6], slot[7]));
+        const float sk = p2_scale(mk), sv = v_scale(mv), uv = v_unit(mv);
+#pragma unroll
+        for (int i = 0; i < G::NLD; ++i) {
+            const int row = lrow + G::RSTEP * i;
+            uint32_t h0, l0, h1, l1;
+            split2(kr[i].x * sk, kr[i].y * sk, h0, l0);
+            split2(kr[i].z * sk, kr[i].w * sk, h1, l1);
+            *reinterpret_cast<uint2*>(smem + G::K_HI + row * G::KSTR + lcol) = make_uint2(h0, h1);
+            *reinterpret_cast<uint2*>(smem + G::K_LO + row * G::KSTR + lcol) = make_uint2(l0, l1);
+            split2(vr[i].x * sv, vr[i].y * sv, h0, l0);
+            split2(vr[i].z * sv, vr[i].w * sv, h1, l1);
+            *reinterpret_cast<uint2*>(smem + G::V_HI + row * G::VSTR + lcol) = make_uint2(h0, h1);
+            *reinterpret_cast<uint2*>(smem + G::V_LO + row * G::VSTR + lcol) = make_uint2(l0, l1);
+        }
+        if (t + 1 < ntiles) issue(k0 + G::KT);  // lands while this tile computes
+        __syncthreads();
+
+        // ---- S^T tile: s[j] = keys 16 j + 4 lg + r, query lr
+        v4f s[G::NJ];
+#pragma unroll
+        for (int j = 0; j < G::NJ; ++j) s[j] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < G::KS; ++ks) {
+#pragma unroll
+            for (int j = 0; j < G::NJ; ++j) {
+                const int a = (16 * j + lr) * G::KSTR + 32 * ks + 8 * lg;
+                const f16x8 ah = lds8(smem + G::K_HI + a), al = lds8(smem + G::K_LO + a);
+                s[j] = mfma(ah, qh[ks], s[j]);
+                s[j] = mfma(ah, ql[ks], s[j]);
+                s[j] = mfma(al, qh[ks], s[j]);
+            }
+        }
+
+        // ---- online softmax over the tile (keys past Lk score -inf)
+        const float c = scale * uq * p2_unit(mk);
+        float mt = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < G::NJ; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int key = k0 + 16 * j + 4 * lg + r;
+                const float x = key < Lk ? s[j][r] * c : -INFINITY;
+                s[j][r] = x;
+                mt = fmaxf(mt, x);
+            }
+        mt = xgroup_max(mt);
+        const float m_new = fmaxf(m_run, mt);
+        const float alpha = __expf(m_run - m_new);  // 0 on the first tile
+        m_run = m_new;
+        float ps = 0.f;
+        // P as the B operand of block b: elements 0..3 tile 2b, 4..7 tile 2b+1
+        f16x8 ph[G::NB], pl[G::NB];
+#pragma unroll
+        for (int b = 0; b < G::NB; ++b) {
+            uint32_t h[4], l[4];
+#pragma unroll
+            for (int half = 0; half < 2; ++half) {
+                const v4f& sj = s[2 * b + half];
+                float p[4];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    p[r] = __expf(sj[r] - m_new);
+                    ps += p[r];
+                }
+                split2(p[0] * 32768.f, p[1] * 32768.f, h[2 * half], l[2 * half]);
+                split2(p[2] * 32768.f, p[3] * 32768.f, h[2 * half + 1], l[2 * half + 1]);
+            }
+            ph[b] = __builtin_bit_cast(f16x8, make_uint4(h[0], h[1], h[2], h[3]));
+            pl[b] = __builtin_bit_cast(f16x8, make_uint4(l[0], l[1], l[2], l[3]));
+        }
+        l_run = l_run * alpha + ps;  // this lane's keys; summed over lane groups at the end
+        const float f = alpha * (uv_prev * sv);  // the old output in the new tile's units
+        uv_prev = uv;
+
+        // ---- O^T += V^T P^T: A = V^T from the transposing read, keys of
+        // block b in P's order (rows 4 lg + 0..3, then 16 + 4 lg + 0..3)
+        const int vrow = 4 * lg + (lr >> 2), vcol = 4 * (lr & 3);
+#pragma unroll
+        for (int dt = 0; dt < G::NDT; ++dt) {
+            o[dt] *= f;
+#pragma unroll
+            for (int b = 0; b < G::NB; ++b) {
+                const int a = (32 * b + vrow) * G::VSTR + 16 * dt + vcol;
+                const uint2 h0 = ds_read_tr16(smem + G::V_HI + a);
+                const uint2 h1 = ds_read_tr16(smem + G::V_HI + a + 16 * G::VSTR);
+                const uint2 l0 = ds_read_tr16(smem + G::V_LO + a);
+                const uint2 l1 = ds_read_tr16(smem + G::V_LO + a + 16 * G::VSTR);
+                const f16x8 vh = __builtin_bit_cast(f16x8, make_uint4(h0.x, h0.y, h1.x, h1.y));
+                const f16x8 vl = __builtin_bit_cast(f16x8, make_uint4(l0.x, l0.y, l1.x, l1.y));
+                o[dt] = mfma(vh, ph[b], o[dt]);
+                o[dt] = mfma(vh, pl[b], o[dt]);
+                o[dt] = mfma(vl, ph[b], o[dt]);
+            }
+        }
+    }
+
+    // ---- O = O^T uv / (2^15 l): one 16-byte store per dim tile
+    const float l = xgroup_sum(l_run);
+    const float inv = 1.0f / (l * 32768.f);
+    if (qrow < Lq) {
+        float* orow = Og + ((size_t)bh * Lq + qrow) * D;
+#pragma unroll
+        for (int dt = 0; dt < G::NDT; ++dt) {
+            const int d = 16 * dt + 4 * lg;
+            if (d < D)
+                *reinterpret_cast<float4*>(orow + d) =
+                    make_float4(o[dt][0] * inv * uv_prev, o[dt][1] * inv * uv_prev,
+                                o[dt][2] * inv * uv_prev, o[dt][3] * inv * uv_prev);
+        }
+    }
+}
+
+template <int DP, int PEK>
+hipError_t launch_t(const float* Q, const float* K, const float* V, float* O, int BH, int Lq,
+                    int Lk, int D, float scale, const PeSide& pq, const PeSide& pk,
+                    hipStream_t st) {
+    constexpr int lds = FlashGeo<DP, PEK != kPeNone>::BYTES;
+    static bool attr = false;
+    if (!attr) {
+        hipError_t e = hipFuncSetAttribute((const void*)k_flash_f32<DP, PEK>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+        if (e != hipSuccess) return e;
+        attr = true;
+    }
+    const int qblocks = (Lq + kFlashRows - 1) / kFlashRows;
+    hipLaunchKernelGGL((k_flash_f32<DP, PEK>), dim3((unsigned)(BH * qblocks)),
+                       dim3(kFlashThreads), lds, st, Q, K, V, O, Lq, Lk, D, qblocks, scale, pq, pk);
+    return hipGetLastError();
+}
+
+template <int PEK>
+hipError_t launch_pe(const float* Q, const float* K, const float* V, float* O, int BH, int Lq,
+                     int Lk, int D, float scale, const PeSide& pq, const PeSide& pk,
+                     hipStream_t st) {
+    if (D <= 32) return launch_t<32, PEK>(Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk, st);
+    if (D <= 64) return launch_t<64, PEK>(Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk, st);
+    if (D <= 128) return launch_t<128, PEK>(Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk, st);
+    if constexpr (PEK == kPeNone)
+        return launch_t<256, PEK>(Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk, st);
+    return hipErrorInvalidValue;  // flash_supported: encoded calls have D <= 128
+}
+
+}  // namespace
+
+bool flash_supported(int dtype, int pek, int D) {
+    return dtype == kDtypeF32 && D >= 1 && D % 4 == 0 &&
+           D <= (pek == kPeNone ? kFlashMaxD : kFlashMaxDEncoded);
+}
+
+hipError_t launch_flash(int pek, const float* Q, const float* K, const float* V, float* O,
+                        int BH, int Lq, int Lk, int D, float scale, const PeSide& pq,
+                        const PeSide& pk, hipStream_t st) {
+    switch (pek) {
+        case kPeNone: return launch_pe<kPeNone>(Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk, st);
+        case kPeRopeInterleaved:
+            return launch_pe<kPeRopeInterleaved>(Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk, st);
+        case kPeRopeHalf:
+            return launch_pe<kPeRopeHalf>(Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk, st);
+        case kPeSinusoidal:
+            return launch_pe<kPeSinusoidal>(Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk, st);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace atn

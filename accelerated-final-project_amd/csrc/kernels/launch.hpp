@@ -61,6 +61,16 @@ hipError_t launch_gemm_pv(const uint16_t* E, int ldE, float* st_m, float* st_l, 
                           const uint16_t* V, uint16_t* O, int BH, int Lq, int Lk, int D,
                           hipStream_t st);
 
+// Flash-style fp32 attention (flash.hip): any len_q and len_k, head_d <=
+// kFlashMaxD (kFlashMaxDEncoded with a positional encoding) with head_d % 4
+// == 0, 16-byte aligned bases, and every head's Q or K/V under 2^31 bytes
+// (32-bit buffer offsets); no scratch.
+constexpr int kFlashMaxD = 256, kFlashMaxDEncoded = 128;
+bool flash_supported(int dtype, int pek, int D);
+hipError_t launch_flash(int pek, const float* Q, const float* K, const float* V, float* O,
+                        int BH, int Lq, int Lk, int D, float scale, const PeSide& pq,
+                        const PeSide& pk, hipStream_t st);
+
 // Allocation-free entry point: the per-device scratch array (noalloc.hip),
 // kNoAllocScratchBytes long.  noalloc_scratch() returns its device address
 // for device `dev` (hipGetSymbolAddress, taken once per device) and, on the

@@ -453,6 +453,7 @@ def main():
     roof["kernel"] = {
         am.ATN_PATH_FUSED_SMALL: "k_fused_small (one launch per step)",
         am.ATN_PATH_SPLIT_D: "split-D pipeline (k_qk_partial + k_softmax + k_pv per step)",
+        am.ATN_PATH_FLASH: "k_flash_f32 (one launch per step)",
         am.ATN_PATH_GEMM: ("GEMM path (encode, QK^T GEMM with exp epilogue, PV GEMM per step; "
                            "whole-step figure, per-kernel split in profiles/)"),
     }.get(path, "unknown")

@@ -143,14 +143,22 @@ def test_workspace_bytes_bound_every_plan(am, tuner, dtype, shape):
         assert am.workspace_bytes(dtype, *shape) == base, (rows, dc, x)
 
 
-def test_path_selection_without_device(am):
+def test_path_selection_without_device(am, tuner):
     """Short sequences take the single-launch kernel, long ones the pipeline."""
     assert am.path(0, 1, 4, 64, 64, 2048) == am.ATN_PATH_FUSED_SMALL       # config 2
     assert am.path(1, 1, 4, 32, 128, 8192) == am.ATN_PATH_FUSED_SMALL      # config 3
     assert am.path(0, 1, 1, 4, 4, 8) == am.ATN_PATH_FUSED_SMALL            # config 1
-    assert am.path(0, 4, 32, 512, 512, 128) == am.ATN_PATH_SPLIT_D
-    assert am.path(0, 1, 1, 3, 129, 36) == am.ATN_PATH_SPLIT_D
-    assert am.path(0, 1, 300, 16, 16, 64) == am.ATN_PATH_SPLIT_D           # more heads than CUs
+    # fp32 outside the single-launch window with head_d <= 256 (128 with an
+    # encoding) and head_d % 4 == 0 runs on the flash kernel
+    assert am.path(0, 4, 32, 512, 512, 128) == am.ATN_PATH_FLASH
+    assert am.path(0, 1, 1, 3, 129, 36) == am.ATN_PATH_FLASH
+    assert am.path(0, 1, 300, 16, 16, 64) == am.ATN_PATH_FLASH             # more heads than CUs
+    assert am.path(0, 1, 4, 512, 512, 256) == am.ATN_PATH_FLASH
+    assert am.path(0, 1, 4, 512, 512, 128, am.make_pe("rope")) == am.ATN_PATH_FLASH
+    assert am.path(0, 1, 4, 512, 512, 256, am.make_pe("rope")) == am.ATN_PATH_SPLIT_D
+    assert am.path(0, 1, 4, 512, 512, 260) == am.ATN_PATH_SPLIT_D           # head_d > 256
+    assert am.path(0, 1, 4, 512, 512, 130) == am.ATN_PATH_SPLIT_D           # head_d % 4 != 0
+    assert am.path(0, 1, 4, 512, 512, 2048) == am.ATN_PATH_SPLIT_D
     # bf16 outside the single-launch window runs on the MFMA GEMM path
     # whenever D % 8 == 0, whatever len_q and len_k are
     assert am.path(1, 8, 8, 1024, 1024, 4096) == am.ATN_PATH_GEMM          # config 4
@@ -159,6 +167,8 @@ def test_path_selection_without_device(am):
     assert am.path(1, 1, 2, 200, 20, 512) == am.ATN_PATH_GEMM
     assert am.path(1, 1, 2, 200, 20, 36) == am.ATN_PATH_SPLIT_D           # D % 8 != 0
     assert am.path(0, 0, 4, 64, 64, 2048) == -2
+    tuner.set(no_flash=True)
+    assert am.path(0, 4, 32, 512, 512, 128) == am.ATN_PATH_SPLIT_D
 
 
 def test_no_device_path(am, L):

@@ -1,0 +1,199 @@
+"""The flash kernel (fp32, head_d <= 256, any sequence length; flash.hip)
+against the CPU oracle: tile edges of the key loop, head dims padded to the
+kernel's 32/64/128/256 forms, query blocks past the sequence, positional
+encodings applied at load, wide logits, values outside fp16's range
+(power-of-two linearity), and agreement with the split-D pipeline on the
+same inputs.  The reference's own long-sequence test shape (4, 32, 512,
+512, 128) (final/attention.cu:522) runs here too, as in test_gpu_parity.py.
+"""
+import numpy as np
+import pytest
+
+import helpers as H
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+
+def _f32_call(am, Q, K, V, desc=None):
+    (q, k, v) = (H.upload(x) for x in (Q, K, V))
+    out = H.empty(Q.shape)
+    am.attention_ex(q, k, v, out, pe=desc)
+    import hip_rt
+    hip_rt.synchronize()
+    return out.numpy()
+
+
+# key lengths around the 64- and 32-key tiles, query lengths around the
+# 64-row blocks, head dims at and below each padded form
+_SHAPES = [
+    (1, 2, 65, 1, 64), (1, 2, 65, 63, 64), (1, 2, 65, 64, 64), (1, 2, 70, 65, 64),
+    (1, 3, 130, 129, 32), (1, 1, 200, 300, 128), (1, 2, 129, 513, 100), (1, 1, 80, 1025, 60),
+    (1, 2, 96, 200, 256), (1, 1, 70, 65, 200), (1, 1, 65, 33, 160), (2, 3, 100, 140, 8),
+    (1, 4, 512, 512, 128), (1, 300, 16, 16, 64),
+]
+
+
+@pytest.mark.parametrize("shape", _SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_flash_f32(am, dev, shape):
+    B, Hh, Lq, Lk, D = shape
+    print(f"[case] flash f32 {shape}", flush=True)
+    assert am.path(0, B, Hh, Lq, Lk, D) == am.ATN_PATH_FLASH
+    Q, K, V = H.rng_inputs((B, Hh, Lq, D), (B, Hh, Lk, D), seed=500 + Lk + D)
+    got = _f32_call(am, Q, K, V)
+    ref = oracle.attention(Q, K, V, nthreads=16)
+    n, mabs, mrel = H.check_f32(got, ref)
+    assert n == 0, f"{n} mismatches, max abs {mabs}, max rel {mrel}"
+
+
+def test_flash_reference_long_shape(am, dev):
+    """The reference's long-sequence test shape (final/attention.cu:522)."""
+    B, Hh, L, D = 4, 32, 512, 128
+    print("[case] flash f32 (4,32,512,512,128)", flush=True)
+    assert am.path(0, B, Hh, L, L, D) == am.ATN_PATH_FLASH
+    Q, K, V = H.rng_inputs((B, Hh, L, D), (B, Hh, L, D), seed=522)
+    got = _f32_call(am, Q, K, V)
+    n, mabs, mrel = H.check_f32(got, oracle.attention(Q, K, V, nthreads=16))
+    assert n == 0, f"{n} mismatches, max abs {mabs}, max rel {mrel}"
+
+
+@pytest.mark.parametrize("shape", [(1, 2, 200, 300, 128), (1, 1, 96, 200, 256)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_flash_wide_logits(am, dev, shape):
+    """sigma 3 inputs (logits to about +-40, scores spread over many key
+    tiles, so the running maximum moves between tiles)."""
+    B, Hh, Lq, Lk, D = shape
+    print(f"[case] flash f32 sigma 3 {shape}", flush=True)
+    Q, K, V = H.rng_inputs((B, Hh, Lq, D), (B, Hh, Lk, D), seed=77 + D, sigma=3.0)
+    got = _f32_call(am, Q, K, V)
+    n, mabs, _ = H.check_f32(got, oracle.attention(Q, K, V, nthreads=16))
+    assert n == 0, f"{n} mismatches, max abs {mabs}"
+
+
+def test_flash_increasing_scores(am, dev):
+    """Scores that grow key tile by key tile (each tile's maximum above the
+    last), so every tile rescales the running output by exp(m_old - m_new)."""
+    B, Hh, Lq, Lk, D = 1, 2, 64, 512, 64
+    print("[case] flash f32 rising scores", flush=True)
+    Q, K, V = H.rng_inputs((B, Hh, Lq, D), (B, Hh, Lk, D), seed=91)
+    Q[..., 0] = np.abs(Q[..., 0]) + 1.0  # a positive first coordinate,
+    Q[..., 1:] *= np.float32(0.1)        # which dominates each score
+    K[..., 0] = np.linspace(-40, 40, Lk, dtype=np.float32)[None, None, :]
+    got = _f32_call(am, Q, K, V)
+    n, mabs, _ = H.check_f32(got, oracle.attention(Q, K, V, nthreads=16))
+    assert n == 0, f"{n} mismatches, max abs {mabs}"
+
+
+@pytest.mark.parametrize("exps", [(17, -17, 0), (0, 0, 19), (-12, -12, -12), (17, -17, 21)],
+                         ids=["qk-big", "v-big", "all-small", "all-big"])
+def test_flash_outside_fp16_range(am, dev, exps):
+    """Head 1 scaled by powers of two (exact, so the oracle on the unscaled V
+    times 2^ev is the reference): K tiles always carry a power-of-two scale,
+    V tiles one only beyond fp16's range, carried into the running output."""
+    B, Hh, Lq, Lk, D = 1, 3, 100, 300, 128
+    eq, ek, ev = exps
+    print(f"[case] flash f32 scaled 2^{exps}", flush=True)
+    Q, K, V = H.rng_inputs((B, Hh, Lq, D), (B, Hh, Lk, D), seed=31)
+    Q[:, 1] *= np.float32(2.0 ** eq)
+    K[:, 1] *= np.float32(2.0 ** ek)
+    Vs = V.copy()
+    Vs[:, 1] *= np.float32(2.0 ** ev)
+    got = _f32_call(am, Q, K, Vs)
+    assert np.isfinite(got).all()
+    got[:, 1] *= np.float32(2.0 ** -ev)
+    n, mabs, mrel = H.check_f32(got, oracle.attention(Q, K, V, nthreads=16))
+    assert n == 0, f"{n} mismatches, max abs {mabs}, max rel {mrel}"
+
+
+def test_flash_v_scale_changes_between_tiles(am, dev):
+    """One key tile of V beyond fp16's range among ordinary ones: its scale
+    differs from its neighbours', and the running output is carried across
+    the change in both directions."""
+    B, Hh, Lq, Lk, D = 1, 1, 64, 256, 64
+    print("[case] flash f32 V scale change", flush=True)
+    Q, K, V = H.rng_inputs((B, Hh, Lq, D), (B, Hh, Lk, D), seed=33, sigma=0.3)
+    V[:, :, 64:128] *= np.float32(2.0 ** 18)
+    got = _f32_call(am, Q, K, V)
+    ref = oracle.attention(Q, K, V, nthreads=16)
+    # outputs mix values of 2^18 and 1: compare in units of the largest
+    n, mabs, _ = H.check_f32(got / 2.0 ** 18, ref / 2.0 ** 18)
+    assert n == 0, f"{n} mismatches, max abs {mabs} (units of 2^18)"
+
+
+@pytest.mark.parametrize("pe,rot,aq,ak", [("rope", 0, True, True), ("rope", 48, True, True),
+                                          ("rope_half", 0, True, True),
+                                          ("sinusoidal", 0, True, True),
+                                          ("rope", 0, True, False), ("sinusoidal", 0, False, True)],
+                         ids=["rope", "rope-partial", "rope-half", "sin", "rope-q", "sin-k"])
+def test_flash_encodings(am, dev, pe, rot, aq, ak):
+    B, Hh, Lq, Lk, D = 1, 2, 150, 333, 128
+    print(f"[case] flash f32 {pe} rot={rot} q={aq} k={ak}", flush=True)
+    desc = {"rope": am.make_pe("rope", rotary_dim=rot, apply_q=aq, apply_k=ak),
+            "rope_half": am.make_pe("rope", pairing="half", apply_q=aq, apply_k=ak),
+            "sinusoidal": am.make_pe("sinusoidal", apply_q=aq, apply_k=ak)}[pe]
+    assert am.path(0, B, Hh, Lq, Lk, D, desc) == am.ATN_PATH_FLASH
+    sigma = 0.5 if pe == "sinusoidal" else 1.0
+    Q, K, V = H.rng_inputs((B, Hh, Lq, D), (B, Hh, Lk, D), seed=61, sigma=sigma)
+    got = _f32_call(am, Q, K, V, desc)
+    L = max(Lq, Lk)
+    if pe == "sinusoidal":
+        st, ct = oracle.sinusoidal_table(L, D)
+        ref = oracle.attention_sinusoidal(Q, K, V, st, ct, add_q=aq, add_k=ak, nthreads=16)
+    else:
+        r = rot or D
+        c, s = oracle.rope_cache(L, r)
+        ref = oracle.attention_rope(Q, K, V, c, s, rotary_dim=r,
+                                    pairing="half" if pe == "rope_half" else "interleaved",
+                                    rotate_q=aq, rotate_k=ak, nthreads=16)
+    n, mabs, _ = H.check_f32(got, ref)
+    assert n == 0, f"{n} mismatches, max abs {mabs}"
+
+
+@pytest.mark.parametrize("shape", [(1, 4, 200, 200, 128), (1, 2, 65, 1025, 64)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_flash_matches_split_d(am, dev, tuner, shape):
+    """The flash kernel and the split-D pipeline (forced with
+    atn_tuning.no_flash) on the same inputs, both against the oracle."""
+    B, Hh, Lq, Lk, D = shape
+    print(f"[case] flash vs split-D {shape}", flush=True)
+    Q, K, V = H.rng_inputs((B, Hh, Lq, D), (B, Hh, Lk, D), seed=3 + Lk)
+    ref = oracle.attention(Q, K, V, nthreads=16)
+    got_f = _f32_call(am, Q, K, V)
+    tuner.set(no_flash=True)
+    assert am.path(0, B, Hh, Lq, Lk, D) == am.ATN_PATH_SPLIT_D
+    got_s = _f32_call(am, Q, K, V)
+    for got in (got_f, got_s):
+        n, mabs, _ = H.check_f32(got, ref)
+        assert n == 0, mabs
+    n, mabs, _ = H.check_f32(got_f, got_s)
+    assert n == 0, mabs
+
+
+def test_flash_graph_replays(am, dev):
+    """Captured HIP graph of flash calls replayed with eager work between the
+    replays: every replay equals the eager result bit for bit."""
+    import hip_rt
+    B, Hh, Lq, Lk, D = 1, 4, 200, 300, 128
+    print("[case] flash graph replay", flush=True)
+    (q, k, v), (Q, K, V) = H.device_inputs((B, Hh, Lq, D), (B, Hh, Lk, D), 95)
+    st = hip_rt.Stream()
+    eager = H.empty(Q.shape)
+    am.attention_ex(q, k, v, eager, stream=st)
+    st.synchronize()
+    ref = eager.bits()
+    outs = [H.empty(Q.shape) for _ in range(2)]
+    g = hip_rt.Graph(st, lambda: [am.attention_ex(q, k, v, o, stream=st) for o in outs])
+    for _ in range(3):
+        for o in outs:
+            o.fill_nan()
+        hip_rt.synchronize()
+        g.launch()
+        st.synchronize()
+        for o in outs:
+            assert np.array_equal(o.bits(), ref)
+        am.attention_ex(q, k, v, eager, stream=st)
+        st.synchronize()
+    g.destroy()
+    n, mabs, _ = H.check_f32(ref, oracle.attention(Q, K, V, nthreads=16))
+    assert n == 0, mabs
+    st.destroy()

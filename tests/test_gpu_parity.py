@@ -167,13 +167,15 @@ def test_sdpa_f32_nonfinite_inputs_propagate(am, dev):
 @pytest.mark.parametrize("shape", [(1, 1, 70, 1, 64), (1, 3, 65, 255, 40), (1, 8, 70, 1025, 64),
                                    (1, 4, 65, 2048, 64), (1, 2, 100, 2049, 32)],
                          ids=lambda s: "x".join(map(str, s)))
-def test_sdpa_f32_split_d_softmax_rows(am, dev, shape):
-    """fp32 rows on the split-D pipeline without D-chunk partials: one key,
-    the edges of the one-wave-per-row softmax's register blocks (256, 1024,
-    2048 keys) and the first row length past it (2049 keys, the
-    workgroup-per-row softmax)."""
+def test_sdpa_f32_split_d_softmax_rows(am, dev, tuner, shape):
+    """fp32 rows on the split-D pipeline (forced: these head dims take the
+    flash kernel by default) without D-chunk partials: one key, the edges of
+    the one-wave-per-row softmax's register blocks (256, 1024, 2048 keys) and
+    the first row length past it (2049 keys, the workgroup-per-row
+    softmax)."""
     B, Hh, Lq, Lk, D = shape
     print(f"[case] sdpa f32 split-D softmax rows {shape}", flush=True)
+    tuner.set(no_flash=True)
     assert am.path(0, B, Hh, Lq, Lk, D) == am.ATN_PATH_SPLIT_D
     Q, K, V = H.rng_inputs((B, Hh, Lq, D), (B, Hh, Lk, D), seed=40 + Lk)
     got = _f32_call(am.attention_forward_optimized, Q, K, V)

@@ -24,7 +24,8 @@ pytestmark = pytest.mark.gpu
 CASES = [  # (dtype, pe, (B, H, Lq, Lk, D), expected path)
     ("bf16", "sinusoidal", (1, 2, 256, 384, 256), "gemm"),
     ("bf16", "rope_half", (1, 2, 128, 640, 128), "gemm"),
-    ("f32", "none", (1, 2, 100, 300, 64), "split_d"),
+    ("f32", "none", (1, 2, 100, 300, 64), "flash"),
+    ("f32", "none", (1, 2, 100, 300, 520), "split_d"),
     ("bf16", "sinusoidal", (1, 1, 129, 1040, 512), "gemm"),
 ]
 
@@ -48,7 +49,7 @@ def _ref(pe, Q, K, V):
 def test_threads_share_library_state(am, dev):
     import hip_rt
     print("[case] four host threads, four streams, library workspaces", flush=True)
-    paths = {"gemm": am.ATN_PATH_GEMM, "split_d": am.ATN_PATH_SPLIT_D}
+    paths = {"gemm": am.ATN_PATH_GEMM, "split_d": am.ATN_PATH_SPLIT_D, "flash": am.ATN_PATH_FLASH}
     jobs = []
     for i, (dt, pe, shape, want) in enumerate(CASES):
         B, Hh, Lq, Lk, D = shape

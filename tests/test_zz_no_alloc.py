@@ -39,9 +39,10 @@ def _pair(am, shape, dtype, pe, seed):
     ((1, 4, 64, 64, 2048), (1, 2, 32, 32, 512), "f32", None),          # single-launch kernel
     ((1, 4, 32, 128, 8192), (1, 1, 16, 100, 1024), "bf16", None),      # single-launch, bf16
     ((1, 2, 256, 512, 256), (1, 1, 128, 256, 128), "bf16", "rope_half"),  # GEMM path
-    ((1, 2, 300, 200, 36), (1, 1, 70, 90, 20), "f32", None),           # split-D pipeline
+    ((1, 2, 300, 200, 260), (1, 1, 70, 90, 22), "f32", None),          # split-D pipeline
+    ((1, 2, 300, 200, 36), (1, 1, 70, 90, 20), "f32", None),           # flash kernel
     ((2, 2, 256, 512, 128), (1, 2, 128, 128, 128), "bf16", "sinusoidal"),  # GEMM path
-], ids=["fused-f32", "fused-bf16", "gemm-rope", "splitd", "gemm-sin"])
+], ids=["fused-f32", "fused-bf16", "gemm-rope", "splitd", "flash", "gemm-sin"])
 def test_noalloc_matches_ex_two_calls(am, dev, first, second, dtype, pe):
     desc = None
     if pe == "rope_half":
