@@ -37,15 +37,11 @@
 
 #include "common.hpp"
 #include "launch.hpp"
+#include "split16.hpp"
 
 namespace atn {
 
 namespace {
-
-typedef float v4f __attribute__((ext_vector_type(4)));
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
-typedef short v4i16 __attribute__((ext_vector_type(4)));
 
 constexpr int kFlashThreads = 256;
 constexpr int kFlashRows = 64;  // query rows per workgroup, 16 per wave
@@ -71,66 +67,6 @@ struct FlashGeo {
     static constexpr int BYTES = 2 * (2 * KT * KSTR + 2 * KT * VSTR);
     static_assert(KT % RSTEP == 0, "whole load rounds");
 };
-
-// hi + lo fp16 parts of two values (|x| < 65504): hi rounded toward zero,
-// lo the residual rounded to nearest even (|x - hi - lo| <= 2^-22 |x|, and
-// 2^-25 absolute below 2^-3; fp16 subnormals are kept by the conversion and
-// by the MFMA)
-__device__ __forceinline__ void split2(float a, float b, uint32_t& h, uint32_t& l) {
-    const f16x2 hh = __builtin_bit_cast(f16x2, __builtin_amdgcn_cvt_pkrtz(a, b));
-    const f16x2 lv = {(_Float16)(a - (float)hh[0]), (_Float16)(b - (float)hh[1])};
-    h = __builtin_bit_cast(uint32_t, hh);
-    l = __builtin_bit_cast(uint32_t, lv);
-}
-
-__device__ __forceinline__ v4f mfma(const f16x8& a, const f16x8& b, const v4f& c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
-}
-
-__device__ __forceinline__ f16x8 lds8(const uint16_t* p) {
-    return __builtin_bit_cast(f16x8, *reinterpret_cast<const uint4*>(p));
-}
-
-__device__ __forceinline__ uint2 ds_read_tr16(const uint16_t* p) {
-    return __builtin_bit_cast(
-        uint2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4i16*)(p)));
-}
-
-// Power-of-two scale s for values of largest finite magnitude m: m s in
-// [2^14, 2^15) (s within [2^-114, 2^126]); 1 for m == 0.  unit = 1 / s.
-__device__ __forceinline__ float p2_scale(float m) {
-    int eb = (__float_as_int(m) >> 23) & 0xff;
-    if (eb == 0) return 1.f;
-    eb = eb < 15 ? 15 : eb;
-    return __int_as_float((268 - eb) << 23);
-}
-__device__ __forceinline__ float p2_unit(float m) {
-    int eb = (__float_as_int(m) >> 23) & 0xff;
-    if (eb == 0) return 1.f;
-    eb = eb < 15 ? 15 : eb;
-    return __int_as_float((eb - 14) << 23);
-}
-
-// V's scale: 1 while the tile fits the fp16 split (so that consecutive
-// tiles' scales, whose ratio rescales the running output, stay equal on
-// ordinary data), else a power of two as for K
-__device__ __forceinline__ float v_scale(float m) { return m < 65504.0f ? 1.f : p2_scale(m); }
-__device__ __forceinline__ float v_unit(float m) { return m < 65504.0f ? 1.f : p2_unit(m); }
-
-// largest finite magnitude of m and 4 values (infinities and NaNs count as 0)
-__device__ __forceinline__ float max_fin4(float m, float4 f) {
-    auto fa = [](float x) {
-        const float a = fabsf(x);
-        return a < INFINITY ? a : 0.f;
-    };
-    return fmaxf(fmaxf(m, fmaxf(fa(f.x), fa(f.y))), fmaxf(fa(f.z), fa(f.w)));
-}
-
-__device__ __forceinline__ float4 ld_buf4(__amdgpu_buffer_rsrc_t r, int off) {
-    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
-    return make_float4(__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]),
-                       __uint_as_float(v[3]));
-}
 
 // lanes L, L ^ 16, L ^ 32, L ^ 48 (the four lane groups of one query)
 __device__ __forceinline__ float xgroup_max(float v) {
@@ -169,7 +105,7 @@ __global__ __launch_bounds__(kFlashThreads, 2) void k_flash_f32(const float* __r
     const float* Qh = Qg + (size_t)bh * Lq * D;
     const float* Kh = Kg + (size_t)bh * Lk * D;
     const float* Vh = Vg + (size_t)bh * Lk * D;
-    constexpr int kOob = 0x7ffffff0;
+    constexpr int kOob = kBufOob;
 
     // ---- Q: this wave's 16 rows as the B operand of S^T = K Q^T: lane
     // (query lr, group lg) holds dims 32 ks + 8 lg + 0..7, scaled by a
@@ -180,33 +116,32 @@ __global__ __launch_bounds__(kFlashThreads, 2) void k_flash_f32(const float* __r
     {
         float4 qv[G::KS][2];
         float mq = 0.f;
-        const __amdgpu_buffer_rsrc_t rq =
-            __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(Qh), 0, Lq * D * 4, 0x00020000);
+        const __amdgpu_buffer_rsrc_t rq = buf_rsrc(Qh, Lq * D * 4);
 #pragma unroll
         for (int ks = 0; ks < G::KS; ++ks)
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
                 const int d = 32 * ks + 8 * lg + 4 * h;
                 if constexpr (PEK == kPeNone) {
-                    qv[ks][h] = ld_buf4(rq, d < D ? (qrow * D + d) * 4 : kOob);
+                    qv[ks][h] = ld_buf_f4(rq, d < D ? (qrow * D + d) * 4 : kOob);
                 } else {
                     qv[ks][h] = make_float4(0.f, 0.f, 0.f, 0.f);
                     if (qrow < Lq && d < D)
                         qv[ks][h] = load_row4_pe<float, PEK>(Qh + (size_t)qrow * D, qrow, d, D, pq,
                                                              true);
                 }
-                mq = max_fin4(mq, qv[ks][h]);
+                mq = max_finite4(mq, qv[ks][h]);
             }
         mq = wave_max(mq);
-        const float sq = p2_scale(mq);
-        uq = p2_unit(mq);
+        const float sq = pow2_scale(mq);
+        uq = pow2_unit(mq);
 #pragma unroll
         for (int ks = 0; ks < G::KS; ++ks) {
             uint32_t h[4], l[4];
-            split2(qv[ks][0].x * sq, qv[ks][0].y * sq, h[0], l[0]);
-            split2(qv[ks][0].z * sq, qv[ks][0].w * sq, h[1], l[1]);
-            split2(qv[ks][1].x * sq, qv[ks][1].y * sq, h[2], l[2]);
-            split2(qv[ks][1].z * sq, qv[ks][1].w * sq, h[3], l[3]);
+            split2_f16(qv[ks][0].x * sq, qv[ks][0].y * sq, h[0], l[0]);
+            split2_f16(qv[ks][0].z * sq, qv[ks][0].w * sq, h[1], l[1]);
+            split2_f16(qv[ks][1].x * sq, qv[ks][1].y * sq, h[2], l[2]);
+            split2_f16(qv[ks][1].z * sq, qv[ks][1].w * sq, h[3], l[3]);
             qh[ks] = __builtin_bit_cast(f16x8, make_uint4(h[0], h[1], h[2], h[3]));
             ql[ks] = __builtin_bit_cast(f16x8, make_uint4(l[0], l[1], l[2], l[3]));
         }
@@ -215,10 +150,8 @@ __global__ __launch_bounds__(kFlashThreads, 2) void k_flash_f32(const float* __r
     // ---- K/V tile loads: thread t holds 16-byte vector t % VPR of rows
     // t / VPR + RSTEP i (rows past Lk and columns past D read as zeros)
     const int lrow = tid / G::VPR, lcol = (tid % G::VPR) * 4;
-    const __amdgpu_buffer_rsrc_t rk =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(Kh), 0, Lk * D * 4, 0x00020000);
-    const __amdgpu_buffer_rsrc_t rv =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(Vh), 0, Lk * D * 4, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rk = buf_rsrc(Kh, Lk * D * 4);
+    const __amdgpu_buffer_rsrc_t rv = buf_rsrc(Vh, Lk * D * 4);
     float4 kr[G::NLD], vr[G::NLD];
     auto issue = [&](int k0) {
 #pragma unroll
@@ -226,13 +159,13 @@ __global__ __launch_bounds__(kFlashThreads, 2) void k_flash_f32(const float* __r
             const int key = k0 + lrow + G::RSTEP * i;
             const int off = lcol < D ? (key * D + lcol) * 4 : kOob;
             if constexpr (PEK == kPeNone) {
-                kr[i] = ld_buf4(rk, off);
+                kr[i] = ld_buf_f4(rk, off);
             } else {
                 kr[i] = make_float4(0.f, 0.f, 0.f, 0.f);
                 if (key < Lk && lcol < D)
                     kr[i] = load_row4_pe<float, PEK>(Kh + (size_t)key * D, key, lcol, D, pk, true);
             }
-            vr[i] = ld_buf4(rv, off);
+            vr[i] = ld_buf_f4(rv, off);
         }
     };
 
@@ -254,8 +187,8 @@ __global__ __launch_bounds__(kFlashThreads, 2) void k_flash_f32(const float* __r
         float mk = 0.f, mv = 0.f;
 #pragma unroll
         for (int i = 0; i < G::NLD; ++i) {
-            mk = max_fin4(mk, kr[i]);
-            mv = max_fin4(mv, vr[i]);
+            mk = max_finite4(mk, kr[i]);
+            mv = max_finite4(mv, vr[i]);
         }
         mk = wave_max(mk);
         mv = wave_max(mv);
@@ -266,17 +199,17 @@ __global__ __launch_bounds__(kFlashThreads, 2) void k_flash_f32(const float* __r
         __syncthreads();
         mk = fmaxf(fmaxf(slot[0], slot[1]), fmaxf(slot[2], slot[3]));
         mv = fmaxf(fmaxf(slot[4], slot[5]), fmaxf(slot[6], slot[7]));
-        const float sk = p2_scale(mk), sv = v_scale(mv), uv = v_unit(mv);
+        const float sk = pow2_scale(mk), sv = range_scale(mv), uv = range_unit(mv);
 #pragma unroll
         for (int i = 0; i < G::NLD; ++i) {
             const int row = lrow + G::RSTEP * i;
             uint32_t h0, l0, h1, l1;
-            split2(kr[i].x * sk, kr[i].y * sk, h0, l0);
-            split2(kr[i].z * sk, kr[i].w * sk, h1, l1);
+            split2_f16(kr[i].x * sk, kr[i].y * sk, h0, l0);
+            split2_f16(kr[i].z * sk, kr[i].w * sk, h1, l1);
             *reinterpret_cast<uint2*>(smem + G::K_HI + row * G::KSTR + lcol) = make_uint2(h0, h1);
             *reinterpret_cast<uint2*>(smem + G::K_LO + row * G::KSTR + lcol) = make_uint2(l0, l1);
-            split2(vr[i].x * sv, vr[i].y * sv, h0, l0);
-            split2(vr[i].z * sv, vr[i].w * sv, h1, l1);
+            split2_f16(vr[i].x * sv, vr[i].y * sv, h0, l0);
+            split2_f16(vr[i].z * sv, vr[i].w * sv, h1, l1);
             *reinterpret_cast<uint2*>(smem + G::V_HI + row * G::VSTR + lcol) = make_uint2(h0, h1);
             *reinterpret_cast<uint2*>(smem + G::V_LO + row * G::VSTR + lcol) = make_uint2(l0, l1);
         }
@@ -292,15 +225,15 @@ __global__ __launch_bounds__(kFlashThreads, 2) void k_flash_f32(const float* __r
 #pragma unroll
             for (int j = 0; j < G::NJ; ++j) {
                 const int a = (16 * j + lr) * G::KSTR + 32 * ks + 8 * lg;
-                const f16x8 ah = lds8(smem + G::K_HI + a), al = lds8(smem + G::K_LO + a);
-                s[j] = mfma(ah, qh[ks], s[j]);
-                s[j] = mfma(ah, ql[ks], s[j]);
-                s[j] = mfma(al, qh[ks], s[j]);
+                const f16x8 ah = lds8_f16(smem + G::K_HI + a), al = lds8_f16(smem + G::K_LO + a);
+                s[j] = mfma_f16(ah, qh[ks], s[j]);
+                s[j] = mfma_f16(ah, ql[ks], s[j]);
+                s[j] = mfma_f16(al, qh[ks], s[j]);
             }
         }
 
         // ---- online softmax over the tile (keys past Lk score -inf)
-        const float c = scale * uq * p2_unit(mk);
+        const float c = scale * uq * pow2_unit(mk);
         float mt = -INFINITY;
 #pragma unroll
         for (int j = 0; j < G::NJ; ++j)
@@ -330,8 +263,8 @@ __global__ __launch_bounds__(kFlashThreads, 2) void k_flash_f32(const float* __r
                     p[r] = __expf(sj[r] - m_new);
                     ps += p[r];
                 }
-                split2(p[0] * 32768.f, p[1] * 32768.f, h[2 * half], l[2 * half]);
-                split2(p[2] * 32768.f, p[3] * 32768.f, h[2 * half + 1], l[2 * half + 1]);
+                split2_f16(p[0] * 32768.f, p[1] * 32768.f, h[2 * half], l[2 * half]);
+                split2_f16(p[2] * 32768.f, p[3] * 32768.f, h[2 * half + 1], l[2 * half + 1]);
             }
             ph[b] = __builtin_bit_cast(f16x8, make_uint4(h[0], h[1], h[2], h[3]));
             pl[b] = __builtin_bit_cast(f16x8, make_uint4(l[0], l[1], l[2], l[3]));
@@ -349,15 +282,15 @@ __global__ __launch_bounds__(kFlashThreads, 2) void k_flash_f32(const float* __r
 #pragma unroll
             for (int b = 0; b < G::NB; ++b) {
                 const int a = (32 * b + vrow) * G::VSTR + 16 * dt + vcol;
-                const uint2 h0 = ds_read_tr16(smem + G::V_HI + a);
-                const uint2 h1 = ds_read_tr16(smem + G::V_HI + a + 16 * G::VSTR);
-                const uint2 l0 = ds_read_tr16(smem + G::V_LO + a);
-                const uint2 l1 = ds_read_tr16(smem + G::V_LO + a + 16 * G::VSTR);
+                const uint2 h0 = lds_tr16(smem + G::V_HI + a);
+                const uint2 h1 = lds_tr16(smem + G::V_HI + a + 16 * G::VSTR);
+                const uint2 l0 = lds_tr16(smem + G::V_LO + a);
+                const uint2 l1 = lds_tr16(smem + G::V_LO + a + 16 * G::VSTR);
                 const f16x8 vh = __builtin_bit_cast(f16x8, make_uint4(h0.x, h0.y, h1.x, h1.y));
                 const f16x8 vl = __builtin_bit_cast(f16x8, make_uint4(l0.x, l0.y, l1.x, l1.y));
-                o[dt] = mfma(vh, ph[b], o[dt]);
-                o[dt] = mfma(vh, pl[b], o[dt]);
-                o[dt] = mfma(vl, ph[b], o[dt]);
+                o[dt] = mfma_f16(vh, ph[b], o[dt]);
+                o[dt] = mfma_f16(vh, pl[b], o[dt]);
+                o[dt] = mfma_f16(vl, ph[b], o[dt]);
             }
         }
     }

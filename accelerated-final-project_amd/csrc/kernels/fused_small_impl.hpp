@@ -97,6 +97,7 @@
 
 #include "common.hpp"
 #include "launch.hpp"
+#include "split16.hpp"
 
 namespace atn {
 
@@ -150,10 +151,7 @@ int fused_small_per_cu_bf16_xl(int lds);
 
 namespace {
 
-typedef float v4f __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kThreads = 256;
 constexpr int kSpinLimit = 1 << 18;  // polls (each >= one memory round trip): ~0.3 s bound
@@ -497,55 +495,13 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
     return __builtin_bit_cast(uint32_t, v);
 }
 
-// hi + lo parts of two values, packed: bf16 parts (hi rounded to nearest
-// even, lo the residual rounded; 16 significant bits) ...
+// hi + lo bf16 parts of two values, packed (hi rounded to nearest even, lo
+// the residual rounded; 16 significant bits): the split of bf16 inputs
+// after a positional encoding (fp32 inputs use split2_f16, split16.hpp)
 __device__ __forceinline__ void split2_bf16(float a, float b, uint32_t& h, uint32_t& l) {
     h = pack_bf16x2(a, b);
     l = pack_bf16x2(a - __uint_as_float(h << 16), b - __uint_as_float(h & 0xffff0000u));
 }
-// ... or fp16 parts: hi = x rounded toward zero (v_cvt_pkrtz_f16_f32, whose
-// result the residuals are formed from), lo = the residual rounded to
-// nearest even (v_cvt_pk_f16_f32; fp16 subnormals are kept, and the MFMA
-// keeps them): |x - hi - lo| <= 2^-22 |x| for |x| >= 2^-3 (hi then 11
-// significant bits, the residual below one fp16 ulp of x) and <= 2^-25
-// below; needs |x| < 65504.
-__device__ __forceinline__ void split2_f16(float a, float b, uint32_t& h, uint32_t& l) {
-    const f16x2 hh = __builtin_bit_cast(f16x2, __builtin_amdgcn_cvt_pkrtz(a, b));
-    const f16x2 lv = {(_Float16)(a - (float)hh[0]), (_Float16)(b - (float)hh[1])};
-    h = __builtin_bit_cast(uint32_t, hh);
-    l = __builtin_bit_cast(uint32_t, lv);
-}
-
-// Largest magnitude an fp32 operand may have for the fp16 split.
-constexpr float kF16Range = 65504.0f;
-
-// Power-of-two scale s for a slice of largest magnitude m (m >= 0) that
-// does not fit the fp16 split: m s in [2^14, 2^15) (s = 2^(14 - e) for m in
-// [2^e, 2^(e+1)), kept within [2^-114, 2^126]), so every scaled value
-// converts without overflow; the unit 1 / s undoes it exactly.
-__device__ __forceinline__ float pow2_scale(float m) {
-    int eb = (__float_as_int(m) >> 23) & 0xff;
-    if (eb == 0) return 1.f;
-    eb = eb < 15 ? 15 : eb;
-    return __int_as_float((268 - eb) << 23);
-}
-// The largest finite magnitude of m and the 4 values (infinities and NaNs
-// count as 0: they stay non-finite through the scaling, and must not set the
-// scale of the finite values beside them).
-__device__ __forceinline__ float max_finite4(float m, float4 f) {
-    auto fa = [](float x) {
-        const float a = fabsf(x);
-        return a < INFINITY ? a : 0.f;
-    };
-    return fmaxf(fmaxf(m, fmaxf(fa(f.x), fa(f.y))), fmaxf(fa(f.z), fa(f.w)));
-}
-__device__ __forceinline__ float pow2_unit(float m) {
-    int eb = (__float_as_int(m) >> 23) & 0xff;
-    if (eb == 0) return 1.f;
-    eb = eb < 15 ? 15 : eb;
-    return __int_as_float((eb - 14) << 23);
-}
-
 // NT independent 16x16 MFMA accumulations sharing one A operand (k step
 // 32, 8 elements per lane, contiguous along k; VT = bf16x8 or f16x8):
 // acc[u] += A B_u^T over k in [0, kdim), where lane (lr, lk) reads A at a
@@ -591,7 +547,6 @@ __device__ __forceinline__ void mma16(const uint16_t* a, const uint16_t* a_lo, c
     }
 }
 
-typedef short v4i16 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ v4i16 ds_read_tr16(const uint16_t* p) {
     return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4i16*)(p));
 }

@@ -21,6 +21,14 @@ hipError_t launch_softmax(const float* S, float* P, long rows, int Lk, int nspli
                           size_t split_stride, float scale, hipStream_t st);
 hipError_t launch_pv(int dtype, const float* P, const void* V, void* O, int BH, int Lq, int Lk,
                      int D, int vec_ok, hipStream_t st);
+// Stages 1 and 3 for fp32 on 16-bit MFMA (stream16.hip; launch_qk_partial
+// and launch_pv choose them for fp32 with head_d % 4 == 0, 16-byte aligned
+// bases and per-head byte offsets under 2^31).
+hipError_t launch_qk_s16(int pek, const float* Q, const float* K, float* S, int BH, int Lq, int Lk,
+                         int D, int dchunk, int nsplit, const PeSide& pq, const PeSide& pk,
+                         hipStream_t st);
+hipError_t launch_pv_s16(const float* P, const float* V, float* O, int BH, int Lq, int Lk, int D,
+                         hipStream_t st);
 // Single-launch split-D kernel for len_q <= 64, len_k <= 128 (fused_small.hip):
 // row groups of MB query rows, D slices of dc dims; gather1 selects the
 // one-gather exchange (each thread polls (MB*NK/256) * nchunk <= 64 words)

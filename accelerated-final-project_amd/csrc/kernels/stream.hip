@@ -11,7 +11,9 @@
 //            workgroup per (bh, 64x64 score tile, D-chunk) -- every Q/K element
 //            is read once when the tile covers Lq x Lk;
 //   stage 2  k_softmax     P = softmax(scale * sum_split S_part) per row, exact
-//            (max, exp, sum, divide -- final/attention.cu:262-270 order);
+//            (max, exp, sum, divide -- final/attention.cu:262-270 order),
+//            written scaled by 2^15 (p / (l 2^-15) = 2^15 (p / l) exactly), so
+//            that the 16-bit PV operands keep small probabilities' bits;
 //   stage 3  k_pv          O[bh][i][d] = sum_j P_ij V_jd, one workgroup per
 //            (bh, 64 rows, 64 dims) -- every V element is read once per
 //            64-row query block.
@@ -19,7 +21,9 @@
 // All math is fp32; bf16 storage is widened at load and rounded (RNE) once
 // at the final store.  Workgroups are 256 threads (4 waves) computing 64x64
 // tiles, a 32x32 quadrant per wave on fp32 MFMA, from LDS-staged 32-deep
-// slices.
+// slices.  fp32 calls with head_d % 4 == 0 and 16-byte aligned bases run
+// stages 1 and 3 on 16-bit MFMA instead (stream16.hip); these kernels serve
+// bf16 (head_d % 8 != 0 or misaligned), odd head dims and misaligned fp32.
 #include <algorithm>
 
 #include "common.hpp"
@@ -32,6 +36,7 @@ namespace {
 constexpr int kTile = 64;   // rows x cols of an output tile
 constexpr int kDepth = 32;  // contraction slice staged in LDS per step (loaded in two halves)
 constexpr int kPad = 4;     // LDS row padding (floats), keeps float4 alignment
+constexpr float kPInv = 1.0f / 32768.0f;  // P is stored times 2^15
 
 typedef float v16f __attribute__((ext_vector_type(16)));
 
@@ -163,7 +168,8 @@ __global__ __launch_bounds__(256) void k_softmax(const float* __restrict__ S, fl
         if (lane == 0) red_sum[wid] = l;
         __syncthreads();
         l = (red_sum[0] + red_sum[1]) + (red_sum[2] + red_sum[3]);
-        for (int j = tid; j < Lk; j += 256) p[j] = p[j] / l;
+        const float l15 = l * kPInv;  // P written times 2^15 (exact)
+        for (int j = tid; j < Lk; j += 256) p[j] = p[j] / l15;
         __syncthreads();  // red_* reused by the next row
     }
 }
@@ -201,7 +207,7 @@ __global__ __launch_bounds__(256) void k_softmax_rows(const float* __restrict__ 
             v[u] = lane + 64 * u < Lk ? expf(v[u] - m) : 0.f;
             l += v[u];
         }
-        l = wave_sum(l);
+        l = wave_sum(l) * kPInv;  // P written times 2^15 (exact)
 #pragma unroll
         for (int u = 0; u < NPL; ++u) {
             const int j = lane + 64 * u;
@@ -288,7 +294,8 @@ __global__ __launch_bounds__(256) void k_pv(const float* __restrict__ P, const T
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
         const int row = q0 + mfma_row(wm, lane, r);
-        if (row < Lq && dd < D) Elem<T>::st(O + ((size_t)bh * Lq + row) * D, dd, acc[r]);
+        if (row < Lq && dd < D)
+            Elem<T>::st(O + ((size_t)bh * Lq + row) * D, dd, acc[r] * kPInv);  // P's 2^15
     }
 }
 
@@ -375,9 +382,21 @@ hipError_t pe_apply_t(int pek, const void* in, void* out, long n_rows, int seq_l
 
 }  // namespace
 
+// fp32 with head_d % 4 == 0 and 16-byte aligned bases takes the 16-bit
+// MFMA forms (stream16.hip), while every per-head byte offset fits the
+// 32-bit buffer offsets they use.
+static bool s16_ok(int dtype, int vec_ok, int Lq, int Lk, int D) {
+    const long long lim = 1LL << 31;
+    return dtype == kDtypeF32 && vec_ok && D % 4 == 0 && (long long)Lq * D * 4 < lim &&
+           (long long)Lk * D * 4 < lim && (long long)Lq * Lk * 4 < lim;
+}
+
 hipError_t launch_qk_partial(int dtype, int pek, const void* Q, const void* K, float* S, int BH,
                              int Lq, int Lk, int D, int dchunk, int nsplit, const PeSide& pq,
                              const PeSide& pk, int vec_ok, hipStream_t st) {
+    if (s16_ok(dtype, vec_ok, Lq, Lk, D))
+        return launch_qk_s16(pek, static_cast<const float*>(Q), static_cast<const float*>(K), S,
+                             BH, Lq, Lk, D, dchunk, nsplit, pq, pk, st);
     if (dtype == kDtypeF32)
         return qk_partial_t<float>(pek, Q, K, S, BH, Lq, Lk, D, dchunk, nsplit, pq, pk, vec_ok,
                                    st);
@@ -413,6 +432,9 @@ hipError_t launch_softmax(const float* S, float* P, long rows, int Lk, int nspli
 
 hipError_t launch_pv(int dtype, const float* P, const void* V, void* O, int BH, int Lq, int Lk,
                      int D, int vec_ok, hipStream_t st) {
+    if (s16_ok(dtype, vec_ok, Lq, Lk, D))
+        return launch_pv_s16(P, static_cast<const float*>(V), static_cast<float*>(O), BH, Lq, Lk,
+                             D, st);
     const int tiles_q = (Lq + kTile - 1) / kTile, tiles_d = (D + kTile - 1) / kTile;
     const dim3 grid((unsigned)((long)BH * tiles_q * tiles_d)), block(256);
     if (dtype == kDtypeF32) {

@@ -404,3 +404,29 @@ def test_sinusoidal_bf16(am, dev, shape):
     ref = oracle.attention_sinusoidal(Q, K, V, st, ct, nthreads=16)
     n, nrel, mabs = H.check_bf16(out.numpy(), ref)
     assert n == 0, f"normwise rel {nrel}, max abs {mabs}"
+
+
+@pytest.mark.parametrize("exps", [(17, -17, 0), (0, 0, 19), (17, -17, 21), (-12, -12, -12)],
+                         ids=["qk-big", "v-big", "all-big", "all-small"])
+@pytest.mark.parametrize("shape", [(1, 3, 100, 130, 520), (1, 3, 70, 300, 1024)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_split_d_outside_fp16_range(am, dev, shape, exps):
+    """fp32 beyond the single-launch window with head_d > 256 runs the
+    split-D pipeline, whose contractions use the fp16 split too: a stage
+    with a value outside fp16's range is staged again with power-of-two
+    scales.  Head 1 is scaled by 2^eq, 2^ek, 2^ev (exact); its output is
+    compared in units of 2^ev with the oracle on the unscaled V."""
+    B, Hh, Lq, Lk, D = shape
+    eq, ek, ev = exps
+    print(f"[case] split-D f32 scaled 2^{exps} {shape}", flush=True)
+    assert am.path(0, B, Hh, Lq, Lk, D) == am.ATN_PATH_SPLIT_D
+    Q, K, V = H.rng_inputs((B, Hh, Lq, D), (B, Hh, Lk, D), seed=37 + D)
+    Q[:, 1] *= np.float32(2.0 ** eq)
+    K[:, 1] *= np.float32(2.0 ** ek)
+    Vs = V.copy()
+    Vs[:, 1] *= np.float32(2.0 ** ev)
+    got = _f32_call(am.attention_forward_optimized, Q, K, Vs)
+    assert np.isfinite(got).all()
+    got[:, 1] *= np.float32(2.0 ** -ev)
+    n, mabs, mrel = H.check_f32(got, oracle.attention(Q, K, V, nthreads=16))
+    assert n == 0, f"{n} mismatches, max abs {mabs}, max rel {mrel}"
