@@ -75,6 +75,11 @@ def parse():
     ap.add_argument("--config", type=int, default=0, choices=[0] + sorted(CONFIGS),
                     help="one config only (0 = headline config 2 plus every other config)")
     ap.add_argument("--head-dim", type=int, default=0, help="override D (config-2 sweep)")
+    ap.add_argument("--shape", default="", metavar="B,H,LQ,LK,D",
+                    help="time this fp32 shape instead (no encoding; for profiling the flash "
+                         "and split-D paths)")
+    ap.add_argument("--no-flash", action="store_true",
+                    help="keep fp32 calls off the flash kernel (atn_tuning.no_flash)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="CPU-oracle sample time of the headline (0 = skip every CPU baseline)")
     ap.add_argument("--cpu-seconds-other", type=float, default=3.0,
@@ -420,6 +425,12 @@ def main():
         sys.exit(1)
     head_cfg_id = a.config or 2
     cfg = list(CONFIGS[head_cfg_id])
+    if a.no_flash:
+        am.set_tuning(no_flash=True)
+    if a.shape:
+        b_, h_, lq_, lk_, d_ = (int(x) for x in a.shape.split(","))
+        cfg = [f"fp32 SDPA ({b_},{h_},{lq_},{lk_},{d_})", "f32", b_, h_, lq_, lk_, d_, "none", 1.0]
+        head_cfg_id = 0
     if a.head_dim:
         cfg[6] = a.head_dim
         cfg[0] = cfg[0].split(" (")[0] + f" ({cfg[2]},{cfg[3]},{cfg[4]},{cfg[5]},{cfg[6]})"
@@ -429,7 +440,7 @@ def main():
           file=sys.stderr, flush=True)
 
     res, host, rows_fn = run_config(am, hip_rt, cfg, a.steps, a.warmup, a.seed,
-                                    cold=head_cfg_id <= 3)
+                                    cold=1 <= head_cfg_id <= 3)
     if a.calib_copy > 0:
         n = a.calib_copy << 20
         src, dst = hip_rt.DeviceArray((n // 4,), "f32", fill=0), hip_rt.DeviceArray((n // 4,), "f32")
@@ -483,7 +494,7 @@ def main():
 
     all_ok = check["ok"]
     per_config = None
-    if a.config == 0:
+    if a.config == 0 and not a.shape:
         per_config = {}
         others = [(f"cfg2_D{d}", 2, d) for d in SWEEP_D] + [(f"cfg{c}", c, 0) for c in (1, 3, 4, 5)]
         for key, cid, dov in others:
