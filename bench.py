@@ -42,6 +42,8 @@ import numpy as np  # noqa: E402
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
 FP32_PEAK_TFLOPS = 157.3
+# fp32 work carried as three fp16 MFMA products (the hi + lo split)
+F32_SPLIT_PEAK_TFLOPS = BF16_PEAK_TFLOPS / 3
 MALL_FLUSH_MIB = 512  # > the 256 MiB MALL: a copy this large evicts it
 
 # HBM traffic per launch of the dominant kernel, measured with rocprofv3
@@ -402,11 +404,15 @@ def summarize(cfg, res):
     ms = res["ms_per_step"]
     gbs = alg_bytes / (ms * 1e-3) / 1e9
     tflops = flops / (ms * 1e-3) / 1e12
-    bound = "hbm" if flops / alg_bytes < (312 if dtype == "bf16" else 19.7) else "mfma"
+    # fp32 work runs on fp16 matrix cores as three products of hi + lo parts
+    # per fp32 product: its matrix ceiling is the fp16 rate / 3 (ridge 104
+    # FLOP/B), above fp32 MFMA's 157.3 TFLOP/s
+    mpeak = BF16_PEAK_TFLOPS if dtype == "bf16" else F32_SPLIT_PEAK_TFLOPS
+    bound = "hbm" if flops / alg_bytes < mpeak * 1e12 / (HBM_PEAK_GBS * 1e9) else "mfma"
     if bound == "hbm":
         frac = gbs / HBM_PEAK_GBS
     else:
-        frac = tflops / (BF16_PEAK_TFLOPS if dtype == "bf16" else FP32_PEAK_TFLOPS)
+        frac = tflops / mpeak
     return alg_bytes, flops, gbs, tflops, bound, frac
 
 
@@ -457,9 +463,13 @@ def main():
         roof = {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(frac, 4), "traffic": traffic}
     else:
-        peak = BF16_PEAK_TFLOPS if dtype == "bf16" else FP32_PEAK_TFLOPS
+        peak = BF16_PEAK_TFLOPS if dtype == "bf16" else F32_SPLIT_PEAK_TFLOPS
         roof = {"bound": "mfma", "achieved": round(tflops, 2), "peak": peak, "unit": "TFLOP/s",
                 "frac": round(frac, 4), "traffic": traffic}
+        if dtype == "f32":
+            roof["peak_note"] = ("fp32 work as three fp16 MFMA products (hi + lo parts): the "
+                                 "fp16 dense rate 2500 / 3; fp32 MFMA's own peak is "
+                                 f"{FP32_PEAK_TFLOPS} TFLOP/s")
     path = res["path"]
     roof["kernel"] = {
         am.ATN_PATH_FUSED_SMALL: "k_fused_small (one launch per step)",
