@@ -74,7 +74,7 @@ class Tuning(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int) for n in (
         "fused_rows", "fused_dc", "fused_exchange", "fused_xcd", "no_fused", "no_flash",
         "gemm_fused_k",
-        "workspace_cap_mib", "model_cus", "model_xccs", "preset_status")]
+        "workspace_cap_mib", "model_cus", "model_xccs", "preset_status", "flash_waves")]
 
 
 class FusedPlanInfo(ctypes.Structure):
@@ -184,11 +184,13 @@ _FUSED_K = {None: 0, "on": 1, "off": 2}
 def set_tuning(fused_rows: int = 0, fused_dc: int = 0, fused_exchange: str | None = None,
                fused_xcd: str | None = None, no_fused: bool = False, no_flash: bool = False,
                gemm_fused_k: str | None = None, workspace_cap_mib: int = 0, model_cus: int = 0,
-               model_xccs: int = 0, preset_status: bool = False) -> None:
+               model_xccs: int = 0, preset_status: bool = False, flash_waves: int = 0) -> None:
     """atn_set_tuning_ex with named fields (every field not given is reset)."""
+    if flash_waves not in (0, 4, 8):
+        raise ValueError("flash_waves is 4, 8 or 0 (by grid size)")
     t = Tuning(fused_rows, fused_dc, _EXCHANGE[fused_exchange], _SCOPE[fused_xcd],
                int(no_fused), int(no_flash), _FUSED_K[gemm_fused_k], workspace_cap_mib,
-               model_cus, model_xccs, int(preset_status))
+               model_cus, model_xccs, int(preset_status), flash_waves)
     st = lib().atn_set_tuning_ex(ctypes.byref(t))
     if st != ATN_OK:
         raise AtnError(st, "atn_set_tuning_ex")

@@ -749,6 +749,26 @@ bool flash_ok(int dtype, const Shape& s, const PePlan& plan) {
            (int64_t)s.Lq * s.D * 4 < lim && (int64_t)s.Lk * s.D * 4 < lim;
 }
 
+// Workgroup size of the flash kernel, in waves (16 query rows each): 8
+// waves convert each K/V tile once for 128 rows, which pays when the grid of
+// 128-row blocks still gives every CU a workgroup; smaller grids take 4
+// waves (twice the workgroups).  atn_tuning.flash_waves forces either.
+int flash_waves(const Shape& s, int dev) {
+    const int forced = tune().flash_waves;
+    if (forced == 4 || forced == 8) return forced;
+    int cus = 0;
+    {
+        std::lock_guard<std::mutex> lk(g_mu);
+        DeviceState& ds = g_dev[dev];
+        if (ds.cus == 0 &&
+            hipDeviceGetAttribute(&ds.cus, hipDeviceAttributeMultiprocessorCount, dev) !=
+                hipSuccess)
+            ds.cus = 0;
+        cus = ds.cus > 0 ? ds.cus : 256;
+    }
+    return s.BH * ((s.Lq + 127) / 128) >= (int64_t)cus ? 8 : 4;
+}
+
 // Scratch bytes of the path a call of shape s takes: fused (when planned and
 // vector-aligned), else GEMM (when planned and 16-byte aligned), else the
 // split-D pipeline.  vec / a16: the alignment of the call's pointers; pass
@@ -918,7 +938,7 @@ int attention_run(int dtype, const void* Q, const void* K, const void* V, void* 
         return ATN_OK;
     }
     if (use_flash) {
-        ATN_HIP(atn::launch_flash(plan.pek, static_cast<const float*>(Q),
+        ATN_HIP(atn::launch_flash(plan.pek, flash_waves(s, dev), static_cast<const float*>(Q),
                                   static_cast<const float*>(K), static_cast<const float*>(V),
                                   static_cast<float*>(out), (int)s.BH, Lq, Lk, D, scale, plan.q,
                                   plan.k, stream));

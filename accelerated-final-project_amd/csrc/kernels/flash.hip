@@ -3,10 +3,12 @@
 //
 // The reference's kernel (final/attention.cu:84-191) walks the keys of one
 // query row in 64-key tiles with an online softmax and keeps the running
-// output in global memory.  Here a workgroup owns 64 query rows (16 per
-// wave) of one head and walks the head's keys in tiles of KT keys (64 for
-// D <= 128 without an encoding, else 32), with the running output of its
-// rows in registers:
+// output in global memory.  Here a workgroup owns 64 or 128 query rows (16
+// per wave, 4 or 8 waves) of one head and walks the head's keys in tiles of
+// KT keys (64 for D <= 128 without an encoding, else 32; at least one load
+// round of the workgroup), with the running output of its rows in
+// registers.  8 waves convert each K/V tile once for twice the rows, 4
+// waves make twice the workgroups for grids that would not fill the chip:
 //
 //   per tile: K and V rows are loaded (16-byte loads, the next tile's in
 //   flight while this one computes), K scaled by a power of two from the
@@ -31,7 +33,7 @@
 //   of consecutive V tiles' scales.
 //
 // The score matrix never reaches memory: per call the kernel reads Q once
-// and K and V once per 64-row query block, and writes O once.  Positional
+// and K and V once per query block, and writes O once.  Positional
 // encodings (RoPE, sinusoidal) are applied to Q and K at load.
 #include <algorithm>
 
@@ -43,21 +45,22 @@ namespace atn {
 
 namespace {
 
-constexpr int kFlashThreads = 256;
-constexpr int kFlashRows = 64;  // query rows per workgroup, 16 per wave
-
-// Tiling for head dims padded to DP (32, 64, 128 or 256); with a
+// Tiling for head dims padded to DP (32, 64, 128 or 256) and NW waves per
+// workgroup (4 or 8; 16 query rows each, sharing each K/V tile); with a
 // positional encoding (PE) the key tile is 32 keys (the encoding's table
 // loads need the registers of half the prefetched rows).
-template <int DP, bool PE>
+template <int DP, bool PE, int NW>
 struct FlashGeo {
-    static constexpr int KT = DP <= 128 && !PE ? 64 : 32;  // keys per tile
+    static constexpr int THREADS = 64 * NW, ROWS = 16 * NW;
+    // keys per tile, at least one load round of rows
+    static constexpr int KT0 = DP <= 128 && !PE ? 64 : 32;
+    static constexpr int KT = KT0 > THREADS / (DP / 4) ? KT0 : THREADS / (DP / 4);
     static constexpr int KS = DP / 32;              // 32-deep steps of Q K^T
     static constexpr int NJ = KT / 16;              // 16-key tiles of S^T
     static constexpr int NB = KT / 32;              // 32-key blocks of P V
     static constexpr int NDT = DP / 16;             // 16-dim tiles of O^T
     static constexpr int VPR = DP / 4;              // 16-byte vectors per row
-    static constexpr int RSTEP = kFlashThreads / VPR;  // rows per load round
+    static constexpr int RSTEP = THREADS / VPR;     // rows per load round
     static constexpr int NLD = KT / RSTEP;             // load rounds per tile
     // LDS rows in 16-bit elements: K padded by 8 (16-byte fragment reads),
     // V by 16 (the transposing read's 4 rows x 32 bytes in distinct banks)
@@ -78,18 +81,18 @@ __device__ __forceinline__ float xgroup_sum(float v) {
     return v + __shfl_xor(v, 32);
 }
 
-template <int DP, int PEK>
-__global__ __launch_bounds__(kFlashThreads, 2) void k_flash_f32(const float* __restrict__ Qg,
+template <int DP, int PEK, int NW>
+__global__ __launch_bounds__(64 * NW, 8 / NW) void k_flash_f32(const float* __restrict__ Qg,
                                                                  const float* __restrict__ Kg,
                                                                  const float* __restrict__ Vg,
                                                                  float* __restrict__ Og, int Lq,
                                                                  int Lk, int D, int qblocks,
                                                                  float scale, PeSide pq,
                                                                  PeSide pk) {
-    using G = FlashGeo<DP, PEK != kPeNone>;
+    using G = FlashGeo<DP, PEK != kPeNone, NW>;
     extern __shared__ __align__(16) unsigned char smem_raw[];
     uint16_t* smem = reinterpret_cast<uint16_t*>(smem_raw);
-    __shared__ float slot[8];
+    __shared__ float slot[2 * NW];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -101,7 +104,7 @@ __global__ __launch_bounds__(kFlashThreads, 2) void k_flash_f32(const float* __r
     int id = (int)blockIdx.x;
     if ((nwg & 7) == 0) id = (id & 7) * (nwg >> 3) + (id >> 3);
     const int bh = id / qblocks, qb = id - bh * qblocks;
-    const int q0 = qb * kFlashRows;
+    const int q0 = qb * G::ROWS;
     const float* Qh = Qg + (size_t)bh * Lq * D;
     const float* Kh = Kg + (size_t)bh * Lk * D;
     const float* Vh = Vg + (size_t)bh * Lk * D;
@@ -194,11 +197,16 @@ __global__ __launch_bounds__(kFlashThreads, 2) void k_flash_f32(const float* __r
         mv = wave_max(mv);
         if (lane == 0) {
             slot[wave] = mk;
-            slot[4 + wave] = mv;
+            slot[NW + wave] = mv;
         }
         __syncthreads();
-        mk = fmaxf(fmaxf(slot[0], slot[1]), fmaxf(slot[2], slot[3]));
-        mv = fmaxf(fmaxf(slot[4], slot[5]), fmaxf(slot[6], slot[7]));
+        mk = slot[0];
+        mv = slot[NW];
+#pragma unroll
+        for (int w = 1; w < NW; ++w) {
+            mk = fmaxf(mk, slot[w]);
+            mv = fmaxf(mv, slot[NW + w]);
+        }
         const float sk = pow2_scale(mk), sv = range_scale(mv), uv = range_unit(mv);
 #pragma unroll
         for (int i = 0; i < G::NLD; ++i) {
@@ -311,34 +319,44 @@ __global__ __launch_bounds__(kFlashThreads, 2) void k_flash_f32(const float* __r
     }
 }
 
-template <int DP, int PEK>
+template <int DP, int PEK, int NW>
 hipError_t launch_t(const float* Q, const float* K, const float* V, float* O, int BH, int Lq,
                     int Lk, int D, float scale, const PeSide& pq, const PeSide& pk,
                     hipStream_t st) {
-    constexpr int lds = FlashGeo<DP, PEK != kPeNone>::BYTES;
+    using G = FlashGeo<DP, PEK != kPeNone, NW>;
     static bool attr = false;
     if (!attr) {
-        hipError_t e = hipFuncSetAttribute((const void*)k_flash_f32<DP, PEK>,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+        hipError_t e = hipFuncSetAttribute((const void*)k_flash_f32<DP, PEK, NW>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, G::BYTES);
         if (e != hipSuccess) return e;
         attr = true;
     }
-    const int qblocks = (Lq + kFlashRows - 1) / kFlashRows;
-    hipLaunchKernelGGL((k_flash_f32<DP, PEK>), dim3((unsigned)(BH * qblocks)),
-                       dim3(kFlashThreads), lds, st, Q, K, V, O, Lq, Lk, D, qblocks, scale, pq, pk);
+    const int qblocks = (Lq + G::ROWS - 1) / G::ROWS;
+    hipLaunchKernelGGL((k_flash_f32<DP, PEK, NW>), dim3((unsigned)(BH * qblocks)),
+                       dim3(G::THREADS), G::BYTES, st, Q, K, V, O, Lq, Lk, D, qblocks, scale, pq,
+                       pk);
     return hipGetLastError();
 }
 
-template <int PEK>
+template <int PEK, int NW>
 hipError_t launch_pe(const float* Q, const float* K, const float* V, float* O, int BH, int Lq,
                      int Lk, int D, float scale, const PeSide& pq, const PeSide& pk,
                      hipStream_t st) {
-    if (D <= 32) return launch_t<32, PEK>(Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk, st);
-    if (D <= 64) return launch_t<64, PEK>(Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk, st);
-    if (D <= 128) return launch_t<128, PEK>(Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk, st);
+    if (D <= 32) return launch_t<32, PEK, NW>(Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk, st);
+    if (D <= 64) return launch_t<64, PEK, NW>(Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk, st);
+    if (D <= 128) return launch_t<128, PEK, NW>(Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk, st);
     if constexpr (PEK == kPeNone)
-        return launch_t<256, PEK>(Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk, st);
+        return launch_t<256, PEK, NW>(Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk, st);
     return hipErrorInvalidValue;  // flash_supported: encoded calls have D <= 128
+}
+
+template <int PEK>
+hipError_t launch_w(int waves, const float* Q, const float* K, const float* V, float* O, int BH,
+                    int Lq, int Lk, int D, float scale, const PeSide& pq, const PeSide& pk,
+                    hipStream_t st) {
+    if (waves == 8) return launch_pe<PEK, 8>(Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk, st);
+    if (waves == 4) return launch_pe<PEK, 4>(Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk, st);
+    return hipErrorInvalidValue;
 }
 
 }  // namespace
@@ -348,17 +366,19 @@ bool flash_supported(int dtype, int pek, int D) {
            D <= (pek == kPeNone ? kFlashMaxD : kFlashMaxDEncoded);
 }
 
-hipError_t launch_flash(int pek, const float* Q, const float* K, const float* V, float* O,
-                        int BH, int Lq, int Lk, int D, float scale, const PeSide& pq,
+hipError_t launch_flash(int pek, int waves, const float* Q, const float* K, const float* V,
+                        float* O, int BH, int Lq, int Lk, int D, float scale, const PeSide& pq,
                         const PeSide& pk, hipStream_t st) {
     switch (pek) {
-        case kPeNone: return launch_pe<kPeNone>(Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk, st);
+        case kPeNone:
+            return launch_w<kPeNone>(waves, Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk, st);
         case kPeRopeInterleaved:
-            return launch_pe<kPeRopeInterleaved>(Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk, st);
+            return launch_w<kPeRopeInterleaved>(waves, Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk,
+                                                st);
         case kPeRopeHalf:
-            return launch_pe<kPeRopeHalf>(Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk, st);
+            return launch_w<kPeRopeHalf>(waves, Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk, st);
         case kPeSinusoidal:
-            return launch_pe<kPeSinusoidal>(Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk, st);
+            return launch_w<kPeSinusoidal>(waves, Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk, st);
         default: return hipErrorInvalidValue;
     }
 }

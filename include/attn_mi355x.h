@@ -331,6 +331,8 @@ typedef struct atn_tuning {
                               its workspace's status word set, as a timed-out call leaves
                               it, so its workgroups take the fail-closed exit (no wait is
                               entered) */
+    int flash_waves;       /* flash kernel: 4 or 8 waves (64 or 128 query rows) per
+                              workgroup; 0: by grid size */
 } atn_tuning;
 /* Replaces the overrides (NULL: all zero) and drops cached plans.  Plans
  * that a forced setting makes impossible fall back to the library's

@@ -46,6 +46,34 @@ def test_flash_f32(am, dev, shape):
     assert n == 0, f"{n} mismatches, max abs {mabs}, max rel {mrel}"
 
 
+@pytest.mark.parametrize("waves", [4, 8])
+@pytest.mark.parametrize("shape,pe", [((1, 3, 130, 129, 32), None), ((1, 2, 200, 300, 128), None),
+                                      ((1, 2, 96, 200, 256), None), ((1, 2, 129, 97, 64), "rope"),
+                                      ((1, 2, 150, 333, 128), "sinusoidal")],
+                         ids=lambda v: "x".join(map(str, v)) if isinstance(v, tuple) else str(v))
+def test_flash_workgroup_forms(am, dev, tuner, waves, shape, pe):
+    """Both workgroup sizes (4 and 8 waves: 64- and 128-row query blocks,
+    key tiles of at least one load round) forced on the same inputs."""
+    B, Hh, Lq, Lk, D = shape
+    print(f"[case] flash f32 {waves} waves {shape} {pe}", flush=True)
+    tuner.set(flash_waves=waves)
+    Q, K, V = H.rng_inputs((B, Hh, Lq, D), (B, Hh, Lk, D), seed=7 + Lk + waves,
+                           sigma=0.5 if pe == "sinusoidal" else 1.0)
+    desc = None if pe is None else am.make_pe(pe)
+    got = _f32_call(am, Q, K, V, desc)
+    L = max(Lq, Lk)
+    if pe == "sinusoidal":
+        st, ct = oracle.sinusoidal_table(L, D)
+        ref = oracle.attention_sinusoidal(Q, K, V, st, ct, nthreads=16)
+    elif pe == "rope":
+        c, s = oracle.rope_cache(L, D)
+        ref = oracle.attention_rope(Q, K, V, c, s, rotary_dim=D, nthreads=16)
+    else:
+        ref = oracle.attention(Q, K, V, nthreads=16)
+    n, mabs, mrel = H.check_f32(got, ref)
+    assert n == 0, f"{n} mismatches, max abs {mabs}, max rel {mrel}"
+
+
 def test_flash_reference_long_shape(am, dev):
     """The reference's long-sequence test shape (final/attention.cu:522)."""
     B, Hh, L, D = 4, 32, 512, 128
