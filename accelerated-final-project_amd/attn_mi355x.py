@@ -187,7 +187,7 @@ def set_tuning(fused_rows: int = 0, fused_dc: int = 0, fused_exchange: str | Non
                model_xccs: int = 0, preset_status: bool = False, flash_waves: int = 0) -> None:
     """atn_set_tuning_ex with named fields (every field not given is reset)."""
     if flash_waves not in (0, 4, 8):
-        raise ValueError("flash_waves is 4, 8 or 0 (by grid size)")
+        raise ValueError("flash_waves is 4, 8 or 0 (the default, 8)")
     t = Tuning(fused_rows, fused_dc, _EXCHANGE[fused_exchange], _SCOPE[fused_xcd],
                int(no_fused), int(no_flash), _FUSED_K[gemm_fused_k], workspace_cap_mib,
                model_cus, model_xccs, int(preset_status), flash_waves)

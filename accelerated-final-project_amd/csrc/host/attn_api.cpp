@@ -750,23 +750,14 @@ bool flash_ok(int dtype, const Shape& s, const PePlan& plan) {
 }
 
 // Workgroup size of the flash kernel, in waves (16 query rows each): 8
-// waves convert each K/V tile once for 128 rows, which pays when the grid of
-// 128-row blocks still gives every CU a workgroup; smaller grids take 4
-// waves (twice the workgroups).  atn_tuning.flash_waves forces either.
-int flash_waves(const Shape& s, int dev) {
+// (128 rows sharing each K/V tile's conversion, 64-key tiles at head_d <=
+// 128) measured ahead of 4 (64 rows, 32-key tiles so that two workgroups'
+// double-buffered tiles fit a CU's LDS) on every shape tried, grids of
+// fewer workgroups than CUs included.  atn_tuning.flash_waves forces 4
+// (head dims past 128 always run 8, chosen by the launcher).
+int flash_waves() {
     const int forced = tune().flash_waves;
-    if (forced == 4 || forced == 8) return forced;
-    int cus = 0;
-    {
-        std::lock_guard<std::mutex> lk(g_mu);
-        DeviceState& ds = g_dev[dev];
-        if (ds.cus == 0 &&
-            hipDeviceGetAttribute(&ds.cus, hipDeviceAttributeMultiprocessorCount, dev) !=
-                hipSuccess)
-            ds.cus = 0;
-        cus = ds.cus > 0 ? ds.cus : 256;
-    }
-    return s.BH * ((s.Lq + 127) / 128) >= (int64_t)cus ? 8 : 4;
+    return forced == 4 ? 4 : 8;
 }
 
 // Scratch bytes of the path a call of shape s takes: fused (when planned and
@@ -938,7 +929,7 @@ int attention_run(int dtype, const void* Q, const void* K, const void* V, void* 
         return ATN_OK;
     }
     if (use_flash) {
-        ATN_HIP(atn::launch_flash(plan.pek, flash_waves(s, dev), static_cast<const float*>(Q),
+        ATN_HIP(atn::launch_flash(plan.pek, flash_waves(), static_cast<const float*>(Q),
                                   static_cast<const float*>(K), static_cast<const float*>(V),
                                   static_cast<float*>(out), (int)s.BH, Lq, Lk, D, scale, plan.q,
                                   plan.k, stream));

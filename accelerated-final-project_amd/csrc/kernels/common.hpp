@@ -171,21 +171,13 @@ __device__ __forceinline__ float sin_pe(const PeSide& t, int pos, int d) {
     return (d & 1) ? t.b[idx] : t.a[idx];
 }
 
-// Loads x[d..d+3] of one row (row pointer xr, position pos), applies the
-// positional encoding of this side, and returns fp32.  Elements at or past
-// dend read as 0.  d is a multiple of 4.
+// The positional encoding of this side applied to x[d..d+3] of one row
+// (row pointer xr, position pos), already loaded as x (elements at or past
+// dend 0: they stay 0).  d is a multiple of 4.
 template <typename T, int PEK>
-__device__ __forceinline__ float4 load_row4_pe(const T* __restrict__ xr, int pos, int d, int dend,
-                                              const PeSide& pe, bool vec_ok) {
-    float v[4] = {0.f, 0.f, 0.f, 0.f};
-    if (vec_ok && d + 3 < dend) {
-        float4 t = Elem<T>::ld4(xr, d);
-        v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
-    } else {
-#pragma unroll
-        for (int c = 0; c < 4; ++c)
-            if (d + c < dend) v[c] = Elem<T>::ld(xr, d + c);
-    }
+__device__ __forceinline__ float4 apply_pe4(float4 x, const T* __restrict__ xr, int pos, int d,
+                                           int dend, const PeSide& pe) {
+    float v[4] = {x.x, x.y, x.z, x.w};
     if constexpr (PEK == kPeRopeInterleaved) {
         if (pe.on) {
 #pragma unroll
@@ -226,6 +218,24 @@ __device__ __forceinline__ float4 load_row4_pe(const T* __restrict__ xr, int pos
         }
     }
     return make_float4(v[0], v[1], v[2], v[3]);
+}
+
+// Loads x[d..d+3] of one row (row pointer xr, position pos), applies the
+// positional encoding of this side, and returns fp32.  Elements at or past
+// dend read as 0.  d is a multiple of 4.
+template <typename T, int PEK>
+__device__ __forceinline__ float4 load_row4_pe(const T* __restrict__ xr, int pos, int d, int dend,
+                                              const PeSide& pe, bool vec_ok) {
+    float v[4] = {0.f, 0.f, 0.f, 0.f};
+    if (vec_ok && d + 3 < dend) {
+        float4 t = Elem<T>::ld4(xr, d);
+        v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
+    } else {
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+            if (d + c < dend) v[c] = Elem<T>::ld(xr, d + c);
+    }
+    return apply_pe4<T, PEK>(make_float4(v[0], v[1], v[2], v[3]), xr, pos, d, dend, pe);
 }
 
 }  // namespace atn

@@ -5,37 +5,40 @@
 // query row in 64-key tiles with an online softmax and keeps the running
 // output in global memory.  Here a workgroup owns 64 or 128 query rows (16
 // per wave, 4 or 8 waves) of one head and walks the head's keys in tiles of
-// KT keys (64 for D <= 128 without an encoding, else 32; at least one load
-// round of the workgroup), with the running output of its rows in
-// registers.  8 waves convert each K/V tile once for twice the rows, 4
-// waves make twice the workgroups for grids that would not fill the chip:
+// KT keys (64 for 8 waves at D <= 128 without an encoding, else 32; at
+// least one load round of the workgroup), with the running output of its
+// rows in registers.  8 waves (the library's choice) convert each K/V tile
+// once for twice the rows of 4 (a tuning override, which makes twice the
+// workgroups).
 //
-//   per tile: K and V rows are loaded (16-byte loads, the next tile's in
-//   flight while this one computes), K scaled by a power of two from the
-//   tile's largest finite magnitude (V only when it exceeds the fp16
-//   range: its scale carries over into the running output) and stored to
-//   LDS as hi + lo
-//   fp16 parts (the fp32 split of the single-launch kernel: 22 significant
-//   bits per operand, exact products on v_mfma_f32_16x16x32_f16, fp32
-//   accumulation);
-//   each wave computes S^T = K Q^T for its 16 query rows (Q in registers,
+//   Per tile: K and V rows are loaded (16-byte loads) two tiles ahead, K
+//   encoded (RoPE, sinusoidal) once they land, and reduced to per-wave
+//   magnitude maxima; a tile ahead, the workgroup maxima set the tile's
+//   scales (K scaled by a power of two when its largest finite magnitude
+//   lies outside [2^-3, 65504), V only beyond fp16's range: its scale
+//   carries over into the running output) and it is stored to one of two
+//   LDS buffers as hi + lo fp16 parts (the fp32 split of the single-launch
+//   kernel: 22 significant bits per operand, exact products on
+//   v_mfma_f32_16x16x32_f16, fp32 accumulation).  One barrier per tile
+//   orders all of it.
+//   Each wave computes S^T = K Q^T for its 16 query rows (Q in registers,
 //   split once, scaled by a power of two per wave) -- transposed, so that a
-//   lane holds 16 scores of ONE query: the online-softmax statistics (running
-//   max m, running sum l) of a query live in the lanes that hold its scores
-//   and its output row, and reductions over a tile's keys are 16 values in
-//   registers plus two cross-lane steps;
-//   P = exp(S - m) (scaled by 2^15, exact) stays in registers, where the
-//   accumulator layout of S^T is already the B operand of O^T += V^T P^T
-//   (the keys of each 32-key block in the order 4g + 0..3, 16 + 4g + 0..3 for
-//   lane group g; V's transposing LDS read, ds_read_b64_tr_b16, takes the
-//   same order), and O^T (16 dims x 16 queries per MFMA tile) accumulates
-//   in registers, rescaled per tile by exp(m_old - m_new) and by the ratio
-//   of consecutive V tiles' scales.
+//   lane holds 16 scores of ONE query: the online-softmax statistics
+//   (running max m, running sum l) of a query live in the lanes that hold
+//   its scores and its output row, and reductions over a tile's keys are 16
+//   values in registers plus two row swaps (v_permlane16/32_swap).
+//   P = 2^(x - m + 15) (base 2, its 2^15 via the exponent) stays in
+//   registers, where the accumulator layout of S^T is already the B operand
+//   of O^T += V^T P^T (the keys of each 32-key block in the order
+//   4g + 0..3, 16 + 4g + 0..3 for lane group g; V's transposing LDS read,
+//   ds_read_b64_tr_b16, takes the same order), and O^T (16 dims x 16
+//   queries per MFMA tile) accumulates in registers, rescaled per tile by
+//   2^(m_old - m_new) and by the ratio of consecutive V tiles' scales.
 //
 // The score matrix never reaches memory: per call the kernel reads Q once
-// and K and V once per query block, and writes O once.  Positional
-// encodings (RoPE, sinusoidal) are applied to Q and K at load.
+// and K and V once per query block, and writes O once.
 #include <algorithm>
+#include <type_traits>
 
 #include "common.hpp"
 #include "launch.hpp"
@@ -46,14 +49,14 @@ namespace atn {
 namespace {
 
 // Tiling for head dims padded to DP (32, 64, 128 or 256) and NW waves per
-// workgroup (4 or 8; 16 query rows each, sharing each K/V tile); with a
-// positional encoding (PE) the key tile is 32 keys (the encoding's table
-// loads need the registers of half the prefetched rows).
+// workgroup (4 or 8; 16 query rows each, sharing each K/V tile).  The key
+// tile is 64 keys for 8 waves at DP <= 128 without a positional encoding
+// (PE), else 32 (two LDS buffers of it then leave room for two 4-wave
+// workgroups per CU), and at least one load round of the workgroup.
 template <int DP, bool PE, int NW>
 struct FlashGeo {
     static constexpr int THREADS = 64 * NW, ROWS = 16 * NW;
-    // keys per tile, at least one load round of rows
-    static constexpr int KT0 = DP <= 128 && !PE ? 64 : 32;
+    static constexpr int KT0 = DP <= 128 && !PE && NW == 8 ? 64 : 32;
     static constexpr int KT = KT0 > THREADS / (DP / 4) ? KT0 : THREADS / (DP / 4);
     static constexpr int KS = DP / 32;              // 32-deep steps of Q K^T
     static constexpr int NJ = KT / 16;              // 16-key tiles of S^T
@@ -61,24 +64,56 @@ struct FlashGeo {
     static constexpr int NDT = DP / 16;             // 16-dim tiles of O^T
     static constexpr int VPR = DP / 4;              // 16-byte vectors per row
     static constexpr int RSTEP = THREADS / VPR;     // rows per load round
-    static constexpr int NLD = KT / RSTEP;             // load rounds per tile
+    static constexpr int NLD = KT / RSTEP;          // load rounds per tile
     // LDS rows in 16-bit elements: K padded by 8 (16-byte fragment reads),
-    // V by 16 (the transposing read's 4 rows x 32 bytes in distinct banks)
+    // V by 16 (the transposing read's 4 rows x 32 bytes in distinct banks);
+    // two buffers of TILE elements
     static constexpr int KSTR = DP + 8, VSTR = DP + 16;
     static constexpr int K_HI = 0, K_LO = KT * KSTR, V_HI = 2 * KT * KSTR,
                          V_LO = V_HI + KT * VSTR;
-    static constexpr int BYTES = 2 * (2 * KT * KSTR + 2 * KT * VSTR);
+    static constexpr int TILE = 2 * KT * KSTR + 2 * KT * VSTR;
+    static constexpr int BYTES = 2 * 2 * TILE;
     static_assert(KT % RSTEP == 0, "whole load rounds");
+    static_assert(BYTES <= 160 * 1024, "LDS");
 };
 
-// lanes L, L ^ 16, L ^ 32, L ^ 48 (the four lane groups of one query)
+// max without the operand canonicalization fmaxf brings (the values are
+// never signalling NaNs).  Inline asm: the compiler's hazard checks do not
+// cover it, so it never reads an MFMA result (the MFMA pipeline may not
+// have written it yet), and a value it writes passes a compiler-visible
+// instruction before a cross-lane operation or an MFMA reads it.
+__device__ __forceinline__ float fmax_raw(float a, float b) { return vmaxf(a, b); }
+
+// lanes L, L ^ 16, L ^ 32, L ^ 48 (the four lane groups of one query), by
+// gfx950's row-swapping permutes: v_permlane16_swap and v_permlane32_swap
+// each leave a lane its own value and its partner's, in registers, in the
+// same order for both lanes of a pair (so sums agree bit for bit)
 __device__ __forceinline__ float xgroup_max(float v) {
-    v = fmaxf(v, swz_xor16(v));
-    return fmaxf(v, __shfl_xor(v, 32));
+    v = __builtin_canonicalizef(v);
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v),
+                                                    false, false);
+    v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v),
+                                                    false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 __device__ __forceinline__ float xgroup_sum(float v) {
-    v += swz_xor16(v);
-    return v + __shfl_xor(v, 32);
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v),
+                                                    false, false);
+    v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v),
+                                                    false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+// full-wave max in every lane: DPP within each row of 16 lanes, then the
+// row swaps
+__device__ __forceinline__ float wave_max_rows(float v) {
+    v = __builtin_canonicalizef(v);
+    v = fmaxf(v, dpp<kDppQuadXor1>(v));
+    v = fmaxf(v, dpp<kDppQuadXor2>(v));
+    v = fmaxf(v, dpp<kDppRowHalfMirror>(v));
+    v = fmaxf(v, dpp<kDppRowMirror>(v));
+    return xgroup_max(v);
 }
 
 template <int DP, int PEK, int NW>
@@ -92,8 +127,10 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_flash_f32(const float* __re
     using G = FlashGeo<DP, PEK != kPeNone, NW>;
     extern __shared__ __align__(16) unsigned char smem_raw[];
     uint16_t* smem = reinterpret_cast<uint16_t*>(smem_raw);
-    __shared__ float slot[2 * NW];
+    // per-wave K and V magnitude maxima of a loaded tile, by tile parity
+    __shared__ float slot[2][2 * NW];
 
+    const float one = unit_opaque();  // (see split2_f16_one)
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lr = lane & 15, lg = lane >> 4;
@@ -150,8 +187,15 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_flash_f32(const float* __re
         }
     }
 
-    // ---- K/V tile loads: thread t holds 16-byte vector t % VPR of rows
-    // t / VPR + RSTEP i (rows past Lk and columns past D read as zeros)
+    // ---- K/V tiles.  Thread t loads 16-byte vector t % VPR of rows t / VPR
+    // + RSTEP i (rows past Lk and columns past D read as zeros).  Tile u is
+    // handled over three iterations of the loop below, with one barrier per
+    // iteration: in iteration u - 2 its loads are issued before the tile
+    // then computed, and after that tile its K rows are encoded (PE) and
+    // its per-wave magnitude maxima go to slot[u & 1]; in iteration u - 1
+    // the workgroup maxima set its scales and its hi + lo parts go to LDS
+    // buffer u & 1; iteration u computes it.  Staging, loads and maxima thus
+    // run beside another tile's products, and LDS holds two tiles.
     const int lrow = tid / G::VPR, lcol = (tid % G::VPR) * 4;
     const __amdgpu_buffer_rsrc_t rk = buf_rsrc(Kh, Lk * D * 4);
     const __amdgpu_buffer_rsrc_t rv = buf_rsrc(Vh, Lk * D * 4);
@@ -161,101 +205,180 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_flash_f32(const float* __re
         for (int i = 0; i < G::NLD; ++i) {
             const int key = k0 + lrow + G::RSTEP * i;
             const int off = lcol < D ? (key * D + lcol) * 4 : kOob;
-            if constexpr (PEK == kPeNone) {
-                kr[i] = ld_buf_f4(rk, off);
-            } else {
-                kr[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-                if (key < Lk && lcol < D)
-                    kr[i] = load_row4_pe<float, PEK>(Kh + (size_t)key * D, key, lcol, D, pk, true);
-            }
+            kr[i] = ld_buf_f4(rk, off);
             vr[i] = ld_buf_f4(rv, off);
         }
     };
+    // K's encoding, then the per-wave maxima of the tile's K and V
+    // magnitudes (one v_max3 per value pair).  A wave whose values include
+    // an infinity or NaN takes its finite values only: non-finite values
+    // stay so through a scaling and must not set the scale of the finite
+    // values beside them.
+    auto maxima = [&](int k0, int par) {
+        if constexpr (PEK != kPeNone) {
+#pragma unroll
+            for (int i = 0; i < G::NLD; ++i) {
+                const int key = k0 + lrow + G::RSTEP * i;
+                if (key < Lk && lcol < D)
+                    kr[i] = apply_pe4<float, PEK>(kr[i], Kh + (size_t)key * D, key, lcol, D, pk);
+            }
+        }
+        float mk = 0.f, mv = 0.f;
+#pragma unroll
+        for (int i = 0; i < G::NLD; ++i) {
+            mk = vmax3abs(mk, kr[i].x, kr[i].y);
+            mk = vmax3abs(mk, kr[i].z, kr[i].w);
+            mv = vmax3abs(mv, vr[i].x, vr[i].y);
+            mv = vmax3abs(mv, vr[i].z, vr[i].w);
+        }
+        mk = wave_max_rows(mk);
+        mv = wave_max_rows(mv);
+        if (!(mk < INFINITY) || !(mv < INFINITY)) {  // the same in every lane
+            mk = 0.f;
+            mv = 0.f;
+#pragma unroll
+            for (int i = 0; i < G::NLD; ++i) {
+                mk = max_finite4(mk, kr[i]);
+                mv = max_finite4(mv, vr[i]);
+            }
+            mk = wave_max_rows(mk);
+            mv = wave_max_rows(mv);
+        }
+        if (lane == 0) {
+            slot[par][wave] = mk;
+            slot[par][NW + wave] = mv;
+        }
+    };
+    // scales of the tile whose maxima are in slot[par] (K as it is where its
+    // largest magnitude lies in [2^-3, 65504): the split then keeps 2^-22 of
+    // that magnitude; else a power of two brings it to [2^14, 2^15); V
+    // scaled only beyond fp16's range), and its hi + lo fp16 parts into LDS
+    // buffer par
+    auto stage = [&](int par, float& uk, float& sv, float& uv) {
+        float mk = slot[par][0], mv = slot[par][NW];
+#pragma unroll
+        for (int w = 1; w < NW; ++w) {
+            mk = fmax_raw(mk, slot[par][w]);
+            mv = fmax_raw(mv, slot[par][NW + w]);
+        }
+        const bool k_plain = mk >= 0.125f && mk < kF16Range;
+        const float sk = k_plain ? 1.f : pow2_scale(mk);
+        uk = k_plain ? 1.f : pow2_unit(mk);
+        sv = range_scale(mv);
+        uv = range_unit(mv);
+        uint16_t* buf = smem + par * G::TILE;
+        auto put = [&](auto plain) {
+#pragma unroll
+            for (int i = 0; i < G::NLD; ++i) {
+                const int row = lrow + G::RSTEP * i;
+                uint32_t h0, l0, h1, l1, h2, l2, h3, l3;
+                if constexpr (decltype(plain)::value) {
+                    split2_f16_one(kr[i].x, kr[i].y, one, h0, l0);
+                    split2_f16_one(kr[i].z, kr[i].w, one, h1, l1);
+                    split2_f16_one(vr[i].x, vr[i].y, one, h2, l2);
+                    split2_f16_one(vr[i].z, vr[i].w, one, h3, l3);
+                } else {
+                    split2_f16_mix(kr[i].x, kr[i].y, sk, h0, l0);
+                    split2_f16_mix(kr[i].z, kr[i].w, sk, h1, l1);
+                    split2_f16_mix(vr[i].x, vr[i].y, sv, h2, l2);
+                    split2_f16_mix(vr[i].z, vr[i].w, sv, h3, l3);
+                }
+                *reinterpret_cast<uint2*>(buf + G::K_HI + row * G::KSTR + lcol) =
+                    make_uint2(h0, h1);
+                *reinterpret_cast<uint2*>(buf + G::K_LO + row * G::KSTR + lcol) =
+                    make_uint2(l0, l1);
+                *reinterpret_cast<uint2*>(buf + G::V_HI + row * G::VSTR + lcol) =
+                    make_uint2(h2, h3);
+                *reinterpret_cast<uint2*>(buf + G::V_LO + row * G::VSTR + lcol) =
+                    make_uint2(l2, l3);
+            }
+        };
+        if (k_plain && sv == 1.f)
+            put(std::true_type{});
+        else
+            put(std::false_type{});
+    };
 
     // running statistics of this lane's query and its output rows (O^T
-    // tiles: lane holds dims 16 t + 4 lg + 0..3 of query lr), in units of
-    // uv / 2^15 for the current V tile's unit uv = 1 / sv
+    // tiles: lane holds dims 16 t + 4 lg + 0..3 of query lr): the max in
+    // base-2 units of the scores, the sum in units of 2^15, the output in
+    // units of uv / 2^15 for the current V tile's unit uv = 1 / sv
     float m_run = -INFINITY, l_run = 0.f, uv_prev = 1.f;
     v4f o[G::NDT];
 #pragma unroll
     for (int t = 0; t < G::NDT; ++t) o[t] = v4f{0.f, 0.f, 0.f, 0.f};
 
     const int ntiles = (Lk + G::KT - 1) / G::KT;
+    float uk, sv, uv;  // scales of the tile staged last
     issue(0);
+    maxima(0, 0);
+    __syncthreads();
+    stage(0, uk, sv, uv);
+    if (ntiles > 1) {
+        issue(G::KT);
+        maxima(G::KT, 1);
+    }
+    __syncthreads();
     for (int t = 0; t < ntiles; ++t) {
-        const int k0 = t * G::KT;
-        // tile scales: workgroup maxima of the loaded K and V values (the
-        // slots are read after the barrier that also ends the previous
-        // tile's LDS reads)
-        float mk = 0.f, mv = 0.f;
-#pragma unroll
-        for (int i = 0; i < G::NLD; ++i) {
-            mk = max_finite4(mk, kr[i]);
-            mv = max_finite4(mv, vr[i]);
+        const int k0 = t * G::KT, par = t & 1;
+        const float uk_t = uk, sv_t = sv, uv_t = uv;
+        if (t + 1 < ntiles) {
+            stage(par ^ 1, uk, sv, uv);
+            if (t + 2 < ntiles) issue(k0 + 2 * G::KT);
         }
-        mk = wave_max(mk);
-        mv = wave_max(mv);
-        if (lane == 0) {
-            slot[wave] = mk;
-            slot[NW + wave] = mv;
-        }
-        __syncthreads();
-        mk = slot[0];
-        mv = slot[NW];
-#pragma unroll
-        for (int w = 1; w < NW; ++w) {
-            mk = fmaxf(mk, slot[w]);
-            mv = fmaxf(mv, slot[NW + w]);
-        }
-        const float sk = pow2_scale(mk), sv = range_scale(mv), uv = range_unit(mv);
-#pragma unroll
-        for (int i = 0; i < G::NLD; ++i) {
-            const int row = lrow + G::RSTEP * i;
-            uint32_t h0, l0, h1, l1;
-            split2_f16(kr[i].x * sk, kr[i].y * sk, h0, l0);
-            split2_f16(kr[i].z * sk, kr[i].w * sk, h1, l1);
-            *reinterpret_cast<uint2*>(smem + G::K_HI + row * G::KSTR + lcol) = make_uint2(h0, h1);
-            *reinterpret_cast<uint2*>(smem + G::K_LO + row * G::KSTR + lcol) = make_uint2(l0, l1);
-            split2_f16(vr[i].x * sv, vr[i].y * sv, h0, l0);
-            split2_f16(vr[i].z * sv, vr[i].w * sv, h1, l1);
-            *reinterpret_cast<uint2*>(smem + G::V_HI + row * G::VSTR + lcol) = make_uint2(h0, h1);
-            *reinterpret_cast<uint2*>(smem + G::V_LO + row * G::VSTR + lcol) = make_uint2(l0, l1);
-        }
-        if (t + 1 < ntiles) issue(k0 + G::KT);  // lands while this tile computes
-        __syncthreads();
+        const uint16_t* buf = smem + par * G::TILE;
 
         // ---- S^T tile: s[j] = keys 16 j + 4 lg + r, query lr
         v4f s[G::NJ];
 #pragma unroll
         for (int j = 0; j < G::NJ; ++j) s[j] = v4f{0.f, 0.f, 0.f, 0.f};
+        // per 32-deep step: the step's 2 NJ fragment reads first, then its
+        // 3 NJ products (kept in that order, so the reads' latencies overlap
+        // instead of each read being waited for before its product)
 #pragma unroll
         for (int ks = 0; ks < G::KS; ++ks) {
+            f16x8 ah[G::NJ], al[G::NJ];
 #pragma unroll
             for (int j = 0; j < G::NJ; ++j) {
                 const int a = (16 * j + lr) * G::KSTR + 32 * ks + 8 * lg;
-                const f16x8 ah = lds8_f16(smem + G::K_HI + a), al = lds8_f16(smem + G::K_LO + a);
-                s[j] = mfma_f16(ah, qh[ks], s[j]);
-                s[j] = mfma_f16(ah, ql[ks], s[j]);
-                s[j] = mfma_f16(al, qh[ks], s[j]);
+                ah[j] = lds8_f16(buf + G::K_HI + a);
+                al[j] = lds8_f16(buf + G::K_LO + a);
             }
+#pragma unroll
+            for (int j = 0; j < G::NJ; ++j) s[j] = mfma_f16(ah[j], qh[ks], s[j]);
+#pragma unroll
+            for (int j = 0; j < G::NJ; ++j) s[j] = mfma_f16(ah[j], ql[ks], s[j]);
+#pragma unroll
+            for (int j = 0; j < G::NJ; ++j) s[j] = mfma_f16(al[j], qh[ks], s[j]);
+            __builtin_amdgcn_sched_group_barrier(0x100, 2 * G::NJ, 0);  // DS reads
+            __builtin_amdgcn_sched_group_barrier(0x008, 3 * G::NJ, 0);  // MFMA
         }
 
-        // ---- online softmax over the tile (keys past Lk score -inf)
-        const float c = scale * uq * pow2_unit(mk);
+        // ---- online softmax over the tile in base 2: x = S c2 with c2 =
+        // scale log2(e) / (sq sk), the running max m_run in the same units
+        // (keys past Lk score -inf, on the last tile only)
+        const float c2 = scale * 1.44269504088896341f * uq * uk_t;
         float mt = -INFINITY;
+        if (k0 + G::KT <= Lk) {
 #pragma unroll
-        for (int j = 0; j < G::NJ; ++j)
+            for (int j = 0; j < G::NJ; ++j)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int key = k0 + 16 * j + 4 * lg + r;
-                const float x = key < Lk ? s[j][r] * c : -INFINITY;
-                s[j][r] = x;
-                mt = fmaxf(mt, x);
-            }
-        mt = xgroup_max(mt);
-        const float m_new = fmaxf(m_run, mt);
-        const float alpha = __expf(m_run - m_new);  // 0 on the first tile
+                for (int r = 0; r < 4; ++r) mt = fmaxf(mt, s[j][r]);
+        } else {
+#pragma unroll
+            for (int j = 0; j < G::NJ; ++j)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    if (k0 + 16 * j + 4 * lg + r >= Lk) s[j][r] = -INFINITY;
+                    mt = fmaxf(mt, s[j][r]);
+                }
+        }
+        const float m_new = fmaxf(m_run, xgroup_max(mt) * c2);  // c2 > 0
+        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // 0 on the first tile
         m_run = m_new;
+        // P = 2^(x - m_new + 15): one FMA and one v_exp_f32 per score, the
+        // 2^15 that keeps P's lo parts normal in fp16 folded into the exponent
+        const float nm = 15.f - m_new;
         float ps = 0.f;
         // P as the B operand of block b: elements 0..3 tile 2b, 4..7 tile 2b+1
         f16x8 ph[G::NB], pl[G::NB];
@@ -268,32 +391,35 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_flash_f32(const float* __re
                 float p[4];
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    p[r] = __expf(sj[r] - m_new);
+                    p[r] = __builtin_amdgcn_exp2f(fmaf(sj[r], c2, nm));
                     ps += p[r];
                 }
-                split2_f16(p[0] * 32768.f, p[1] * 32768.f, h[2 * half], l[2 * half]);
-                split2_f16(p[2] * 32768.f, p[3] * 32768.f, h[2 * half + 1], l[2 * half + 1]);
+                split2_f16_one(p[0], p[1], one, h[2 * half], l[2 * half]);
+                split2_f16_one(p[2], p[3], one, h[2 * half + 1], l[2 * half + 1]);
             }
             ph[b] = __builtin_bit_cast(f16x8, make_uint4(h[0], h[1], h[2], h[3]));
             pl[b] = __builtin_bit_cast(f16x8, make_uint4(l[0], l[1], l[2], l[3]));
         }
         l_run = l_run * alpha + ps;  // this lane's keys; summed over lane groups at the end
-        const float f = alpha * (uv_prev * sv);  // the old output in the new tile's units
-        uv_prev = uv;
+        const float f = alpha * (uv_prev * sv_t);  // the old output in the new tile's units
+        uv_prev = uv_t;
+        if (__builtin_amdgcn_ballot_w64(f != 1.f)) {  // skipped while no row's max moves
+#pragma unroll
+            for (int dt = 0; dt < G::NDT; ++dt) o[dt] *= f;
+        }
 
         // ---- O^T += V^T P^T: A = V^T from the transposing read, keys of
         // block b in P's order (rows 4 lg + 0..3, then 16 + 4 lg + 0..3)
         const int vrow = 4 * lg + (lr >> 2), vcol = 4 * (lr & 3);
 #pragma unroll
         for (int dt = 0; dt < G::NDT; ++dt) {
-            o[dt] *= f;
 #pragma unroll
             for (int b = 0; b < G::NB; ++b) {
                 const int a = (32 * b + vrow) * G::VSTR + 16 * dt + vcol;
-                const uint2 h0 = lds_tr16(smem + G::V_HI + a);
-                const uint2 h1 = lds_tr16(smem + G::V_HI + a + 16 * G::VSTR);
-                const uint2 l0 = lds_tr16(smem + G::V_LO + a);
-                const uint2 l1 = lds_tr16(smem + G::V_LO + a + 16 * G::VSTR);
+                const uint2 h0 = lds_tr16(buf + G::V_HI + a);
+                const uint2 h1 = lds_tr16(buf + G::V_HI + a + 16 * G::VSTR);
+                const uint2 l0 = lds_tr16(buf + G::V_LO + a);
+                const uint2 l1 = lds_tr16(buf + G::V_LO + a + 16 * G::VSTR);
                 const f16x8 vh = __builtin_bit_cast(f16x8, make_uint4(h0.x, h0.y, h1.x, h1.y));
                 const f16x8 vl = __builtin_bit_cast(f16x8, make_uint4(l0.x, l0.y, l1.x, l1.y));
                 o[dt] = mfma_f16(vh, ph[b], o[dt]);
@@ -301,11 +427,15 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_flash_f32(const float* __re
                 o[dt] = mfma_f16(vl, ph[b], o[dt]);
             }
         }
+
+        if (t + 2 < ntiles) maxima(k0 + 2 * G::KT, par);
+        __syncthreads();
     }
 
-    // ---- O = O^T uv / (2^15 l): one 16-byte store per dim tile
+    // ---- O = O^T uv / l (O^T and l both in units of 2^15): one 16-byte
+    // store per dim tile
     const float l = xgroup_sum(l_run);
-    const float inv = 1.0f / (l * 32768.f);
+    const float inv = 1.0f / l;
     if (qrow < Lq) {
         float* orow = Og + ((size_t)bh * Lq + qrow) * D;
 #pragma unroll
@@ -345,16 +475,20 @@ hipError_t launch_pe(const float* Q, const float* K, const float* V, float* O, i
     if (D <= 32) return launch_t<32, PEK, NW>(Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk, st);
     if (D <= 64) return launch_t<64, PEK, NW>(Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk, st);
     if (D <= 128) return launch_t<128, PEK, NW>(Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk, st);
-    if constexpr (PEK == kPeNone)
+    if constexpr (PEK == kPeNone && NW == 8)
         return launch_t<256, PEK, NW>(Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk, st);
-    return hipErrorInvalidValue;  // flash_supported: encoded calls have D <= 128
+    return hipErrorInvalidValue;  // encoded calls have D <= 128; D > 128 takes 8 waves
 }
 
 template <int PEK>
 hipError_t launch_w(int waves, const float* Q, const float* K, const float* V, float* O, int BH,
                     int Lq, int Lk, int D, float scale, const PeSide& pq, const PeSide& pk,
                     hipStream_t st) {
-    if (waves == 8) return launch_pe<PEK, 8>(Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk, st);
+    // (head dims past 128 take 8 waves: two buffers of a 256-wide tile
+    // leave room for one workgroup per CU, so 4 waves would leave half the
+    // SIMDs' wave slots empty)
+    if (waves == 8 || D > 128)
+        return launch_pe<PEK, 8>(Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk, st);
     if (waves == 4) return launch_pe<PEK, 4>(Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk, st);
     return hipErrorInvalidValue;
 }

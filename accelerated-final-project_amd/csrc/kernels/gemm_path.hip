@@ -189,6 +189,15 @@ __device__ __forceinline__ float dppb(float v) {
 }
 // Max / sum over each half-wave (lanes with the same lane / 32): DPP within
 // quads, 8 and 16 lanes, then the 16-lane hop by ds_swizzle.
+// Inline asm that reads MFMA results must run after the MFMA pipeline has
+// written them: the compiler places the wait states before its own
+// instructions, not before inline asm.  This is the accumulator tile's
+// next reader and waits 24 cycles first (an MFMA of 16 passes needs 18),
+// so every MFMA issued before it has written its results.
+__device__ __forceinline__ void mfma_settle(v16f& a) {
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" : "+v"(a));
+}
+
 __device__ __forceinline__ float half_max(float v) {
     v = vmaxf(v, dppb<kDppQuadXor1>(v));
     v = vmaxf(v, dppb<kDppQuadXor2>(v));
@@ -281,6 +290,11 @@ __device__ __forceinline__ void nt_exp_epilogue(const GemmArgs& g, v16f (&acc)[T
                 for (int r = 0; r < 16; ++r) acc[i][j][r] = ok ? acc[i][j][r] * c : -INFINITY;
         }
     }
+    // (the row maxima below read the accumulators by inline asm)
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) mfma_settle(acc[i][j]);
     float rm[TI][16], rl[TI][16];
 #pragma unroll
     for (int i = 0; i < TI; ++i)

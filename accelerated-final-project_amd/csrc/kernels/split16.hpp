@@ -34,6 +34,39 @@ __device__ __forceinline__ void split2_f16(float a, float b, uint32_t& h, uint32
     l = __builtin_bit_cast(uint32_t, lv);
 }
 
+// The same split of a s and b s for s = 1 or a power of two (so the
+// products are exact) in three instructions per pair: hi by
+// v_cvt_pkrtz_f16_f32, each lo as an fp32 fma of a s minus the fp16 hi
+// (exact in fp32) rounded to fp16, which the compiler emits as one
+// v_fma_mix.  Written in C, not as inline asm, so that the compiler's
+// hazard checks see the writes (the parts feed MFMA operands).  For s = 1
+// use split2_f16_one: an fma by a known 1 is folded to an add, which does
+// not take the mixed form.
+__device__ __forceinline__ void split2_f16_mix(float a, float b, float s, uint32_t& h,
+                                               uint32_t& l) {
+    const f16x2 hh = __builtin_bit_cast(f16x2, __builtin_amdgcn_cvt_pkrtz(a * s, b * s));
+    const f16x2 lv = {(_Float16)__builtin_fmaf(a, s, -(float)hh[0]),
+                      (_Float16)__builtin_fmaf(b, s, -(float)hh[1])};
+    h = __builtin_bit_cast(uint32_t, hh);
+    l = __builtin_bit_cast(uint32_t, lv);
+}
+// 1.0 in a register the compiler treats as unknown (an empty asm marks it
+// modified; no instruction is emitted)
+__device__ __forceinline__ float unit_opaque() {
+    float one = 1.f;
+    asm volatile("" : "+v"(one));
+    return one;
+}
+// split2_f16_mix for s = 1 (`one` from unit_opaque()): no multiplications
+__device__ __forceinline__ void split2_f16_one(float a, float b, float one, uint32_t& h,
+                                               uint32_t& l) {
+    const f16x2 hh = __builtin_bit_cast(f16x2, __builtin_amdgcn_cvt_pkrtz(a, b));
+    const f16x2 lv = {(_Float16)__builtin_fmaf(a, one, -(float)hh[0]),
+                      (_Float16)__builtin_fmaf(b, one, -(float)hh[1])};
+    h = __builtin_bit_cast(uint32_t, hh);
+    l = __builtin_bit_cast(uint32_t, lv);
+}
+
 __device__ __forceinline__ v4f mfma_f16(const f16x8& a, const f16x8& b, const v4f& c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }

@@ -332,7 +332,7 @@ typedef struct atn_tuning {
                               it, so its workgroups take the fail-closed exit (no wait is
                               entered) */
     int flash_waves;       /* flash kernel: 4 or 8 waves (64 or 128 query rows) per
-                              workgroup; 0: by grid size */
+                              workgroup (head_d > 128 always 8); 0: 8 */
 } atn_tuning;
 /* Replaces the overrides (NULL: all zero) and drops cached plans.  Plans
  * that a forced setting makes impossible fall back to the library's
