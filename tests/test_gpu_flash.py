@@ -74,6 +74,25 @@ def test_flash_workgroup_forms(am, dev, tuner, waves, shape, pe):
     assert n == 0, f"{n} mismatches, max abs {mabs}, max rel {mrel}"
 
 
+@pytest.mark.parametrize("waves", [4, 8])
+@pytest.mark.parametrize("D", [32, 64, 128])
+def test_flash_tile_counts(am, dev, tuner, waves, D):
+    """Key lengths of 2 to 17 tiles, two seeds each, both workgroup forms.
+    Regression: a build whose softmax read the QK^T accumulators through an
+    inline-asm max (which the compiler's MFMA hazard waits do not cover)
+    gave wrong rows scattered over these cases whenever the schedule put
+    that read right behind the MFMAs."""
+    tuner.set(flash_waves=waves)
+    B, Hh, Lq = 1, 2, 70
+    for Lk in (65, 70, 96, 97, 128, 129, 200, 513):
+        for seed in (1, 2):
+            print(f"[case] flash f32 {waves} waves D={D} Lk={Lk} seed={seed}", flush=True)
+            Q, K, V = H.rng_inputs((B, Hh, Lq, D), (B, Hh, Lk, D), seed=seed * 1000 + Lk + D)
+            got = _f32_call(am, Q, K, V)
+            n, mabs, mrel = H.check_f32(got, oracle.attention(Q, K, V, nthreads=16))
+            assert n == 0, f"Lk={Lk} seed={seed}: {n} mismatches, max abs {mabs}"
+
+
 def test_flash_reference_long_shape(am, dev):
     """The reference's long-sequence test shape (final/attention.cu:522)."""
     B, Hh, L, D = 4, 32, 512, 128
@@ -112,12 +131,16 @@ def test_flash_increasing_scores(am, dev):
     assert n == 0, f"{n} mismatches, max abs {mabs}"
 
 
-@pytest.mark.parametrize("exps", [(17, -17, 0), (0, 0, 19), (-12, -12, -12), (17, -17, 21)],
-                         ids=["qk-big", "v-big", "all-small", "all-big"])
+@pytest.mark.parametrize("exps", [(17, -17, 0), (0, 0, 19), (-12, -12, -12), (17, -17, 21),
+                                  (4, -4, 0), (5, -5, 0)],
+                         ids=["qk-big", "v-big", "all-small", "all-big", "k-plain-low",
+                              "k-scaled-low"])
 def test_flash_outside_fp16_range(am, dev, exps):
     """Head 1 scaled by powers of two (exact, so the oracle on the unscaled V
-    times 2^ev is the reference): K tiles always carry a power-of-two scale,
-    V tiles one only beyond fp16's range, carried into the running output."""
+    times 2^ev is the reference): K tiles carry a power-of-two scale when
+    their largest magnitude lies outside [2^-3, 65504) (k-plain-low puts it
+    near 2^-2, unscaled; k-scaled-low near 2^-3, either side), V tiles one
+    only beyond fp16's range, carried into the running output."""
     B, Hh, Lq, Lk, D = 1, 3, 100, 300, 128
     eq, ek, ev = exps
     print(f"[case] flash f32 scaled 2^{exps}", flush=True)
