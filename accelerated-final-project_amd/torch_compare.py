@@ -2,6 +2,7 @@
 
     python accelerated-final-project_amd/torch_compare.py [--iters 100] [--json out.json]
         [--shapes cfg2,"ref hdim=512"] [--save DIR]
+    python accelerated-final-project_amd/torch_compare.py --gemm-ceiling [--json out.json]
 
 The reference's PyTorch harness (final/benchmark_pytorch_wrapper.cu:25-130)
 times F.scaled_dot_product_attention ("optimized") and matmul -> softmax ->
@@ -13,6 +14,12 @@ and on torch's current stream, timed by the same events.  For the RoPE
 (rotate-half) and sinusoidal configurations the torch side encodes Q and K
 with elementwise ops from tables built the way the reference builds its
 caches (final/rope.cu:20-40, final/sinusoidal.cu:838-855), then attends.
+
+--gemm-ceiling instead times torch.bmm (hipBLASLt / rocBLAS) in bf16 on the
+two contractions of BASELINE configs 4 and 5 (Q K^T and P V per head,
+contiguous operands, bf16 out): plain library GEMMs with no encoding and no
+softmax, the floor under any two-GEMM attention of those shapes on this
+device.
 
 The printed max |difference| against torch SDPA is context only; parity is
 established against the CPU oracle by the test suite (--save writes each
@@ -51,10 +58,11 @@ SHAPES = [
     ("cfg3", "bf16", 1, 4, 32, 128, 8192, "none"),
     ("cfg4 rope-half", "bf16", 8, 8, 1024, 1024, 4096, "rope_half"),
     ("cfg5 sinusoidal", "bf16", 4, 16, 256, 2048, 1024, "sinusoidal"),
-    # fp32 beyond the single-launch window (split-D pipeline): the reference's
-    # own long-sequence test shape (final/attention.cu:522) and a large-head one
-    ("ref llama (4,32,512,128)", "f32", 4, 32, 512, 512, 128, "none"),
-    ("f32 long (1,4,512,512,2048)", "f32", 1, 4, 512, 512, 2048, "none"),
+    # fp32 beyond the single-launch window: the reference's own long-sequence
+    # test shape (final/attention.cu:522, the flash kernel) and a large-head
+    # one (the split-D pipeline); names without commas (--shapes splits on them)
+    ("ref llama 4x32x512x128", "f32", 4, 32, 512, 512, 128, "none"),
+    ("f32 long 1x4x512x512x2048", "f32", 1, 4, 512, 512, 2048, "none"),
 ]
 
 
@@ -92,6 +100,44 @@ def torch_encode(torch, x, pe, cos, sin):
     return y.to(x.dtype)
 
 
+# (name, batch of heads, M, K, N) of C[b] = A[b] B[b]: Q K^T and P V of
+# BASELINE configs 4 (B=8 H=8 L=1024 D=4096) and 5 (B=4 H=16 Lq=256 Lk=2048
+# D=1024)
+GEMMS = [
+    ("cfg4 QK^T", 64, 1024, 4096, 1024),
+    ("cfg4 PV", 64, 1024, 1024, 4096),
+    ("cfg5 QK^T", 64, 256, 1024, 2048),
+    ("cfg5 PV", 64, 256, 2048, 1024),
+]
+
+
+def write_json(path, rows):
+    d = os.path.dirname(path)
+    if d:
+        os.makedirs(d, exist_ok=True)
+    with open(path, "w") as f:
+        json.dump(rows, f, indent=1)
+
+
+def gemm_ceiling(torch, dev, timed):
+    """bf16 torch.bmm on the config-4/5 contractions (contiguous operands)."""
+    rows = []
+    g = torch.Generator(device=dev).manual_seed(0)
+    for name, b, m, k, n in GEMMS:
+        A = torch.randn(b, m, k, device=dev, generator=g).to(torch.bfloat16)
+        Bm = torch.randn(b, k, n, device=dev, generator=g).to(torch.bfloat16).contiguous()
+        C = torch.empty(b, m, n, device=dev, dtype=torch.bfloat16)
+        ms = timed(lambda: torch.bmm(A, Bm, out=C))
+        flops = 2 * b * m * k * n
+        nbytes = 2 * (b * m * k + b * k * n + b * m * n)
+        rows.append({"gemm": name, "batch": b, "M": m, "K": k, "N": n, "ms": ms,
+                     "tflops": flops / ms / 1e9, "gbs": nbytes / ms / 1e6})
+        print(f"{name:10s} bmm bf16 [{b}x{m}x{k}] x [{b}x{k}x{n}]  {ms * 1e3:9.1f} us  "
+              f"{flops / ms / 1e9:8.1f} TFLOP/s  {nbytes / ms / 1e6:8.1f} GB/s", flush=True)
+        del A, Bm, C
+    return rows
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--iters", type=int, default=100)
@@ -101,6 +147,8 @@ def main():
                     help="comma-separated shape names to run (default: all)")
     ap.add_argument("--save", default="",
                     help="directory for each shape's inputs and this library's output (.npy)")
+    ap.add_argument("--gemm-ceiling", action="store_true",
+                    help="time torch.bmm on the config-4/5 contractions instead")
     a = ap.parse_args()
     wanted = [w.strip() for w in a.shapes.split(",") if w.strip()]
     shapes = [sh for sh in SHAPES if not wanted or sh[0] in wanted]
@@ -138,6 +186,12 @@ def main():
         e1.record()
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) / a.iters
+
+    if a.gemm_ceiling:
+        rows = gemm_ceiling(torch, dev, timed)
+        if a.json:
+            write_json(a.json, rows)
+        return
 
     rows = []
     g = torch.Generator(device=dev).manual_seed(0)
@@ -218,8 +272,7 @@ def main():
         del Q, K, V, out, ws
         torch.cuda.empty_cache()
     if a.json:
-        with open(a.json, "w") as f:
-            json.dump(rows, f, indent=1)
+        write_json(a.json, rows)
 
 
 if __name__ == "__main__":
