@@ -8,8 +8,10 @@ HBM.  The headline workload (`value`) is BASELINE config 2: fp32 SDPA,
 batch 1, 4 heads, len_q = len_k = 64, head_dim 2048, Q/K/V iid N(0,1).
 
 With no --config, the same line also carries `per_config`: configs 1, 3, 4
-and 5 and the config-2 head_dim sweep (512 / 4096 / 8192), each timed the
-same way, checked against the CPU oracle on sampled rows of the first, a
+and 5, the config-2 head_dim sweep (512 / 4096 / 8192) and two fp32 shapes
+beyond the single-launch window (the reference's own long test shape, on the
+flash kernel, and a head_dim-2048 one, on the split-D pipeline), each timed
+the same way, checked against the CPU oracle on sampled rows of the first, a
 middle and the last head, and with its own CPU baseline.  --config N (and
 --head-dim D) print one config's line only (for profiling).
 
@@ -65,8 +67,17 @@ CONFIGS = {
         "sinusoidal", 0.5),
 }
 SWEEP_D = (512, 4096, 8192)
+# fp32 beyond the single-launch window, measured beside the configs: the
+# reference's own long-sequence test shape (final/attention.cu:522; the flash
+# kernel) and a head_dim-2048 shape of the same length (the split-D pipeline)
+LONG_F32 = {
+    "ref_long_f32": ("fp32 SDPA, the reference's long test shape (4,32,512,512,128)", "f32", 4, 32,
+                     512, 512, 128, "none", 1.0),
+    "long_f32_D2048": ("fp32 SDPA (1,4,512,512,2048)", "f32", 1, 4, 512, 512, 2048, "none", 1.0),
+}
 
 F32_ABS, F32_REL, BF16_REL = 1e-4, 1e-4, 2e-2
+PATH_NAMES: dict = {}  # atn_attention_path_ex code -> kernel(s) per step, filled in main
 
 
 def parse():
@@ -471,13 +482,14 @@ def main():
                                  "fp16 dense rate 2500 / 3; fp32 MFMA's own peak is "
                                  f"{FP32_PEAK_TFLOPS} TFLOP/s")
     path = res["path"]
-    roof["kernel"] = {
+    PATH_NAMES.update({
         am.ATN_PATH_FUSED_SMALL: "k_fused_small (one launch per step)",
-        am.ATN_PATH_SPLIT_D: "split-D pipeline (k_qk_partial + k_softmax + k_pv per step)",
+        am.ATN_PATH_SPLIT_D: "split-D pipeline (QK^T partials + softmax + PV per step)",
         am.ATN_PATH_FLASH: "k_flash_f32 (one launch per step)",
         am.ATN_PATH_GEMM: ("GEMM path (encode, QK^T GEMM with exp epilogue, PV GEMM per step; "
                            "whole-step figure, per-kernel split in profiles/)"),
-    }.get(path, "unknown")
+    })
+    roof["kernel"] = PATH_NAMES.get(path, "unknown")
     roof["timing"] = "HIP events around one graph replay of all timed steps, on its stream"
     ck = cold_kernel(cfg, res)
     if ck is not None:
@@ -507,21 +519,22 @@ def main():
     if a.config == 0 and not a.shape:
         per_config = {}
         others = [(f"cfg2_D{d}", 2, d) for d in SWEEP_D] + [(f"cfg{c}", c, 0) for c in (1, 3, 4, 5)]
+        others += [(k, 0, 0) for k in LONG_F32]
         for key, cid, dov in others:
-            c = list(CONFIGS[cid])
+            c = list(CONFIGS[cid] if cid else LONG_F32[key])
             if dov:
                 c[6] = dov
                 c[0] = c[0].split(" (")[0] + f" ({c[2]},{c[3]},{c[4]},{c[5]},{c[6]})"
             c = tuple(c)
             print(f"[bench] per_config {key}: {c[0]}", file=sys.stderr, flush=True)
-            r, h, rf = run_config(am, hip_rt, c, a.steps, a.warmup, a.seed, cold=cid <= 3)
+            r, h, rf = run_config(am, hip_rt, c, a.steps, a.warmup, a.seed, cold=1 <= cid <= 3)
             chk = sampled_check(c, h, rf)
             ab, fl, g, tf, bd, fr = summarize(c, r)
             ent = {"workload": c[0], "dtype": c[1], "pe": c[7], "ms_per_step": round(r["ms_per_step"], 6),
                    "ms_per_step_median5": round(r["median5_ms_per_step"], 6),
                    "tflops": round(tf, 3), "gbs": round(g, 2), "roofline_bound": bd,
                    "roofline_frac": round(fr, 4), "alg_bytes": ab, "flops": fl,
-                   "check": chk}
+                   "path": PATH_NAMES.get(r["path"], "unknown"), "check": chk}
             if "cold_ms_per_step" in r:
                 ent["cold_ms_per_step"] = round(r["cold_ms_per_step"], 6)
                 ent["bracketed_ms_per_step"] = round(r["bracketed_ms_per_step"], 6)
