@@ -74,7 +74,7 @@ class Tuning(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int) for n in (
         "fused_rows", "fused_dc", "fused_exchange", "fused_xcd", "no_fused", "no_flash",
         "gemm_fused_k",
-        "workspace_cap_mib", "model_cus", "model_xccs", "preset_status", "flash_waves")]
+        "workspace_cap_mib", "model_cus", "model_xccs", "preset_status", "flash_form")]
 
 
 class FusedPlanInfo(ctypes.Structure):
@@ -181,16 +181,19 @@ _SCOPE = {None: 0, "xcd": 1, "device": 2}
 _FUSED_K = {None: 0, "on": 1, "off": 2}
 
 
+_FLASH_FORM = {None: 0, "4x16": 1, "8x16": 2, "4x32": 3}
+
+
 def set_tuning(fused_rows: int = 0, fused_dc: int = 0, fused_exchange: str | None = None,
                fused_xcd: str | None = None, no_fused: bool = False, no_flash: bool = False,
                gemm_fused_k: str | None = None, workspace_cap_mib: int = 0, model_cus: int = 0,
-               model_xccs: int = 0, preset_status: bool = False, flash_waves: int = 0) -> None:
-    """atn_set_tuning_ex with named fields (every field not given is reset)."""
-    if flash_waves not in (0, 4, 8):
-        raise ValueError("flash_waves is 4, 8 or 0 (the default, 8)")
+               model_xccs: int = 0, preset_status: bool = False, flash_form: str | None = None
+               ) -> None:
+    """atn_set_tuning_ex with named fields (every field not given is reset).
+    flash_form: "4x16", "8x16" or "4x32" (waves x query rows per wave)."""
     t = Tuning(fused_rows, fused_dc, _EXCHANGE[fused_exchange], _SCOPE[fused_xcd],
                int(no_fused), int(no_flash), _FUSED_K[gemm_fused_k], workspace_cap_mib,
-               model_cus, model_xccs, int(preset_status), flash_waves)
+               model_cus, model_xccs, int(preset_status), _FLASH_FORM[flash_form])
     st = lib().atn_set_tuning_ex(ctypes.byref(t))
     if st != ATN_OK:
         raise AtnError(st, "atn_set_tuning_ex")

@@ -749,15 +749,29 @@ bool flash_ok(int dtype, const Shape& s, const PePlan& plan) {
            (int64_t)s.Lq * s.D * 4 < lim && (int64_t)s.Lk * s.D * 4 < lim;
 }
 
-// Workgroup size of the flash kernel, in waves (16 query rows each): 8
-// (128 rows sharing each K/V tile's conversion, 64-key tiles at head_d <=
-// 128) measured ahead of 4 (64 rows, 32-key tiles so that two workgroups'
-// double-buffered tiles fit a CU's LDS) on every shape tried, grids of
-// fewer workgroups than CUs included.  atn_tuning.flash_waves forces 4
-// (head dims past 128 always run 8, chosen by the launcher).
-int flash_waves() {
-    const int forced = tune().flash_waves;
-    return forced == 4 ? 4 : 8;
+// The flash kernel's workgroup form (atn_tuning.flash_form forces one).
+// Both default forms hold 128 query rows per workgroup.  4 waves of 32 rows
+// (32 x 32 MFMA tiles) read each K/V tile from LDS once per 32 rows instead
+// of 16 and fit two workgroups per CU, which pays at 64 < head_d <= 128
+// when the grid gives every CU two workgroups (the reference's
+// (4,32,512,512,128): 76 -> 67 us); with fewer, a CU would hold one
+// 4-wave workgroup, and 8 waves of 16 rows are faster (measured).
+int flash_form(const Shape& s, int dev) {
+    const int forced = tune().flash_form;
+    if (forced >= atn::kFlashForm4x16 && forced <= atn::kFlashForm4x32) return forced;
+    if (s.D <= 64 || s.D > 128) return atn::kFlashForm8x16;
+    int cus = 0;
+    {
+        std::lock_guard<std::mutex> lk(g_mu);
+        DeviceState& ds = g_dev[dev];
+        if (ds.cus == 0 &&
+            hipDeviceGetAttribute(&ds.cus, hipDeviceAttributeMultiprocessorCount, dev) !=
+                hipSuccess)
+            ds.cus = 0;
+        cus = ds.cus > 0 ? ds.cus : 256;
+    }
+    return s.BH * ((s.Lq + 127) / 128) >= (int64_t)2 * cus ? atn::kFlashForm4x32
+                                                           : atn::kFlashForm8x16;
 }
 
 // Scratch bytes of the path a call of shape s takes: fused (when planned and
@@ -929,7 +943,7 @@ int attention_run(int dtype, const void* Q, const void* K, const void* V, void* 
         return ATN_OK;
     }
     if (use_flash) {
-        ATN_HIP(atn::launch_flash(plan.pek, flash_waves(), static_cast<const float*>(Q),
+        ATN_HIP(atn::launch_flash(plan.pek, flash_form(s, dev), static_cast<const float*>(Q),
                                   static_cast<const float*>(K), static_cast<const float*>(V),
                                   static_cast<float*>(out), (int)s.BH, Lq, Lk, D, scale, plan.q,
                                   plan.k, stream));

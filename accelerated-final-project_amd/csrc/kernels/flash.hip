@@ -3,13 +3,14 @@
 //
 // The reference's kernel (final/attention.cu:84-191) walks the keys of one
 // query row in 64-key tiles with an online softmax and keeps the running
-// output in global memory.  Here a workgroup owns 64 or 128 query rows (16
-// per wave, 4 or 8 waves) of one head and walks the head's keys in tiles of
-// KT keys (64 for 8 waves at D <= 128 without an encoding, else 32; at
-// least one load round of the workgroup), with the running output of its
-// rows in registers.  8 waves (the library's choice) convert each K/V tile
-// once for twice the rows of 4 (a tuning override, which makes twice the
-// workgroups).
+// output in global memory.  Here a workgroup owns the query rows of its
+// waves, 16 or 32 per wave (v_mfma_f32_16x16x32_f16 or 32x32x16 tiles), of
+// one head and walks the head's keys in tiles of KT keys, with the running
+// output of its rows in registers.  Three forms: 8 waves of 16 rows (64-key
+// tiles at D <= 128 without an encoding), 4 waves of 32 rows (D <= 128,
+// 32-key tiles: each wave reads a K/V tile from LDS once per 32 rows
+// instead of 16, and two workgroups fit a CU), and 4 waves of 16 rows (a
+// tuning override).
 //
 //   Per tile: K and V rows are loaded (16-byte loads) two tiles ahead, K
 //   encoded (RoPE, sinusoidal) once they land, and reduced to per-wave
@@ -18,22 +19,23 @@
 //   lies outside [2^-3, 65504), V only beyond fp16's range: its scale
 //   carries over into the running output) and it is stored to one of two
 //   LDS buffers as hi + lo fp16 parts (the fp32 split of the single-launch
-//   kernel: 22 significant bits per operand, exact products on
-//   v_mfma_f32_16x16x32_f16, fp32 accumulation).  One barrier per tile
-//   orders all of it.
-//   Each wave computes S^T = K Q^T for its 16 query rows (Q in registers,
+//   kernel: 22 significant bits per operand, exact products on the fp16
+//   MFMAs, fp32 accumulation).  One barrier per tile orders all of it.
+//   Each wave computes S^T = K Q^T for its query rows (Q in registers,
 //   split once, scaled by a power of two per wave) -- transposed, so that a
 //   lane holds 16 scores of ONE query: the online-softmax statistics
 //   (running max m, running sum l) of a query live in the lanes that hold
-//   its scores and its output row, and reductions over a tile's keys are 16
-//   values in registers plus two row swaps (v_permlane16/32_swap).
+//   its scores and its output row (4 lanes with 16-row tiles, 2 with
+//   32-row ones), and reductions over a tile's keys are 16 values in
+//   registers plus one or two row swaps (v_permlane16/32_swap).
 //   P = 2^(x - m + 15) (base 2, its 2^15 via the exponent) stays in
 //   registers, where the accumulator layout of S^T is already the B operand
-//   of O^T += V^T P^T (the keys of each 32-key block in the order
-//   4g + 0..3, 16 + 4g + 0..3 for lane group g; V's transposing LDS read,
-//   ds_read_b64_tr_b16, takes the same order), and O^T (16 dims x 16
-//   queries per MFMA tile) accumulates in registers, rescaled per tile by
-//   2^(m_old - m_new) and by the ratio of consecutive V tiles' scales.
+//   of O^T += V^T P^T (the keys of each 32- or 16-key block in the order
+//   4g + 0..3, then 16 + 4g + 0..3 or 8 + 4g + 0..3, for lane group g; V's
+//   transposing LDS read, ds_read_b64_tr_b16, takes the same order), and O^T
+//   (dims x queries per MFMA tile) accumulates in registers, rescaled per
+//   tile by 2^(m_old - m_new) and by the ratio of consecutive V tiles'
+//   scales.
 //
 // The score matrix never reaches memory: per call the kernel reads Q once
 // and K and V once per query block, and writes O once.
@@ -48,20 +50,26 @@ namespace atn {
 
 namespace {
 
-// Tiling for head dims padded to DP (32, 64, 128 or 256) and NW waves per
-// workgroup (4 or 8; 16 query rows each, sharing each K/V tile).  The key
-// tile is 64 keys for 8 waves at DP <= 128 without a positional encoding
-// (PE), else 32 (two LDS buffers of it then leave room for two 4-wave
-// workgroups per CU), and at least one load round of the workgroup.
-template <int DP, bool PE, int NW>
+// Tiling for head dims padded to DP (32, 64, 128 or 256), NW waves per
+// workgroup (4 or 8) and RW query rows per wave (16: v_mfma_f32_16x16x32_f16
+// tiles; 32: v_mfma_f32_32x32x16_f16 tiles, D <= 128), every wave sharing
+// each K/V tile.  The key tile is 64 keys for 8 waves of 16 rows at DP <=
+// 128 without a positional encoding (PE), else 32 (two LDS buffers of it
+// then leave room for two 4-wave workgroups per CU), and at least one load
+// round of the workgroup.
+template <int DP, bool PE, int NW, int RW>
 struct FlashGeo {
-    static constexpr int THREADS = 64 * NW, ROWS = 16 * NW;
-    static constexpr int KT0 = DP <= 128 && !PE && NW == 8 ? 64 : 32;
+    static_assert(RW == 16 || (RW == 32 && DP <= 128), "forms");
+    static constexpr int THREADS = 64 * NW, ROWS = RW * NW;
+    static constexpr int KT0 = DP <= 128 && !PE && NW == 8 && RW == 16 ? 64 : 32;
     static constexpr int KT = KT0 > THREADS / (DP / 4) ? KT0 : THREADS / (DP / 4);
-    static constexpr int KS = DP / 32;              // 32-deep steps of Q K^T
-    static constexpr int NJ = KT / 16;              // 16-key tiles of S^T
-    static constexpr int NB = KT / 32;              // 32-key blocks of P V
-    static constexpr int NDT = DP / 16;             // 16-dim tiles of O^T
+    static constexpr int MT = RW;                   // MFMA tile edge
+    static constexpr int KD = RW == 16 ? 32 : 16;   // MFMA depth: dims of Q K^T, keys of P V
+    static constexpr int KS = DP / KD;              // KD-deep steps of Q K^T
+    static constexpr int NJ = KT / MT;              // MT-key tiles of S^T
+    static constexpr int NB = KT / KD;              // KD-key blocks of P V
+    static constexpr int NDT = DP / MT;             // MT-dim tiles of O^T
+    static constexpr int SPT = MT * MT / 64;        // accumulator floats per lane and tile
     static constexpr int VPR = DP / 4;              // 16-byte vectors per row
     static constexpr int RSTEP = THREADS / VPR;     // rows per load round
     static constexpr int NLD = KT / RSTEP;          // load rounds per tile
@@ -73,9 +81,11 @@ struct FlashGeo {
                          V_LO = V_HI + KT * VSTR;
     static constexpr int TILE = 2 * KT * KSTR + 2 * KT * VSTR;
     static constexpr int BYTES = 2 * 2 * TILE;
-    static_assert(KT % RSTEP == 0, "whole load rounds");
+    static_assert(KT % RSTEP == 0 && KT % MT == 0 && KT % KD == 0, "whole tiles");
     static_assert(BYTES <= 160 * 1024, "LDS");
 };
+
+typedef float v16f __attribute__((ext_vector_type(16)));
 
 // max without the operand canonicalization fmaxf brings (the values are
 // never signalling NaNs).  Inline asm: the compiler's hazard checks do not
@@ -84,23 +94,30 @@ struct FlashGeo {
 // instruction before a cross-lane operation or an MFMA reads it.
 __device__ __forceinline__ float fmax_raw(float a, float b) { return vmaxf(a, b); }
 
-// lanes L, L ^ 16, L ^ 32, L ^ 48 (the four lane groups of one query), by
-// gfx950's row-swapping permutes: v_permlane16_swap and v_permlane32_swap
-// each leave a lane its own value and its partner's, in registers, in the
-// same order for both lanes of a pair (so sums agree bit for bit)
+// the lanes that hold one query's scores (RW = 16: L, L ^ 16, L ^ 32,
+// L ^ 48; RW = 32: L, L ^ 32), by gfx950's row-swapping permutes:
+// v_permlane16_swap and v_permlane32_swap each leave a lane its own value
+// and its partner's, in registers, in the same order for both lanes of a
+// pair (so sums agree bit for bit)
+template <int RW>
 __device__ __forceinline__ float xgroup_max(float v) {
     v = __builtin_canonicalizef(v);
-    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v),
-                                                    false, false);
-    v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    if constexpr (RW == 16) {
+        const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v),
+                                                        false, false);
+        v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    }
     const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v),
                                                     false, false);
     return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
+template <int RW>
 __device__ __forceinline__ float xgroup_sum(float v) {
-    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v),
-                                                    false, false);
-    v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    if constexpr (RW == 16) {
+        const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v),
+                                                        false, false);
+        v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    }
     const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v),
                                                     false, false);
     return __uint_as_float(b[0]) + __uint_as_float(b[1]);
@@ -113,10 +130,18 @@ __device__ __forceinline__ float wave_max_rows(float v) {
     v = fmaxf(v, dpp<kDppQuadXor2>(v));
     v = fmaxf(v, dpp<kDppRowHalfMirror>(v));
     v = fmaxf(v, dpp<kDppRowMirror>(v));
-    return xgroup_max(v);
+    return xgroup_max<16>(v);
 }
 
-template <int DP, int PEK, int NW>
+// the form's MFMA: 16 x 16 x 32 or 32 x 32 x 16, fp16 operands, fp32 sums
+__device__ __forceinline__ v4f mfma_rw(const f16x8& a, const f16x8& b, const v4f& c) {
+    return mfma_f16(a, b, c);
+}
+__device__ __forceinline__ v16f mfma_rw(const f16x8& a, const f16x8& b, const v16f& c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+template <int DP, int PEK, int NW, int RW>
 __global__ __launch_bounds__(64 * NW, 8 / NW) void k_flash_f32(const float* __restrict__ Qg,
                                                                  const float* __restrict__ Kg,
                                                                  const float* __restrict__ Vg,
@@ -124,7 +149,8 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_flash_f32(const float* __re
                                                                  int Lk, int D, int qblocks,
                                                                  float scale, PeSide pq,
                                                                  PeSide pk) {
-    using G = FlashGeo<DP, PEK != kPeNone, NW>;
+    using G = FlashGeo<DP, PEK != kPeNone, NW, RW>;
+    typedef std::conditional_t<RW == 16, v4f, v16f> acc_t;
     extern __shared__ __align__(16) unsigned char smem_raw[];
     uint16_t* smem = reinterpret_cast<uint16_t*>(smem_raw);
     // per-wave K and V magnitude maxima of a loaded tile, by tile parity
@@ -133,7 +159,8 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_flash_f32(const float* __re
     const float one = unit_opaque();  // (see split2_f16_one)
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int lr = lane & 15, lg = lane >> 4;
+    // lane (row lr of its MFMA tiles, lane group lg)
+    const int lr = lane & (RW - 1), lg = lane / RW;
     // workgroup -> (head, query block); with a grid that is a multiple of 8
     // the query blocks of a head are consecutive on one XCD (the dispatcher
     // deals ids to the 8 XCDs round robin), so its K and V stay in that L2
@@ -147,10 +174,10 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_flash_f32(const float* __re
     const float* Vh = Vg + (size_t)bh * Lk * D;
     constexpr int kOob = kBufOob;
 
-    // ---- Q: this wave's 16 rows as the B operand of S^T = K Q^T: lane
-    // (query lr, group lg) holds dims 32 ks + 8 lg + 0..7, scaled by a
+    // ---- Q: this wave's RW rows as the B operand of S^T = K Q^T: lane
+    // (query lr, group lg) holds dims KD ks + 8 lg + 0..7, scaled by a
     // power of two from the wave's largest finite magnitude
-    const int qrow = q0 + 16 * wave + lr;
+    const int qrow = q0 + RW * wave + lr;
     f16x8 qh[G::KS], ql[G::KS];
     float uq;
     {
@@ -161,7 +188,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_flash_f32(const float* __re
         for (int ks = 0; ks < G::KS; ++ks)
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
-                const int d = 32 * ks + 8 * lg + 4 * h;
+                const int d = G::KD * ks + 8 * lg + 4 * h;
                 if constexpr (PEK == kPeNone) {
                     qv[ks][h] = ld_buf_f4(rq, d < D ? (qrow * D + d) * 4 : kOob);
                 } else {
@@ -204,7 +231,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_flash_f32(const float* __re
 #pragma unroll
         for (int i = 0; i < G::NLD; ++i) {
             const int key = k0 + lrow + G::RSTEP * i;
-            const int off = lcol < D ? (key * D + lcol) * 4 : kOob;
+            const int off = key < Lk && lcol < D ? (key * D + lcol) * 4 : kOob;
             kr[i] = ld_buf_f4(rk, off);
             vr[i] = ld_buf_f4(rv, off);
         }
@@ -300,13 +327,14 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_flash_f32(const float* __re
     };
 
     // running statistics of this lane's query and its output rows (O^T
-    // tiles: lane holds dims 16 t + 4 lg + 0..3 of query lr): the max in
-    // base-2 units of the scores, the sum in units of 2^15, the output in
-    // units of uv / 2^15 for the current V tile's unit uv = 1 / sv
+    // tiles: register r of tile t holds dim MT t + 8 (r / 4) + 4 lg + r % 4
+    // of query lr): the max in base-2 units of the scores, the sum in units
+    // of 2^15, the output in units of uv / 2^15 for the current V tile's
+    // unit uv = 1 / sv
     float m_run = -INFINITY, l_run = 0.f, uv_prev = 1.f;
-    v4f o[G::NDT];
+    acc_t o[G::NDT];
 #pragma unroll
-    for (int t = 0; t < G::NDT; ++t) o[t] = v4f{0.f, 0.f, 0.f, 0.f};
+    for (int t = 0; t < G::NDT; ++t) o[t] = acc_t{};
 
     const int ntiles = (Lk + G::KT - 1) / G::KT;
     float uk, sv, uv;  // scales of the tile staged last
@@ -328,11 +356,12 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_flash_f32(const float* __re
         }
         const uint16_t* buf = smem + par * G::TILE;
 
-        // ---- S^T tile: s[j] = keys 16 j + 4 lg + r, query lr
-        v4f s[G::NJ];
+        // ---- S^T tiles: register r of s[j] = key MT j + 8 (r / 4) + 4 lg +
+        // r % 4, query lr
+        acc_t s[G::NJ];
 #pragma unroll
-        for (int j = 0; j < G::NJ; ++j) s[j] = v4f{0.f, 0.f, 0.f, 0.f};
-        // per 32-deep step: the step's 2 NJ fragment reads first, then its
+        for (int j = 0; j < G::NJ; ++j) s[j] = acc_t{};
+        // per KD-deep step: the step's 2 NJ fragment reads first, then its
         // 3 NJ products (kept in that order, so the reads' latencies overlap
         // instead of each read being waited for before its product)
 #pragma unroll
@@ -340,16 +369,16 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_flash_f32(const float* __re
             f16x8 ah[G::NJ], al[G::NJ];
 #pragma unroll
             for (int j = 0; j < G::NJ; ++j) {
-                const int a = (16 * j + lr) * G::KSTR + 32 * ks + 8 * lg;
+                const int a = (G::MT * j + lr) * G::KSTR + G::KD * ks + 8 * lg;
                 ah[j] = lds8_f16(buf + G::K_HI + a);
                 al[j] = lds8_f16(buf + G::K_LO + a);
             }
 #pragma unroll
-            for (int j = 0; j < G::NJ; ++j) s[j] = mfma_f16(ah[j], qh[ks], s[j]);
+            for (int j = 0; j < G::NJ; ++j) s[j] = mfma_rw(ah[j], qh[ks], s[j]);
 #pragma unroll
-            for (int j = 0; j < G::NJ; ++j) s[j] = mfma_f16(ah[j], ql[ks], s[j]);
+            for (int j = 0; j < G::NJ; ++j) s[j] = mfma_rw(ah[j], ql[ks], s[j]);
 #pragma unroll
-            for (int j = 0; j < G::NJ; ++j) s[j] = mfma_f16(al[j], qh[ks], s[j]);
+            for (int j = 0; j < G::NJ; ++j) s[j] = mfma_rw(al[j], qh[ks], s[j]);
             __builtin_amdgcn_sched_group_barrier(0x100, 2 * G::NJ, 0);  // DS reads
             __builtin_amdgcn_sched_group_barrier(0x008, 3 * G::NJ, 0);  // MFMA
         }
@@ -363,39 +392,41 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_flash_f32(const float* __re
 #pragma unroll
             for (int j = 0; j < G::NJ; ++j)
 #pragma unroll
-                for (int r = 0; r < 4; ++r) mt = fmaxf(mt, s[j][r]);
+                for (int r = 0; r < G::SPT; ++r) mt = fmaxf(mt, s[j][r]);
         } else {
 #pragma unroll
             for (int j = 0; j < G::NJ; ++j)
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    if (k0 + 16 * j + 4 * lg + r >= Lk) s[j][r] = -INFINITY;
+                for (int r = 0; r < G::SPT; ++r) {
+                    if (k0 + G::MT * j + 8 * (r >> 2) + 4 * lg + (r & 3) >= Lk)
+                        s[j][r] = -INFINITY;
                     mt = fmaxf(mt, s[j][r]);
                 }
         }
-        const float m_new = fmaxf(m_run, xgroup_max(mt) * c2);  // c2 > 0
+        const float m_new = fmaxf(m_run, xgroup_max<RW>(mt) * c2);  // c2 > 0
         const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // 0 on the first tile
         m_run = m_new;
         // P = 2^(x - m_new + 15): one FMA and one v_exp_f32 per score, the
         // 2^15 that keeps P's lo parts normal in fp16 folded into the exponent
         const float nm = 15.f - m_new;
         float ps = 0.f;
-        // P as the B operand of block b: elements 0..3 tile 2b, 4..7 tile 2b+1
+        // P as the B operand of block b: the lane's scores 8 b .. 8 b + 7 in
+        // the order of s (RW = 16: elements 0..3 from tile 2b, 4..7 from
+        // tile 2b + 1, i.e. keys 4 lg + 0..3, 16 + 4 lg + 0..3 of the 32-key
+        // block; RW = 32: registers 8 (b % 2) + 0..7 of tile b / 2, i.e.
+        // keys 4 lg + 0..3, 8 + 4 lg + 0..3 of the 16-key block)
         f16x8 ph[G::NB], pl[G::NB];
 #pragma unroll
         for (int b = 0; b < G::NB; ++b) {
             uint32_t h[4], l[4];
 #pragma unroll
-            for (int half = 0; half < 2; ++half) {
-                const v4f& sj = s[2 * b + half];
-                float p[4];
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    p[r] = __builtin_amdgcn_exp2f(fmaf(sj[r], c2, nm));
-                    ps += p[r];
-                }
-                split2_f16_one(p[0], p[1], one, h[2 * half], l[2 * half]);
-                split2_f16_one(p[2], p[3], one, h[2 * half + 1], l[2 * half + 1]);
+            for (int e = 0; e < 8; e += 2) {
+                const int i0 = 8 * b + e, i1 = i0 + 1;
+                const float p0 = __builtin_amdgcn_exp2f(fmaf(s[i0 / G::SPT][i0 % G::SPT], c2, nm));
+                const float p1 = __builtin_amdgcn_exp2f(fmaf(s[i1 / G::SPT][i1 % G::SPT], c2, nm));
+                ps += p0;
+                ps += p1;
+                split2_f16_one(p0, p1, one, h[e / 2], l[e / 2]);
             }
             ph[b] = __builtin_bit_cast(f16x8, make_uint4(h[0], h[1], h[2], h[3]));
             pl[b] = __builtin_bit_cast(f16x8, make_uint4(l[0], l[1], l[2], l[3]));
@@ -408,23 +439,28 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_flash_f32(const float* __re
             for (int dt = 0; dt < G::NDT; ++dt) o[dt] *= f;
         }
 
-        // ---- O^T += V^T P^T: A = V^T from the transposing read, keys of
-        // block b in P's order (rows 4 lg + 0..3, then 16 + 4 lg + 0..3)
-        const int vrow = 4 * lg + (lr >> 2), vcol = 4 * (lr & 3);
+        // ---- O^T += V^T P^T: A = V^T from the transposing read (each group
+        // of 16 lanes reads 4 key rows x 16 dims; a lane receives its dim's 4
+        // keys), keys of block b in P's order: rows 4 lg + 0..3, then
+        // KD / 2 + 4 lg + 0..3 of the block; RW = 16: dims 16 dt + lane % 16;
+        // RW = 32: dims 32 dt + lane % 32
+        const int vrow = 4 * lg + ((lane & 15) >> 2);
+        const int vcol = (RW == 32 ? 16 * ((lane >> 4) & 1) : 0) + 4 * (lane & 3);
 #pragma unroll
         for (int dt = 0; dt < G::NDT; ++dt) {
 #pragma unroll
             for (int b = 0; b < G::NB; ++b) {
-                const int a = (32 * b + vrow) * G::VSTR + 16 * dt + vcol;
+                const int a = (G::KD * b + vrow) * G::VSTR + G::MT * dt + vcol;
+                constexpr int half = G::KD / 2 * G::VSTR;
                 const uint2 h0 = lds_tr16(buf + G::V_HI + a);
-                const uint2 h1 = lds_tr16(buf + G::V_HI + a + 16 * G::VSTR);
+                const uint2 h1 = lds_tr16(buf + G::V_HI + a + half);
                 const uint2 l0 = lds_tr16(buf + G::V_LO + a);
-                const uint2 l1 = lds_tr16(buf + G::V_LO + a + 16 * G::VSTR);
+                const uint2 l1 = lds_tr16(buf + G::V_LO + a + half);
                 const f16x8 vh = __builtin_bit_cast(f16x8, make_uint4(h0.x, h0.y, h1.x, h1.y));
                 const f16x8 vl = __builtin_bit_cast(f16x8, make_uint4(l0.x, l0.y, l1.x, l1.y));
-                o[dt] = mfma_f16(vh, ph[b], o[dt]);
-                o[dt] = mfma_f16(vh, pl[b], o[dt]);
-                o[dt] = mfma_f16(vl, ph[b], o[dt]);
+                o[dt] = mfma_rw(vh, ph[b], o[dt]);
+                o[dt] = mfma_rw(vh, pl[b], o[dt]);
+                o[dt] = mfma_rw(vl, ph[b], o[dt]);
             }
         }
 
@@ -432,65 +468,75 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_flash_f32(const float* __re
         __syncthreads();
     }
 
-    // ---- O = O^T uv / l (O^T and l both in units of 2^15): one 16-byte
-    // store per dim tile
-    const float l = xgroup_sum(l_run);
-    const float inv = 1.0f / l;
+    // ---- O = O^T uv / l (O^T and l both in units of 2^15): 16-byte stores
+    // of 4 consecutive dims
+    const float l = xgroup_sum<RW>(l_run);
+    const float inv = uv_prev / l;
     if (qrow < Lq) {
         float* orow = Og + ((size_t)bh * Lq + qrow) * D;
 #pragma unroll
-        for (int dt = 0; dt < G::NDT; ++dt) {
-            const int d = 16 * dt + 4 * lg;
-            if (d < D)
-                *reinterpret_cast<float4*>(orow + d) =
-                    make_float4(o[dt][0] * inv * uv_prev, o[dt][1] * inv * uv_prev,
-                                o[dt][2] * inv * uv_prev, o[dt][3] * inv * uv_prev);
-        }
+        for (int dt = 0; dt < G::NDT; ++dt)
+#pragma unroll
+            for (int r = 0; r < G::SPT; r += 4) {
+                const int d = G::MT * dt + 8 * (r >> 2) + 4 * lg;
+                if (d < D)
+                    *reinterpret_cast<float4*>(orow + d) =
+                        make_float4(o[dt][r] * inv, o[dt][r + 1] * inv, o[dt][r + 2] * inv,
+                                    o[dt][r + 3] * inv);
+            }
     }
 }
 
-template <int DP, int PEK, int NW>
+template <int DP, int PEK, int NW, int RW>
 hipError_t launch_t(const float* Q, const float* K, const float* V, float* O, int BH, int Lq,
                     int Lk, int D, float scale, const PeSide& pq, const PeSide& pk,
                     hipStream_t st) {
-    using G = FlashGeo<DP, PEK != kPeNone, NW>;
+    using G = FlashGeo<DP, PEK != kPeNone, NW, RW>;
     static bool attr = false;
     if (!attr) {
-        hipError_t e = hipFuncSetAttribute((const void*)k_flash_f32<DP, PEK, NW>,
+        hipError_t e = hipFuncSetAttribute((const void*)k_flash_f32<DP, PEK, NW, RW>,
                                            hipFuncAttributeMaxDynamicSharedMemorySize, G::BYTES);
         if (e != hipSuccess) return e;
         attr = true;
     }
     const int qblocks = (Lq + G::ROWS - 1) / G::ROWS;
-    hipLaunchKernelGGL((k_flash_f32<DP, PEK, NW>), dim3((unsigned)(BH * qblocks)),
+    hipLaunchKernelGGL((k_flash_f32<DP, PEK, NW, RW>), dim3((unsigned)(BH * qblocks)),
                        dim3(G::THREADS), G::BYTES, st, Q, K, V, O, Lq, Lk, D, qblocks, scale, pq,
                        pk);
     return hipGetLastError();
 }
 
-template <int PEK, int NW>
+// head dims padded to 32, 64, 128 (and 256 for 8 waves of 16 rows without
+// an encoding)
+template <int PEK, int NW, int RW>
 hipError_t launch_pe(const float* Q, const float* K, const float* V, float* O, int BH, int Lq,
                      int Lk, int D, float scale, const PeSide& pq, const PeSide& pk,
                      hipStream_t st) {
-    if (D <= 32) return launch_t<32, PEK, NW>(Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk, st);
-    if (D <= 64) return launch_t<64, PEK, NW>(Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk, st);
-    if (D <= 128) return launch_t<128, PEK, NW>(Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk, st);
-    if constexpr (PEK == kPeNone && NW == 8)
-        return launch_t<256, PEK, NW>(Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk, st);
-    return hipErrorInvalidValue;  // encoded calls have D <= 128; D > 128 takes 8 waves
+    if (D <= 32) return launch_t<32, PEK, NW, RW>(Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk, st);
+    if (D <= 64) return launch_t<64, PEK, NW, RW>(Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk, st);
+    if (D <= 128) return launch_t<128, PEK, NW, RW>(Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk, st);
+    if constexpr (PEK == kPeNone && NW == 8 && RW == 16)
+        return launch_t<256, PEK, NW, RW>(Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk, st);
+    return hipErrorInvalidValue;
 }
 
 template <int PEK>
-hipError_t launch_w(int waves, const float* Q, const float* K, const float* V, float* O, int BH,
-                    int Lq, int Lk, int D, float scale, const PeSide& pq, const PeSide& pk,
-                    hipStream_t st) {
-    // (head dims past 128 take 8 waves: two buffers of a 256-wide tile
-    // leave room for one workgroup per CU, so 4 waves would leave half the
-    // SIMDs' wave slots empty)
-    if (waves == 8 || D > 128)
-        return launch_pe<PEK, 8>(Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk, st);
-    if (waves == 4) return launch_pe<PEK, 4>(Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk, st);
-    return hipErrorInvalidValue;
+hipError_t launch_form(int form, const float* Q, const float* K, const float* V, float* O,
+                       int BH, int Lq, int Lk, int D, float scale, const PeSide& pq,
+                       const PeSide& pk, hipStream_t st) {
+    // head dims past 128 run 8 waves of 16 rows: two buffers of a 256-wide
+    // tile leave room for one workgroup per CU, and 32-row waves would not
+    // hold the query's and the output's registers
+    if (D > 128) form = kFlashForm8x16;
+    switch (form) {
+        case kFlashForm4x16:
+            return launch_pe<PEK, 4, 16>(Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk, st);
+        case kFlashForm8x16:
+            return launch_pe<PEK, 8, 16>(Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk, st);
+        case kFlashForm4x32:
+            return launch_pe<PEK, 4, 32>(Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk, st);
+        default: return hipErrorInvalidValue;
+    }
 }
 
 }  // namespace
@@ -500,19 +546,19 @@ bool flash_supported(int dtype, int pek, int D) {
            D <= (pek == kPeNone ? kFlashMaxD : kFlashMaxDEncoded);
 }
 
-hipError_t launch_flash(int pek, int waves, const float* Q, const float* K, const float* V,
+hipError_t launch_flash(int pek, int form, const float* Q, const float* K, const float* V,
                         float* O, int BH, int Lq, int Lk, int D, float scale, const PeSide& pq,
                         const PeSide& pk, hipStream_t st) {
     switch (pek) {
         case kPeNone:
-            return launch_w<kPeNone>(waves, Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk, st);
+            return launch_form<kPeNone>(form, Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk, st);
         case kPeRopeInterleaved:
-            return launch_w<kPeRopeInterleaved>(waves, Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk,
-                                                st);
+            return launch_form<kPeRopeInterleaved>(form, Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk,
+                                                   st);
         case kPeRopeHalf:
-            return launch_w<kPeRopeHalf>(waves, Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk, st);
+            return launch_form<kPeRopeHalf>(form, Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk, st);
         case kPeSinusoidal:
-            return launch_w<kPeSinusoidal>(waves, Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk, st);
+            return launch_form<kPeSinusoidal>(form, Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk, st);
         default: return hipErrorInvalidValue;
     }
 }

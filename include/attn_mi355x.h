@@ -331,8 +331,9 @@ typedef struct atn_tuning {
                               its workspace's status word set, as a timed-out call leaves
                               it, so its workgroups take the fail-closed exit (no wait is
                               entered) */
-    int flash_waves;       /* flash kernel: 4 or 8 waves (64 or 128 query rows) per
-                              workgroup (head_d > 128 always 8); 0: 8 */
+    int flash_form;        /* flash kernel workgroup: 1 = 4 waves of 16 query rows,
+                              2 = 8 waves of 16, 3 = 4 waves of 32 (head_d <= 128;
+                              head_d > 128 always runs 2); 0: the library's choice */
 } atn_tuning;
 /* Replaces the overrides (NULL: all zero) and drops cached plans.  Plans
  * that a forced setting makes impossible fall back to the library's

@@ -268,10 +268,10 @@ def test_tuning_round_trip_and_plan_overrides(am, tuner):
     tuner.set(no_fused=True)
     assert am.fused_plan(0, 1, 4, 64, 64, 2048) is None
     assert am.path(0, 1, 4, 64, 64, 2048) == am.ATN_PATH_SPLIT_D
-    tuner.set(flash_waves=8)
-    assert am.get_tuning().flash_waves == 8
-    with pytest.raises(ValueError):
-        am.set_tuning(flash_waves=6)
+    tuner.set(flash_form="4x32")
+    assert am.get_tuning().flash_form == 3
+    with pytest.raises(KeyError):
+        am.set_tuning(flash_form="6x16")
 
 
 @pytest.mark.parametrize("cus,xccs", [(32, 1), (64, 2), (128, 4), (256, 4), (252, 8), (256, 8)])

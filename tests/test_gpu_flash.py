@@ -46,18 +46,20 @@ def test_flash_f32(am, dev, shape):
     assert n == 0, f"{n} mismatches, max abs {mabs}, max rel {mrel}"
 
 
-@pytest.mark.parametrize("waves", [4, 8])
+@pytest.mark.parametrize("form", ["4x16", "8x16", "4x32"])
 @pytest.mark.parametrize("shape,pe", [((1, 3, 130, 129, 32), None), ((1, 2, 200, 300, 128), None),
                                       ((1, 2, 96, 200, 256), None), ((1, 2, 129, 97, 64), "rope"),
                                       ((1, 2, 150, 333, 128), "sinusoidal")],
                          ids=lambda v: "x".join(map(str, v)) if isinstance(v, tuple) else str(v))
-def test_flash_workgroup_forms(am, dev, tuner, waves, shape, pe):
-    """Both workgroup sizes (4 and 8 waves: 64- and 128-row query blocks,
-    key tiles of at least one load round) forced on the same inputs."""
+def test_flash_workgroup_forms(am, dev, tuner, form, shape, pe):
+    """Every workgroup form forced on the same inputs: 4 waves of 16 query
+    rows, 8 of 16 and 4 of 32 (16 x 16 x 32 or 32 x 32 x 16 MFMA tiles;
+    64-, 128- and 128-row query blocks; key tiles of at least one load
+    round); head_d 256 runs 8 of 16 whatever is forced."""
     B, Hh, Lq, Lk, D = shape
-    print(f"[case] flash f32 {waves} waves {shape} {pe}", flush=True)
-    tuner.set(flash_waves=waves)
-    Q, K, V = H.rng_inputs((B, Hh, Lq, D), (B, Hh, Lk, D), seed=7 + Lk + waves,
+    print(f"[case] flash f32 form {form} {shape} {pe}", flush=True)
+    tuner.set(flash_form=form)
+    Q, K, V = H.rng_inputs((B, Hh, Lq, D), (B, Hh, Lk, D), seed=7 + Lk + len(form),
                            sigma=0.5 if pe == "sinusoidal" else 1.0)
     desc = None if pe is None else am.make_pe(pe)
     got = _f32_call(am, Q, K, V, desc)
@@ -74,19 +76,19 @@ def test_flash_workgroup_forms(am, dev, tuner, waves, shape, pe):
     assert n == 0, f"{n} mismatches, max abs {mabs}, max rel {mrel}"
 
 
-@pytest.mark.parametrize("waves", [4, 8])
+@pytest.mark.parametrize("form", ["4x16", "8x16", "4x32"])
 @pytest.mark.parametrize("D", [32, 64, 128])
-def test_flash_tile_counts(am, dev, tuner, waves, D):
+def test_flash_tile_counts(am, dev, tuner, form, D):
     """Key lengths of 2 to 17 tiles, two seeds each, both workgroup forms.
     Regression: a build whose softmax read the QK^T accumulators through an
     inline-asm max (which the compiler's MFMA hazard waits do not cover)
     gave wrong rows scattered over these cases whenever the schedule put
     that read right behind the MFMAs."""
-    tuner.set(flash_waves=waves)
+    tuner.set(flash_form=form)
     B, Hh, Lq = 1, 2, 70
     for Lk in (65, 70, 96, 97, 128, 129, 200, 513):
         for seed in (1, 2):
-            print(f"[case] flash f32 {waves} waves D={D} Lk={Lk} seed={seed}", flush=True)
+            print(f"[case] flash f32 form {form} D={D} Lk={Lk} seed={seed}", flush=True)
             Q, K, V = H.rng_inputs((B, Hh, Lq, D), (B, Hh, Lk, D), seed=seed * 1000 + Lk + D)
             got = _f32_call(am, Q, K, V)
             n, mabs, mrel = H.check_f32(got, oracle.attention(Q, K, V, nthreads=16))
