@@ -181,7 +181,7 @@ _SCOPE = {None: 0, "xcd": 1, "device": 2}
 _FUSED_K = {None: 0, "on": 1, "off": 2}
 
 
-_FLASH_FORM = {None: 0, "4x16": 1, "8x16": 2, "4x32": 3}
+_FLASH_FORM = {None: 0, "4x16": 1, "8x16": 2, "4x32": 3, "8x32": 4}
 
 
 def set_tuning(fused_rows: int = 0, fused_dc: int = 0, fused_exchange: str | None = None,

@@ -750,16 +750,17 @@ bool flash_ok(int dtype, const Shape& s, const PePlan& plan) {
 }
 
 // The flash kernel's workgroup form (atn_tuning.flash_form forces one).
-// Both default forms hold 128 query rows per workgroup.  4 waves of 32 rows
-// (32 x 32 MFMA tiles) read each K/V tile from LDS once per 32 rows instead
-// of 16 and fit two workgroups per CU, which pays at 64 < head_d <= 128
-// when the grid gives every CU two workgroups (the reference's
-// (4,32,512,512,128): 76 -> 67 us); with fewer, a CU would hold one
-// 4-wave workgroup, and 8 waves of 16 rows are faster (measured).
+// 8 waves of 32 query rows (32 x 32 MFMA tiles: each wave reads a K/V tile
+// from LDS once per 32 rows, and each tile is converted once per 256 rows)
+// when head_d <= 128 and the grid of 256-row blocks gives every CU a
+// workgroup; else 8 waves of 16 rows (twice the workgroups).  Measured
+// with interleaved rounds on 14 shapes: the reference's (4,32,512,512,128)
+// 70.6 -> 62.9 us, RoPE there 108 -> 86 us; below a workgroup per CU the
+// 32-row form loses (up to 1.6x at (1,4,2048,2048,128)).
 int flash_form(const Shape& s, int dev) {
     const int forced = tune().flash_form;
-    if (forced >= atn::kFlashForm4x16 && forced <= atn::kFlashForm4x32) return forced;
-    if (s.D <= 64 || s.D > 128) return atn::kFlashForm8x16;
+    if (forced >= atn::kFlashForm4x16 && forced <= atn::kFlashForm8x32) return forced;
+    if (s.D > 128) return atn::kFlashForm8x16;
     int cus = 0;
     {
         std::lock_guard<std::mutex> lk(g_mu);
@@ -770,8 +771,8 @@ int flash_form(const Shape& s, int dev) {
             ds.cus = 0;
         cus = ds.cus > 0 ? ds.cus : 256;
     }
-    return s.BH * ((s.Lq + 127) / 128) >= (int64_t)2 * cus ? atn::kFlashForm4x32
-                                                           : atn::kFlashForm8x16;
+    return s.BH * ((s.Lq + 255) / 256) >= (int64_t)cus ? atn::kFlashForm8x32
+                                                       : atn::kFlashForm8x16;
 }
 
 // Scratch bytes of the path a call of shape s takes: fused (when planned and

@@ -6,11 +6,11 @@
 // output in global memory.  Here a workgroup owns the query rows of its
 // waves, 16 or 32 per wave (v_mfma_f32_16x16x32_f16 or 32x32x16 tiles), of
 // one head and walks the head's keys in tiles of KT keys, with the running
-// output of its rows in registers.  Three forms: 8 waves of 16 rows (64-key
-// tiles at D <= 128 without an encoding), 4 waves of 32 rows (D <= 128,
-// 32-key tiles: each wave reads a K/V tile from LDS once per 32 rows
-// instead of 16, and two workgroups fit a CU), and 4 waves of 16 rows (a
-// tuning override).
+// output of its rows in registers.  Forms: 8 waves of 16 rows (64-key tiles
+// at D <= 128 without an encoding) and 8 waves of 32 rows (D <= 128, 32-key
+// tiles: each wave reads a K/V tile from LDS once per 32 rows instead of 16,
+// and each tile is converted once per 256 rows), the library's two; 4 waves
+// of 16 or of 32 rows as tuning overrides.
 //
 //   Per tile: K and V rows are loaded (16-byte loads) two tiles ahead, K
 //   encoded (RoPE, sinusoidal) once they land, and reduced to per-wave
@@ -535,6 +535,8 @@ hipError_t launch_form(int form, const float* Q, const float* K, const float* V,
             return launch_pe<PEK, 8, 16>(Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk, st);
         case kFlashForm4x32:
             return launch_pe<PEK, 4, 32>(Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk, st);
+        case kFlashForm8x32:
+            return launch_pe<PEK, 8, 32>(Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk, st);
         default: return hipErrorInvalidValue;
     }
 }

@@ -73,10 +73,10 @@ hipError_t launch_gemm_pv(const uint16_t* E, int ldE, float* st_m, float* st_l, 
 // kFlashMaxD (kFlashMaxDEncoded with a positional encoding) with head_d % 4
 // == 0, 16-byte aligned bases, and every head's Q or K/V under 2^31 bytes
 // (32-bit buffer offsets); no scratch.
-// `form`: the workgroup -- 4 waves of 16 query rows, 8 of 16, or 4 of 32
-// (head_d <= 128; past 128 every form runs 8 of 16).
+// `form`: the workgroup -- 4 waves of 16 query rows, 8 of 16, 4 of 32 or 8
+// of 32 (head_d <= 128; past 128 every form runs 8 of 16).
 constexpr int kFlashMaxD = 256, kFlashMaxDEncoded = 128;
-constexpr int kFlashForm4x16 = 1, kFlashForm8x16 = 2, kFlashForm4x32 = 3;
+constexpr int kFlashForm4x16 = 1, kFlashForm8x16 = 2, kFlashForm4x32 = 3, kFlashForm8x32 = 4;
 bool flash_supported(int dtype, int pek, int D);
 hipError_t launch_flash(int pek, int form, const float* Q, const float* K, const float* V,
                         float* O, int BH, int Lq, int Lk, int D, float scale, const PeSide& pq,

@@ -332,8 +332,9 @@ typedef struct atn_tuning {
                               it, so its workgroups take the fail-closed exit (no wait is
                               entered) */
     int flash_form;        /* flash kernel workgroup: 1 = 4 waves of 16 query rows,
-                              2 = 8 waves of 16, 3 = 4 waves of 32 (head_d <= 128;
-                              head_d > 128 always runs 2); 0: the library's choice */
+                              2 = 8 waves of 16, 3 = 4 waves of 32, 4 = 8 waves of 32
+                              (3 and 4: head_d <= 128; head_d > 128 always runs 2);
+                              0: the library's choice */
 } atn_tuning;
 /* Replaces the overrides (NULL: all zero) and drops cached plans.  Plans
  * that a forced setting makes impossible fall back to the library's

@@ -46,16 +46,16 @@ def test_flash_f32(am, dev, shape):
     assert n == 0, f"{n} mismatches, max abs {mabs}, max rel {mrel}"
 
 
-@pytest.mark.parametrize("form", ["4x16", "8x16", "4x32"])
+@pytest.mark.parametrize("form", ["4x16", "8x16", "4x32", "8x32"])
 @pytest.mark.parametrize("shape,pe", [((1, 3, 130, 129, 32), None), ((1, 2, 200, 300, 128), None),
                                       ((1, 2, 96, 200, 256), None), ((1, 2, 129, 97, 64), "rope"),
                                       ((1, 2, 150, 333, 128), "sinusoidal")],
                          ids=lambda v: "x".join(map(str, v)) if isinstance(v, tuple) else str(v))
 def test_flash_workgroup_forms(am, dev, tuner, form, shape, pe):
     """Every workgroup form forced on the same inputs: 4 waves of 16 query
-    rows, 8 of 16 and 4 of 32 (16 x 16 x 32 or 32 x 32 x 16 MFMA tiles;
-    64-, 128- and 128-row query blocks; key tiles of at least one load
-    round); head_d 256 runs 8 of 16 whatever is forced."""
+    rows, 8 of 16, 4 of 32 and 8 of 32 (16 x 16 x 32 or 32 x 32 x 16 MFMA
+    tiles; 64-, 128-, 128- and 256-row query blocks; key tiles of at least
+    one load round); head_d 256 runs 8 of 16 whatever is forced."""
     B, Hh, Lq, Lk, D = shape
     print(f"[case] flash f32 form {form} {shape} {pe}", flush=True)
     tuner.set(flash_form=form)
@@ -76,7 +76,7 @@ def test_flash_workgroup_forms(am, dev, tuner, form, shape, pe):
     assert n == 0, f"{n} mismatches, max abs {mabs}, max rel {mrel}"
 
 
-@pytest.mark.parametrize("form", ["4x16", "8x16", "4x32"])
+@pytest.mark.parametrize("form", ["4x16", "8x16", "4x32", "8x32"])
 @pytest.mark.parametrize("D", [32, 64, 128])
 def test_flash_tile_counts(am, dev, tuner, form, D):
     """Key lengths of 2 to 17 tiles, two seeds each, both workgroup forms.
