@@ -401,12 +401,14 @@ struct StreamPlan {
 StreamPlan stream_plan(const Shape& s) {
     StreamPlan p{};
     const int64_t tiles = s.BH * ((s.Lq + 63) / 64) * ((s.Lk + 63) / 64);
-    // D-chunks until about 1024 workgroups run (four per CU, so that one
-    // workgroup's slice loads overlap another's MFMAs), chunks of at least 64
-    // dims, rounded to the kernels' 32-deep slices
+    // D-chunks until about 1024 workgroups of 64 x 64 tiles run (four per CU,
+    // so that one workgroup's slice loads overlap another's MFMAs), or 512 of
+    // 128 x 128 where those can run (two per CU), chunks of at least 64 dims,
+    // rounded to the kernels' 32-deep slices
+    const int64_t target = atn::s16_fits_128(s.Lq, s.Lk) ? 2048 : 1024;  // in 64 x 64 tiles
     int nsplit = 1;
-    if (tiles < 1024) {
-        const int64_t want = (1024 + tiles - 1) / tiles;
+    if (tiles < target) {
+        const int64_t want = (target + tiles - 1) / tiles;
         const int64_t maxs = s.D / 64 > 1 ? s.D / 64 : 1;
         nsplit = (int)(want < maxs ? want : maxs);
     }
@@ -1263,6 +1265,7 @@ int atn_device_count(void) {
 
 int atn_set_tuning_ex(const atn_tuning* t) {
     std::unique_ptr<const atn_tuning> fresh(new atn_tuning(t ? *t : atn_tuning{}));
+    atn::s16_set_tile(fresh->splitd_tile);
     std::lock_guard<std::mutex> tl(g_tune_mu);
     const atn_tuning* old = g_tune.exchange(fresh.release(), std::memory_order_acq_rel);
     g_tune_old.emplace_back(old);

@@ -23,7 +23,20 @@ hipError_t launch_pv(int dtype, const float* P, const void* V, void* O, int BH, 
                      int D, int vec_ok, hipStream_t st);
 // Stages 1 and 3 for fp32 on 16-bit MFMA (stream16.hip; launch_qk_partial
 // and launch_pv choose them for fp32 with head_d % 4 == 0, 16-byte aligned
-// bases and per-head byte offsets under 2^31).
+// bases and per-head byte offsets under 2^31).  Output tiles of 128 x 128
+// where both of a tile's sides reach 128 and their grid gives every CU two
+// workgroups, else 64 x 64; s16_set_tile(64 or 128) forces a size wherever
+// it fits, s16_set_tile(0) restores the rule (a tuning override).
+void s16_set_tile(int tile);
+// Sides a x b (queries x keys for QK^T, queries x dims for PV) that 128 x
+// 128 tiles cover with at most 10 % more padding than 64 x 64 ones, both
+// sides reaching 128 (the host's D-chunk plan uses the same test).
+inline bool s16_fits_128(int a, int b) {
+    if (a < 128 || b < 128) return false;
+    const double p128 = (double)((a + 127) / 128 * 128) * ((b + 127) / 128 * 128);
+    const double p64 = (double)((a + 63) / 64 * 64) * ((b + 63) / 64 * 64);
+    return p128 <= 1.1 * p64;
+}
 hipError_t launch_qk_s16(int pek, const float* Q, const float* K, float* S, int BH, int Lq, int Lk,
                          int D, int dchunk, int nsplit, const PeSide& pq, const PeSide& pk,
                          hipStream_t st);

@@ -335,6 +335,10 @@ typedef struct atn_tuning {
                               2 = 8 waves of 16, 3 = 4 waves of 32, 4 = 8 waves of 32
                               (3 and 4: head_d <= 128; head_d > 128 always runs 2);
                               0: the library's choice */
+    int splitd_tile;       /* split-D pipeline, fp32 16-bit kernels: 64 or 128 forces
+                              that output tile (128 where both of its sides reach
+                              128); 0: 128 x 128 where that grid gives every CU two
+                              workgroups, else 64 x 64 */
 } atn_tuning;
 /* Replaces the overrides (NULL: all zero) and drops cached plans.  Plans
  * that a forced setting makes impossible fall back to the library's

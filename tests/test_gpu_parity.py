@@ -406,19 +406,59 @@ def test_sinusoidal_bf16(am, dev, shape):
     assert n == 0, f"normwise rel {nrel}, max abs {mabs}"
 
 
+@pytest.mark.parametrize("tile", [64, 128])
+@pytest.mark.parametrize("shape,pe", [((1, 2, 200, 300, 520), None), ((1, 3, 130, 129, 1024), None),
+                                      ((2, 2, 256, 256, 384), None), ((1, 2, 129, 257, 520), "rope"),
+                                      ((1, 2, 140, 200, 640), "sinusoidal")],
+                         ids=lambda v: "x".join(map(str, v)) if isinstance(v, tuple) else str(v))
+def test_split_d_tiles(am, dev, tuner, tile, shape, pe):
+    """The split-D pipeline's fp32 contractions with each output tile forced
+    (64 x 64, or 128 x 128 wherever both of a tile's sides reach 128):
+    ragged edges of either tile, D-chunks of whole and partial stages, and
+    the encodings applied at load."""
+    import hip_rt
+    B, Hh, Lq, Lk, D = shape
+    print(f"[case] split-D f32 tile {tile} {shape} {pe}", flush=True)
+    tuner.set(splitd_tile=tile)
+    desc = None if pe is None else am.make_pe(pe)
+    assert am.path(0, B, Hh, Lq, Lk, D, desc) == am.ATN_PATH_SPLIT_D
+    Q, K, V = H.rng_inputs((B, Hh, Lq, D), (B, Hh, Lk, D), seed=29 + D + tile,
+                           sigma=0.5 if pe == "sinusoidal" else 1.0)
+    (q, k, v) = (H.upload(x) for x in (Q, K, V))
+    out = H.empty(Q.shape)
+    am.attention_ex(q, k, v, out, pe=desc)
+    hip_rt.synchronize()
+    got = out.numpy()
+    L = max(Lq, Lk)
+    if pe == "sinusoidal":
+        st_, ct_ = oracle.sinusoidal_table(L, D)
+        ref = oracle.attention_sinusoidal(Q, K, V, st_, ct_, nthreads=16)
+    elif pe == "rope":
+        c_, s_ = oracle.rope_cache(L, D)
+        ref = oracle.attention_rope(Q, K, V, c_, s_, rotary_dim=D, nthreads=16)
+    else:
+        ref = oracle.attention(Q, K, V, nthreads=16)
+    n, mabs, _ = H.check_f32(got, ref)
+    assert n == 0, f"{n} mismatches, max abs {mabs}"
+
+
+@pytest.mark.parametrize("tile", [64, 128])
 @pytest.mark.parametrize("exps", [(17, -17, 0), (0, 0, 19), (17, -17, 21), (-12, -12, -12)],
                          ids=["qk-big", "v-big", "all-big", "all-small"])
-@pytest.mark.parametrize("shape", [(1, 3, 100, 130, 520), (1, 3, 70, 300, 1024)],
+@pytest.mark.parametrize("shape", [(1, 3, 100, 130, 520), (1, 3, 70, 300, 1024),
+                                   (1, 2, 200, 300, 520)],
                          ids=lambda s: "x".join(map(str, s)))
-def test_split_d_outside_fp16_range(am, dev, shape, exps):
+def test_split_d_outside_fp16_range(am, dev, tuner, shape, exps, tile):
     """fp32 beyond the single-launch window with head_d > 256 runs the
     split-D pipeline, whose contractions use the fp16 split too: a stage
     with a value outside fp16's range is staged again with power-of-two
-    scales.  Head 1 is scaled by 2^eq, 2^ek, 2^ev (exact); its output is
-    compared in units of 2^ev with the oracle on the unscaled V."""
+    scales (in both output tile sizes).  Head 1 is scaled by 2^eq, 2^ek,
+    2^ev (exact); its output is compared in units of 2^ev with the oracle on
+    the unscaled V."""
     B, Hh, Lq, Lk, D = shape
     eq, ek, ev = exps
-    print(f"[case] split-D f32 scaled 2^{exps} {shape}", flush=True)
+    print(f"[case] split-D f32 tile {tile} scaled 2^{exps} {shape}", flush=True)
+    tuner.set(splitd_tile=tile)
     assert am.path(0, B, Hh, Lq, Lk, D) == am.ATN_PATH_SPLIT_D
     Q, K, V = H.rng_inputs((B, Hh, Lq, D), (B, Hh, Lk, D), seed=37 + D)
     Q[:, 1] *= np.float32(2.0 ** eq)
