@@ -28,14 +28,15 @@
 //   its scores and its output row (4 lanes with 16-row tiles, 2 with
 //   32-row ones), and reductions over a tile's keys are 16 values in
 //   registers plus one or two row swaps (v_permlane16/32_swap).
-//   P = 2^(x - m + 15) (base 2, its 2^15 via the exponent) stays in
+//   P = 2^(x - m + 8) (base 2, its 2^8 via the exponent; the running max m
+//   moves only when a tile's max exceeds it by more than 7) stays in
 //   registers, where the accumulator layout of S^T is already the B operand
 //   of O^T += V^T P^T (the keys of each 32- or 16-key block in the order
 //   4g + 0..3, then 16 + 4g + 0..3 or 8 + 4g + 0..3, for lane group g; V's
 //   transposing LDS read, ds_read_b64_tr_b16, takes the same order), and O^T
-//   (dims x queries per MFMA tile) accumulates in registers, rescaled per
-//   tile by 2^(m_old - m_new) and by the ratio of consecutive V tiles'
-//   scales.
+//   (dims x queries per MFMA tile) accumulates in registers, rescaled by
+//   2^(m_old - m_new) when m moves and by the ratio of consecutive V tiles'
+//   scales when they differ.
 //
 // The score matrix never reaches memory: per call the kernel reads Q once
 // and K and V once per query block, and writes O once.
@@ -328,9 +329,9 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_flash_f32(const float* __re
 
     // running statistics of this lane's query and its output rows (O^T
     // tiles: register r of tile t holds dim MT t + 8 (r / 4) + 4 lg + r % 4
-    // of query lr): the max in base-2 units of the scores, the sum in units
-    // of 2^15, the output in units of uv / 2^15 for the current V tile's
-    // unit uv = 1 / sv
+    // of query lr): the running max m_run in base-2 units of the scores, the
+    // sum in units of 2^(m_run - 8), the output in units of uv 2^(m_run - 8)
+    // for the current V tile's unit uv = 1 / sv
     float m_run = -INFINITY, l_run = 0.f, uv_prev = 1.f;
     acc_t o[G::NDT];
 #pragma unroll
@@ -403,12 +404,20 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_flash_f32(const float* __re
                     mt = fmaxf(mt, s[j][r]);
                 }
         }
-        const float m_new = fmaxf(m_run, xgroup_max<RW>(mt) * c2);  // c2 > 0
-        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // 0 on the first tile
+        // The running max moves only on the first tile and when a tile's max
+        // exceeds it by more than 7 (a factor 2^7): P = 2^(x - m + 8) then
+        // stays at most 2^15 (its fp16 hi part in range), and most tiles
+        // leave the output's scale alone.  (A NaN max moves it, so that NaN
+        // propagates.)
+        const float mt2 = xgroup_max<RW>(mt) * c2;  // c2 > 0
+        const bool move = !(m_run >= mt2 - 7.f);
+        const float m_new = move ? mt2 : m_run;
+        const float alpha = move ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.f;  // 0 on the first tile
         m_run = m_new;
-        // P = 2^(x - m_new + 15): one FMA and one v_exp_f32 per score, the
-        // 2^15 that keeps P's lo parts normal in fp16 folded into the exponent
-        const float nm = 15.f - m_new;
+        // P = 2^(x - m_run + 8): one FMA and one v_exp_f32 per score, the 2^8
+        // that keeps P's lo parts from fp16's subnormal range folded into the
+        // exponent
+        const float nm = 8.f - m_new;
         float ps = 0.f;
         // P as the B operand of block b: the lane's scores 8 b .. 8 b + 7 in
         // the order of s (RW = 16: elements 0..3 from tile 2b, 4..7 from
@@ -435,6 +444,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_flash_f32(const float* __re
         const float f = alpha * (uv_prev * sv_t);  // the old output in the new tile's units
         uv_prev = uv_t;
         if (__builtin_amdgcn_ballot_w64(f != 1.f)) {  // skipped while no row's max moves
+                                                      // (and V's scale stays)
 #pragma unroll
             for (int dt = 0; dt < G::NDT; ++dt) o[dt] *= f;
         }
@@ -468,7 +478,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_flash_f32(const float* __re
         __syncthreads();
     }
 
-    // ---- O = O^T uv / l (O^T and l both in units of 2^15): 16-byte stores
+    // ---- O = O^T uv / l (the sums' common unit cancels): 16-byte stores
     // of 4 consecutive dims
     const float l = xgroup_sum<RW>(l_run);
     const float inv = uv_prev / l;

@@ -158,6 +158,28 @@ def test_flash_outside_fp16_range(am, dev, exps):
     assert n == 0, f"{n} mismatches, max abs {mabs}, max rel {mrel}"
 
 
+def test_flash_nonfinite_inputs_propagate(am, dev, tuner):
+    """As in the reference: an infinite query element makes its own output
+    row non-finite, a NaN value element its output column NaN; every other
+    element keeps the bar (the tile scales take finite magnitudes only)."""
+    for form in ("8x16", "8x32"):
+        B, Hh, Lq, Lk, D = 1, 2, 300, 333, 128
+        print(f"[case] flash f32 non-finite inputs, form {form}", flush=True)
+        tuner.set(flash_form=form)
+        Q, K, V = H.rng_inputs((B, Hh, Lq, D), (B, Hh, Lk, D), seed=71)
+        Q[0, 1, 5, 100] = np.inf
+        V[0, 0, 200, 33] = np.nan
+        got = _f32_call(am, Q, K, V)
+        ref = oracle.attention(Q, K, V, nthreads=16)
+        assert not np.isfinite(ref[0, 1, 5]).any() and not np.isfinite(got[0, 1, 5]).any()
+        assert np.isnan(ref[0, 0, :, 33]).all() and np.isnan(got[0, 0, :, 33]).all()
+        keep = np.ones((Hh, Lq, D), dtype=bool)
+        keep[1, 5, :] = False
+        keep[0, :, 33] = False
+        n, mabs, _ = H.check_f32(got[0][keep], ref[0][keep])
+        assert n == 0, mabs
+
+
 def test_flash_v_scale_changes_between_tiles(am, dev):
     """One key tile of V beyond fp16's range among ordinary ones: its scale
     differs from its neighbours', and the running output is carried across
