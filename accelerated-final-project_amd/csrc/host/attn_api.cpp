@@ -742,13 +742,20 @@ size_t library_cap() {
     return mib > 0 ? (size_t)mib << 20 : (size_t)1 << 30;
 }
 
-// The flash kernel takes fp32 calls with head_d <= 256 (128 with an
-// encoding), head_d % 4 == 0 and 16-byte aligned bases (checked by the
-// caller), whose per-head Q and K/V byte offsets fit 32 bits.
+// The flash kernel takes fp32 and bf16 calls with head_d <= 256 (128 with
+// an encoding), head_d % 4 == 0 and 16-byte aligned bases (checked by the
+// caller), whose per-head Q and K/V byte offsets fit 32 bits.  bf16 calls
+// past head_d 128 take the GEMM path where it runs: its 256 x 256 tiles
+// reuse each operand over more products than the flash kernel's 64-key
+// tiles (measured: (4,32,512,512,256) 62 us there, 78 us here; at head_d
+// 128 the flash kernel leads, (4,32,512,512,128) 36 us against 56 us).
 bool flash_ok(int dtype, const Shape& s, const PePlan& plan) {
     const int64_t lim = (int64_t)1 << 31;
-    return !plan.no_flash && atn::flash_supported(dtype, plan.pek, s.D) &&
-           (int64_t)s.Lq * s.D * 4 < lim && (int64_t)s.Lk * s.D * 4 < lim;
+    const int64_t es = dtype == ATN_DTYPE_F32 ? 4 : 2;
+    if (plan.no_flash || !atn::flash_supported(dtype, plan.pek, s.D) ||
+        (int64_t)s.Lq * s.D * es >= lim || (int64_t)s.Lk * s.D * es >= lim)
+        return false;
+    return dtype == ATN_DTYPE_F32 || s.D <= 128 || !gemm_plan(dtype, s, plan).ok;
 }
 
 // The flash kernel's workgroup form (atn_tuning.flash_form forces one).
@@ -946,10 +953,8 @@ int attention_run(int dtype, const void* Q, const void* K, const void* V, void* 
         return ATN_OK;
     }
     if (use_flash) {
-        ATN_HIP(atn::launch_flash(plan.pek, flash_form(s, dev), static_cast<const float*>(Q),
-                                  static_cast<const float*>(K), static_cast<const float*>(V),
-                                  static_cast<float*>(out), (int)s.BH, Lq, Lk, D, scale, plan.q,
-                                  plan.k, stream));
+        ATN_HIP(atn::launch_flash(dtype, plan.pek, flash_form(s, dev), Q, K, V, out, (int)s.BH,
+                                  Lq, Lk, D, scale, plan.q, plan.k, stream));
         return ATN_OK;
     }
     float* S = scratch;

@@ -58,11 +58,11 @@ namespace {
 // 128 without a positional encoding (PE), else 32 (two LDS buffers of it
 // then leave room for two 4-wave workgroups per CU), and at least one load
 // round of the workgroup.
-template <int DP, bool PE, int NW, int RW>
+template <int DP, bool PE, int NW, int RW, bool HL = true>
 struct FlashGeo {
     static_assert(RW == 16 || (RW == 32 && DP <= 128), "forms");
     static constexpr int THREADS = 64 * NW, ROWS = RW * NW;
-    static constexpr int KT0 = DP <= 128 && !PE && NW == 8 && RW == 16 ? 64 : 32;
+    static constexpr int KT0 = !HL || (DP <= 128 && !PE && NW == 8 && RW == 16) ? 64 : 32;
     static constexpr int KT = KT0 > THREADS / (DP / 4) ? KT0 : THREADS / (DP / 4);
     static constexpr int MT = RW;                   // MFMA tile edge
     static constexpr int KD = RW == 16 ? 32 : 16;   // MFMA depth: dims of Q K^T, keys of P V
@@ -76,11 +76,13 @@ struct FlashGeo {
     static constexpr int NLD = KT / RSTEP;          // load rounds per tile
     // LDS rows in 16-bit elements: K padded by 8 (16-byte fragment reads),
     // V by 16 (the transposing read's 4 rows x 32 bytes in distinct banks);
-    // two buffers of TILE elements
+    // two buffers of TILE elements, holding hi and lo parts (HL) or hi parts
+    // only (bf16 inputs, exact in fp16)
     static constexpr int KSTR = DP + 8, VSTR = DP + 16;
-    static constexpr int K_HI = 0, K_LO = KT * KSTR, V_HI = 2 * KT * KSTR,
+    static constexpr int NP = HL ? 2 : 1;  // parts per operand
+    static constexpr int K_HI = 0, K_LO = KT * KSTR, V_HI = NP * KT * KSTR,
                          V_LO = V_HI + KT * VSTR;
-    static constexpr int TILE = 2 * KT * KSTR + 2 * KT * VSTR;
+    static constexpr int TILE = NP * (KT * KSTR + KT * VSTR);
     static constexpr int BYTES = 2 * 2 * TILE;
     static_assert(KT % RSTEP == 0 && KT % MT == 0 && KT % KD == 0, "whole tiles");
     static_assert(BYTES <= 160 * 1024, "LDS");
@@ -134,6 +136,25 @@ __device__ __forceinline__ float wave_max_rows(float v) {
     return xgroup_max<16>(v);
 }
 
+// 4 consecutive elements at byte offset `off` of a raw buffer as fp32
+// (zeros past its end): fp32 16 bytes, bf16 8 bytes
+template <typename T>
+__device__ __forceinline__ float4 ld4_t(__amdgpu_buffer_rsrc_t r, int off) {
+    if constexpr (sizeof(T) == 4) {
+        return ld_buf_f4(r, off);
+    } else {
+        const auto w = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+        return make_float4(__uint_as_float(w[0] << 16), __uint_as_float(w[0] & 0xffff0000u),
+                           __uint_as_float(w[1] << 16), __uint_as_float(w[1] & 0xffff0000u));
+    }
+}
+
+// two values as fp16, rounded to nearest even, packed
+__device__ __forceinline__ uint32_t pk_f16_rne(float a, float b) {
+    const f16x2 h = {(_Float16)a, (_Float16)b};
+    return __builtin_bit_cast(uint32_t, h);
+}
+
 // the form's MFMA: 16 x 16 x 32 or 32 x 32 x 16, fp16 operands, fp32 sums
 __device__ __forceinline__ v4f mfma_rw(const f16x8& a, const f16x8& b, const v4f& c) {
     return mfma_f16(a, b, c);
@@ -142,15 +163,20 @@ __device__ __forceinline__ v16f mfma_rw(const f16x8& a, const f16x8& b, const v1
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
-template <int DP, int PEK, int NW, int RW>
-__global__ __launch_bounds__(64 * NW, 8 / NW) void k_flash_f32(const float* __restrict__ Qg,
-                                                                 const float* __restrict__ Kg,
-                                                                 const float* __restrict__ Vg,
-                                                                 float* __restrict__ Og, int Lq,
-                                                                 int Lk, int D, int qblocks,
-                                                                 float scale, PeSide pq,
-                                                                 PeSide pk) {
-    using G = FlashGeo<DP, PEK != kPeNone, NW, RW>;
+// T = float: fp32 inputs as hi + lo fp16 parts, three products each; T =
+// uint16_t: bf16 inputs (bf16 bits), exact in fp16 within its range (a
+// power-of-two scale per tile brings K and V there), one product each, P as
+// one fp16 part, the output rounded to bf16.
+template <typename T, int DP, int PEK, int NW, int RW>
+__global__ __launch_bounds__(64 * NW, 8 / NW) void k_flash(const T* __restrict__ Qg,
+                                                             const T* __restrict__ Kg,
+                                                             const T* __restrict__ Vg,
+                                                             T* __restrict__ Og, int Lq, int Lk,
+                                                             int D, int qblocks, float scale,
+                                                             PeSide pq, PeSide pk) {
+    constexpr bool kBf = sizeof(T) == 2;
+    constexpr int es = (int)sizeof(T);
+    using G = FlashGeo<DP, PEK != kPeNone, NW, RW, !kBf>;
     typedef std::conditional_t<RW == 16, v4f, v16f> acc_t;
     extern __shared__ __align__(16) unsigned char smem_raw[];
     uint16_t* smem = reinterpret_cast<uint16_t*>(smem_raw);
@@ -170,9 +196,9 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_flash_f32(const float* __re
     if ((nwg & 7) == 0) id = (id & 7) * (nwg >> 3) + (id >> 3);
     const int bh = id / qblocks, qb = id - bh * qblocks;
     const int q0 = qb * G::ROWS;
-    const float* Qh = Qg + (size_t)bh * Lq * D;
-    const float* Kh = Kg + (size_t)bh * Lk * D;
-    const float* Vh = Vg + (size_t)bh * Lk * D;
+    const T* Qh = Qg + (size_t)bh * Lq * D;
+    const T* Kh = Kg + (size_t)bh * Lk * D;
+    const T* Vh = Vg + (size_t)bh * Lk * D;
     constexpr int kOob = kBufOob;
 
     // ---- Q: this wave's RW rows as the B operand of S^T = K Q^T: lane
@@ -184,19 +210,18 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_flash_f32(const float* __re
     {
         float4 qv[G::KS][2];
         float mq = 0.f;
-        const __amdgpu_buffer_rsrc_t rq = buf_rsrc(Qh, Lq * D * 4);
+        const __amdgpu_buffer_rsrc_t rq = buf_rsrc(Qh, Lq * D * es);
 #pragma unroll
         for (int ks = 0; ks < G::KS; ++ks)
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
                 const int d = G::KD * ks + 8 * lg + 4 * h;
                 if constexpr (PEK == kPeNone) {
-                    qv[ks][h] = ld_buf_f4(rq, d < D ? (qrow * D + d) * 4 : kOob);
+                    qv[ks][h] = ld4_t<T>(rq, d < D ? (qrow * D + d) * es : kOob);
                 } else {
                     qv[ks][h] = make_float4(0.f, 0.f, 0.f, 0.f);
                     if (qrow < Lq && d < D)
-                        qv[ks][h] = load_row4_pe<float, PEK>(Qh + (size_t)qrow * D, qrow, d, D, pq,
-                                                             true);
+                        qv[ks][h] = load_row4_pe<T, PEK>(Qh + (size_t)qrow * D, qrow, d, D, pq, true);
                 }
                 mq = max_finite4(mq, qv[ks][h]);
             }
@@ -206,6 +231,15 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_flash_f32(const float* __re
 #pragma unroll
         for (int ks = 0; ks < G::KS; ++ks) {
             uint32_t h[4], l[4];
+            if constexpr (kBf) {
+                h[0] = pk_f16_rne(qv[ks][0].x * sq, qv[ks][0].y * sq);
+                h[1] = pk_f16_rne(qv[ks][0].z * sq, qv[ks][0].w * sq);
+                h[2] = pk_f16_rne(qv[ks][1].x * sq, qv[ks][1].y * sq);
+                h[3] = pk_f16_rne(qv[ks][1].z * sq, qv[ks][1].w * sq);
+                qh[ks] = __builtin_bit_cast(f16x8, make_uint4(h[0], h[1], h[2], h[3]));
+                ql[ks] = qh[ks];  // (unused)
+                continue;
+            }
             split2_f16(qv[ks][0].x * sq, qv[ks][0].y * sq, h[0], l[0]);
             split2_f16(qv[ks][0].z * sq, qv[ks][0].w * sq, h[1], l[1]);
             split2_f16(qv[ks][1].x * sq, qv[ks][1].y * sq, h[2], l[2]);
@@ -225,16 +259,16 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_flash_f32(const float* __re
     // buffer u & 1; iteration u computes it.  Staging, loads and maxima thus
     // run beside another tile's products, and LDS holds two tiles.
     const int lrow = tid / G::VPR, lcol = (tid % G::VPR) * 4;
-    const __amdgpu_buffer_rsrc_t rk = buf_rsrc(Kh, Lk * D * 4);
-    const __amdgpu_buffer_rsrc_t rv = buf_rsrc(Vh, Lk * D * 4);
+    const __amdgpu_buffer_rsrc_t rk = buf_rsrc(Kh, Lk * D * es);
+    const __amdgpu_buffer_rsrc_t rv = buf_rsrc(Vh, Lk * D * es);
     float4 kr[G::NLD], vr[G::NLD];
     auto issue = [&](int k0) {
 #pragma unroll
         for (int i = 0; i < G::NLD; ++i) {
             const int key = k0 + lrow + G::RSTEP * i;
-            const int off = key < Lk && lcol < D ? (key * D + lcol) * 4 : kOob;
-            kr[i] = ld_buf_f4(rk, off);
-            vr[i] = ld_buf_f4(rv, off);
+            const int off = key < Lk && lcol < D ? (key * D + lcol) * es : kOob;
+            kr[i] = ld4_t<T>(rk, off);
+            vr[i] = ld4_t<T>(rv, off);
         }
     };
     // K's encoding, then the per-wave maxima of the tile's K and V
@@ -248,7 +282,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_flash_f32(const float* __re
             for (int i = 0; i < G::NLD; ++i) {
                 const int key = k0 + lrow + G::RSTEP * i;
                 if (key < Lk && lcol < D)
-                    kr[i] = apply_pe4<float, PEK>(kr[i], Kh + (size_t)key * D, key, lcol, D, pk);
+                    kr[i] = apply_pe4<T, PEK>(kr[i], Kh + (size_t)key * D, key, lcol, D, pk);
             }
         }
         float mk = 0.f, mv = 0.f;
@@ -279,9 +313,10 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_flash_f32(const float* __re
     };
     // scales of the tile whose maxima are in slot[par] (K as it is where its
     // largest magnitude lies in [2^-3, 65504): the split then keeps 2^-22 of
-    // that magnitude; else a power of two brings it to [2^14, 2^15); V
-    // scaled only beyond fp16's range), and its hi + lo fp16 parts into LDS
-    // buffer par
+    // that magnitude; else a power of two brings it to [2^14, 2^15); V the
+    // same for bf16, whose one fp16 part must stay out of the subnormal
+    // range, and for fp32 scaled only beyond fp16's range), and its hi + lo
+    // (fp32) or hi (bf16) fp16 parts into LDS buffer par
     auto stage = [&](int par, float& uk, float& sv, float& uv) {
         float mk = slot[par][0], mv = slot[par][NW];
 #pragma unroll
@@ -292,14 +327,26 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_flash_f32(const float* __re
         const bool k_plain = mk >= 0.125f && mk < kF16Range;
         const float sk = k_plain ? 1.f : pow2_scale(mk);
         uk = k_plain ? 1.f : pow2_unit(mk);
-        sv = range_scale(mv);
-        uv = range_unit(mv);
+        const bool v_plain = kBf ? mv >= 0.125f && mv < kF16Range : mv < kF16Range;
+        sv = v_plain ? 1.f : pow2_scale(mv);
+        uv = v_plain ? 1.f : pow2_unit(mv);
         uint16_t* buf = smem + par * G::TILE;
         auto put = [&](auto plain) {
 #pragma unroll
             for (int i = 0; i < G::NLD; ++i) {
                 const int row = lrow + G::RSTEP * i;
                 uint32_t h0, l0, h1, l1, h2, l2, h3, l3;
+                if constexpr (kBf) {
+                    const float fk = decltype(plain)::value ? 1.f : sk;
+                    const float fv = decltype(plain)::value ? 1.f : sv;
+                    *reinterpret_cast<uint2*>(buf + G::K_HI + row * G::KSTR + lcol) =
+                        make_uint2(pk_f16_rne(kr[i].x * fk, kr[i].y * fk),
+                                   pk_f16_rne(kr[i].z * fk, kr[i].w * fk));
+                    *reinterpret_cast<uint2*>(buf + G::V_HI + row * G::VSTR + lcol) =
+                        make_uint2(pk_f16_rne(vr[i].x * fv, vr[i].y * fv),
+                                   pk_f16_rne(vr[i].z * fv, vr[i].w * fv));
+                    continue;
+                }
                 if constexpr (decltype(plain)::value) {
                     split2_f16_one(kr[i].x, kr[i].y, one, h0, l0);
                     split2_f16_one(kr[i].z, kr[i].w, one, h1, l1);
@@ -321,7 +368,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_flash_f32(const float* __re
                     make_uint2(l2, l3);
             }
         };
-        if (k_plain && sv == 1.f)
+        if (k_plain && v_plain)
             put(std::true_type{});
         else
             put(std::false_type{});
@@ -329,9 +376,14 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_flash_f32(const float* __re
 
     // running statistics of this lane's query and its output rows (O^T
     // tiles: register r of tile t holds dim MT t + 8 (r / 4) + 4 lg + r % 4
-    // of query lr): the running max m_run in base-2 units of the scores, the
-    // sum in units of 2^(m_run - 8), the output in units of uv 2^(m_run - 8)
-    // for the current V tile's unit uv = 1 / sv
+    // of query lr): the running max m_run of the scores in units of uq (the
+    // accumulators times their tile's K unit uk: powers of two, so maxima of
+    // different tiles compare exactly), the sum in units of 2^(c0 m_run -
+    // 8), the output in units of uv 2^(c0 m_run - 8) for the current V
+    // tile's unit uv = 1 / sv; c0 turns them into base-2 exponents, and a
+    // tile's accumulators take c2 = c0 uk
+    const float c0 = scale * 1.44269504088896341f * uq;
+    const float thr = 7.f / c0;
     float m_run = -INFINITY, l_run = 0.f, uv_prev = 1.f;
     acc_t o[G::NDT];
 #pragma unroll
@@ -372,22 +424,24 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_flash_f32(const float* __re
             for (int j = 0; j < G::NJ; ++j) {
                 const int a = (G::MT * j + lr) * G::KSTR + G::KD * ks + 8 * lg;
                 ah[j] = lds8_f16(buf + G::K_HI + a);
-                al[j] = lds8_f16(buf + G::K_LO + a);
+                if constexpr (!kBf) al[j] = lds8_f16(buf + G::K_LO + a);
             }
 #pragma unroll
             for (int j = 0; j < G::NJ; ++j) s[j] = mfma_rw(ah[j], qh[ks], s[j]);
+            if constexpr (!kBf) {
 #pragma unroll
-            for (int j = 0; j < G::NJ; ++j) s[j] = mfma_rw(ah[j], ql[ks], s[j]);
+                for (int j = 0; j < G::NJ; ++j) s[j] = mfma_rw(ah[j], ql[ks], s[j]);
 #pragma unroll
-            for (int j = 0; j < G::NJ; ++j) s[j] = mfma_rw(al[j], qh[ks], s[j]);
-            __builtin_amdgcn_sched_group_barrier(0x100, 2 * G::NJ, 0);  // DS reads
-            __builtin_amdgcn_sched_group_barrier(0x008, 3 * G::NJ, 0);  // MFMA
+                for (int j = 0; j < G::NJ; ++j) s[j] = mfma_rw(al[j], qh[ks], s[j]);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x100, G::NP * G::NJ, 0);  // DS reads
+            __builtin_amdgcn_sched_group_barrier(0x008, (2 * G::NP - 1) * G::NJ, 0);  // MFMA
         }
 
         // ---- online softmax over the tile in base 2: x = S c2 with c2 =
-        // scale log2(e) / (sq sk), the running max m_run in the same units
-        // (keys past Lk score -inf, on the last tile only)
-        const float c2 = scale * 1.44269504088896341f * uq * uk_t;
+        // scale log2(e) / (sq sk) (keys past Lk score -inf, on the last tile
+        // only)
+        const float c2 = c0 * uk_t;
         float mt = -INFINITY;
         if (k0 + G::KT <= Lk) {
 #pragma unroll
@@ -405,19 +459,33 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_flash_f32(const float* __re
                 }
         }
         // The running max moves only on the first tile and when a tile's max
-        // exceeds it by more than 7 (a factor 2^7): P = 2^(x - m + 8) then
-        // stays at most 2^15 (its fp16 hi part in range), and most tiles
-        // leave the output's scale alone.  (A NaN max moves it, so that NaN
-        // propagates.)
-        const float mt2 = xgroup_max<RW>(mt) * c2;  // c2 > 0
-        const bool move = !(m_run >= mt2 - 7.f);
-        const float m_new = move ? mt2 : m_run;
-        const float alpha = move ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.f;  // 0 on the first tile
+        // exceeds it by more than 7 in base 2 (a factor 2^7): P = 2^(x - m +
+        // 8) then stays at most 2^15 (its fp16 hi part in range), and most
+        // tiles leave the output's scale alone.  (A NaN max moves it, so that
+        // NaN propagates.)
+        const float mtu = xgroup_max<RW>(mt) * uk_t;
+        const bool move = !(m_run >= mtu - thr);
+        const float m_new = move ? mtu : m_run;
+        const float alpha = move ? __builtin_amdgcn_exp2f((m_run - m_new) * c0) : 1.f;  // 0 on the first tile
         m_run = m_new;
-        // P = 2^(x - m_run + 8): one FMA and one v_exp_f32 per score, the 2^8
-        // that keeps P's lo parts from fp16's subnormal range folded into the
-        // exponent
-        const float nm = 8.f - m_new;
+        // P = 2^(x - c0 m_run + 8), the 2^8 that keeps P's lo parts from
+        // fp16's subnormal range folded into the exponent: one FMA and one
+        // v_exp_f32 per score, with c0 m_run rounded once per tile.  Where
+        // |c0 m_run| reaches 2^8 that rounding would reach 2^-16 of the
+        // exponent (and far more for huge logits, where it would turn the
+        // weights of the largest scores into garbage): such waves first
+        // rewrite each score as its difference from the max (one FMA, exact
+        // near the max), as a plain softmax subtracts the max.
+        const float mc = m_new * c0;
+        float cx = c2, nm = 8.f - mc;
+        if (__builtin_amdgcn_ballot_w64(!(__builtin_fabsf(mc) < 256.f))) {
+#pragma unroll
+            for (int j = 0; j < G::NJ; ++j)
+#pragma unroll
+                for (int r = 0; r < G::SPT; ++r) s[j][r] = fmaf(s[j][r], uk_t, -m_new);
+            cx = c0;
+            nm = 8.f;
+        }
         float ps = 0.f;
         // P as the B operand of block b: the lane's scores 8 b .. 8 b + 7 in
         // the order of s (RW = 16: elements 0..3 from tile 2b, 4..7 from
@@ -431,11 +499,14 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_flash_f32(const float* __re
 #pragma unroll
             for (int e = 0; e < 8; e += 2) {
                 const int i0 = 8 * b + e, i1 = i0 + 1;
-                const float p0 = __builtin_amdgcn_exp2f(fmaf(s[i0 / G::SPT][i0 % G::SPT], c2, nm));
-                const float p1 = __builtin_amdgcn_exp2f(fmaf(s[i1 / G::SPT][i1 % G::SPT], c2, nm));
+                const float p0 = __builtin_amdgcn_exp2f(fmaf(s[i0 / G::SPT][i0 % G::SPT], cx, nm));
+                const float p1 = __builtin_amdgcn_exp2f(fmaf(s[i1 / G::SPT][i1 % G::SPT], cx, nm));
                 ps += p0;
                 ps += p1;
-                split2_f16_one(p0, p1, one, h[e / 2], l[e / 2]);
+                if constexpr (kBf)
+                    h[e / 2] = l[e / 2] = pk_f16_rne(p0, p1);  // one part (lo unused)
+                else
+                    split2_f16_one(p0, p1, one, h[e / 2], l[e / 2]);
             }
             ph[b] = __builtin_bit_cast(f16x8, make_uint4(h[0], h[1], h[2], h[3]));
             pl[b] = __builtin_bit_cast(f16x8, make_uint4(l[0], l[1], l[2], l[3]));
@@ -464,13 +535,16 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_flash_f32(const float* __re
                 constexpr int half = G::KD / 2 * G::VSTR;
                 const uint2 h0 = lds_tr16(buf + G::V_HI + a);
                 const uint2 h1 = lds_tr16(buf + G::V_HI + a + half);
-                const uint2 l0 = lds_tr16(buf + G::V_LO + a);
-                const uint2 l1 = lds_tr16(buf + G::V_LO + a + half);
                 const f16x8 vh = __builtin_bit_cast(f16x8, make_uint4(h0.x, h0.y, h1.x, h1.y));
-                const f16x8 vl = __builtin_bit_cast(f16x8, make_uint4(l0.x, l0.y, l1.x, l1.y));
                 o[dt] = mfma_rw(vh, ph[b], o[dt]);
-                o[dt] = mfma_rw(vh, pl[b], o[dt]);
-                o[dt] = mfma_rw(vl, ph[b], o[dt]);
+                if constexpr (!kBf) {
+                    const uint2 l0 = lds_tr16(buf + G::V_LO + a);
+                    const uint2 l1 = lds_tr16(buf + G::V_LO + a + half);
+                    const f16x8 vl =
+                        __builtin_bit_cast(f16x8, make_uint4(l0.x, l0.y, l1.x, l1.y));
+                    o[dt] = mfma_rw(vh, pl[b], o[dt]);
+                    o[dt] = mfma_rw(vl, ph[b], o[dt]);
+                }
             }
         }
 
@@ -478,39 +552,38 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_flash_f32(const float* __re
         __syncthreads();
     }
 
-    // ---- O = O^T uv / l (the sums' common unit cancels): 16-byte stores
-    // of 4 consecutive dims
+    // ---- O = O^T uv / l (the sums' common unit cancels): stores of 4
+    // consecutive dims (16 bytes fp32, 8 bytes bf16 rounded to nearest even)
     const float l = xgroup_sum<RW>(l_run);
     const float inv = uv_prev / l;
     if (qrow < Lq) {
-        float* orow = Og + ((size_t)bh * Lq + qrow) * D;
+        T* orow = Og + ((size_t)bh * Lq + qrow) * D;
 #pragma unroll
         for (int dt = 0; dt < G::NDT; ++dt)
 #pragma unroll
             for (int r = 0; r < G::SPT; r += 4) {
                 const int d = G::MT * dt + 8 * (r >> 2) + 4 * lg;
                 if (d < D)
-                    *reinterpret_cast<float4*>(orow + d) =
-                        make_float4(o[dt][r] * inv, o[dt][r + 1] * inv, o[dt][r + 2] * inv,
-                                    o[dt][r + 3] * inv);
+                    Elem<T>::st4(orow, d,
+                                 make_float4(o[dt][r] * inv, o[dt][r + 1] * inv,
+                                             o[dt][r + 2] * inv, o[dt][r + 3] * inv));
             }
     }
 }
 
-template <int DP, int PEK, int NW, int RW>
-hipError_t launch_t(const float* Q, const float* K, const float* V, float* O, int BH, int Lq,
-                    int Lk, int D, float scale, const PeSide& pq, const PeSide& pk,
-                    hipStream_t st) {
-    using G = FlashGeo<DP, PEK != kPeNone, NW, RW>;
+template <typename T, int DP, int PEK, int NW, int RW>
+hipError_t launch_t(const T* Q, const T* K, const T* V, T* O, int BH, int Lq, int Lk, int D,
+                    float scale, const PeSide& pq, const PeSide& pk, hipStream_t st) {
+    using G = FlashGeo<DP, PEK != kPeNone, NW, RW, sizeof(T) == 4>;
     static bool attr = false;
     if (!attr) {
-        hipError_t e = hipFuncSetAttribute((const void*)k_flash_f32<DP, PEK, NW, RW>,
+        hipError_t e = hipFuncSetAttribute((const void*)k_flash<T, DP, PEK, NW, RW>,
                                            hipFuncAttributeMaxDynamicSharedMemorySize, G::BYTES);
         if (e != hipSuccess) return e;
         attr = true;
     }
     const int qblocks = (Lq + G::ROWS - 1) / G::ROWS;
-    hipLaunchKernelGGL((k_flash_f32<DP, PEK, NW, RW>), dim3((unsigned)(BH * qblocks)),
+    hipLaunchKernelGGL((k_flash<T, DP, PEK, NW, RW>), dim3((unsigned)(BH * qblocks)),
                        dim3(G::THREADS), G::BYTES, st, Q, K, V, O, Lq, Lk, D, qblocks, scale, pq,
                        pk);
     return hipGetLastError();
@@ -518,35 +591,57 @@ hipError_t launch_t(const float* Q, const float* K, const float* V, float* O, in
 
 // head dims padded to 32, 64, 128 (and 256 for 8 waves of 16 rows without
 // an encoding)
-template <int PEK, int NW, int RW>
-hipError_t launch_pe(const float* Q, const float* K, const float* V, float* O, int BH, int Lq,
-                     int Lk, int D, float scale, const PeSide& pq, const PeSide& pk,
-                     hipStream_t st) {
-    if (D <= 32) return launch_t<32, PEK, NW, RW>(Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk, st);
-    if (D <= 64) return launch_t<64, PEK, NW, RW>(Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk, st);
-    if (D <= 128) return launch_t<128, PEK, NW, RW>(Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk, st);
+template <typename T, int PEK, int NW, int RW>
+hipError_t launch_pe(const T* Q, const T* K, const T* V, T* O, int BH, int Lq, int Lk, int D,
+                     float scale, const PeSide& pq, const PeSide& pk, hipStream_t st) {
+    if (D <= 32) return launch_t<T, 32, PEK, NW, RW>(Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk, st);
+    if (D <= 64) return launch_t<T, 64, PEK, NW, RW>(Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk, st);
+    if (D <= 128)
+        return launch_t<T, 128, PEK, NW, RW>(Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk, st);
     if constexpr (PEK == kPeNone && NW == 8 && RW == 16)
-        return launch_t<256, PEK, NW, RW>(Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk, st);
+        return launch_t<T, 256, PEK, NW, RW>(Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk, st);
     return hipErrorInvalidValue;
 }
 
-template <int PEK>
-hipError_t launch_form(int form, const float* Q, const float* K, const float* V, float* O,
-                       int BH, int Lq, int Lk, int D, float scale, const PeSide& pq,
-                       const PeSide& pk, hipStream_t st) {
+template <typename T, int PEK>
+hipError_t launch_form(int form, const T* Q, const T* K, const T* V, T* O, int BH, int Lq, int Lk,
+                       int D, float scale, const PeSide& pq, const PeSide& pk, hipStream_t st) {
     // head dims past 128 run 8 waves of 16 rows: two buffers of a 256-wide
     // tile leave room for one workgroup per CU, and 32-row waves would not
     // hold the query's and the output's registers
     if (D > 128) form = kFlashForm8x16;
     switch (form) {
         case kFlashForm4x16:
-            return launch_pe<PEK, 4, 16>(Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk, st);
+            return launch_pe<T, PEK, 4, 16>(Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk, st);
         case kFlashForm8x16:
-            return launch_pe<PEK, 8, 16>(Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk, st);
+            return launch_pe<T, PEK, 8, 16>(Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk, st);
         case kFlashForm4x32:
-            return launch_pe<PEK, 4, 32>(Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk, st);
+            return launch_pe<T, PEK, 4, 32>(Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk, st);
         case kFlashForm8x32:
-            return launch_pe<PEK, 8, 32>(Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk, st);
+            return launch_pe<T, PEK, 8, 32>(Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk, st);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+template <typename T>
+hipError_t launch_typed(int pek, int form, const void* Q, const void* K, const void* V, void* O,
+                        int BH, int Lq, int Lk, int D, float scale, const PeSide& pq,
+                        const PeSide& pk, hipStream_t st) {
+    const T* q = static_cast<const T*>(Q);
+    const T* k = static_cast<const T*>(K);
+    const T* v = static_cast<const T*>(V);
+    T* o = static_cast<T*>(O);
+    switch (pek) {
+        case kPeNone:
+            return launch_form<T, kPeNone>(form, q, k, v, o, BH, Lq, Lk, D, scale, pq, pk, st);
+        case kPeRopeInterleaved:
+            return launch_form<T, kPeRopeInterleaved>(form, q, k, v, o, BH, Lq, Lk, D, scale, pq,
+                                                      pk, st);
+        case kPeRopeHalf:
+            return launch_form<T, kPeRopeHalf>(form, q, k, v, o, BH, Lq, Lk, D, scale, pq, pk, st);
+        case kPeSinusoidal:
+            return launch_form<T, kPeSinusoidal>(form, q, k, v, o, BH, Lq, Lk, D, scale, pq, pk,
+                                                 st);
         default: return hipErrorInvalidValue;
     }
 }
@@ -554,25 +649,18 @@ hipError_t launch_form(int form, const float* Q, const float* K, const float* V,
 }  // namespace
 
 bool flash_supported(int dtype, int pek, int D) {
-    return dtype == kDtypeF32 && D >= 1 && D % 4 == 0 &&
+    return (dtype == kDtypeF32 || dtype == kDtypeBF16) && D >= 1 && D % 4 == 0 &&
            D <= (pek == kPeNone ? kFlashMaxD : kFlashMaxDEncoded);
 }
 
-hipError_t launch_flash(int pek, int form, const float* Q, const float* K, const float* V,
-                        float* O, int BH, int Lq, int Lk, int D, float scale, const PeSide& pq,
+hipError_t launch_flash(int dtype, int pek, int form, const void* Q, const void* K, const void* V,
+                        void* O, int BH, int Lq, int Lk, int D, float scale, const PeSide& pq,
                         const PeSide& pk, hipStream_t st) {
-    switch (pek) {
-        case kPeNone:
-            return launch_form<kPeNone>(form, Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk, st);
-        case kPeRopeInterleaved:
-            return launch_form<kPeRopeInterleaved>(form, Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk,
-                                                   st);
-        case kPeRopeHalf:
-            return launch_form<kPeRopeHalf>(form, Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk, st);
-        case kPeSinusoidal:
-            return launch_form<kPeSinusoidal>(form, Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk, st);
-        default: return hipErrorInvalidValue;
-    }
+    if (dtype == kDtypeF32)
+        return launch_typed<float>(pek, form, Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk, st);
+    if (dtype == kDtypeBF16)
+        return launch_typed<uint16_t>(pek, form, Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk, st);
+    return hipErrorInvalidValue;
 }
 
 }  // namespace atn

@@ -82,17 +82,17 @@ hipError_t launch_gemm_pv(const uint16_t* E, int ldE, float* st_m, float* st_l, 
                           const uint16_t* V, uint16_t* O, int BH, int Lq, int Lk, int D,
                           hipStream_t st);
 
-// Flash-style fp32 attention (flash.hip): any len_q and len_k, head_d <=
-// kFlashMaxD (kFlashMaxDEncoded with a positional encoding) with head_d % 4
-// == 0, 16-byte aligned bases, and every head's Q or K/V under 2^31 bytes
-// (32-bit buffer offsets); no scratch.
+// Flash-style attention (flash.hip), fp32 or bf16 storage (dtype): any
+// len_q and len_k, head_d <= kFlashMaxD (kFlashMaxDEncoded with a positional
+// encoding) with head_d % 4 == 0, 16-byte aligned bases, and every head's Q
+// or K/V under 2^31 bytes (32-bit buffer offsets); no scratch.
 // `form`: the workgroup -- 4 waves of 16 query rows, 8 of 16, 4 of 32 or 8
 // of 32 (head_d <= 128; past 128 every form runs 8 of 16).
 constexpr int kFlashMaxD = 256, kFlashMaxDEncoded = 128;
 constexpr int kFlashForm4x16 = 1, kFlashForm8x16 = 2, kFlashForm4x32 = 3, kFlashForm8x32 = 4;
 bool flash_supported(int dtype, int pek, int D);
-hipError_t launch_flash(int pek, int form, const float* Q, const float* K, const float* V,
-                        float* O, int BH, int Lq, int Lk, int D, float scale, const PeSide& pq,
+hipError_t launch_flash(int dtype, int pek, int form, const void* Q, const void* K, const void* V,
+                        void* O, int BH, int Lq, int Lk, int D, float scale, const PeSide& pq,
                         const PeSide& pk, hipStream_t st);
 
 // Allocation-free entry point: the per-device scratch array (noalloc.hip),

@@ -17,6 +17,13 @@ import oracle
 pytestmark = pytest.mark.gpu
 
 
+@pytest.fixture(autouse=True)
+def _scratch_paths(tuner):
+    """The flash kernel needs no scratch: these tests hold calls on the
+    paths that do (the GEMM path, the split-D pipeline)."""
+    tuner.set(no_flash=True)
+
+
 def _desc(am, pe):
     return {"none": None, "rope_half": am.make_pe("rope", pairing="half"),
             "rope_inter": am.make_pe("rope"), "sinusoidal": am.make_pe("sinusoidal")}[pe]
@@ -47,8 +54,6 @@ def test_chunked_library_workspace(am, dev, tuner, shape, dtype, pe, cap_mib):
     desc = _desc(am, pe)
     sigma = 0.5 if pe == "sinusoidal" else 1.0
     (q, k, v), (Q, K, V) = H.device_inputs((B, Hh, Lq, D), (B, Hh, Lk, D), 1200 + Lq, dtype, sigma)
-    if dtype == "f32":  # the flash kernel needs no scratch: chunk the split-D pipeline
-        tuner.set(no_flash=True)
     full = H.empty(Q.shape, dtype)
     am.attention_ex(q, k, v, full, pe=desc)
     hip_rt.synchronize()

@@ -1,10 +1,14 @@
-"""The flash kernel (fp32, head_d <= 256, any sequence length; flash.hip)
-against the CPU oracle: tile edges of the key loop, head dims padded to the
-kernel's 32/64/128/256 forms, query blocks past the sequence, positional
-encodings applied at load, wide logits, values outside fp16's range
-(power-of-two linearity), and agreement with the split-D pipeline on the
-same inputs.  The reference's own long-sequence test shape (4, 32, 512,
-512, 128) (final/attention.cu:522) runs here too, as in test_gpu_parity.py.
+"""The flash kernel (fp32 and bf16, head_d <= 256, any sequence length;
+flash.hip) against the CPU oracle: tile edges of the key loop, head dims
+padded to the kernel's 32/64/128/256 forms, query blocks past the sequence,
+positional encodings applied at load, wide logits, values outside fp16's
+range (power-of-two linearity), and agreement with the split-D pipeline
+(fp32) and the GEMM path (bf16) on the same inputs.  The reference's own
+long-sequence test shape (4, 32, 512, 512, 128) (final/attention.cu:522)
+runs here too, as in test_gpu_parity.py.
+
+fp32 bar: the reference's (abs and rel above 1e-4).  bf16 bar: within rel
+2e-2 of the fp32 oracle run on the bf16-rounded inputs (helpers.check_bf16).
 """
 import numpy as np
 import pytest
@@ -22,6 +26,38 @@ def _f32_call(am, Q, K, V, desc=None):
     import hip_rt
     hip_rt.synchronize()
     return out.numpy()
+
+
+def _bf16(x):
+    """x rounded to bf16 (nearest even), as float32."""
+    import hip_rt
+    return hip_rt.bf16_bits_to_f32(hip_rt.f32_to_bf16_bits(np.ascontiguousarray(x)))
+
+
+def _bf16_call(am, Q, K, V, desc=None):
+    """One bf16 call on the bf16 roundings of Q, K, V (the caller passes
+    already-rounded values, so the oracle sees what the kernel sees)."""
+    import hip_rt
+    (q, k, v) = (H.upload(x, "bf16") for x in (Q, K, V))
+    out = H.empty(Q.shape, "bf16")
+    am.attention_ex(q, k, v, out, pe=desc)
+    hip_rt.synchronize()
+    got = out.numpy()
+    for x in (q, k, v, out):
+        x.free()
+    return got
+
+
+def _ref(pe, Q, K, V, **kw):
+    L, D = max(Q.shape[2], K.shape[2]), Q.shape[3]
+    if pe == "sinusoidal":
+        st, ct = oracle.sinusoidal_table(L, D)
+        return oracle.attention_sinusoidal(Q, K, V, st, ct, nthreads=16, **kw)
+    if pe in ("rope", "rope_half"):
+        c, s = oracle.rope_cache(L, D)
+        return oracle.attention_rope(Q, K, V, c, s, rotary_dim=D, nthreads=16,
+                                     pairing="half" if pe == "rope_half" else "interleaved", **kw)
+    return oracle.attention(Q, K, V, nthreads=16, **kw)
 
 
 # key lengths around the 64- and 32-key tiles, query lengths around the
@@ -134,15 +170,17 @@ def test_flash_increasing_scores(am, dev):
 
 
 @pytest.mark.parametrize("exps", [(17, -17, 0), (0, 0, 19), (-12, -12, -12), (17, -17, 21),
-                                  (4, -4, 0), (5, -5, 0)],
+                                  (4, -4, 0), (5, -5, 0), (30, 10, 0)],
                          ids=["qk-big", "v-big", "all-small", "all-big", "k-plain-low",
-                              "k-scaled-low"])
+                              "k-scaled-low", "logits-huge"])
 def test_flash_outside_fp16_range(am, dev, exps):
     """Head 1 scaled by powers of two (exact, so the oracle on the unscaled V
     times 2^ev is the reference): K tiles carry a power-of-two scale when
     their largest magnitude lies outside [2^-3, 65504) (k-plain-low puts it
     near 2^-2, unscaled; k-scaled-low near 2^-3, either side), V tiles one
-    only beyond fp16's range, carried into the running output."""
+    only beyond fp16's range, carried into the running output.  logits-huge
+    puts head 1's logits near 2^40, where the softmax subtracts the running
+    max from each score before scaling it (as the oracle does)."""
     B, Hh, Lq, Lk, D = 1, 3, 100, 300, 128
     eq, ek, ev = exps
     print(f"[case] flash f32 scaled 2^{exps}", flush=True)
@@ -271,4 +309,190 @@ def test_flash_graph_replays(am, dev):
     g.destroy()
     n, mabs, _ = H.check_f32(ref, oracle.attention(Q, K, V, nthreads=16))
     assert n == 0, mabs
+    st.destroy()
+
+
+# ---------------------------------------------------------------- bf16
+# bf16 inputs are exact in fp16 wherever a power-of-two scale brings a tile
+# there, so the kernel stages one fp16 part per operand (64-key tiles in
+# every form) and makes one product where fp32 makes three; P goes in as one
+# fp16 part and the output is rounded to bf16.
+
+_BF16_SHAPES = [
+    (1, 2, 65, 1, 64), (1, 2, 65, 64, 64), (1, 2, 70, 65, 64), (1, 3, 130, 129, 32),
+    (1, 1, 200, 300, 128), (1, 2, 129, 513, 100), (1, 1, 80, 1025, 60), (2, 3, 100, 140, 8),
+    (1, 2, 96, 200, 252), (1, 1, 70, 65, 196), (1, 300, 16, 16, 64), (1, 1, 2, 3000, 128),
+]
+
+
+@pytest.mark.parametrize("shape", _BF16_SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_flash_bf16(am, dev, shape):
+    """bf16 calls outside the single-launch window with head_d <= 128 (and
+    up to 256 where the GEMM path does not run: head_d % 8 != 0)."""
+    B, Hh, Lq, Lk, D = shape
+    print(f"[case] flash bf16 {shape}", flush=True)
+    assert am.path(1, B, Hh, Lq, Lk, D) == am.ATN_PATH_FLASH
+    Q, K, V = (_bf16(x) for x in H.rng_inputs((B, Hh, Lq, D), (B, Hh, Lk, D), seed=900 + Lk + D))
+    got = _bf16_call(am, Q, K, V)
+    n, nrel, mabs = H.check_bf16(got, oracle.attention(Q, K, V, nthreads=16))
+    assert n == 0, f"{n} failures, normwise rel {nrel}, max abs {mabs}"
+
+
+@pytest.mark.parametrize("form", ["4x16", "8x16", "4x32", "8x32"])
+@pytest.mark.parametrize("shape,pe", [((1, 3, 130, 129, 32), None), ((1, 2, 200, 300, 128), None),
+                                      ((1, 2, 96, 200, 252), None), ((1, 2, 129, 97, 64), "rope"),
+                                      ((1, 2, 150, 333, 128), "rope_half"),
+                                      ((1, 2, 150, 333, 128), "sinusoidal")],
+                         ids=lambda v: "x".join(map(str, v)) if isinstance(v, tuple) else str(v))
+def test_flash_bf16_forms(am, dev, tuner, form, shape, pe):
+    """Every workgroup form forced, bf16, with and without an encoding
+    (head_d 252: the 256-wide form, which the library takes where the GEMM
+    path does not run; past head_d 128 every form runs 8 waves of 16 rows)."""
+    B, Hh, Lq, Lk, D = shape
+    print(f"[case] flash bf16 form {form} {shape} {pe}", flush=True)
+    tuner.set(flash_form=form)
+    Q, K, V = (_bf16(x) for x in H.rng_inputs((B, Hh, Lq, D), (B, Hh, Lk, D), seed=17 + Lk,
+                                              sigma=0.5 if pe == "sinusoidal" else 1.0))
+    desc = {None: None, "rope": am.make_pe("rope"),
+            "rope_half": am.make_pe("rope", pairing="half"),
+            "sinusoidal": am.make_pe("sinusoidal")}[pe]
+    assert am.path(1, B, Hh, Lq, Lk, D, desc) == am.ATN_PATH_FLASH
+    got = _bf16_call(am, Q, K, V, desc)
+    n, nrel, mabs = H.check_bf16(got, _ref(pe, Q, K, V))
+    assert n == 0, f"{n} failures, normwise rel {nrel}, max abs {mabs}"
+
+
+@pytest.mark.parametrize("form", ["8x16", "8x32"])
+@pytest.mark.parametrize("D", [32, 64, 128])
+def test_flash_bf16_tile_counts(am, dev, tuner, form, D):
+    """Key lengths of 1 to 9 64-key tiles and the edges between them."""
+    tuner.set(flash_form=form)
+    B, Hh, Lq = 1, 2, 70
+    for Lk in (63, 64, 65, 127, 128, 129, 257, 513):
+        print(f"[case] flash bf16 form {form} D={D} Lk={Lk}", flush=True)
+        Q, K, V = (_bf16(x) for x in H.rng_inputs((B, Hh, Lq, D), (B, Hh, Lk, D),
+                                                  seed=3000 + Lk + D))
+        got = _bf16_call(am, Q, K, V)
+        n, nrel, mabs = H.check_bf16(got, oracle.attention(Q, K, V, nthreads=16))
+        assert n == 0, f"Lk={Lk}: {n} failures, normwise rel {nrel}, max abs {mabs}"
+
+
+@pytest.mark.parametrize("exps", [(30, -30, 0), (0, 0, 40), (0, 0, -40), (-20, -20, -20),
+                                  (20, 20, 20), (3, -3, 0), (0, -5, -3)],
+                         ids=["qk-big", "v-big", "v-small", "all-small", "all-big",
+                              "k-scaled-low", "k-and-v-low"])
+def test_flash_bf16_outside_fp16_range(am, dev, exps):
+    """bf16's range is fp32's: head 1 scaled by powers of two far outside
+    fp16's (exact, so the oracle on the unscaled V times 2^ev is the
+    reference).  Q takes a scale per wave, K and V one per key tile whenever
+    the tile's largest magnitude lies outside [2^-3, 65504), so that small
+    values keep their bits in the one fp16 part too; all-big puts head 1's
+    logits near 2^40 (the softmax's exact form)."""
+    B, Hh, Lq, Lk, D = 1, 3, 100, 300, 128
+    eq, ek, ev = exps
+    print(f"[case] flash bf16 scaled 2^{exps}", flush=True)
+    Q, K, V = (_bf16(x) for x in H.rng_inputs((B, Hh, Lq, D), (B, Hh, Lk, D), seed=37))
+    Q[:, 1] *= np.float32(2.0 ** eq)
+    K[:, 1] *= np.float32(2.0 ** ek)
+    Vs = V.copy()
+    Vs[:, 1] *= np.float32(2.0 ** ev)
+    got = _bf16_call(am, Q, K, Vs)
+    assert np.isfinite(got).all()
+    got[:, 1] *= np.float32(2.0 ** -ev)
+    n, nrel, mabs = H.check_bf16(got, oracle.attention(Q, K, V, nthreads=16))
+    assert n == 0, f"{n} failures, normwise rel {nrel}, max abs {mabs}"
+
+
+def test_flash_bf16_wide_logits_and_rising_scores(am, dev):
+    """sigma 3 inputs (logits to about +-40), and scores that rise key tile
+    by key tile, so that the running maximum moves and the output is
+    rescaled between tiles."""
+    B, Hh, Lq, Lk, D = 1, 2, 200, 600, 128
+    print("[case] flash bf16 sigma 3", flush=True)
+    Q, K, V = (_bf16(x) for x in H.rng_inputs((B, Hh, Lq, D), (B, Hh, Lk, D), seed=79, sigma=3.0))
+    got = _bf16_call(am, Q, K, V)
+    n, nrel, mabs = H.check_bf16(got, oracle.attention(Q, K, V, nthreads=16))
+    assert n == 0, f"sigma 3: {n} failures, normwise rel {nrel}, max abs {mabs}"
+    print("[case] flash bf16 rising scores", flush=True)
+    Q, K, V = H.rng_inputs((B, Hh, 64, 64), (B, Hh, 512, 64), seed=93)
+    Q[..., 0] = np.abs(Q[..., 0]) + 1.0
+    Q[..., 1:] *= np.float32(0.1)
+    K[..., 0] = np.linspace(-40, 40, 512, dtype=np.float32)[None, None, :]
+    Q, K, V = _bf16(Q), _bf16(K), _bf16(V)
+    got = _bf16_call(am, Q, K, V)
+    n, nrel, mabs = H.check_bf16(got, oracle.attention(Q, K, V, nthreads=16))
+    assert n == 0, f"rising: {n} failures, normwise rel {nrel}, max abs {mabs}"
+
+
+def test_flash_bf16_nonfinite_inputs_propagate(am, dev, tuner):
+    """An infinite query element makes its output row non-finite, a NaN
+    value element its output column NaN; every other element keeps the bar."""
+    for form in ("8x16", "8x32"):
+        B, Hh, Lq, Lk, D = 1, 2, 300, 333, 128
+        print(f"[case] flash bf16 non-finite inputs, form {form}", flush=True)
+        tuner.set(flash_form=form)
+        Q, K, V = (_bf16(x) for x in H.rng_inputs((B, Hh, Lq, D), (B, Hh, Lk, D), seed=73))
+        Q[0, 1, 5, 100] = np.inf
+        V[0, 0, 200, 33] = np.nan
+        got = _bf16_call(am, Q, K, V)
+        ref = oracle.attention(Q, K, V, nthreads=16)
+        assert not np.isfinite(got[0, 1, 5]).any() and np.isnan(got[0, 0, :, 33]).all()
+        keep = np.ones((Hh, Lq, D), dtype=bool)
+        keep[1, 5, :] = False
+        keep[0, :, 33] = False
+        n, nrel, mabs = H.check_bf16(got[0][keep], ref[0][keep])
+        assert n == 0, (nrel, mabs)
+
+
+@pytest.mark.parametrize("shape,pe", [((1, 4, 200, 200, 128), None), ((1, 2, 65, 1025, 64), None),
+                                      ((1, 2, 300, 520, 128), "rope_half")],
+                         ids=lambda v: "x".join(map(str, v)) if isinstance(v, tuple) else str(v))
+def test_flash_bf16_matches_gemm_path(am, dev, tuner, shape, pe):
+    """The bf16 flash kernel and the GEMM path (forced with
+    atn_tuning.no_flash) on the same inputs: both within the bar of the
+    oracle and of each other."""
+    B, Hh, Lq, Lk, D = shape
+    print(f"[case] flash bf16 vs GEMM {shape} {pe}", flush=True)
+    desc = None if pe is None else am.make_pe("rope", pairing="half")
+    Q, K, V = (_bf16(x) for x in H.rng_inputs((B, Hh, Lq, D), (B, Hh, Lk, D), seed=5 + Lk))
+    ref = _ref(pe, Q, K, V)
+    assert am.path(1, B, Hh, Lq, Lk, D, desc) == am.ATN_PATH_FLASH
+    got_f = _bf16_call(am, Q, K, V, desc)
+    tuner.set(no_flash=True)
+    assert am.path(1, B, Hh, Lq, Lk, D, desc) == am.ATN_PATH_GEMM
+    got_g = _bf16_call(am, Q, K, V, desc)
+    for got in (got_f, got_g):
+        n, nrel, mabs = H.check_bf16(got, ref)
+        assert n == 0, (nrel, mabs)
+    n, nrel, mabs = H.check_bf16(got_f, got_g)
+    assert n == 0, (nrel, mabs)
+
+
+def test_flash_bf16_graph_replays(am, dev):
+    """Captured HIP graph of bf16 flash calls replayed with eager work
+    between the replays: every replay equals the eager result bit for bit."""
+    import hip_rt
+    B, Hh, Lq, Lk, D = 1, 4, 200, 300, 128
+    print("[case] flash bf16 graph replay", flush=True)
+    (q, k, v), (Q, K, V) = H.device_inputs((B, Hh, Lq, D), (B, Hh, Lk, D), 97, "bf16")
+    st = hip_rt.Stream()
+    eager = H.empty(Q.shape, "bf16")
+    am.attention_ex(q, k, v, eager, stream=st)
+    st.synchronize()
+    ref = eager.bits()
+    outs = [H.empty(Q.shape, "bf16") for _ in range(2)]
+    g = hip_rt.Graph(st, lambda: [am.attention_ex(q, k, v, o, stream=st) for o in outs])
+    for _ in range(3):
+        for o in outs:
+            o.fill_nan()
+        hip_rt.synchronize()
+        g.launch()
+        st.synchronize()
+        for o in outs:
+            assert np.array_equal(o.bits(), ref)
+        am.attention_ex(q, k, v, eager, stream=st)
+        st.synchronize()
+    g.destroy()
+    n, nrel, mabs = H.check_bf16(eager.numpy(), oracle.attention(Q, K, V, nthreads=16))
+    assert n == 0, (nrel, mabs)
     st.destroy()

@@ -5,10 +5,10 @@ the encoding tables grow (to more positions) while kernels of other threads
 that read the smaller tables are still queued.  ctypes releases the GIL
 around each foreign call, so the calls overlap in the library's host code.
 
-The shapes take the GEMM path (bf16, with and without encodings) and the
-split-D pipeline (fp32 beyond the single-launch window): neither waits on
-other workgroups, so kernels of the other threads holding CUs only delay
-them.  (The single-launch kernel's exchange needs its whole grid resident;
+The shapes take the GEMM path (bf16, with and without encodings), the
+flash kernel (bf16 and fp32) and the split-D pipeline (fp32 past head_d
+256): none waits on other workgroups, so kernels of the other threads
+holding CUs only delay them.  (The single-launch kernel's exchange needs its whole grid resident;
 its concurrency contract is covered in test_gpu_fused.py.)
 """
 import threading
@@ -23,7 +23,7 @@ pytestmark = pytest.mark.gpu
 
 CASES = [  # (dtype, pe, (B, H, Lq, Lk, D), expected path)
     ("bf16", "sinusoidal", (1, 2, 256, 384, 256), "gemm"),
-    ("bf16", "rope_half", (1, 2, 128, 640, 128), "gemm"),
+    ("bf16", "rope_half", (1, 2, 128, 640, 128), "flash"),
     ("f32", "none", (1, 2, 100, 300, 64), "flash"),
     ("f32", "none", (1, 2, 100, 300, 520), "split_d"),
     ("bf16", "sinusoidal", (1, 1, 129, 1040, 512), "gemm"),

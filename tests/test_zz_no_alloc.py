@@ -38,11 +38,12 @@ def _pair(am, shape, dtype, pe, seed):
 @pytest.mark.parametrize("first,second,dtype,pe", [
     ((1, 4, 64, 64, 2048), (1, 2, 32, 32, 512), "f32", None),          # single-launch kernel
     ((1, 4, 32, 128, 8192), (1, 1, 16, 100, 1024), "bf16", None),      # single-launch, bf16
-    ((1, 2, 256, 512, 256), (1, 1, 128, 256, 128), "bf16", "rope_half"),  # GEMM path
+    ((1, 2, 256, 512, 256), (1, 1, 128, 256, 256), "bf16", "rope_half"),  # GEMM path
     ((1, 2, 300, 200, 260), (1, 1, 70, 90, 22), "f32", None),          # split-D pipeline
     ((1, 2, 300, 200, 36), (1, 1, 70, 90, 20), "f32", None),           # flash kernel
-    ((2, 2, 256, 512, 128), (1, 2, 128, 128, 128), "bf16", "sinusoidal"),  # GEMM path
-], ids=["fused-f32", "fused-bf16", "gemm-rope", "splitd", "flash", "gemm-sin"])
+    ((1, 2, 300, 200, 128), (1, 1, 70, 90, 64), "bf16", "rope_half"),  # flash kernel, bf16
+    ((2, 2, 256, 512, 256), (1, 2, 128, 128, 256), "bf16", "sinusoidal"),  # GEMM path
+], ids=["fused-f32", "fused-bf16", "gemm-rope", "splitd", "flash", "flash-bf16", "gemm-sin"])
 def test_noalloc_matches_ex_two_calls(am, dev, first, second, dtype, pe):
     desc = None
     if pe == "rope_half":
@@ -67,18 +68,22 @@ def test_noalloc_chunks_large_shapes(am, dev):
     _pair(am, shape, "bf16", None, 950)
 
 
-def test_noalloc_refuses_what_it_cannot_do(am, dev):
+def test_noalloc_refuses_what_it_cannot_do(am, dev, tuner):
     import hip_rt
     print("[case] noalloc refusals", flush=True)
     L_ = am.lib()
-    # one query row against 32 Mi keys: even a one-row chunk needs 64 MiB of
-    # scores -- refused before anything is launched
+    # one query row against 32 Mi keys on the GEMM path (the flash kernel,
+    # which bf16 at head_d 8 takes by default, needs no scratch): even a
+    # one-row chunk needs 64 MiB of scores -- refused before anything is
+    # launched
+    tuner.set(no_flash=True)
     Lk = 1 << 25
     q, o = hip_rt.DeviceArray((1, 1, 1, 8), "bf16"), hip_rt.DeviceArray((1, 1, 1, 8), "bf16")
     k, v = hip_rt.DeviceArray((1, 1, Lk, 8), "bf16"), hip_rt.DeviceArray((1, 1, Lk, 8), "bf16")
     st = L_.atn_attention_fwd_noalloc_ex(1, q.ptr, k.ptr, v.ptr, o.ptr, 1, 1, 1, Lk, 8, None,
                                          None)
     assert st == am.ATN_ERR_SCRATCH_LIMIT, st
+    tuner.clear()
     # an encoding base whose tables were never built
     odd = am.make_pe("rope", pairing="half", base=1234.5)
     qs, os_ = (hip_rt.DeviceArray((1, 1, 64, 256), "bf16") for _ in range(2))
