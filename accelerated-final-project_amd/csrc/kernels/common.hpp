@@ -173,48 +173,93 @@ __device__ __forceinline__ float sin_pe(const PeSide& t, int pos, int d) {
 
 // The positional encoding of this side applied to x[d..d+3] of one row
 // (row pointer xr, position pos), already loaded as x (elements at or past
-// dend 0: they stay 0).  d is a multiple of 4.
+// dend 0: they stay 0).  d is a multiple of 4.  vec: the row may be read 4
+// elements at a time (aligned for Elem<T>::ld4).  With the library's compact
+// tables (dup = 0, whose rows are 16-byte aligned where a group needs it) a
+// whole group of 4 reads its angles and its rotate-half partners as vectors;
+// the rotation arithmetic is the same either way.
 template <typename T, int PEK>
 __device__ __forceinline__ float4 apply_pe4(float4 x, const T* __restrict__ xr, int pos, int d,
-                                           int dend, const PeSide& pe) {
+                                           int dend, const PeSide& pe, bool vec) {
     float v[4] = {x.x, x.y, x.z, x.w};
     if constexpr (PEK == kPeRopeInterleaved) {
         if (pe.on) {
+            if (!pe.dup && (pe.ld & 1) == 0 && d + 3 < pe.rotary) {
+                // frequencies d / 2 and d / 2 + 1: 8 bytes of each table
+                const size_t idx = (size_t)pos * pe.ld + (d >> 1);
+                const float2 c = *reinterpret_cast<const float2*>(pe.a + idx);
+                const float2 sn = *reinterpret_cast<const float2*>(pe.b + idx);
+                const float x0 = v[0], x1 = v[1], x2 = v[2], x3 = v[3];
+                v[0] = rot_first(x0, x1, c.x, sn.x);
+                v[1] = rot_second(x0, x1, c.x, sn.x);
+                v[2] = rot_first(x2, x3, c.y, sn.y);
+                v[3] = rot_second(x2, x3, c.y, sn.y);
+            } else {
 #pragma unroll
-            for (int c = 0; c < 4; c += 2) {
-                const int e = d + c;  // even
-                if (e < pe.rotary) {
-                    float cs, sn;
-                    rope_cs(pe, pos, e >> 1, cs, sn);
-                    const float x0 = v[c], x1 = v[c + 1];
-                    v[c] = rot_first(x0, x1, cs, sn);
-                    v[c + 1] = rot_second(x0, x1, cs, sn);
+                for (int c = 0; c < 4; c += 2) {
+                    const int e = d + c;  // even
+                    if (e < pe.rotary) {
+                        float cs, sn;
+                        rope_cs(pe, pos, e >> 1, cs, sn);
+                        const float x0 = v[c], x1 = v[c + 1];
+                        v[c] = rot_first(x0, x1, cs, sn);
+                        v[c + 1] = rot_second(x0, x1, cs, sn);
+                    }
                 }
             }
         }
     } else if constexpr (PEK == kPeRopeHalf) {
         if (pe.on) {
             const int h = pe.rotary >> 1;
+            if (vec && !pe.dup && (h & 3) == 0 && (pe.ld & 3) == 0 && d + 3 < pe.rotary &&
+                d + 3 < dend) {
+                // the 4 dims lie on one side of h: their partners are the 4
+                // dims h away, their frequencies 4 consecutive ones
+                const bool lo = d < h;
+                const float4 xp = Elem<T>::ld4(xr, lo ? d + h : d - h);
+                const size_t idx = (size_t)pos * pe.ld + (lo ? d : d - h);
+                const float4 c = *reinterpret_cast<const float4*>(pe.a + idx);
+                const float4 sn = *reinterpret_cast<const float4*>(pe.b + idx);
+                const float p[4] = {xp.x, xp.y, xp.z, xp.w};
+                const float cc[4] = {c.x, c.y, c.z, c.w}, ss[4] = {sn.x, sn.y, sn.z, sn.w};
 #pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                const int e = d + c;
-                // (past dend the element stays 0: its partner is loaded from
-                // the row itself, which would make it nonzero)
-                if (e < pe.rotary && e < dend) {
-                    const bool lo = e < h;
-                    const int f = lo ? e : e - h;
-                    const float xp = Elem<T>::ld(xr, lo ? e + h : e - h);
-                    float cs, sn;
-                    rope_cs(pe, pos, f, cs, sn);
-                    v[c] = lo ? rot_first(v[c], xp, cs, sn) : rot_second(xp, v[c], cs, sn);
+                for (int k = 0; k < 4; ++k)
+                    v[k] = lo ? rot_first(v[k], p[k], cc[k], ss[k])
+                              : rot_second(p[k], v[k], cc[k], ss[k]);
+            } else {
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    const int e = d + c;
+                    // (past dend the element stays 0: its partner is loaded
+                    // from the row itself, which would make it nonzero)
+                    if (e < pe.rotary && e < dend) {
+                        const bool lo = e < h;
+                        const int f = lo ? e : e - h;
+                        const float xp = Elem<T>::ld(xr, lo ? e + h : e - h);
+                        float cs, sn;
+                        rope_cs(pe, pos, f, cs, sn);
+                        v[c] = lo ? rot_first(v[c], xp, cs, sn) : rot_second(xp, v[c], cs, sn);
+                    }
                 }
             }
         }
     } else if constexpr (PEK == kPeSinusoidal) {
         if (pe.on) {
+            if (!pe.dup && (pe.ld & 1) == 0 && d + 3 < dend) {
+                // dims d, d + 2 take sin of frequencies d / 2, d / 2 + 1, dims
+                // d + 1, d + 3 their cos: 8 bytes of each table
+                const size_t idx = (size_t)pos * pe.ld + (d >> 1);
+                const float2 sn = *reinterpret_cast<const float2*>(pe.a + idx);
+                const float2 c = *reinterpret_cast<const float2*>(pe.b + idx);
+                v[0] = v[0] + sn.x;
+                v[1] = v[1] + c.x;
+                v[2] = v[2] + sn.y;
+                v[3] = v[3] + c.y;
+            } else {
 #pragma unroll
-            for (int c = 0; c < 4; ++c)
-                if (d + c < dend) v[c] = v[c] + sin_pe(pe, pos, d + c);
+                for (int c = 0; c < 4; ++c)
+                    if (d + c < dend) v[c] = v[c] + sin_pe(pe, pos, d + c);
+            }
         }
     }
     return make_float4(v[0], v[1], v[2], v[3]);
@@ -235,7 +280,7 @@ __device__ __forceinline__ float4 load_row4_pe(const T* __restrict__ xr, int pos
         for (int c = 0; c < 4; ++c)
             if (d + c < dend) v[c] = Elem<T>::ld(xr, d + c);
     }
-    return apply_pe4<T, PEK>(make_float4(v[0], v[1], v[2], v[3]), xr, pos, d, dend, pe);
+    return apply_pe4<T, PEK>(make_float4(v[0], v[1], v[2], v[3]), xr, pos, d, dend, pe, vec_ok);
 }
 
 }  // namespace atn

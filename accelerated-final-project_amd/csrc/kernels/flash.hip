@@ -282,7 +282,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_flash(const T* __restrict__
             for (int i = 0; i < G::NLD; ++i) {
                 const int key = k0 + lrow + G::RSTEP * i;
                 if (key < Lk && lcol < D)
-                    kr[i] = apply_pe4<T, PEK>(kr[i], Kh + (size_t)key * D, key, lcol, D, pk);
+                    kr[i] = apply_pe4<T, PEK>(kr[i], Kh + (size_t)key * D, key, lcol, D, pk, true);
             }
         }
         float mk = 0.f, mv = 0.f;

@@ -63,6 +63,12 @@ SHAPES = [
     # one (the split-D pipeline); names without commas (--shapes splits on them)
     ("ref llama 4x32x512x128", "f32", 4, 32, 512, 512, 128, "none"),
     ("f32 long 1x4x512x512x2048", "f32", 1, 4, 512, 512, 2048, "none"),
+    # bf16 at head_dim <= 128 beyond the single-launch window (the flash
+    # kernel; torch's SDPA runs its own flash kernel here)
+    ("bf16 llama 4x32x512x128", "bf16", 4, 32, 512, 512, 128, "none"),
+    ("bf16 rope-half 4x32x512x128", "bf16", 4, 32, 512, 512, 128, "rope_half"),
+    ("bf16 long 1x8x4096x4096x128", "bf16", 1, 8, 4096, 4096, 128, "none"),
+    ("bf16 long 1x32x2048x2048x64", "bf16", 1, 32, 2048, 2048, 64, "none"),
 ]
 
 

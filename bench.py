@@ -67,12 +67,15 @@ CONFIGS = {
         "sinusoidal", 0.5),
 }
 SWEEP_D = (512, 4096, 8192)
-# fp32 beyond the single-launch window, measured beside the configs: the
+# beyond the single-launch window, measured beside the configs: the
 # reference's own long-sequence test shape (final/attention.cu:522; the flash
-# kernel) and a head_dim-2048 shape of the same length (the split-D pipeline)
-LONG_F32 = {
+# kernel) in fp32 and in bf16, and a head_dim-2048 fp32 shape of the same
+# length (the split-D pipeline)
+LONG = {
     "ref_long_f32": ("fp32 SDPA, the reference's long test shape (4,32,512,512,128)", "f32", 4, 32,
                      512, 512, 128, "none", 1.0),
+    "ref_long_bf16": ("bf16 SDPA at the reference's long test shape (4,32,512,512,128)", "bf16", 4,
+                      32, 512, 512, 128, "none", 1.0),
     "long_f32_D2048": ("fp32 SDPA (1,4,512,512,2048)", "f32", 1, 4, 512, 512, 2048, "none", 1.0),
 }
 
@@ -89,10 +92,12 @@ def parse():
                     help="one config only (0 = headline config 2 plus every other config)")
     ap.add_argument("--head-dim", type=int, default=0, help="override D (config-2 sweep)")
     ap.add_argument("--shape", default="", metavar="B,H,LQ,LK,D",
-                    help="time this fp32 shape instead (no encoding; for profiling the flash "
+                    help="time this shape instead (no encoding; for profiling the flash, GEMM "
                          "and split-D paths)")
+    ap.add_argument("--dtype", default="f32", choices=["f32", "bf16"],
+                    help="element type of --shape")
     ap.add_argument("--no-flash", action="store_true",
-                    help="keep fp32 calls off the flash kernel (atn_tuning.no_flash)")
+                    help="keep calls off the flash kernel (atn_tuning.no_flash)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="CPU-oracle sample time of the headline (0 = skip every CPU baseline)")
     ap.add_argument("--cpu-seconds-other", type=float, default=3.0,
@@ -446,7 +451,9 @@ def main():
         am.set_tuning(no_flash=True)
     if a.shape:
         b_, h_, lq_, lk_, d_ = (int(x) for x in a.shape.split(","))
-        cfg = [f"fp32 SDPA ({b_},{h_},{lq_},{lk_},{d_})", "f32", b_, h_, lq_, lk_, d_, "none", 1.0]
+        lbl = "fp32" if a.dtype == "f32" else "bf16"
+        cfg = [f"{lbl} SDPA ({b_},{h_},{lq_},{lk_},{d_})", a.dtype, b_, h_, lq_, lk_, d_, "none",
+               1.0]
         head_cfg_id = 0
     if a.head_dim:
         cfg[6] = a.head_dim
@@ -485,7 +492,7 @@ def main():
     PATH_NAMES.update({
         am.ATN_PATH_FUSED_SMALL: "k_fused_small (one launch per step)",
         am.ATN_PATH_SPLIT_D: "split-D pipeline (QK^T partials + softmax + PV per step)",
-        am.ATN_PATH_FLASH: "k_flash_f32 (one launch per step)",
+        am.ATN_PATH_FLASH: "k_flash (one launch per step)",
         am.ATN_PATH_GEMM: ("GEMM path (encode, QK^T GEMM with exp epilogue, PV GEMM per step; "
                            "whole-step figure, per-kernel split in profiles/)"),
     })
@@ -519,9 +526,9 @@ def main():
     if a.config == 0 and not a.shape:
         per_config = {}
         others = [(f"cfg2_D{d}", 2, d) for d in SWEEP_D] + [(f"cfg{c}", c, 0) for c in (1, 3, 4, 5)]
-        others += [(k, 0, 0) for k in LONG_F32]
+        others += [(k, 0, 0) for k in LONG]
         for key, cid, dov in others:
-            c = list(CONFIGS[cid] if cid else LONG_F32[key])
+            c = list(CONFIGS[cid] if cid else LONG[key])
             if dov:
                 c[6] = dov
                 c[0] = c[0].split(" (")[0] + f" ({c[2]},{c[3]},{c[4]},{c[5]},{c[6]})"
