@@ -293,11 +293,12 @@ int atn_prepare_pe_ex(const atn_pe_desc *pe, int head_d, int max_positions);
  * units. */
 #define ATN_PATH_FUSED_SMALL 1 /* one launch: split-D slices + device-side S all-reduce */
 #define ATN_PATH_SPLIT_D 2     /* three launches: partial QK^T, softmax, PV */
-#define ATN_PATH_FLASH 4       /* fp32, head_d <= 256 (128 with an encoding), head_d % 4 == 0,
-                                  outside the single-launch window: one launch, online softmax
-                                  over key tiles, no scratch */
-#define ATN_PATH_GEMM 3        /* bf16, D % 8 == 0, outside the single-launch window: MFMA QK^T GEMM,
-                                  row softmax, MFMA PV GEMM */
+#define ATN_PATH_FLASH 4       /* outside the single-launch window, head_d % 4 == 0: fp32 with
+                                  head_d <= 256 (128 with an encoding), bf16 with head_d <= 128
+                                  (up to 256 where the GEMM path does not run): one launch,
+                                  online softmax over key tiles, no scratch */
+#define ATN_PATH_GEMM 3        /* bf16, D % 8 == 0, head_d > 128, outside the single-launch
+                                  window: MFMA QK^T GEMM, row softmax, MFMA PV GEMM */
 int atn_attention_path_ex(int dtype, int batch, int heads, int len_q, int len_k, int head_d,
                           const atn_pe_desc *pe);
 
@@ -318,8 +319,8 @@ typedef struct atn_tuning {
     int fused_exchange;    /* 1: one gather, 2: reduce-scatter + all-gather */
     int fused_xcd;         /* 1: exchange inside one XCD's L2, 2: at device scope */
     int no_fused;          /* nonzero: never the single-launch kernel (the other paths) */
-    int no_flash;          /* nonzero: never the flash kernel (fp32 calls it would take run on
-                              the split-D pipeline) */
+    int no_flash;          /* nonzero: never the flash kernel (calls it would take run on
+                              the GEMM path, bf16 with D % 8 == 0, or the split-D pipeline) */
     int gemm_fused_k;      /* long-sequence path: 1 K's encoding inside the QK^T GEMM
                               wherever it can run there, 2 never */
     int workspace_cap_mib; /* cap of the library's own workspace before a call is chunked
