@@ -75,7 +75,7 @@ class Tuning(ctypes.Structure):
         "fused_rows", "fused_dc", "fused_exchange", "fused_xcd", "no_fused", "no_flash",
         "gemm_fused_k",
         "workspace_cap_mib", "model_cus", "model_xccs", "preset_status", "flash_form",
-        "splitd_tile")]
+        "splitd_tile", "flash_split")]
 
 
 class FusedPlanInfo(ctypes.Structure):
@@ -189,12 +189,15 @@ def set_tuning(fused_rows: int = 0, fused_dc: int = 0, fused_exchange: str | Non
                fused_xcd: str | None = None, no_fused: bool = False, no_flash: bool = False,
                gemm_fused_k: str | None = None, workspace_cap_mib: int = 0, model_cus: int = 0,
                model_xccs: int = 0, preset_status: bool = False, flash_form: str | None = None,
-               splitd_tile: int = 0) -> None:
+               splitd_tile: int = 0, flash_split: int = 0) -> None:
     """atn_set_tuning_ex with named fields (every field not given is reset).
-    flash_form: "4x16", "8x16" or "4x32" (waves x query rows per wave)."""
+    flash_form: "4x16", "8x16", "4x32" or "8x32" (waves x query rows per
+    wave); flash_split: 1 never split the flash kernel's keys, n >= 2 into
+    n parts."""
     t = Tuning(fused_rows, fused_dc, _EXCHANGE[fused_exchange], _SCOPE[fused_xcd],
                int(no_fused), int(no_flash), _FUSED_K[gemm_fused_k], workspace_cap_mib,
-               model_cus, model_xccs, int(preset_status), _FLASH_FORM[flash_form], splitd_tile)
+               model_cus, model_xccs, int(preset_status), _FLASH_FORM[flash_form], splitd_tile,
+               flash_split)
     st = lib().atn_set_tuning_ex(ctypes.byref(t))
     if st != ATN_OK:
         raise AtnError(st, "atn_set_tuning_ex")

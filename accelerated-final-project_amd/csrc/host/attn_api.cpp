@@ -784,6 +784,54 @@ int flash_form(const Shape& s, int dev) {
                                                        : atn::kFlashForm8x16;
 }
 
+// Query rows per workgroup of a flash form.
+int flash_rows(int form, int D) {
+    if (D > 128) form = atn::kFlashForm8x16;
+    return form == atn::kFlashForm4x16 ? 64 : (form == atn::kFlashForm8x32 ? 256 : 128);
+}
+
+// Key splits of the flash kernel.  A workgroup walks all keys of its query
+// block, so a grid of few (head, query block) pairs leaves CUs idle (64
+// workgroups at (1,4,2048,2048,128), 32 for 16 queries against 4096 keys at
+// 32 heads).  Such calls split the keys into parts of whole 64-key chunks,
+// two at least, so that the grid reaches about kFlashSplitTarget workgroups;
+// each part writes its normalized output and statistics (fp32) and a second
+// kernel merges them.  Decided from the shape alone (plus
+// atn_tuning.flash_split), so the workspace queries need no device.
+struct FlashSplit {
+    int nsplit = 1, kchunk = 0;
+    size_t bytes = 0;  // scratch of the parts
+};
+constexpr int kFlashSplitTarget = 256, kFlashSplitBelow = 128, kFlashSplitMax = 32;
+
+FlashSplit flash_split(const Shape& s, int rows) {
+    FlashSplit f;
+    const int forced = tune().flash_split;
+    if (forced == 1) return f;
+    const int64_t grid = s.BH * ((s.Lq + rows - 1) / rows);
+    const int chunks = (s.Lk + 63) / 64;
+    int64_t n;
+    if (forced >= 2) {
+        n = std::min<int64_t>(forced, chunks);
+    } else {
+        if (grid > kFlashSplitBelow) return f;
+        n = std::min<int64_t>({(kFlashSplitTarget + grid - 1) / grid, chunks / 2, kFlashSplitMax});
+    }
+    if (n < 2) return f;
+    f.kchunk = (int)((chunks + n - 1) / n) * 64;
+    f.nsplit = (s.Lk + f.kchunk - 1) / f.kchunk;
+    if (f.nsplit < 2) return FlashSplit{};
+    f.bytes = (size_t)f.nsplit * s.BH * s.Lq * (s.D + 4) * 4;
+    return f;
+}
+
+// The most scratch any flash form's split of this shape takes.
+size_t flash_split_bound(const Shape& s) {
+    size_t b = 0;
+    for (int rows : {64, 128, 256}) b = std::max(b, flash_split(s, rows).bytes);
+    return b;
+}
+
 // Scratch bytes of the path a call of shape s takes: fused (when planned and
 // vector-aligned), else GEMM (when planned and 16-byte aligned), else the
 // split-D pipeline.  vec / a16: the alignment of the call's pointers; pass
@@ -794,9 +842,12 @@ size_t path_need(int dtype, const Shape& s, const PePlan& plan, bool query_devic
     const GemmPlan gp = gemm_plan(dtype, s, plan);
     const size_t split = kSyncBytes + stream_plan(s).bytes;
     if (vec < 0 || a16 < 0)
-        return std::max({fp.ok ? fp.bytes : (size_t)0, gp.ok ? gp.bytes : (size_t)0, split});
+        return std::max({fp.ok ? fp.bytes : (size_t)0, gp.ok ? gp.bytes : (size_t)0, split,
+                         flash_ok(dtype, s, plan) ? kSyncBytes + flash_split_bound(s)
+                                                  : (size_t)0});
     if (fp.ok && vec) return fp.bytes;
-    if (a16 && flash_ok(dtype, s, plan)) return kSyncBytes;  // the flash kernel: no scratch
+    if (a16 && flash_ok(dtype, s, plan))  // the flash kernel: only its key splits' parts
+        return kSyncBytes + flash_split_bound(s);
     if (gp.ok && a16) return gp.bytes;
     return split;
 }
@@ -864,9 +915,12 @@ int attention_run(int dtype, const void* Q, const void* K, const void* V, void* 
     const bool use_flash = !use_fused && a16 && flash_ok(dtype, s, plan);
     const bool use_gemm = !use_fused && !use_flash && gp.ok && aligned(Q, 16) && aligned(K, 16) &&
                           aligned(V, 16) && aligned(out, 16);
+    const int fform = use_flash ? flash_form(s, dev) : 0;
+    const FlashSplit fs = use_flash ? flash_split(s, flash_rows(fform, D)) : FlashSplit{};
     const size_t need =
         use_fused ? fd.bytes
-                  : (use_flash ? kSyncBytes : (use_gemm ? gp.bytes : kSyncBytes + sp.bytes));
+                  : (use_flash ? kSyncBytes + fs.bytes
+                               : (use_gemm ? gp.bytes : kSyncBytes + sp.bytes));
     void* ws = workspace;
     if (no_alloc) {
         if (need > atn::kNoAllocScratchBytes) return ATN_ERR_SCRATCH_LIMIT;
@@ -953,8 +1007,8 @@ int attention_run(int dtype, const void* Q, const void* K, const void* V, void* 
         return ATN_OK;
     }
     if (use_flash) {
-        ATN_HIP(atn::launch_flash(dtype, plan.pek, flash_form(s, dev), Q, K, V, out, (int)s.BH,
-                                  Lq, Lk, D, scale, plan.q, plan.k, stream));
+        ATN_HIP(atn::launch_flash(dtype, plan.pek, fform, Q, K, V, out, (int)s.BH, Lq, Lk, D,
+                                  scale, plan.q, plan.k, fs.nsplit, fs.kchunk, scratch, stream));
         return ATN_OK;
     }
     float* S = scratch;

@@ -171,9 +171,11 @@ template <typename T, int DP, int PEK, int NW, int RW>
 __global__ __launch_bounds__(64 * NW, 8 / NW) void k_flash(const T* __restrict__ Qg,
                                                              const T* __restrict__ Kg,
                                                              const T* __restrict__ Vg,
-                                                             T* __restrict__ Og, int Lq, int Lk,
+                                                             T* __restrict__ Og, int Lq, int LkAll,
                                                              int D, int qblocks, float scale,
-                                                             PeSide pq, PeSide pk) {
+                                                             PeSide pq, PeSide pk, int nsplit,
+                                                             int kchunk, float* __restrict__ part,
+                                                             float4* __restrict__ stats) {
     constexpr bool kBf = sizeof(T) == 2;
     constexpr int es = (int)sizeof(T);
     using G = FlashGeo<DP, PEK != kPeNone, NW, RW, !kBf>;
@@ -188,17 +190,23 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_flash(const T* __restrict__
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     // lane (row lr of its MFMA tiles, lane group lg)
     const int lr = lane & (RW - 1), lg = lane / RW;
-    // workgroup -> (head, query block); with a grid that is a multiple of 8
-    // the query blocks of a head are consecutive on one XCD (the dispatcher
-    // deals ids to the 8 XCDs round robin), so its K and V stay in that L2
+    // workgroup -> (head, query block, key split); with a grid that is a
+    // multiple of 8 the workgroups of a head are consecutive on one XCD (the
+    // dispatcher deals ids to the 8 XCDs round robin), so its K and V stay in
+    // that L2.  Split sp takes keys [sp kchunk, sp kchunk + Lk) of the head
+    // (without a split: all of them, kchunk >= LkAll).
     const int nwg = (int)gridDim.x;
     int id = (int)blockIdx.x;
     if ((nwg & 7) == 0) id = (id & 7) * (nwg >> 3) + (id >> 3);
-    const int bh = id / qblocks, qb = id - bh * qblocks;
+    const int per_head = qblocks * nsplit;
+    const int bh = id / per_head, rem = id - bh * per_head;
+    const int qb = rem / nsplit, sp = rem - qb * nsplit;
+    const int kbeg = sp * kchunk;
+    const int Lk = min(kchunk, LkAll - kbeg);
     const int q0 = qb * G::ROWS;
     const T* Qh = Qg + (size_t)bh * Lq * D;
-    const T* Kh = Kg + (size_t)bh * Lk * D;
-    const T* Vh = Vg + (size_t)bh * Lk * D;
+    const T* Kh = Kg + ((size_t)bh * LkAll + kbeg) * D;
+    const T* Vh = Vg + ((size_t)bh * LkAll + kbeg) * D;
     constexpr int kOob = kBufOob;
 
     // ---- Q: this wave's RW rows as the B operand of S^T = K Q^T: lane
@@ -282,7 +290,8 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_flash(const T* __restrict__
             for (int i = 0; i < G::NLD; ++i) {
                 const int key = k0 + lrow + G::RSTEP * i;
                 if (key < Lk && lcol < D)
-                    kr[i] = apply_pe4<T, PEK>(kr[i], Kh + (size_t)key * D, key, lcol, D, pk, true);
+                    kr[i] = apply_pe4<T, PEK>(kr[i], Kh + (size_t)key * D, kbeg + key, lcol, D, pk,
+                                              true);
             }
         }
         float mk = 0.f, mv = 0.f;
@@ -553,27 +562,94 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_flash(const T* __restrict__
     }
 
     // ---- O = O^T uv / l (the sums' common unit cancels): stores of 4
-    // consecutive dims (16 bytes fp32, 8 bytes bf16 rounded to nearest even)
+    // consecutive dims (16 bytes fp32, 8 bytes bf16 rounded to nearest even).
+    // With a key split: this split's normalized output in fp32 and its
+    // statistics (running max, c0, log2 of the sum in units of 2^(c0 m)),
+    // which k_flash_combine weighs.
     const float l = xgroup_sum<RW>(l_run);
     const float inv = uv_prev / l;
     if (qrow < Lq) {
-        T* orow = Og + ((size_t)bh * Lq + qrow) * D;
+        if (nsplit == 1) {
+            T* orow = Og + ((size_t)bh * Lq + qrow) * D;
 #pragma unroll
-        for (int dt = 0; dt < G::NDT; ++dt)
+            for (int dt = 0; dt < G::NDT; ++dt)
 #pragma unroll
-            for (int r = 0; r < G::SPT; r += 4) {
-                const int d = G::MT * dt + 8 * (r >> 2) + 4 * lg;
-                if (d < D)
-                    Elem<T>::st4(orow, d,
-                                 make_float4(o[dt][r] * inv, o[dt][r + 1] * inv,
-                                             o[dt][r + 2] * inv, o[dt][r + 3] * inv));
-            }
+                for (int r = 0; r < G::SPT; r += 4) {
+                    const int d = G::MT * dt + 8 * (r >> 2) + 4 * lg;
+                    if (d < D)
+                        Elem<T>::st4(orow, d,
+                                     make_float4(o[dt][r] * inv, o[dt][r + 1] * inv,
+                                                 o[dt][r + 2] * inv, o[dt][r + 3] * inv));
+                }
+        } else {
+            const size_t prow = (size_t)(bh * nsplit + sp) * Lq + qrow;
+            float* orow = part + prow * D;
+#pragma unroll
+            for (int dt = 0; dt < G::NDT; ++dt)
+#pragma unroll
+                for (int r = 0; r < G::SPT; r += 4) {
+                    const int d = G::MT * dt + 8 * (r >> 2) + 4 * lg;
+                    if (d < D)
+                        *reinterpret_cast<float4*>(orow + d) =
+                            make_float4(o[dt][r] * inv, o[dt][r + 1] * inv, o[dt][r + 2] * inv,
+                                        o[dt][r + 3] * inv);
+                }
+            if (lg == 0) stats[prow] = make_float4(m_run, c0, __log2f(l) - 8.f, 0.f);
+        }
     }
 }
 
+// Merges the key splits of k_flash: for each (head, query) row, split s
+// holds its normalized output O_s and statistics (m_s, c0, g_s) with
+// log2 of its weight sum = c0 m_s + g_s (c0 is the same for every split of
+// a row: the query's scale does not depend on the keys).  O = sum w_s O_s /
+// sum w_s with w_s = 2^((m_s - M) c0 + g_s), M = max m_s (differences of the
+// maxima first, so that huge logits stay exact).  One thread per 4 dims,
+// 4 rows per workgroup.
+template <typename T>
+__global__ __launch_bounds__(256) void k_flash_combine(const float* __restrict__ part,
+                                                       const float4* __restrict__ stats,
+                                                       T* __restrict__ Og, int Lq, int D,
+                                                       int nsplit, int rows) {
+    const int t = threadIdx.x;
+    const int row = blockIdx.x * 4 + (t >> 6), d = 4 * (t & 63);
+    if (row >= rows || d >= D) return;
+    const int bh = row / Lq, q = row - bh * Lq;
+    const size_t base = (size_t)bh * nsplit * Lq + q;
+    float M = -INFINITY;
+    for (int s = 0; s < nsplit; ++s) M = fmaxf(M, stats[base + (size_t)s * Lq].x);
+    float wsum = 0.f;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int s = 0; s < nsplit; ++s) {
+        const size_t pr = base + (size_t)s * Lq;
+        const float4 st = stats[pr];
+        const float w = __builtin_amdgcn_exp2f(fmaf(st.x - M, st.y, st.z));
+        const float4 v = *reinterpret_cast<const float4*>(part + pr * D + d);
+        wsum += w;
+        acc.x = fmaf(w, v.x, acc.x);
+        acc.y = fmaf(w, v.y, acc.y);
+        acc.z = fmaf(w, v.z, acc.z);
+        acc.w = fmaf(w, v.w, acc.w);
+    }
+    const float inv = 1.f / wsum;
+    Elem<T>::st4(Og + (size_t)row * D, d,
+                 make_float4(acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv));
+}
+
+// the arguments of one flash call (pointers typed by the launch)
+struct FlashArgs {
+    const void *Q, *K, *V;
+    void* O;
+    int BH, Lq, Lk, D;
+    float scale;
+    PeSide pq, pk;
+    int nsplit, kchunk;
+    float* part;
+    float4* stats;
+};
+
 template <typename T, int DP, int PEK, int NW, int RW>
-hipError_t launch_t(const T* Q, const T* K, const T* V, T* O, int BH, int Lq, int Lk, int D,
-                    float scale, const PeSide& pq, const PeSide& pk, hipStream_t st) {
+hipError_t launch_t(const FlashArgs& a, hipStream_t st) {
     using G = FlashGeo<DP, PEK != kPeNone, NW, RW, sizeof(T) == 4>;
     static bool attr = false;
     if (!attr) {
@@ -582,66 +658,54 @@ hipError_t launch_t(const T* Q, const T* K, const T* V, T* O, int BH, int Lq, in
         if (e != hipSuccess) return e;
         attr = true;
     }
-    const int qblocks = (Lq + G::ROWS - 1) / G::ROWS;
-    hipLaunchKernelGGL((k_flash<T, DP, PEK, NW, RW>), dim3((unsigned)(BH * qblocks)),
-                       dim3(G::THREADS), G::BYTES, st, Q, K, V, O, Lq, Lk, D, qblocks, scale, pq,
-                       pk);
+    const int qblocks = (a.Lq + G::ROWS - 1) / G::ROWS;
+    const int kchunk = a.nsplit > 1 ? a.kchunk : a.Lk;
+    hipLaunchKernelGGL((k_flash<T, DP, PEK, NW, RW>), dim3((unsigned)(a.BH * qblocks * a.nsplit)),
+                       dim3(G::THREADS), G::BYTES, st, static_cast<const T*>(a.Q),
+                       static_cast<const T*>(a.K), static_cast<const T*>(a.V), static_cast<T*>(a.O),
+                       a.Lq, a.Lk, a.D, qblocks, a.scale, a.pq, a.pk, a.nsplit, kchunk, a.part,
+                       a.stats);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || a.nsplit == 1) return e;
+    const int rows = a.BH * a.Lq;
+    hipLaunchKernelGGL((k_flash_combine<T>), dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, st,
+                       a.part, a.stats, static_cast<T*>(a.O), a.Lq, a.D, a.nsplit, rows);
     return hipGetLastError();
 }
 
 // head dims padded to 32, 64, 128 (and 256 for 8 waves of 16 rows without
 // an encoding)
 template <typename T, int PEK, int NW, int RW>
-hipError_t launch_pe(const T* Q, const T* K, const T* V, T* O, int BH, int Lq, int Lk, int D,
-                     float scale, const PeSide& pq, const PeSide& pk, hipStream_t st) {
-    if (D <= 32) return launch_t<T, 32, PEK, NW, RW>(Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk, st);
-    if (D <= 64) return launch_t<T, 64, PEK, NW, RW>(Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk, st);
-    if (D <= 128)
-        return launch_t<T, 128, PEK, NW, RW>(Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk, st);
-    if constexpr (PEK == kPeNone && NW == 8 && RW == 16)
-        return launch_t<T, 256, PEK, NW, RW>(Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk, st);
+hipError_t launch_pe(const FlashArgs& a, hipStream_t st) {
+    if (a.D <= 32) return launch_t<T, 32, PEK, NW, RW>(a, st);
+    if (a.D <= 64) return launch_t<T, 64, PEK, NW, RW>(a, st);
+    if (a.D <= 128) return launch_t<T, 128, PEK, NW, RW>(a, st);
+    if constexpr (PEK == kPeNone && NW == 8 && RW == 16) return launch_t<T, 256, PEK, NW, RW>(a, st);
     return hipErrorInvalidValue;
 }
 
 template <typename T, int PEK>
-hipError_t launch_form(int form, const T* Q, const T* K, const T* V, T* O, int BH, int Lq, int Lk,
-                       int D, float scale, const PeSide& pq, const PeSide& pk, hipStream_t st) {
+hipError_t launch_form(int form, const FlashArgs& a, hipStream_t st) {
     // head dims past 128 run 8 waves of 16 rows: two buffers of a 256-wide
     // tile leave room for one workgroup per CU, and 32-row waves would not
     // hold the query's and the output's registers
-    if (D > 128) form = kFlashForm8x16;
+    if (a.D > 128) form = kFlashForm8x16;
     switch (form) {
-        case kFlashForm4x16:
-            return launch_pe<T, PEK, 4, 16>(Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk, st);
-        case kFlashForm8x16:
-            return launch_pe<T, PEK, 8, 16>(Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk, st);
-        case kFlashForm4x32:
-            return launch_pe<T, PEK, 4, 32>(Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk, st);
-        case kFlashForm8x32:
-            return launch_pe<T, PEK, 8, 32>(Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk, st);
+        case kFlashForm4x16: return launch_pe<T, PEK, 4, 16>(a, st);
+        case kFlashForm8x16: return launch_pe<T, PEK, 8, 16>(a, st);
+        case kFlashForm4x32: return launch_pe<T, PEK, 4, 32>(a, st);
+        case kFlashForm8x32: return launch_pe<T, PEK, 8, 32>(a, st);
         default: return hipErrorInvalidValue;
     }
 }
 
 template <typename T>
-hipError_t launch_typed(int pek, int form, const void* Q, const void* K, const void* V, void* O,
-                        int BH, int Lq, int Lk, int D, float scale, const PeSide& pq,
-                        const PeSide& pk, hipStream_t st) {
-    const T* q = static_cast<const T*>(Q);
-    const T* k = static_cast<const T*>(K);
-    const T* v = static_cast<const T*>(V);
-    T* o = static_cast<T*>(O);
+hipError_t launch_typed(int pek, int form, const FlashArgs& a, hipStream_t st) {
     switch (pek) {
-        case kPeNone:
-            return launch_form<T, kPeNone>(form, q, k, v, o, BH, Lq, Lk, D, scale, pq, pk, st);
-        case kPeRopeInterleaved:
-            return launch_form<T, kPeRopeInterleaved>(form, q, k, v, o, BH, Lq, Lk, D, scale, pq,
-                                                      pk, st);
-        case kPeRopeHalf:
-            return launch_form<T, kPeRopeHalf>(form, q, k, v, o, BH, Lq, Lk, D, scale, pq, pk, st);
-        case kPeSinusoidal:
-            return launch_form<T, kPeSinusoidal>(form, q, k, v, o, BH, Lq, Lk, D, scale, pq, pk,
-                                                 st);
+        case kPeNone: return launch_form<T, kPeNone>(form, a, st);
+        case kPeRopeInterleaved: return launch_form<T, kPeRopeInterleaved>(form, a, st);
+        case kPeRopeHalf: return launch_form<T, kPeRopeHalf>(form, a, st);
+        case kPeSinusoidal: return launch_form<T, kPeSinusoidal>(form, a, st);
         default: return hipErrorInvalidValue;
     }
 }
@@ -655,11 +719,14 @@ bool flash_supported(int dtype, int pek, int D) {
 
 hipError_t launch_flash(int dtype, int pek, int form, const void* Q, const void* K, const void* V,
                         void* O, int BH, int Lq, int Lk, int D, float scale, const PeSide& pq,
-                        const PeSide& pk, hipStream_t st) {
-    if (dtype == kDtypeF32)
-        return launch_typed<float>(pek, form, Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk, st);
-    if (dtype == kDtypeBF16)
-        return launch_typed<uint16_t>(pek, form, Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk, st);
+                        const PeSide& pk, int nsplit, int kchunk, float* part, hipStream_t st) {
+    if (nsplit < 1 || (nsplit > 1 && (part == nullptr || kchunk < 1 ||
+                                      (long long)kchunk * (nsplit - 1) >= Lk)))
+        return hipErrorInvalidValue;
+    FlashArgs a{Q, K, V, O, BH, Lq, Lk, D, scale, pq, pk, nsplit, kchunk, part,
+                reinterpret_cast<float4*>(part + (size_t)nsplit * BH * Lq * D)};
+    if (dtype == kDtypeF32) return launch_typed<float>(pek, form, a, st);
+    if (dtype == kDtypeBF16) return launch_typed<uint16_t>(pek, form, a, st);
     return hipErrorInvalidValue;
 }
 

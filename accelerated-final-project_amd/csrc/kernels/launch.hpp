@@ -90,10 +90,14 @@ hipError_t launch_gemm_pv(const uint16_t* E, int ldE, float* st_m, float* st_l, 
 // of 32 (head_d <= 128; past 128 every form runs 8 of 16).
 constexpr int kFlashMaxD = 256, kFlashMaxDEncoded = 128;
 constexpr int kFlashForm4x16 = 1, kFlashForm8x16 = 2, kFlashForm4x32 = 3, kFlashForm8x32 = 4;
+// Key split (nsplit > 1): workgroup split s takes keys [s kchunk, (s + 1)
+// kchunk) and writes its normalized output and statistics to `part`
+// (nsplit BH Lq D floats, then nsplit BH Lq float4s; 16-byte aligned), which
+// a second kernel merges into O.  nsplit == 1: no scratch (part unused).
 bool flash_supported(int dtype, int pek, int D);
 hipError_t launch_flash(int dtype, int pek, int form, const void* Q, const void* K, const void* V,
                         void* O, int BH, int Lq, int Lk, int D, float scale, const PeSide& pq,
-                        const PeSide& pk, hipStream_t st);
+                        const PeSide& pk, int nsplit, int kchunk, float* part, hipStream_t st);
 
 // Allocation-free entry point: the per-device scratch array (noalloc.hip),
 // kNoAllocScratchBytes long.  noalloc_scratch() returns its device address

@@ -340,6 +340,10 @@ typedef struct atn_tuning {
                               that output tile (128 where both of its sides reach
                               128); 0: 128 x 128 where that grid gives every CU two
                               workgroups, else 64 x 64 */
+    int flash_split;       /* flash kernel key splits: 1 never split, n >= 2 split the keys
+                              into n parts (fewer for short key lengths: two 64-key chunks
+                              at least per part); 0: the library's choice (splits where
+                              the grid would leave CUs idle) */
 } atn_tuning;
 /* Replaces the overrides (NULL: all zero) and drops cached plans.  Plans
  * that a forced setting makes impossible fall back to the library's

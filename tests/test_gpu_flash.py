@@ -496,3 +496,130 @@ def test_flash_bf16_graph_replays(am, dev):
     n, nrel, mabs = H.check_bf16(eager.numpy(), oracle.attention(Q, K, V, nthreads=16))
     assert n == 0, (nrel, mabs)
     st.destroy()
+
+
+# ---------------------------------------------------------------- key splits
+# A grid of few (head, query block) pairs leaves CUs idle: such calls split
+# the keys into parts (whole 64-key chunks, two at least per part), each
+# part writes its normalized output and statistics, and a second kernel
+# merges them (weights 2^((m_s - M) c0 + g_s), maxima subtracted first).
+
+
+def _call(am, dt, Q, K, V, desc=None):
+    return _f32_call(am, Q, K, V, desc) if dt == "f32" else _bf16_call(am, Q, K, V, desc)
+
+
+def _check(dt, got, ref):
+    if dt == "f32":
+        n, mabs, _ = H.check_f32(got, ref)
+        return n, mabs
+    n, nrel, mabs = H.check_bf16(got, ref)
+    return n, (nrel, mabs)
+
+
+@pytest.mark.parametrize("dt,shape", [("f32", (1, 4, 2048, 2048, 128)), ("bf16", (1, 4, 2048, 2048, 128)),
+                                      ("bf16", (1, 32, 16, 4096, 128)), ("f32", (1, 8, 1, 3000, 64)),
+                                      ("f32", (2, 2, 100, 5000, 256)), ("bf16", (1, 1, 200, 700, 252))],
+                         ids=lambda v: "x".join(map(str, v)) if isinstance(v, tuple) else v)
+def test_flash_split_auto(am, dev, dt, shape):
+    """Shapes whose grid leaves CUs idle take key splits by themselves;
+    against the oracle and against the same call with splits turned off."""
+    B, Hh, Lq, Lk, D = shape
+    print(f"[case] flash split auto {dt} {shape}", flush=True)
+    code = 0 if dt == "f32" else 1
+    assert am.path(code, B, Hh, Lq, Lk, D) == am.ATN_PATH_FLASH
+    Q, K, V = H.rng_inputs((B, Hh, Lq, D), (B, Hh, Lk, D), seed=4000 + Lk + D)
+    if dt == "bf16":
+        Q, K, V = _bf16(Q), _bf16(K), _bf16(V)
+    got = _call(am, dt, Q, K, V)
+    n, info = _check(dt, got, oracle.attention(Q, K, V, nthreads=16))
+    assert n == 0, info
+    am.set_tuning(flash_split=1)
+    try:
+        whole = _call(am, dt, Q, K, V)
+    finally:
+        am.set_tuning()
+    n, info = _check(dt, got, whole)
+    assert n == 0, info
+
+
+@pytest.mark.parametrize("nsplit", [2, 3, 7])
+@pytest.mark.parametrize("dt,pe,form", [("f32", None, "8x16"), ("bf16", None, "8x32"),
+                                        ("f32", "rope", "4x16"), ("bf16", "rope_half", "8x16"),
+                                        ("bf16", "sinusoidal", "4x32"), ("f32", "sinusoidal", "8x32")])
+def test_flash_split_forced(am, dev, tuner, nsplit, dt, pe, form):
+    """Forced split counts on ragged key lengths (the last part short), every
+    form, with encodings (a part's keys keep their own positions)."""
+    tuner.set(flash_split=nsplit, flash_form=form)
+    desc = {None: None, "rope": am.make_pe("rope"), "rope_half": am.make_pe("rope", pairing="half"),
+            "sinusoidal": am.make_pe("sinusoidal")}[pe]
+    for (B, Hh, Lq, Lk, D) in ((1, 2, 70, 200, 64), (1, 3, 130, 1000, 128), (2, 1, 33, 450, 32)):
+        print(f"[case] flash split {nsplit} {dt} {pe} {form} {(B, Hh, Lq, Lk, D)}", flush=True)
+        Q, K, V = H.rng_inputs((B, Hh, Lq, D), (B, Hh, Lk, D), seed=nsplit * 100 + Lk,
+                               sigma=0.5 if pe == "sinusoidal" else 1.0)
+        if dt == "bf16":
+            Q, K, V = _bf16(Q), _bf16(K), _bf16(V)
+        got = _call(am, dt, Q, K, V, desc)
+        n, info = _check(dt, got, _ref(pe, Q, K, V))
+        assert n == 0, (Lk, info)
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+def test_flash_split_huge_logits_and_nonfinite(am, dev, tuner, dt):
+    """Splits merged with their maxima subtracted first: logits near 2^40
+    (head 1) match the oracle; an infinite query element makes its row
+    non-finite and a NaN value element its column NaN, the rest keeps the
+    bar."""
+    tuner.set(flash_split=4)
+    B, Hh, Lq, Lk, D = 1, 3, 100, 900, 128
+    print(f"[case] flash split huge logits {dt}", flush=True)
+    Q, K, V = H.rng_inputs((B, Hh, Lq, D), (B, Hh, Lk, D), seed=87)
+    if dt == "bf16":
+        Q, K, V = _bf16(Q), _bf16(K), _bf16(V)
+    Q[:, 1] *= np.float32(2.0 ** 30)
+    K[:, 1] *= np.float32(2.0 ** 10)
+    got = _call(am, dt, Q, K, V)
+    n, info = _check(dt, got, oracle.attention(Q, K, V, nthreads=16))
+    assert n == 0, info
+    Q[0, 2, 5, 7] = np.inf
+    V[0, 0, 600, 9] = np.nan
+    got = _call(am, dt, Q, K, V)
+    ref = oracle.attention(Q, K, V, nthreads=16)
+    assert not np.isfinite(got[0, 2, 5]).any() and np.isnan(got[0, 0, :, 9]).all()
+    keep = np.ones((Hh, Lq, D), dtype=bool)
+    keep[2, 5, :] = False
+    keep[0, :, 9] = False
+    n, info = _check(dt, got[0][keep], ref[0][keep])
+    assert n == 0, info
+
+
+def test_flash_split_graph_replays(am, dev):
+    """A captured graph of split calls (parts in the stream's workspace)
+    replayed with eager calls between: every replay equals the eager result
+    bit for bit."""
+    import hip_rt
+    B, Hh, Lq, Lk, D = 1, 2, 300, 3000, 128
+    print("[case] flash split graph replay", flush=True)
+    assert am.workspace_bytes(1, B, Hh, Lq, Lk, D) > 40960  # the parts need scratch
+    (q, k, v), (Q, K, V) = H.device_inputs((B, Hh, Lq, D), (B, Hh, Lk, D), 99, "bf16")
+    st = hip_rt.Stream()
+    eager = H.empty(Q.shape, "bf16")
+    am.attention_ex(q, k, v, eager, stream=st)
+    st.synchronize()
+    ref = eager.bits()
+    outs = [H.empty(Q.shape, "bf16") for _ in range(2)]
+    g = hip_rt.Graph(st, lambda: [am.attention_ex(q, k, v, o, stream=st) for o in outs])
+    for _ in range(3):
+        for o in outs:
+            o.fill_nan()
+        hip_rt.synchronize()
+        g.launch()
+        st.synchronize()
+        for o in outs:
+            assert np.array_equal(o.bits(), ref)
+        am.attention_ex(q, k, v, eager, stream=st)
+        st.synchronize()
+    g.destroy()
+    n, nrel, mabs = H.check_bf16(eager.numpy(), oracle.attention(Q, K, V, nthreads=16))
+    assert n == 0, (nrel, mabs)
+    st.destroy()

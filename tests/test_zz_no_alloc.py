@@ -42,8 +42,10 @@ def _pair(am, shape, dtype, pe, seed):
     ((1, 2, 300, 200, 260), (1, 1, 70, 90, 22), "f32", None),          # split-D pipeline
     ((1, 2, 300, 200, 36), (1, 1, 70, 90, 20), "f32", None),           # flash kernel
     ((1, 2, 300, 200, 128), (1, 1, 70, 90, 64), "bf16", "rope_half"),  # flash kernel, bf16
+    ((1, 4, 1024, 2048, 128), (1, 2, 16, 1000, 64), "bf16", None),      # flash, key splits
     ((2, 2, 256, 512, 256), (1, 2, 128, 128, 256), "bf16", "sinusoidal"),  # GEMM path
-], ids=["fused-f32", "fused-bf16", "gemm-rope", "splitd", "flash", "flash-bf16", "gemm-sin"])
+], ids=["fused-f32", "fused-bf16", "gemm-rope", "splitd", "flash", "flash-bf16", "flash-split",
+        "gemm-sin"])
 def test_noalloc_matches_ex_two_calls(am, dev, first, second, dtype, pe):
     desc = None
     if pe == "rope_half":
