@@ -765,11 +765,15 @@ bool flash_ok(int dtype, const Shape& s, const PePlan& plan) {
 // workgroup; else 8 waves of 16 rows (twice the workgroups).  Measured
 // with interleaved rounds on 14 shapes: the reference's (4,32,512,512,128)
 // 70.6 -> 62.9 us, RoPE there 108 -> 86 us; below a workgroup per CU the
-// 32-row form loses (up to 1.6x at (1,4,2048,2048,128)).
+// 32-row form loses (up to 1.6x at (1,4,2048,2048,128)).  Up to 64 query
+// rows, 4 waves of 16 rows (64-row blocks: no wave of padding rows; with key
+// splits, same box: (1,32,16,4096,128) bf16 33.2 -> 29.6 us, (1,8,64,4096,
+// 128) fp32 35.7 -> 33.8 us).
 int flash_form(const Shape& s, int dev) {
     const int forced = tune().flash_form;
     if (forced >= atn::kFlashForm4x16 && forced <= atn::kFlashForm8x32) return forced;
     if (s.D > 128) return atn::kFlashForm8x16;
+    if (s.Lq <= 64) return atn::kFlashForm4x16;
     int cus = 0;
     {
         std::lock_guard<std::mutex> lk(g_mu);
