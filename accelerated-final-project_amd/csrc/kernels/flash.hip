@@ -302,18 +302,33 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_flash(const T* __restrict__
             mv = vmax3abs(mv, vr[i].x, vr[i].y);
             mv = vmax3abs(mv, vr[i].z, vr[i].w);
         }
-        mk = wave_max_rows(mk);
-        mv = wave_max_rows(mv);
-        if (!(mk < INFINITY) || !(mv < INFINITY)) {  // the same in every lane
-            mk = 0.f;
-            mv = 0.f;
-#pragma unroll
-            for (int i = 0; i < G::NLD; ++i) {
-                mk = max_finite4(mk, kr[i]);
-                mv = max_finite4(mv, vr[i]);
-            }
+        // Usually ballots settle it with no reduction: a wave whose K values
+        // all lie below kF16Range and some at 2^-3 or above (V likewise; fp32
+        // V: below kF16Range only) reports the sentinel 1, a value of that
+        // range, so the workgroup maximum over the slots is in range exactly
+        // when the true one is, and when a wave lies beyond the range its own
+        // (reduced) maximum still decides the scale.  Other waves reduce.
+        const bool k_ok = !__builtin_amdgcn_ballot_w64(!(mk < kF16Range)) &&
+                          __builtin_amdgcn_ballot_w64(mk >= 0.125f) != 0;
+        const bool v_ok = !__builtin_amdgcn_ballot_w64(!(mv < kF16Range)) &&
+                          (!kBf || __builtin_amdgcn_ballot_w64(mv >= 0.125f) != 0);
+        if (k_ok && v_ok) {
+            mk = 1.f;
+            mv = 1.f;
+        } else {
             mk = wave_max_rows(mk);
             mv = wave_max_rows(mv);
+            if (!(mk < INFINITY) || !(mv < INFINITY)) {  // the same in every lane
+                mk = 0.f;
+                mv = 0.f;
+#pragma unroll
+                for (int i = 0; i < G::NLD; ++i) {
+                    mk = max_finite4(mk, kr[i]);
+                    mv = max_finite4(mv, vr[i]);
+                }
+                mk = wave_max_rows(mk);
+                mv = wave_max_rows(mv);
+            }
         }
         if (lane == 0) {
             slot[par][wave] = mk;
@@ -510,12 +525,18 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_flash(const T* __restrict__
                 const int i0 = 8 * b + e, i1 = i0 + 1;
                 const float p0 = __builtin_amdgcn_exp2f(fmaf(s[i0 / G::SPT][i0 % G::SPT], cx, nm));
                 const float p1 = __builtin_amdgcn_exp2f(fmaf(s[i1 / G::SPT][i1 % G::SPT], cx, nm));
-                ps += p0;
-                ps += p1;
-                if constexpr (kBf)
-                    h[e / 2] = l[e / 2] = pk_f16_rne(p0, p1);  // one part (lo unused)
-                else
+                if constexpr (kBf) {
+                    // one part (lo unused); the sum takes the rounded values
+                    // the product takes, two per v_dot2_f32_f16
+                    h[e / 2] = l[e / 2] = pk_f16_rne(p0, p1);
+                    const f16x2 one2 = {(_Float16)1.f, (_Float16)1.f};
+                    ps = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, h[e / 2]), one2, ps,
+                                                false);
+                } else {
+                    ps += p0;
+                    ps += p1;
                     split2_f16_one(p0, p1, one, h[e / 2], l[e / 2]);
+                }
             }
             ph[b] = __builtin_bit_cast(f16x8, make_uint4(h[0], h[1], h[2], h[3]));
             pl[b] = __builtin_bit_cast(f16x8, make_uint4(l[0], l[1], l[2], l[3]));
