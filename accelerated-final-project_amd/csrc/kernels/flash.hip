@@ -155,18 +155,38 @@ __device__ __forceinline__ uint32_t pk_f16_rne(float a, float b) {
     return __builtin_bit_cast(uint32_t, h);
 }
 
-// the form's MFMA: 16 x 16 x 32 or 32 x 32 x 16, fp16 operands, fp32 sums
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+// the form's MFMA: 16 x 16 x 32 or 32 x 32 x 16, fp16 or bf16 operands,
+// fp32 sums
 __device__ __forceinline__ v4f mfma_rw(const f16x8& a, const f16x8& b, const v4f& c) {
     return mfma_f16(a, b, c);
 }
 __device__ __forceinline__ v16f mfma_rw(const f16x8& a, const f16x8& b, const v16f& c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
+__device__ __forceinline__ v4f mfma_rw(const bf16x8_t& a, const bf16x8_t& b, const v4f& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ v16f mfma_rw(const bf16x8_t& a, const bf16x8_t& b, const v16f& c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// two values as bf16, rounded to nearest even (v_cvt_pk_bf16_f32), packed
+__device__ __forceinline__ uint32_t pk_bf16_rne(float a, float b) {
+    const f32x2_t v = {a, b};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
+}
 
 // T = float: fp32 inputs as hi + lo fp16 parts, three products each; T =
-// uint16_t: bf16 inputs (bf16 bits), exact in fp16 within its range (a
-// power-of-two scale per tile brings K and V there), one product each, P as
-// one fp16 part, the output rounded to bf16.
+// uint16_t: bf16 inputs (bf16 bits), one product each, the output rounded to
+// bf16 -- without an encoding ("raw") the loaded bits go to LDS as they are
+// and the products run on the bf16 MFMA (exact products, fp32's exponent
+// range: no scales, no tile maxima), P as bf16; with an encoding the
+// encoded values are fp32, staged as one fp16 part each (a power-of-two
+// scale per tile brings K and V into fp16's normal range), P as fp16.
 template <typename T, int DP, int PEK, int NW, int RW>
 __global__ __launch_bounds__(64 * NW, 8 / NW) void k_flash(const T* __restrict__ Qg,
                                                              const T* __restrict__ Kg,
@@ -177,7 +197,9 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_flash(const T* __restrict__
                                                              int kchunk, float* __restrict__ part,
                                                              float4* __restrict__ stats) {
     constexpr bool kBf = sizeof(T) == 2;
+    constexpr bool kRaw = kBf && PEK == kPeNone;
     constexpr int es = (int)sizeof(T);
+    typedef std::conditional_t<kRaw, bf16x8_t, f16x8> op_t;  // MFMA operands
     using G = FlashGeo<DP, PEK != kPeNone, NW, RW, !kBf>;
     typedef std::conditional_t<RW == 16, v4f, v16f> acc_t;
     extern __shared__ __align__(16) unsigned char smem_raw[];
@@ -213,9 +235,23 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_flash(const T* __restrict__
     // (query lr, group lg) holds dims KD ks + 8 lg + 0..7, scaled by a
     // power of two from the wave's largest finite magnitude
     const int qrow = q0 + RW * wave + lr;
-    f16x8 qh[G::KS], ql[G::KS];
-    float uq;
-    {
+    op_t qh[G::KS];
+    f16x8 ql[G::KS];
+    float uq = 1.f;
+    if constexpr (kRaw) {
+        // the bf16 bits as they are (8 bytes per 4 dims; dims past D and rows
+        // past Lq read as zeros)
+        const __amdgpu_buffer_rsrc_t rq = buf_rsrc(Qh, Lq * D * es);
+#pragma unroll
+        for (int ks = 0; ks < G::KS; ++ks) {
+            const int d = G::KD * ks + 8 * lg;
+            const auto a = __builtin_amdgcn_raw_buffer_load_b64(rq, d < D ? (qrow * D + d) * 2 : kOob,
+                                                                0, 0);
+            const auto b = __builtin_amdgcn_raw_buffer_load_b64(
+                rq, d + 4 < D ? (qrow * D + d + 4) * 2 : kOob, 0, 0);
+            qh[ks] = __builtin_bit_cast(op_t, make_uint4(a[0], a[1], b[0], b[1]));
+        }
+    } else {
         float4 qv[G::KS][2];
         float mq = 0.f;
         const __amdgpu_buffer_rsrc_t rq = buf_rsrc(Qh, Lq * D * es);
@@ -244,15 +280,14 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_flash(const T* __restrict__
                 h[1] = pk_f16_rne(qv[ks][0].z * sq, qv[ks][0].w * sq);
                 h[2] = pk_f16_rne(qv[ks][1].x * sq, qv[ks][1].y * sq);
                 h[3] = pk_f16_rne(qv[ks][1].z * sq, qv[ks][1].w * sq);
-                qh[ks] = __builtin_bit_cast(f16x8, make_uint4(h[0], h[1], h[2], h[3]));
-                ql[ks] = qh[ks];  // (unused)
+                qh[ks] = __builtin_bit_cast(op_t, make_uint4(h[0], h[1], h[2], h[3]));
                 continue;
             }
             split2_f16(qv[ks][0].x * sq, qv[ks][0].y * sq, h[0], l[0]);
             split2_f16(qv[ks][0].z * sq, qv[ks][0].w * sq, h[1], l[1]);
             split2_f16(qv[ks][1].x * sq, qv[ks][1].y * sq, h[2], l[2]);
             split2_f16(qv[ks][1].z * sq, qv[ks][1].w * sq, h[3], l[3]);
-            qh[ks] = __builtin_bit_cast(f16x8, make_uint4(h[0], h[1], h[2], h[3]));
+            qh[ks] = __builtin_bit_cast(op_t, make_uint4(h[0], h[1], h[2], h[3]));
             ql[ks] = __builtin_bit_cast(f16x8, make_uint4(l[0], l[1], l[2], l[3]));
         }
     }
@@ -270,13 +305,21 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_flash(const T* __restrict__
     const __amdgpu_buffer_rsrc_t rk = buf_rsrc(Kh, Lk * D * es);
     const __amdgpu_buffer_rsrc_t rv = buf_rsrc(Vh, Lk * D * es);
     float4 kr[G::NLD], vr[G::NLD];
+    uint2 kw[G::NLD], vw[G::NLD];  // raw bf16: the loaded bits
     auto issue = [&](int k0) {
 #pragma unroll
         for (int i = 0; i < G::NLD; ++i) {
             const int key = k0 + lrow + G::RSTEP * i;
             const int off = key < Lk && lcol < D ? (key * D + lcol) * es : kOob;
-            kr[i] = ld4_t<T>(rk, off);
-            vr[i] = ld4_t<T>(rv, off);
+            if constexpr (kRaw) {
+                const auto a = __builtin_amdgcn_raw_buffer_load_b64(rk, off, 0, 0);
+                const auto b = __builtin_amdgcn_raw_buffer_load_b64(rv, off, 0, 0);
+                kw[i] = make_uint2(a[0], a[1]);
+                vw[i] = make_uint2(b[0], b[1]);
+            } else {
+                kr[i] = ld4_t<T>(rk, off);
+                vr[i] = ld4_t<T>(rv, off);
+            }
         }
     };
     // K's encoding, then the per-wave maxima of the tile's K and V
@@ -285,6 +328,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_flash(const T* __restrict__
     // stay so through a scaling and must not set the scale of the finite
     // values beside them.
     auto maxima = [&](int k0, int par) {
+        if constexpr (kRaw) return;  // no scales
         if constexpr (PEK != kPeNone) {
 #pragma unroll
             for (int i = 0; i < G::NLD; ++i) {
@@ -342,6 +386,17 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_flash(const T* __restrict__
     // range, and for fp32 scaled only beyond fp16's range), and its hi + lo
     // (fp32) or hi (bf16) fp16 parts into LDS buffer par
     auto stage = [&](int par, float& uk, float& sv, float& uv) {
+        if constexpr (kRaw) {
+            uk = sv = uv = 1.f;
+            uint16_t* buf = smem + par * G::TILE;
+#pragma unroll
+            for (int i = 0; i < G::NLD; ++i) {
+                const int row = lrow + G::RSTEP * i;
+                *reinterpret_cast<uint2*>(buf + G::K_HI + row * G::KSTR + lcol) = kw[i];
+                *reinterpret_cast<uint2*>(buf + G::V_HI + row * G::VSTR + lcol) = vw[i];
+            }
+            return;
+        }
         float mk = slot[par][0], mv = slot[par][NW];
 #pragma unroll
         for (int w = 1; w < NW; ++w) {
@@ -443,11 +498,12 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_flash(const T* __restrict__
         // instead of each read being waited for before its product)
 #pragma unroll
         for (int ks = 0; ks < G::KS; ++ks) {
-            f16x8 ah[G::NJ], al[G::NJ];
+            op_t ah[G::NJ];
+            f16x8 al[G::NJ];
 #pragma unroll
             for (int j = 0; j < G::NJ; ++j) {
                 const int a = (G::MT * j + lr) * G::KSTR + G::KD * ks + 8 * lg;
-                ah[j] = lds8_f16(buf + G::K_HI + a);
+                ah[j] = __builtin_bit_cast(op_t, lds8_f16(buf + G::K_HI + a));
                 if constexpr (!kBf) al[j] = lds8_f16(buf + G::K_LO + a);
             }
 #pragma unroll
@@ -516,7 +572,8 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_flash(const T* __restrict__
         // tile 2b + 1, i.e. keys 4 lg + 0..3, 16 + 4 lg + 0..3 of the 32-key
         // block; RW = 32: registers 8 (b % 2) + 0..7 of tile b / 2, i.e.
         // keys 4 lg + 0..3, 8 + 4 lg + 0..3 of the 16-key block)
-        f16x8 ph[G::NB], pl[G::NB];
+        op_t ph[G::NB];
+        f16x8 pl[G::NB];
 #pragma unroll
         for (int b = 0; b < G::NB; ++b) {
             uint32_t h[4], l[4];
@@ -525,7 +582,14 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_flash(const T* __restrict__
                 const int i0 = 8 * b + e, i1 = i0 + 1;
                 const float p0 = __builtin_amdgcn_exp2f(fmaf(s[i0 / G::SPT][i0 % G::SPT], cx, nm));
                 const float p1 = __builtin_amdgcn_exp2f(fmaf(s[i1 / G::SPT][i1 % G::SPT], cx, nm));
-                if constexpr (kBf) {
+                if constexpr (kRaw) {
+                    // P as bf16 (the operand type of the raw products), the sum
+                    // from the same rounded values
+                    h[e / 2] = l[e / 2] = pk_bf16_rne(p0, p1);
+                    const bf16x2_t one2 = {(__bf16)1.f, (__bf16)1.f};
+                    ps = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, h[e / 2]),
+                                                         one2, ps, false);
+                } else if constexpr (kBf) {
                     // one part (lo unused); the sum takes the rounded values
                     // the product takes, two per v_dot2_f32_f16
                     h[e / 2] = l[e / 2] = pk_f16_rne(p0, p1);
@@ -538,7 +602,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_flash(const T* __restrict__
                     split2_f16_one(p0, p1, one, h[e / 2], l[e / 2]);
                 }
             }
-            ph[b] = __builtin_bit_cast(f16x8, make_uint4(h[0], h[1], h[2], h[3]));
+            ph[b] = __builtin_bit_cast(op_t, make_uint4(h[0], h[1], h[2], h[3]));
             pl[b] = __builtin_bit_cast(f16x8, make_uint4(l[0], l[1], l[2], l[3]));
         }
         l_run = l_run * alpha + ps;  // this lane's keys; summed over lane groups at the end
@@ -565,7 +629,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_flash(const T* __restrict__
                 constexpr int half = G::KD / 2 * G::VSTR;
                 const uint2 h0 = lds_tr16(buf + G::V_HI + a);
                 const uint2 h1 = lds_tr16(buf + G::V_HI + a + half);
-                const f16x8 vh = __builtin_bit_cast(f16x8, make_uint4(h0.x, h0.y, h1.x, h1.y));
+                const op_t vh = __builtin_bit_cast(op_t, make_uint4(h0.x, h0.y, h1.x, h1.y));
                 o[dt] = mfma_rw(vh, ph[b], o[dt]);
                 if constexpr (!kBf) {
                     const uint2 l0 = lds_tr16(buf + G::V_LO + a);
