@@ -745,17 +745,16 @@ size_t library_cap() {
 // The flash kernel takes fp32 and bf16 calls with head_d <= 256 (128 with
 // an encoding), head_d % 4 == 0 and 16-byte aligned bases (checked by the
 // caller), whose per-head Q and K/V byte offsets fit 32 bits.  bf16 calls
-// past head_d 128 take the GEMM path where it runs: its 256 x 256 tiles
-// reuse each operand over more products than the flash kernel's 64-key
-// tiles (measured: (4,32,512,512,256) 62 us there, 78 us here; at head_d
-// 128 the flash kernel leads, (4,32,512,512,128) 36 us against 56 us).
+// with an encoding past head_d 128 therefore take the GEMM path.  Without
+// one the flash kernel's bf16 products run on the raw bits, and at head_d
+// 256 it ties or beats the GEMM path (same box, flash at head_d 252 against
+// the GEMM path at 256: (4,32,512,512) 64.0 / 64.4 us, (2,16,1024,1024)
+// 54.6 / 66.9 us, (1,8,4096,4096) 165 / 315 us).
 bool flash_ok(int dtype, const Shape& s, const PePlan& plan) {
     const int64_t lim = (int64_t)1 << 31;
     const int64_t es = dtype == ATN_DTYPE_F32 ? 4 : 2;
-    if (plan.no_flash || !atn::flash_supported(dtype, plan.pek, s.D) ||
-        (int64_t)s.Lq * s.D * es >= lim || (int64_t)s.Lk * s.D * es >= lim)
-        return false;
-    return dtype == ATN_DTYPE_F32 || s.D <= 128 || !gemm_plan(dtype, s, plan).ok;
+    return !plan.no_flash && atn::flash_supported(dtype, plan.pek, s.D) &&
+           (int64_t)s.Lq * s.D * es < lim && (int64_t)s.Lk * s.D * es < lim;
 }
 
 // The flash kernel's workgroup form (atn_tuning.flash_form forces one).

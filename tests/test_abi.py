@@ -160,14 +160,14 @@ def test_path_selection_without_device(am, tuner):
     assert am.path(0, 1, 4, 512, 512, 130) == am.ATN_PATH_SPLIT_D           # head_d % 4 != 0
     assert am.path(0, 1, 4, 512, 512, 2048) == am.ATN_PATH_SPLIT_D
     # bf16 outside the single-launch window: the flash kernel at head_d <=
-    # 128 (head_d % 4 == 0), past that the MFMA GEMM path whenever D % 8 == 0,
-    # whatever len_q and len_k are, and the flash kernel up to 256 where the
-    # GEMM path does not run
+    # 256 (128 with an encoding; head_d % 4 == 0), past that the MFMA GEMM
+    # path whenever D % 8 == 0, whatever len_q and len_k are
     assert am.path(1, 4, 32, 512, 512, 128) == am.ATN_PATH_FLASH
     assert am.path(1, 1, 4, 512, 512, 128, am.make_pe("rope")) == am.ATN_PATH_FLASH
     assert am.path(1, 1, 2, 200, 20, 36) == am.ATN_PATH_FLASH
-    assert am.path(1, 1, 4, 512, 512, 256) == am.ATN_PATH_GEMM
-    assert am.path(1, 1, 4, 512, 512, 252) == am.ATN_PATH_FLASH           # D % 8 != 0
+    assert am.path(1, 1, 4, 512, 512, 256) == am.ATN_PATH_FLASH
+    assert am.path(1, 1, 4, 512, 512, 256, am.make_pe("rope")) == am.ATN_PATH_GEMM
+    assert am.path(1, 1, 4, 512, 512, 264) == am.ATN_PATH_GEMM
     assert am.path(1, 8, 8, 1024, 1024, 4096) == am.ATN_PATH_GEMM          # config 4
     assert am.path(1, 1, 8, 64, 4096, 2048) == am.ATN_PATH_GEMM
     assert am.path(1, 1, 4, 100, 100, 2048) == am.ATN_PATH_GEMM

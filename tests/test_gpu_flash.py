@@ -322,13 +322,13 @@ _BF16_SHAPES = [
     (1, 2, 65, 1, 64), (1, 2, 65, 64, 64), (1, 2, 70, 65, 64), (1, 3, 130, 129, 32),
     (1, 1, 200, 300, 128), (1, 2, 129, 513, 100), (1, 1, 80, 1025, 60), (2, 3, 100, 140, 8),
     (1, 2, 96, 200, 252), (1, 1, 70, 65, 196), (1, 300, 16, 16, 64), (1, 1, 2, 3000, 128),
+    (1, 2, 96, 200, 256), (1, 1, 70, 300, 200), (2, 2, 129, 513, 136),
 ]
 
 
 @pytest.mark.parametrize("shape", _BF16_SHAPES, ids=lambda s: "x".join(map(str, s)))
 def test_flash_bf16(am, dev, shape):
-    """bf16 calls outside the single-launch window with head_d <= 128 (and
-    up to 256 where the GEMM path does not run: head_d % 8 != 0)."""
+    """bf16 calls outside the single-launch window with head_d <= 256."""
     B, Hh, Lq, Lk, D = shape
     print(f"[case] flash bf16 {shape}", flush=True)
     assert am.path(1, B, Hh, Lq, Lk, D) == am.ATN_PATH_FLASH
