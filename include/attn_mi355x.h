@@ -293,14 +293,14 @@ int atn_prepare_pe_ex(const atn_pe_desc *pe, int head_d, int max_positions);
  * units. */
 #define ATN_PATH_FUSED_SMALL 1 /* one launch: split-D slices + device-side S all-reduce */
 #define ATN_PATH_SPLIT_D 2     /* three launches: partial QK^T, softmax, PV */
-#define ATN_PATH_FLASH 4       /* outside the single-launch window, head_d % 4 == 0: fp32 with
-                                  head_d <= 256 (128 with an encoding), bf16 with head_d <= 128
-                                  (up to 256 where the GEMM path does not run): one launch,
+#define ATN_PATH_FLASH 4       /* outside the single-launch window, head_d % 4 == 0, fp32 and
+                                  bf16: head_d <= 256 (128 with an encoding): one launch,
                                   online softmax over key tiles, no scratch; grids that would
                                   leave CUs idle split the keys (parts in the workspace, a
                                   second launch merges them) */
-#define ATN_PATH_GEMM 3        /* bf16, D % 8 == 0, head_d > 128, outside the single-launch
-                                  window: MFMA QK^T GEMM, row softmax, MFMA PV GEMM */
+#define ATN_PATH_GEMM 3        /* bf16, D % 8 == 0, head_d > 256 (> 128 with an encoding),
+                                  outside the single-launch window: MFMA QK^T GEMM, row
+                                  softmax, MFMA PV GEMM */
 int atn_attention_path_ex(int dtype, int batch, int heads, int len_q, int len_k, int head_d,
                           const atn_pe_desc *pe);
 
