@@ -187,8 +187,17 @@ __device__ __forceinline__ uint32_t pk_bf16_rne(float a, float b) {
 // range: no scales, no tile maxima), P as bf16; with an encoding the
 // encoded values are fp32, staged as one fp16 part each (a power-of-two
 // scale per tile brings K and V into fp16's normal range), P as fp16.
+// waves per SIMD the register allocation leaves room for: 4 (two 8-wave
+// workgroups per CU) for the raw bf16 form of 8 waves of 16 rows at head_d
+// <= 128, which needs few registers; else what the form itself brings
 template <typename T, int DP, int PEK, int NW, int RW>
-__global__ __launch_bounds__(64 * NW, 8 / NW) void k_flash(const T* __restrict__ Qg,
+constexpr int flash_waves_per_simd() {
+    return sizeof(T) == 2 && PEK == kPeNone && NW == 8 && RW == 16 && DP <= 128 ? 4 : 8 / NW;
+}
+
+template <typename T, int DP, int PEK, int NW, int RW>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(
+    flash_waves_per_simd<T, DP, PEK, NW, RW>()))) void k_flash(const T* __restrict__ Qg,
                                                              const T* __restrict__ Kg,
                                                              const T* __restrict__ Vg,
                                                              T* __restrict__ Og, int Lq, int LkAll,
