@@ -208,7 +208,10 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(
     constexpr bool kBf = sizeof(T) == 2;
     constexpr bool kRaw = kBf && PEK == kPeNone;
     constexpr int es = (int)sizeof(T);
-    typedef std::conditional_t<kRaw, bf16x8_t, f16x8> op_t;  // MFMA operands
+    // MFMA operands: Q K^T (op_t) and P V (pv_t).  bf16 V is never encoded,
+    // so it always goes in as loaded, with P as bf16.
+    typedef std::conditional_t<kRaw, bf16x8_t, f16x8> op_t;
+    typedef std::conditional_t<kBf, bf16x8_t, f16x8> pv_t;
     using G = FlashGeo<DP, PEK != kPeNone, NW, RW, !kBf>;
     typedef std::conditional_t<RW == 16, v4f, v16f> acc_t;
     extern __shared__ __align__(16) unsigned char smem_raw[];
@@ -322,11 +325,14 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(
             const int off = key < Lk && lcol < D ? (key * D + lcol) * es : kOob;
             if constexpr (kRaw) {
                 const auto a = __builtin_amdgcn_raw_buffer_load_b64(rk, off, 0, 0);
-                const auto b = __builtin_amdgcn_raw_buffer_load_b64(rv, off, 0, 0);
                 kw[i] = make_uint2(a[0], a[1]);
-                vw[i] = make_uint2(b[0], b[1]);
             } else {
                 kr[i] = ld4_t<T>(rk, off);
+            }
+            if constexpr (kBf) {
+                const auto b = __builtin_amdgcn_raw_buffer_load_b64(rv, off, 0, 0);
+                vw[i] = make_uint2(b[0], b[1]);
+            } else {
                 vr[i] = ld4_t<T>(rv, off);
             }
         }
@@ -347,40 +353,41 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(
                                               true);
             }
         }
-        float mk = 0.f, mv = 0.f;
+        float mk = 0.f, mv = 0.f;  // (bf16 V goes in as loaded: no maximum)
 #pragma unroll
         for (int i = 0; i < G::NLD; ++i) {
             mk = vmax3abs(mk, kr[i].x, kr[i].y);
             mk = vmax3abs(mk, kr[i].z, kr[i].w);
-            mv = vmax3abs(mv, vr[i].x, vr[i].y);
-            mv = vmax3abs(mv, vr[i].z, vr[i].w);
+            if constexpr (!kBf) {
+                mv = vmax3abs(mv, vr[i].x, vr[i].y);
+                mv = vmax3abs(mv, vr[i].z, vr[i].w);
+            }
         }
         // Usually ballots settle it with no reduction: a wave whose K values
-        // all lie below kF16Range and some at 2^-3 or above (V likewise; fp32
-        // V: below kF16Range only) reports the sentinel 1, a value of that
+        // all lie below kF16Range and some at 2^-3 or above (fp32 V: below
+        // kF16Range) reports the sentinel 1, a value of that
         // range, so the workgroup maximum over the slots is in range exactly
         // when the true one is, and when a wave lies beyond the range its own
         // (reduced) maximum still decides the scale.  Other waves reduce.
         const bool k_ok = !__builtin_amdgcn_ballot_w64(!(mk < kF16Range)) &&
                           __builtin_amdgcn_ballot_w64(mk >= 0.125f) != 0;
-        const bool v_ok = !__builtin_amdgcn_ballot_w64(!(mv < kF16Range)) &&
-                          (!kBf || __builtin_amdgcn_ballot_w64(mv >= 0.125f) != 0);
+        const bool v_ok = kBf || !__builtin_amdgcn_ballot_w64(!(mv < kF16Range));
         if (k_ok && v_ok) {
             mk = 1.f;
             mv = 1.f;
         } else {
             mk = wave_max_rows(mk);
-            mv = wave_max_rows(mv);
+            mv = kBf ? 1.f : wave_max_rows(mv);
             if (!(mk < INFINITY) || !(mv < INFINITY)) {  // the same in every lane
                 mk = 0.f;
-                mv = 0.f;
+                mv = kBf ? 1.f : 0.f;
 #pragma unroll
                 for (int i = 0; i < G::NLD; ++i) {
                     mk = max_finite4(mk, kr[i]);
-                    mv = max_finite4(mv, vr[i]);
+                    if constexpr (!kBf) mv = max_finite4(mv, vr[i]);
                 }
                 mk = wave_max_rows(mk);
-                mv = wave_max_rows(mv);
+                if constexpr (!kBf) mv = wave_max_rows(mv);
             }
         }
         if (lane == 0) {
@@ -390,10 +397,10 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(
     };
     // scales of the tile whose maxima are in slot[par] (K as it is where its
     // largest magnitude lies in [2^-3, 65504): the split then keeps 2^-22 of
-    // that magnitude; else a power of two brings it to [2^14, 2^15); V the
-    // same for bf16, whose one fp16 part must stay out of the subnormal
-    // range, and for fp32 scaled only beyond fp16's range), and its hi + lo
-    // (fp32) or hi (bf16) fp16 parts into LDS buffer par
+    // that magnitude, one fp16 part 2^-11; else a power of two brings it to
+    // [2^14, 2^15); fp32 V scaled only beyond fp16's range), and its hi + lo
+    // (fp32) or hi (encoded bf16 K) fp16 parts into LDS buffer par; bf16 V
+    // goes in as loaded
     auto stage = [&](int par, float& uk, float& sv, float& uv) {
         if constexpr (kRaw) {
             uk = sv = uv = 1.f;
@@ -415,7 +422,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(
         const bool k_plain = mk >= 0.125f && mk < kF16Range;
         const float sk = k_plain ? 1.f : pow2_scale(mk);
         uk = k_plain ? 1.f : pow2_unit(mk);
-        const bool v_plain = kBf ? mv >= 0.125f && mv < kF16Range : mv < kF16Range;
+        const bool v_plain = kBf || mv < kF16Range;
         sv = v_plain ? 1.f : pow2_scale(mv);
         uv = v_plain ? 1.f : pow2_unit(mv);
         uint16_t* buf = smem + par * G::TILE;
@@ -426,13 +433,10 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(
                 uint32_t h0, l0, h1, l1, h2, l2, h3, l3;
                 if constexpr (kBf) {
                     const float fk = decltype(plain)::value ? 1.f : sk;
-                    const float fv = decltype(plain)::value ? 1.f : sv;
                     *reinterpret_cast<uint2*>(buf + G::K_HI + row * G::KSTR + lcol) =
                         make_uint2(pk_f16_rne(kr[i].x * fk, kr[i].y * fk),
                                    pk_f16_rne(kr[i].z * fk, kr[i].w * fk));
-                    *reinterpret_cast<uint2*>(buf + G::V_HI + row * G::VSTR + lcol) =
-                        make_uint2(pk_f16_rne(vr[i].x * fv, vr[i].y * fv),
-                                   pk_f16_rne(vr[i].z * fv, vr[i].w * fv));
+                    *reinterpret_cast<uint2*>(buf + G::V_HI + row * G::VSTR + lcol) = vw[i];
                     continue;
                 }
                 if constexpr (decltype(plain)::value) {
@@ -581,7 +585,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(
         // tile 2b + 1, i.e. keys 4 lg + 0..3, 16 + 4 lg + 0..3 of the 32-key
         // block; RW = 32: registers 8 (b % 2) + 0..7 of tile b / 2, i.e.
         // keys 4 lg + 0..3, 8 + 4 lg + 0..3 of the 16-key block)
-        op_t ph[G::NB];
+        pv_t ph[G::NB];
         f16x8 pl[G::NB];
 #pragma unroll
         for (int b = 0; b < G::NB; ++b) {
@@ -591,27 +595,21 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(
                 const int i0 = 8 * b + e, i1 = i0 + 1;
                 const float p0 = __builtin_amdgcn_exp2f(fmaf(s[i0 / G::SPT][i0 % G::SPT], cx, nm));
                 const float p1 = __builtin_amdgcn_exp2f(fmaf(s[i1 / G::SPT][i1 % G::SPT], cx, nm));
-                if constexpr (kRaw) {
-                    // P as bf16 (the operand type of the raw products), the sum
-                    // from the same rounded values
+                if constexpr (kBf) {
+                    // P as bf16 (the operand type of the products with V's
+                    // bits), the sum from the same rounded values, two per
+                    // v_dot2_f32_bf16
                     h[e / 2] = l[e / 2] = pk_bf16_rne(p0, p1);
                     const bf16x2_t one2 = {(__bf16)1.f, (__bf16)1.f};
                     ps = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, h[e / 2]),
                                                          one2, ps, false);
-                } else if constexpr (kBf) {
-                    // one part (lo unused); the sum takes the rounded values
-                    // the product takes, two per v_dot2_f32_f16
-                    h[e / 2] = l[e / 2] = pk_f16_rne(p0, p1);
-                    const f16x2 one2 = {(_Float16)1.f, (_Float16)1.f};
-                    ps = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, h[e / 2]), one2, ps,
-                                                false);
                 } else {
                     ps += p0;
                     ps += p1;
                     split2_f16_one(p0, p1, one, h[e / 2], l[e / 2]);
                 }
             }
-            ph[b] = __builtin_bit_cast(op_t, make_uint4(h[0], h[1], h[2], h[3]));
+            ph[b] = __builtin_bit_cast(pv_t, make_uint4(h[0], h[1], h[2], h[3]));
             pl[b] = __builtin_bit_cast(f16x8, make_uint4(l[0], l[1], l[2], l[3]));
         }
         l_run = l_run * alpha + ps;  // this lane's keys; summed over lane groups at the end
@@ -638,7 +636,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(
                 constexpr int half = G::KD / 2 * G::VSTR;
                 const uint2 h0 = lds_tr16(buf + G::V_HI + a);
                 const uint2 h1 = lds_tr16(buf + G::V_HI + a + half);
-                const op_t vh = __builtin_bit_cast(op_t, make_uint4(h0.x, h0.y, h1.x, h1.y));
+                const pv_t vh = __builtin_bit_cast(pv_t, make_uint4(h0.x, h0.y, h1.x, h1.y));
                 o[dt] = mfma_rw(vh, ph[b], o[dt]);
                 if constexpr (!kBf) {
                     const uint2 l0 = lds_tr16(buf + G::V_LO + a);
