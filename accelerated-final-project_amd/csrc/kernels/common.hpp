@@ -265,6 +265,95 @@ __device__ __forceinline__ float4 apply_pe4(float4 x, const T* __restrict__ xr, 
     return make_float4(v[0], v[1], v[2], v[3]);
 }
 
+// Whether pe4_batch serves this side: the library's compact tables
+// (dup = 0) with rows a whole number of the vectors it reads (interleaved
+// RoPE: rotary a multiple of 4; rotate-half: rotary / 2 a multiple of 4;
+// sinusoidal: head_d a multiple of 4, which every caller has).
+__device__ __forceinline__ bool pe4_batch_ok(int pek, const PeSide& pe) {
+    if (pe.dup) return false;
+    if (pek == kPeRopeInterleaved) return (pe.rotary & 3) == 0;
+    if (pek == kPeRopeHalf) return (pe.rotary & 7) == 0;
+    return (pe.ld & 1) == 0;
+}
+
+// apply_pe4 on N groups of 4 elements at once, every load (the angles, the
+// rotate-half partners) issued before any arithmetic, so that the groups'
+// latencies overlap instead of each group waiting in turn.  Group i holds
+// x[i] = dims d[i]..d[i] + 3 (d[i] a multiple of 4) of the row at xr[i],
+// position pos[i] (a row of the tables), loaded (zeros at or past dend).
+// Only where pe4_batch_ok holds, and with rows 8-byte aligned for T =
+// uint16_t, 16-byte for float.  Addresses of groups that take no encoding
+// (past the rotary width or dend) are clamped into the row and the table, so
+// every load is valid and its result unused.  The arithmetic is apply_pe4's.
+template <typename T, int PEK, int N>
+__device__ __forceinline__ void pe4_batch(float4 (&x)[N], const int (&d)[N],
+                                          const T* const (&xr)[N], const int (&pos)[N], int dend,
+                                          const PeSide& pe) {
+    if constexpr (PEK == kPeRopeInterleaved) {
+        float2 c[N], sn[N];
+#pragma unroll
+        for (int i = 0; i < N; ++i) {
+            const int f = min(d[i], pe.rotary - 4) >> 1;  // frequencies f, f + 1
+            const size_t idx = (size_t)pos[i] * pe.ld + f;
+            c[i] = *reinterpret_cast<const float2*>(pe.a + idx);
+            sn[i] = *reinterpret_cast<const float2*>(pe.b + idx);
+        }
+#pragma unroll
+        for (int i = 0; i < N; ++i) {
+            if (d[i] + 3 < pe.rotary) {
+                const float4 v = x[i];
+                x[i] = make_float4(rot_first(v.x, v.y, c[i].x, sn[i].x),
+                                   rot_second(v.x, v.y, c[i].x, sn[i].x),
+                                   rot_first(v.z, v.w, c[i].y, sn[i].y),
+                                   rot_second(v.z, v.w, c[i].y, sn[i].y));
+            }
+        }
+    } else if constexpr (PEK == kPeRopeHalf) {
+        const int h = pe.rotary >> 1;
+        float4 c[N], sn[N], p[N];
+#pragma unroll
+        for (int i = 0; i < N; ++i) {
+            const bool lo = d[i] < h;
+            const int f = min(lo ? d[i] : d[i] - h, h - 4);
+            const size_t idx = (size_t)pos[i] * pe.ld + f;
+            c[i] = *reinterpret_cast<const float4*>(pe.a + idx);
+            sn[i] = *reinterpret_cast<const float4*>(pe.b + idx);
+            // the partner h away (clamped into the row for groups past dend)
+            p[i] = Elem<T>::ld4(xr[i], min(lo ? d[i] + h : d[i] - h, dend - 4));
+        }
+#pragma unroll
+        for (int i = 0; i < N; ++i) {
+            if (d[i] + 3 < pe.rotary && d[i] + 3 < dend) {
+                const bool lo = d[i] < h;
+                const float v[4] = {x[i].x, x[i].y, x[i].z, x[i].w};
+                const float q[4] = {p[i].x, p[i].y, p[i].z, p[i].w};
+                const float cc[4] = {c[i].x, c[i].y, c[i].z, c[i].w};
+                const float ss[4] = {sn[i].x, sn[i].y, sn[i].z, sn[i].w};
+                float r[4];
+#pragma unroll
+                for (int k = 0; k < 4; ++k)
+                    r[k] = lo ? rot_first(v[k], q[k], cc[k], ss[k]) : rot_second(q[k], v[k], cc[k], ss[k]);
+                x[i] = make_float4(r[0], r[1], r[2], r[3]);
+            }
+        }
+    } else if constexpr (PEK == kPeSinusoidal) {
+        float2 sn[N], c[N];
+#pragma unroll
+        for (int i = 0; i < N; ++i) {
+            const size_t idx = (size_t)pos[i] * pe.ld + (min(d[i], dend - 4) >> 1);
+            sn[i] = *reinterpret_cast<const float2*>(pe.a + idx);
+            c[i] = *reinterpret_cast<const float2*>(pe.b + idx);
+        }
+#pragma unroll
+        for (int i = 0; i < N; ++i) {
+            if (d[i] + 3 < dend) {
+                const float4 v = x[i];
+                x[i] = make_float4(v.x + sn[i].x, v.y + c[i].x, v.z + sn[i].y, v.w + c[i].y);
+            }
+        }
+    }
+}
+
 // Loads x[d..d+3] of one row (row pointer xr, position pos), applies the
 // positional encoding of this side, and returns fp32.  Elements at or past
 // dend read as 0.  d is a multiple of 4.

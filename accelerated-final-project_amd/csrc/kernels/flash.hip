@@ -267,20 +267,70 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(
         float4 qv[G::KS][2];
         float mq = 0.f;
         const __amdgpu_buffer_rsrc_t rq = buf_rsrc(Qh, Lq * D * es);
+        if constexpr (PEK == kPeNone) {
 #pragma unroll
-        for (int ks = 0; ks < G::KS; ++ks)
+            for (int ks = 0; ks < G::KS; ++ks)
 #pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const int d = G::KD * ks + 8 * lg + 4 * h;
-                if constexpr (PEK == kPeNone) {
+                for (int h = 0; h < 2; ++h) {
+                    const int d = G::KD * ks + 8 * lg + 4 * h;
                     qv[ks][h] = ld4_t<T>(rq, d < D ? (qrow * D + d) * es : kOob);
-                } else {
-                    qv[ks][h] = make_float4(0.f, 0.f, 0.f, 0.f);
-                    if (qrow < Lq && d < D)
-                        qv[ks][h] = load_row4_pe<T, PEK>(Qh + (size_t)qrow * D, qrow, d, D, pq, true);
+                    mq = max_finite4(mq, qv[ks][h]);
                 }
-                mq = max_finite4(mq, qv[ks][h]);
+        } else {
+            // The encoding needs the angles of each element, and in the MFMA
+            // layout each lane holds a query row of its own: their table
+            // reads would take a cache line per lane.  So the wave encodes its
+            // rows with consecutive lanes on consecutive dims (coalesced, all
+            // loads first), 16 rows a round, and passes them through LDS (free
+            // until the first tile is staged) into the MFMA layout.
+            constexpr int VPR = DP / 4, GPR = VPR / 4;  // vectors per row, per lane and round
+            constexpr int NR = RW / 16, NG = NR * GPR, QSTR = DP + 4;
+            static_assert(NW * 16 * QSTR * 4 <= G::BYTES, "Q staging fits the tile buffers");
+            float4 x[NG];
+            int dd[NG], pp[NG], rw[NG];
+            const T* rr[NG];
+#pragma unroll
+            for (int g = 0; g < NG; ++g) {
+                const int v = lane + 64 * (g % GPR);
+                rw[g] = q0 + RW * wave + 16 * (g / GPR) + v / VPR;
+                pp[g] = min(rw[g], Lq - 1);
+                dd[g] = (v % VPR) * 4;
+                rr[g] = Qh + (size_t)pp[g] * D;
+                x[g] = ld4_t<T>(rq, rw[g] < Lq && dd[g] < D ? (rw[g] * D + dd[g]) * es : kOob);
             }
+            if (pq.on) {
+                if (pe4_batch_ok(PEK, pq)) {
+                    pe4_batch<T, PEK, NG>(x, dd, rr, pp, D, pq);
+                } else {
+#pragma unroll
+                    for (int g = 0; g < NG; ++g)
+                        if (dd[g] < D) x[g] = apply_pe4<T, PEK>(x[g], rr[g], pp[g], dd[g], D, pq, true);
+                }
+            }
+#pragma unroll
+            for (int g = 0; g < NG; ++g) {
+                if (rw[g] >= Lq) x[g] = make_float4(0.f, 0.f, 0.f, 0.f);  // rows past Lq: zero
+                mq = max_finite4(mq, x[g]);
+            }
+            float* qs = reinterpret_cast<float*>(smem_raw) + wave * 16 * QSTR;
+#pragma unroll
+            for (int rnd = 0; rnd < NR; ++rnd) {
+#pragma unroll
+                for (int j = 0; j < GPR; ++j) {
+                    const int v = lane + 64 * j;
+                    *reinterpret_cast<float4*>(qs + (v / VPR) * QSTR + (v % VPR) * 4) =
+                        x[rnd * GPR + j];
+                }
+                if ((lr >> 4) == rnd) {  // the lanes whose query is among these rows
+#pragma unroll
+                    for (int ks = 0; ks < G::KS; ++ks)
+#pragma unroll
+                        for (int h = 0; h < 2; ++h)
+                            qv[ks][h] = *reinterpret_cast<const float4*>(
+                                qs + (lr & 15) * QSTR + G::KD * ks + 8 * lg + 4 * h);
+                }
+            }
+        }
         mq = wave_max(mq);
         const float sq = pow2_scale(mq);
         uq = pow2_unit(mq);
