@@ -395,12 +395,30 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(
     auto maxima = [&](int k0, int par) {
         if constexpr (kRaw) return;  // no scales
         if constexpr (PEK != kPeNone) {
+            if (pk.on && pe4_batch_ok(PEK, pk)) {
+                // every group's loads at once (rows past Lk clamped, their
+                // values kept zero)
+                int dd[G::NLD], pp[G::NLD];
+                const T* rr[G::NLD];
 #pragma unroll
-            for (int i = 0; i < G::NLD; ++i) {
-                const int key = k0 + lrow + G::RSTEP * i;
-                if (key < Lk && lcol < D)
-                    kr[i] = apply_pe4<T, PEK>(kr[i], Kh + (size_t)key * D, kbeg + key, lcol, D, pk,
-                                              true);
+                for (int i = 0; i < G::NLD; ++i) {
+                    const int kc = min(k0 + lrow + G::RSTEP * i, Lk - 1);
+                    dd[i] = lcol;
+                    pp[i] = kbeg + kc;
+                    rr[i] = Kh + (size_t)kc * D;
+                }
+                pe4_batch<T, PEK, G::NLD>(kr, dd, rr, pp, D, pk);
+#pragma unroll
+                for (int i = 0; i < G::NLD; ++i)
+                    if (k0 + lrow + G::RSTEP * i >= Lk) kr[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+            } else {
+#pragma unroll
+                for (int i = 0; i < G::NLD; ++i) {
+                    const int key = k0 + lrow + G::RSTEP * i;
+                    if (key < Lk && lcol < D)
+                        kr[i] = apply_pe4<T, PEK>(kr[i], Kh + (size_t)key * D, kbeg + key, lcol, D,
+                                                  pk, true);
+                }
             }
         }
         float mk = 0.f, mv = 0.f;  // (bf16 V goes in as loaded: no maximum)
