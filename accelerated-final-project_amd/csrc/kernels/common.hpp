@@ -354,6 +354,45 @@ __device__ __forceinline__ void pe4_batch(float4 (&x)[N], const int (&d)[N],
     }
 }
 
+// Rotate-half over whole rows (rotary = the row's length) where a row's
+// 4-dim groups lie in 2 XM consecutive lanes, group g in lane g of them: the
+// partner of a group (the dims half a row away) is then in the lane XM away
+// (lane ^ XM), taken by ds_swizzle instead of loaded again; only the angles
+// are loaded, all before the arithmetic.  Otherwise as pe4_batch (compact
+// tables, rotary / 2 a multiple of 4).
+template <int XM>
+__device__ __forceinline__ float swz_xor_lanes(float v) {
+    static_assert(XM == 4 || XM == 8 || XM == 16, "xor within 32 lanes");
+    return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x1F | (XM << 10)));
+}
+template <int N, int XM>
+__device__ __forceinline__ void pe4_batch_half_lanes(float4 (&x)[N], const int (&d)[N],
+                                                     const int (&pos)[N], const PeSide& pe) {
+    const int h = pe.rotary >> 1;
+    float4 c[N], sn[N], p[N];
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        const size_t idx = (size_t)pos[i] * pe.ld + (d[i] < h ? d[i] : d[i] - h);
+        c[i] = *reinterpret_cast<const float4*>(pe.a + idx);
+        sn[i] = *reinterpret_cast<const float4*>(pe.b + idx);
+        p[i] = make_float4(swz_xor_lanes<XM>(x[i].x), swz_xor_lanes<XM>(x[i].y),
+                           swz_xor_lanes<XM>(x[i].z), swz_xor_lanes<XM>(x[i].w));
+    }
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        const bool lo = d[i] < h;
+        const float v[4] = {x[i].x, x[i].y, x[i].z, x[i].w};
+        const float q[4] = {p[i].x, p[i].y, p[i].z, p[i].w};
+        const float cc[4] = {c[i].x, c[i].y, c[i].z, c[i].w};
+        const float ss[4] = {sn[i].x, sn[i].y, sn[i].z, sn[i].w};
+        float r[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            r[k] = lo ? rot_first(v[k], q[k], cc[k], ss[k]) : rot_second(q[k], v[k], cc[k], ss[k]);
+        x[i] = make_float4(r[0], r[1], r[2], r[3]);
+    }
+}
+
 // Loads x[d..d+3] of one row (row pointer xr, position pos), applies the
 // positional encoding of this side, and returns fp32.  Elements at or past
 // dend read as 0.  d is a multiple of 4.

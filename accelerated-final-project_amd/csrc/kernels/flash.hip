@@ -299,7 +299,12 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(
                 x[g] = ld4_t<T>(rq, rw[g] < Lq && dd[g] < D ? (rw[g] * D + dd[g]) * es : kOob);
             }
             if (pq.on) {
-                if (pe4_batch_ok(PEK, pq)) {
+                if (PEK == kPeRopeHalf && VPR <= 32 && D == DP && pq.rotary == D &&
+                    pe4_batch_ok(PEK, pq)) {
+                    // a row's groups in VPR consecutive lanes: partners by lane
+                    if constexpr (PEK == kPeRopeHalf && VPR <= 32 && VPR >= 8)
+                        pe4_batch_half_lanes<NG, VPR / 2>(x, dd, pp, pq);
+                } else if (pe4_batch_ok(PEK, pq)) {
                     pe4_batch<T, PEK, NG>(x, dd, rr, pp, D, pq);
                 } else {
 #pragma unroll
@@ -397,7 +402,9 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(
         if constexpr (PEK != kPeNone) {
             if (pk.on && pe4_batch_ok(PEK, pk)) {
                 // every group's loads at once (rows past Lk clamped, their
-                // values kept zero)
+                // values kept zero); rotate-half over whole rows takes each
+                // partner from the lane VPR / 2 away (a row's groups lie in VPR
+                // consecutive lanes)
                 int dd[G::NLD], pp[G::NLD];
                 const T* rr[G::NLD];
 #pragma unroll
@@ -407,7 +414,12 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(
                     pp[i] = kbeg + kc;
                     rr[i] = Kh + (size_t)kc * D;
                 }
-                pe4_batch<T, PEK, G::NLD>(kr, dd, rr, pp, D, pk);
+                constexpr bool kLanes = PEK == kPeRopeHalf && G::VPR >= 8 && G::VPR <= 32;
+                if (kLanes && D == DP && pk.rotary == D) {
+                    if constexpr (kLanes) pe4_batch_half_lanes<G::NLD, G::VPR / 2>(kr, dd, pp, pk);
+                } else {
+                    pe4_batch<T, PEK, G::NLD>(kr, dd, rr, pp, D, pk);
+                }
 #pragma unroll
                 for (int i = 0; i < G::NLD; ++i)
                     if (k0 + lrow + G::RSTEP * i >= Lk) kr[i] = make_float4(0.f, 0.f, 0.f, 0.f);
