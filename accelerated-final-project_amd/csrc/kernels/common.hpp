@@ -318,8 +318,10 @@ __device__ __forceinline__ void pe4_batch(float4 (&x)[N], const int (&d)[N],
             const size_t idx = (size_t)pos[i] * pe.ld + f;
             c[i] = *reinterpret_cast<const float4*>(pe.a + idx);
             sn[i] = *reinterpret_cast<const float4*>(pe.b + idx);
-            // the partner h away (clamped into the row for groups past dend)
-            p[i] = Elem<T>::ld4(xr[i], min(lo ? d[i] + h : d[i] - h, dend - 4));
+            // the partner h away (clamped below the rotary width, inside the
+            // row, for groups that take no encoding; dend may end a slice of
+            // the row, the partner lies outside it)
+            p[i] = Elem<T>::ld4(xr[i], min(lo ? d[i] + h : d[i] - h, pe.rotary - 4));
         }
 #pragma unroll
         for (int i = 0; i < N; ++i) {
