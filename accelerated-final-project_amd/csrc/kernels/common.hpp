@@ -276,84 +276,93 @@ __device__ __forceinline__ bool pe4_batch_ok(int pek, const PeSide& pe) {
     return (pe.ld & 1) == 0;
 }
 
-// apply_pe4 on N groups of 4 elements at once, every load (the angles, the
-// rotate-half partners) issued before any arithmetic, so that the groups'
-// latencies overlap instead of each group waiting in turn.  Group i holds
-// x[i] = dims d[i]..d[i] + 3 (d[i] a multiple of 4) of the row at xr[i],
-// position pos[i] (a row of the tables), loaded (zeros at or past dend).
-// Only where pe4_batch_ok holds, and with rows 8-byte aligned for T =
-// uint16_t, 16-byte for float.  Addresses of groups that take no encoding
-// (past the rotary width or dend) are clamped into the row and the table, so
-// every load is valid and its result unused.  The arithmetic is apply_pe4's.
+// The positional encoding of one group of 4 elements in two phases:
+// pe4_fetch loads its operands (the angles, the rotate-half partners) and
+// pe4_apply does the arithmetic, so that a caller can issue the loads of
+// many groups before any arithmetic and the groups' latencies overlap
+// instead of each group waiting in turn.  The group holds dims d..d + 3 (d a
+// multiple of 4) of the row at xr, position pos (a row of the tables), at or
+// past dend zeros.  Only where pe4_batch_ok holds, and with rows 8-byte
+// aligned for T = uint16_t, 16-byte for float.  Addresses of groups that
+// take no encoding (past the rotary width or dend) are clamped into the row
+// and the table, so every load is valid and its result unused.  The
+// arithmetic is apply_pe4's.
+template <int PEK>
+struct Pe4Ops {};
+template <>
+struct Pe4Ops<kPeRopeInterleaved> {
+    float2 c, s;  // frequencies d / 2 and d / 2 + 1
+};
+template <>
+struct Pe4Ops<kPeRopeHalf> {
+    float4 c, s, p;  // 4 consecutive frequencies; the partners h away
+};
+template <>
+struct Pe4Ops<kPeSinusoidal> {
+    float2 s, c;  // sin and cos of frequencies d / 2 and d / 2 + 1
+};
+template <typename T, int PEK>
+__device__ __forceinline__ Pe4Ops<PEK> pe4_fetch(int d, const T* __restrict__ xr, int pos,
+                                                 int dend, const PeSide& pe) {
+    Pe4Ops<PEK> o;
+    if constexpr (PEK == kPeRopeInterleaved) {
+        const size_t idx = (size_t)pos * pe.ld + (min(d, pe.rotary - 4) >> 1);
+        o.c = *reinterpret_cast<const float2*>(pe.a + idx);
+        o.s = *reinterpret_cast<const float2*>(pe.b + idx);
+    } else if constexpr (PEK == kPeRopeHalf) {
+        const int h = pe.rotary >> 1;
+        const bool lo = d < h;
+        const size_t idx = (size_t)pos * pe.ld + min(lo ? d : d - h, h - 4);
+        o.c = *reinterpret_cast<const float4*>(pe.a + idx);
+        o.s = *reinterpret_cast<const float4*>(pe.b + idx);
+        // the partner h away (clamped below the rotary width, inside the
+        // row, for groups that take no encoding; dend may end a slice of the
+        // row, the partner lies outside it)
+        o.p = Elem<T>::ld4(xr, min(lo ? d + h : d - h, pe.rotary - 4));
+    } else if constexpr (PEK == kPeSinusoidal) {
+        const size_t idx = (size_t)pos * pe.ld + (min(d, dend - 4) >> 1);
+        o.s = *reinterpret_cast<const float2*>(pe.a + idx);
+        o.c = *reinterpret_cast<const float2*>(pe.b + idx);
+    }
+    return o;
+}
+template <int PEK>
+__device__ __forceinline__ float4 pe4_apply(float4 x, const Pe4Ops<PEK>& o, int d, int dend,
+                                            const PeSide& pe) {
+    if constexpr (PEK == kPeRopeInterleaved) {
+        if (d + 3 < pe.rotary)
+            x = make_float4(rot_first(x.x, x.y, o.c.x, o.s.x), rot_second(x.x, x.y, o.c.x, o.s.x),
+                            rot_first(x.z, x.w, o.c.y, o.s.y), rot_second(x.z, x.w, o.c.y, o.s.y));
+    } else if constexpr (PEK == kPeRopeHalf) {
+        if (d + 3 < pe.rotary && d + 3 < dend) {
+            const bool lo = d < (pe.rotary >> 1);
+            const float v[4] = {x.x, x.y, x.z, x.w};
+            const float q[4] = {o.p.x, o.p.y, o.p.z, o.p.w};
+            const float cc[4] = {o.c.x, o.c.y, o.c.z, o.c.w};
+            const float ss[4] = {o.s.x, o.s.y, o.s.z, o.s.w};
+            float r[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                r[k] = lo ? rot_first(v[k], q[k], cc[k], ss[k]) : rot_second(q[k], v[k], cc[k], ss[k]);
+            x = make_float4(r[0], r[1], r[2], r[3]);
+        }
+    } else if constexpr (PEK == kPeSinusoidal) {
+        if (d + 3 < dend) x = make_float4(x.x + o.s.x, x.y + o.c.x, x.z + o.s.y, x.w + o.c.y);
+    }
+    return x;
+}
+
+// pe4_fetch and pe4_apply on N groups at once (group i: x[i], dims d[i].., row
+// xr[i], position pos[i]), every load issued before any arithmetic.
 template <typename T, int PEK, int N>
 __device__ __forceinline__ void pe4_batch(float4 (&x)[N], const int (&d)[N],
                                           const T* const (&xr)[N], const int (&pos)[N], int dend,
                                           const PeSide& pe) {
-    if constexpr (PEK == kPeRopeInterleaved) {
-        float2 c[N], sn[N];
+    Pe4Ops<PEK> o[N];
 #pragma unroll
-        for (int i = 0; i < N; ++i) {
-            const int f = min(d[i], pe.rotary - 4) >> 1;  // frequencies f, f + 1
-            const size_t idx = (size_t)pos[i] * pe.ld + f;
-            c[i] = *reinterpret_cast<const float2*>(pe.a + idx);
-            sn[i] = *reinterpret_cast<const float2*>(pe.b + idx);
-        }
+    for (int i = 0; i < N; ++i) o[i] = pe4_fetch<T, PEK>(d[i], xr[i], pos[i], dend, pe);
 #pragma unroll
-        for (int i = 0; i < N; ++i) {
-            if (d[i] + 3 < pe.rotary) {
-                const float4 v = x[i];
-                x[i] = make_float4(rot_first(v.x, v.y, c[i].x, sn[i].x),
-                                   rot_second(v.x, v.y, c[i].x, sn[i].x),
-                                   rot_first(v.z, v.w, c[i].y, sn[i].y),
-                                   rot_second(v.z, v.w, c[i].y, sn[i].y));
-            }
-        }
-    } else if constexpr (PEK == kPeRopeHalf) {
-        const int h = pe.rotary >> 1;
-        float4 c[N], sn[N], p[N];
-#pragma unroll
-        for (int i = 0; i < N; ++i) {
-            const bool lo = d[i] < h;
-            const int f = min(lo ? d[i] : d[i] - h, h - 4);
-            const size_t idx = (size_t)pos[i] * pe.ld + f;
-            c[i] = *reinterpret_cast<const float4*>(pe.a + idx);
-            sn[i] = *reinterpret_cast<const float4*>(pe.b + idx);
-            // the partner h away (clamped below the rotary width, inside the
-            // row, for groups that take no encoding; dend may end a slice of
-            // the row, the partner lies outside it)
-            p[i] = Elem<T>::ld4(xr[i], min(lo ? d[i] + h : d[i] - h, pe.rotary - 4));
-        }
-#pragma unroll
-        for (int i = 0; i < N; ++i) {
-            if (d[i] + 3 < pe.rotary && d[i] + 3 < dend) {
-                const bool lo = d[i] < h;
-                const float v[4] = {x[i].x, x[i].y, x[i].z, x[i].w};
-                const float q[4] = {p[i].x, p[i].y, p[i].z, p[i].w};
-                const float cc[4] = {c[i].x, c[i].y, c[i].z, c[i].w};
-                const float ss[4] = {sn[i].x, sn[i].y, sn[i].z, sn[i].w};
-                float r[4];
-#pragma unroll
-                for (int k = 0; k < 4; ++k)
-                    r[k] = lo ? rot_first(v[k], q[k], cc[k], ss[k]) : rot_second(q[k], v[k], cc[k], ss[k]);
-                x[i] = make_float4(r[0], r[1], r[2], r[3]);
-            }
-        }
-    } else if constexpr (PEK == kPeSinusoidal) {
-        float2 sn[N], c[N];
-#pragma unroll
-        for (int i = 0; i < N; ++i) {
-            const size_t idx = (size_t)pos[i] * pe.ld + (min(d[i], dend - 4) >> 1);
-            sn[i] = *reinterpret_cast<const float2*>(pe.a + idx);
-            c[i] = *reinterpret_cast<const float2*>(pe.b + idx);
-        }
-#pragma unroll
-        for (int i = 0; i < N; ++i) {
-            if (d[i] + 3 < dend) {
-                const float4 v = x[i];
-                x[i] = make_float4(v.x + sn[i].x, v.y + c[i].x, v.z + sn[i].y, v.w + c[i].y);
-            }
-        }
-    }
+    for (int i = 0; i < N; ++i) x[i] = pe4_apply<PEK>(x[i], o[i], d[i], dend, pe);
 }
 
 // Rotate-half over whole rows (rotary = the row's length) where a row's

@@ -831,29 +831,80 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
         }
     };
     {
+        // Rows kk = j * NR + u of Q (isq) or K in round j (loaded as r[NR]),
+        // encoded, into LDS.  With the library's compact tables the rows go
+        // kEncBatch at a time, every load of a batch (angles, rotate-half
+        // partners) issued before its arithmetic, rows clamped into the
+        // sequence so that every load is valid; otherwise (the caller's
+        // duplicated tables) one row at a time.  A side without an encoding
+        // (pe.on == 0) is stored as loaded.
+        constexpr int kEncBatch = PEK == kPeRopeHalf ? 4 : 8;
+        auto encode_store = [&](bool isq, int j, auto& r) {
+            constexpr int NR = sizeof(r) / sizeof(r[0]);
+            const int cnt = isq ? cq : ckv, len = isq ? Lq : Lk, p0 = isq ? q0 : 0;
+            const T* __restrict__ X = isq ? Q : K;
+            const PeSide& pe = isq ? a.pq : a.pk;
+            if (!pe.on) {
+#pragma unroll
+                for (int u = 0; u < NR; ++u) {
+                    const int kk = j * NR + u;
+                    if (kk < cnt) store_qk(isq, r0 + kk * rstep, Raw4<T>::f4(r[u]));
+                }
+            } else if (pe4_batch_ok(PEK, pe)) {
+#pragma unroll
+                for (int b = 0; b < NR; b += kEncBatch) {
+                    Pe4Ops<PEK> o[kEncBatch];
+#pragma unroll
+                    for (int u = 0; u < kEncBatch && b + u < NR; ++u) {
+                        const int rc = min(r0 + (j * NR + b + u) * rstep, len - 1);
+                        o[u] = pe4_fetch<T, PEK>(d, X + (size_t)rc * D, p0 + rc, D, pe);
+                    }
+#pragma unroll
+                    for (int u = 0; u < kEncBatch && b + u < NR; ++u) {
+                        const int kk = j * NR + b + u, row = r0 + kk * rstep;
+                        if (kk < cnt) {
+                            float4 f = Raw4<T>::f4(r[b + u]);
+                            if (lane_ok && row < len) f = pe4_apply<PEK>(f, o[u], d, D, pe);
+                            store_qk(isq, row, f);
+                        }
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int u = 0; u < NR; ++u) {
+                    const int kk = j * NR + u, row = r0 + kk * rstep;
+                    if (kk < cnt) {
+                        float4 f = Raw4<T>::f4(r[u]);
+                        if (lane_ok && row < len)
+                            f = encode4<T, PEK>(f, X + (size_t)row * D, p0 + row, d, pe);
+                        store_qk(isq, row, f);
+                    }
+                }
+            }
+        };
         // round j into LDS: Q and K (and, unless deferred, V)
         auto store_round = [&](int j, Raw (&q)[kQ], Raw (&k)[kKV], Raw (&v)[kKV],
                                bool store_v_now) {
+            if constexpr (PEK != kPeNone) {
+                encode_store(true, j, q);
+                encode_store(false, j, k);
+                if (store_v_now) {
+#pragma unroll
+                    for (int u = 0; u < kKV; ++u)
+                        if (j * kKV + u < ckv) store_v(r0 + (j * kKV + u) * rstep, v[u]);
+                }
+                return;
+            }
 #pragma unroll
             for (int u = 0; u < kQ; ++u) {
                 const int kk = j * kQ + u, row = r0 + kk * rstep;
-                if (kk < cq) {
-                    float4 f = Raw4<T>::f4(q[u]);
-                    if constexpr (PEK != kPeNone)
-                        if (lane_ok && row < Lq)
-                            f = encode4<T, PEK>(f, Q + (size_t)row * D, q0 + row, d, a.pq);
-                    store_qk(true, row, f);
-                }
+                if (kk < cq) store_qk(true, row, Raw4<T>::f4(q[u]));
             }
 #pragma unroll
             for (int u = 0; u < kKV; ++u) {
                 const int kk = j * kKV + u, row = r0 + kk * rstep;
                 if (kk < ckv) {
-                    float4 f = Raw4<T>::f4(k[u]);
-                    if constexpr (PEK != kPeNone)
-                        if (lane_ok && row < Lk)
-                            f = encode4<T, PEK>(f, K + (size_t)row * D, row, d, a.pk);
-                    store_qk(false, row, f);
+                    store_qk(false, row, Raw4<T>::f4(k[u]));
                     if (store_v_now) store_v(row, v[u]);
                 }
             }

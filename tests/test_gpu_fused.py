@@ -120,6 +120,73 @@ def test_fused_with_encodings_bf16(am, dev, pe):
     assert n == 0, f"normwise rel {nrel}, max abs {mabs}"
 
 
+# Encodings on the single-launch kernel.  With the library's compact tables
+# each thread encodes its rows a batch at a time (the angle and partner loads
+# of a batch issued together, rows clamped into the sequence); the caller's
+# duplicated tables and a rotate-half width whose half is not a multiple of 4
+# take the row-at-a-time form; a side without an encoding is stored as
+# loaded.
+_FUSED_PE = {
+    "rope_half": dict(kind="rope", pairing="half"),
+    "rope_inter": dict(kind="rope"),
+    "rope_inter_r64": dict(kind="rope", rotary_dim=64),
+    "rope_half_r96": dict(kind="rope", pairing="half", rotary_dim=96),
+    "rope_half_r52": dict(kind="rope", pairing="half", rotary_dim=52),
+    "sinusoidal": dict(kind="sinusoidal"),
+    "rope_q_only": dict(kind="rope", pairing="half", apply_k=False),
+    "rope_k_only": dict(kind="rope", apply_q=False),
+    "sin_k_only": dict(kind="sinusoidal", apply_q=False),
+    "rope_caller": dict(kind="rope", caller=True),
+    "sin_caller": dict(kind="sinusoidal", caller=True),
+}
+
+
+@pytest.mark.parametrize("mode", list(_FUSED_PE))
+@pytest.mark.parametrize("shape,dtype", [((1, 2, 37, 100, 512), "f32"),
+                                         ((1, 3, 20, 128, 256), "bf16"),
+                                         ((1, 2, 48, 96, 1024), "f32")],
+                         ids=["f32-ragged", "bf16", "f32-d1024"])
+def test_fused_encodings(am, dev, shape, dtype, mode):
+    import hip_rt
+    B, Hh, Lq, Lk, D = shape
+    kw = dict(_FUSED_PE[mode])
+    caller = kw.pop("caller", False)
+    print(f"[case] fused encodings {dtype} {shape} {mode}", flush=True)
+    n = max(Lq, Lk)
+    sin = kw["kind"] == "sinusoidal"
+    r = kw.get("rotary_dim", 0) or D
+    tabs = oracle.sinusoidal_table(n, D) if sin else oracle.rope_cache(n, r)
+    held = []
+    if caller:
+        held = [H.upload(t) for t in tabs]
+        kw.update(table_a=held[0], table_b=held[1])
+    desc = am.make_pe(**kw)
+    dcode = 0 if dtype == "f32" else 1
+    assert am.path(dcode, B, Hh, Lq, Lk, D, desc) == am.ATN_PATH_FUSED_SMALL
+    (q, k, v), (Q, K, V) = H.device_inputs((B, Hh, Lq, D), (B, Hh, Lk, D), 61 + r, dtype,
+                                           0.5 if sin else 1.0)
+    out = H.empty(Q.shape, dtype)
+    am.attention_ex(q, k, v, out, pe=desc)
+    hip_rt.synchronize()
+    assert am.sync_status() == 0
+    if sin:
+        ref = oracle.attention_sinusoidal(Q, K, V, *tabs, add_q=kw.get("apply_q", True),
+                                          add_k=kw.get("apply_k", True), nthreads=16)
+    else:
+        ref = oracle.attention_rope(Q, K, V, *tabs, rotary_dim=r,
+                                    pairing=kw.get("pairing", "interleaved"),
+                                    rotate_q=kw.get("apply_q", True),
+                                    rotate_k=kw.get("apply_k", True), nthreads=16)
+    if dtype == "f32":
+        bad, mabs, _ = H.check_f32(out.numpy(), ref)
+        assert bad == 0, mabs
+    else:
+        bad, nrel, mabs = H.check_bf16(out.numpy(), ref)
+        assert bad == 0, (nrel, mabs)
+    for x in (q, k, v, out, *held):
+        x.free()
+
+
 @pytest.mark.parametrize("xcd", ["0", "1", ""], ids=["device", "xcd", "default"])
 @pytest.mark.parametrize("shape", [(1, 4, 64, 64, 2048), (1, 2, 130, 70, 256)],
                          ids=lambda s: "x".join(map(str, s)))
