@@ -781,6 +781,32 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
     // it loads V with Q and K.
     Raw bq[kQ], bk[kKV], bv[kKV];
     if constexpr (defer_v) issue(0, bq, bk, bv, n == 1);
+    // The encoding operands of the first batch of Q rows and of K rows
+    // (below), in the one-round forms fetched here, with the rows' loads, so
+    // that their latency too hides behind the set-up.  Not where holding
+    // them would bring the kernel to its 256 registers (fp32 rotate-half
+    // beyond the smallest form, fp32 in the largest one-round form).
+    constexpr int kEncBatch = PEK == kPeRopeHalf ? 4 : 8;
+    constexpr bool kPrefetch = defer_v && PEK != kPeNone &&
+                               (kBf16 || FORM == 1 || (FORM == 2 && PEK != kPeRopeHalf));
+    constexpr int kPreQ = kQ < kEncBatch ? kQ : kEncBatch;
+    constexpr int kPreK = kKV < kEncBatch ? kKV : kEncBatch;
+    Pe4Ops<PEK> preq[kPreQ], prek[kPreK];
+    auto enc_fetch = [&](bool isq, int row0, auto& o) {
+        constexpr int NB = sizeof(o) / sizeof(o[0]);
+        const int len = isq ? Lq : Lk, p0 = isq ? q0 : 0;
+        const T* __restrict__ X = isq ? Q : K;
+        const PeSide& pe = isq ? a.pq : a.pk;
+#pragma unroll
+        for (int u = 0; u < NB; ++u) {
+            const int rc = min(row0 + u * rstep, len - 1);
+            o[u] = pe4_fetch<T, PEK>(d, X + (size_t)rc * D, p0 + rc, D, pe);
+        }
+    };
+    if constexpr (kPrefetch) {
+        if (a.pq.on && pe4_batch_ok(PEK, a.pq)) enc_fetch(true, r0, preq);
+        if (a.pk.on && pe4_batch_ok(PEK, a.pk)) enc_fetch(false, r0, prek);
+    }
 
     const Geo g = make_geo(!kBf16, PEK != kPeNone, a.nchunk > 1, a.MB, Lk, dc);
     const int MQ = g.MQ, NK = g.NK, E = MQ * NK, nrb = MQ / 16;
@@ -838,8 +864,7 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
         // sequence so that every load is valid; otherwise (the caller's
         // duplicated tables) one row at a time.  A side without an encoding
         // (pe.on == 0) is stored as loaded.
-        constexpr int kEncBatch = PEK == kPeRopeHalf ? 4 : 8;
-        auto encode_store = [&](bool isq, int j, auto& r) {
+        auto encode_store = [&](bool isq, int j, auto& r, auto& pre) {
             constexpr int NR = sizeof(r) / sizeof(r[0]);
             const int cnt = isq ? cq : ckv, len = isq ? Lq : Lk, p0 = isq ? q0 : 0;
             const T* __restrict__ X = isq ? Q : K;
@@ -854,10 +879,15 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
 #pragma unroll
                 for (int b = 0; b < NR; b += kEncBatch) {
                     Pe4Ops<PEK> o[kEncBatch];
+                    if (kPrefetch && b == 0) {
 #pragma unroll
-                    for (int u = 0; u < kEncBatch && b + u < NR; ++u) {
-                        const int rc = min(r0 + (j * NR + b + u) * rstep, len - 1);
-                        o[u] = pe4_fetch<T, PEK>(d, X + (size_t)rc * D, p0 + rc, D, pe);
+                        for (int u = 0; u < kEncBatch && u < NR; ++u) o[u] = pre[u];
+                    } else {
+#pragma unroll
+                        for (int u = 0; u < kEncBatch && b + u < NR; ++u) {
+                            const int rc = min(r0 + (j * NR + b + u) * rstep, len - 1);
+                            o[u] = pe4_fetch<T, PEK>(d, X + (size_t)rc * D, p0 + rc, D, pe);
+                        }
                     }
 #pragma unroll
                     for (int u = 0; u < kEncBatch && b + u < NR; ++u) {
@@ -886,8 +916,8 @@ __global__ __launch_bounds__(kThreads) void k_fused_small(FusedArgs a) {
         auto store_round = [&](int j, Raw (&q)[kQ], Raw (&k)[kKV], Raw (&v)[kKV],
                                bool store_v_now) {
             if constexpr (PEK != kPeNone) {
-                encode_store(true, j, q);
-                encode_store(false, j, k);
+                encode_store(true, j, q, preq);
+                encode_store(false, j, k, prek);
                 if (store_v_now) {
 #pragma unroll
                     for (int u = 0; u < kKV; ++u)
