@@ -586,28 +586,46 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(
         acc_t s[G::NJ];
 #pragma unroll
         for (int j = 0; j < G::NJ; ++j) s[j] = acc_t{};
-        // per KD-deep step: the step's 2 NJ fragment reads first, then its
-        // 3 NJ products (kept in that order, so the reads' latencies overlap
-        // instead of each read being waited for before its product)
-#pragma unroll
-        for (int ks = 0; ks < G::KS; ++ks) {
-            op_t ah[G::NJ];
-            f16x8 al[G::NJ];
+        // per KD-deep step its NP NJ fragment reads and (2 NP - 1) NJ
+        // products; the reads of step ks + 1 are issued before the products
+        // of step ks (two register sets), so that a step's reads are in
+        // flight while the previous step multiplies instead of being waited
+        // for right after their issue -- not in the form held to 128
+        // registers (4 waves per SIMD), where the second set would spill: it
+        // reads each step's fragments before the step's products
+        constexpr bool kPre = flash_waves_per_simd<T, DP, PEK, NW, RW>() < 4;
+        op_t ah[2][G::NJ];
+        f16x8 al[2][G::NJ];
+        auto frags = [&](int ks, int r) {
 #pragma unroll
             for (int j = 0; j < G::NJ; ++j) {
                 const int a = (G::MT * j + lr) * G::KSTR + G::KD * ks + 8 * lg;
-                ah[j] = __builtin_bit_cast(op_t, lds8_f16(buf + G::K_HI + a));
-                if constexpr (!kBf) al[j] = lds8_f16(buf + G::K_LO + a);
+                ah[r][j] = __builtin_bit_cast(op_t, lds8_f16(buf + G::K_HI + a));
+                if constexpr (!kBf) al[r][j] = lds8_f16(buf + G::K_LO + a);
+            }
+        };
+        if constexpr (kPre) {
+            frags(0, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, G::NP * G::NJ, 0);  // DS reads
+        }
+#pragma unroll
+        for (int ks = 0; ks < G::KS; ++ks) {
+            const int r = kPre ? ks & 1 : 0;
+            if constexpr (kPre) {
+                if (ks + 1 < G::KS) frags(ks + 1, r ^ 1);
+            } else {
+                frags(ks, 0);
             }
 #pragma unroll
-            for (int j = 0; j < G::NJ; ++j) s[j] = mfma_rw(ah[j], qh[ks], s[j]);
+            for (int j = 0; j < G::NJ; ++j) s[j] = mfma_rw(ah[r][j], qh[ks], s[j]);
             if constexpr (!kBf) {
 #pragma unroll
-                for (int j = 0; j < G::NJ; ++j) s[j] = mfma_rw(ah[j], ql[ks], s[j]);
+                for (int j = 0; j < G::NJ; ++j) s[j] = mfma_rw(ah[r][j], ql[ks], s[j]);
 #pragma unroll
-                for (int j = 0; j < G::NJ; ++j) s[j] = mfma_rw(al[j], qh[ks], s[j]);
+                for (int j = 0; j < G::NJ; ++j) s[j] = mfma_rw(al[r][j], qh[ks], s[j]);
             }
-            __builtin_amdgcn_sched_group_barrier(0x100, G::NP * G::NJ, 0);  // DS reads
+            if (!kPre || ks + 1 < G::KS)
+                __builtin_amdgcn_sched_group_barrier(0x100, G::NP * G::NJ, 0);  // DS reads
             __builtin_amdgcn_sched_group_barrier(0x008, (2 * G::NP - 1) * G::NJ, 0);  // MFMA
         }
 
@@ -708,24 +726,37 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(
         // RW = 32: dims 32 dt + lane % 32
         const int vrow = 4 * lg + ((lane & 15) >> 2);
         const int vcol = (RW == 32 ? 16 * ((lane >> 4) & 1) : 0) + 4 * (lane & 3);
+        // (dt, b) = (i / NB, i % NB) in turn, the fragments of step i + 1
+        // read before the products of step i (two register sets; as above,
+        // not in the form held to 128 registers)
+        constexpr bool kVPre = kPre;
+        pv_t vh[2];
+        f16x8 vl[2];
+        auto vfrags = [&](int i, int r) {
+            const int a = (G::KD * (i % G::NB) + vrow) * G::VSTR + G::MT * (i / G::NB) + vcol;
+            constexpr int half = G::KD / 2 * G::VSTR;
+            const uint2 h0 = lds_tr16(buf + G::V_HI + a);
+            const uint2 h1 = lds_tr16(buf + G::V_HI + a + half);
+            vh[r] = __builtin_bit_cast(pv_t, make_uint4(h0.x, h0.y, h1.x, h1.y));
+            if constexpr (!kBf) {
+                const uint2 l0 = lds_tr16(buf + G::V_LO + a);
+                const uint2 l1 = lds_tr16(buf + G::V_LO + a + half);
+                vl[r] = __builtin_bit_cast(f16x8, make_uint4(l0.x, l0.y, l1.x, l1.y));
+            }
+        };
+        if constexpr (kVPre) vfrags(0, 0);
 #pragma unroll
-        for (int dt = 0; dt < G::NDT; ++dt) {
-#pragma unroll
-            for (int b = 0; b < G::NB; ++b) {
-                const int a = (G::KD * b + vrow) * G::VSTR + G::MT * dt + vcol;
-                constexpr int half = G::KD / 2 * G::VSTR;
-                const uint2 h0 = lds_tr16(buf + G::V_HI + a);
-                const uint2 h1 = lds_tr16(buf + G::V_HI + a + half);
-                const pv_t vh = __builtin_bit_cast(pv_t, make_uint4(h0.x, h0.y, h1.x, h1.y));
-                o[dt] = mfma_rw(vh, ph[b], o[dt]);
-                if constexpr (!kBf) {
-                    const uint2 l0 = lds_tr16(buf + G::V_LO + a);
-                    const uint2 l1 = lds_tr16(buf + G::V_LO + a + half);
-                    const f16x8 vl =
-                        __builtin_bit_cast(f16x8, make_uint4(l0.x, l0.y, l1.x, l1.y));
-                    o[dt] = mfma_rw(vh, pl[b], o[dt]);
-                    o[dt] = mfma_rw(vl, ph[b], o[dt]);
-                }
+        for (int i = 0; i < G::NDT * G::NB; ++i) {
+            const int dt = i / G::NB, b = i % G::NB, r = kVPre ? i & 1 : 0;
+            if constexpr (kVPre) {
+                if (i + 1 < G::NDT * G::NB) vfrags(i + 1, r ^ 1);
+            } else {
+                vfrags(i, 0);
+            }
+            o[dt] = mfma_rw(vh[r], ph[b], o[dt]);
+            if constexpr (!kBf) {
+                o[dt] = mfma_rw(vh[r], pl[b], o[dt]);
+                o[dt] = mfma_rw(vl[r], ph[b], o[dt]);
             }
         }
 
