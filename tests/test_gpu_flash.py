@@ -543,6 +543,32 @@ def test_flash_split_auto(am, dev, dt, shape):
     assert n == 0, info
 
 
+@pytest.mark.parametrize("dt,pe,shape", [("bf16", None, (1, 2, 300, 4100, 128)),
+                                         ("bf16", "rope_half", (1, 2, 300, 4100, 128)),
+                                         ("f32", "sinusoidal", (1, 1, 257, 4500, 96)),
+                                         ("f32", None, (1, 2, 300, 4100, 128)),
+                                         ("f32", None, (1, 2, 300, 4100, 64)),
+                                         ("bf16", "rope", (1, 1, 100, 8200, 64))],
+                         ids=lambda v: "x".join(map(str, v)) if isinstance(v, tuple) else str(v))
+def test_flash_long_keys(am, dev, dt, pe, shape):
+    """From 4096 keys on, grids below a workgroup per CU take 32-row waves
+    with key splits (fp32 without an encoding at head_d <= 64 keeps 16-row
+    waves): ragged key and query lengths against the oracle."""
+    B, Hh, Lq, Lk, D = shape
+    print(f"[case] flash long keys {dt} {pe} {shape}", flush=True)
+    desc = None if pe is None else (am.make_pe("rope", pairing="half") if pe == "rope_half"
+                                    else am.make_pe(pe))
+    code = 0 if dt == "f32" else 1
+    assert am.path(code, B, Hh, Lq, Lk, D, desc) == am.ATN_PATH_FLASH
+    Q, K, V = H.rng_inputs((B, Hh, Lq, D), (B, Hh, Lk, D), seed=700 + D,
+                           sigma=0.5 if pe == "sinusoidal" else 1.0)
+    if dt == "bf16":
+        Q, K, V = _bf16(Q), _bf16(K), _bf16(V)
+    got = _call(am, dt, Q, K, V, desc)
+    n, info = _check(dt, got, _ref(pe, Q, K, V))
+    assert n == 0, info
+
+
 @pytest.mark.parametrize("nsplit", [2, 3, 7])
 @pytest.mark.parametrize("dt,pe,form", [("f32", None, "8x16"), ("bf16", None, "8x32"),
                                         ("f32", "rope", "4x16"), ("bf16", "rope_half", "8x16"),
