@@ -58,6 +58,10 @@ SHAPES = [
     ("cfg3", "bf16", 1, 4, 32, 128, 8192, "none"),
     ("cfg4 rope-half", "bf16", 8, 8, 1024, 1024, 4096, "rope_half"),
     ("cfg5 sinusoidal", "bf16", 4, 16, 256, 2048, 1024, "sinusoidal"),
+    # the encodings inside the single-launch kernel at configs 2 and 3
+    ("cfg2 rope-half", "f32", 1, 4, 64, 64, 2048, "rope_half"),
+    ("cfg2 sinusoidal", "f32", 1, 4, 64, 64, 2048, "sinusoidal"),
+    ("cfg3 rope-half", "bf16", 1, 4, 32, 128, 8192, "rope_half"),
     # fp32 beyond the single-launch window: the reference's own long-sequence
     # test shape (final/attention.cu:522, the flash kernel) and a large-head
     # one (the split-D pipeline); names without commas (--shapes splits on them)
@@ -69,6 +73,7 @@ SHAPES = [
     ("bf16 rope-half 4x32x512x128", "bf16", 4, 32, 512, 512, 128, "rope_half"),
     ("bf16 long 1x8x4096x4096x128", "bf16", 1, 8, 4096, 4096, 128, "none"),
     ("bf16 long 1x32x2048x2048x64", "bf16", 1, 32, 2048, 2048, 64, "none"),
+    ("bf16 rope-half long 1x8x4096x4096x128", "bf16", 1, 8, 4096, 4096, 128, "rope_half"),
 ]
 
 
