@@ -92,10 +92,11 @@ def parse():
                     help="one config only (0 = headline config 2 plus every other config)")
     ap.add_argument("--head-dim", type=int, default=0, help="override D (config-2 sweep)")
     ap.add_argument("--shape", default="", metavar="B,H,LQ,LK,D",
-                    help="time this shape instead (no encoding; for profiling the flash, GEMM "
-                         "and split-D paths)")
+                    help="time this shape instead (for profiling one kernel or path)")
     ap.add_argument("--dtype", default="f32", choices=["f32", "bf16"],
                     help="element type of --shape")
+    ap.add_argument("--pe", default="none", choices=["none", "rope_half", "sinusoidal"],
+                    help="positional encoding of --shape (sinusoidal inputs at sigma 0.5)")
     ap.add_argument("--no-flash", action="store_true",
                     help="keep calls off the flash kernel (atn_tuning.no_flash)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
@@ -452,8 +453,9 @@ def main():
     if a.shape:
         b_, h_, lq_, lk_, d_ = (int(x) for x in a.shape.split(","))
         lbl = "fp32" if a.dtype == "f32" else "bf16"
-        cfg = [f"{lbl} SDPA ({b_},{h_},{lq_},{lk_},{d_})", a.dtype, b_, h_, lq_, lk_, d_, "none",
-               1.0]
+        enc = {"none": "", "rope_half": " RoPE rotate-half", "sinusoidal": " sinusoidal"}[a.pe]
+        cfg = [f"{lbl} SDPA{enc} ({b_},{h_},{lq_},{lk_},{d_})", a.dtype, b_, h_, lq_, lk_, d_,
+               a.pe, 0.5 if a.pe == "sinusoidal" else 1.0]
         head_cfg_id = 0
     if a.head_dim:
         cfg[6] = a.head_dim
