@@ -52,9 +52,52 @@ def _cases():
 
 CASES = _cases()
 
+# A second set weighted toward long key rows with few query rows (the flash
+# kernel's 32-row waves with key splits from 4096 keys on) and encodings in
+# the single-launch window, rotate-half at partial rotary widths too.
+N_LONG = 60
+SEED_LONG = 20261203
+
+
+def _long_cases():
+    rng = np.random.default_rng(SEED_LONG)
+    out = []
+    for i in range(N_LONG):
+        dt = str(rng.choice(["f32", "bf16"]))
+        pe = str(rng.choice(["none", "rope", "rope_half", "sinusoidal"]))
+        if rng.integers(0, 2) == 0:  # long keys
+            B, Hh = 1, int(rng.integers(1, 3))
+            Lq, Lk = int(rng.integers(1, 260)), int(rng.integers(3000, 9000))
+            D = int(rng.choice([32, 64, 100, 128, 192, 256]))
+        else:  # the single-launch window
+            B, Hh = int(rng.integers(1, 3)), int(rng.integers(1, 4))
+            Lq, Lk = int(rng.integers(1, 65)), int(rng.integers(1, 129))
+            D = int(rng.choice([64, 128, 512, 1024, 2048, 4096]))
+        if B * Hh * max(Lq, Lk) * D > 8_000_000:
+            D = max(8, 8_000_000 // (B * Hh * max(Lq, Lk)) // 8 * 8)
+        aq, ak = [(True, True), (True, True), (True, False), (False, True)][int(rng.integers(0, 4))]
+        rot = D
+        if pe in ("rope", "rope_half") and rng.integers(0, 3) == 0:
+            rot = int(rng.integers(1, D // 2 + 1)) * 2
+        out.append((1000 + i, dt, pe, (B, Hh, Lq, Lk, D), aq, ak, rot, False))
+    return out
+
+
+LONG_CASES = _long_cases()
+
 
 @pytest.mark.parametrize("case", CASES, ids=lambda c: f"{c[0]}-{c[1]}-{c[2]}-" + "x".join(map(str, c[3])))
 def test_random_shape(am, dev, case):
+    _run_case(am, case)
+
+
+@pytest.mark.parametrize("case", LONG_CASES,
+                         ids=lambda c: f"{c[0]}-{c[1]}-{c[2]}-" + "x".join(map(str, c[3])))
+def test_random_long_keys_and_encodings(am, dev, case):
+    _run_case(am, case)
+
+
+def _run_case(am, case):
     import hip_rt
     i, dt, pe, shape, aq, ak, rot, noalloc = case
     B, Hh, Lq, Lk, D = shape
@@ -62,7 +105,8 @@ def test_random_shape(am, dev, case):
           flush=True)
     desc = {"none": None,
             "rope": am.make_pe("rope", rotary_dim=rot, apply_q=aq, apply_k=ak),
-            "rope_half": am.make_pe("rope", pairing="half", apply_q=aq, apply_k=ak),
+            "rope_half": am.make_pe("rope", pairing="half", rotary_dim=rot, apply_q=aq,
+                                    apply_k=ak),
             "sinusoidal": am.make_pe("sinusoidal", apply_q=aq, apply_k=ak)}[pe]
     sigma = 0.5 if pe == "sinusoidal" else 1.0
     (q, k, v), (Q, K, V) = H.device_inputs((B, Hh, Lq, D), (B, Hh, Lk, D), 1000 + i, dt, sigma)
