@@ -772,10 +772,10 @@ bool flash_ok(int dtype, const Shape& s, const PePlan& plan) {
 // and encoded once per 256 rows outweighs the splits' merge there (same box:
 // bf16 (1,8,4096,4096,128) 102 -> 91 us, (1,2,16384,16384,128) 346 -> 280 us,
 // RoPE rotate-half 173 -> 128 us, sinusoidal (1,4,8192,8192,128) 338 -> 216
-// us, fp32 (1,4,8192,8192,128) 432 -> 395 us; at 1024 keys the 16-row form
-// stays ahead: 33 against 43 us at (2,16,1024,1024,128)), except for fp32
-// without an encoding at head_d <= 64 (135 against 138 us).
-int flash_form(const Shape& s, int dev, int dtype, int pek) {
+// us, fp32 (1,4,8192,8192,128) 432 -> 395 us, fp32 (1,8,4096,4096,64) 131
+// -> 123 us; at 1024 keys the 16-row form stays ahead: 33 against 43 us at
+// (2,16,1024,1024,128)).
+int flash_form(const Shape& s, int dev) {
     const int forced = tune().flash_form;
     if (forced >= atn::kFlashForm4x16 && forced <= atn::kFlashForm8x32) return forced;
     if (s.D > 128) return atn::kFlashForm8x16;
@@ -791,8 +791,7 @@ int flash_form(const Shape& s, int dev, int dtype, int pek) {
         cus = ds.cus > 0 ? ds.cus : 256;
     }
     if (s.BH * ((s.Lq + 255) / 256) >= (int64_t)cus) return atn::kFlashForm8x32;
-    const bool long_keys = s.Lk >= 4096 && !(dtype == ATN_DTYPE_F32 && pek == atn::kPeNone && s.D <= 64);
-    return long_keys ? atn::kFlashForm8x32 : atn::kFlashForm8x16;
+    return s.Lk >= 4096 ? atn::kFlashForm8x32 : atn::kFlashForm8x16;
 }
 
 // Query rows per workgroup of a flash form.
@@ -926,7 +925,7 @@ int attention_run(int dtype, const void* Q, const void* K, const void* V, void* 
     const bool use_flash = !use_fused && a16 && flash_ok(dtype, s, plan);
     const bool use_gemm = !use_fused && !use_flash && gp.ok && aligned(Q, 16) && aligned(K, 16) &&
                           aligned(V, 16) && aligned(out, 16);
-    const int fform = use_flash ? flash_form(s, dev, dtype, plan.pek) : 0;
+    const int fform = use_flash ? flash_form(s, dev) : 0;
     const FlashSplit fs = use_flash ? flash_split(s, flash_rows(fform, D)) : FlashSplit{};
     const size_t need =
         use_fused ? fd.bytes

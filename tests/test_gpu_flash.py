@@ -552,8 +552,8 @@ def test_flash_split_auto(am, dev, dt, shape):
                          ids=lambda v: "x".join(map(str, v)) if isinstance(v, tuple) else str(v))
 def test_flash_long_keys(am, dev, dt, pe, shape):
     """From 4096 keys on, grids below a workgroup per CU take 32-row waves
-    with key splits (fp32 without an encoding at head_d <= 64 keeps 16-row
-    waves): ragged key and query lengths against the oracle."""
+    with key splits (fp32 without an encoding at head_d <= 64 with 64-key
+    tiles): ragged key and query lengths against the oracle."""
     B, Hh, Lq, Lk, D = shape
     print(f"[case] flash long keys {dt} {pe} {shape}", flush=True)
     desc = None if pe is None else (am.make_pe("rope", pairing="half") if pe == "rope_half"
