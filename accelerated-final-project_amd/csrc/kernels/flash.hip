@@ -7,10 +7,11 @@
 // waves, 16 or 32 per wave (v_mfma_f32_16x16x32_f16 or 32x32x16 tiles), of
 // one head and walks the head's keys in tiles of KT keys, with the running
 // output of its rows in registers.  Forms: 8 waves of 16 rows (64-key tiles
-// at D <= 128 without an encoding) and 8 waves of 32 rows (D <= 128, 32-key
-// tiles: each wave reads a K/V tile from LDS once per 32 rows instead of 16,
-// and each tile is converted once per 256 rows), the library's two; 4 waves
-// of 16 or of 32 rows as tuning overrides.
+// at D <= 128) and 8 waves of 32 rows (D <= 128; 64-key tiles at D <= 64, 32
+// at D = 128: each wave reads a K/V tile from LDS once per 32 rows instead of
+// 16, and each tile is converted once per 256 rows), the library's two; 4
+// waves of 16 rows for up to 64 query rows, and of 32 rows as a tuning
+// override.
 //
 //   Per tile: K and V rows are loaded (16-byte loads) two tiles ahead, K
 //   encoded (RoPE, sinusoidal) once they land, and reduced to per-wave
@@ -55,7 +56,7 @@ namespace {
 // workgroup (4 or 8) and RW query rows per wave (16: v_mfma_f32_16x16x32_f16
 // tiles; 32: v_mfma_f32_32x32x16_f16 tiles, D <= 128), every wave sharing
 // each K/V tile.  The key tile is 64 keys for bf16 inputs (HL false) and,
-// without a positional encoding (PE), for 8 waves of 16 rows at DP <= 128
+// with or without a positional encoding, for 8 waves of 16 rows at DP <= 128
 // and of 32 rows at DP <= 64 (at DP = 128 the 32-row form's extra scores
 // spill), else 32 (two LDS buffers of it then leave room for two 4-wave
 // workgroups per CU), and at least one load round of the workgroup.
@@ -64,7 +65,7 @@ struct FlashGeo {
     static_assert(RW == 16 || (RW == 32 && DP <= 128), "forms");
     static constexpr int THREADS = 64 * NW, ROWS = RW * NW;
     static constexpr int KT0 =
-        !HL || (!PE && NW == 8 && (RW == 16 ? DP <= 128 : DP <= 64)) ? 64 : 32;
+        !HL || (NW == 8 && (RW == 16 ? DP <= 128 : DP <= 64)) ? 64 : 32;
     static constexpr int KT = KT0 > THREADS / (DP / 4) ? KT0 : THREADS / (DP / 4);
     static constexpr int MT = RW;                   // MFMA tile edge
     static constexpr int KD = RW == 16 ? 32 : 16;   // MFMA depth: dims of Q K^T, keys of P V
