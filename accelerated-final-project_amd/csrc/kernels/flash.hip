@@ -56,16 +56,19 @@ namespace {
 // workgroup (4 or 8) and RW query rows per wave (16: v_mfma_f32_16x16x32_f16
 // tiles; 32: v_mfma_f32_32x32x16_f16 tiles, D <= 128), every wave sharing
 // each K/V tile.  The key tile is 64 keys for bf16 inputs (HL false) and,
-// with or without a positional encoding, for 8 waves of 16 rows at DP <= 128
-// and of 32 rows at DP <= 64 (at DP = 128 the 32-row form's extra scores
-// spill), else 32 (two LDS buffers of it then leave room for two 4-wave
+// with or without a positional encoding, for 8 waves of 16 rows at DP <= 128,
+// of 32 rows at DP <= 64 (at DP = 128 the 32-row form's extra scores spill)
+// and 4 waves of 16 rows at DP <= 64 (two workgroups per CU still fit in
+// LDS), else 32 (two LDS buffers of it then leave room for two 4-wave
 // workgroups per CU), and at least one load round of the workgroup.
 template <int DP, bool PE, int NW, int RW, bool HL = true>
 struct FlashGeo {
     static_assert(RW == 16 || (RW == 32 && DP <= 128), "forms");
     static constexpr int THREADS = 64 * NW, ROWS = RW * NW;
     static constexpr int KT0 =
-        !HL || (NW == 8 && (RW == 16 ? DP <= 128 : DP <= 64)) ? 64 : 32;
+        !HL || (NW == 8 && (RW == 16 ? DP <= 128 : DP <= 64)) || (NW == 4 && RW == 16 && DP <= 64)
+            ? 64
+            : 32;
     static constexpr int KT = KT0 > THREADS / (DP / 4) ? KT0 : THREADS / (DP / 4);
     static constexpr int MT = RW;                   // MFMA tile edge
     static constexpr int KD = RW == 16 ? 32 : 16;   // MFMA depth: dims of Q K^T, keys of P V
